@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the CSR sparse x dense hot path on one MI355X.
+
+A step is one CSR SpMV ``y = A @ x`` through the drop-in API (``CSRArray``
+with its cached row-block plan, ``A @ x`` on torch's current stream) on the
+headline workload: n = 4,194,304 rows, exactly 16 columns per row drawn
+uniformly without replacement, float32 values / int32 indices (synthetic,
+seeded).  Inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line.  ``value`` is the effective bandwidth on compulsory
+traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
+
+- ``roofline``: the SpMV kernel's achieved GB/s from HIP events around back-to-
+  back launches on the launch stream, against the 8 TB/s HBM peak;
+  ``traffic`` is filled from rocprofv3 FETCH_SIZE/WRITE_SIZE when
+  ``--traffic-json`` points at a summary made by ``profiles/`` tooling, else null;
+- ``cold``: the same SpMV with a 1 GiB buffer written between launches
+  (evicts the 256 MB Infinity Cache), median of per-launch times;
+- ``spmm``: CSR SpMM with k=64 on the 3D 7-point Poisson matrix (128^3),
+  GFLOP/s, and its ratio to SpMV GFLOP/s on the same matrix and on the
+  headline matrix;
+- ``cpu_baseline``: the C restatement of the reference CPU kernel
+  (oracle/, ``-O3`` without ``-march=native``), threads split like the
+  reference, timed on this host's cores on the same matrix.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mlx-sparse_amd"))
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _events_time(fn, iters: int) -> float:
+    """Mean milliseconds per call of ``fn`` from HIP events on the current
+    stream (the stream the kernels are launched on)."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def _cold_time(fn, iters: int, scratch: torch.Tensor) -> float:
+    """Median ms per call with a 1 GiB write between calls (untimed)."""
+    times = []
+    for _ in range(iters):
+        scratch.fill_(1.0)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    return statistics.median(times)
+
+
+def cpu_baseline(m, x, seconds: float = 12.0) -> dict:
+    """Time the oracle's reference-CPU restatement on a bounded sample."""
+    from oracle import oracle as orc
+
+    threads = orc.cpu_worker_count()
+    for _ in range(2):
+        orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=threads)
+    samples = []
+    t_end = time.perf_counter() + seconds
+    while len(samples) < 10 or (time.perf_counter() < t_end and len(samples) < 30):
+        t0 = time.perf_counter()
+        orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=threads)
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    from mlx_sparse import synthetic
+
+    nbytes = synthetic.compulsory_bytes(m.nnz, m.shape[0], m.shape[1], 4, 4)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{len(samples)} full SpMV calls on the same matrix, median "
+                   f"{med * 1e3:.1f} ms; gcc -O3 -ffp-contract=off, no -march=native; "
+                   f"{threads} threads of {len(os.sched_getaffinity(0))} in affinity; {model}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
+    ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "spmv_random16_traffic.json"))
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device.", file=sys.stderr)
+        return 2
+
+    import mlx_sparse as ms
+    from mlx_sparse import synthetic
+    from mlx_sparse._ext_loader import extension
+
+    ext = extension()
+    ms.use_gpu(0)
+    dev = torch.device("cuda", 0)
+
+    # ---- headline: random 16/row SpMV -----------------------------------------
+    t0 = time.perf_counter()
+    m = synthetic.random_fixed_row(1 << 22, 16, seed=0)
+    x_np = synthetic.uniform(m.shape[1], -1.0, 1.0, seed=1)
+    log(f"generated {m.name} nnz={m.nnz} in {time.perf_counter() - t0:.1f}s")
+    A = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
+    x = torch.from_numpy(x_np).to(dev)
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    plan = A.plan(dev)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    info = plan.info()
+    log(f"plan: {info} built in {plan_ms:.1f} ms")
+
+    nbytes = synthetic.compulsory_bytes(m.nnz, m.shape[0], m.shape[1], 4, 4)
+    nflops = synthetic.flops(m.nnz)
+
+    def step():
+        return A @ x
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        y = step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    value = nbytes / (wall / args.steps) / 1e9
+    log(f"api step: {ms_per_step * 1e3:.1f} us  {value:.0f} GB/s")
+
+    # kernel-only timing: the C-ABI launch on torch's current stream
+    data, indices, indptr = A.buffers(dev)
+    yk = torch.empty_like(y)
+
+    def launch():
+        ext.csr_matvec(data, indices, indptr, x, m.shape[0], m.shape[1], plan=plan)
+
+    kern_ms = _events_time(launch, args.steps)
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"kernel (events): {kern_ms * 1e3:.1f} us  {achieved:.0f} GB/s  {achieved / HBM_PEAK_GBS:.3f} of peak")
+
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    cold_ms = _cold_time(launch, 30, scratch)
+    cold_gbs = nbytes / (cold_ms * 1e-3) / 1e9
+    log(f"cold: {cold_ms * 1e3:.1f} us  {cold_gbs:.0f} GB/s")
+
+    traffic = None
+    tj = Path(args.traffic_json)
+    if tj.exists():
+        try:
+            traffic = json.loads(tj.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": "CSR SpMV effective HBM GB/s (% of peak) + SpMM GFLOP/s, fp32, 1xMI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded): uniform random columns, N(0,1) values, x~U[-1,1]",
+        "config": {"workload": "csr_spmv random16 n=4194304 nnz=67108864 f32/i32",
+                   "n_rows": m.shape[0], "nnz": m.nnz, "index": "int32",
+                   "compulsory_bytes": nbytes, "plan_build_ms": round(plan_ms, 3)},
+        "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 2),
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "spmv_blocks<F32,int>",
+                     "kernel_us": round(kern_ms * 1e3, 2)},
+        "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),
+                 "frac": round(cold_gbs / HBM_PEAK_GBS, 4)},
+    }
+    del y, yk
+
+    # ---- SpMM k=64 on the 3D Poisson matrix --------------------------------------
+    if not args.no_spmm:
+        spmv_gflops_cfg2 = nflops / (kern_ms * 1e-3) / 1e9
+        del A, x, data, indices, indptr, plan
+        torch.cuda.empty_cache()
+        p = synthetic.poisson_3d(128)
+        P = ms.csr_array((p.data, p.indices, p.indptr), shape=p.shape)
+        xp = torch.from_numpy(synthetic.uniform(p.shape[1], -1.0, 1.0, seed=1)).to(dev)
+        Xp = torch.from_numpy(synthetic.normal(p.shape[1], seed=2, k=64)).to(dev)
+        pd, pi, pp = P.buffers(dev)
+        pplan = P.plan(dev)
+        spmv_ms = _events_time(lambda: ext.csr_matvec(pd, pi, pp, xp, p.shape[0], p.shape[1], plan=pplan), 100)
+        spmm_ms = _events_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1]), 50)
+        for _ in range(3):
+            P @ Xp
+        spmm_cold = _cold_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1]), 15, scratch)
+        f_spmv = synthetic.flops(p.nnz)
+        f_spmm = synthetic.flops(p.nnz, 64)
+        b_spmm = synthetic.compulsory_bytes(p.nnz, p.shape[0], p.shape[1], 4, 4, k=64)
+        b_spmv = synthetic.compulsory_bytes(p.nnz, p.shape[0], p.shape[1], 4, 4)
+        g_spmv = f_spmv / (spmv_ms * 1e-3) / 1e9
+        g_spmm = f_spmm / (spmm_ms * 1e-3) / 1e9
+        result["spmm"] = {
+            "workload": "poisson3d 128^3 n=2097152 nnz=14581760, X n x 64 row-major, f32/i32",
+            "k": 64, "kernel_us": round(spmm_ms * 1e3, 2), "gflops": round(g_spmm, 1),
+            "gbs": round(b_spmm / (spmm_ms * 1e-3) / 1e9, 1),
+            "frac": round(b_spmm / (spmm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "cold_us": round(spmm_cold * 1e3, 2),
+            "cold_frac": round(b_spmm / (spmm_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "spmv_same_matrix_us": round(spmv_ms * 1e3, 2),
+            "spmv_same_matrix_gflops": round(g_spmv, 1),
+            "spmv_same_matrix_gbs": round(b_spmv / (spmv_ms * 1e-3) / 1e9, 1),
+            "ratio_vs_spmv_same_matrix": round(g_spmm / g_spmv, 2),
+            "ratio_vs_headline_spmv": round(g_spmm / spmv_gflops_cfg2, 2),
+        }
+        log(f"spmm k=64: {spmm_ms * 1e3:.1f} us {g_spmm:.0f} GFLOP/s; spmv same matrix "
+            f"{spmv_ms * 1e3:.1f} us {g_spmv:.0f} GFLOP/s")
+        del P, Xp, xp, pd, pi, pp, pplan
+
+    # ---- CPU baseline (reference CPU kernel restated in C) -------------------------
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(m, x_np)
+        log(f"cpu: {result['cpu_baseline']}")
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,216 @@
+/*
+ * msx_sparse.h - C ABI of the MI355X (gfx950) CSR sparse x dense library.
+ *
+ * This is the drop-in boundary for mlx-sparse's sparse x dense hot path:
+ * CSR SpMV (y = A x) and CSR SpMM with a dense row-major right-hand side
+ * (Y = A X).  Every entry point takes plain pointers and sizes; no C++ or
+ * framework type crosses it.
+ *
+ * Conventions
+ *   - The caller owns every buffer.  Outputs (y / Y) are allocated by the
+ *     caller; the library only writes them.  Plans are the one object the
+ *     library allocates (device memory for row blocks), released by
+ *     msx_csr_plan_destroy.
+ *   - GPU entry points are asynchronous and ordered on the HIP stream passed
+ *     as `stream` (a hipStream_t; NULL means the default stream).  They
+ *     return after the launch, not after completion.  Calls on different
+ *     streams may run concurrently; a plan is read-only after creation and
+ *     may be shared by concurrent calls.
+ *   - Errors are status codes; msx_last_error() returns a thread-local text
+ *     for the last failing call on the calling thread.  The texts for shape
+ *     and dtype problems follow the reference validators
+ *     (reference: src/common/common.cpp:104-177).
+ *   - `indices` and `indptr` share one index type; `data`, `x`/`X` and
+ *     `y`/`Y` share one value type (reference: src/common/common.cpp:146-168).
+ *   - Sizes are int64_t, but n_rows, n_cols and k must be below 2^31, as in
+ *     the reference, whose shapes are `int` (reference:
+ *     src/sparse/csr_matvec/csr_matvec.h:25-27).
+ *   - Arithmetic: float16/bfloat16 operands are widened to float32,
+ *     multiplied and summed in float32, and rounded once to the storage type
+ *     (round to nearest even).  float32 sums in float32; complex64 sums in
+ *     complex64 with the textbook product.  Products and sums are rounded
+ *     separately (no fused multiply-add), as in the reference CPU kernels
+ *     (reference: src/common/common.h:52-79).
+ */
+#ifndef MSX_SPARSE_H
+#define MSX_SPARSE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSX_ABI_VERSION 1
+
+typedef enum msx_vtype {
+  MSX_F32 = 0,  /* float32 */
+  MSX_F16 = 1,  /* IEEE binary16, passed as raw 16-bit storage */
+  MSX_BF16 = 2, /* bfloat16, passed as raw 16-bit storage */
+  MSX_C64 = 3   /* complex64: interleaved (real, imag) float32 pairs */
+} msx_vtype;
+
+typedef enum msx_itype {
+  MSX_I32 = 0, /* int32 indices / indptr */
+  MSX_I64 = 1  /* int64 indices / indptr */
+} msx_itype;
+
+typedef enum msx_status {
+  MSX_OK = 0,
+  MSX_EINVAL = 1, /* bad shape, size, pointer or plan (ValueError) */
+  MSX_ETYPE = 2,  /* unsupported or mismatched dtype (TypeError) */
+  MSX_EHIP = 3,   /* a HIP runtime call failed (RuntimeError) */
+  MSX_ENOMEM = 4  /* device or host allocation failed (MemoryError) */
+} msx_status;
+
+/* Opaque row-block plan built from `indptr` on the device. */
+typedef struct msx_csr_plan msx_csr_plan;
+
+/* Summary of a plan, for callers that report or test it. */
+typedef struct msx_plan_info {
+  int64_t n_rows;
+  int64_t nnz;
+  int64_t block_nnz;   /* W: a short block holds rows whose starts fall in one
+                          W-wide window of the nnz range; rows with more than
+                          W stored values are "long" */
+  int64_t block_rows;  /* R: a short block never crosses a multiple of R rows */
+  int64_t chunk_nnz;   /* C: long rows are split into chunks of C values */
+  int64_t n_blocks;    /* short blocks */
+  int64_t n_long_rows; /* rows with more than W stored values */
+  int64_t n_chunks;    /* total chunks over all long rows */
+  int64_t device;      /* HIP device ordinal the plan lives on */
+  int64_t plan_bytes;  /* device bytes held by the plan */
+} msx_plan_info;
+
+/* ABI version of the loaded library (MSX_ABI_VERSION at build time). */
+int msx_abi_version(void);
+
+/* Thread-local text of the last error on this thread ("" if none). */
+const char *msx_last_error(void);
+
+/* Number of HIP devices visible to the library (0 when none). */
+msx_status msx_device_count(int *count);
+
+/*
+ * Build a row-block plan from a device-resident `indptr` (n_rows + 1
+ * entries of type `it`) on `stream`.  The plan splits the rows into short
+ * blocks (consecutive rows processed by one wavefront) and long rows (split
+ * into chunks processed by whole workgroups, then summed in chunk order).
+ * Synchronises `stream` once to read the block counts.  `block_nnz` selects
+ * W (0 = library default; otherwise a power of two in [64, 1024]).
+ *
+ * Replaces the reference's per-launch kernel choice `nnz >= 32 * n_rows`
+ * (reference: src/sparse/csr_matvec/csr_matvec.cpp:291-296), which has no
+ * persistent object; the reference container is immutable
+ * (reference: mlx_sparse/_csr.py:33), so a plan may be cached with it.
+ */
+msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
+                               const void *indptr, int64_t block_nnz,
+                               void *stream, msx_csr_plan **out);
+
+/* Release a plan (NULL is accepted).  Synchronises the plan's device. */
+msx_status msx_csr_plan_destroy(msx_csr_plan *plan);
+
+/* Fill `info` from a plan. */
+msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info *info);
+
+/*
+ * Copy a plan's index arrays to host memory (synchronous), for bit-exact
+ * checks of the binning.  Each pointer may be NULL to skip that array.
+ *   block_row_begin: n_blocks + 1 int64 (first row of each short block, then
+ *                    a sentinel equal to n_rows);
+ *   long_rows:       n_long_rows int64 (row ids, ascending);
+ *   long_chunk_begin: n_long_rows + 1 int64 (first chunk of each long row,
+ *                    then n_chunks).
+ */
+msx_status msx_csr_plan_export(const msx_csr_plan *plan,
+                               int64_t *block_row_begin, int64_t *long_rows,
+                               int64_t *long_chunk_begin);
+
+/*
+ * y[i] = sum_{p = indptr[i]}^{indptr[i+1]-1} data[p] * x[indices[p]]
+ * for i in [0, n_rows).  All pointers are device pointers.  `plan` may be
+ * NULL (a plan-free kernel sized from nnz / n_rows is used); a non-NULL plan
+ * must have been built from this `indptr`.
+ *
+ * Replaces CSRMatVec::eval_gpu (reference:
+ * src/sparse/csr_matvec/csr_matvec.cpp:278-317) and the Metal kernels
+ * csr_matvec_* / csr_matvec_vector_* (reference:
+ * src/sparse/csr_matvec/csr_matvec.metal:17-123).
+ */
+msx_status msx_csr_spmv(msx_vtype vt, msx_itype it, int64_t n_rows,
+                        int64_t n_cols, int64_t nnz, const void *data,
+                        const void *indices, const void *indptr,
+                        const void *x, void *y, const msx_csr_plan *plan,
+                        void *stream);
+
+/*
+ * Y[i, c] = sum_p data[p] * X[indices[p], c] for c in [0, k), with X an
+ * n_cols x k row-major matrix of leading dimension ldx (>= k) and Y an
+ * n_rows x k row-major matrix of leading dimension ldy (>= k).  Device
+ * pointers.  `plan` is accepted for symmetry and may be NULL.
+ *
+ * Replaces CSRMatMul::eval_gpu (reference:
+ * src/sparse/csr_matmul/csr_matmul.cpp:260-300) and the Metal kernels
+ * csr_matmul_* (reference: src/sparse/csr_matmul/csr_matmul.metal:17-135).
+ */
+msx_status msx_csr_spmm(msx_vtype vt, msx_itype it, int64_t n_rows,
+                        int64_t n_cols, int64_t nnz, const void *data,
+                        const void *indices, const void *indptr, int64_t k,
+                        const void *X, int64_t ldx, void *Y, int64_t ldy,
+                        const msx_csr_plan *plan, void *stream);
+
+/*
+ * Host (CPU) SpMV with host pointers, the `use_cpu()` device: rows are summed
+ * sequentially in stored order, rows are split over `n_threads` std::threads
+ * in nnz-balanced contiguous ranges (n_threads <= 0: the resolved worker
+ * count of msx_cpu_worker_count).  Output is independent of n_threads.
+ *
+ * Replaces csr_matvec_cpu_impl / CSRMatVec::eval_cpu (reference:
+ * src/sparse/csr_matvec/csr_matvec.cpp:79-200).
+ */
+msx_status msx_csr_spmv_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                            int64_t n_cols, int64_t nnz, const void *data,
+                            const void *indices, const void *indptr,
+                            const void *x, void *y, int n_threads);
+
+/*
+ * Host (CPU) SpMM, contiguous row-major X (n_cols x k) and Y (n_rows x k).
+ *
+ * Replaces csr_matmul_cpu_impl / CSRMatMul::eval_cpu (reference:
+ * src/sparse/csr_matmul/csr_matmul.cpp:83-257).
+ */
+msx_status msx_csr_spmm_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                            int64_t n_cols, int64_t nnz, const void *data,
+                            const void *indices, const void *indptr,
+                            int64_t k, const void *X, void *Y, int n_threads);
+
+/*
+ * CPU worker count resolved from the environment: MLX_SPARSE_CPU_THREADS,
+ * then MLX_SPARSE_N_THREADS, then OMP_NUM_THREADS, SLURM_CPUS_PER_TASK,
+ * PBS_NP, LSB_DJOB_NUMPROC, NSLOTS, then the process affinity mask, then
+ * hardware concurrency.
+ *
+ * Replaces configured_cpu_worker_count (reference:
+ * src/common/cpu_parallel.cpp:97-135).
+ */
+int msx_cpu_worker_count(void);
+
+/*
+ * Contiguous row ranges for `n` rows of per-row work `work` over `parts`
+ * workers: equal ranges when all rows carry the same work, otherwise
+ * work-balanced ranges (ceil targets, each range non-empty).  Writes
+ * *n_ranges pairs (begin, end) into `ranges` (capacity 2 * parts int64).
+ *
+ * Replaces cpu_ranges_for_output_work / equal_cpu_ranges /
+ * weighted_cpu_ranges (reference: src/common/cpu_parallel.h:134-164,
+ * src/common/cpu_parallel.cpp:183-253).
+ */
+msx_status msx_cpu_ranges(const int64_t *work, int64_t n, int parts,
+                          int64_t *ranges, int64_t *n_ranges);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MSX_SPARSE_H */

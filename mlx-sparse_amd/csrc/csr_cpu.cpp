@@ -1,0 +1,456 @@
+// csr_cpu.cpp - host SpMV / SpMM for the `use_cpu()` device.
+//
+// Restates the reference CPU backend on plain host pointers:
+//   - rows summed sequentially in stored order in the accumulator type;
+//     SpMV rows of length 1..4 start from their first product, longer rows
+//     from zero (reference: src/sparse/csr_matvec/csr_matvec.cpp:79-114);
+//   - SpMM keeps one accumulator per RHS column and sums each from zero in
+//     stored order (reference: src/sparse/csr_matmul/csr_matmul.cpp:83-133);
+//   - per call: an O(n) row-work prepass, contiguous work-balanced row ranges
+//     and one std::thread per extra range, the first exception rethrown on
+//     the caller (reference: csr_matvec.cpp:116-168, csr_matmul.cpp:172-222,
+//     src/common/cpu_parallel.h:50-164, src/common/cpu_parallel.cpp:97-253).
+// Threads own disjoint rows, so the output does not depend on the thread
+// count.  Compiled without -ffp-contract: every product and sum is rounded
+// on its own.
+#include <sched.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
+#include <exception>
+#include <limits>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "msx_sparse.h"
+
+namespace msx {
+msx_status fail(msx_status code, const std::string &msg);
+void clear_error();
+}  // namespace msx
+
+namespace msx {
+namespace cpu {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Value types on the host.
+
+struct cf32 {
+  float re, im;
+};
+
+inline float bits_to_float(uint32_t u) {
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+inline uint32_t float_to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  return u;
+}
+
+// binary16 -> binary32, exact.
+float half_to_float(uint16_t h) {
+  const uint32_t s = static_cast<uint32_t>(h >> 15) << 31;
+  const uint32_t e = (h >> 10) & 31u;
+  const uint32_t m = h & 1023u;
+  if (e == 31) return bits_to_float(s | 0x7f800000u | (m << 13));
+  if (e != 0) return bits_to_float(s | ((e + 112u) << 23) | (m << 13));
+  if (m == 0) return bits_to_float(s);
+  // subnormal: normalise the significand
+  int shift = 0;
+  uint32_t mm = m;
+  while ((mm & 1024u) == 0) {
+    mm <<= 1;
+    ++shift;
+  }
+  return bits_to_float(s | ((113u - shift) << 23) | ((mm & 1023u) << 13));
+}
+
+// binary32 -> binary16, round to nearest even.  Works on the magnitude in
+// units of the target's last place: the binary16 grid below 2^-14 is uniform
+// (2^-24 steps), above it the exponent field is rebased.
+uint16_t float_to_half(float f) {
+  const uint32_t u = float_to_bits(f);
+  const uint16_t s = static_cast<uint16_t>((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return static_cast<uint16_t>(s | (a > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  const int e = static_cast<int>(a >> 23) - 127;
+  if (e >= 16) return static_cast<uint16_t>(s | 0x7c00u);
+  uint32_t sig = (a & 0x7fffffu) | (a >= 0x00800000u ? 0x800000u : 0u);
+  // number of low bits of the 24-bit significand that fall below the
+  // binary16 last place at this exponent
+  int drop = e < -14 ? (13 + (-14 - e)) : 13;
+  if (a < 0x00800000u) drop = 13 + 14 + 112;  // binary32 subnormal: far below 2^-24
+  if (drop > 31) return s;
+  uint32_t q = sig >> drop;
+  const uint32_t rem = sig & ((1u << drop) - 1u);
+  const uint32_t half = 1u << (drop - 1);
+  if (rem > half || (rem == half && (q & 1u))) ++q;
+  if (e < -14) return static_cast<uint16_t>(s | q);  // subnormal (q may round up to 0x400)
+  // normal: q holds the implicit bit at 2^10; carry may bump the exponent
+  const uint32_t biased = static_cast<uint32_t>(e + 15);
+  const uint32_t out = (biased << 10) + (q - 1024u);
+  return static_cast<uint16_t>(s | std::min<uint32_t>(out, 0x7c00u));
+}
+
+float bf16_to_float(uint16_t b) { return bits_to_float(static_cast<uint32_t>(b) << 16); }
+
+uint16_t float_to_bf16(float f) {
+  uint32_t u = float_to_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+struct F32 {
+  using S = float;
+  using A = float;
+  static A widen(S v) { return v; }
+  static S narrow(A v) { return v; }
+  static A mul(S a, S b) { return a * b; }
+};
+struct F16 {
+  using S = uint16_t;
+  using A = float;
+  static A widen(S v) { return half_to_float(v); }
+  static S narrow(A v) { return float_to_half(v); }
+  static A mul(S a, S b) { return half_to_float(a) * half_to_float(b); }
+};
+struct BF16 {
+  using S = uint16_t;
+  using A = float;
+  static A widen(S v) { return bf16_to_float(v); }
+  static S narrow(A v) { return float_to_bf16(v); }
+  static A mul(S a, S b) { return bf16_to_float(a) * bf16_to_float(b); }
+};
+struct C64 {
+  using S = cf32;
+  using A = cf32;
+  static A widen(S v) { return v; }
+  static S narrow(A v) { return v; }
+  static A mul(S a, S b) {
+    const float rr = a.re * b.re, ii = a.im * b.im, ri = a.re * b.im, ir = a.im * b.re;
+    return cf32{rr - ii, ri + ir};
+  }
+};
+
+inline float add(float a, float b) { return a + b; }
+inline cf32 add(cf32 a, cf32 b) { return cf32{a.re + b.re, a.im + b.im}; }
+
+// ---------------------------------------------------------------------------
+// Worker count and ranges.
+
+int parse_positive(const char *v) {
+  if (v == nullptr || *v == '\0') return 0;
+  char *end = nullptr;
+  const long x = std::strtol(v, &end, 10);
+  if (end == v || x <= 0 || x > std::numeric_limits<int>::max()) return 0;
+  if (*end != '\0' && *end != ',') return 0;
+  return static_cast<int>(x);
+}
+
+int auto_workers() {
+  if (int c = parse_positive(std::getenv("OMP_NUM_THREADS")); c > 0) return c;
+  for (const char *name : {"SLURM_CPUS_PER_TASK", "PBS_NP", "LSB_DJOB_NUMPROC", "NSLOTS"})
+    if (int c = parse_positive(std::getenv(name)); c > 0) return c;
+  cpu_set_t set;
+  CPU_ZERO(&set);
+  if (sched_getaffinity(0, sizeof(set), &set) == 0)
+    if (int c = CPU_COUNT(&set); c > 0) return c;
+  const int hw = static_cast<int>(std::thread::hardware_concurrency());
+  return hw > 0 ? hw : 1;
+}
+
+struct Range {
+  int64_t begin, end;
+};
+
+std::vector<Range> equal_ranges(int64_t n, int parts) {
+  std::vector<Range> out;
+  if (n <= 0) return out;
+  const int count = std::max(1, parts);
+  for (int p = 0; p < count; ++p) {
+    const int64_t b = (static_cast<int64_t>(p) * n) / count;
+    const int64_t e = (static_cast<int64_t>(p + 1) * n) / count;
+    if (b < e) out.push_back({b, e});
+  }
+  return out;
+}
+
+std::vector<Range> weighted_ranges(const std::vector<int64_t> &work, int parts) {
+  const int64_t n = static_cast<int64_t>(work.size());
+  if (n <= 0) return {};
+  const int count = std::max(1, parts);
+  if (count == 1) return {{0, n}};
+  if (count >= n) return equal_ranges(n, count);
+  std::vector<int64_t> prefix(static_cast<size_t>(n) + 1, 0);
+  for (int64_t r = 0; r < n; ++r) {
+    const int64_t next = prefix[r] + std::max<int64_t>(0, work[r]);
+    prefix[r + 1] = next < prefix[r] ? std::numeric_limits<int64_t>::max() : next;
+  }
+  if (prefix.back() <= 0) return equal_ranges(n, count);
+  std::vector<Range> out;
+  int64_t begin = 0;
+  for (int part = 0; part < count && begin < n; ++part) {
+    const int left = count - part;
+    if (left == 1) {
+      out.push_back({begin, n});
+      break;
+    }
+    const int64_t target = prefix[begin] + (prefix.back() - prefix[begin] + left - 1) / left;
+    int64_t end = std::lower_bound(prefix.begin() + begin + 1, prefix.end(), target) - prefix.begin();
+    end = std::max(end, begin + 1);
+    end = std::min(end, n - (left - 1));
+    out.push_back({begin, end});
+    begin = end;
+  }
+  return out;
+}
+
+std::vector<Range> ranges_for_work(const std::vector<int64_t> &work, int parts) {
+  if (work.empty()) return {};
+  const int64_t n = static_cast<int64_t>(work.size());
+  if (parts <= 1) return {{0, n}};
+  bool uneven = false;
+  for (size_t i = 1; i < work.size() && !uneven; ++i)
+    uneven = std::max<int64_t>(0, work[i]) != std::max<int64_t>(0, work[i - 1]);
+  return uneven ? weighted_ranges(work, parts) : equal_ranges(n, parts);
+}
+
+template <class Fn>
+void parallel_for(const std::vector<Range> &ranges, Fn &&fn) {
+  if (ranges.empty()) return;
+  if (ranges.size() == 1) {
+    fn(ranges[0]);
+    return;
+  }
+  std::atomic<bool> failed{false};
+  std::exception_ptr first = nullptr;
+  auto run = [&](Range r) {
+    if (failed.load(std::memory_order_relaxed)) return;
+    try {
+      fn(r);
+    } catch (...) {
+      bool expected = false;
+      if (failed.compare_exchange_strong(expected, true)) first = std::current_exception();
+    }
+  };
+  std::vector<std::thread> threads;
+  threads.reserve(ranges.size() - 1);
+  for (size_t i = 1; i < ranges.size(); ++i) threads.emplace_back(run, ranges[i]);
+  run(ranges[0]);
+  for (auto &t : threads) t.join();
+  if (first) std::rethrow_exception(first);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels.
+
+template <class I>
+inline int64_t at(const I *p, int64_t i) {
+  return static_cast<int64_t>(p[i]);
+}
+
+template <class V, class I>
+void spmv_rows(const typename V::S *data, const I *indices, const I *indptr,
+               const typename V::S *x, typename V::S *y, Range r) {
+  using A = typename V::A;
+  for (int64_t row = r.begin; row < r.end; ++row) {
+    const int64_t b = at(indptr, row), e = at(indptr, row + 1);
+    A acc{};
+    int64_t p = b;
+    if (e - b >= 1 && e - b <= 4) {
+      acc = V::mul(data[p], x[at(indices, p)]);
+      ++p;
+    }
+    for (; p < e; ++p) acc = add(acc, V::mul(data[p], x[at(indices, p)]));
+    y[row] = V::narrow(acc);
+  }
+}
+
+template <class V, class I>
+void spmm_rows(const typename V::S *data, const I *indices, const I *indptr,
+               const typename V::S *X, typename V::S *Y, int64_t k, Range r) {
+  using A = typename V::A;
+  std::vector<A> acc(static_cast<size_t>(std::max<int64_t>(k, 1)));
+  for (int64_t row = r.begin; row < r.end; ++row) {
+    std::fill(acc.begin(), acc.end(), A{});
+    for (int64_t p = at(indptr, row); p < at(indptr, row + 1); ++p) {
+      const typename V::S v = data[p];
+      const typename V::S *xr = X + at(indices, p) * k;
+      for (int64_t c = 0; c < k; ++c) acc[c] = add(acc[c], V::mul(v, xr[c]));
+    }
+    for (int64_t c = 0; c < k; ++c) Y[row * k + c] = V::narrow(acc[c]);
+  }
+}
+
+template <class I>
+std::vector<int64_t> row_work(const I *indptr, int64_t n, int64_t scale) {
+  std::vector<int64_t> w(static_cast<size_t>(n));
+  for (int64_t r = 0; r < n; ++r) w[r] = (at(indptr, r + 1) - at(indptr, r)) * scale;
+  return w;
+}
+
+template <class V, class I>
+void spmv(int64_t n, const void *data, const void *indices, const void *indptr, const void *x,
+          void *y, int workers) {
+  const auto *d = static_cast<const typename V::S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *xv = static_cast<const typename V::S *>(x);
+  auto *yv = static_cast<typename V::S *>(y);
+  auto body = [&](Range r) { spmv_rows<V, I>(d, ix, ip, xv, yv, r); };
+  if (workers <= 1 || n <= 0) return body({0, n});
+  const auto ranges = ranges_for_work(row_work(ip, n, 1), workers);
+  if (ranges.size() <= 1) return body({0, n});
+  parallel_for(ranges, body);
+}
+
+template <class V, class I>
+void spmm(int64_t n, int64_t k, const void *data, const void *indices, const void *indptr,
+          const void *X, void *Y, int workers) {
+  const auto *d = static_cast<const typename V::S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *xv = static_cast<const typename V::S *>(X);
+  auto *yv = static_cast<typename V::S *>(Y);
+  auto body = [&](Range r) { spmm_rows<V, I>(d, ix, ip, xv, yv, k, r); };
+  if (workers <= 1 || n <= 0) return body({0, n});
+  const auto ranges = ranges_for_work(row_work(ip, n, std::max<int64_t>(k, 1)), workers);
+  if (ranges.size() <= 1) return body({0, n});
+  parallel_for(ranges, body);
+}
+
+}  // namespace
+
+int worker_count() {
+  const char *raw = std::getenv("MLX_SPARSE_CPU_THREADS");
+  if (raw == nullptr || *raw == '\0') raw = std::getenv("MLX_SPARSE_N_THREADS");
+  if (int c = parse_positive(raw); c > 0) return c;
+  return auto_workers();
+}
+
+}  // namespace cpu
+}  // namespace msx
+
+using namespace msx;
+
+namespace {
+
+msx_status check_cpu(const char *op, msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                     int64_t nnz, const void *data, const void *indices, const void *indptr) {
+  if (it != MSX_I32 && it != MSX_I64)
+    return fail(MSX_ETYPE, std::string(op) + " requires int32 or int64 indices.");
+  if (vt < MSX_F32 || vt > MSX_C64) return fail(MSX_ETYPE, std::string(op) + " unsupported value dtype.");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0)
+    return fail(MSX_EINVAL, std::string(op) + " shape dimensions must be non-negative.");
+  if (indptr == nullptr) return fail(MSX_EINVAL, std::string(op) + " indptr is NULL.");
+  if (nnz > 0 && (data == nullptr || indices == nullptr))
+    return fail(MSX_EINVAL, std::string(op) + " data and indices must be non-NULL when nnz > 0.");
+  return MSX_OK;
+}
+
+template <class Fn>
+msx_status guarded(const char *op, Fn &&fn) {
+  try {
+    fn();
+  } catch (const std::bad_alloc &) {
+    return fail(MSX_ENOMEM, std::string(op) + ": host allocation failed.");
+  } catch (const std::exception &e) {
+    return fail(MSX_EINVAL, std::string(op) + ": " + e.what());
+  }
+  return MSX_OK;
+}
+
+}  // namespace
+
+extern "C" msx_status msx_csr_spmv_cpu(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                                       int64_t nnz, const void *data, const void *indices,
+                                       const void *indptr, const void *x, void *y, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matvec", vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (n_rows > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec y is NULL.");
+  const int workers = n_threads > 0 ? n_threads : cpu::worker_count();
+  return guarded("csr_matvec", [&] {
+    const bool i64 = it == MSX_I64;
+    switch (vt) {
+    case MSX_F32:
+      i64 ? cpu::spmv<cpu::F32, int64_t>(n_rows, data, indices, indptr, x, y, workers)
+          : cpu::spmv<cpu::F32, int32_t>(n_rows, data, indices, indptr, x, y, workers);
+      break;
+    case MSX_F16:
+      i64 ? cpu::spmv<cpu::F16, int64_t>(n_rows, data, indices, indptr, x, y, workers)
+          : cpu::spmv<cpu::F16, int32_t>(n_rows, data, indices, indptr, x, y, workers);
+      break;
+    case MSX_BF16:
+      i64 ? cpu::spmv<cpu::BF16, int64_t>(n_rows, data, indices, indptr, x, y, workers)
+          : cpu::spmv<cpu::BF16, int32_t>(n_rows, data, indices, indptr, x, y, workers);
+      break;
+    case MSX_C64:
+      i64 ? cpu::spmv<cpu::C64, int64_t>(n_rows, data, indices, indptr, x, y, workers)
+          : cpu::spmv<cpu::C64, int32_t>(n_rows, data, indices, indptr, x, y, workers);
+      break;
+    }
+  });
+}
+
+extern "C" msx_status msx_csr_spmm_cpu(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                                       int64_t nnz, const void *data, const void *indices,
+                                       const void *indptr, int64_t k, const void *X, void *Y,
+                                       int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matmul", vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (k < 0) return fail(MSX_EINVAL, "csr_matmul rhs column count must be non-negative.");
+  if (n_rows > 0 && k > 0 && Y == nullptr) return fail(MSX_EINVAL, "csr_matmul Y is NULL.");
+  const int workers = n_threads > 0 ? n_threads : cpu::worker_count();
+  return guarded("csr_matmul", [&] {
+    const bool i64 = it == MSX_I64;
+    switch (vt) {
+    case MSX_F32:
+      i64 ? cpu::spmm<cpu::F32, int64_t>(n_rows, k, data, indices, indptr, X, Y, workers)
+          : cpu::spmm<cpu::F32, int32_t>(n_rows, k, data, indices, indptr, X, Y, workers);
+      break;
+    case MSX_F16:
+      i64 ? cpu::spmm<cpu::F16, int64_t>(n_rows, k, data, indices, indptr, X, Y, workers)
+          : cpu::spmm<cpu::F16, int32_t>(n_rows, k, data, indices, indptr, X, Y, workers);
+      break;
+    case MSX_BF16:
+      i64 ? cpu::spmm<cpu::BF16, int64_t>(n_rows, k, data, indices, indptr, X, Y, workers)
+          : cpu::spmm<cpu::BF16, int32_t>(n_rows, k, data, indices, indptr, X, Y, workers);
+      break;
+    case MSX_C64:
+      i64 ? cpu::spmm<cpu::C64, int64_t>(n_rows, k, data, indices, indptr, X, Y, workers)
+          : cpu::spmm<cpu::C64, int32_t>(n_rows, k, data, indices, indptr, X, Y, workers);
+      break;
+    }
+  });
+}
+
+extern "C" int msx_cpu_worker_count(void) { return cpu::worker_count(); }
+
+extern "C" msx_status msx_cpu_ranges(const int64_t *work, int64_t n, int parts, int64_t *ranges,
+                                     int64_t *n_ranges) {
+  clear_error();
+  if (n < 0 || (n > 0 && work == nullptr) || ranges == nullptr || n_ranges == nullptr)
+    return fail(MSX_EINVAL, "msx_cpu_ranges: invalid arguments.");
+  return guarded("msx_cpu_ranges", [&] {
+    std::vector<int64_t> w(work, work + n);
+    const auto r = cpu::ranges_for_work(w, parts);
+    for (size_t i = 0; i < r.size(); ++i) {
+      ranges[2 * i] = r[i].begin;
+      ranges[2 * i + 1] = r[i].end;
+    }
+    *n_ranges = static_cast<int64_t>(r.size());
+  });
+}

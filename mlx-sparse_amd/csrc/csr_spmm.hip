@@ -1,0 +1,192 @@
+// csr_spmm.hip - CSR SpMM with a dense row-major right-hand side, gfx950.
+//
+//   Y[i, c] = sum_{p in [indptr[i], indptr[i+1])} data[p] * X[indices[p], c]
+//
+// The reference launches one Metal thread per output element (or 128 lanes
+// per element), so each row's indices/data are re-read k times (reference:
+// src/sparse/csr_matmul/csr_matmul.metal:17-39,86-120).  Here one group of LR
+// lanes owns a whole row of Y: each lane holds CW consecutive columns in
+// registers (CW * sizeof(value) = 16 bytes when the layout allows, else 1
+// column), walks the row's stored values once in order, and reads the
+// matching X row as one 16-byte load per lane, so the LR lanes together read
+// a contiguous X row segment.  A row's indices and data are read once per
+// column tile of 64 * CW columns instead of once per column.  Each column is
+// summed from zero in stored order - the reference's CPU order
+// (src/sparse/csr_matmul/csr_matmul.cpp:83-133) - so float32 results match
+// its CPU kernel bit for bit.  The value loop issues four X loads before
+// the first use to keep several gathers in flight per lane.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "msx_device.h"
+#include "msx_internal.h"
+
+namespace msx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kMaxGrid = 1u << 20;
+constexpr int kUnroll = 4;
+
+template <class S, int CW>
+struct Vec {
+  S v[CW];
+};
+
+template <class S, int CW>
+__device__ inline Vec<S, CW> load_vec(const S *p) {
+  if constexpr (CW * sizeof(S) == 16) {
+    const uint4 raw = *reinterpret_cast<const uint4 *>(p);
+    return __builtin_bit_cast(Vec<S, CW>, raw);
+  } else {
+    Vec<S, CW> r;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) r.v[c] = p[c];
+    return r;
+  }
+}
+
+template <class S, int CW>
+__device__ inline void store_vec(S *p, const Vec<S, CW> &v) {
+  if constexpr (CW * sizeof(S) == 16) {
+    *reinterpret_cast<uint4 *>(p) = __builtin_bit_cast(uint4, v);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CW; ++c) p[c] = v.v[c];
+  }
+}
+
+__device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+template <class V, class I, int CW>
+__global__ void __launch_bounds__(kThreads)
+    spmm_rows(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+              const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
+              int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
+              int64_t nnz, int64_t n_cols, int64_t k, int LR, int64_t n_col_tiles) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  const int rows_per_group = kThreads / LR;
+  const int g = threadIdx.x / LR;
+  const int l = threadIdx.x % LR;
+  const int64_t tile_cols = static_cast<int64_t>(LR) * CW;
+  const int64_t n_row_tiles = (n_rows + rows_per_group - 1) / rows_per_group;
+  const int64_t n_tiles = n_row_tiles * n_col_tiles;
+  for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_tiles; t += gridDim.x) {
+    const int64_t rt = t / n_col_tiles;
+    const int64_t ct = t - rt * n_col_tiles;
+    const int64_t row = rt * rows_per_group + g;
+    const int64_t col = ct * tile_cols + static_cast<int64_t>(l) * CW;
+    if (row >= n_rows || col >= k) continue;
+    A acc[CW];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) acc[c] = vzero<A>();
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    int64_t p = s;
+    for (; p + kUnroll <= e; p += kUnroll) {
+      int64_t ci[kUnroll];
+      A av[kUnroll];
+      Vec<S, CW> xv[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        ci[u] = static_cast<int64_t>(indices[p + u]);
+        av[u] = V::widen(data[p + u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (static_cast<uint64_t>(ci[u]) < static_cast<uint64_t>(n_cols))
+          xv[u] = load_vec<S, CW>(X + ci[u] * ldx + col);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (static_cast<uint64_t>(ci[u]) < static_cast<uint64_t>(n_cols)) {
+#pragma unroll
+          for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(av[u], xv[u].v[c]));
+        }
+      }
+    }
+    for (; p < e; ++p) {
+      const int64_t cidx = static_cast<int64_t>(indices[p]);
+      if (static_cast<uint64_t>(cidx) < static_cast<uint64_t>(n_cols)) {
+        const A a = V::widen(data[p]);
+        const Vec<S, CW> xv = load_vec<S, CW>(X + cidx * ldx + col);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(a, xv.v[c]));
+      }
+    }
+    Vec<S, CW> out;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) out.v[c] = V::narrow(acc[c]);
+    store_vec<S, CW>(Y + row * ldy + col, out);
+  }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <class V, class I>
+msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data_v,
+                      const void *indices_v, const void *indptr_v, int64_t k, const void *X_v,
+                      int64_t ldx, void *Y_v, int64_t ldy, hipStream_t stream) {
+  using S = typename V::Storage;
+  constexpr int CWV = static_cast<int>(16 / sizeof(S));
+  const auto *data = static_cast<const S *>(data_v);
+  const auto *indices = static_cast<const I *>(indices_v);
+  const auto *indptr = static_cast<const I *>(indptr_v);
+  const auto *X = static_cast<const S *>(X_v);
+  auto *Y = static_cast<S *>(Y_v);
+  const bool vec = (k % CWV) == 0 && (ldx % CWV) == 0 && (ldy % CWV) == 0 && aligned16(X) &&
+                   aligned16(Y);
+  const int CW = vec ? CWV : 1;
+  const int64_t lanes = (k + CW - 1) / CW;
+  int LR = 1;
+  while (LR < lanes && LR < 64) LR <<= 1;
+  const int64_t n_col_tiles = (k + static_cast<int64_t>(LR) * CW - 1) / (static_cast<int64_t>(LR) * CW);
+  const int64_t rows_per_group = kThreads / LR;
+  const int64_t tiles = ((n_rows + rows_per_group - 1) / rows_per_group) * n_col_tiles;
+  const uint32_t grid = static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(tiles, kMaxGrid)));
+  if (vec) {
+    hipLaunchKernelGGL((spmm_rows<V, I, CWV>), dim3(grid), dim3(kThreads), 0, stream, data,
+                       indices, indptr, X, ldx, Y, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles);
+  } else {
+    hipLaunchKernelGGL((spmm_rows<V, I, 1>), dim3(grid), dim3(kThreads), 0, stream, data, indices,
+                       indptr, X, ldx, Y, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles);
+  }
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+template <class V>
+msx_status spmm_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                   const void *indices, const void *indptr, int64_t k, const void *X, int64_t ldx,
+                   void *Y, int64_t ldy, hipStream_t stream) {
+  if (it == MSX_I32)
+    return spmm_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
+                                  stream);
+  return spmm_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
+                                stream);
+}
+
+}  // namespace
+
+msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                       const void *data, const void *indices, const void *indptr, int64_t k,
+                       const void *X, int64_t ldx, void *Y, int64_t ldy, hipStream_t stream) {
+  switch (vt) {
+  case MSX_F32:
+    return spmm_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
+  case MSX_F16:
+    return spmm_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
+  case MSX_BF16:
+    return spmm_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
+                         stream);
+  case MSX_C64:
+    return spmm_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
+  }
+  return fail(MSX_ETYPE, "csr_matmul unsupported value dtype.");
+}
+
+}  // namespace msx

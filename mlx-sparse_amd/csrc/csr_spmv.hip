@@ -1,0 +1,331 @@
+// csr_spmv.hip - CSR SpMV kernels for gfx950.
+//
+//   y[i] = sum_{p in [indptr[i], indptr[i+1])} data[p] * x[indices[p]]
+//
+// The reference computes this with one Metal thread per row, or a 128-lane
+// threadgroup per row when nnz >= 32 * n_rows, each lane reading data/indices
+// strided by the row length (reference:
+// src/sparse/csr_matvec/csr_matvec.metal:17-36,76-108).  Here the work comes
+// from a row-block plan (csr_plan.hip):
+//
+//   spmv_blocks      one wavefront per short block (< 2W values, <= R rows).
+//                    Phase 1 streams the block's contiguous indices/data with
+//                    16-32 byte buffer loads (4 values per lane per step; the
+//                    buffer descriptor returns zero past the array end, so the
+//                    ragged edges need no scalar tail), gathers x, and stages
+//                    the products in LDS.  Phase 2 sums each row from LDS:
+//                    one lane per row in stored order when rows average <= 32
+//                    values (the reference's summation order, so results
+//                    match its CPU kernel bit for bit), otherwise L lanes per
+//                    row and an XOR butterfly.
+//   spmv_long        one 256-thread workgroup per C-value chunk of a long
+//                    row; a fixed-order tree gives each chunk's sum.
+//   spmv_long_fixup  one wavefront per multi-chunk row adds the chunk sums.
+//   spmv_rowgroup    plan-free kernel: G lanes per row, G from the mean row
+//                    length.  Used without a plan or for misaligned buffers.
+//
+// Every x gather is guarded by 0 <= col < n_cols (an out-of-range column
+// adds nothing), and row bounds are clamped to [0, nnz], so malformed CSR
+// input cannot read outside the caller's buffers.  No atomics: repeated
+// calls produce identical bits.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "msx_device.h"
+#include "msx_internal.h"
+
+namespace msx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerGroup = kThreads / kWave;
+constexpr uint32_t kMaxGrid = 1u << 20;  // workgroups per launch; kernels stride beyond
+constexpr size_t kMaxLds = 64 * 1024;    // LDS requested per workgroup, at most
+
+__device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// --------------------------------------------------------------------------
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    spmv_blocks(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
+                typename V::Storage *__restrict__ y, const int32_t *__restrict__ block_row_begin,
+                int64_t n_blocks, int64_t nnz, int64_t n_cols, int W) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  extern __shared__ char lds_raw[];
+  const int lane = threadIdx.x % kWave;
+  // wave-uniform by construction; readfirstlane lets the compiler keep the
+  // block's buffer descriptors in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int cap = 2 * W + 4;
+  A *lds = reinterpret_cast<A *>(lds_raw) + wave * cap;
+
+  const uint32_t first = xcd_remap(blockIdx.x, gridDim.x);
+  for (int64_t wg = first; wg * kWavesPerGroup < n_blocks; wg += gridDim.x) {
+    const int64_t b = wg * kWavesPerGroup + wave;
+    if (b >= n_blocks) break;
+    const int64_t r0 = block_row_begin[b];
+    const int64_t r1 = block_row_begin[b + 1];
+    const int64_t m = r1 - r0;
+    const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+    const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0,
+                               std::min<int64_t>(nnz, p0 + 2 * W - 1));
+    const int64_t a0 = p0 & ~int64_t{3};
+    const int nq = static_cast<int>((p1 - a0 + 3) >> 2);
+
+    // Phase 1: products of the block's values into LDS, index q - a0.
+    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(nnz - a0) * sizeof(I));
+    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
+#pragma unroll 2
+    for (int q = lane; q < nq; q += kWave) {
+      const Quad<I> iq = load_quad<I>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
+      const Quad<S> dq = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t pos = a0 + 4 * q + e;
+        const int64_t col = static_cast<int64_t>(iq.v[e]);
+        A prod = vzero<A>();
+        if (pos >= p0 && pos < p1 && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+          prod = vmul<V>(dq.v[e], x[col]);
+        lds[4 * q + e] = prod;
+      }
+    }
+    wave_lds_sync();
+
+    // Phase 2: row sums from LDS.
+    const int64_t avg = m > 0 ? (p1 - p0) / m : 0;
+    int L = 1;
+    if (avg > 32 && m <= 32) {
+      L = kWave;
+      while (L * m > kWave) L >>= 1;
+    }
+    const int rows_per_pass = kWave / L;
+    const int g = lane / L;
+    const int j = lane % L;
+    for (int64_t i0 = 0; i0 < m; i0 += rows_per_pass) {
+      const int64_t i = i0 + g;
+      A acc = vzero<A>();
+      if (i < m) {
+        const int64_t s = clamp64(static_cast<int64_t>(indptr[r0 + i]), p0, p1);
+        const int64_t e = clamp64(static_cast<int64_t>(indptr[r0 + i + 1]), s, p1);
+        for (int64_t q = s + j; q < e; q += L) acc = vadd(acc, lds[q - a0]);
+      }
+      for (int d = L >> 1; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
+      if (i < m && j == 0) y[r0 + i] = V::narrow(acc);
+    }
+    wave_lds_sync();  // LDS is rewritten by the next block of this wave
+  }
+}
+
+// --------------------------------------------------------------------------
+template <class A>
+__device__ inline A block_sum(A v, A *lds4) {
+  // fixed-order tree: XOR butterfly in each wave, then waves 0..3 in order
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) v = vadd(v, shfl_xor(v, d));
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  if (lane == 0) lds4[wave] = v;
+  __syncthreads();
+  A total = lds4[0];
+  for (int w = 1; w < kWavesPerGroup; ++w) total = vadd(total, lds4[w]);
+  __syncthreads();
+  return total;
+}
+
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    spmv_long(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+              const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
+              typename V::Storage *__restrict__ y, const int32_t *__restrict__ long_rows,
+              const int32_t *__restrict__ long_chunk_begin, const int32_t *__restrict__ chunk_row,
+              typename V::Acc *__restrict__ partials, int64_t n_chunks, int64_t nnz,
+              int64_t n_cols, int64_t C) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  __shared__ A lds4[kWavesPerGroup];
+  for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    const int32_t li = chunk_row[c];
+    const int64_t row = long_rows[li];
+    const int64_t c_first = long_chunk_begin[li];
+    const int64_t n_ch = long_chunk_begin[li + 1] - c_first;
+    const int64_t rb = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t re = clamp64(static_cast<int64_t>(indptr[row + 1]), rb, nnz);
+    const int64_t q0 = std::min(rb + (c - c_first) * C, re);
+    const int64_t q1 = std::min(q0 + C, re);
+    const int64_t a0 = q0 & ~int64_t{3};
+    const int nq = static_cast<int>((q1 - a0 + 3) >> 2);
+    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(nnz - a0) * sizeof(I));
+    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
+    A acc = vzero<A>();
+#pragma unroll 2
+    for (int q = threadIdx.x; q < nq; q += kThreads) {
+      const Quad<I> iq = load_quad<I>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
+      const Quad<S> dq = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t pos = a0 + 4 * q + e;
+        const int64_t col = static_cast<int64_t>(iq.v[e]);
+        if (pos >= q0 && pos < q1 && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+          acc = vadd(acc, vmul<V>(dq.v[e], x[col]));
+      }
+    }
+    const A total = block_sum(acc, lds4);
+    if (threadIdx.x == 0) {
+      if (n_ch == 1)
+        y[row] = V::narrow(total);
+      else
+        partials[c] = total;
+    }
+  }
+}
+
+template <class V>
+__global__ void __launch_bounds__(kThreads)
+    spmv_long_fixup(typename V::Storage *__restrict__ y, const int32_t *__restrict__ long_rows,
+                    const int32_t *__restrict__ long_chunk_begin,
+                    const typename V::Acc *__restrict__ partials, int64_t n_long) {
+  using A = typename V::Acc;
+  const int lane = threadIdx.x % kWave;
+  const int64_t li = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + threadIdx.x / kWave;
+  if (li >= n_long) return;
+  const int64_t c0 = long_chunk_begin[li];
+  const int64_t c1 = long_chunk_begin[li + 1];
+  if (c1 - c0 <= 1) return;
+  A acc = vzero<A>();
+  for (int64_t c = c0 + lane; c < c1; c += kWave) acc = vadd(acc, partials[c]);
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
+  if (lane == 0) y[long_rows[li]] = V::narrow(acc);
+}
+
+// --------------------------------------------------------------------------
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    spmv_rowgroup(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                  const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
+                  typename V::Storage *__restrict__ y, int64_t n_rows, int64_t nnz,
+                  int64_t n_cols, int G) {
+  using A = typename V::Acc;
+  const int rows_per_group = kThreads / G;
+  const int g = threadIdx.x / G;
+  const int j = threadIdx.x % G;
+  const int64_t n_tiles = (n_rows + rows_per_group - 1) / rows_per_group;
+  for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_tiles; t += gridDim.x) {
+    const int64_t row = t * rows_per_group + g;
+    A acc = vzero<A>();
+    if (row < n_rows) {
+      const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+      const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+      for (int64_t q = s + j; q < e; q += G) {
+        const int64_t col = static_cast<int64_t>(indices[q]);
+        if (static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+          acc = vadd(acc, vmul<V>(data[q], x[col]));
+      }
+    }
+    for (int d = G >> 1; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
+    if (row < n_rows && j == 0) y[row] = V::narrow(acc);
+  }
+}
+
+// --------------------------------------------------------------------------
+uint32_t grid_for(int64_t tiles) {
+  return static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(tiles, kMaxGrid)));
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+template <class V, class I>
+msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data_v,
+                      const void *indices_v, const void *indptr_v, const void *x_v, void *y_v,
+                      const msx_csr_plan *plan, hipStream_t stream) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  const auto *data = static_cast<const S *>(data_v);
+  const auto *indices = static_cast<const I *>(indices_v);
+  const auto *indptr = static_cast<const I *>(indptr_v);
+  const auto *x = static_cast<const S *>(x_v);
+  auto *y = static_cast<S *>(y_v);
+  // Quad loads of 4 values: require the streams aligned to their quad size
+  // (capped at 16 bytes).
+  const bool quads_ok = aligned(data, std::min<size_t>(16, 4 * sizeof(S))) &&
+                        aligned(indices, std::min<size_t>(16, 4 * sizeof(I)));
+  const size_t plan_lds =
+      plan ? static_cast<size_t>(kWavesPerGroup) * (2 * plan->block_nnz + 4) * sizeof(A) : 0;
+  if (plan != nullptr && quads_ok && plan_lds <= kMaxLds) {
+    if (plan->n_blocks > 0) {
+      const int W = static_cast<int>(plan->block_nnz);
+      const size_t lds = plan_lds;
+      const int64_t groups = (plan->n_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
+      hipLaunchKernelGGL((spmv_blocks<V, I>), dim3(grid_for(groups)), dim3(kThreads), lds, stream,
+                         data, indices, indptr, x, y, plan->block_row_begin, plan->n_blocks, nnz,
+                         n_cols, W);
+      MSX_HIP_TRY(hipGetLastError());
+    }
+    if (plan->n_chunks > 0) {
+      hipLaunchKernelGGL((spmv_long<V, I>), dim3(grid_for(plan->n_chunks)), dim3(kThreads), 0,
+                         stream, data, indices, indptr, x, y, plan->long_rows,
+                         plan->long_chunk_begin, plan->chunk_row,
+                         static_cast<A *>(plan->partials), plan->n_chunks, nnz, n_cols,
+                         plan->chunk_nnz);
+      MSX_HIP_TRY(hipGetLastError());
+      if (plan->n_chunks > plan->n_long) {
+        const int64_t groups = (plan->n_long + kWavesPerGroup - 1) / kWavesPerGroup;
+        hipLaunchKernelGGL((spmv_long_fixup<V>), dim3(static_cast<uint32_t>(groups)),
+                           dim3(kThreads), 0, stream, y, plan->long_rows, plan->long_chunk_begin,
+                           static_cast<const A *>(plan->partials), plan->n_long);
+        MSX_HIP_TRY(hipGetLastError());
+      }
+    }
+    return MSX_OK;
+  }
+  // Plan-free: G lanes per row, the power of two at or below the mean row
+  // length (1..64).
+  const int64_t avg = n_rows > 0 ? nnz / n_rows : 0;
+  int G = 1;
+  while (G < kWave && 2 * G <= avg) G <<= 1;
+  const int64_t tiles = (n_rows + (kThreads / G) - 1) / (kThreads / G);
+  hipLaunchKernelGGL((spmv_rowgroup<V, I>), dim3(grid_for(tiles)), dim3(kThreads), 0, stream, data,
+                     indices, indptr, x, y, n_rows, nnz, n_cols, G);
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+template <class V>
+msx_status spmv_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                   const void *indices, const void *indptr, const void *x, void *y,
+                   const msx_csr_plan *plan, hipStream_t stream) {
+  if (it == MSX_I32)
+    return spmv_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+  return spmv_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+}
+
+}  // namespace
+
+msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                       const void *data, const void *indices, const void *indptr, const void *x,
+                       void *y, const msx_csr_plan *plan, hipStream_t stream) {
+  switch (vt) {
+  case MSX_F32:
+    return spmv_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+  case MSX_F16:
+    return spmv_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+  case MSX_BF16:
+    return spmv_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+  case MSX_C64:
+    return spmv_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan, stream);
+  }
+  return fail(MSX_ETYPE, "csr_matvec unsupported value dtype.");
+}
+
+}  // namespace msx

@@ -1,0 +1,205 @@
+// msx_device.h - device-side value traits and memory helpers for gfx950.
+//
+// Value arithmetic follows the reference accumulator rules
+// (reference: src/common/common.h:52-79, src/common/metal_common.h:24-52):
+//   float32  : multiply and sum in float32;
+//   float16  : widen both operands to float32, multiply and sum in float32,
+//              round once to float16 (nearest even);
+//   bfloat16 : same with bfloat16 storage;
+//   complex64: textbook complex product, sum in complex64.
+// The library is compiled with -ffp-contract=off, so products and sums are
+// rounded separately, as in the reference's CPU kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "msx_sparse.h"
+
+namespace msx {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Value traits.  `Storage` is the element type in memory, `Acc` the type sums
+// are carried in.
+
+struct F32 {
+  using Storage = float;
+  using Acc = float;
+  static constexpr msx_vtype kType = MSX_F32;
+  __device__ static inline Acc widen(Storage v) { return v; }
+  __device__ static inline Storage narrow(Acc v) { return v; }
+};
+
+__device__ inline float half_bits_to_float(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Round-to-nearest-even float32 -> binary16 via the hardware conversion
+// (v_cvt_f16_f32 rounds to nearest even under the default mode).
+__device__ inline uint16_t float_to_half_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+__device__ inline float bf16_bits_to_float(uint16_t b) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float32 -> bfloat16 on the bit pattern; NaNs stay
+// NaN (quiet bit forced).
+__device__ inline uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+struct F16 {
+  using Storage = uint16_t;
+  using Acc = float;
+  static constexpr msx_vtype kType = MSX_F16;
+  __device__ static inline Acc widen(Storage v) { return half_bits_to_float(v); }
+  __device__ static inline Storage narrow(Acc v) { return float_to_half_bits(v); }
+};
+
+struct BF16 {
+  using Storage = uint16_t;
+  using Acc = float;
+  static constexpr msx_vtype kType = MSX_BF16;
+  __device__ static inline Acc widen(Storage v) { return bf16_bits_to_float(v); }
+  __device__ static inline Storage narrow(Acc v) { return float_to_bf16_bits(v); }
+};
+
+struct c64 {
+  float re, im;
+};
+
+struct C64 {
+  using Storage = c64;
+  using Acc = c64;
+  static constexpr msx_vtype kType = MSX_C64;
+  __device__ static inline Acc widen(Storage v) { return v; }
+  __device__ static inline Storage narrow(Acc v) { return v; }
+};
+
+// Product of two stored values in the accumulator type.
+template <class V>
+__device__ inline typename V::Acc vmul(typename V::Storage a, typename V::Storage b) {
+  return V::widen(a) * V::widen(b);
+}
+template <>
+__device__ inline c64 vmul<C64>(c64 a, c64 b) {
+  const float rr = a.re * b.re;
+  const float ii = a.im * b.im;
+  const float ri = a.re * b.im;
+  const float ir = a.im * b.re;
+  return c64{rr - ii, ri + ir};
+}
+
+// Product of a widened matrix value and a stored RHS value.
+template <class V>
+__device__ inline typename V::Acc vmul_acc(typename V::Acc a, typename V::Storage b) {
+  return a * V::widen(b);
+}
+template <>
+__device__ inline c64 vmul_acc<C64>(c64 a, c64 b) {
+  return vmul<C64>(a, b);
+}
+
+__device__ inline float vadd(float a, float b) { return a + b; }
+__device__ inline c64 vadd(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
+
+template <class A>
+__device__ inline A vzero() {
+  return A{};
+}
+
+// XOR butterfly exchange inside a wavefront.
+__device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ inline c64 shfl_xor(c64 v, int m) {
+  return c64{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources.  A raw buffer descriptor bounds every load to
+// [base, base + num_bytes): out-of-range lanes read zero instead of faulting,
+// which lets the edge chunks of a row block use full-width loads.
+
+constexpr int kBufferFlags = 0x00020000;  // gfx9 raw-buffer dword3
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t num_bytes) {
+  const uint32_t n = num_bytes > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(num_bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(n), kBufferFlags);
+}
+
+// Load N bytes (8, 16 or 32) at byte offset `off` from a buffer.
+template <int N>
+struct BufLoad;
+
+template <>
+struct BufLoad<8> {
+  using T = uint64_t;
+  __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return static_cast<uint64_t>(v[0]) | (static_cast<uint64_t>(v[1]) << 32);
+  }
+};
+
+struct u32x4 {
+  uint32_t w[4];
+};
+struct u32x8 {
+  uint32_t w[8];
+};
+
+template <>
+struct BufLoad<16> {
+  using T = u32x4;
+  __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return u32x4{{v[0], v[1], v[2], v[3]}};
+  }
+};
+
+template <>
+struct BufLoad<32> {
+  using T = u32x8;
+  __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    auto a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    auto b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+    return u32x8{{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}};
+  }
+};
+
+// Four consecutive elements of type E loaded as one vector from a buffer and
+// unpacked.
+template <class E>
+struct Quad {
+  E v[4];
+};
+
+template <class E>
+__device__ inline Quad<E> load_quad(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  static_assert(sizeof(E) == 2 || sizeof(E) == 4 || sizeof(E) == 8, "element size");
+  auto raw = BufLoad<4 * sizeof(E)>::load(r, byte_off);
+  return __builtin_bit_cast(Quad<E>, raw);
+}
+
+// ---------------------------------------------------------------------------
+// XCD-aware workgroup order.  The hardware hands workgroups to the 8 XCDs
+// round-robin (workgroup b runs on XCD b % 8).  Remapping b so each XCD
+// receives one contiguous run of logical tiles keeps neighbouring rows, and
+// the x / X entries they share, in one XCD's L2.
+constexpr int kNumXcd = 8;
+
+__device__ inline uint32_t xcd_remap(uint32_t b, uint32_t grid) {
+  const uint32_t q = grid / kNumXcd;
+  const uint32_t r = grid % kNumXcd;
+  const uint32_t xcd = b % kNumXcd;
+  const uint32_t slot = b / kNumXcd;
+  return xcd * q + (xcd < r ? xcd : r) + slot;
+}
+
+}  // namespace msx

@@ -1,0 +1,72 @@
+// msx_internal.h - host-side internals shared by the library's translation
+// units: error state, the plan object, argument checks and launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "msx_sparse.h"
+
+namespace msx {
+
+// Thread-local error text behind msx_last_error().
+void set_error(const std::string &msg);
+void clear_error();
+msx_status fail(msx_status code, const std::string &msg);
+msx_status hip_fail(hipError_t err, const char *what);
+
+#define MSX_HIP_TRY(expr)                                 \
+  do {                                                    \
+    hipError_t _e = (expr);                               \
+    if (_e != hipSuccess) return ::msx::hip_fail(_e, #expr); \
+  } while (0)
+
+size_t value_bytes(msx_vtype vt);
+size_t index_bytes(msx_itype it);
+bool valid_vtype(int vt);
+bool valid_itype(int it);
+
+// Plan defaults.  W: window of the nnz range that a short block's row starts
+// fall in (block nnz < 2W); R: short blocks never cross a multiple of R rows;
+// C: chunk length of long rows.
+constexpr int64_t kDefaultBlockNnz = 256;
+constexpr int64_t kBlockRows = 256;
+constexpr int64_t kChunkNnz = 4096;
+
+}  // namespace msx
+
+struct msx_csr_plan {
+  msx_itype itype;
+  int64_t n_rows;
+  int64_t nnz;
+  int64_t block_nnz;   // W
+  int64_t block_rows;  // R
+  int64_t chunk_nnz;   // C
+  int64_t n_blocks;
+  int64_t n_long;
+  int64_t n_chunks;
+  int device;
+  size_t bytes;
+  // Device arrays, all int32 (rows < 2^31; chunk ids < 2^31 checked at build).
+  int32_t *block_row_begin;   // n_blocks + 1
+  int32_t *long_rows;         // n_long
+  int32_t *long_chunk_begin;  // n_long + 1
+  int32_t *chunk_row;         // n_chunks: index into long_rows
+  void *partials;             // n_chunks * 8 bytes: long-row chunk sums
+  void *base;                 // single allocation holding the arrays above
+};
+
+namespace msx {
+
+// Launchers (csr_spmv.hip / csr_spmm.hip).  Arguments are already checked.
+msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                       const void *data, const void *indices, const void *indptr,
+                       const void *x, void *y, const msx_csr_plan *plan, hipStream_t stream);
+
+msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                       const void *data, const void *indices, const void *indptr, int64_t k,
+                       const void *X, int64_t ldx, void *Y, int64_t ldy, hipStream_t stream);
+
+}  // namespace msx

@@ -1,0 +1,27 @@
+"""Dispatch shim to the native module (reference: mlx_sparse/_native.py:179-189,
+286-296).
+
+The reference routes to ``_ext`` or, when the extension is missing, to a
+NumPy fallback.  Here there is no fallback: a missing extension raises, so a
+result always comes from the HIP kernels (GPU operands) or the native CPU
+path (``use_cpu()``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from mlx_sparse._ext_loader import extension
+from mlx_sparse._typing import Shape2D
+
+
+def csr_matvec(data, indices, indptr, x, shape: Shape2D, plan=None) -> torch.Tensor:
+    return extension().csr_matvec(data, indices, indptr, x, shape[0], shape[1], plan=plan)
+
+
+def csr_matmul(data, indices, indptr, rhs, shape: Shape2D, plan=None) -> torch.Tensor:
+    return extension().csr_matmul(data, indices, indptr, rhs, shape[0], shape[1], plan=plan)
+
+
+def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0):
+    return extension().csr_plan(indptr, n_rows, nnz, block_nnz)

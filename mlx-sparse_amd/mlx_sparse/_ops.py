@@ -1,0 +1,118 @@
+"""Public operator wrappers for the CSR sparse x dense path (reference:
+mlx_sparse/_ops.py:780-818 ``csr_matvec``, :972-1000 rank-2/batched helpers,
+:1118-1167 ``csr_matmul``).
+
+Operations run on the selected device (``use_cpu``/``use_gpu``); operands
+are moved there first.  GPU SpMV uses the matrix's cached row-block plan.
+Unlike MLX the result is not lazy: the kernel is enqueued on torch's current
+stream and the returned tensor is ordered after it, which composes with any
+torch operation on that stream.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+import mlx_sparse._native as _native
+from mlx_sparse._csr import CSRArray
+from mlx_sparse._device import default_torch_device
+from mlx_sparse._validation import (
+    ensure_array,
+    validate_csr_matmul_inputs,
+    validate_csr_matvec_inputs,
+)
+
+
+def _prod(shape) -> int:
+    return int(math.prod(int(d) for d in shape))
+
+
+def csr_matvec(a: CSRArray, x) -> torch.Tensor:
+    """Multiply a CSR sparse matrix by a dense vector: ``y = A @ x``.
+
+    Args:
+        a: The sparse matrix, shape ``(n_rows, n_cols)``.
+        x: Dense vector, shape ``(n_cols,)``, same dtype as ``a.data``.
+
+    Returns:
+        Dense vector of shape ``(n_rows,)`` with the dtype of ``a.data``.
+
+    Raises:
+        TypeError: ``a`` is not a CSRArray, or the dtypes of ``a.data`` and
+            ``x`` differ or are unsupported.
+        ValueError: shape constraints are violated.
+    """
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_matvec expects CSRArray, got {type(a).__name__}.")
+    device = default_torch_device()
+    x = ensure_array(x, device=device)
+    validate_csr_matvec_inputs(a.data, a.indices, a.indptr, x, a.shape)
+    data, indices, indptr = a.buffers(device)
+    return _native.csr_matvec(data, indices, indptr, x, a.shape, plan=a.plan(device))
+
+
+def _csr_matmul_rank2(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
+    validate_csr_matmul_inputs(a.data, a.indices, a.indptr, rhs, a.shape)
+    data, indices, indptr = a.buffers(rhs.device)
+    return _native.csr_matmul(data, indices, indptr, rhs, a.shape, plan=None)
+
+
+def _csr_matmul_batched(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
+    """``out[b] = A @ rhs[b]`` for every batch index, as ONE SpMM: the batch
+    is folded into the RHS columns, ``(B, n, k) -> (n, B*k)``, so the
+    matrix is streamed once instead of B times."""
+    if a.data.dtype != rhs.dtype:
+        raise TypeError(
+            "csr_matmul requires sparse data and RHS to have the same dtype, "
+            f"got {a.data.dtype} and {rhs.dtype}."
+        )
+    batch_shape = tuple(int(d) for d in rhs.shape[:-2])
+    k = int(rhs.shape[-1])
+    b = _prod(batch_shape)
+    folded = rhs.reshape(b, a.shape[1], k).permute(1, 0, 2).reshape(a.shape[1], b * k)
+    out = _csr_matmul_rank2(a, folded.contiguous())
+    return out.reshape(a.shape[0], b, k).permute(1, 0, 2).reshape(*batch_shape, a.shape[0], k)
+
+
+def csr_matmul(a: CSRArray, rhs) -> torch.Tensor:
+    """Multiply a CSR sparse matrix by a dense matrix: ``Y = A @ B``.
+
+    ``rhs`` is ``(n_cols, k)`` or batched ``(..., n_cols, k)``.
+
+    Raises:
+        TypeError: ``a`` is not a CSRArray or dtypes are violated.
+        ValueError: shape constraints are violated.
+    """
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_matmul expects CSRArray, got {type(a).__name__}.")
+    rhs = ensure_array(rhs, device=default_torch_device())
+    if rhs.ndim == 2:
+        return _csr_matmul_rank2(a, rhs)
+    if rhs.ndim < 2:
+        raise ValueError(f"csr_matmul expects rank-2 or higher RHS, got {tuple(rhs.shape)}.")
+    if rhs.shape[-2] != a.shape[1]:
+        raise ValueError(
+            f"csr_matmul RHS has sparse dimension {rhs.shape[-2]}, "
+            f"but sparse n_cols={a.shape[1]}."
+        )
+    return _csr_matmul_batched(a, rhs)
+
+
+def csr_batched_matvec(a: CSRArray, rhs) -> torch.Tensor:
+    """``out[..., :] = A @ rhs[..., :]`` for a batch of vectors
+    ``(..., n_cols)`` (reference: mlx_sparse/_ops.py csr_batched_matvec),
+    computed as one SpMM on the transposed batch."""
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_batched_matvec expects CSRArray, got {type(a).__name__}.")
+    rhs = ensure_array(rhs, device=default_torch_device())
+    if rhs.ndim < 1 or rhs.shape[-1] != a.shape[1]:
+        raise ValueError(
+            f"csr_batched_matvec RHS has sparse dimension {rhs.shape[-1] if rhs.ndim else None}, "
+            f"but sparse n_cols={a.shape[1]}."
+        )
+    batch_shape = tuple(int(d) for d in rhs.shape[:-1])
+    flat = rhs.reshape(_prod(batch_shape), a.shape[1])
+    out = _csr_matmul_rank2(a, flat.transpose(0, 1).contiguous())
+    return out.transpose(0, 1).reshape(*batch_shape, a.shape[0])

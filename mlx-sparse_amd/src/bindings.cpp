@@ -1,0 +1,282 @@
+// bindings.cpp - the `mlx_sparse._ext` Python module (pybind11).
+//
+// Mirrors the reference nanobind module's entry points for this path
+// (reference: src/bindings.cpp:279-295 `_compiled_capabilities`,
+// :874-883 `csr_matvec`, :965-975 `csr_matmul`): same names and argument
+// order (data, indices, indptr, x | rhs, n_rows, n_cols).  Arrays are torch
+// tensors; the module reads their pointer, dtype, shape, strides and device
+// through the tensor's Python attributes, so no torch headers are compiled
+// here.  Inputs are made contiguous (the reference's mx::contiguous), the
+// output is allocated with torch.empty on the inputs' device, device work is
+// ordered on torch's current stream for that device, and errors surface as
+// ValueError (std::invalid_argument), RuntimeError or MemoryError.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common/array_view.h"
+#include "common/validate.h"
+#include "msx_sparse.h"
+#include "sparse/csr_matmul/csr_matmul.h"
+#include "sparse/csr_matvec/csr_matvec.h"
+
+namespace py = pybind11;
+using msx::ArrayView;
+using msx::DType;
+
+namespace {
+
+py::module_ &torch() {
+  static py::module_ mod = py::module_::import("torch");
+  return mod;
+}
+
+DType dtype_of(const std::string &name) {
+  if (name == "float32") return DType::Float32;
+  if (name == "float16") return DType::Float16;
+  if (name == "bfloat16") return DType::BFloat16;
+  if (name == "complex64") return DType::Complex64;
+  if (name == "int32") return DType::Int32;
+  if (name == "int64") return DType::Int64;
+  return DType::Other;
+}
+
+std::string dtype_name(py::handle dtype) {
+  std::string s = py::str(dtype);
+  const std::string prefix = "torch.";
+  if (s.rfind(prefix, 0) == 0) s = s.substr(prefix.size());
+  return s;
+}
+
+int device_index(py::handle tensor) {
+  py::object dev = tensor.attr("device");
+  const std::string type = py::str(dev.attr("type"));
+  if (type == "cpu") return -1;
+  if (type != "cuda") throw std::invalid_argument("mlx_sparse supports cpu and HIP (cuda) tensors only, got " + type + ".");
+  py::object idx = dev.attr("index");
+  return idx.is_none() ? torch().attr("cuda").attr("current_device")().cast<int>() : idx.cast<int>();
+}
+
+ArrayView view_of(py::handle t) {
+  ArrayView v;
+  v.dtype_name = dtype_name(t.attr("dtype"));
+  v.dtype = dtype_of(v.dtype_name);
+  v.ndim = t.attr("dim")().cast<int>();
+  if (v.ndim <= 2) {
+    auto shape = t.attr("shape").cast<std::vector<int64_t>>();
+    auto strides = t.attr("stride")().cast<std::vector<int64_t>>();
+    for (int i = 0; i < v.ndim; ++i) {
+      v.shape[i] = shape[i];
+      v.strides[i] = strides[i];
+    }
+  }
+  v.ptr = reinterpret_cast<void *>(t.attr("data_ptr")().cast<uintptr_t>());
+  v.device = device_index(t);
+  return v;
+}
+
+py::object as_tensor(py::handle obj) {
+  if (py::isinstance(obj, torch().attr("Tensor"))) return py::reinterpret_borrow<py::object>(obj);
+  return torch().attr("as_tensor")(obj);
+}
+
+py::object contiguous(py::handle obj) { return as_tensor(obj).attr("contiguous")(); }
+
+void *stream_for(int device) {
+  if (device < 0) return nullptr;
+  const int current = torch().attr("cuda").attr("current_device")().cast<int>();
+  if (current != device)
+    throw std::invalid_argument("mlx_sparse: GPU operands must be on the current device (cuda:" +
+                                std::to_string(current) + "), got cuda:" + std::to_string(device) + ".");
+  py::object s = torch().attr("cuda").attr("current_stream")(device);
+  return reinterpret_cast<void *>(s.attr("cuda_stream").cast<uintptr_t>());
+}
+
+// Owner of a device plan; destroyed with the Python object.
+struct Plan {
+  msx_csr_plan *p = nullptr;
+  int64_t n_rows = 0;
+  int64_t nnz = 0;
+  std::string index_dtype;
+  int device = -1;
+  ~Plan() {
+    if (p) msx_csr_plan_destroy(p);
+  }
+};
+
+std::shared_ptr<Plan> make_plan(py::handle indptr_obj, int64_t n_rows, int64_t nnz,
+                                int64_t block_nnz) {
+  py::object indptr = contiguous(indptr_obj);
+  ArrayView v = view_of(indptr);
+  msx::require_rank(v, 1, "csr_plan indptr");
+  msx::require_index_dtype(v, "csr_plan indptr");
+  msx::require_size(v, n_rows + 1, "csr_plan indptr");
+  if (v.device < 0) throw std::invalid_argument("csr_plan indptr must be a GPU tensor.");
+  void *stream = stream_for(v.device);
+  auto plan = std::make_shared<Plan>();
+  plan->n_rows = n_rows;
+  plan->nnz = nnz;
+  plan->index_dtype = v.dtype_name;
+  plan->device = v.device;
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_plan_create(msx::to_itype(v.dtype), n_rows, nnz, v.ptr, block_nnz, stream,
+                             &plan->p);
+  }
+  msx::check_status(st, "csr_plan");
+  return plan;
+}
+
+const msx_csr_plan *plan_ptr(const py::object &plan) {
+  if (plan.is_none()) return nullptr;
+  return plan.cast<std::shared_ptr<Plan>>()->p;
+}
+
+py::object empty_like_out(const ArrayView &data, py::handle data_obj, py::tuple shape) {
+  py::dict kw;
+  kw["dtype"] = data_obj.attr("dtype");
+  kw["device"] = data_obj.attr("device");
+  return torch().attr("empty")(shape, **kw);
+}
+
+py::object csr_matvec(py::handle data_o, py::handle indices_o, py::handle indptr_o, py::handle x_o,
+                      int64_t n_rows, int64_t n_cols, py::object plan, int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), x = contiguous(x_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vx = view_of(x);
+  py::object out = empty_like_out(vd, data, py::make_tuple(std::max<int64_t>(n_rows, 0)));
+  const ArrayView vo = view_of(out);
+  msx::ExecContext ctx;
+  ctx.n_threads = n_threads;
+  ctx.stream = vd.device >= 0 ? stream_for(vd.device) : nullptr;
+  const msx_csr_plan *p = plan_ptr(plan);
+  if (vd.device >= 0) {
+    msx::csr_matvec(vd, vi, vp, vx, vo, n_rows, n_cols, p, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matvec(vd, vi, vp, vx, vo, n_rows, n_cols, nullptr, ctx);
+  }
+  return out;
+}
+
+py::object csr_matmul(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                      py::handle rhs_o, int64_t n_rows, int64_t n_cols, py::object plan,
+                      int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), rhs = contiguous(rhs_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr),
+                  vr = view_of(rhs);
+  if (vr.ndim != 2) msx::require_rank(vr, 2, "csr_matmul rhs");
+  py::object out = empty_like_out(vd, data, py::make_tuple(std::max<int64_t>(n_rows, 0), vr.shape[1]));
+  const ArrayView vo = view_of(out);
+  msx::ExecContext ctx;
+  ctx.n_threads = n_threads;
+  ctx.stream = vd.device >= 0 ? stream_for(vd.device) : nullptr;
+  const msx_csr_plan *p = plan_ptr(plan);
+  if (vd.device >= 0) {
+    msx::csr_matmul(vd, vi, vp, vr, vo, n_rows, n_cols, p, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matmul(vd, vi, vp, vr, vo, n_rows, n_cols, nullptr, ctx);
+  }
+  return out;
+}
+
+py::dict plan_info(const Plan &plan) {
+  msx_plan_info info{};
+  msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_info");
+  py::dict d;
+  d["n_rows"] = info.n_rows;
+  d["nnz"] = info.nnz;
+  d["block_nnz"] = info.block_nnz;
+  d["block_rows"] = info.block_rows;
+  d["chunk_nnz"] = info.chunk_nnz;
+  d["n_blocks"] = info.n_blocks;
+  d["n_long_rows"] = info.n_long_rows;
+  d["n_chunks"] = info.n_chunks;
+  d["device"] = info.device;
+  d["plan_bytes"] = info.plan_bytes;
+  return d;
+}
+
+py::tuple plan_export(const Plan &plan) {
+  msx_plan_info info{};
+  msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_export");
+  py::dict kw;
+  kw["dtype"] = torch().attr("int64");
+  py::object blocks = torch().attr("empty")(info.n_blocks + 1, **kw);
+  py::object longs = torch().attr("empty")(info.n_long_rows, **kw);
+  py::object chunks = torch().attr("empty")(info.n_long_rows + 1, **kw);
+  auto ptr = [](py::object &t) {
+    return reinterpret_cast<int64_t *>(t.attr("data_ptr")().cast<uintptr_t>());
+  };
+  msx::check_status(msx_csr_plan_export(plan.p, ptr(blocks), info.n_long_rows ? ptr(longs) : nullptr,
+                                        ptr(chunks)),
+                    "csr_plan_export");
+  return py::make_tuple(blocks, longs, chunks);
+}
+
+py::dict compiled_capabilities() {
+  py::dict info;
+  info["extension"] = true;
+  info["cpu"] = true;
+  info["metal"] = false;
+  info["accelerate"] = false;
+  info["accelerate_framework"] = false;
+  info["cuda"] = false;
+  info["rocm"] = true;
+  info["platform"] = "linux";
+  info["architecture"] = "gfx950";
+  info["abi_version"] = msx_abi_version();
+  return info;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_ext, m) {
+  m.doc() = "MI355X (gfx950) CSR sparse x dense primitives for mlx_sparse";
+
+  py::class_<Plan, std::shared_ptr<Plan>>(m, "CSRPlan")
+      .def_readonly("n_rows", &Plan::n_rows)
+      .def_readonly("nnz", &Plan::nnz)
+      .def_readonly("index_dtype", &Plan::index_dtype)
+      .def_readonly("device", &Plan::device)
+      .def("info", &plan_info, "Plan summary (block and long-row counts, sizes).")
+      .def("export", &plan_export,
+           "Host copies (int64 tensors) of block_row_begin, long_rows and long_chunk_begin.");
+
+  m.def("_compiled_capabilities", &compiled_capabilities,
+        "Return compile-time native backend facts for capability reporting.");
+  m.def("csr_plan", &make_plan, py::arg("indptr"), py::arg("n_rows"), py::arg("nnz"),
+        py::arg("block_nnz") = 0, "Build a row-block plan from a GPU indptr.");
+  m.def("csr_matvec", &csr_matvec, py::arg("data"), py::arg("indices"), py::arg("indptr"),
+        py::arg("x"), py::arg("n_rows"), py::arg("n_cols"), py::arg("plan") = py::none(),
+        py::arg("n_threads") = 0, "Multiply CSR buffers by a dense vector.");
+  m.def("csr_matmul", &csr_matmul, py::arg("data"), py::arg("indices"), py::arg("indptr"),
+        py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"), py::arg("plan") = py::none(),
+        py::arg("n_threads") = 0, "Multiply CSR buffers by a dense matrix.");
+  m.def("cpu_worker_count", &msx_cpu_worker_count, "Resolved CPU worker count.");
+  m.def(
+      "cpu_ranges",
+      [](std::vector<int64_t> work, int parts) {
+        std::vector<int64_t> out(2 * static_cast<size_t>(std::max(parts, 1)));
+        int64_t n = 0;
+        msx::check_status(msx_cpu_ranges(work.data(), static_cast<int64_t>(work.size()), parts,
+                                         out.data(), &n),
+                          "cpu_ranges");
+        std::vector<std::pair<int64_t, int64_t>> r;
+        for (int64_t i = 0; i < n; ++i) r.emplace_back(out[2 * i], out[2 * i + 1]);
+        return r;
+      },
+      py::arg("work"), py::arg("parts"), "Row ranges the CPU path splits work into.");
+  m.def("device_count", []() {
+    int c = 0;
+    msx::check_status(msx_device_count(&c), "device_count");
+    return c;
+  });
+  m.def("abi_version", &msx_abi_version);
+}

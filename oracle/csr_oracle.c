@@ -1,0 +1,485 @@
+/*
+ * csr_oracle.c - TEST INFRASTRUCTURE ONLY.
+ *
+ * Plain-C restatement of mlx-sparse's CPU CSR sparse x dense kernels, used
+ * as the parity checker for the HIP library and as the CPU baseline that
+ * bench.py times.  Nothing in the product links or calls this file; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * What it restates (reference files under mlx-sparse):
+ *   - per-row SpMV sum, stored order, lengths 0..4 written out in the same
+ *     left-to-right order (src/sparse/csr_matvec/csr_matvec.cpp:79-114);
+ *   - the SpMV driver: serial O(n) row-work prepass, work-balanced row
+ *     ranges, one std::thread per extra range, spawned per call
+ *     (csr_matvec.cpp:116-168, src/common/cpu_parallel.h:50-97);
+ *   - SpMM: one accumulator per RHS column, rows summed in stored order,
+ *     row work nnz_row * k (src/sparse/csr_matmul/csr_matmul.cpp:83-222);
+ *   - accumulator rules: float32 -> float32, complex64 -> complex64,
+ *     float16/bfloat16 -> float32 with operands widened before the multiply
+ *     and one rounding at the end (src/common/common.h:52-79);
+ *   - worker-count resolution and range partitioning
+ *     (src/common/cpu_parallel.cpp:46-253, cpu_parallel.h:134-164).
+ *
+ * Built with -ffp-contract=off so every product and every sum is rounded on
+ * its own, as the reference's separate multiply_accumulate / `+=` are.
+ *
+ * Pinning (tests/test_oracle_*.py): reference KATs and SciPy products,
+ * SuiteSparse fixtures, closed forms of stencil matrices, float64 brute
+ * force on small inputs, numpy's float16 rounding and an exhaustive check of
+ * the bfloat16 rounding rule, and a naive re-derivation of the range rule.
+ * The exact float16/bfloat16 rounding and complex product of MLX
+ * (mx::float16_t, mx::bfloat16_t, mx::complex64_t, un-vendored) are assumed
+ * IEEE round-to-nearest-even and textbook; only tolerance tests pin them.
+ */
+#define _GNU_SOURCE
+#include <errno.h>
+#include <limits.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+enum { V_F32 = 0, V_F16 = 1, V_BF16 = 2, V_C64 = 3 };
+enum { I_I32 = 0, I_I64 = 1 };
+
+typedef struct {
+  float re, im;
+} cf32;
+
+/* ---------------------------------------------------------------------- */
+/* float16 / bfloat16 <-> float32, from the IEEE 754 binary16 layout and the
+ * bfloat16 layout (top 16 bits of binary32).  Narrowing rounds to nearest,
+ * ties to even. */
+
+static float f32_from_bits(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static uint32_t bits_from_f32(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  if (exp == 0) {
+    if (man == 0) return f32_from_bits(sign);
+    /* subnormal: value = man * 2^-24, exact in binary32 */
+    float v = (float)man * 5.9604644775390625e-8f;
+    return sign ? -v : v;
+  }
+  if (exp == 31) return f32_from_bits(sign | 0x7f800000u | (man << 13));
+  return f32_from_bits(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t oracle_f32_to_f16(float f) {
+  uint32_t u = bits_from_f32(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu)); /* NaN */
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+  if (a < 0x38800000u) {
+    /* result is subnormal or zero: scale to units of 2^-24 and round */
+    int e = (int)(a >> 23);                       /* biased binary32 exponent */
+    if (e < 102) return sign;                     /* below half of 2^-24 */
+    uint32_t m = (a & 0x7fffffu) | 0x800000u;     /* 24-bit significand */
+    int shift = 126 - e;                          /* (e-127)-23+24 => right shift */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  /* normal: rebias exponent, round 13 dropped bits to nearest even */
+  uint32_t r = a - 0x38000000u; /* exponent 127 -> 15 */
+  uint32_t q = r >> 13;
+  uint32_t rem = r & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+
+float oracle_bf16_to_f32(uint16_t b) { return f32_from_bits((uint32_t)b << 16); }
+
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t u = bits_from_f32(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Accumulator rules (reference: src/common/common.h:52-79). */
+
+static inline float mul_f32(float a, float b) { return a * b; }
+static inline cf32 mul_c64(cf32 a, cf32 b) {
+  float rr = a.re * b.re;
+  float ii = a.im * b.im;
+  float ri = a.re * b.im;
+  float ir = a.im * b.re;
+  cf32 r = {rr - ii, ri + ir};
+  return r;
+}
+static inline cf32 add_c64(cf32 a, cf32 b) {
+  cf32 r = {a.re + b.re, a.im + b.im};
+  return r;
+}
+
+static inline float widen(int vt, const void *base, int64_t i) {
+  switch (vt) {
+  case V_F16: return oracle_f16_to_f32(((const uint16_t *)base)[i]);
+  case V_BF16: return oracle_bf16_to_f32(((const uint16_t *)base)[i]);
+  default: return ((const float *)base)[i];
+  }
+}
+
+static inline void narrow_store(int vt, void *base, int64_t i, float v) {
+  switch (vt) {
+  case V_F16: ((uint16_t *)base)[i] = oracle_f32_to_f16(v); break;
+  case V_BF16: ((uint16_t *)base)[i] = oracle_f32_to_bf16(v); break;
+  default: ((float *)base)[i] = v; break;
+  }
+}
+
+static inline int64_t load_index(int it, const void *base, int64_t i) {
+  return it == I_I64 ? ((const int64_t *)base)[i] : (int64_t)((const int32_t *)base)[i];
+}
+
+/* One SpMV row: restates csr_matvec_row_accum (csr_matvec.cpp:79-114).
+ * Lengths 1..4 start from the first product (no leading +0.0), longer rows
+ * start from the zero accumulator, both summed left to right. */
+static void matvec_row(int vt, int it, const void *data, const void *indices,
+                       int64_t begin, int64_t end, const void *x, void *y,
+                       int64_t row) {
+  int64_t len = end - begin;
+  if (vt == V_C64) {
+    const cf32 *d = (const cf32 *)data, *xv = (const cf32 *)x;
+    cf32 acc = {0.0f, 0.0f};
+    int64_t p = begin;
+    if (len >= 1 && len <= 4) {
+      acc = mul_c64(d[p], xv[load_index(it, indices, p)]);
+      p++;
+    }
+    for (; p < end; ++p) acc = add_c64(acc, mul_c64(d[p], xv[load_index(it, indices, p)]));
+    ((cf32 *)y)[row] = acc;
+    return;
+  }
+  float acc = 0.0f;
+  int64_t p = begin;
+  if (len >= 1 && len <= 4) {
+    acc = mul_f32(widen(vt, data, p), widen(vt, x, load_index(it, indices, p)));
+    p++;
+  }
+  for (; p < end; ++p)
+    acc = acc + mul_f32(widen(vt, data, p), widen(vt, x, load_index(it, indices, p)));
+  narrow_store(vt, y, row, acc);
+}
+
+/* SpMM rows [r0, r1): restates csr_matmul_small_rhs_cpu_impl and
+ * csr_matmul_generic_cpu_impl (csr_matmul.cpp:83-133); both sum each column
+ * from the zero accumulator in stored order. */
+static void matmul_rows(int vt, int it, const void *data, const void *indices,
+                        const void *indptr, const void *X, void *Y, int64_t k,
+                        int64_t r0, int64_t r1, void *scratch) {
+  for (int64_t row = r0; row < r1; ++row) {
+    int64_t b = load_index(it, indptr, row), e = load_index(it, indptr, row + 1);
+    if (vt == V_C64) {
+      cf32 *acc = (cf32 *)scratch;
+      for (int64_t c = 0; c < k; ++c) acc[c].re = acc[c].im = 0.0f;
+      const cf32 *d = (const cf32 *)data, *xv = (const cf32 *)X;
+      for (int64_t p = b; p < e; ++p) {
+        const cf32 *xr = xv + load_index(it, indices, p) * k;
+        for (int64_t c = 0; c < k; ++c) acc[c] = add_c64(acc[c], mul_c64(d[p], xr[c]));
+      }
+      for (int64_t c = 0; c < k; ++c) ((cf32 *)Y)[row * k + c] = acc[c];
+    } else {
+      float *acc = (float *)scratch;
+      for (int64_t c = 0; c < k; ++c) acc[c] = 0.0f;
+      for (int64_t p = b; p < e; ++p) {
+        float v = widen(vt, data, p);
+        int64_t off = load_index(it, indices, p) * k;
+        for (int64_t c = 0; c < k; ++c) acc[c] = acc[c] + mul_f32(v, widen(vt, X, off + c));
+      }
+      for (int64_t c = 0; c < k; ++c) narrow_store(vt, Y, row * k + c, acc[c]);
+    }
+  }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Worker count and ranges (reference: src/common/cpu_parallel.cpp:46-253). */
+
+static int parse_positive_int(const char *v) {
+  if (v == NULL || *v == '\0') return 0;
+  char *end = NULL;
+  errno = 0;
+  long parsed = strtol(v, &end, 10);
+  if (end == v || parsed <= 0 || parsed > INT_MAX) return 0;
+  if (*end != '\0' && *end != ',') return 0;
+  return (int)parsed;
+}
+
+int oracle_cpu_worker_count(void) {
+  const char *raw = getenv("MLX_SPARSE_CPU_THREADS");
+  if (raw == NULL || *raw == '\0') raw = getenv("MLX_SPARSE_N_THREADS");
+  int c = parse_positive_int(raw);
+  if (c > 0) return c;
+  c = parse_positive_int(getenv("OMP_NUM_THREADS"));
+  if (c > 0) return c;
+  const char *names[] = {"SLURM_CPUS_PER_TASK", "PBS_NP", "LSB_DJOB_NUMPROC", "NSLOTS"};
+  for (int i = 0; i < 4; ++i) {
+    c = parse_positive_int(getenv(names[i]));
+    if (c > 0) return c;
+  }
+  cpu_set_t set;
+  CPU_ZERO(&set);
+  if (sched_getaffinity(0, sizeof(set), &set) == 0) {
+    c = CPU_COUNT(&set);
+    if (c > 0) return c;
+  }
+  long hw = sysconf(_SC_NPROCESSORS_ONLN);
+  return hw > 0 ? (int)hw : 1;
+}
+
+/* equal_cpu_ranges: part p gets [p*n/count, (p+1)*n/count), empties dropped. */
+static int64_t equal_ranges(int64_t n, int parts, int64_t *out) {
+  if (n <= 0) return 0;
+  int count = parts < 1 ? 1 : parts;
+  int64_t m = 0;
+  for (int p = 0; p < count; ++p) {
+    int64_t b = ((int64_t)p * n) / count, e = ((int64_t)(p + 1) * n) / count;
+    if (b < e) {
+      out[2 * m] = b;
+      out[2 * m + 1] = e;
+      m++;
+    }
+  }
+  return m;
+}
+
+/* weighted_cpu_ranges: walk the work prefix sum, each part takes rows up to
+ * the first prefix >= begin_prefix + ceil(remaining / remaining_parts),
+ * at least one row, leaving one row for each later part. */
+static int64_t weighted_ranges(const int64_t *work, int64_t n, int parts, int64_t *out) {
+  if (n <= 0) return 0;
+  int count = parts < 1 ? 1 : parts;
+  if (count == 1) {
+    out[0] = 0;
+    out[1] = n;
+    return 1;
+  }
+  if (count >= n) return equal_ranges(n, count, out);
+  int64_t *prefix = (int64_t *)malloc((size_t)(n + 1) * sizeof(int64_t));
+  if (!prefix) return -1;
+  prefix[0] = 0;
+  for (int64_t r = 0; r < n; ++r) {
+    int64_t w = work[r] > 0 ? work[r] : 0;
+    int64_t next = prefix[r] + w;
+    prefix[r + 1] = next < prefix[r] ? INT64_MAX : next;
+  }
+  if (prefix[n] <= 0) {
+    free(prefix);
+    return equal_ranges(n, count, out);
+  }
+  int64_t m = 0, begin = 0;
+  for (int part = 0; part < count && begin < n; ++part) {
+    int remaining_parts = count - part;
+    if (remaining_parts == 1) {
+      out[2 * m] = begin;
+      out[2 * m + 1] = n;
+      m++;
+      break;
+    }
+    int64_t remaining = prefix[n] - prefix[begin];
+    int64_t target = prefix[begin] + (remaining + remaining_parts - 1) / remaining_parts;
+    /* lower_bound over prefix[begin+1 .. n] */
+    int64_t lo = begin + 1, hi = n + 1;
+    while (lo < hi) {
+      int64_t mid = lo + (hi - lo) / 2;
+      if (prefix[mid] < target) lo = mid + 1;
+      else hi = mid;
+    }
+    int64_t end = lo;
+    if (end < begin + 1) end = begin + 1;
+    if (end > n - (remaining_parts - 1)) end = n - (remaining_parts - 1);
+    out[2 * m] = begin;
+    out[2 * m + 1] = end;
+    m++;
+    begin = end;
+  }
+  free(prefix);
+  return m;
+}
+
+/* cpu_ranges_for_output_work (cpu_parallel.h:134-164). Returns the number of
+ * ranges written into out (2 * parts capacity), or -1 on allocation failure. */
+int64_t oracle_cpu_ranges(const int64_t *work, int64_t n, int parts, int64_t *out) {
+  if (n <= 0) return 0;
+  if (parts <= 1) {
+    out[0] = 0;
+    out[1] = n;
+    return 1;
+  }
+  int imbalance = 0;
+  int64_t prev = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t c = work[i] > 0 ? work[i] : 0;
+    if (prev >= 0 && c != prev) {
+      imbalance = 1;
+      break;
+    }
+    prev = c;
+  }
+  if (!imbalance) return equal_ranges(n, parts, out);
+  return weighted_ranges(work, n, parts, out);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Drivers. */
+
+typedef struct {
+  int op; /* 0 = matvec, 1 = matmul */
+  int vt, it;
+  const void *data, *indices, *indptr, *x;
+  void *y;
+  int64_t k;
+  int64_t r0, r1;
+  int failed;
+} job_t;
+
+static void run_job(job_t *j) {
+  if (j->op == 0) {
+    for (int64_t r = j->r0; r < j->r1; ++r)
+      matvec_row(j->vt, j->it, j->data, j->indices, load_index(j->it, j->indptr, r),
+                 load_index(j->it, j->indptr, r + 1), j->x, j->y, r);
+  } else {
+    size_t bytes = (size_t)(j->k > 0 ? j->k : 1) * (j->vt == V_C64 ? 8 : 4);
+    void *scratch = malloc(bytes);
+    if (!scratch) {
+      j->failed = 1;
+      return;
+    }
+    matmul_rows(j->vt, j->it, j->data, j->indices, j->indptr, j->x, j->y, j->k, j->r0, j->r1,
+                scratch);
+    free(scratch);
+  }
+}
+
+static void *job_thread(void *arg) {
+  run_job((job_t *)arg);
+  return NULL;
+}
+
+/* Shared driver: n_threads <= 0 resolves the worker count like the
+ * reference.  Returns 0 on success. */
+static int drive(job_t base, int64_t n_rows, int n_threads) {
+  int workers = n_threads > 0 ? n_threads : oracle_cpu_worker_count();
+  if (workers <= 1 || n_rows <= 0) {
+    base.r0 = 0;
+    base.r1 = n_rows;
+    run_job(&base);
+    return base.failed ? -1 : 0;
+  }
+  int64_t *work = (int64_t *)malloc((size_t)n_rows * sizeof(int64_t));
+  int64_t *ranges = (int64_t *)malloc((size_t)workers * 2 * sizeof(int64_t));
+  if (!work || !ranges) {
+    free(work);
+    free(ranges);
+    return -1;
+  }
+  int64_t kk = base.op == 1 ? (base.k > 1 ? base.k : 1) : 1;
+  for (int64_t r = 0; r < n_rows; ++r)
+    work[r] = (load_index(base.it, base.indptr, r + 1) - load_index(base.it, base.indptr, r)) * kk;
+  int64_t m = oracle_cpu_ranges(work, n_rows, workers, ranges);
+  free(work);
+  if (m < 0) {
+    free(ranges);
+    return -1;
+  }
+  if (m <= 1) {
+    free(ranges);
+    base.r0 = 0;
+    base.r1 = n_rows;
+    run_job(&base);
+    return base.failed ? -1 : 0;
+  }
+  job_t *jobs = (job_t *)calloc((size_t)m, sizeof(job_t));
+  pthread_t *th = (pthread_t *)calloc((size_t)m, sizeof(pthread_t));
+  if (!jobs || !th) {
+    free(jobs);
+    free(th);
+    free(ranges);
+    return -1;
+  }
+  for (int64_t i = 0; i < m; ++i) {
+    jobs[i] = base;
+    jobs[i].r0 = ranges[2 * i];
+    jobs[i].r1 = ranges[2 * i + 1];
+  }
+  int rc = 0;
+  int64_t started = 1;
+  for (int64_t i = 1; i < m; ++i) {
+    if (pthread_create(&th[i], NULL, job_thread, &jobs[i]) != 0) {
+      jobs[i].failed = 1;
+      break;
+    }
+    started++;
+  }
+  run_job(&jobs[0]);
+  for (int64_t i = 1; i < started; ++i) pthread_join(th[i], NULL);
+  for (int64_t i = 0; i < m; ++i)
+    if (jobs[i].failed) rc = -1;
+  free(jobs);
+  free(th);
+  free(ranges);
+  return rc;
+}
+
+int oracle_csr_matvec(int vt, int it, int64_t n_rows, const void *data, const void *indices,
+                      const void *indptr, const void *x, void *y, int n_threads) {
+  job_t j;
+  memset(&j, 0, sizeof(j));
+  j.op = 0;
+  j.vt = vt;
+  j.it = it;
+  j.data = data;
+  j.indices = indices;
+  j.indptr = indptr;
+  j.x = x;
+  j.y = y;
+  return drive(j, n_rows, n_threads);
+}
+
+int oracle_csr_matmul(int vt, int it, int64_t n_rows, int64_t k, const void *data,
+                      const void *indices, const void *indptr, const void *X, void *Y,
+                      int n_threads) {
+  job_t j;
+  memset(&j, 0, sizeof(j));
+  j.op = 1;
+  j.vt = vt;
+  j.it = it;
+  j.data = data;
+  j.indices = indices;
+  j.indptr = indptr;
+  j.x = X;
+  j.y = Y;
+  j.k = k;
+  return drive(j, n_rows, n_threads);
+}
+
+/* Array forms of the conversions, for tests that pin them. kind: 0 = f16,
+ * 1 = bf16. */
+void oracle_narrow_array(int kind, const float *src, uint16_t *dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    dst[i] = kind == 0 ? oracle_f32_to_f16(src[i]) : oracle_f32_to_bf16(src[i]);
+}
+
+void oracle_widen_array(int kind, const uint16_t *src, float *dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    dst[i] = kind == 0 ? oracle_f16_to_f32(src[i]) : oracle_bf16_to_f32(src[i]);
+}

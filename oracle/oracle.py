@@ -1,0 +1,210 @@
+"""CPU oracle for the CSR sparse x dense path - TEST INFRASTRUCTURE ONLY.
+
+ctypes front end of ``csr_oracle.c`` (a plain-C restatement of mlx-sparse's
+CPU kernels, reference: src/sparse/csr_matvec/csr_matvec.cpp:79-168,
+src/sparse/csr_matmul/csr_matmul.cpp:83-222, src/common/common.h:52-79,
+src/common/cpu_parallel.cpp:46-253).  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
+this module, always as the checker or the timed CPU baseline, never as the
+product path.
+
+Value arrays are numpy arrays of the storage type: float32, float16,
+complex64, and bfloat16 as raw ``uint16`` bit patterns (numpy has no
+bfloat16).  Pass ``vtype`` explicitly for bfloat16.
+
+Parity status of each function (the checks live in tests/test_oracle_*.py):
+
+- ``csr_matvec``/``csr_matmul`` float32: pinned (reference KATs, SciPy,
+  SuiteSparse fixtures, closed forms, float64 brute force).
+- float16/bfloat16: pinned to the rule "widen, multiply and sum in float32,
+  round once (nearest even)"; the rounding functions are pinned against
+  numpy float16 and torch bfloat16 casts.  MLX's own rounding is un-vendored.
+- complex64: pinned against numpy complex products and the split into real
+  SpMVs; the bit pattern of MLX's complex product is un-vendored.
+- ``cpu_ranges``/``cpu_worker_count``: pinned against a naive re-derivation
+  and environment cases.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "libcsr_oracle.so"
+
+VTYPES = {"float32": 0, "float16": 1, "bfloat16": 2, "complex64": 3}
+ITYPES = {np.dtype(np.int32): 0, np.dtype(np.int64): 1}
+_STORAGE = {
+    "float32": np.dtype(np.float32),
+    "float16": np.dtype(np.float16),
+    "bfloat16": np.dtype(np.uint16),
+    "complex64": np.dtype(np.complex64),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile the oracle with its Makefile (gcc, -O3, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        _lib.oracle_csr_matvec.argtypes = [ci, ci, i64, vp, vp, vp, vp, vp, ci]
+        _lib.oracle_csr_matvec.restype = ci
+        _lib.oracle_csr_matmul.argtypes = [ci, ci, i64, i64, vp, vp, vp, vp, vp, ci]
+        _lib.oracle_csr_matmul.restype = ci
+        _lib.oracle_cpu_ranges.argtypes = [vp, i64, ci, vp]
+        _lib.oracle_cpu_ranges.restype = i64
+        _lib.oracle_cpu_worker_count.argtypes = []
+        _lib.oracle_cpu_worker_count.restype = ci
+        _lib.oracle_narrow_array.argtypes = [ci, vp, vp, i64]
+        _lib.oracle_narrow_array.restype = None
+        _lib.oracle_widen_array.argtypes = [ci, vp, vp, i64]
+        _lib.oracle_widen_array.restype = None
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _vtype_of(arr: np.ndarray, vtype: str | None) -> str:
+    if vtype is not None:
+        return vtype
+    for name, dt in _STORAGE.items():
+        if arr.dtype == dt and name != "bfloat16":
+            return name
+    raise TypeError(f"oracle: unsupported value dtype {arr.dtype}")
+
+
+def _prep(data, indices, indptr, vtype):
+    vt = _vtype_of(np.asarray(data), vtype)
+    data = np.ascontiguousarray(data, dtype=_STORAGE[vt])
+    indices = np.ascontiguousarray(indices)
+    indptr = np.ascontiguousarray(indptr)
+    if indices.dtype != indptr.dtype or indices.dtype not in ITYPES:
+        raise TypeError("oracle: indices/indptr must share int32 or int64")
+    return vt, data, indices, indptr
+
+
+def csr_matvec(data, indices, indptr, x, n_rows: int, *, vtype: str | None = None,
+               n_threads: int = 1) -> np.ndarray:
+    """Sequential-order CSR SpMV (reference csr_matvec.cpp:79-168)."""
+    vt, data, indices, indptr = _prep(data, indices, indptr, vtype)
+    x = np.ascontiguousarray(x, dtype=_STORAGE[vt])
+    y = np.empty(n_rows, dtype=_STORAGE[vt])
+    rc = lib().oracle_csr_matvec(VTYPES[vt], ITYPES[indices.dtype], n_rows, _ptr(data),
+                                 _ptr(indices), _ptr(indptr), _ptr(x), _ptr(y), n_threads)
+    if rc != 0:
+        raise MemoryError("oracle_csr_matvec failed")
+    return y
+
+
+def csr_matmul(data, indices, indptr, X, n_rows: int, *, vtype: str | None = None,
+               n_threads: int = 1) -> np.ndarray:
+    """Sequential-order CSR SpMM with row-major X (reference csr_matmul.cpp:83-222)."""
+    vt, data, indices, indptr = _prep(data, indices, indptr, vtype)
+    X = np.ascontiguousarray(X, dtype=_STORAGE[vt])
+    if X.ndim != 2:
+        raise ValueError("oracle: X must be rank-2")
+    k = X.shape[1]
+    Y = np.empty((n_rows, k), dtype=_STORAGE[vt])
+    rc = lib().oracle_csr_matmul(VTYPES[vt], ITYPES[indices.dtype], n_rows, k, _ptr(data),
+                                 _ptr(indices), _ptr(indptr), _ptr(X), _ptr(Y), n_threads)
+    if rc != 0:
+        raise MemoryError("oracle_csr_matmul failed")
+    return Y
+
+
+def cpu_ranges(work, parts: int) -> list[tuple[int, int]]:
+    """cpu_ranges_for_output_work (reference cpu_parallel.h:134-164)."""
+    work = np.ascontiguousarray(work, dtype=np.int64)
+    out = np.empty(2 * max(parts, 1), dtype=np.int64)
+    m = lib().oracle_cpu_ranges(_ptr(work), work.size, parts, _ptr(out))
+    if m < 0:
+        raise MemoryError("oracle_cpu_ranges failed")
+    return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(m)]
+
+
+def cpu_worker_count() -> int:
+    """configured_cpu_worker_count (reference cpu_parallel.cpp:97-135)."""
+    return int(lib().oracle_cpu_worker_count())
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().oracle_narrow_array(1, _ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f32_to_f16_bits(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().oracle_narrow_array(0, _ptr(a), _ptr(out), a.size)
+    return out
+
+
+def bf16_bits_to_f32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().oracle_widen_array(1, _ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f16_bits_to_f32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().oracle_widen_array(0, _ptr(a), _ptr(out), a.size)
+    return out
+
+
+def row_scale(data, indices, indptr, x, n_rows: int, *, vtype: str | None = None) -> np.ndarray:
+    """Per-row sum of |a_ij * x_j| in float64, the scale of the parity tolerance."""
+    vt = _vtype_of(np.asarray(data), vtype)
+    d = np.asarray(data)
+    xv = np.asarray(x)
+    if vt == "bfloat16":
+        d = bf16_bits_to_f32(d)
+        xv = bf16_bits_to_f32(xv)
+    d = np.abs(d.astype(np.complex128 if vt == "complex64" else np.float64))
+    xv = np.abs(xv.astype(np.complex128 if vt == "complex64" else np.float64))
+    indptr = np.asarray(indptr, dtype=np.int64)
+    rows = np.repeat(np.arange(n_rows), np.diff(indptr))
+    if xv.ndim == 1:
+        terms = d * xv[np.asarray(indices, dtype=np.int64)]
+        return np.bincount(rows, weights=terms, minlength=n_rows)
+    terms = d[:, None] * xv[np.asarray(indices, dtype=np.int64)]
+    out = np.zeros((n_rows, xv.shape[1]))
+    np.add.at(out, rows, terms)
+    return out
+
+
+__all__ = [
+    "VTYPES",
+    "build",
+    "lib",
+    "csr_matvec",
+    "csr_matmul",
+    "cpu_ranges",
+    "cpu_worker_count",
+    "f32_to_bf16_bits",
+    "f32_to_f16_bits",
+    "bf16_bits_to_f32",
+    "f16_bits_to_f32",
+    "row_scale",
+    "os",
+]

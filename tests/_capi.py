@@ -1,0 +1,128 @@
+"""ctypes front end of libmsx_sparse (include/msx_sparse.h) for the tests:
+the GPU parity tests call the HIP path through exactly this C ABI."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "msx_sparse.h"
+LIB = ROOT / "mlx-sparse_amd" / "mlx_sparse" / "libmsx_sparse.so"
+
+VT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.complex64: 3}
+IT = {torch.int32: 0, torch.int64: 1}
+OK, EINVAL, ETYPE, EHIP, ENOMEM = range(5)
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int64) for name in (
+        "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_long_rows",
+        "n_chunks", "device", "plan_bytes")]
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(msx_\w+)\s*\(", text, re.M)))
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(str(LIB))
+        i64, vp, ci = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+        L.msx_abi_version.restype = ci
+        L.msx_last_error.restype = ctypes.c_char_p
+        L.msx_device_count.argtypes = [ctypes.POINTER(ci)]
+        L.msx_csr_plan_create.argtypes = [ci, i64, i64, vp, i64, vp, ctypes.POINTER(vp)]
+        L.msx_csr_plan_destroy.argtypes = [vp]
+        L.msx_csr_plan_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
+        L.msx_csr_plan_export.argtypes = [vp, vp, vp, vp]
+        L.msx_csr_spmv.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmm.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp, i64, vp, vp]
+        L.msx_csr_spmv_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
+        L.msx_csr_spmm_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp, ci]
+        L.msx_cpu_worker_count.restype = ci
+        L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
+        for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_destroy",
+                     "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_spmv", "msx_csr_spmm",
+                     "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges"):
+            getattr(L, name).restype = ci
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().msx_last_error().decode()
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+class Plan:
+    def __init__(self, indptr: torch.Tensor, n_rows: int, nnz: int, block_nnz: int = 0):
+        self.ptr = ctypes.c_void_p()
+        st = lib().msx_csr_plan_create(IT[indptr.dtype], n_rows, nnz, _p(indptr), block_nnz,
+                                       _stream(), ctypes.byref(self.ptr))
+        if st != OK:
+            raise RuntimeError(f"plan_create: {st} {last_error()}")
+
+    def info(self) -> PlanInfo:
+        info = PlanInfo()
+        assert lib().msx_csr_plan_info(self.ptr, ctypes.byref(info)) == OK
+        return info
+
+    def export(self):
+        info = self.info()
+        blocks = torch.empty(info.n_blocks + 1, dtype=torch.int64)
+        longs = torch.empty(max(info.n_long_rows, 1), dtype=torch.int64)
+        chunks = torch.empty(info.n_long_rows + 1, dtype=torch.int64)
+        st = lib().msx_csr_plan_export(self.ptr, _p(blocks), _p(longs), _p(chunks))
+        assert st == OK, last_error()
+        return blocks.numpy(), longs[: info.n_long_rows].numpy(), chunks.numpy()
+
+    def close(self):
+        if self.ptr:
+            lib().msx_csr_plan_destroy(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def spmv(data, indices, indptr, x, n_rows, n_cols, plan: Plan | None = None, y=None):
+    if y is None:
+        y = torch.empty(n_rows, dtype=data.dtype, device=data.device)
+    st = lib().msx_csr_spmv(VT[data.dtype], IT[indices.dtype], n_rows, n_cols, data.numel(),
+                            _p(data), _p(indices), _p(indptr), _p(x), _p(y),
+                            plan.ptr if plan else None, _stream())
+    if st != OK:
+        raise RuntimeError(f"msx_csr_spmv: {st} {last_error()}")
+    return y
+
+
+def spmm(data, indices, indptr, X, n_rows, n_cols, Y=None, ldx=None, ldy=None):
+    k = X.shape[1]
+    if Y is None:
+        Y = torch.empty((n_rows, k), dtype=data.dtype, device=data.device)
+    st = lib().msx_csr_spmm(VT[data.dtype], IT[indices.dtype], n_rows, n_cols, data.numel(),
+                            _p(data), _p(indices), _p(indptr), k, _p(X),
+                            ldx if ldx is not None else X.stride(0), _p(Y),
+                            ldy if ldy is not None else Y.stride(0), None, _stream())
+    if st != OK:
+        raise RuntimeError(f"msx_csr_spmm: {st} {last_error()}")
+    return Y

@@ -1,0 +1,69 @@
+"""Shared test helpers: dtype plumbing between numpy/torch/oracle and the
+per-row parity tolerance of the path (|got - want| <= tol * sum|a_ij x_j|)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+TOL = {"float32": 1e-5, "complex64": 1e-5, "float16": 1e-2, "bfloat16": 1e-2}
+TORCH = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16,
+         "complex64": torch.complex64}
+
+
+def storage(values: np.ndarray, vtype: str) -> np.ndarray:
+    """float32/complex input -> numpy storage of `vtype` (bfloat16 as uint16
+    bits, rounded to nearest even by torch)."""
+    if vtype == "bfloat16":
+        t = torch.from_numpy(np.ascontiguousarray(values, dtype=np.float32)).to(torch.bfloat16)
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if vtype == "float16":
+        return np.ascontiguousarray(values, dtype=np.float16)
+    if vtype == "complex64":
+        return np.ascontiguousarray(values, dtype=np.complex64)
+    return np.ascontiguousarray(values, dtype=np.float32)
+
+
+def to_torch(arr: np.ndarray, vtype: str | None = None, device="cpu") -> torch.Tensor:
+    if vtype == "bfloat16":
+        t = torch.from_numpy(np.ascontiguousarray(arr).view(np.int16)).view(torch.bfloat16)
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(arr))
+    return t.to(device)
+
+
+def to_numpy(t: torch.Tensor) -> np.ndarray:
+    """Tensor -> numpy storage (bfloat16 as uint16 bits)."""
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def widen(arr: np.ndarray, vtype: str) -> np.ndarray:
+    """Storage -> float64 / complex128 values."""
+    if vtype == "bfloat16":
+        return (arr.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    if vtype == "complex64":
+        return arr.astype(np.complex128)
+    return arr.astype(np.float64)
+
+
+def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtype: str,
+                      what: str = "") -> float:
+    """Per-row parity: |got - want| <= TOL[vtype] * scale (+ a denormal floor).
+    Returns the largest error relative to the scale."""
+    g = widen(got, vtype)
+    w = widen(want, vtype)
+    err = np.abs(g - w)
+    bound = TOL[vtype] * scale + 1e-30
+    bad = err > bound
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} entries outside {TOL[vtype]}*sum|a*x| "
+            f"(first {idx.tolist()}: got {g[tuple(idx[0])]}, want {w[tuple(idx[0])]}, "
+            f"scale {scale[tuple(idx[0])]})")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        rel = np.where(scale > 0, err / np.maximum(scale, 1e-300), 0.0)
+    return float(rel.max()) if rel.size else 0.0

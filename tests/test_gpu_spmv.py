@@ -1,0 +1,274 @@
+"""HIP SpMV parity with the CPU oracle, through the C ABI.
+
+Bar: index work (the row-block plan) bit-exact against oracle/plan_oracle.py;
+values within |gpu - oracle| <= tol * sum_j |a_ij x_j| per row with tol =
+1e-5 (float32, complex64) or 1e-2 (float16, bfloat16).  float32 rows that the
+kernels sum in stored order (short blocks with mean row length <= 32, and
+the plan-free kernel at one lane per row) are also checked for equality.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _capi
+from _util import TORCH, assert_rows_close, storage, to_numpy, to_torch
+from oracle import oracle as orc
+from oracle import plan_oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+VTYPES = ["float32", "float16", "bfloat16", "complex64"]
+
+
+def _upload(data, indices, indptr, vtype):
+    return (to_torch(data, vtype, DEV), to_torch(indices, None, DEV), to_torch(indptr, None, DEV))
+
+
+def _values(rng, n, vtype):
+    v = rng.standard_normal(n)
+    if vtype == "complex64":
+        v = v + 1j * rng.standard_normal(n)
+    return storage(v, vtype)
+
+
+def _random_csr(rng, n_rows, n_cols, lengths, index_dtype):
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    nnz = int(indptr[-1])
+    indices = rng.integers(0, n_cols, nnz)
+    return indices.astype(index_dtype), indptr.astype(index_dtype), nnz
+
+
+def _check_spmv(data, indices, indptr, x, n_rows, n_cols, vtype, plan_w=0, what=""):
+    want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+    scale = orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype)
+    d, i, p = _upload(data, indices, indptr, vtype)
+    xt = to_torch(x, vtype, DEV)
+    out = {}
+    plan = _capi.Plan(p, n_rows, int(data.shape[0]), plan_w) if plan_w is not None else None
+    for label, pl in (("plan", plan), ("planfree", None)):
+        y = _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=pl)
+        torch.cuda.synchronize()
+        got = to_numpy(y)
+        assert_rows_close(got, want, scale, vtype, f"{what} {label}")
+        out[label] = got
+    if plan is not None:
+        plan.close()
+    return out, want
+
+
+# -- reference KATs through the drop-in API on the GPU ---------------------------
+
+def test_kat_through_api(gpu):
+    ms = gpu
+    A = ms.csr_array((np.array([2.0, -1.0, 4.0, 5.0], np.float32), np.array([0, 2, 1, 3], np.int32),
+                      np.array([0, 2, 2, 4], np.int32)), shape=(3, 4))
+    assert A.data.device.type == "cuda"
+    y = A @ np.array([3.0, 10.0, 7.0, -2.0], np.float32)
+    assert y.device.type == "cuda"
+    np.testing.assert_array_equal(y.cpu().numpy(), [-1.0, 0.0, 30.0])
+    # non-contiguous operands (reference tests/test_csr_matvec.py:318-333)
+    data = torch.tensor([99.0, 2.0, 99.0, -1.0, 99.0, 4.0, 99.0, 5.0], device=DEV)[1::2]
+    idx = torch.tensor([9, 0, 9, 2, 9, 1, 9, 3], dtype=torch.int32, device=DEV)[1::2]
+    x = torch.tensor([99.0, 3.0, 99.0, 10.0, 99.0, 7.0, 99.0, -2.0], device=DEV)[1::2]
+    B = ms.csr_array((data, idx, torch.tensor([0, 2, 2, 4], dtype=torch.int32)), shape=(3, 4))
+    np.testing.assert_array_equal((B @ x).cpu().numpy(), [-1.0, 0.0, 30.0])
+    # bfloat16 returns bfloat16 (reference tests/test_dtypes.py:64-77)
+    C = ms.csr_array((torch.tensor([2.0, -1.0], dtype=torch.bfloat16), torch.tensor([0, 1], dtype=torch.int32),
+                      torch.tensor([0, 2], dtype=torch.int32)), shape=(1, 2))
+    yb = C @ torch.tensor([3.0, 7.0], dtype=torch.bfloat16)
+    assert yb.dtype == torch.bfloat16 and yb.float().item() == -1.0
+
+
+def test_errors_through_api(gpu):
+    ms = gpu
+    A = ms.csr_array((np.ones(1, np.float32), np.zeros(1, np.int32), np.array([0, 1], np.int32)),
+                     shape=(1, 2))
+    with pytest.raises(ValueError, match="n_cols"):
+        A @ torch.ones(1, device=DEV)
+    with pytest.raises(TypeError, match="dtype must be one"):
+        A @ torch.ones(2, dtype=torch.int32, device=DEV)
+    with pytest.raises(TypeError, match="same dtype"):
+        A @ torch.ones(2, dtype=torch.float16, device=DEV)
+
+
+# -- golden fixtures -------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["well1033", "illc1033", "bcsstk03"])
+def test_suitesparse_fixtures(name):
+    from pathlib import Path
+
+    z = np.load(Path(__file__).parent / "golden" / f"suitesparse_{name}.npz")
+    shape = tuple(int(v) for v in z["shape"])
+    out, want = _check_spmv(z["data"], z["indices"], z["indptr"], z["x"], shape[0], shape[1],
+                            "float32", what=name)
+    np.testing.assert_array_equal(want, z["scipy_x"])
+    np.testing.assert_array_equal(out["plan"], want)  # short rows: stored-order sums
+
+
+# -- dtype x index type sweep with ragged and empty rows ------------------------
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_random_ragged(vtype, index_dtype):
+    rng = np.random.default_rng(100 + VTYPES.index(vtype))
+    n_rows, n_cols = 5000, 3000
+    lengths = rng.integers(0, 30, n_rows)
+    lengths[rng.random(n_rows) < 0.1] = 0
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, index_dtype)
+    out, want = _check_spmv(_values(rng, nnz, vtype), indices, indptr, _values(rng, n_cols, vtype),
+                            n_rows, n_cols, vtype, what=f"{vtype}/{index_dtype.__name__}")
+    if vtype == "float32":
+        np.testing.assert_array_equal(out["plan"], want)
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+def test_long_rows_and_fixup(vtype):
+    # lengths straddling W=256 (short/long), C=4096 (one chunk / several)
+    rng = np.random.default_rng(7)
+    special = [0, 1, 4, 5, 255, 256, 257, 1000, 4095, 4096, 4097, 8192, 12289, 60000]
+    lengths = np.concatenate([rng.integers(0, 20, 300), special, rng.integers(0, 3, 500), special[::-1]])
+    rng.shuffle(lengths)
+    n_rows, n_cols = lengths.size, 70000
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, np.int32)
+    _check_spmv(_values(rng, nnz, vtype), indices, indptr, _values(rng, n_cols, vtype), n_rows,
+                n_cols, vtype, what=f"long/{vtype}")
+
+
+@pytest.mark.parametrize("W", [64, 128, 256, 512, 1024])
+def test_plan_bins_bit_exact(W):
+    rng = np.random.default_rng(W)
+    lengths = rng.integers(0, 50, 20000)
+    big = rng.random(lengths.size) < 0.01
+    lengths[big] = rng.integers(W + 1, 20 * W, big.sum())
+    lengths[5000:6500] = 0  # a long run of empty rows
+    for index_dtype in (np.int32, np.int64):
+        indptr = np.zeros(lengths.size + 1, np.int64)
+        np.cumsum(lengths, out=indptr[1:])
+        p = torch.from_numpy(indptr.astype(index_dtype)).to(DEV)
+        plan = _capi.Plan(p, lengths.size, int(indptr[-1]), W)
+        got = plan.export()
+        want = plan_oracle.plan(indptr, W=W)
+        for g, w, name in zip(got, want, ("blocks", "long_rows", "chunk_begin")):
+            np.testing.assert_array_equal(g, w, err_msg=name)
+        info = plan.info()
+        assert info.n_blocks == want[0].size - 1 and info.n_long_rows == want[1].size
+        plan.close()
+
+
+def test_empty_and_degenerate():
+    for n_rows, n_cols, lengths in [(0, 5, []), (4, 0, [0, 0, 0, 0]), (3, 7, [0, 0, 0]),
+                                    (1, 1, [1]), (2, 3, [3, 0])]:
+        lengths = np.asarray(lengths, np.int64)
+        rng = np.random.default_rng(0)
+        indices, indptr, nnz = _random_csr(rng, n_rows, max(n_cols, 1), lengths, np.int32)
+        data = _values(rng, nnz, "float32")
+        x = _values(rng, n_cols, "float32")
+        d, i, p = _upload(data, indices, indptr, "float32")
+        y = _capi.spmv(d, i, p, to_torch(x, None, DEV), n_rows, n_cols,
+                       plan=_capi.Plan(p, n_rows, nnz))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_numpy(y), orc.csr_matvec(data, indices, indptr, x, n_rows))
+
+
+def test_out_of_range_columns_add_nothing():
+    # malformed input: columns outside [0, n_cols) must not be read
+    data = np.ones(6, np.float32)
+    indices = np.array([0, -1, 5, 1, 1 << 30, 2], np.int32)
+    indptr = np.array([0, 3, 6], np.int32)
+    x = np.array([1.0, 2.0, 4.0], np.float32)
+    d, i, p = _upload(data, indices, indptr, "float32")
+    for plan in (_capi.Plan(p, 2, 6), None):
+        y = _capi.spmv(d, i, p, to_torch(x, None, DEV), 2, 3, plan=plan)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_numpy(y), [1.0, 6.0])
+
+
+def test_misaligned_buffers_use_plan_free_path():
+    rng = np.random.default_rng(3)
+    lengths = rng.integers(0, 40, 2000)
+    indices, indptr, nnz = _random_csr(rng, 2000, 2000, lengths, np.int32)
+    data = _values(rng, nnz + 1, "float32")
+    x = _values(rng, 2000, "float32")
+    dd = to_torch(data, None, DEV)[1:]  # 4-byte offset: not 16-byte aligned
+    ii = to_torch(np.concatenate([[0], indices]).astype(np.int32), None, DEV)[1:]
+    p = to_torch(indptr, None, DEV)
+    plan = _capi.Plan(p, 2000, nnz)
+    y = _capi.spmv(dd, ii, p, to_torch(x, None, DEV), 2000, 2000, plan=plan)
+    torch.cuda.synchronize()
+    want = orc.csr_matvec(data[1:], indices, indptr, x, 2000)
+    assert_rows_close(to_numpy(y), want, orc.row_scale(data[1:], indices, indptr, x, 2000),
+                      "float32", "misaligned")
+
+
+def test_repeat_calls_bitwise_identical():
+    rng = np.random.default_rng(9)
+    lengths = np.clip(rng.zipf(1.7, 20000), 1, 30000)
+    indices, indptr, nnz = _random_csr(rng, 20000, 20000, lengths, np.int32)
+    d, i, p = _upload(_values(rng, nnz, "float32"), indices, indptr, "float32")
+    x = to_torch(_values(rng, 20000, "float32"), None, DEV)
+    plan = _capi.Plan(p, 20000, nnz)
+    ys = [_capi.spmv(d, i, p, x, 20000, 20000, plan=plan).clone() for _ in range(3)]
+    torch.cuda.synchronize()
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+
+
+def test_plan_for_other_matrix_is_rejected():
+    p1 = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
+    plan = _capi.Plan(p1, 2, 2)
+    d = torch.ones(3, device=DEV)
+    i = torch.zeros(3, dtype=torch.int32, device=DEV)
+    p2 = torch.tensor([0, 1, 3], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="different matrix"):
+        _capi.spmv(d, i, p2, torch.ones(1, device=DEV), 2, 1, plan=plan)
+
+
+# -- benchmark configurations --------------------------------------------------------
+
+def _config(name, small):
+    from mlx_sparse import synthetic as s
+
+    if name == "laplacian":
+        return s.laplacian_2d(128 if small else 1024), s.uniform(128 * 128 if small else 1 << 20, -1, 1, 1)
+    if name == "random16":
+        n = 1 << 16 if small else 1 << 22
+        return s.random_fixed_row(n, 16, seed=0), s.uniform(n, -1, 1, 1)
+    if name == "powerlaw":
+        n = 1 << 16 if small else 1 << 21
+        return s.power_law(n, 2.0, 200_000, seed=0), s.uniform(n, 0, 1, 1)
+    if name == "poisson":
+        g = 32 if small else 128
+        return s.poisson_3d(g), s.uniform(g ** 3, -1, 1, 1)
+    n = 1 << 16 if small else 1 << 20
+    return s.banded(n, 32, 0.65, 70.0, seed=0), s.uniform(n, -1, 1, 1)
+
+
+@pytest.mark.parametrize("name", ["laplacian", "random16", "powerlaw", "poisson", "banded"])
+def test_configs_small(name):
+    m, x = _config(name, small=True)
+    vtypes = ["float32"] if name != "banded" else ["bfloat16", "float16", "complex64"]
+    for vtype in vtypes:
+        if vtype == "complex64":
+            from mlx_sparse import synthetic as s
+
+            data = s.complex_values(m, 3)
+            xv = storage(x + 1j * x[::-1], vtype)
+        else:
+            data, xv = storage(m.data, vtype), storage(x, vtype)
+        out, want = _check_spmv(data, m.indices, m.indptr, xv, m.shape[0], m.shape[1], vtype,
+                                what=f"{name}/{vtype}")
+
+
+@pytest.mark.parametrize("name", ["random16", "powerlaw"])
+def test_configs_full_size(name):
+    """The north-star matrices at their benchmark size, against the oracle."""
+    m, x = _config(name, small=False)
+    out, want = _check_spmv(m.data, m.indices, m.indptr, x, m.shape[0], m.shape[1], "float32",
+                            what=f"{name}/full")
+    if name == "random16":
+        np.testing.assert_array_equal(out["plan"], want)
