@@ -1,0 +1,138 @@
+"""HIP SpMM parity with the CPU oracle, through the C ABI and the drop-in API.
+
+Each output column is summed from zero in stored order on both sides, so
+float32 results must be equal; other dtypes within tol * sum_j |a_ij x_jc|
+(1e-5 complex64, 1e-2 float16/bfloat16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _capi
+from _util import assert_rows_close, storage, to_numpy, to_torch
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+VTYPES = ["float32", "float16", "bfloat16", "complex64"]
+
+
+def _values(rng, shape, vtype):
+    v = rng.standard_normal(shape)
+    if vtype == "complex64":
+        v = v + 1j * rng.standard_normal(shape)
+    return storage(v, vtype)
+
+
+def _matrix(rng, n_rows, n_cols, max_len, index_dtype):
+    lengths = rng.integers(0, max_len, n_rows)
+    lengths[rng.random(n_rows) < 0.1] = 0
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    nnz = int(indptr[-1])
+    return rng.integers(0, n_cols, nnz).astype(index_dtype), indptr.astype(index_dtype), nnz
+
+
+def _check(data, indices, indptr, X, n_rows, n_cols, vtype, what):
+    want = orc.csr_matmul(data, indices, indptr, X, n_rows, vtype=vtype, n_threads=8)
+    d = to_torch(data, vtype, DEV)
+    i = to_torch(indices, None, DEV)
+    p = to_torch(indptr, None, DEV)
+    Y = _capi.spmm(d, i, p, to_torch(X, vtype, DEV), n_rows, n_cols)
+    torch.cuda.synchronize()
+    got = to_numpy(Y)
+    if vtype == "float32":
+        np.testing.assert_array_equal(got, want, err_msg=what)
+    else:
+        scale = orc.row_scale(data, indices, indptr, X, n_rows, vtype=vtype)
+        assert_rows_close(got, want, scale, vtype, what)
+    return got
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("k", [1, 2, 3, 7, 8, 16, 33, 64, 256, 300])
+def test_widths(vtype, k):
+    rng = np.random.default_rng(k)
+    indices, indptr, nnz = _matrix(rng, 700, 500, 25, np.int32)
+    _check(_values(rng, nnz, vtype), indices, indptr, _values(rng, (500, k), vtype), 700, 500,
+           vtype, f"{vtype} k={k}")
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+def test_int64_and_long_rows(vtype):
+    rng = np.random.default_rng(4)
+    indices, indptr, nnz = _matrix(rng, 300, 9000, 30, np.int64)
+    lengths = np.diff(indptr)
+    lengths[[3, 77, 200]] = [5000, 12000, 9000]
+    indptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    indices = rng.integers(0, 9000, int(indptr[-1])).astype(np.int64)
+    _check(_values(rng, indices.size, vtype), indices, indptr, _values(rng, (9000, 16), vtype),
+           300, 9000, vtype, f"long {vtype}")
+
+
+def test_padded_leading_dimensions_and_scalar_path():
+    rng = np.random.default_rng(8)
+    indices, indptr, nnz = _matrix(rng, 400, 300, 20, np.int32)
+    data = _values(rng, nnz, "float32")
+    Xfull = _values(rng, (300, 40), "float32")
+    want = orc.csr_matmul(data, indices, indptr, np.ascontiguousarray(Xfull[:, :32]), 400)
+    d, i, p = (to_torch(a, None, DEV) for a in (data, indices, indptr))
+    Xt = to_torch(Xfull, None, DEV)
+    # ldx = 40 (multiple of 4): vector path on a padded X; ldy = 36
+    Yb = torch.full((400, 36), 7.0, device=DEV)
+    _capi.spmm(d, i, p, Xt[:, :32], 400, 300, Y=Yb, ldx=40, ldy=36)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(Yb[:, :32].cpu().numpy(), want)
+    assert torch.all(Yb[:, 32:] == 7.0)  # padding untouched
+    # ldx = 39: scalar path
+    X39 = to_torch(np.ascontiguousarray(Xfull[:, :39]), None, DEV)
+    Y = _capi.spmm(d, i, p, X39[:, :32], 400, 300, ldx=39, ldy=32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(Y.cpu().numpy(), want)
+
+
+def test_golden_widths_and_batched_api(gpu):
+    from pathlib import Path
+
+    ms = gpu
+    z = np.load(Path(__file__).parent / "golden" / "scipy_cases.npz")
+    for k in (1, 2, 4, 8, 16, 32):
+        pre = f"widths{k}"
+        shape = tuple(int(v) for v in z[f"{pre}.shape"])
+        A = ms.csr_array((z[f"{pre}.data"], z[f"{pre}.indices"], z[f"{pre}.indptr"]), shape=shape)
+        Y = (A @ torch.from_numpy(z[f"{pre}.X"]).to(DEV)).cpu().numpy()
+        np.testing.assert_allclose(Y, z[f"{pre}.scipy"], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(Y, z[f"{pre}.dense64"], rtol=1e-5, atol=1e-5)
+    # batched RHS (reference tests/test_numerical_correctness.py:76-80)
+    shape = tuple(int(v) for v in z["numcorr.shape"])
+    A = ms.csr_array((z["numcorr.data"], z["numcorr.indices"], z["numcorr.indptr"]), shape=shape)
+    out = (A @ torch.from_numpy(z["numcorr.B"]).to(DEV)).cpu().numpy()
+    np.testing.assert_allclose(out, z["numcorr.dense64_B"], rtol=1e-5, atol=1e-5)
+    # complex (reference tests/test_numerical_correctness.py:83-113)
+    shape = tuple(int(v) for v in z["complex.shape"])
+    C = ms.csr_array((z["complex.data"], z["complex.indices"], z["complex.indptr"]), shape=shape)
+    np.testing.assert_allclose((C @ torch.from_numpy(z["complex.X"]).to(DEV)).cpu().numpy(),
+                               z["complex.dense128_X"], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose((C @ torch.from_numpy(z["complex.x"]).to(DEV)).cpu().numpy(),
+                               z["complex.dense128_x"], rtol=1e-5, atol=1e-5)
+
+
+def test_poisson_spmm_k64_full_size():
+    """The SpMM benchmark matrix at full size: column c equals SpMV of X[:, c]
+    (checked on 4 columns) and the whole product equals the oracle."""
+    from mlx_sparse import synthetic
+
+    m = synthetic.poisson_3d(128)
+    X = synthetic.normal(m.shape[1], seed=2, k=64)
+    got = _check(m.data, m.indices, m.indptr, X, m.shape[0], m.shape[1], "float32", "poisson k=64")
+    d, i, p = (to_torch(a, None, DEV) for a in (m.data, m.indices, m.indptr))
+    plan = _capi.Plan(p, m.shape[0], m.nnz)  # short blocks sum rows in stored order
+    for c in (0, 17, 40, 63):
+        y = _capi.spmv(d, i, p, to_torch(np.ascontiguousarray(X[:, c]), None, DEV), m.shape[0],
+                       m.shape[1], plan=plan)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_numpy(y), got[:, c])
