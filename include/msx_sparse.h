@@ -14,8 +14,8 @@
  *   - GPU entry points are asynchronous and ordered on the HIP stream passed
  *     as `stream` (a hipStream_t; NULL means the default stream).  They
  *     return after the launch, not after completion.  Calls on different
- *     streams may run concurrently; a plan is read-only after creation and
- *     may be shared by concurrent calls.
+ *     streams may run concurrently, except calls that share one plan (see
+ *     msx_csr_plan_create).
  *   - Errors are status codes; msx_last_error() returns a thread-local text
  *     for the last failing call on the calling thread.  The texts for shape
  *     and dtype problems follow the reference validators
@@ -76,6 +76,7 @@ typedef struct msx_plan_info {
   int64_t block_rows;  /* R: a short block never crosses a multiple of R rows */
   int64_t chunk_nnz;   /* C: long rows are split into chunks of C values */
   int64_t n_blocks;    /* short blocks */
+  int64_t n_bounds;    /* entries of the bounds list: short blocks + long rows */
   int64_t n_long_rows; /* rows with more than W stored values */
   int64_t n_chunks;    /* total chunks over all long rows */
   int64_t device;      /* HIP device ordinal the plan lives on */
@@ -97,7 +98,9 @@ msx_status msx_device_count(int *count);
  * blocks (consecutive rows processed by one wavefront) and long rows (split
  * into chunks processed by whole workgroups, then summed in chunk order).
  * Synchronises `stream` once to read the block counts.  `block_nnz` selects
- * W (0 = library default; otherwise a power of two in [64, 1024]).
+ * W (0 = library default 512; otherwise a power of two in [64, 1024]).
+ * The plan holds scratch for long-row chunk sums: calls sharing one plan
+ * must be ordered (one stream) - concurrent calls on a shared plan race.
  *
  * Replaces the reference's per-launch kernel choice `nnz >= 32 * n_rows`
  * (reference: src/sparse/csr_matvec/csr_matvec.cpp:291-296), which has no
@@ -117,14 +120,16 @@ msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info *info);
 /*
  * Copy a plan's index arrays to host memory (synchronous), for bit-exact
  * checks of the binning.  Each pointer may be NULL to skip that array.
- *   block_row_begin: n_blocks + 1 int64 (first row of each short block, then
- *                    a sentinel equal to n_rows);
+ *   bounds:          n_bounds + 1 int64: in row order, each row that starts a
+ *                    short block or is long, long rows with bit 31 set
+ *                    (value row | 2^31), then a sentinel equal to n_rows.  A
+ *                    short block spans its entry up to the next entry;
  *   long_rows:       n_long_rows int64 (row ids, ascending);
  *   long_chunk_begin: n_long_rows + 1 int64 (first chunk of each long row,
  *                    then n_chunks).
  */
 msx_status msx_csr_plan_export(const msx_csr_plan *plan,
-                               int64_t *block_row_begin, int64_t *long_rows,
+                               int64_t *bounds, int64_t *long_rows,
                                int64_t *long_chunk_begin);
 
 /*

@@ -12,6 +12,12 @@
 //                  chunks; each chunk is summed by one workgroup and the chunk
 //                  sums of a row are added in chunk order.
 //
+// Storage: `bounds` lists, in row order, every row that starts a short block
+// or is long (long rows flagged in bit 31), then the sentinel n_rows; a short
+// block runs from its entry to the next entry, so it never contains a long
+// row.  `bounds_nnz` holds indptr at each entry (int64), which saves the
+// kernels one dependent load.  Long rows also get a chunk list.
+//
 // This replaces the reference's single per-launch choice between a
 // one-thread-per-row and a 128-lane-per-row kernel from the matrix average
 // `nnz >= 32 * n_rows` (reference: src/sparse/csr_matvec/csr_matvec.cpp:40-41,
@@ -35,9 +41,10 @@ namespace {
 constexpr int kPlanThreads = 256;
 constexpr int kRowsPerThread = 16;
 constexpr int64_t kTileRows = static_cast<int64_t>(kPlanThreads) * kRowsPerThread;
+constexpr uint32_t kLongFlag = 0x80000000u;
 
 struct Counts {
-  int64_t starts;
+  int64_t bounds;  // rows that start a short block or are long
   int64_t longs;
   int64_t chunks;
 };
@@ -101,11 +108,11 @@ __global__ void __launch_bounds__(kPlanThreads)
     const int64_t r = r0 + i;
     if (r >= n) break;
     const RowClass rc = classify(indptr, r, W, R, C);
-    c.starts += rc.start;
+    c.bounds += rc.start || rc.is_long;
     c.longs += rc.is_long;
     c.chunks += rc.chunks;
   }
-  const int64_t s = block_inclusive_scan(c.starts, lds[0]);
+  const int64_t s = block_inclusive_scan(c.bounds, lds[0]);
   const int64_t l = block_inclusive_scan(c.longs, lds[1]);
   const int64_t k = block_inclusive_scan(c.chunks, lds[2]);
   if (threadIdx.x == kPlanThreads - 1) tile_counts[tile] = Counts{s, l, k};
@@ -119,17 +126,17 @@ __global__ void __launch_bounds__(kPlanThreads)
   for (int64_t base = 0; base < n_tiles; base += kPlanThreads) {
     const int64_t t = base + threadIdx.x;
     const Counts v = t < n_tiles ? tile_counts[t] : Counts{0, 0, 0};
-    const int64_t s = block_inclusive_scan(v.starts, lds[0]);
+    const int64_t s = block_inclusive_scan(v.bounds, lds[0]);
     const int64_t l = block_inclusive_scan(v.longs, lds[1]);
     const int64_t k = block_inclusive_scan(v.chunks, lds[2]);
     if (t < n_tiles)
-      tile_counts[t] = Counts{carry.starts + s - v.starts, carry.longs + l - v.longs,
+      tile_counts[t] = Counts{carry.bounds + s - v.bounds, carry.longs + l - v.longs,
                               carry.chunks + k - v.chunks};
     // the last thread holds the batch total; broadcast through LDS
     __shared__ Counts batch_total;
     if (threadIdx.x == kPlanThreads - 1) batch_total = Counts{s, l, k};
     __syncthreads();
-    carry.starts += batch_total.starts;
+    carry.bounds += batch_total.bounds;
     carry.longs += batch_total.longs;
     carry.chunks += batch_total.chunks;
     __syncthreads();
@@ -140,8 +147,8 @@ __global__ void __launch_bounds__(kPlanThreads)
 template <class I>
 __global__ void __launch_bounds__(kPlanThreads)
     plan_scatter(const I *__restrict__ indptr, int64_t n, int64_t W, int64_t R, int64_t C,
-                 const Counts *__restrict__ tile_offsets, int64_t n_blocks, int64_t n_long,
-                 int64_t n_chunks, int32_t *__restrict__ block_row_begin,
+                 const Counts *__restrict__ tile_offsets, int64_t n_bounds, int64_t n_long,
+                 int64_t n_chunks, int32_t *__restrict__ bounds, int64_t *__restrict__ bounds_nnz,
                  int32_t *__restrict__ long_rows, int32_t *__restrict__ long_chunk_begin,
                  int32_t *__restrict__ chunk_row) {
   __shared__ int64_t lds[3][kPlanThreads / kWave];
@@ -152,19 +159,23 @@ __global__ void __launch_bounds__(kPlanThreads)
     const int64_t r = r0 + i;
     if (r >= n) break;
     const RowClass rc = classify(indptr, r, W, R, C);
-    c.starts += rc.start;
+    c.bounds += rc.start || rc.is_long;
     c.longs += rc.is_long;
     c.chunks += rc.chunks;
   }
   const Counts base = tile_offsets[tile];
-  int64_t s = base.starts + block_inclusive_scan(c.starts, lds[0]) - c.starts;
+  int64_t s = base.bounds + block_inclusive_scan(c.bounds, lds[0]) - c.bounds;
   int64_t l = base.longs + block_inclusive_scan(c.longs, lds[1]) - c.longs;
   int64_t k = base.chunks + block_inclusive_scan(c.chunks, lds[2]) - c.chunks;
   for (int i = 0; i < kRowsPerThread; ++i) {
     const int64_t r = r0 + i;
     if (r >= n) break;
     const RowClass rc = classify(indptr, r, W, R, C);
-    if (rc.start) block_row_begin[s++] = static_cast<int32_t>(r);
+    if (rc.start || rc.is_long) {
+      bounds[s] = static_cast<int32_t>(static_cast<uint32_t>(r) | (rc.is_long ? kLongFlag : 0u));
+      bounds_nnz[s] = static_cast<int64_t>(indptr[r]);
+      ++s;
+    }
     if (rc.is_long) {
       long_rows[l] = static_cast<int32_t>(r);
       long_chunk_begin[l] = static_cast<int32_t>(k);
@@ -174,7 +185,8 @@ __global__ void __launch_bounds__(kPlanThreads)
     }
   }
   if (tile == 0 && threadIdx.x == 0) {
-    block_row_begin[n_blocks] = static_cast<int32_t>(n);
+    bounds[n_bounds] = static_cast<int32_t>(n);
+    bounds_nnz[n_bounds] = static_cast<int64_t>(indptr[n]);
     long_chunk_begin[n_long] = static_cast<int32_t>(n_chunks);
   }
 }
@@ -200,23 +212,26 @@ msx_status build_plan(msx_csr_plan *p, const I *indptr, hipStream_t stream) {
       (void)hipFree(tmp);
       return hip_fail(e, "plan count");
     }
-    p->n_blocks = totals.starts;
+    p->n_bounds = totals.bounds;
     p->n_long = totals.longs;
     p->n_chunks = totals.chunks;
+    p->n_blocks = p->n_bounds - p->n_long;
   } else {
-    p->n_blocks = p->n_long = p->n_chunks = 0;
+    p->n_bounds = p->n_blocks = p->n_long = p->n_chunks = 0;
   }
-  if (p->n_chunks >= (int64_t{1} << 31) || p->n_blocks >= (int64_t{1} << 31)) {
+  if (p->n_chunks >= (int64_t{1} << 31) || p->n_bounds >= (int64_t{1} << 31)) {
     if (tmp) (void)hipFree(tmp);
     return fail(MSX_EINVAL, "msx_csr_plan_create: matrix too large for an int32 plan.");
   }
-  // One allocation: four int32 arrays then 8-byte chunk partial sums.
-  const size_t a0 = align_up(sizeof(int32_t) * (p->n_blocks + 1), 256);
-  const size_t a1 = align_up(sizeof(int32_t) * std::max<int64_t>(p->n_long, 1), 256);
-  const size_t a2 = align_up(sizeof(int32_t) * (p->n_long + 1), 256);
-  const size_t a3 = align_up(sizeof(int32_t) * std::max<int64_t>(p->n_chunks, 1), 256);
-  const size_t a4 = align_up(8 * std::max<int64_t>(p->n_chunks, 1), 256);
-  p->bytes = a0 + a1 + a2 + a3 + a4;
+  // One allocation: int32 bounds, int64 bounds_nnz, three int32 long-row
+  // arrays, then 8-byte chunk partial sums.
+  const size_t a0 = align_up(sizeof(int32_t) * (p->n_bounds + 1), 256);
+  const size_t a1 = align_up(sizeof(int64_t) * (p->n_bounds + 1), 256);
+  const size_t a2 = align_up(sizeof(int32_t) * std::max<int64_t>(p->n_long, 1), 256);
+  const size_t a3 = align_up(sizeof(int32_t) * (p->n_long + 1), 256);
+  const size_t a4 = align_up(sizeof(int32_t) * std::max<int64_t>(p->n_chunks, 1), 256);
+  const size_t a5 = align_up(8 * std::max<int64_t>(p->n_chunks, 1), 256);
+  p->bytes = a0 + a1 + a2 + a3 + a4 + a5;
   char *base = nullptr;
   hipError_t e = hipMalloc(&base, p->bytes);
   if (e != hipSuccess) {
@@ -225,16 +240,17 @@ msx_status build_plan(msx_csr_plan *p, const I *indptr, hipStream_t stream) {
     return fail(MSX_ENOMEM, "msx_csr_plan_create: device allocation of the plan failed.");
   }
   p->base = base;
-  p->block_row_begin = reinterpret_cast<int32_t *>(base);
-  p->long_rows = reinterpret_cast<int32_t *>(base + a0);
-  p->long_chunk_begin = reinterpret_cast<int32_t *>(base + a0 + a1);
-  p->chunk_row = reinterpret_cast<int32_t *>(base + a0 + a1 + a2);
-  p->partials = base + a0 + a1 + a2 + a3;
+  p->bounds = reinterpret_cast<int32_t *>(base);
+  p->bounds_nnz = reinterpret_cast<int64_t *>(base + a0);
+  p->long_rows = reinterpret_cast<int32_t *>(base + a0 + a1);
+  p->long_chunk_begin = reinterpret_cast<int32_t *>(base + a0 + a1 + a2);
+  p->chunk_row = reinterpret_cast<int32_t *>(base + a0 + a1 + a2 + a3);
+  p->partials = base + a0 + a1 + a2 + a3 + a4;
   if (n_tiles > 0) {
     hipLaunchKernelGGL(plan_scatter<I>, dim3(static_cast<uint32_t>(n_tiles)), dim3(kPlanThreads), 0,
                        stream, indptr, n, p->block_nnz, p->block_rows, p->chunk_nnz, tmp,
-                       p->n_blocks, p->n_long, p->n_chunks, p->block_row_begin, p->long_rows,
-                       p->long_chunk_begin, p->chunk_row);
+                       p->n_bounds, p->n_long, p->n_chunks, p->bounds, p->bounds_nnz,
+                       p->long_rows, p->long_chunk_begin, p->chunk_row);
     e = hipGetLastError();
     // tmp is read by the scatter kernel: release only after it has run.
     hipError_t e2 = hipStreamSynchronize(stream);
@@ -242,9 +258,10 @@ msx_status build_plan(msx_csr_plan *p, const I *indptr, hipStream_t stream) {
     if (e != hipSuccess) return hip_fail(e, "plan_scatter launch");
     if (e2 != hipSuccess) return hip_fail(e2, "plan_scatter");
   } else {
-    // n == 0: a single sentinel row id 0 and chunk offset 0
-    const int32_t zeros[2] = {0, 0};
-    MSX_HIP_TRY(hipMemcpy(p->block_row_begin, zeros, sizeof(int32_t), hipMemcpyHostToDevice));
+    // n == 0: sentinels only (row 0, nnz offset 0, chunk 0)
+    const int64_t zeros[2] = {0, 0};
+    MSX_HIP_TRY(hipMemcpy(p->bounds, zeros, sizeof(int32_t), hipMemcpyHostToDevice));
+    MSX_HIP_TRY(hipMemcpy(p->bounds_nnz, zeros, sizeof(int64_t), hipMemcpyHostToDevice));
     MSX_HIP_TRY(hipMemcpy(p->long_chunk_begin, zeros, sizeof(int32_t), hipMemcpyHostToDevice));
   }
   return MSX_OK;
@@ -320,6 +337,7 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->block_rows = plan->block_rows;
   info->chunk_nnz = plan->chunk_nnz;
   info->n_blocks = plan->n_blocks;
+  info->n_bounds = plan->n_bounds;
   info->n_long_rows = plan->n_long;
   info->n_chunks = plan->n_chunks;
   info->device = plan->device;
@@ -341,14 +359,14 @@ msx_status export_i32(const int32_t *src, int64_t count, int64_t *dst) {
 }
 }  // namespace
 
-extern "C" msx_status msx_csr_plan_export(const msx_csr_plan *plan, int64_t *block_row_begin,
+extern "C" msx_status msx_csr_plan_export(const msx_csr_plan *plan, int64_t *bounds,
                                           int64_t *long_rows, int64_t *long_chunk_begin) {
   clear_error();
   if (plan == nullptr) return fail(MSX_EINVAL, "msx_csr_plan_export: plan is NULL.");
   int prev = 0;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(plan->device);
-  msx_status st = export_i32(plan->block_row_begin, plan->n_blocks + 1, block_row_begin);
+  msx_status st = export_i32(plan->bounds, plan->n_bounds + 1, bounds);
   if (st == MSX_OK) st = export_i32(plan->long_rows, plan->n_long, long_rows);
   if (st == MSX_OK) st = export_i32(plan->long_chunk_begin, plan->n_long + 1, long_chunk_begin);
   (void)hipSetDevice(prev);

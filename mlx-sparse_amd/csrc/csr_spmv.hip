@@ -10,7 +10,7 @@
 //
 //   spmv_blocks      one wavefront per short block (< 2W values, <= R rows).
 //                    Phase 1 streams the block's contiguous indices/data with
-//                    16-32 byte buffer loads (4 values per lane per step; the
+//                    8-32 byte buffer loads (4 values per lane per load; the
 //                    buffer descriptor returns zero past the array end, so the
 //                    ragged edges need no scalar tail), gathers x, and stages
 //                    the products in LDS.  Phase 2 sums each row from LDS:
@@ -41,7 +41,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / kWave;
 constexpr uint32_t kMaxGrid = 1u << 20;  // workgroups per launch; kernels stride beyond
-constexpr size_t kMaxLds = 64 * 1024;    // LDS requested per workgroup, at most
 
 __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -54,71 +53,125 @@ __device__ inline void wave_lds_sync() {
 }
 
 // --------------------------------------------------------------------------
-template <class V, class I>
+// Short blocks.  W is a compile-time constant so each lane holds its whole
+// share of the block (QPL quads of 4 values) in registers: all index/value
+// loads of the block are issued before the first x gather, and all gathers
+// before the first use, so a wave keeps ~8 loads and 4*QPL gathers in flight
+// per lane.  The dependent chain per block is: plan entries -> (row pointers,
+// indices, values) -> x gathers -> LDS -> y.
+constexpr int kBlockRows = 256;  // R; equals the plan's block_rows
+
+template <class V, class I, int W>
 __global__ void __launch_bounds__(kThreads)
     spmv_blocks(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
-                typename V::Storage *__restrict__ y, const int32_t *__restrict__ block_row_begin,
-                int64_t n_blocks, int64_t nnz, int64_t n_cols, int W) {
+                typename V::Storage *__restrict__ y, const int32_t *__restrict__ bounds,
+                const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
+                int64_t n_cols) {
   using S = typename V::Storage;
   using A = typename V::Acc;
-  extern __shared__ char lds_raw[];
+  // A block spans < 2W values; with the 4-aligned start, <= W/2 + 1 quads.
+  constexpr int kQuads = W / 2 + 1;
+  constexpr int QPL = (kQuads + kWave - 1) / kWave;
+  constexpr int kCap = 4 * kQuads;  // products staged per wave
+  __shared__ A lds_prod[kWavesPerGroup][kCap];
+  __shared__ int32_t lds_ptr[kWavesPerGroup][kBlockRows + 1];
+
   const int lane = threadIdx.x % kWave;
   // wave-uniform by construction; readfirstlane lets the compiler keep the
   // block's buffer descriptors in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int cap = 2 * W + 4;
-  A *lds = reinterpret_cast<A *>(lds_raw) + wave * cap;
+  A *prod = lds_prod[wave];
+  int32_t *rptr = lds_ptr[wave];
 
   const uint32_t first = xcd_remap(blockIdx.x, gridDim.x);
-  for (int64_t wg = first; wg * kWavesPerGroup < n_blocks; wg += gridDim.x) {
+  for (int64_t wg = first; wg * kWavesPerGroup < n_bounds; wg += gridDim.x) {
     const int64_t b = wg * kWavesPerGroup + wave;
-    if (b >= n_blocks) break;
-    const int64_t r0 = block_row_begin[b];
-    const int64_t r1 = block_row_begin[b + 1];
-    const int64_t m = r1 - r0;
-    const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
-    const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0,
-                               std::min<int64_t>(nnz, p0 + 2 * W - 1));
+    if (b >= n_bounds) break;
+    const uint32_t e0 = static_cast<uint32_t>(bounds[b]);
+    if (e0 & 0x80000000u) continue;  // long row: summed by spmv_long
+    const int64_t r0 = e0;
+    const int64_t r1 = static_cast<uint32_t>(bounds[b + 1]) & 0x7fffffffu;
+    const int m = static_cast<int>(std::min<int64_t>(r1 - r0, kBlockRows));
+    const int64_t p0 = clamp64(bounds_nnz[b], 0, nnz);
+    const int64_t p1 = clamp64(bounds_nnz[b + 1], p0, std::min<int64_t>(nnz, p0 + 2 * W - 1));
     const int64_t a0 = p0 & ~int64_t{3};
     const int nq = static_cast<int>((p1 - a0 + 3) >> 2);
 
-    // Phase 1: products of the block's values into LDS, index q - a0.
+    // Row pointers of the block, relative to a0 and clamped into the block.
+    int32_t rp[(kBlockRows + kWave) / kWave];
+#pragma unroll
+    for (int k = 0; k < (kBlockRows + kWave) / kWave; ++k) {
+      const int i = lane + k * kWave;
+      rp[k] = 0;
+      if (i <= m) rp[k] = static_cast<int32_t>(clamp64(static_cast<int64_t>(indptr[r0 + i]), p0, p1) - a0);
+    }
+
+    // Phase 1: all quads of the block, then all gathers, then products.
     const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(nnz - a0) * sizeof(I));
     const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
-#pragma unroll 2
-    for (int q = lane; q < nq; q += kWave) {
-      const Quad<I> iq = load_quad<I>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
-      const Quad<S> dq = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+    Quad<I> iq[QPL];
+    Quad<S> dq[QPL];
+#pragma unroll
+    for (int k = 0; k < QPL; ++k) {
+      const int q = lane + k * kWave;
+      if (q < nq) {
+        iq[k] = load_quad<I>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
+        dq[k] = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+      }
+    }
+    S xv[QPL][4];
+#pragma unroll
+    for (int k = 0; k < QPL; ++k) {
+      const int q = lane + k * kWave;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t pos = a0 + 4 * q + e;
-        const int64_t col = static_cast<int64_t>(iq.v[e]);
-        A prod = vzero<A>();
-        if (pos >= p0 && pos < p1 && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
-          prod = vmul<V>(dq.v[e], x[col]);
-        lds[4 * q + e] = prod;
+        const int64_t col = static_cast<int64_t>(iq[k].v[e]);
+        xv[k][e] = S{};
+        if (q < nq && pos >= p0 && pos < p1 &&
+            static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+          xv[k][e] = x[col];
       }
+    }
+#pragma unroll
+    for (int k = 0; k < QPL; ++k) {
+      const int q = lane + k * kWave;
+      if (q < nq) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = a0 + 4 * q + e;
+          A pv = vzero<A>();
+          if (pos >= p0 && pos < p1) pv = vmul<V>(dq[k].v[e], xv[k][e]);
+          prod[4 * q + e] = pv;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < (kBlockRows + kWave) / kWave; ++k) {
+      const int i = lane + k * kWave;
+      if (i <= m) rptr[i] = rp[k];
     }
     wave_lds_sync();
 
-    // Phase 2: row sums from LDS.
-    const int64_t avg = m > 0 ? (p1 - p0) / m : 0;
-    int L = 1;
-    if (avg > 32 && m <= 32) {
-      L = kWave;
-      while (L * m > kWave) L >>= 1;
+    // Phase 2: row sums from LDS.  One lane per row (stored order) unless
+    // the block holds few rows averaging more than 32 values; then L lanes
+    // per row and an XOR butterfly.
+    int lg = 0;
+    if (p1 - p0 > 32 * static_cast<int64_t>(m) && m <= 32) {
+      lg = 6;
+      while ((m << lg) > kWave) --lg;
     }
-    const int rows_per_pass = kWave / L;
-    const int g = lane / L;
-    const int j = lane % L;
-    for (int64_t i0 = 0; i0 < m; i0 += rows_per_pass) {
-      const int64_t i = i0 + g;
+    const int L = 1 << lg;
+    const int g = lane >> lg;
+    const int j = lane & (L - 1);
+    for (int i0 = 0; i0 < m; i0 += (kWave >> lg)) {
+      const int i = i0 + g;
       A acc = vzero<A>();
       if (i < m) {
-        const int64_t s = clamp64(static_cast<int64_t>(indptr[r0 + i]), p0, p1);
-        const int64_t e = clamp64(static_cast<int64_t>(indptr[r0 + i + 1]), s, p1);
-        for (int64_t q = s + j; q < e; q += L) acc = vadd(acc, lds[q - a0]);
+        const int s = rptr[i];
+        const int e = rptr[i + 1];
+        for (int q = s + j; q < e; q += L) acc = vadd(acc, prod[q]);
       }
       for (int d = L >> 1; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
       if (i < m && j == 0) y[r0 + i] = V::narrow(acc);
@@ -260,16 +313,21 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // (capped at 16 bytes).
   const bool quads_ok = aligned(data, std::min<size_t>(16, 4 * sizeof(S))) &&
                         aligned(indices, std::min<size_t>(16, 4 * sizeof(I)));
-  const size_t plan_lds =
-      plan ? static_cast<size_t>(kWavesPerGroup) * (2 * plan->block_nnz + 4) * sizeof(A) : 0;
-  if (plan != nullptr && quads_ok && plan_lds <= kMaxLds) {
-    if (plan->n_blocks > 0) {
-      const int W = static_cast<int>(plan->block_nnz);
-      const size_t lds = plan_lds;
-      const int64_t groups = (plan->n_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
-      hipLaunchKernelGGL((spmv_blocks<V, I>), dim3(grid_for(groups)), dim3(kThreads), lds, stream,
-                         data, indices, indptr, x, y, plan->block_row_begin, plan->n_blocks, nnz,
-                         n_cols, W);
+  if (plan != nullptr && quads_ok) {
+    if (plan->n_bounds > plan->n_long) {
+      const int64_t groups = (plan->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
+      const dim3 grid(grid_for(groups)), block(kThreads);
+#define MSX_SPMV_BLOCKS(WV)                                                                  \
+  hipLaunchKernelGGL((spmv_blocks<V, I, WV>), grid, block, 0, stream, data, indices, indptr, x, \
+                     y, plan->bounds, plan->bounds_nnz, plan->n_bounds, nnz, n_cols)
+      switch (plan->block_nnz) {
+      case 64: MSX_SPMV_BLOCKS(64); break;
+      case 128: MSX_SPMV_BLOCKS(128); break;
+      case 256: MSX_SPMV_BLOCKS(256); break;
+      case 512: MSX_SPMV_BLOCKS(512); break;
+      default: MSX_SPMV_BLOCKS(1024); break;
+      }
+#undef MSX_SPMV_BLOCKS
       MSX_HIP_TRY(hipGetLastError());
     }
     if (plan->n_chunks > 0) {

@@ -124,12 +124,18 @@ __device__ inline c64 shfl_xor(c64 v, int m) {
 // ---------------------------------------------------------------------------
 // Buffer resources.  A raw buffer descriptor bounds every load to
 // [base, base + num_bytes): out-of-range lanes read zero instead of faulting,
-// which lets the edge chunks of a row block use full-width loads.
+// which lets the edge chunks of a row block use full-width loads.  The range
+// check works on whole dwords - a dword that straddles the end reads as zero
+// - so the size is rounded up to a dword.  Callers pass a base aligned to at
+// least 4 bytes, so the rounded tail lies in the same aligned dword as the
+// last valid byte (never another page); the kernels mask elements past the
+// end themselves.
 
 constexpr int kBufferFlags = 0x00020000;  // gfx9 raw-buffer dword3
 
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t num_bytes) {
-  const uint32_t n = num_bytes > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(num_bytes);
+  num_bytes = (num_bytes + 3) & ~uint64_t{3};
+  const uint32_t n = num_bytes > 0xfffffffcull ? 0xfffffffcu : static_cast<uint32_t>(num_bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
                                            static_cast<int>(n), kBufferFlags);
 }

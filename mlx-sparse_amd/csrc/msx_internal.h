@@ -31,7 +31,7 @@ bool valid_itype(int it);
 // Plan defaults.  W: window of the nnz range that a short block's row starts
 // fall in (block nnz < 2W); R: short blocks never cross a multiple of R rows;
 // C: chunk length of long rows.
-constexpr int64_t kDefaultBlockNnz = 256;
+constexpr int64_t kDefaultBlockNnz = 512;
 constexpr int64_t kBlockRows = 256;
 constexpr int64_t kChunkNnz = 4096;
 
@@ -44,13 +44,15 @@ struct msx_csr_plan {
   int64_t block_nnz;   // W
   int64_t block_rows;  // R
   int64_t chunk_nnz;   // C
-  int64_t n_blocks;
+  int64_t n_blocks;    // short blocks
+  int64_t n_bounds;    // short blocks + long rows
   int64_t n_long;
   int64_t n_chunks;
   int device;
   size_t bytes;
-  // Device arrays, all int32 (rows < 2^31; chunk ids < 2^31 checked at build).
-  int32_t *block_row_begin;   // n_blocks + 1
+  // Device arrays (rows < 2^31; chunk ids < 2^31 checked at build).
+  int32_t *bounds;            // n_bounds + 1: block-start or long row (bit 31), sentinel n
+  int64_t *bounds_nnz;        // n_bounds + 1: indptr at each entry
   int32_t *long_rows;         // n_long
   int32_t *long_chunk_begin;  // n_long + 1
   int32_t *chunk_row;         // n_chunks: index into long_rows

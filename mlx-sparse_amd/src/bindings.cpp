@@ -196,6 +196,7 @@ py::dict plan_info(const Plan &plan) {
   d["block_rows"] = info.block_rows;
   d["chunk_nnz"] = info.chunk_nnz;
   d["n_blocks"] = info.n_blocks;
+  d["n_bounds"] = info.n_bounds;
   d["n_long_rows"] = info.n_long_rows;
   d["n_chunks"] = info.n_chunks;
   d["device"] = info.device;
@@ -208,7 +209,7 @@ py::tuple plan_export(const Plan &plan) {
   msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_export");
   py::dict kw;
   kw["dtype"] = torch().attr("int64");
-  py::object blocks = torch().attr("empty")(info.n_blocks + 1, **kw);
+  py::object blocks = torch().attr("empty")(info.n_bounds + 1, **kw);
   py::object longs = torch().attr("empty")(info.n_long_rows, **kw);
   py::object chunks = torch().attr("empty")(info.n_long_rows + 1, **kw);
   auto ptr = [](py::object &t) {
@@ -247,7 +248,7 @@ PYBIND11_MODULE(_ext, m) {
       .def_readonly("device", &Plan::device)
       .def("info", &plan_info, "Plan summary (block and long-row counts, sizes).")
       .def("export", &plan_export,
-           "Host copies (int64 tensors) of block_row_begin, long_rows and long_chunk_begin.");
+           "Host copies (int64 tensors) of bounds, long_rows and long_chunk_begin.");
 
   m.def("_compiled_capabilities", &compiled_capabilities,
         "Return compile-time native backend facts for capability reporting.");

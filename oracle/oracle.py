@@ -193,6 +193,30 @@ def row_scale(data, indices, indptr, x, n_rows: int, *, vtype: str | None = None
     return out
 
 
+def row_exact(data, indices, indptr, x, n_rows: int, *, vtype: str | None = None) -> np.ndarray:
+    """Per-row sum of a_ij * x_j in float64 / complex128: products of two
+    binary16/bfloat16/binary32 values are exact in binary64, so only the
+    float64 summation rounds (relative error ~ n * 2^-53)."""
+    vt = _vtype_of(np.asarray(data), vtype)
+    d, xv = np.asarray(data), np.asarray(x)
+    if vt == "bfloat16":
+        d, xv = bf16_bits_to_f32(d), bf16_bits_to_f32(xv)
+    wide = np.complex128 if vt == "complex64" else np.float64
+    d, xv = d.astype(wide), xv.astype(wide)
+    indptr = np.asarray(indptr, dtype=np.int64)
+    rows = np.repeat(np.arange(n_rows), np.diff(indptr))
+    cols = np.asarray(indices, dtype=np.int64)
+    if xv.ndim == 1:
+        terms = d * xv[cols]
+        if vt == "complex64":
+            return (np.bincount(rows, weights=terms.real, minlength=n_rows)
+                    + 1j * np.bincount(rows, weights=terms.imag, minlength=n_rows))
+        return np.bincount(rows, weights=terms, minlength=n_rows)
+    out = np.zeros((n_rows, xv.shape[1]), dtype=wide)
+    np.add.at(out, rows, d[:, None] * xv[cols])
+    return out
+
+
 __all__ = [
     "VTYPES",
     "build",
@@ -206,5 +230,5 @@ __all__ = [
     "bf16_bits_to_f32",
     "f16_bits_to_f32",
     "row_scale",
-    "os",
+    "row_exact",
 ]

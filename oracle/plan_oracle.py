@@ -9,7 +9,10 @@ len(r) = indptr[r+1] - indptr[r]:
 
 - r is long when len(r) > W; a long row has ceil(len / C) chunks;
 - a row that is not long starts a short block when r == 0, r % R == 0,
-  row r-1 is long, or floor(indptr[r] / W) != floor(indptr[r-1] / W).
+  row r-1 is long, or floor(indptr[r] / W) != floor(indptr[r-1] / W);
+- ``bounds`` lists, in row order, every block-start row and every long row,
+  long rows with bit 31 set, then the sentinel n; a short block spans its
+  entry up to the next entry.
 
 Pinned in tests/test_plan_oracle.py by a per-row pure-Python loop and by the
 block invariants (coverage, < 2W values, <= R rows).
@@ -20,9 +23,12 @@ from __future__ import annotations
 import numpy as np
 
 
-def plan(indptr, W: int = 256, R: int = 256, C: int = 4096):
-    """Returns (block_row_begin incl. sentinel n, long_rows, long_chunk_begin
-    incl. sentinel n_chunks) as int64 arrays."""
+LONG_FLAG = 1 << 31
+
+
+def plan(indptr, W: int = 512, R: int = 256, C: int = 4096):
+    """Returns (bounds incl. sentinel n, long_rows, long_chunk_begin incl.
+    sentinel n_chunks) as int64 arrays."""
     p = np.asarray(indptr, dtype=np.int64)
     n = p.shape[0] - 1
     if n <= 0:
@@ -36,14 +42,16 @@ def plan(indptr, W: int = 256, R: int = 256, C: int = 4096):
     window = np.floor_divide(p[:-1], W)
     start[1:] |= is_long[:-1] | (window[1:] != window[:-1])
     start &= ~is_long
-    blocks = np.concatenate([np.nonzero(start)[0], [n]]).astype(np.int64)
+    entries = np.nonzero(start | is_long)[0].astype(np.int64)
+    entries = entries | np.where(is_long[entries], LONG_FLAG, 0)
+    blocks = np.concatenate([entries, [n]]).astype(np.int64)
     long_rows = np.nonzero(is_long)[0].astype(np.int64)
     chunks = -(-length[long_rows] // C)
     chunk_begin = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int64)
     return blocks, long_rows, chunk_begin
 
 
-def plan_loop(indptr, W: int = 256, R: int = 256, C: int = 4096):
+def plan_loop(indptr, W: int = 512, R: int = 256, C: int = 4096):
     """Same rule as ``plan`` with plain per-row loops (small inputs only)."""
     p = [int(v) for v in indptr]
     n = len(p) - 1
@@ -52,6 +60,7 @@ def plan_loop(indptr, W: int = 256, R: int = 256, C: int = 4096):
         ln = p[r + 1] - p[r]
         if ln > W:
             longs.append(r)
+            blocks.append(r + LONG_FLAG)
             chunk_begin.append(chunk_begin[-1] + (ln + C - 1) // C)
             continue
         prev_long = r > 0 and p[r] - p[r - 1] > W

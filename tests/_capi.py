@@ -20,7 +20,7 @@ OK, EINVAL, ETYPE, EHIP, ENOMEM = range(5)
 
 class PlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in (
-        "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_long_rows",
+        "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_bounds", "n_long_rows",
         "n_chunks", "device", "plan_bytes")]
 
 
@@ -85,7 +85,7 @@ class Plan:
 
     def export(self):
         info = self.info()
-        blocks = torch.empty(info.n_blocks + 1, dtype=torch.int64)
+        blocks = torch.empty(info.n_bounds + 1, dtype=torch.int64)
         longs = torch.empty(max(info.n_long_rows, 1), dtype=torch.int64)
         chunks = torch.empty(info.n_long_rows + 1, dtype=torch.int64)
         st = lib().msx_csr_plan_export(self.ptr, _p(blocks), _p(longs), _p(chunks))

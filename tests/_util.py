@@ -50,14 +50,35 @@ def widen(arr: np.ndarray, vtype: str) -> np.ndarray:
 
 
 def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtype: str,
-                      what: str = "") -> float:
+                      what: str = "", exact: np.ndarray | None = None,
+                      lengths: np.ndarray | None = None, min_len_exempt: int = 0) -> dict:
     """Per-row parity: |got - want| <= TOL[vtype] * scale (+ a denormal floor).
-    Returns the largest error relative to the scale."""
+
+    With ``exact`` (float64 row sums), a row outside the bound still passes
+    when it is at least as close to the exact sum as the oracle is AND the
+    row holds at least ``min_len_exempt`` values: on such long rows the
+    oracle's sequential float32 sum itself drifts past the tolerance (error
+    ~ 2^-24 * sqrt(n) relative), and a GPU tree sum that is more accurate
+    must not fail for that.  Such rows are counted in the returned report.
+    """
     g = widen(got, vtype)
     w = widen(want, vtype)
     err = np.abs(g - w)
     bound = TOL[vtype] * scale + 1e-30
     bad = err > bound
+    report = {"rows_outside_tol_vs_oracle": int(bad.sum()), "exempt_rows": 0}
+    if bad.any() and exact is not None:
+        closer = np.abs(g - exact) <= np.abs(w - exact)
+        long_enough = np.ones_like(bad) if lengths is None else (
+            np.broadcast_to(lengths.reshape(-1, *([1] * (bad.ndim - 1))), bad.shape) >= min_len_exempt)
+        exempt = bad & closer & long_enough
+        report["exempt_rows"] = int(exempt.sum())
+        if exempt.any():
+            idx = np.argwhere(exempt)[0]
+            report["example"] = {"row": idx.tolist(), "gpu_err_vs_exact": float(np.abs(g - exact)[tuple(idx)]),
+                                 "oracle_err_vs_exact": float(np.abs(w - exact)[tuple(idx)]),
+                                 "scale": float(scale[tuple(idx)])}
+        bad = bad & ~exempt
     if bad.any():
         idx = np.argwhere(bad)[:5]
         raise AssertionError(
@@ -66,4 +87,5 @@ def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtyp
             f"scale {scale[tuple(idx[0])]})")
     with np.errstate(divide="ignore", invalid="ignore"):
         rel = np.where(scale > 0, err / np.maximum(scale, 1e-300), 0.0)
-    return float(rel.max()) if rel.size else 0.0
+    report["max_rel_err"] = float(rel.max()) if rel.size else 0.0
+    return report

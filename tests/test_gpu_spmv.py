@@ -43,9 +43,18 @@ def _random_csr(rng, n_rows, n_cols, lengths, index_dtype):
     return indices.astype(index_dtype), indptr.astype(index_dtype), nnz
 
 
+# Rows this long may differ from the oracle by more than the tolerance only
+# where the GPU sum is the more accurate one: the oracle's stored-order
+# float32 sum has a typical relative error 2^-24 * sqrt(n / 3), which passes
+# 1e-5 near n = 10^5 (the power-law matrix holds rows up to 200,000 values).
+LONG_ROW_EXEMPT = 10_000
+
+
 def _check_spmv(data, indices, indptr, x, n_rows, n_cols, vtype, plan_w=0, what=""):
     want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
     scale = orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype)
+    exact = orc.row_exact(data, indices, indptr, x, n_rows, vtype=vtype)
+    lengths = np.diff(np.asarray(indptr, dtype=np.int64))
     d, i, p = _upload(data, indices, indptr, vtype)
     xt = to_torch(x, vtype, DEV)
     out = {}
@@ -54,7 +63,10 @@ def _check_spmv(data, indices, indptr, x, n_rows, n_cols, vtype, plan_w=0, what=
         y = _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=pl)
         torch.cuda.synchronize()
         got = to_numpy(y)
-        assert_rows_close(got, want, scale, vtype, f"{what} {label}")
+        rep = assert_rows_close(got, want, scale, vtype, f"{what} {label}", exact=exact,
+                                lengths=lengths, min_len_exempt=LONG_ROW_EXEMPT)
+        if rep["exempt_rows"]:
+            print(f"{what} {label}: {rep}")
         out[label] = got
     if plan is not None:
         plan.close()
@@ -156,7 +168,8 @@ def test_plan_bins_bit_exact(W):
         for g, w, name in zip(got, want, ("blocks", "long_rows", "chunk_begin")):
             np.testing.assert_array_equal(g, w, err_msg=name)
         info = plan.info()
-        assert info.n_blocks == want[0].size - 1 and info.n_long_rows == want[1].size
+        assert info.n_bounds == want[0].size - 1 and info.n_long_rows == want[1].size
+        assert info.n_blocks == info.n_bounds - info.n_long_rows
         plan.close()
 
 

@@ -27,7 +27,7 @@ def _indptr(rng, n, kind):
 
 
 @pytest.mark.parametrize("kind", ["uniform", "mixed", "empty", "zipf"])
-@pytest.mark.parametrize("W", [64, 256, 1024])
+@pytest.mark.parametrize("W", [64, 256, 512, 1024])
 def test_vectorised_rule_matches_loop(kind, W):
     rng = np.random.default_rng(W)
     p = _indptr(rng, 3000, kind)
@@ -39,23 +39,28 @@ def test_vectorised_rule_matches_loop(kind, W):
 
 @pytest.mark.parametrize("kind", ["uniform", "mixed", "empty", "zipf"])
 def test_block_invariants(kind):
-    W, R, C = 256, 256, 4096
+    W, R, C = 512, 256, 4096
     rng = np.random.default_rng(3)
     p = _indptr(rng, 5000, kind)
-    blocks, longs, chunk_begin = plan_oracle.plan(p, W=W, R=R, C=C)
+    bounds, longs, chunk_begin = plan_oracle.plan(p, W=W, R=R, C=C)
     lengths = np.diff(p)
+    flag = plan_oracle.LONG_FLAG
+    rows = bounds & (flag - 1)
+    assert np.all(np.diff(rows) > 0)  # strictly increasing entries
     covered = np.zeros(len(lengths), int)
-    for b0, b1 in zip(blocks[:-1], blocks[1:]):
-        # a block runs up to the next block start, skipping long rows after it
-        rows = np.arange(b0, b1)
-        rows = rows[lengths[rows] <= W]
-        stop = rows[0] + np.argmax(np.concatenate([lengths[rows[0]:b1] > W, [True]]))
-        rows = np.arange(b0, stop)
-        covered[rows] += 1
-        assert len(rows) <= R
-        assert p[rows[-1] + 1] - p[rows[0]] < 2 * W
-    covered[longs] += 1
+    for e, nxt in zip(bounds[:-1], rows[1:]):
+        r0 = e & (flag - 1)
+        if e & flag:
+            assert lengths[r0] > W
+            covered[r0] += 1
+            continue
+        block = np.arange(r0, nxt)
+        assert np.all(lengths[block] <= W)  # never contains a long row
+        assert len(block) <= R
+        assert p[block[-1] + 1] - p[block[0]] < 2 * W
+        covered[block] += 1
     assert np.all(covered == 1)
+    np.testing.assert_array_equal(rows[:-1][bounds[:-1] >= flag], longs)
     np.testing.assert_array_equal(np.diff(chunk_begin), -(-lengths[longs] // C))
 
 
