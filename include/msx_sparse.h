@@ -66,6 +66,20 @@ typedef enum msx_status {
 /* Opaque row-block plan built from `indptr` on the device. */
 typedef struct msx_csr_plan msx_csr_plan;
 
+/* Column slicing of a bound plan (msx_csr_plan_create_bound). */
+typedef enum msx_slice_mode {
+  MSX_SLICE_AUTO = 0, /* slice when x exceeds 8 MB and most blocks' columns
+                         span over a quarter of the columns */
+  MSX_SLICE_OFF = 1,
+  MSX_SLICE_ON = 2
+} msx_slice_mode;
+
+typedef struct msx_plan_options {
+  int64_t block_nnz;  /* W: 0 = default (512), else a power of two in [64, 1024] */
+  int32_t slice_mode; /* msx_slice_mode */
+  int32_t reserved;   /* must be 0 */
+} msx_plan_options;
+
 /* Summary of a plan, for callers that report or test it. */
 typedef struct msx_plan_info {
   int64_t n_rows;
@@ -81,6 +95,9 @@ typedef struct msx_plan_info {
   int64_t n_chunks;    /* total chunks over all long rows */
   int64_t device;      /* HIP device ordinal the plan lives on */
   int64_t plan_bytes;  /* device bytes held by the plan */
+  int64_t n_slices;    /* 0, or 8 when the plan holds a column-sliced copy */
+  int64_t slice_width; /* columns per slice */
+  int64_t slice_bytes; /* device bytes of the sliced copy and its partial sums */
 } msx_plan_info;
 
 /* ABI version of the loaded library (MSX_ABI_VERSION at build time). */
@@ -110,6 +127,30 @@ msx_status msx_device_count(int *count);
 msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
                                const void *indptr, int64_t block_nnz,
                                void *stream, msx_csr_plan **out);
+
+/*
+ * Build a plan bound to one matrix's values (`data`, `indices`, `indptr`,
+ * all device pointers) on `stream`: the row blocks of msx_csr_plan_create,
+ * plus - when `opts->slice_mode` asks for it, or in AUTO mode when x is over
+ * 8 MB and the columns are scattered - a copy of the short blocks' values
+ * reordered into 8 column slices.  Sliced SpMV runs slice s on the
+ * workgroups the hardware places on XCD s, so each XCD gathers from one
+ * eighth of x, which stays in its L2; per-slice row sums are then added in
+ * slice order.  `opts` may be NULL (defaults).  Synchronises `stream`.
+ *
+ * A bound plan reads the matrix from its own copy: msx_csr_spmv must be
+ * given the same data/indices/indptr pointers it was built from (other
+ * pointers are rejected with MSX_EINVAL), and the values must not change
+ * while the plan is in use.  Replaces, like msx_csr_plan_create, the
+ * reference's per-launch kernel choice (reference:
+ * src/sparse/csr_matvec/csr_matvec.cpp:291-296).
+ */
+msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it,
+                                     int64_t n_rows, int64_t n_cols,
+                                     int64_t nnz, const void *data,
+                                     const void *indices, const void *indptr,
+                                     const msx_plan_options *opts,
+                                     void *stream, msx_csr_plan **out);
 
 /* Release a plan (NULL is accepted).  Synchronises the plan's device. */
 msx_status msx_csr_plan_destroy(msx_csr_plan *plan);

@@ -62,11 +62,15 @@ msx_status check_common(const char *op, msx_vtype vt, msx_itype it, int64_t n_ro
   return MSX_OK;
 }
 
-msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_itype it, int64_t n_rows,
-                      int64_t nnz) {
+msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, msx_itype it,
+                      int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                      const void *indices) {
   if (plan == nullptr) return MSX_OK;
   if (plan->itype != it || plan->n_rows != n_rows || plan->nnz != nnz)
     return fail(MSX_EINVAL, std::string(op) + ": plan was built for a different matrix.");
+  if (plan->bound_data != nullptr && (plan->bound_data != data || plan->bound_indices != indices ||
+                                      plan->vtype != vt || plan->n_cols != n_cols))
+    return fail(MSX_EINVAL, std::string(op) + ": plan is bound to other data/indices buffers.");
   int dev = -1;
   MSX_HIP_TRY(hipGetDevice(&dev));
   if (dev != plan->device)
@@ -108,7 +112,7 @@ extern "C" msx_status msx_csr_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, i
   if (st != MSX_OK) return st;
   if (n_rows > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec y is NULL.");
   if (n_cols > 0 && nnz > 0 && x == nullptr) return fail(MSX_EINVAL, "csr_matvec x is NULL.");
-  st = check_plan("csr_matvec", plan, it, n_rows, nnz);
+  st = check_plan("csr_matvec", plan, vt, it, n_rows, n_cols, nnz, data, indices);
   if (st != MSX_OK) return st;
   if (n_rows == 0) return MSX_OK;
   return launch_spmv(vt, it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan,
@@ -128,7 +132,7 @@ extern "C" msx_status msx_csr_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, i
   if (n_rows > 0 && k > 0 && Y == nullptr) return fail(MSX_EINVAL, "csr_matmul Y is NULL.");
   if (n_cols > 0 && k > 0 && nnz > 0 && X == nullptr)
     return fail(MSX_EINVAL, "csr_matmul X is NULL.");
-  st = check_plan("csr_matmul", plan, it, n_rows, nnz);
+  st = check_plan("csr_matmul", plan, vt, it, n_rows, n_cols, nnz, data, indices);
   if (st != MSX_OK) return st;
   if (n_rows == 0 || k == 0) return MSX_OK;
   return launch_spmm(vt, it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,

@@ -272,10 +272,10 @@ msx_status build_plan(msx_csr_plan *p, const I *indptr, hipStream_t stream) {
 
 using namespace msx;
 
-extern "C" msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
-                                          const void *indptr, int64_t block_nnz, void *stream,
-                                          msx_csr_plan **out) {
-  clear_error();
+namespace {
+
+msx_status create_plan(msx_itype it, int64_t n_rows, int64_t nnz, const void *indptr,
+                       int64_t block_nnz, void *stream, msx_csr_plan **out) {
   if (out == nullptr) return fail(MSX_EINVAL, "msx_csr_plan_create: out is NULL.");
   *out = nullptr;
   if (!valid_itype(it))
@@ -296,6 +296,7 @@ extern "C" msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t 
   p->block_nnz = block_nnz;
   p->block_rows = kBlockRows;
   p->chunk_nnz = kChunkNnz;
+  p->slice_mode = MSX_SLICE_OFF;
   hipError_t e = hipGetDevice(&p->device);
   if (e != hipSuccess) {
     delete p;
@@ -313,6 +314,56 @@ extern "C" msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t 
   return MSX_OK;
 }
 
+void release(msx_csr_plan *p) {
+  if (p->base) (void)hipFree(p->base);
+  if (p->s_base) (void)hipFree(p->s_base);
+  delete p;
+}
+
+}  // namespace
+
+extern "C" msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
+                                          const void *indptr, int64_t block_nnz, void *stream,
+                                          msx_csr_plan **out) {
+  clear_error();
+  return create_plan(it, n_rows, nnz, indptr, block_nnz, stream, out);
+}
+
+extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                int64_t n_cols, int64_t nnz, const void *data,
+                                                const void *indices, const void *indptr,
+                                                const msx_plan_options *opts, void *stream,
+                                                msx_csr_plan **out) {
+  clear_error();
+  if (!valid_vtype(vt))
+    return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+  if (n_cols < 0 || n_cols > 2147483647)
+    return fail(MSX_EINVAL, "msx_csr_plan_create_bound: n_cols must be in [0, 2^31).");
+  if (nnz > 0 && (data == nullptr || indices == nullptr))
+    return fail(MSX_EINVAL, "msx_csr_plan_create_bound: data and indices must be non-NULL.");
+  const msx_plan_options defaults{0, MSX_SLICE_AUTO, 0};
+  if (opts == nullptr) opts = &defaults;
+  if (opts->slice_mode < MSX_SLICE_AUTO || opts->slice_mode > MSX_SLICE_ON || opts->reserved != 0)
+    return fail(MSX_EINVAL, "msx_csr_plan_create_bound: invalid options.");
+  msx_csr_plan *p = nullptr;
+  msx_status st = create_plan(it, n_rows, nnz, indptr, opts->block_nnz, stream, &p);
+  if (st != MSX_OK) return st;
+  p->vtype = vt;
+  p->n_cols = n_cols;
+  p->slice_mode = opts->slice_mode;
+  p->bound_data = data;
+  p->bound_indices = indices;
+  if (opts->slice_mode != MSX_SLICE_OFF && p->n_blocks > 0) {
+    st = build_slices(p, data, indices, indptr, static_cast<hipStream_t>(stream));
+    if (st != MSX_OK) {
+      release(p);
+      return st;
+    }
+  }
+  *out = p;
+  return MSX_OK;
+}
+
 extern "C" msx_status msx_csr_plan_destroy(msx_csr_plan *plan) {
   clear_error();
   if (plan == nullptr) return MSX_OK;
@@ -320,9 +371,8 @@ extern "C" msx_status msx_csr_plan_destroy(msx_csr_plan *plan) {
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(plan->device);
   hipError_t e = hipDeviceSynchronize();
-  if (plan->base) (void)hipFree(plan->base);
+  release(plan);
   (void)hipSetDevice(prev);
-  delete plan;
   if (e != hipSuccess) return hip_fail(e, "msx_csr_plan_destroy");
   return MSX_OK;
 }
@@ -341,18 +391,24 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->n_long_rows = plan->n_long;
   info->n_chunks = plan->n_chunks;
   info->device = plan->device;
-  info->plan_bytes = static_cast<int64_t>(plan->bytes);
+  info->plan_bytes = static_cast<int64_t>(plan->bytes + plan->s_bytes);
+  info->n_slices = plan->n_slices;
+  info->slice_width = plan->slice_width;
+  info->slice_bytes = static_cast<int64_t>(plan->s_bytes);
   return MSX_OK;
 }
 
 namespace {
-msx_status export_i32(const int32_t *src, int64_t count, int64_t *dst) {
+// Device int32 array -> host int64.  `as_unsigned` zero-extends (the bounds
+// list carries a flag in bit 31).
+msx_status export_i32(const int32_t *src, int64_t count, int64_t *dst, bool as_unsigned = false) {
   if (dst == nullptr || count <= 0) return MSX_OK;
   int32_t *tmp = new (std::nothrow) int32_t[count];
   if (tmp == nullptr) return fail(MSX_ENOMEM, "msx_csr_plan_export: host allocation failed.");
   hipError_t e = hipMemcpy(tmp, src, sizeof(int32_t) * count, hipMemcpyDeviceToHost);
   if (e == hipSuccess)
-    for (int64_t i = 0; i < count; ++i) dst[i] = tmp[i];
+    for (int64_t i = 0; i < count; ++i)
+      dst[i] = as_unsigned ? static_cast<int64_t>(static_cast<uint32_t>(tmp[i])) : tmp[i];
   delete[] tmp;
   if (e != hipSuccess) return hip_fail(e, "msx_csr_plan_export");
   return MSX_OK;
@@ -366,7 +422,7 @@ extern "C" msx_status msx_csr_plan_export(const msx_csr_plan *plan, int64_t *bou
   int prev = 0;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(plan->device);
-  msx_status st = export_i32(plan->bounds, plan->n_bounds + 1, bounds);
+  msx_status st = export_i32(plan->bounds, plan->n_bounds + 1, bounds, true);
   if (st == MSX_OK) st = export_i32(plan->long_rows, plan->n_long, long_rows);
   if (st == MSX_OK) st = export_i32(plan->long_chunk_begin, plan->n_long + 1, long_chunk_begin);
   (void)hipSetDevice(prev);

@@ -38,6 +38,12 @@
 namespace msx {
 namespace {
 
+#define MSX_HIP_TRY_ST(expr)         \
+  do {                               \
+    msx_status _s = (expr);          \
+    if (_s != MSX_OK) return _s;     \
+  } while (0)
+
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / kWave;
 constexpr uint32_t kMaxGrid = 1u << 20;  // workgroups per launch; kernels stride beyond
@@ -313,7 +319,12 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // (capped at 16 bytes).
   const bool quads_ok = aligned(data, std::min<size_t>(16, 4 * sizeof(S))) &&
                         aligned(indices, std::min<size_t>(16, 4 * sizeof(I)));
-  if (plan != nullptr && quads_ok) {
+  // Misaligned streams cannot use the quad loads of the plan kernels (the
+  // long-row kernel reads the caller's arrays even on a sliced plan).
+  const bool use_plan = plan != nullptr && quads_ok;
+  if (use_plan && plan->n_slices > 0) {
+    MSX_HIP_TRY_ST(launch_spmv_sliced(plan, x, y, stream));
+  } else if (use_plan) {
     if (plan->n_bounds > plan->n_long) {
       const int64_t groups = (plan->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
       const dim3 grid(grid_for(groups)), block(kThreads);
@@ -330,6 +341,8 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
 #undef MSX_SPMV_BLOCKS
       MSX_HIP_TRY(hipGetLastError());
     }
+  }
+  if (use_plan) {
     if (plan->n_chunks > 0) {
       hipLaunchKernelGGL((spmv_long<V, I>), dim3(grid_for(plan->n_chunks)), dim3(kThreads), 0,
                          stream, data, indices, indptr, x, y, plan->long_rows,

@@ -34,6 +34,8 @@ bool valid_itype(int it);
 constexpr int64_t kDefaultBlockNnz = 512;
 constexpr int64_t kBlockRows = 256;
 constexpr int64_t kChunkNnz = 4096;
+// Column slices of a sliced plan: one per XCD.
+constexpr int kSlices = 8;
 
 }  // namespace msx
 
@@ -58,6 +60,21 @@ struct msx_csr_plan {
   int32_t *chunk_row;         // n_chunks: index into long_rows
   void *partials;             // n_chunks * 8 bytes: long-row chunk sums
   void *base;                 // single allocation holding the arrays above
+  // Column slicing (csr_slice.hip); n_slices == 0 when the plan is not sliced.
+  msx_vtype vtype;
+  int64_t n_cols;
+  int slice_mode;
+  int n_slices;
+  int64_t slice_width;
+  int col_bits;
+  const void *bound_data;     // the buffers a bound plan was built from
+  const void *bound_indices;
+  void *s_data;               // values reordered by slice inside each short block
+  uint32_t *s_col;            // (row_in_block << col_bits) | column_in_slice
+  uint16_t *s_seg;            // n_bounds * (kSlices + 1) slice offsets per block
+  void *s_partial;            // kSlices * n_rows accumulators
+  void *s_base;
+  size_t s_bytes;
 };
 
 namespace msx {
@@ -66,6 +83,11 @@ namespace msx {
 msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr,
                        const void *x, void *y, const msx_csr_plan *plan, hipStream_t stream);
+
+// Sliced plans (csr_slice.hip).
+msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
+                        hipStream_t stream);
+msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream);
 
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,

@@ -99,13 +99,16 @@ class CSRArray:
         device = torch.device(device) if device is not None else self.device
         if device.type != "cuda" or not runtime.get(runtime.RuntimeOption.GPU_PLAN):
             return None
-        _, _, indptr = self.buffers(device)
+        data, indices, indptr = self.buffers(device)
         key = ("plan", str(indptr.device))
         hit = self._cache.get(key)
         if hit is None:
             from mlx_sparse import _native
 
-            hit = _native.csr_plan(indptr, self.shape[0], self.nnz)
+            # bound to this immutable matrix: may hold a column-sliced copy
+            hit = _native.csr_plan(indptr, self.shape[0], self.nnz, data=data, indices=indices,
+                                   n_cols=self.shape[1],
+                                   slice_mode=int(runtime.get(runtime.RuntimeOption.GPU_SLICE)))
             self._cache[key] = hit
         return hit
 

@@ -5,6 +5,8 @@ Only the CPU worker budget reaches this path.  As in the reference, the
 option is mirrored into ``MLX_SPARSE_CPU_THREADS`` in ``os.environ``, which
 the native CPU path reads on every call.  ``GPU_PLAN`` (new) toggles the
 cached row-block plan of the GPU SpMV; without it a plan-free kernel runs.
+``GPU_SLICE`` (new) selects the plan's XCD column slicing: "auto" (default),
+"off" or "on"; it applies to plans built while it is set.
 """
 
 from __future__ import annotations
@@ -15,13 +17,16 @@ import os
 from collections.abc import Iterator, Mapping
 from typing import Any
 
-_ENV = {"n_threads": "MLX_SPARSE_CPU_THREADS", "gpu_plan": "MLX_SPARSE_GPU_PLAN"}
+_ENV = {"n_threads": "MLX_SPARSE_CPU_THREADS", "gpu_plan": "MLX_SPARSE_GPU_PLAN",
+        "gpu_slice": "MLX_SPARSE_GPU_SLICE"}
+_SLICE = {"auto": 0, "off": 1, "on": 2}
 _MISSING = object()
 
 
 class RuntimeOption(str, enum.Enum):
     N_THREADS = "n_threads"
     GPU_PLAN = "gpu_plan"
+    GPU_SLICE = "gpu_slice"  # "auto" | "off" | "on": XCD column slicing of plans
 
 
 def _parse_threads(value: Any) -> int | str:
@@ -57,6 +62,8 @@ def get(option: RuntimeOption | str) -> Any:
             return _parse_threads(raw)
         except (TypeError, ValueError):
             return "auto"
+    if key == "gpu_slice":
+        return _SLICE.get((raw or "auto").strip().lower(), 0)
     return True if raw is None else _parse_bool(raw)
 
 
@@ -70,6 +77,11 @@ def _normalize_option(option) -> str:
 
 
 def _encode(key: str, value: Any) -> str | None:
+    if key == "gpu_slice":
+        v = str(value).strip().lower()
+        if v not in _SLICE:
+            raise ValueError(f"gpu_slice must be one of {sorted(_SLICE)}, got {value!r}.")
+        return v
     if key == "n_threads":
         parsed = _parse_threads(value)
         return None if parsed == "auto" else str(parsed)
@@ -150,6 +162,7 @@ def info() -> dict[str, Any]:
         "n_threads": threads,
         "n_threads_source": source,
         "gpu_plan": get(RuntimeOption.GPU_PLAN),
+        "gpu_slice": get(RuntimeOption.GPU_SLICE),
         "device": str(default_torch_device()),
         "extension": extension_available(),
         "gpu": gpu_name,

@@ -102,13 +102,15 @@ struct Plan {
   int64_t nnz = 0;
   std::string index_dtype;
   int device = -1;
+  py::object bound;  // tensors a bound plan was built from (kept alive)
   ~Plan() {
     if (p) msx_csr_plan_destroy(p);
   }
 };
 
 std::shared_ptr<Plan> make_plan(py::handle indptr_obj, int64_t n_rows, int64_t nnz,
-                                int64_t block_nnz) {
+                                int64_t block_nnz, py::object data_obj, py::object indices_obj,
+                                int64_t n_cols, int slice_mode) {
   py::object indptr = contiguous(indptr_obj);
   ArrayView v = view_of(indptr);
   msx::require_rank(v, 1, "csr_plan indptr");
@@ -122,10 +124,28 @@ std::shared_ptr<Plan> make_plan(py::handle indptr_obj, int64_t n_rows, int64_t n
   plan->index_dtype = v.dtype_name;
   plan->device = v.device;
   msx_status st;
-  {
+  if (data_obj.is_none()) {
     py::gil_scoped_release nogil;
     st = msx_csr_plan_create(msx::to_itype(v.dtype), n_rows, nnz, v.ptr, block_nnz, stream,
                              &plan->p);
+  } else {
+    // A bound plan reads the values it was built from: the caller keeps these
+    // exact (contiguous, same-device) tensors alive and unchanged.
+    const ArrayView vd = view_of(data_obj), vi = view_of(indices_obj);
+    msx::require_rank(vd, 1, "csr_plan data");
+    msx::require_rank(vi, 1, "csr_plan indices");
+    msx::require_supported_value_dtype(vd, "csr_plan data");
+    msx::require_same_index_dtype(vi, v, "csr_plan indices", "csr_plan indptr");
+    msx::require_size(vd, nnz, "csr_plan data");
+    msx::require_size(vi, nnz, "csr_plan indices");
+    msx::require_same_device({&vd, &vi, &v}, "csr_plan");
+    msx::require_contiguous(vd, "csr_plan data");
+    msx::require_contiguous(vi, "csr_plan indices");
+    plan->bound = py::make_tuple(data_obj, indices_obj, indptr);
+    msx_plan_options opts{block_nnz, slice_mode, 0};
+    py::gil_scoped_release nogil;
+    st = msx_csr_plan_create_bound(msx::to_vtype(vd.dtype), msx::to_itype(v.dtype), n_rows, n_cols,
+                                   nnz, vd.ptr, vi.ptr, v.ptr, &opts, stream, &plan->p);
   }
   msx::check_status(st, "csr_plan");
   return plan;
@@ -201,6 +221,9 @@ py::dict plan_info(const Plan &plan) {
   d["n_chunks"] = info.n_chunks;
   d["device"] = info.device;
   d["plan_bytes"] = info.plan_bytes;
+  d["n_slices"] = info.n_slices;
+  d["slice_width"] = info.slice_width;
+  d["slice_bytes"] = info.slice_bytes;
   return d;
 }
 
@@ -253,7 +276,10 @@ PYBIND11_MODULE(_ext, m) {
   m.def("_compiled_capabilities", &compiled_capabilities,
         "Return compile-time native backend facts for capability reporting.");
   m.def("csr_plan", &make_plan, py::arg("indptr"), py::arg("n_rows"), py::arg("nnz"),
-        py::arg("block_nnz") = 0, "Build a row-block plan from a GPU indptr.");
+        py::arg("block_nnz") = 0, py::arg("data") = py::none(), py::arg("indices") = py::none(),
+        py::arg("n_cols") = -1, py::arg("slice_mode") = 0,
+        "Build a row-block plan from a GPU indptr; with data/indices, a plan bound to the "
+        "matrix (slice_mode 0 auto, 1 off, 2 on: column slices per XCD).");
   m.def("csr_matvec", &csr_matvec, py::arg("data"), py::arg("indices"), py::arg("indptr"),
         py::arg("x"), py::arg("n_rows"), py::arg("n_cols"), py::arg("plan") = py::none(),
         py::arg("n_threads") = 0, "Multiply CSR buffers by a dense vector.");

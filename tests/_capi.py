@@ -21,7 +21,15 @@ OK, EINVAL, ETYPE, EHIP, ENOMEM = range(5)
 class PlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in (
         "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_bounds", "n_long_rows",
-        "n_chunks", "device", "plan_bytes")]
+        "n_chunks", "device", "plan_bytes", "n_slices", "slice_width", "slice_bytes")]
+
+
+class PlanOptions(ctypes.Structure):
+    _fields_ = [("block_nnz", ctypes.c_int64), ("slice_mode", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+SLICE_AUTO, SLICE_OFF, SLICE_ON = 0, 1, 2
 
 
 def declared_functions() -> list[str]:
@@ -41,6 +49,8 @@ def lib() -> ctypes.CDLL:
         L.msx_last_error.restype = ctypes.c_char_p
         L.msx_device_count.argtypes = [ctypes.POINTER(ci)]
         L.msx_csr_plan_create.argtypes = [ci, i64, i64, vp, i64, vp, ctypes.POINTER(vp)]
+        L.msx_csr_plan_create_bound.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp,
+                                                ctypes.POINTER(PlanOptions), vp, ctypes.POINTER(vp)]
         L.msx_csr_plan_destroy.argtypes = [vp]
         L.msx_csr_plan_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
         L.msx_csr_plan_export.argtypes = [vp, vp, vp, vp]
@@ -50,7 +60,8 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_spmm_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp, ci]
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
-        for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_destroy",
+        for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
+                     "msx_csr_plan_destroy",
                      "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_spmv", "msx_csr_spmm",
                      "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges"):
             getattr(L, name).restype = ci
@@ -71,10 +82,18 @@ def _stream():
 
 
 class Plan:
-    def __init__(self, indptr: torch.Tensor, n_rows: int, nnz: int, block_nnz: int = 0):
+    def __init__(self, indptr: torch.Tensor, n_rows: int, nnz: int, block_nnz: int = 0, *,
+                 data=None, indices=None, n_cols: int = 0, slice_mode: int | None = None):
         self.ptr = ctypes.c_void_p()
-        st = lib().msx_csr_plan_create(IT[indptr.dtype], n_rows, nnz, _p(indptr), block_nnz,
-                                       _stream(), ctypes.byref(self.ptr))
+        if data is None:
+            st = lib().msx_csr_plan_create(IT[indptr.dtype], n_rows, nnz, _p(indptr), block_nnz,
+                                           _stream(), ctypes.byref(self.ptr))
+        else:
+            opts = PlanOptions(block_nnz, SLICE_AUTO if slice_mode is None else slice_mode, 0)
+            self._keep = (data, indices, indptr)
+            st = lib().msx_csr_plan_create_bound(VT[data.dtype], IT[indptr.dtype], n_rows, n_cols,
+                                                 nnz, _p(data), _p(indices), _p(indptr),
+                                                 ctypes.byref(opts), _stream(), ctypes.byref(self.ptr))
         if st != OK:
             raise RuntimeError(f"plan_create: {st} {last_error()}")
 

@@ -285,3 +285,84 @@ def test_configs_full_size(name):
                             what=f"{name}/full")
     if name == "random16":
         np.testing.assert_array_equal(out["plan"], want)
+        # the benchmark path: bound plan with XCD column slices
+        d, i, p = _upload(m.data, m.indices, m.indptr, "float32")
+        plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1])
+        assert plan.info().n_slices == 8
+        y = _capi.spmv(d, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
+        torch.cuda.synchronize()
+        assert_rows_close(to_numpy(y), want,
+                          orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]), "float32",
+                          "random16 sliced")
+
+
+# -- XCD column slicing (bound plans) ------------------------------------------------
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_sliced_plan_parity(vtype, index_dtype):
+    rng = np.random.default_rng(31)
+    n_rows, n_cols = 6000, 50000
+    lengths = rng.integers(0, 40, n_rows)
+    lengths[rng.random(n_rows) < 0.1] = 0
+    lengths[[17, 2000, 5999]] = [3000, 9000, 700]  # long rows keep the unsliced path
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, index_dtype)
+    indices[::997] = n_cols + 5  # out-of-range columns add nothing
+    data, x = _values(rng, nnz, vtype), _values(rng, n_cols, vtype)
+    want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+    scale = orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype)
+    d, i, p = _upload(data, indices, indptr, vtype)
+    for W in (256, 512):
+        plan = _capi.Plan(p, n_rows, nnz, W, data=d, indices=i, n_cols=n_cols,
+                          slice_mode=_capi.SLICE_ON)
+        info = plan.info()
+        assert info.n_slices == 8 and info.slice_width * 8 >= n_cols
+        for _ in range(2):  # partial sums are rewritten each call
+            y = _capi.spmv(d, i, p, to_torch(x, vtype, DEV), n_rows, n_cols, plan=plan)
+            torch.cuda.synchronize()
+            assert_rows_close(to_numpy(y), want, scale, vtype, f"sliced {vtype} W={W}")
+        plan.close()
+
+
+def test_sliced_auto_selection_and_binding():
+    from mlx_sparse import synthetic as s
+
+    m = s.random_fixed_row(1 << 21, 16, seed=4)  # x = 8.4 MB, columns scattered
+    d, i, p = _upload(m.data, m.indices, m.indptr, "float32")
+    plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1])
+    assert plan.info().n_slices == 8
+    x = s.uniform(m.shape[1], -1, 1, 5)
+    y = _capi.spmv(d, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
+    torch.cuda.synchronize()
+    want = orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=8)
+    assert_rows_close(to_numpy(y), want, orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]),
+                      "float32", "sliced auto")
+    # a bound plan refuses other buffers
+    d2 = d.clone()
+    with pytest.raises(RuntimeError, match="bound to other"):
+        _capi.spmv(d2, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
+    plan.close()
+    # a stencil with the same x size stays unsliced (its gathers are local)
+    g = s.laplacian_2d(1 << 11)
+    d, i, p = _upload(g.data, g.indices, g.indptr, "float32")
+    plan = _capi.Plan(p, g.shape[0], g.nnz, data=d, indices=i, n_cols=g.shape[1])
+    assert plan.info().n_slices == 0
+    plan.close()
+
+
+def test_sliced_through_api(gpu):
+    from mlx_sparse import synthetic as s
+
+    ms = gpu
+    m = s.random_fixed_row(1 << 21, 16, seed=6)
+    A = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
+    assert A.plan().info()["n_slices"] == 8
+    x = s.uniform(m.shape[1], -1, 1, 7)
+    y = (A @ torch.from_numpy(x).to(DEV)).cpu().numpy()
+    want = orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=8)
+    assert_rows_close(y, want, orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]), "float32",
+                      "sliced api")
+    with ms.runtime.context(gpu_slice="off"):
+        B = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
+        assert B.plan().info()["n_slices"] == 0
+        np.testing.assert_array_equal((B @ torch.from_numpy(x).to(DEV)).cpu().numpy(), want)
