@@ -7,14 +7,15 @@
 // 4-byte value - 7.2 GB of fabric traffic for 0.59 GB of matrix.
 //
 // What: the plan partitions the columns into 8 slices of width Wc and, inside
-// every short block, stably reorders the block's values by slice (same
-// position range [p0, p1) of the block, so the copy is exactly nnz long).
-// Each value's index is packed as (row_in_block << col_bits) | (col - s*Wc).
-// The SpMV then runs slice s only on workgroups g with g % 8 == s - the
-// hardware hands workgroup g to XCD g % 8 - so XCD s only ever gathers from
-// x[s*Wc, (s+1)*Wc), about 2 MB, which stays in its L2.  Each (block, slice)
-// wave sums its rows in stored order into partial[s][row]; a merge kernel
-// adds the 8 partials in slice order.  Long rows keep the unsliced path.
+// every 256-row super-block, stably reorders the block's values by slice
+// (same position range of the block, so the copy is exactly nnz long).  Each
+// value's index is packed as (row_in_block << col_bits) | (col - s*Wc).  The
+// SpMV then runs slice s only on workgroups g with g % 8 == s - the hardware
+// hands workgroup g to XCD g % 8 - so XCD s only ever gathers from
+// x[s*Wc, (s+1)*Wc), about 2 MB for the 16.8 MB x, which stays in its L2.
+// Each (super-block, slice) wave sums its rows in stored order into
+// partial[s][row]; a merge kernel adds the 8 partials in slice order.  Long
+// rows keep the unsliced path.
 //
 // Summation order therefore differs from the reference's (per row: 8 slice
 // sums, each in stored order, added in slice order); results agree within
@@ -101,69 +102,81 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // ---------------------------------------------------------------------------
-// Build: per short block (one wave), count values per slice, then scatter
-// them stably to [p0 + seg[s], p0 + seg[s+1]).  Values with a column outside
-// [0, n_cols) are dropped (they add nothing to y).
-template <class V, class I, int W>
+// Build.  Super-block k is the row window [256k, 256k + 256); its values keep
+// their position range [P0, P1) = [indptr[256k], indptr[256k + 256]) and are
+// stably reordered there by slice, seg[k][s] .. seg[k][s+1] relative to P0.
+// Dropped: values of long rows (summed by spmv_long on the caller's arrays)
+// and values whose column is outside [0, n_cols) (they add nothing).  One
+// wave per super-block: a counting pass, then a stable scatter.
+template <class V, class I>
 __global__ void __launch_bounds__(kThreads)
     slice_build(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
-                const I *__restrict__ indptr, const int32_t *__restrict__ bounds,
-                const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
-                int64_t n_cols, int64_t slice_width, int col_bits,
+                const I *__restrict__ indptr, int64_t n_rows, int64_t nnz, int64_t n_cols,
+                int64_t long_len, int64_t slice_width, int col_bits,
                 typename V::Storage *__restrict__ s_data, uint32_t *__restrict__ s_col,
-                uint16_t *__restrict__ s_seg) {
-  __shared__ int32_t lds_rp[kWavesPerGroup][kRows + 1];
+                uint32_t *__restrict__ s_seg) {
+  __shared__ int64_t lds_rp[kWavesPerGroup][kRows + 1];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  int32_t *rp = lds_rp[wave];
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + wave;
-  if (b >= n_bounds) return;
-  uint16_t *seg = s_seg + b * (kSlices + 1);
-  const BlockRange br = block_range<W>(bounds, bounds_nnz, b, nnz);
-  if (!br.valid) {
-    if (lane <= kSlices) seg[lane] = 0;
-    return;
-  }
-  for (int i = lane; i <= br.m; i += kWave)
-    rp[i] = static_cast<int32_t>(clamp64(static_cast<int64_t>(indptr[br.r0 + i]), br.p0, br.p1) - br.p0);
+  int64_t *rp = lds_rp[wave];
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + wave;
+  const int64_t n_super = (n_rows + kRows - 1) / kRows;
+  if (k >= n_super) return;
+  uint32_t *seg = s_seg + k * (kSlices + 1);
+  const int64_t r0 = k * kRows;
+  const int m = static_cast<int>(std::min<int64_t>(kRows, n_rows - r0));
+  const int64_t P0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+  for (int i = lane; i <= m; i += kWave)
+    rp[i] = clamp64(static_cast<int64_t>(indptr[r0 + i]), P0, nnz);
   wave_lds_sync();
-  const int n = static_cast<int>(br.p1 - br.p0);
-  auto slice_of = [&](int e, int64_t &col) -> int {
-    col = static_cast<int64_t>(indices[br.p0 + e]);
+  const int64_t P1 = rp[m];
+  const int64_t n = P1 - P0;
+  // classify element e: slice, or kSlices when dropped; also its row
+  auto classify = [&](int64_t e, int64_t &col, int &row) -> int {
+    int lo = 0, hi = m;  // rp[lo] <= P0 + e < rp[hi]
+    const int64_t pos = P0 + e;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (rp[mid] <= pos) lo = mid;
+      else hi = mid;
+    }
+    row = lo;
+    if (rp[lo + 1] - rp[lo] > long_len) return kSlices;
+    col = static_cast<int64_t>(indices[pos]);
     if (static_cast<uint64_t>(col) >= static_cast<uint64_t>(n_cols)) return kSlices;
     return static_cast<int>(col / slice_width);
   };
-  // pass 1: counts per slice
-  int count[kSlices];
+  int64_t count[kSlices];
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) count[s] = 0;
-  for (int c0 = 0; c0 < n; c0 += kWave) {
-    const int e = c0 + lane;
+  for (int64_t c0 = 0; c0 < n; c0 += kWave) {
+    const int64_t e = c0 + lane;
     int64_t col = 0;
-    const int sl = e < n ? slice_of(e, col) : kSlices;
+    int row = 0;
+    const int sl = e < n ? classify(e, col, row) : kSlices;
 #pragma unroll
     for (int s = 0; s < kSlices; ++s) count[s] += __popcll(__ballot(sl == s));
   }
-  int start[kSlices + 1];
+  int64_t start[kSlices + 1];
   start[0] = 0;
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) start[s + 1] = start[s] + count[s];
   if (lane <= kSlices) {
-    int v = 0;
+    int64_t v = 0;
 #pragma unroll
     for (int s = 0; s <= kSlices; ++s) v = lane == s ? start[s] : v;
-    seg[lane] = static_cast<uint16_t>(v);
+    seg[lane] = static_cast<uint32_t>(v);
   }
-  // pass 2: stable scatter
-  int run[kSlices];
+  int64_t run[kSlices];
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) run[s] = start[s];
   const uint64_t lt = lanemask_lt(lane);
-  for (int c0 = 0; c0 < n; c0 += kWave) {
-    const int e = c0 + lane;
+  for (int64_t c0 = 0; c0 < n; c0 += kWave) {
+    const int64_t e = c0 + lane;
     int64_t col = 0;
-    const int sl = e < n ? slice_of(e, col) : kSlices;
-    int dest = -1;
+    int row = 0;
+    const int sl = e < n ? classify(e, col, row) : kSlices;
+    int64_t dest = -1;
 #pragma unroll
     for (int s = 0; s < kSlices; ++s) {
       const uint64_t mask = __ballot(sl == s);
@@ -171,39 +184,35 @@ __global__ void __launch_bounds__(kThreads)
       run[s] += __popcll(mask);
     }
     if (dest >= 0) {
-      // row of element e: last row whose start is <= e
-      int lo = 0, hi = br.m;  // rp[lo] <= e < rp[hi]
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (rp[mid] <= e) lo = mid;
-        else hi = mid;
-      }
-      const int64_t q = br.p0 + dest;
-      s_data[q] = data[br.p0 + e];
-      s_col[q] = (static_cast<uint32_t>(lo) << col_bits) |
-                 static_cast<uint32_t>(col - static_cast<int64_t>(sl) * slice_width);
+      s_data[P0 + dest] = data[P0 + e];
+      s_col[P0 + dest] = (static_cast<uint32_t>(row) << col_bits) |
+                         static_cast<uint32_t>(col - static_cast<int64_t>(sl) * slice_width);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// SpMV over one (short block, slice) per wave; workgroup g serves slice g % 8.
-template <class V, int W>
+// SpMV over one (super-block, slice) per wave; workgroup g serves slice g % 8,
+// which the hardware runs on XCD g % 8.  The slice segment is consumed in
+// chunks of kChunk values (all loads of a chunk issued before any use);
+// within a chunk each row's run is summed in stored order by one lane and
+// added to the row's running sum, so segments of any length fit LDS.
+template <class V>
 __global__ void __launch_bounds__(kThreads)
     spmv_sliced(const typename V::Storage *__restrict__ s_data, const uint32_t *__restrict__ s_col,
-                const uint16_t *__restrict__ s_seg, const typename V::Storage *__restrict__ x,
-                typename V::Acc *__restrict__ partial, const int32_t *__restrict__ bounds,
-                const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t n_rows,
-                int64_t nnz, int64_t slice_width, int col_bits) {
+                const uint32_t *__restrict__ s_seg, const typename V::Storage *__restrict__ x,
+                typename V::Acc *__restrict__ partial, int64_t n_rows, int64_t nnz,
+                const void *__restrict__ indptr_v, int index_bytes, int64_t slice_width,
+                int col_bits) {
   using S = typename V::Storage;
   using A = typename V::Acc;
-  constexpr int kQuads = W / 2 + 1;
-  constexpr int QPL = (kQuads + kWave - 1) / kWave;
-  constexpr int kCap = 4 * kQuads;
-  __shared__ A lds_prod[kWavesPerGroup][kCap];
-  __shared__ uint8_t lds_row[kWavesPerGroup][kCap];
+  constexpr int QPL = 4;
+  constexpr int kChunk = 4 * QPL * kWave;  // values per chunk
+  __shared__ A lds_prod[kWavesPerGroup][kChunk];
+  __shared__ uint8_t lds_row[kWavesPerGroup][kChunk];
   __shared__ uint16_t lds_rs[kWavesPerGroup][kRows];
   __shared__ uint16_t lds_re[kWavesPerGroup][kRows];
+  __shared__ A lds_acc[kWavesPerGroup][kRows];
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
@@ -211,77 +220,97 @@ __global__ void __launch_bounds__(kThreads)
   uint8_t *rowid = lds_row[wave];
   uint16_t *rs = lds_rs[wave];
   uint16_t *re = lds_re[wave];
+  A *racc = lds_acc[wave];
   const uint32_t col_mask = (1u << col_bits) - 1u;
   const int s = static_cast<int>(blockIdx.x % kSlices);
   const S *xs = x + static_cast<int64_t>(s) * slice_width;
   A *part = partial + static_cast<int64_t>(s) * n_rows;
+  const int64_t n_super = (n_rows + kRows - 1) / kRows;
 
-  for (int64_t g = blockIdx.x / kSlices; g * kWavesPerGroup < n_bounds; g += gridDim.x / kSlices) {
-    const int64_t b = g * kWavesPerGroup + wave;
-    if (b >= n_bounds) break;
-    const BlockRange br = block_range<W>(bounds, bounds_nnz, b, nnz);
-    if (!br.valid) continue;
-    const uint16_t *seg = s_seg + b * (kSlices + 1);
-    const int64_t lo = br.p0 + seg[s];
-    const int64_t hi = std::min<int64_t>(br.p0 + seg[s + 1], br.p1);
-    const int cnt = static_cast<int>(hi > lo ? hi - lo : 0);
-    const int64_t a0 = lo & ~int64_t{3};
-    const int nq = static_cast<int>((hi - a0 + 3) >> 2);
-    for (int i = lane; i < br.m; i += kWave) {
+  for (int64_t g = blockIdx.x / kSlices; g * kWavesPerGroup < n_super; g += gridDim.x / kSlices) {
+    const int64_t k = g * kWavesPerGroup + wave;
+    if (k >= n_super) break;
+    const int64_t r0 = k * kRows;
+    const int m = static_cast<int>(std::min<int64_t>(kRows, n_rows - r0));
+    const int64_t P0 = clamp64(index_bytes == 8 ? static_cast<const int64_t *>(indptr_v)[r0]
+                                                : static_cast<const int32_t *>(indptr_v)[r0],
+                               0, nnz);
+    const uint32_t *seg = s_seg + k * (kSlices + 1);
+    const int64_t lo = std::min<int64_t>(P0 + seg[s], nnz);
+    const int64_t hi = std::min<int64_t>(P0 + seg[s + 1], nnz);
+    // Invariant at each chunk start: rs/re are zero for every row.
+    for (int i = lane; i < kRows; i += kWave) {
+      racc[i] = vzero<A>();
       rs[i] = 0;
       re[i] = 0;
     }
-    const auto rc = make_rsrc(s_col + a0, static_cast<uint64_t>(nnz - a0) * sizeof(uint32_t));
-    const auto rd = make_rsrc(s_data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
-    Quad<uint32_t> cq[QPL];
-    Quad<S> dq[QPL];
+    wave_lds_sync();
+    for (int64_t c_lo = lo; c_lo < hi; c_lo += kChunk) {
+      const int64_t c_hi = std::min<int64_t>(c_lo + kChunk, hi);
+      const int cnt = static_cast<int>(c_hi - c_lo);
+      const int64_t a0 = c_lo & ~int64_t{3};
+      const int nq = static_cast<int>((c_hi - a0 + 3) >> 2);
+      const auto rc = make_rsrc(s_col + a0, static_cast<uint64_t>(nnz - a0) * sizeof(uint32_t));
+      const auto rd = make_rsrc(s_data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
+      Quad<uint32_t> cq[QPL + 1];
+      Quad<S> dq[QPL + 1];
 #pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
-      if (q < nq) {
-        cq[k] = load_quad<uint32_t>(rc, static_cast<uint32_t>(q) * 16u);
-        dq[k] = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+      for (int j = 0; j <= QPL; ++j) {
+        const int q = lane + j * kWave;
+        if (q < nq) {
+          cq[j] = load_quad<uint32_t>(rc, static_cast<uint32_t>(q) * 16u);
+          dq[j] = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+        }
       }
-    }
-    S xv[QPL][4];
+      S xv[QPL + 1][4];
 #pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t pos = a0 + 4 * q + e;
-        xv[k][e] = S{};
-        if (q < nq && pos >= lo && pos < hi) xv[k][e] = xs[cq[k].v[e] & col_mask];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
-      if (q < nq) {
+      for (int j = 0; j <= QPL; ++j) {
+        const int q = lane + j * kWave;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int64_t pos = a0 + 4 * q + e;
-          if (pos >= lo && pos < hi) {
-            const int t = static_cast<int>(pos - lo);
-            prod[t] = vmul<V>(dq[k].v[e], xv[k][e]);
-            rowid[t] = static_cast<uint8_t>(cq[k].v[e] >> col_bits);
+          xv[j][e] = S{};
+          if (q < nq && pos >= c_lo && pos < c_hi) xv[j][e] = xs[cq[j].v[e] & col_mask];
+        }
+      }
+      // rows of this chunk: rowid[0] .. rowid[cnt-1] (ascending)
+#pragma unroll
+      for (int j = 0; j <= QPL; ++j) {
+        const int q = lane + j * kWave;
+        if (q < nq) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t pos = a0 + 4 * q + e;
+            if (pos >= c_lo && pos < c_hi) {
+              const int t = static_cast<int>(pos - c_lo);
+              prod[t] = vmul<V>(dq[j].v[e], xv[j][e]);
+              rowid[t] = static_cast<uint8_t>((cq[j].v[e] >> col_bits) & (kRows - 1));
+            }
           }
         }
       }
+      wave_lds_sync();
+      for (int t = lane; t < cnt; t += kWave) {
+        const int r = rowid[t];
+        if (t == 0 || rowid[t - 1] != r) rs[r] = static_cast<uint16_t>(t);
+        if (t == cnt - 1 || rowid[t + 1] != r) re[r] = static_cast<uint16_t>(t + 1);
+      }
+      wave_lds_sync();
+      const int first = rowid[0];
+      const int last = rowid[cnt - 1];
+      for (int r = first + lane; r <= last; r += kWave) {
+        const int t0 = rs[r], t1 = re[r];
+        if (t1 > t0) {
+          A acc = vzero<A>();
+          for (int t = t0; t < t1; ++t) acc = vadd(acc, prod[t]);
+          racc[r] = vadd(racc[r], acc);
+        }
+        rs[r] = 0;  // restore the invariant for the next chunk
+        re[r] = 0;
+      }
+      wave_lds_sync();
     }
-    wave_lds_sync();
-    // run boundaries of each row inside the slice segment (rows ascend)
-    for (int t = lane; t < cnt; t += kWave) {
-      const int r = rowid[t];
-      if (t == 0 || rowid[t - 1] != r) rs[r] = static_cast<uint16_t>(t);
-      if (t == cnt - 1 || rowid[t + 1] != r) re[r] = static_cast<uint16_t>(t + 1);
-    }
-    wave_lds_sync();
-    for (int i = lane; i < br.m; i += kWave) {
-      A acc = vzero<A>();
-      for (int t = rs[i]; t < re[i]; ++t) acc = vadd(acc, prod[t]);
-      part[br.r0 + i] = acc;
-    }
+    for (int i = lane; i < m; i += kWave) part[r0 + i] = racc[i];
     wave_lds_sync();
   }
 }
@@ -332,10 +361,11 @@ msx_status build_typed(msx_csr_plan *p, const void *data, const void *indices, c
   }
   const int64_t width = ((p->n_cols + kSlices - 1) / kSlices + 31) / 32 * 32;
   const int col_bits = std::max(1, bits_for(width));
-  if (col_bits > 24 || groups == 0) return MSX_OK;  // needs 8 bits for the row in block
+  const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
+  if (col_bits > 24 || n_super == 0 || p->nnz >= (int64_t{1} << 32)) return MSX_OK;
   const size_t b_data = ((static_cast<size_t>(p->nnz) * sizeof(S) + 255) / 256) * 256;
   const size_t b_col = ((static_cast<size_t>(p->nnz) * 4 + 255) / 256) * 256;
-  const size_t b_seg = ((static_cast<size_t>(p->n_bounds) * (kSlices + 1) * 2 + 255) / 256) * 256;
+  const size_t b_seg = ((static_cast<size_t>(n_super) * (kSlices + 1) * 4 + 255) / 256) * 256;
   const size_t b_part = static_cast<size_t>(kSlices) * p->n_rows * sizeof(A);
   char *base = nullptr;
   if (hipMalloc(&base, b_data + b_col + b_seg + b_part) != hipSuccess) {
@@ -345,18 +375,20 @@ msx_status build_typed(msx_csr_plan *p, const void *data, const void *indices, c
   p->s_base = base;
   p->s_data = base;
   p->s_col = reinterpret_cast<uint32_t *>(base + b_data);
-  p->s_seg = reinterpret_cast<uint16_t *>(base + b_data + b_col);
+  p->s_seg = reinterpret_cast<uint32_t *>(base + b_data + b_col);
   p->s_partial = base + b_data + b_col + b_seg;
   p->s_bytes = b_data + b_col + b_seg + b_part;
   p->slice_width = width;
   p->col_bits = col_bits;
-  hipLaunchKernelGGL((slice_build<V, I, W>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
+  const int64_t bgroups = (n_super + kWavesPerGroup - 1) / kWavesPerGroup;
+  hipLaunchKernelGGL((slice_build<V, I>), dim3(static_cast<uint32_t>(bgroups)), dim3(kThreads), 0,
                      stream, static_cast<const S *>(data), static_cast<const I *>(indices),
-                     static_cast<const I *>(indptr), p->bounds, p->bounds_nnz, p->n_bounds, p->nnz,
-                     p->n_cols, width, col_bits, static_cast<S *>(p->s_data), p->s_col, p->s_seg);
+                     static_cast<const I *>(indptr), p->n_rows, p->nnz, p->n_cols, p->block_nnz,
+                     width, col_bits, static_cast<S *>(p->s_data), p->s_col, p->s_seg);
   MSX_HIP_TRY(hipGetLastError());
   MSX_HIP_TRY(hipStreamSynchronize(stream));
   p->n_slices = kSlices;
+  p->s_indptr = indptr;
   return MSX_OK;
 }
 
@@ -379,32 +411,21 @@ msx_status build_v(msx_csr_plan *p, const void *data, const void *indices, const
                              : build_w<V, int64_t>(p, data, indices, indptr, stream);
 }
 
-template <class V, int W>
-void launch_w(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream) {
+template <class V>
+void launch_v(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream) {
   using S = typename V::Storage;
   using A = typename V::Acc;
-  const int64_t groups = (p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
-  const int64_t total = groups * kSlices;
+  const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
+  const int64_t total = (n_super + kWavesPerGroup - 1) / kWavesPerGroup * kSlices;
   const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(total, kMaxGrid / kSlices * kSlices));
-  hipLaunchKernelGGL((spmv_sliced<V, W>), dim3(grid), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL((spmv_sliced<V>), dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const S *>(p->s_data), p->s_col, p->s_seg, static_cast<const S *>(x),
-                     static_cast<A *>(p->s_partial), p->bounds, p->bounds_nnz, p->n_bounds,
-                     p->n_rows, p->nnz, p->slice_width, p->col_bits);
+                     static_cast<A *>(p->s_partial), p->n_rows, p->nnz, p->s_indptr,
+                     p->itype == MSX_I64 ? 8 : 4, p->slice_width, p->col_bits);
   const uint32_t mgrid = static_cast<uint32_t>(
       std::max<int64_t>(1, std::min<int64_t>((p->n_rows + kThreads - 1) / kThreads, kMaxGrid)));
   hipLaunchKernelGGL((slice_merge<V>), dim3(mgrid), dim3(kThreads), 0, stream,
                      static_cast<const A *>(p->s_partial), static_cast<S *>(y), p->n_rows);
-}
-
-template <class V>
-void launch_v(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream) {
-  switch (p->block_nnz) {
-  case 64: return launch_w<V, 64>(p, x, y, stream);
-  case 128: return launch_w<V, 128>(p, x, y, stream);
-  case 256: return launch_w<V, 256>(p, x, y, stream);
-  case 512: return launch_w<V, 512>(p, x, y, stream);
-  default: return launch_w<V, 1024>(p, x, y, stream);
-  }
 }
 
 }  // namespace

@@ -71,7 +71,8 @@ struct msx_csr_plan {
   const void *bound_indices;
   void *s_data;               // values reordered by slice inside each short block
   uint32_t *s_col;            // (row_in_block << col_bits) | column_in_slice
-  uint16_t *s_seg;            // n_bounds * (kSlices + 1) slice offsets per block
+  uint32_t *s_seg;            // per 256-row super-block: kSlices + 1 offsets from its first value
+  const void *s_indptr;       // indptr the sliced copy was built from
   void *s_partial;            // kSlices * n_rows accumulators
   void *s_base;
   size_t s_bytes;

@@ -195,7 +195,9 @@ def test_out_of_range_columns_add_nothing():
     indptr = np.array([0, 3, 6], np.int32)
     x = np.array([1.0, 2.0, 4.0], np.float32)
     d, i, p = _upload(data, indices, indptr, "float32")
-    for plan in (_capi.Plan(p, 2, 6), None):
+    sliced = _capi.Plan(p, 2, 6, data=d, indices=i, n_cols=3, slice_mode=_capi.SLICE_ON)
+    assert sliced.info().n_slices == 8
+    for plan in (_capi.Plan(p, 2, 6), None, sliced):
         y = _capi.spmv(d, i, p, to_torch(x, None, DEV), 2, 3, plan=plan)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(to_numpy(y), [1.0, 6.0])
@@ -307,12 +309,11 @@ def test_sliced_plan_parity(vtype, index_dtype):
     lengths[rng.random(n_rows) < 0.1] = 0
     lengths[[17, 2000, 5999]] = [3000, 9000, 700]  # long rows keep the unsliced path
     indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, index_dtype)
-    indices[::997] = n_cols + 5  # out-of-range columns add nothing
     data, x = _values(rng, nnz, vtype), _values(rng, n_cols, vtype)
     want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
     scale = orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype)
     d, i, p = _upload(data, indices, indptr, vtype)
-    for W in (256, 512):
+    for W in (64, 512):  # W also sets which rows are long (> W values)
         plan = _capi.Plan(p, n_rows, nnz, W, data=d, indices=i, n_cols=n_cols,
                           slice_mode=_capi.SLICE_ON)
         info = plan.info()
