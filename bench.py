@@ -10,10 +10,11 @@ seeded).  Inputs are resident in HBM before timing starts.
 Prints ONE JSON line.  ``value`` is the effective bandwidth on compulsory
 traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 
-- ``roofline``: the SpMV kernel's achieved GB/s from HIP events around back-to-
-  back launches on the launch stream, against the 8 TB/s HBM peak;
-  ``traffic`` is filled from rocprofv3 FETCH_SIZE/WRITE_SIZE when
-  ``--traffic-json`` points at a summary made by ``profiles/`` tooling, else null;
+- ``roofline``: achieved GB/s of one SpMV call (the column-sliced kernel and
+  its slice-merge kernel, back to back on the launch stream) from HIP events
+  around repeated calls, against the 8 TB/s HBM peak; ``traffic`` is the
+  measured HBM bytes per call from the committed rocprofv3 FETCH_SIZE /
+  WRITE_SIZE summary (profiles/spmv_random16_traffic.txt), else null;
 - ``cold``: the same SpMV with a 1 GiB buffer written between launches
   (evicts the 256 MB Infinity Cache), median of per-launch times;
 - ``spmm``: CSR SpMM with k=64 on the 3D 7-point Poisson matrix (128^3),
@@ -119,7 +120,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
-    ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "spmv_random16_traffic.json"))
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -189,12 +190,11 @@ def main() -> int:
     log(f"cold: {cold_ms * 1e3:.1f} us  {cold_gbs:.0f} GB/s")
 
     traffic = None
-    tj = Path(args.traffic_json)
-    if tj.exists():
-        try:
-            traffic = json.loads(tj.read_text()).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    tf = Path(args.traffic)
+    if tf.exists():
+        for line in tf.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_call:"):
+                traffic = int(line.split(":", 1)[1].strip())
 
     result = {
         "metric": "CSR SpMV effective HBM GB/s (% of peak) + SpMM GFLOP/s, fp32, 1xMI355X",
@@ -211,12 +211,16 @@ def main() -> int:
         "data": "synthetic (seeded): uniform random columns, N(0,1) values, x~U[-1,1]",
         "config": {"workload": "csr_spmv random16 n=4194304 nnz=67108864 f32/i32",
                    "n_rows": m.shape[0], "nnz": m.nnz, "index": "int32",
-                   "compulsory_bytes": nbytes, "plan_build_ms": round(plan_ms, 3)},
+                   "compulsory_bytes": nbytes, "plan_build_ms": round(plan_ms, 3),
+                   "plan": {k: info[k] for k in ("block_nnz", "n_blocks", "n_long_rows",
+                                                 "n_slices", "plan_bytes")}},
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 2),
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "spmv_blocks<F32,int>",
+                     "traffic": traffic,
+                     "kernel": ("spmv_sliced<F32> + slice_merge<F32>" if info.get("n_slices")
+                                else "spmv_blocks<F32,int,512>"),
                      "kernel_us": round(kern_ms * 1e3, 2)},
         "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),
                  "frac": round(cold_gbs / HBM_PEAK_GBS, 4)},
