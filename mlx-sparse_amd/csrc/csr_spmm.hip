@@ -13,9 +13,8 @@
 // column tile of 64 * CW columns instead of once per column.  Each column is
 // summed from zero in stored order - the reference's CPU order
 // (src/sparse/csr_matmul/csr_matmul.cpp:83-133) - so float32 results match
-// its CPU kernel bit for bit.  The value loop issues eight X loads (the
-// tail of a row predicated) before the first use, so a short row costs one
-// round trip of X latency.
+// its CPU kernel bit for bit.  The value loop issues four X loads before
+// the first use to keep several gathers in flight per lane.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -28,7 +27,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kMaxGrid = 1u << 20;
-constexpr int kUnroll = 8;
+constexpr int kUnroll = 4;
 
 template <class S, int CW>
 struct Vec {
@@ -87,30 +86,36 @@ __global__ void __launch_bounds__(kThreads)
     for (int c = 0; c < CW; ++c) acc[c] = vzero<A>();
     const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
     const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
-    // Batches of kUnroll values, the tail predicated inside the batch, so a
-    // row of up to kUnroll values issues all of its X loads at once.
-    for (int64_t p = s; p < e; p += kUnroll) {
+    int64_t p = s;
+    for (; p + kUnroll <= e; p += kUnroll) {
       int64_t ci[kUnroll];
       A av[kUnroll];
       Vec<S, CW> xv[kUnroll];
-      bool ok[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        ok[u] = p + u < e;
-        ci[u] = ok[u] ? static_cast<int64_t>(indices[p + u]) : 0;
-        av[u] = ok[u] ? V::widen(data[p + u]) : vzero<A>();
-        ok[u] = ok[u] && static_cast<uint64_t>(ci[u]) < static_cast<uint64_t>(n_cols);
+        ci[u] = static_cast<int64_t>(indices[p + u]);
+        av[u] = V::widen(data[p + u]);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        if (ok[u]) xv[u] = load_vec<S, CW>(X + ci[u] * ldx + col);
+        if (static_cast<uint64_t>(ci[u]) < static_cast<uint64_t>(n_cols))
+          xv[u] = load_vec<S, CW>(X + ci[u] * ldx + col);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        if (ok[u]) {
+        if (static_cast<uint64_t>(ci[u]) < static_cast<uint64_t>(n_cols)) {
 #pragma unroll
           for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(av[u], xv[u].v[c]));
         }
+      }
+    }
+    for (; p < e; ++p) {
+      const int64_t cidx = static_cast<int64_t>(indices[p]);
+      if (static_cast<uint64_t>(cidx) < static_cast<uint64_t>(n_cols)) {
+        const A a = V::widen(data[p]);
+        const Vec<S, CW> xv = load_vec<S, CW>(X + cidx * ldx + col);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(a, xv.v[c]));
       }
     }
     Vec<S, CW> out;
