@@ -266,7 +266,7 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "kernel": ("spmv_sliced<F32> + slice_merge<F32>" if info.get("n_slices")
-                                else "spmv_blocks<F32,int,512>"),
+                                else f"spmv_blocks<F32,int,{info['block_nnz']}>"),
                      "kernel_us": round(kern_ms * 1e3, 2),
                      "timing": "HIP-graph replay of 20 calls x 10, HIP events"},
         "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),

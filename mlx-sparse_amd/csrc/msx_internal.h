@@ -31,7 +31,7 @@ bool valid_itype(int it);
 // Plan defaults.  W: window of the nnz range that a short block's row starts
 // fall in (block nnz < 2W); R: short blocks never cross a multiple of R rows;
 // C: chunk length of long rows.
-constexpr int64_t kDefaultBlockNnz = 512;
+constexpr int64_t kDefaultBlockNnz = 256;
 constexpr int64_t kBlockRows = 256;
 constexpr int64_t kChunkNnz = 4096;
 // Column slices of a sliced plan: one per XCD.

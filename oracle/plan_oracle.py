@@ -26,7 +26,7 @@ import numpy as np
 LONG_FLAG = 1 << 31
 
 
-def plan(indptr, W: int = 512, R: int = 256, C: int = 4096):
+def plan(indptr, W: int = 256, R: int = 256, C: int = 4096):
     """Returns (bounds incl. sentinel n, long_rows, long_chunk_begin incl.
     sentinel n_chunks) as int64 arrays."""
     p = np.asarray(indptr, dtype=np.int64)
@@ -51,7 +51,7 @@ def plan(indptr, W: int = 512, R: int = 256, C: int = 4096):
     return blocks, long_rows, chunk_begin
 
 
-def plan_loop(indptr, W: int = 512, R: int = 256, C: int = 4096):
+def plan_loop(indptr, W: int = 256, R: int = 256, C: int = 4096):
     """Same rule as ``plan`` with plain per-row loops (small inputs only)."""
     p = [int(v) for v in indptr]
     n = len(p) - 1

@@ -54,7 +54,7 @@ def _check(data, indices, indptr, X, n_rows, n_cols, vtype, what):
 
 
 @pytest.mark.parametrize("vtype", VTYPES)
-@pytest.mark.parametrize("k", [1, 2, 3, 7, 8, 16, 33, 64, 256, 300])
+@pytest.mark.parametrize("k", [1, 2, 3, 7, 8, 16, 32, 33, 64, 128, 256, 300])
 def test_widths(vtype, k):
     rng = np.random.default_rng(k)
     indices, indptr, nnz = _matrix(rng, 700, 500, 25, np.int32)
@@ -93,6 +93,41 @@ def test_padded_leading_dimensions_and_scalar_path():
     Y = _capi.spmm(d, i, p, X39[:, :32], 400, 300, ldx=39, ldy=32)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(Y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+def test_two_line_rows_padded_and_out_of_range(vtype):
+    """X rows of exactly two 128-byte lines take the line-tiled kernel: padded
+    leading dimensions, a row count that is not a multiple of the row groups,
+    and indices outside [0, n_cols), which contribute nothing."""
+    k = 256 // storage(np.zeros(1), vtype).itemsize
+    rng = np.random.default_rng(11)
+    n_rows, n_cols = 1001, 600
+    indices, indptr, nnz = _matrix(rng, n_rows, n_cols, 40, np.int32)
+    bad = rng.random(nnz) < 0.05
+    indices = indices.copy()
+    indices[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -3, n_cols + 7)
+    data = _values(rng, nnz, vtype)
+    Xfull = _values(rng, (n_cols, k + 8), vtype)
+    X = np.ascontiguousarray(Xfull[:, :k])
+    keep = ~bad
+    row_of = np.repeat(np.arange(n_rows), np.diff(indptr))
+    kept_ptr = np.concatenate([[0], np.cumsum(np.bincount(row_of[keep], minlength=n_rows))])
+    kept_ptr = kept_ptr.astype(np.int32)
+    want = orc.csr_matmul(data[keep], indices[keep], kept_ptr, X, n_rows, vtype=vtype)
+    d, i, p = (to_torch(a, vtype if a is data else None, DEV) for a in (data, indices, indptr))
+    Xt = to_torch(Xfull, vtype, DEV)
+    Yb = torch.zeros((n_rows, k + 8), dtype=Xt.dtype, device=DEV)
+    Yb[:, k:] = 5
+    _capi.spmm(d, i, p, Xt[:, :k], n_rows, n_cols, Y=Yb, ldx=k + 8, ldy=k + 8)
+    torch.cuda.synchronize()
+    assert torch.all(Yb[:, k:] == 5)  # padding untouched
+    got = to_numpy(Yb)
+    if vtype == "float32":
+        np.testing.assert_array_equal(got[:, :k], want)
+    else:
+        scale = orc.row_scale(data[keep], indices[keep], kept_ptr, X, n_rows, vtype=vtype)
+        assert_rows_close(np.ascontiguousarray(got[:, :k]), want, scale, vtype, vtype)
 
 
 def test_golden_widths_and_batched_api(gpu):
