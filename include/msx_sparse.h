@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 1
+#define MSX_ABI_VERSION 2
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -68,10 +68,12 @@ typedef struct msx_csr_plan msx_csr_plan;
 
 /* Column slicing of a bound plan (msx_csr_plan_create_bound). */
 typedef enum msx_slice_mode {
-  MSX_SLICE_AUTO = 0, /* slice when x exceeds 8 MB and most blocks' columns
-                         span over a quarter of the columns */
-  MSX_SLICE_OFF = 1,
-  MSX_SLICE_ON = 2
+  MSX_SLICE_AUTO = 0,  /* when x exceeds 8 MB and most blocks' columns span
+                          over a quarter of the columns: panels if the matrix
+                          qualifies, else XCD slices */
+  MSX_SLICE_OFF = 1,   /* row blocks only */
+  MSX_SLICE_ON = 2,    /* XCD column slices */
+  MSX_SLICE_PANELS = 3 /* LDS column panels (two-pass SpMV) */
 } msx_slice_mode;
 
 typedef struct msx_plan_options {
@@ -98,6 +100,11 @@ typedef struct msx_plan_info {
   int64_t n_slices;    /* 0, or 8 when the plan holds a column-sliced copy */
   int64_t slice_width; /* columns per slice */
   int64_t slice_bytes; /* device bytes of the sliced copy and its partial sums */
+  int64_t n_panels;    /* 0, or the number of LDS column panels */
+  int64_t panel_width; /* columns per panel */
+  int64_t n_tiles;     /* row tiles of a panel plan */
+  int64_t panel_values;/* values placed in the panel copy (short rows, valid columns) */
+  int64_t panel_bytes; /* device bytes of the panel copy and its product buffer */
 } msx_plan_info;
 
 /* ABI version of the loaded library (MSX_ABI_VERSION at build time). */
@@ -131,12 +138,23 @@ msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
 /*
  * Build a plan bound to one matrix's values (`data`, `indices`, `indptr`,
  * all device pointers) on `stream`: the row blocks of msx_csr_plan_create,
- * plus - when `opts->slice_mode` asks for it, or in AUTO mode when x is over
- * 8 MB and the columns are scattered - a copy of the short blocks' values
- * reordered into 8 column slices.  Sliced SpMV runs slice s on the
- * workgroups the hardware places on XCD s, so each XCD gathers from one
- * eighth of x, which stays in its L2; per-slice row sums are then added in
- * slice order.  `opts` may be NULL (defaults).  Synchronises `stream`.
+ * plus, for scattered gathers, one of two reordered copies of the short
+ * rows' values (`opts->slice_mode`; AUTO picks when x is over 8 MB and the
+ * columns are scattered):
+ *   XCD slices - the values of each 256-row block reordered into 8 column
+ *     slices; slice s runs on the workgroups the hardware places on XCD s,
+ *     so each XCD gathers from one eighth of x, which stays in its L2;
+ *     per-slice row sums are added in slice order.
+ *   panels - x cut into panels of 128 KB (32768 float32/float16/bfloat16
+ *     or 16384 complex64 entries) and the rows into tiles of at most 64 KB
+ *     of products plus one word per row.  Pass 1 holds one panel of x in LDS
+ *     and streams that panel's values, writing their products; pass 2 loads
+ *     one tile's products into LDS by stored position and sums each row in
+ *     stored order, so short rows equal the reference CPU kernel bit for bit.
+ *     Needs nnz < 2^31 and at most 2048 panels; MSX_SLICE_PANELS on a matrix
+ *     outside those limits fails with MSX_EINVAL, AUTO falls back to slices.
+ * Long rows keep the row-block path in every mode.  `opts` may be NULL
+ * (defaults).  Synchronises `stream`.
  *
  * A bound plan reads the matrix from its own copy: msx_csr_spmv must be
  * given the same data/indices/indptr pointers it was built from (other
@@ -172,6 +190,26 @@ msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info *info);
 msx_status msx_csr_plan_export(const msx_csr_plan *plan,
                                int64_t *bounds, int64_t *long_rows,
                                int64_t *long_chunk_begin);
+
+/*
+ * Copy a panel plan's layout to host memory (synchronous), for bit-exact
+ * checks.  Each pointer may be NULL to skip that array.
+ *   tile_begin, tile_end: n_tiles int64 - tile t holds rows
+ *                    [tile_begin[t], tile_end[t]), all short; a short row
+ *                    starts a tile at r = 0, after a long row, or when
+ *                    (indptr[r] + r) / H changes (indptr clamped to
+ *                    [0, nnz]), H = 16384 - W (float32, float16, bfloat16)
+ *                    or 8192 - W (complex64);
+ *   seg_begin:       n_panels * n_tiles + 1 int64 - start of segment
+ *                    (panel p, tile t) at index p * n_tiles + t of the
+ *                    panel copy, whose values are ordered by (panel, tile,
+ *                    stored position); the last entry is panel_values.
+ * MSX_EINVAL when the plan has no panels.  No reference counterpart: a
+ * layout check of this library's own plans.
+ */
+msx_status msx_csr_plan_export_panels(const msx_csr_plan *plan,
+                                      int64_t *tile_begin, int64_t *tile_end,
+                                      int64_t *seg_begin);
 
 /*
  * y[i] = sum_{p = indptr[i]}^{indptr[i+1]-1} data[p] * x[indices[p]]

@@ -1,0 +1,308 @@
+// csr_panel.hip - two-pass SpMV over the column-panel copy of a bound plan.
+//
+// Why: with columns scattered over a large x (the 4M-row random matrix: one
+// random 4-byte gather per value over 16.8 MB), a direct SpMV is bound by
+// the L2 request rate, not by HBM.  Holding x in LDS turns the gather into
+// an LDS read, but LDS holds only a 128 KB panel of x, so the values are
+// processed panel by panel and the row sums need a second pass:
+//
+//   pass 1  (panel_products) one workgroup per chunk of one panel's values:
+//           load the panel of x into LDS (widened to the accumulator type),
+//           stream the chunk's values and panel columns, write each product
+//           a * x[col] - rounded exactly as the reference rounds it before
+//           adding - to the product buffer in the copy's order.  Pure
+//           streaming: 1024 threads, four values per lane per load.
+//   pass 2  (panel_rows) one workgroup per row tile: read the tile's
+//           segment of every panel (all loads issued before the first use),
+//           place each product at its LDS word (stored position inside the
+//           tile), then sum each row from LDS left to right with the
+//           reference's rule - rows of 1..4 values start from their first
+//           product, longer rows from zero (reference:
+//           src/sparse/csr_matvec/csr_matvec.cpp:79-114) - and store y.
+//
+// Short rows therefore equal the reference CPU kernel bit for bit, for every
+// value type.  Long rows (more than W values) keep the plan's chunked path.
+// The layout and its construction are described in csr_panel_build.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "msx_device.h"
+#include "msx_internal.h"
+
+namespace msx {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kUnroll = 4;
+
+__device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Product of two accumulator-type values, rounded as the reference's CPU
+// kernel rounds a*x (common.h:58-79 there: widened operands, one product).
+__device__ inline float amul(float a, float b) { return a * b; }
+__device__ inline c64 amul(c64 a, c64 b) { return vmul<C64>(a, b); }
+
+template <class S>
+struct alignas(4 * sizeof(S)) Four {
+  S v[4];
+};
+
+// Workgroup-wide exclusive scan of one u32 per thread; returns the total.
+__device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t *wsum, uint32_t *excl) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  uint32_t inc = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += o;
+  }
+  if (lane == kWave - 1) wsum[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t s = 0;
+    for (int i = 0; i < kThreads / kWave; ++i) {
+      const uint32_t t = wsum[i];
+      wsum[i] = s;
+      s += t;
+    }
+    wsum[kThreads / kWave] = s;
+  }
+  __syncthreads();
+  *excl = wsum[wave] + inc - v;
+  const uint32_t total = wsum[kThreads / kWave];
+  __syncthreads();  // wsum is reused by the next call
+  return total;
+}
+
+template <class V>
+__global__ void __launch_bounds__(kThreads)
+    panel_products(const typename V::Storage *__restrict__ data, const uint16_t *__restrict__ col,
+                   const typename V::Storage *__restrict__ x, int64_t n_cols,
+                   typename V::Acc *__restrict__ prod, const int64_t *__restrict__ chunk_begin,
+                   const int32_t *__restrict__ chunk_panel, int64_t n_values, int PW) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  A *xs = reinterpret_cast<A *>(lds_raw);
+  const int c = blockIdx.x;
+  const int64_t q = chunk_panel[c];
+  const int64_t b = clamp64(chunk_begin[c], 0, n_values);
+  const int64_t e = clamp64(chunk_begin[c + 1], b, n_values);
+  const int64_t c0 = q * PW;
+  const int w = static_cast<int>(clamp64(n_cols - c0, 0, PW));
+  for (int i = threadIdx.x; i < w; i += kThreads) xs[i] = V::widen(x[c0 + i]);
+  __syncthreads();
+  // A valid copy has col < w; the mask keeps a corrupted one inside LDS.
+  const uint32_t mask = static_cast<uint32_t>(PW - 1);
+  int64_t a = (b + 3) & ~int64_t{3};
+  if (a > e) a = e;
+  for (int64_t i = b + threadIdx.x; i < a; i += kThreads)
+    prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
+  const int64_t nq = (e - a) / 4;
+  const auto *d4 = reinterpret_cast<const Four<S> *>(data + a);
+  const auto *k4 = reinterpret_cast<const uint2 *>(col + a);
+  auto *o4 = reinterpret_cast<Four<A> *>(prod + a);
+  int64_t qd = threadIdx.x;
+  for (; qd + (kUnroll - 1) * kThreads < nq; qd += kUnroll * kThreads) {
+    Four<S> d[kUnroll];
+    uint2 k[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      d[u] = d4[qd + u * kThreads];
+      k[u] = k4[qd + u * kThreads];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      Four<A> o;
+      o.v[0] = amul(V::widen(d[u].v[0]), xs[k[u].x & mask]);
+      o.v[1] = amul(V::widen(d[u].v[1]), xs[(k[u].x >> 16) & mask]);
+      o.v[2] = amul(V::widen(d[u].v[2]), xs[k[u].y & mask]);
+      o.v[3] = amul(V::widen(d[u].v[3]), xs[(k[u].y >> 16) & mask]);
+      o4[qd + u * kThreads] = o;
+    }
+  }
+  for (; qd < nq; qd += kThreads) {
+    const Four<S> d = d4[qd];
+    const uint2 k = k4[qd];
+    Four<A> o;
+    o.v[0] = amul(V::widen(d.v[0]), xs[k.x & mask]);
+    o.v[1] = amul(V::widen(d.v[1]), xs[(k.x >> 16) & mask]);
+    o.v[2] = amul(V::widen(d.v[2]), xs[k.y & mask]);
+    o.v[3] = amul(V::widen(d.v[3]), xs[(k.y >> 16) & mask]);
+    o4[qd] = o;
+  }
+  for (int64_t i = a + 4 * nq + threadIdx.x; i < e; i += kThreads)
+    prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
+}
+
+// NU products per thread cover a whole tile (TW = NU * kThreads words) in
+// one batch; a tile never holds more values than words.
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    panel_rows(const typename V::Acc *__restrict__ prod, const uint16_t *__restrict__ dest,
+               const uint32_t *__restrict__ seg, int64_t n_tiles, int P,
+               const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
+               const I *__restrict__ indptr, int64_t n_rows, int64_t nnz,
+               typename V::Storage *__restrict__ y, int zero_fill) {
+  using A = typename V::Acc;
+  constexpr int TW = 65536 / static_cast<int>(sizeof(A));
+  constexpr int NU = TW / kThreads;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  A *buf = reinterpret_cast<A *>(lds_raw);                   // TW words
+  uint32_t *pre = reinterpret_cast<uint32_t *>(buf + TW);    // P + 1
+  uint32_t *start = pre + (P + 1);                           // P
+  uint32_t *wsum = start + P;                                // kThreads / kWave + 1
+  const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
+
+  // Segment (q, T) of every panel: starts and a prefix of their lengths.
+  uint32_t total = 0;
+  for (int q0 = 0; q0 < P; q0 += kThreads) {
+    const int q = q0 + threadIdx.x;
+    uint32_t len = 0;
+    if (q < P) {
+      const uint32_t s = seg[static_cast<int64_t>(q) * n_tiles + T];
+      const uint32_t e = seg[static_cast<int64_t>(q) * n_tiles + T + 1];
+      start[q] = s;
+      len = e > s ? e - s : 0u;
+    }
+    uint32_t ex;
+    const uint32_t tot = block_exclusive_scan(len, wsum, &ex);
+    if (q < P) pre[q] = total + ex;
+    total += tot;
+  }
+  if (threadIdx.x == 0) pre[P] = total;
+  if (zero_fill)
+    for (int i = threadIdx.x; i < TW; i += kThreads) buf[i] = vzero<A>();
+  __syncthreads();
+
+  for (uint32_t j0 = 0; j0 < total; j0 += NU * kThreads) {
+    A pv[NU];
+    uint32_t dv[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const uint32_t j = j0 + u * kThreads + threadIdx.x;
+      dv[u] = 0xFFFFFFFFu;
+      pv[u] = vzero<A>();
+      if (j < total) {
+        int lo = 0, hi = P;  // last panel whose prefix is <= j
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (pre[mid] <= j) lo = mid; else hi = mid;
+        }
+        const uint32_t idx = start[lo] + (j - pre[lo]);
+        pv[u] = prod[idx];
+        dv[u] = dest[idx];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+      if (dv[u] < static_cast<uint32_t>(TW)) buf[dv[u]] = pv[u];
+  }
+  __syncthreads();
+
+  const int64_t r0 = clamp64(tile_begin[T], 0, n_rows);
+  const int64_t r1 = clamp64(tile_end[T], r0, n_rows);
+  const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+  for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+    const int64_t base = clamp64((s - b0) + (r - r0), 0, TW);
+    const int len = static_cast<int>(std::min<int64_t>(e - s, TW - base));
+    const A *v = buf + base;
+    A acc = vzero<A>();
+    int i = 0;
+    if (len >= 1 && len <= 4) {
+      acc = v[0];
+      i = 1;
+    }
+    for (; i < len; ++i) acc = vadd(acc, v[i]);
+    y[r] = V::narrow(acc);
+  }
+}
+
+template <class A>
+size_t pass1_lds(const msx_csr_plan *p) {
+  return sizeof(A) * static_cast<size_t>(p->panel_width);
+}
+
+template <class A>
+size_t pass2_lds(const msx_csr_plan *p) {
+  return sizeof(A) * static_cast<size_t>(p->tile_words) +
+         sizeof(uint32_t) * (2 * static_cast<size_t>(p->n_panels) + 1 + kThreads / kWave + 1);
+}
+
+// Both passes take more than 64 KB of dynamic LDS.  The limit is raised
+// when a plan is built (on the plan's device), never inside a launch, so a
+// launch stays legal under stream capture.
+template <class V, class I>
+msx_status prepare_typed(const msx_csr_plan *p) {
+  using A = typename V::Acc;
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_products<V>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(pass1_lds<A>(p))));
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_rows<V, I>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(pass2_lds<A>(p))));
+  return MSX_OK;
+}
+
+template <class V>
+msx_status prepare_v(const msx_csr_plan *p) {
+  return p->itype == MSX_I32 ? prepare_typed<V, int32_t>(p) : prepare_typed<V, int64_t>(p);
+}
+
+template <class V, class I>
+msx_status launch_typed(const msx_csr_plan *p, const void *indptr, const void *x, void *y,
+                        hipStream_t stream) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  const size_t lds1 = pass1_lds<A>(p);
+  hipLaunchKernelGGL((panel_products<V>), dim3(static_cast<uint32_t>(p->pn_chunks)), dim3(kThreads), lds1,
+                     stream, static_cast<const S *>(p->pn_data), p->pn_col, static_cast<const S *>(x),
+                     p->n_cols, static_cast<A *>(p->pn_prod), p->pn_chunk_begin, p->pn_chunk_panel,
+                     p->pn_values, static_cast<int>(p->panel_width));
+  MSX_HIP_TRY(hipGetLastError());
+  const size_t lds2 = pass2_lds<A>(p);
+  hipLaunchKernelGGL((panel_rows<V, I>), dim3(static_cast<uint32_t>(p->n_tiles)), dim3(kThreads), lds2,
+                     stream, static_cast<const A *>(p->pn_prod), p->pn_dest, p->pn_seg, p->n_tiles,
+                     static_cast<int>(p->n_panels), p->pn_tile_begin, p->pn_tile_end,
+                     static_cast<const I *>(indptr), p->n_rows, p->nnz, static_cast<S *>(y),
+                     p->pn_dropped ? 1 : 0);
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+template <class V>
+msx_status launch_v(const msx_csr_plan *p, const void *indptr, const void *x, void *y,
+                    hipStream_t stream) {
+  return p->itype == MSX_I32 ? launch_typed<V, int32_t>(p, indptr, x, y, stream)
+                             : launch_typed<V, int64_t>(p, indptr, x, y, stream);
+}
+
+}  // namespace
+
+msx_status prepare_spmv_panels(const msx_csr_plan *p) {
+  switch (p->vtype) {
+  case MSX_F32: return prepare_v<F32>(p);
+  case MSX_F16: return prepare_v<F16>(p);
+  case MSX_BF16: return prepare_v<BF16>(p);
+  case MSX_C64: return prepare_v<C64>(p);
+  }
+  return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+}
+
+msx_status launch_spmv_panels(const msx_csr_plan *p, const void *indptr, const void *x, void *y,
+                              hipStream_t stream) {
+  switch (p->vtype) {
+  case MSX_F32: return launch_v<F32>(p, indptr, x, y, stream);
+  case MSX_F16: return launch_v<F16>(p, indptr, x, y, stream);
+  case MSX_BF16: return launch_v<BF16>(p, indptr, x, y, stream);
+  case MSX_C64: return launch_v<C64>(p, indptr, x, y, stream);
+  }
+  return fail(MSX_ETYPE, "msx_csr_spmv unsupported value dtype.");
+}
+
+}  // namespace msx

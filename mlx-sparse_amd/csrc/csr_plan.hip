@@ -317,6 +317,8 @@ msx_status create_plan(msx_itype it, int64_t n_rows, int64_t nnz, const void *in
 void release(msx_csr_plan *p) {
   if (p->base) (void)hipFree(p->base);
   if (p->s_base) (void)hipFree(p->s_base);
+  if (p->pn_base) (void)hipFree(p->pn_base);
+  if (p->pn_meta) (void)hipFree(p->pn_meta);
   delete p;
 }
 
@@ -343,7 +345,7 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
     return fail(MSX_EINVAL, "msx_csr_plan_create_bound: data and indices must be non-NULL.");
   const msx_plan_options defaults{0, MSX_SLICE_AUTO, 0};
   if (opts == nullptr) opts = &defaults;
-  if (opts->slice_mode < MSX_SLICE_AUTO || opts->slice_mode > MSX_SLICE_ON || opts->reserved != 0)
+  if (opts->slice_mode < MSX_SLICE_AUTO || opts->slice_mode > MSX_SLICE_PANELS || opts->reserved != 0)
     return fail(MSX_EINVAL, "msx_csr_plan_create_bound: invalid options.");
   msx_csr_plan *p = nullptr;
   msx_status st = create_plan(it, n_rows, nnz, indptr, opts->block_nnz, stream, &p);
@@ -353,12 +355,26 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   p->slice_mode = opts->slice_mode;
   p->bound_data = data;
   p->bound_indices = indices;
-  if (opts->slice_mode != MSX_SLICE_OFF && p->n_blocks > 0) {
-    st = build_slices(p, data, indices, indptr, static_cast<hipStream_t>(stream));
-    if (st != MSX_OK) {
-      release(p);
-      return st;
-    }
+  auto s = static_cast<hipStream_t>(stream);
+  int mode = opts->slice_mode;
+  if (mode == MSX_SLICE_AUTO) {
+    bool scattered = false;
+    st = probe_scattered(p, indices, s, &scattered);
+    mode = !scattered ? MSX_SLICE_OFF : (panels_eligible(p) ? MSX_SLICE_PANELS : MSX_SLICE_ON);
+  }
+  if (st == MSX_OK && mode == MSX_SLICE_PANELS && p->n_blocks > 0) {
+    if (!panels_eligible(p))
+      st = fail(MSX_EINVAL,
+                "msx_csr_plan_create_bound: panels need nnz < 2^31, n_cols >= 1 and at most "
+                "2048 panels of x.");
+    else
+      st = build_panels(p, data, indices, indptr, s);
+  } else if (st == MSX_OK && mode == MSX_SLICE_ON && p->n_blocks > 0) {
+    st = build_slices(p, data, indices, indptr, s);
+  }
+  if (st != MSX_OK) {
+    release(p);
+    return st;
   }
   *out = p;
   return MSX_OK;
@@ -391,10 +407,15 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->n_long_rows = plan->n_long;
   info->n_chunks = plan->n_chunks;
   info->device = plan->device;
-  info->plan_bytes = static_cast<int64_t>(plan->bytes + plan->s_bytes);
+  info->plan_bytes = static_cast<int64_t>(plan->bytes + plan->s_bytes + plan->pn_bytes);
   info->n_slices = plan->n_slices;
   info->slice_width = plan->slice_width;
   info->slice_bytes = static_cast<int64_t>(plan->s_bytes);
+  info->n_panels = plan->n_panels;
+  info->panel_width = plan->panel_width;
+  info->n_tiles = plan->n_tiles;
+  info->panel_values = plan->pn_values;
+  info->panel_bytes = static_cast<int64_t>(plan->pn_bytes);
   return MSX_OK;
 }
 
@@ -425,6 +446,24 @@ extern "C" msx_status msx_csr_plan_export(const msx_csr_plan *plan, int64_t *bou
   msx_status st = export_i32(plan->bounds, plan->n_bounds + 1, bounds, true);
   if (st == MSX_OK) st = export_i32(plan->long_rows, plan->n_long, long_rows);
   if (st == MSX_OK) st = export_i32(plan->long_chunk_begin, plan->n_long + 1, long_chunk_begin);
+  (void)hipSetDevice(prev);
+  return st;
+}
+
+extern "C" msx_status msx_csr_plan_export_panels(const msx_csr_plan *plan, int64_t *tile_begin,
+                                                 int64_t *tile_end, int64_t *seg_begin) {
+  clear_error();
+  if (plan == nullptr) return fail(MSX_EINVAL, "msx_csr_plan_export_panels: plan is NULL.");
+  if (plan->n_panels == 0)
+    return fail(MSX_EINVAL, "msx_csr_plan_export_panels: the plan has no panels.");
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(plan->device);
+  msx_status st = export_i32(plan->pn_tile_begin, plan->n_tiles, tile_begin);
+  if (st == MSX_OK) st = export_i32(plan->pn_tile_end, plan->n_tiles, tile_end);
+  if (st == MSX_OK)
+    st = export_i32(reinterpret_cast<const int32_t *>(plan->pn_seg),
+                    plan->n_panels * plan->n_tiles + 1, seg_begin, true);
   (void)hipSetDevice(prev);
   return st;
 }

@@ -336,29 +336,44 @@ int bits_for(int64_t v) {  // smallest b with v <= 2^b
   return b;
 }
 
-template <class V, class I, int W>
+template <class I, int W>
+msx_status probe_typed(const msx_csr_plan *p, const void *indices, hipStream_t stream,
+                       bool *scattered) {
+  const int64_t groups = (p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
+  unsigned long long *counter = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&counter), sizeof(*counter), stream));
+  MSX_HIP_TRY(hipMemsetAsync(counter, 0, sizeof(*counter), stream));
+  hipLaunchKernelGGL((slice_probe<I, W>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
+                     stream, static_cast<const I *>(indices), p->bounds, p->bounds_nnz,
+                     p->n_bounds, p->nnz, p->n_cols, counter);
+  unsigned long long count = 0;
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(&count, counter, sizeof(count), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  (void)hipFreeAsync(counter, stream);
+  if (e != hipSuccess) return hip_fail(e, "slice probe");
+  *scattered = 2 * static_cast<int64_t>(count) > p->n_blocks;  // else mostly local
+  return MSX_OK;
+}
+
+template <class I>
+msx_status probe_w(const msx_csr_plan *p, const void *indices, hipStream_t stream,
+                   bool *scattered) {
+  switch (p->block_nnz) {
+  case 64: return probe_typed<I, 64>(p, indices, stream, scattered);
+  case 128: return probe_typed<I, 128>(p, indices, stream, scattered);
+  case 256: return probe_typed<I, 256>(p, indices, stream, scattered);
+  case 512: return probe_typed<I, 512>(p, indices, stream, scattered);
+  default: return probe_typed<I, 1024>(p, indices, stream, scattered);
+  }
+}
+
+template <class V, class I>
 msx_status build_typed(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                        hipStream_t stream) {
   using S = typename V::Storage;
   using A = typename V::Acc;
-  const int64_t groups = (p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
-  if (p->slice_mode == MSX_SLICE_AUTO) {
-    if (p->n_cols * static_cast<int64_t>(sizeof(S)) < (int64_t{8} << 20) || groups == 0) return MSX_OK;
-    unsigned long long *counter = nullptr;
-    MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&counter), sizeof(*counter), stream));
-    MSX_HIP_TRY(hipMemsetAsync(counter, 0, sizeof(*counter), stream));
-    hipLaunchKernelGGL((slice_probe<I, W>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
-                       stream, static_cast<const I *>(indices), p->bounds, p->bounds_nnz,
-                       p->n_bounds, p->nnz, p->n_cols, counter);
-    unsigned long long scattered = 0;
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(&scattered, counter, sizeof(scattered), hipMemcpyDeviceToHost, stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    (void)hipFreeAsync(counter, stream);
-    if (e != hipSuccess) return hip_fail(e, "slice probe");
-    if (2 * static_cast<int64_t>(scattered) <= p->n_blocks) return MSX_OK;  // mostly local
-  }
   const int64_t width = ((p->n_cols + kSlices - 1) / kSlices + 31) / 32 * 32;
   const int col_bits = std::max(1, bits_for(width));
   const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
@@ -392,23 +407,11 @@ msx_status build_typed(msx_csr_plan *p, const void *data, const void *indices, c
   return MSX_OK;
 }
 
-template <class V, class I>
-msx_status build_w(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
-                   hipStream_t stream) {
-  switch (p->block_nnz) {
-  case 64: return build_typed<V, I, 64>(p, data, indices, indptr, stream);
-  case 128: return build_typed<V, I, 128>(p, data, indices, indptr, stream);
-  case 256: return build_typed<V, I, 256>(p, data, indices, indptr, stream);
-  case 512: return build_typed<V, I, 512>(p, data, indices, indptr, stream);
-  default: return build_typed<V, I, 1024>(p, data, indices, indptr, stream);
-  }
-}
-
 template <class V>
 msx_status build_v(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                    hipStream_t stream) {
-  return p->itype == MSX_I32 ? build_w<V, int32_t>(p, data, indices, indptr, stream)
-                             : build_w<V, int64_t>(p, data, indices, indptr, stream);
+  return p->itype == MSX_I32 ? build_typed<V, int32_t>(p, data, indices, indptr, stream)
+                             : build_typed<V, int64_t>(p, data, indices, indptr, stream);
 }
 
 template <class V>
@@ -439,6 +442,15 @@ msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, 
   case MSX_C64: return build_v<C64>(p, data, indices, indptr, stream);
   }
   return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+}
+
+msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,
+                           bool *scattered) {
+  *scattered = false;
+  const int64_t x_bytes = p->n_cols * static_cast<int64_t>(value_bytes(p->vtype));
+  if (x_bytes < (int64_t{8} << 20) || p->n_bounds == 0 || p->n_blocks == 0) return MSX_OK;
+  return p->itype == MSX_I32 ? probe_w<int32_t>(p, indices, stream, scattered)
+                             : probe_w<int64_t>(p, indices, stream, scattered);
 }
 
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream) {

@@ -322,7 +322,9 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // Misaligned streams cannot use the quad loads of the plan kernels (the
   // long-row kernel reads the caller's arrays even on a sliced plan).
   const bool use_plan = plan != nullptr && quads_ok;
-  if (use_plan && plan->n_slices > 0) {
+  if (use_plan && plan->n_panels > 0) {
+    MSX_HIP_TRY_ST(launch_spmv_panels(plan, indptr, x, y, stream));
+  } else if (use_plan && plan->n_slices > 0) {
     MSX_HIP_TRY_ST(launch_spmv_sliced(plan, x, y, stream));
   } else if (use_plan) {
     if (plan->n_bounds > plan->n_long) {

@@ -76,6 +76,29 @@ struct msx_csr_plan {
   void *s_partial;            // kSlices * n_rows accumulators
   void *s_base;
   size_t s_bytes;
+  // Column panels (csr_panel.hip, csr_panel_build.hip); n_panels == 0 when
+  // the plan has none.  Values of short rows with a valid column, ordered by
+  // (panel, tile, stored position): segment (panel q, tile t) is
+  // [pn_seg[q * n_tiles + t], pn_seg[q * n_tiles + t + 1]).
+  int64_t n_panels;
+  int64_t panel_width;        // columns per panel (LDS-resident in pass 1)
+  int64_t n_tiles;
+  int64_t tile_words;         // LDS words of a tile: products plus one per row
+  int64_t pn_values;          // values in the panel copy
+  int64_t pn_chunks;          // pass-1 workgroups
+  bool pn_dropped;            // some short-row values had a column outside [0, n_cols)
+  int32_t *pn_tile_begin;     // n_tiles
+  int32_t *pn_tile_end;       // n_tiles
+  uint32_t *pn_seg;           // n_panels * n_tiles + 1
+  int64_t *pn_chunk_begin;    // pn_chunks + 1: pass-1 ranges of the panel copy
+  int32_t *pn_chunk_panel;    // pn_chunks
+  void *pn_data;              // pn_values storage values
+  uint16_t *pn_col;           // column within the panel
+  uint16_t *pn_dest;          // LDS word of the value in its tile: (p - tile's first value) + (row - tile's first row)
+  void *pn_prod;              // pn_values accumulator-type products (pass 1 -> pass 2)
+  void *pn_base;              // allocation of pn_data, pn_col, pn_dest, pn_prod
+  void *pn_meta;              // allocation of the tile, segment and chunk arrays
+  size_t pn_bytes;
 };
 
 namespace msx {
@@ -89,6 +112,19 @@ msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_col
 msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                         hipStream_t stream);
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream);
+// True when the short blocks' columns are scattered over an x of more than
+// 8 MB (the AUTO rule for a reordered copy).  Synchronises `stream`.
+msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,
+                           bool *scattered);
+
+// Panel plans (csr_panel_build.hip / csr_panel.hip).
+bool panels_eligible(const msx_csr_plan *p);
+msx_status build_panels(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
+                        hipStream_t stream);
+msx_status launch_spmv_panels(const msx_csr_plan *p, const void *indptr, const void *x, void *y,
+                              hipStream_t stream);
+// Raises the dynamic-LDS limit of the two panel kernels on the current device.
+msx_status prepare_spmv_panels(const msx_csr_plan *p);
 
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,

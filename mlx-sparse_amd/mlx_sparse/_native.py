@@ -26,6 +26,7 @@ def csr_matmul(data, indices, indptr, rhs, shape: Shape2D, plan=None) -> torch.T
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,
-    which may hold a column-sliced copy (slice_mode 0 auto, 1 off, 2 on)."""
+    which may hold a reordered copy for scattered gathers (slice_mode 0 auto,
+    1 off, 2 XCD column slices, 3 LDS column panels)."""
     return extension().csr_plan(indptr, n_rows, nnz, block_nnz, data=data, indices=indices,
                                 n_cols=n_cols, slice_mode=slice_mode)

@@ -5,8 +5,11 @@ Only the CPU worker budget reaches this path.  As in the reference, the
 option is mirrored into ``MLX_SPARSE_CPU_THREADS`` in ``os.environ``, which
 the native CPU path reads on every call.  ``GPU_PLAN`` (new) toggles the
 cached row-block plan of the GPU SpMV; without it a plan-free kernel runs.
-``GPU_SLICE`` (new) selects the plan's XCD column slicing: "auto" (default),
-"off" or "on"; it applies to plans built while it is set.
+``GPU_SLICE`` (new) selects the reordered copy a plan may hold for scattered
+gathers: "auto" (default: panels when the columns are scattered over an x of
+more than 8 MB and the matrix qualifies, else XCD slices), "off", "on" (XCD
+column slices) or "panels" (LDS column panels); it applies to plans built
+while it is set.
 """
 
 from __future__ import annotations
@@ -19,14 +22,14 @@ from typing import Any
 
 _ENV = {"n_threads": "MLX_SPARSE_CPU_THREADS", "gpu_plan": "MLX_SPARSE_GPU_PLAN",
         "gpu_slice": "MLX_SPARSE_GPU_SLICE"}
-_SLICE = {"auto": 0, "off": 1, "on": 2}
+_SLICE = {"auto": 0, "off": 1, "on": 2, "panels": 3}
 _MISSING = object()
 
 
 class RuntimeOption(str, enum.Enum):
     N_THREADS = "n_threads"
     GPU_PLAN = "gpu_plan"
-    GPU_SLICE = "gpu_slice"  # "auto" | "off" | "on": XCD column slicing of plans
+    GPU_SLICE = "gpu_slice"  # "auto" | "off" | "on" | "panels": reordered copy of plans
 
 
 def _parse_threads(value: Any) -> int | str:

@@ -224,6 +224,11 @@ py::dict plan_info(const Plan &plan) {
   d["n_slices"] = info.n_slices;
   d["slice_width"] = info.slice_width;
   d["slice_bytes"] = info.slice_bytes;
+  d["n_panels"] = info.n_panels;
+  d["panel_width"] = info.panel_width;
+  d["n_tiles"] = info.n_tiles;
+  d["panel_values"] = info.panel_values;
+  d["panel_bytes"] = info.panel_bytes;
   return d;
 }
 
@@ -279,7 +284,7 @@ PYBIND11_MODULE(_ext, m) {
         py::arg("block_nnz") = 0, py::arg("data") = py::none(), py::arg("indices") = py::none(),
         py::arg("n_cols") = -1, py::arg("slice_mode") = 0,
         "Build a row-block plan from a GPU indptr; with data/indices, a plan bound to the "
-        "matrix (slice_mode 0 auto, 1 off, 2 on: column slices per XCD).");
+        "matrix (slice_mode 0 auto, 1 off, 2 column slices per XCD, 3 LDS column panels).");
   m.def("csr_matvec", &csr_matvec, py::arg("data"), py::arg("indices"), py::arg("indptr"),
         py::arg("x"), py::arg("n_rows"), py::arg("n_cols"), py::arg("plan") = py::none(),
         py::arg("n_threads") = 0, "Multiply CSR buffers by a dense vector.");

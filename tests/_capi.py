@@ -21,7 +21,8 @@ OK, EINVAL, ETYPE, EHIP, ENOMEM = range(5)
 class PlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in (
         "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_bounds", "n_long_rows",
-        "n_chunks", "device", "plan_bytes", "n_slices", "slice_width", "slice_bytes")]
+        "n_chunks", "device", "plan_bytes", "n_slices", "slice_width", "slice_bytes",
+        "n_panels", "panel_width", "n_tiles", "panel_values", "panel_bytes")]
 
 
 class PlanOptions(ctypes.Structure):
@@ -29,7 +30,7 @@ class PlanOptions(ctypes.Structure):
                 ("reserved", ctypes.c_int32)]
 
 
-SLICE_AUTO, SLICE_OFF, SLICE_ON = 0, 1, 2
+SLICE_AUTO, SLICE_OFF, SLICE_ON, SLICE_PANELS = 0, 1, 2, 3
 
 
 def declared_functions() -> list[str]:
@@ -54,6 +55,7 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_plan_destroy.argtypes = [vp]
         L.msx_csr_plan_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
         L.msx_csr_plan_export.argtypes = [vp, vp, vp, vp]
+        L.msx_csr_plan_export_panels.argtypes = [vp, vp, vp, vp]
         L.msx_csr_spmv.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
         L.msx_csr_spmm.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp, i64, vp, vp]
         L.msx_csr_spmv_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
@@ -62,7 +64,8 @@ def lib() -> ctypes.CDLL:
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
                      "msx_csr_plan_destroy",
-                     "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_spmv", "msx_csr_spmm",
+                     "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_plan_export_panels",
+                     "msx_csr_spmv", "msx_csr_spmm",
                      "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges"):
             getattr(L, name).restype = ci
         _lib = L
@@ -110,6 +113,15 @@ class Plan:
         st = lib().msx_csr_plan_export(self.ptr, _p(blocks), _p(longs), _p(chunks))
         assert st == OK, last_error()
         return blocks.numpy(), longs[: info.n_long_rows].numpy(), chunks.numpy()
+
+    def export_panels(self):
+        info = self.info()
+        tb = torch.empty(max(info.n_tiles, 1), dtype=torch.int64)
+        te = torch.empty(max(info.n_tiles, 1), dtype=torch.int64)
+        seg = torch.empty(info.n_panels * info.n_tiles + 1, dtype=torch.int64)
+        st = lib().msx_csr_plan_export_panels(self.ptr, _p(tb), _p(te), _p(seg))
+        assert st == OK, last_error()
+        return tb[: info.n_tiles].numpy(), te[: info.n_tiles].numpy(), seg.numpy()
 
     def close(self):
         if self.ptr:

@@ -197,7 +197,9 @@ def test_out_of_range_columns_add_nothing():
     d, i, p = _upload(data, indices, indptr, "float32")
     sliced = _capi.Plan(p, 2, 6, data=d, indices=i, n_cols=3, slice_mode=_capi.SLICE_ON)
     assert sliced.info().n_slices == 8
-    for plan in (_capi.Plan(p, 2, 6), None, sliced):
+    panels = _capi.Plan(p, 2, 6, data=d, indices=i, n_cols=3, slice_mode=_capi.SLICE_PANELS)
+    assert panels.info().n_panels == 1 and panels.info().panel_values == 3
+    for plan in (_capi.Plan(p, 2, 6), None, sliced, panels):
         y = _capi.spmv(d, i, p, to_torch(x, None, DEV), 2, 3, plan=plan)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(to_numpy(y), [1.0, 6.0])
@@ -287,11 +289,23 @@ def test_configs_full_size(name):
                             what=f"{name}/full")
     if name == "random16":
         np.testing.assert_array_equal(out["plan"], want)
-        # the benchmark path: bound plan with XCD column slices
         d, i, p = _upload(m.data, m.indices, m.indptr, "float32")
+        xt = to_torch(x, None, DEV)
+        # the benchmark path: bound plan, AUTO picks LDS column panels; every
+        # row is summed in stored order, so the result equals the oracle
         plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1])
+        info = plan.info()
+        assert info.n_panels == 128 and info.n_slices == 0 and info.panel_values == m.nnz
+        for _ in range(2):
+            y = _capi.spmv(d, i, p, xt, m.shape[0], m.shape[1], plan=plan)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(to_numpy(y), want)
+        plan.close()
+        # XCD column slices on request
+        plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1],
+                          slice_mode=_capi.SLICE_ON)
         assert plan.info().n_slices == 8
-        y = _capi.spmv(d, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
+        y = _capi.spmv(d, i, p, xt, m.shape[0], m.shape[1], plan=plan)
         torch.cuda.synchronize()
         assert_rows_close(to_numpy(y), want,
                           orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]), "float32",
@@ -325,29 +339,28 @@ def test_sliced_plan_parity(vtype, index_dtype):
         plan.close()
 
 
-def test_sliced_auto_selection_and_binding():
+def test_auto_selection_and_binding():
     from mlx_sparse import synthetic as s
 
     m = s.random_fixed_row(1 << 21, 16, seed=4)  # x = 8.4 MB, columns scattered
     d, i, p = _upload(m.data, m.indices, m.indptr, "float32")
     plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1])
-    assert plan.info().n_slices == 8
+    assert plan.info().n_panels == 64 and plan.info().n_slices == 0
     x = s.uniform(m.shape[1], -1, 1, 5)
     y = _capi.spmv(d, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
     torch.cuda.synchronize()
     want = orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=8)
-    assert_rows_close(to_numpy(y), want, orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]),
-                      "float32", "sliced auto")
+    np.testing.assert_array_equal(to_numpy(y), want)
     # a bound plan refuses other buffers
     d2 = d.clone()
     with pytest.raises(RuntimeError, match="bound to other"):
         _capi.spmv(d2, i, p, to_torch(x, None, DEV), m.shape[0], m.shape[1], plan=plan)
     plan.close()
-    # a stencil with the same x size stays unsliced (its gathers are local)
+    # a stencil with the same x size keeps the row blocks (its gathers are local)
     g = s.laplacian_2d(1 << 11)
     d, i, p = _upload(g.data, g.indices, g.indptr, "float32")
     plan = _capi.Plan(p, g.shape[0], g.nnz, data=d, indices=i, n_cols=g.shape[1])
-    assert plan.info().n_slices == 0
+    assert plan.info().n_slices == 0 and plan.info().n_panels == 0
     plan.close()
 
 
@@ -357,13 +370,118 @@ def test_sliced_through_api(gpu):
     ms = gpu
     m = s.random_fixed_row(1 << 21, 16, seed=6)
     A = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
-    assert A.plan().info()["n_slices"] == 8
+    assert A.plan().info()["n_panels"] == 64
     x = s.uniform(m.shape[1], -1, 1, 7)
     y = (A @ torch.from_numpy(x).to(DEV)).cpu().numpy()
     want = orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=8)
-    assert_rows_close(y, want, orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]), "float32",
-                      "sliced api")
+    np.testing.assert_array_equal(y, want)
+    with ms.runtime.context(gpu_slice="on"):
+        C = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
+        assert C.plan().info()["n_slices"] == 8 and C.plan().info()["n_panels"] == 0
+        assert_rows_close((C @ torch.from_numpy(x).to(DEV)).cpu().numpy(), want,
+                          orc.row_scale(m.data, m.indices, m.indptr, x, m.shape[0]), "float32",
+                          "sliced api")
     with ms.runtime.context(gpu_slice="off"):
         B = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
-        assert B.plan().info()["n_slices"] == 0
+        assert B.plan().info()["n_slices"] == 0 and B.plan().info()["n_panels"] == 0
         np.testing.assert_array_equal((B @ torch.from_numpy(x).to(DEV)).cpu().numpy(), want)
+
+
+# -- LDS column panels (bound plans) -------------------------------------------------
+
+ACC_BYTES = {"float32": 4, "float16": 4, "bfloat16": 4, "complex64": 8}
+
+
+def _assert_short_rows_equal(got, want, lengths, W, vtype, what):
+    """Rows of at most W values are summed in stored order by both sides:
+    equal bit for bit, the sign of zero included."""
+    short = lengths <= W
+    g, w = got[short], want[short]
+    if vtype == "complex64":
+        g, w = g.view(np.float32), w.view(np.float32)
+    np.testing.assert_array_equal(g, w, err_msg=what)
+    if vtype in ("float32", "complex64"):
+        np.testing.assert_array_equal(np.signbit(g), np.signbit(w), err_msg=f"{what} (signed zero)")
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_panel_plan_parity(vtype, index_dtype):
+    rng = np.random.default_rng(41)
+    n_rows, n_cols = 9000, 200_000
+    lengths = rng.integers(0, 40, n_rows)
+    lengths[rng.random(n_rows) < 0.1] = 0
+    few = rng.random(n_rows) < 0.1
+    lengths[few] = rng.integers(1, 5, int(few.sum()))  # the 1..4-value rule
+    lengths[[17, 2000, 8999]] = [3000, 9000, 700]  # long rows keep the row-block path
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, index_dtype)
+    data, x = _values(rng, nnz, vtype), _values(rng, n_cols, vtype)
+    data[::53] = storage(np.array([-0.0]), vtype)[0] if vtype != "complex64" else data[::53]
+    want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+    scale = orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype)
+    d, i, p = _upload(data, indices, indptr, vtype)
+    xt = to_torch(x, vtype, DEV)
+    for W in (64, 512):
+        plan = _capi.Plan(p, n_rows, nnz, W, data=d, indices=i, n_cols=n_cols,
+                          slice_mode=_capi.SLICE_PANELS)
+        info = plan.info()
+        PW = 131072 // ACC_BYTES[vtype]
+        assert info.n_panels == -(-n_cols // PW) and info.panel_width == PW
+        tb, te, seg = plan.export_panels()
+        otb, ote, oseg = plan_oracle.panel_layout(indptr, indices, n_cols, ACC_BYTES[vtype], W)
+        np.testing.assert_array_equal(tb, otb)
+        np.testing.assert_array_equal(te, ote)
+        np.testing.assert_array_equal(seg, oseg)
+        assert info.panel_values == int(oseg[-1])
+        for _ in range(2):  # products are rewritten each call
+            y = _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan)
+            torch.cuda.synchronize()
+            got = to_numpy(y)
+            _assert_short_rows_equal(got, want, lengths, W, vtype, f"panels {vtype} W={W}")
+            assert_rows_close(got, want, scale, vtype, f"panels {vtype} W={W}")
+        plan.close()
+
+
+def test_panel_plan_small_and_degenerate():
+    # a single panel, empty rows at both ends, one-value rows, n_cols not a
+    # multiple of anything
+    data = np.array([2.0, -1.0, 3.0, -0.0, 5.0], np.float32)
+    indices = np.array([4, 0, 2, 1, 3], np.int32)
+    indptr = np.array([0, 0, 1, 3, 4, 5, 5], np.int32)
+    x = np.array([1.0, 7.0, -2.0, 0.5, 3.0], np.float32)
+    d, i, p = _upload(data, indices, indptr, "float32")
+    plan = _capi.Plan(p, 6, 5, data=d, indices=i, n_cols=5, slice_mode=_capi.SLICE_PANELS)
+    assert plan.info().n_panels == 1 and plan.info().n_tiles == 1
+    y = to_numpy(_capi.spmv(d, i, p, to_torch(x, None, DEV), 6, 5, plan=plan))
+    want = orc.csr_matvec(data, indices, indptr, x, 6)
+    np.testing.assert_array_equal(y, want)
+    np.testing.assert_array_equal(np.signbit(y), np.signbit(want))  # -0.0 * 7 keeps its sign
+
+
+def test_panel_plan_rejects_oversized_x():
+    d = torch.ones(2, device=DEV)
+    i = torch.zeros(2, dtype=torch.int32, device=DEV)
+    p = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="2048 panels"):
+        _capi.Plan(p, 2, 2, data=d, indices=i, n_cols=2048 * 32768 + 1,
+                   slice_mode=_capi.SLICE_PANELS)
+
+
+@pytest.mark.parametrize("name", ["laplacian", "powerlaw", "banded"])
+def test_panel_plan_on_configs(name):
+    """Panels on request for the other benchmark matrices (AUTO keeps row
+    blocks for them): short rows equal the oracle bit for bit."""
+    m, x = _config(name, small=True)
+    vtype = "bfloat16" if name == "banded" else "float32"
+    data, xv = storage(m.data, vtype), storage(x, vtype)
+    want = orc.csr_matvec(data, m.indices, m.indptr, xv, m.shape[0], vtype=vtype, n_threads=8)
+    d, i, p = _upload(data, m.indices, m.indptr, vtype)
+    plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1],
+                      slice_mode=_capi.SLICE_PANELS)
+    assert plan.info().n_panels >= 1
+    y = to_numpy(_capi.spmv(d, i, p, to_torch(xv, vtype, DEV), m.shape[0], m.shape[1], plan=plan))
+    lengths = np.diff(m.indptr.astype(np.int64))
+    _assert_short_rows_equal(y, want, lengths, 256, vtype, f"{name} panels")
+    assert_rows_close(y, want, orc.row_scale(data, m.indices, m.indptr, xv, m.shape[0], vtype=vtype),
+                      vtype, f"{name} panels", lengths=lengths, min_len_exempt=LONG_ROW_EXEMPT,
+                      exact=orc.row_exact(data, m.indices, m.indptr, xv, m.shape[0], vtype=vtype))

@@ -67,3 +67,57 @@ def test_block_invariants(kind):
 def test_empty_matrix():
     blocks, longs, cb = plan_oracle.plan(np.zeros(1, np.int64))
     assert blocks.tolist() == [0] and longs.size == 0 and cb.tolist() == [0]
+
+
+# -- column-panel layout ------------------------------------------------------------
+
+def _panel_case(rng, kind, n=3000, n_cols=70000):
+    p = _indptr(rng, n, kind)
+    idx = rng.integers(0, n_cols, int(p[-1]))
+    if kind == "mixed":  # a few malformed columns, dropped from the copy
+        bad = rng.random(len(idx)) < 0.01
+        idx[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -1, n_cols + 5)
+    return p, idx, n_cols
+
+
+@pytest.mark.parametrize("kind", ["uniform", "mixed", "empty", "zipf"])
+@pytest.mark.parametrize("acc_bytes,W", [(4, 256), (4, 64), (8, 1024)])
+def test_panel_layout_matches_loop(kind, acc_bytes, W):
+    rng = np.random.default_rng(acc_bytes * W)
+    p, idx, n_cols = _panel_case(rng, kind)
+    a = plan_oracle.panel_layout(p, idx, n_cols, acc_bytes, W)
+    b = plan_oracle.panel_layout_loop(p, idx, n_cols, acc_bytes, W)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
+@pytest.mark.parametrize("kind", ["uniform", "mixed", "empty", "zipf"])
+@pytest.mark.parametrize("acc_bytes", [4, 8])
+def test_panel_layout_invariants(kind, acc_bytes):
+    W = 256
+    rng = np.random.default_rng(11)
+    p, idx, n_cols = _panel_case(rng, kind, n=20000, n_cols=200000)
+    PW, TW, H = plan_oracle.panel_constants(acc_bytes, W)
+    tb, te, seg = plan_oracle.panel_layout(p, idx, n_cols, acc_bytes, W)
+    lengths = np.diff(p)
+    # every short row in exactly one tile; long rows in none
+    covered = np.zeros(len(lengths), int)
+    for a, b in zip(tb, te):
+        assert a < b
+        covered[a:b] += 1
+        assert np.all(lengths[a:b] <= W)
+        assert (p[b] - p[a]) + (b - a) <= TW  # products + one word per row fit
+    np.testing.assert_array_equal(covered, (lengths <= W).astype(int))
+    assert np.all(tb[1:] >= te[:-1])
+    # segments partition the valid short-row values by (panel, tile)
+    n_tiles, P = len(tb), -(-n_cols // PW)
+    assert len(seg) == P * n_tiles + 1 and seg[0] == 0 and np.all(np.diff(seg) >= 0)
+    counts = np.zeros(P * n_tiles, np.int64)
+    for t, (a, b) in enumerate(zip(tb, te)):
+        cols = idx[p[a]:p[b]]
+        cols = cols[(cols >= 0) & (cols < n_cols)]
+        np.add.at(counts, (cols // PW) * n_tiles + t, 1)
+    np.testing.assert_array_equal(np.diff(seg), counts)
+    short_vals = sum(int(((idx[p[r]:p[r + 1]] >= 0) & (idx[p[r]:p[r + 1]] < n_cols)).sum())
+                     for r in np.flatnonzero(lengths <= W))
+    assert seg[-1] == short_vals
