@@ -2,19 +2,22 @@
 """Benchmark of the CSR sparse x dense hot path on one MI355X.
 
 A step is one CSR SpMV ``y = A @ x`` through the drop-in API (``CSRArray``
-with its cached row-block plan, ``A @ x`` on torch's current stream) on the
+with its cached bound plan, ``A @ x`` on torch's current stream) on the
 headline workload: n = 4,194,304 rows, exactly 16 columns per row drawn
 uniformly without replacement, float32 values / int32 indices (synthetic,
-seeded).  Inputs are resident in HBM before timing starts.
+seeded).  Inputs are resident in HBM before timing starts.  The plan is the
+library's automatic choice for this matrix: LDS column panels (two passes,
+panel_products then panel_rows).
 
 Prints ONE JSON line.  ``value`` is the effective bandwidth on compulsory
 traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 
-- ``roofline``: achieved GB/s of one SpMV call (the column-sliced kernel and
-  its slice-merge kernel, back to back on the launch stream) from HIP events
-  around repeated calls, against the 8 TB/s HBM peak; ``traffic`` is the
-  measured HBM bytes per call from the committed rocprofv3 FETCH_SIZE /
-  WRITE_SIZE summary (profiles/spmv_random16_traffic.txt), else null;
+- ``roofline``: achieved GB/s of one SpMV call (both kernels of the plan,
+  back to back on the launch stream) from HIP events around HIP-graph
+  replays, against the 8 TB/s HBM peak; ``traffic`` is the measured HBM
+  bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+  summary (profiles/spmv_random16_traffic.txt) when it was taken on the same
+  plan kind, else null;
 - ``cold``: the same SpMV with a 1 GiB buffer written between launches
   (evicts the 256 MB Infinity Cache), median of per-launch times;
 - ``spmm``: CSR SpMM with k=64 on the 3D 7-point Poisson matrix (128^3),
@@ -235,12 +238,14 @@ def main() -> int:
     cold_gbs = nbytes / (cold_ms * 1e-3) / 1e9
     log(f"cold: {cold_ms * 1e3:.1f} us  {cold_gbs:.0f} GB/s")
 
+    plan_kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
     traffic = None
     tf = Path(args.traffic)
     if tf.exists():
-        for line in tf.read_text().splitlines():
-            if line.startswith("hbm_bytes_per_call:"):
-                traffic = int(line.split(":", 1)[1].strip())
+        fields = dict(line.split(":", 1) for line in tf.read_text().splitlines()
+                      if ":" in line and not line.startswith("#"))
+        if fields.get("plan_kind", "").strip() == plan_kind and "hbm_bytes_per_call" in fields:
+            traffic = int(fields["hbm_bytes_per_call"].strip())
 
     result = {
         "metric": "CSR SpMV effective HBM GB/s (% of peak) + SpMM GFLOP/s, fp32, 1xMI355X",
@@ -258,15 +263,18 @@ def main() -> int:
         "config": {"workload": "csr_spmv random16 n=4194304 nnz=67108864 f32/i32",
                    "n_rows": m.shape[0], "nnz": m.nnz, "index": "int32",
                    "compulsory_bytes": nbytes, "plan_build_ms": round(plan_ms, 3),
-                   "plan": {k: info[k] for k in ("block_nnz", "n_blocks", "n_long_rows",
-                                                 "n_slices", "plan_bytes")}},
+                   "plan": {"kind": plan_kind,
+                            **{k: info[k] for k in ("block_nnz", "n_blocks", "n_long_rows",
+                                                    "n_slices", "n_panels", "n_tiles",
+                                                    "plan_bytes")}}},
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 2),
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": ("spmv_sliced<F32> + slice_merge<F32>" if info.get("n_slices")
-                                else f"spmv_blocks<F32,int,{info['block_nnz']}>"),
+                     "kernel": {"panels": "panel_products<F32> + panel_rows<F32,int>",
+                                "slices": "spmv_sliced<F32> + slice_merge<F32>"}.get(
+                                    plan_kind, f"spmv_blocks<F32,int,{info['block_nnz']}>"),
                      "kernel_us": round(kern_ms * 1e3, 2),
                      "timing": "HIP-graph replay of 20 calls x 10, HIP events"},
         "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),

@@ -44,7 +44,7 @@ constexpr int64_t kMaxGrid = int64_t{1} << 20;
 constexpr int64_t kPanelBytes = 131072;  // x panel in LDS during pass 1
 constexpr int64_t kTileBytes = 65536;    // tile products in LDS during pass 2
 constexpr int64_t kMaxPanels = 2048;
-constexpr int64_t kMinChunk = 65536;     // values per pass-1 workgroup, at least
+constexpr int64_t kMinChunk = 65536;     // values per pass-1 workgroup, about
 
 uint32_t grid_for(int64_t n) {
   return static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, kMaxGrid)));
@@ -311,16 +311,18 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   MSX_HIP_TRY(hipStreamSynchronize(stream));
   const int64_t n_values = pb[P];
 
-  // Pass-1 chunks: about one per CU, at least kMinChunk values each, never
-  // across a panel boundary.  Chunks per panel = ceil(len / K) <= len / K + 1,
-  // so the total stays within P + n_values / K <= P + CUs.
-  const int64_t K = std::max<int64_t>(kMinChunk, (n_values + cus - 1) / cus);
+  // Pass-1 chunks: about one per CU (C in total, at least kMinChunk values
+  // each), never across a panel boundary.  Panel q gets round(C * len / total)
+  // chunks, at least one: a panel holding a few values more than its share
+  // must not add a chunk, or the grid spills into a second, nearly empty
+  // round of workgroups.  The total stays within C + P / 2 + 1 <= CUs + P.
+  const int64_t C = std::max<int64_t>(1, std::min<int64_t>(cus, n_values / kMinChunk));
   std::vector<int64_t> cbeg;
   std::vector<int32_t> cpan;
   for (int64_t q = 0; q < P; ++q) {
     const int64_t a = pb[q], b = pb[q + 1];
     if (b <= a) continue;
-    const int64_t c = (b - a + K - 1) / K;
+    const int64_t c = std::max<int64_t>(1, (2 * C * (b - a) + n_values) / (2 * n_values));
     for (int64_t i = 0; i < c; ++i) {
       cbeg.push_back(a + (b - a) * i / c);
       cpan.push_back(static_cast<int32_t>(q));
