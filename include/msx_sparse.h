@@ -245,6 +245,40 @@ msx_status msx_csr_spmm(msx_vtype vt, msx_itype it, int64_t n_rows,
                         const msx_csr_plan *plan, void *stream);
 
 /*
+ * Batched SpMV on the device: Y[b, :] = A X[b, :] for b < batch, X a
+ * batch x n_cols matrix with row stride ldx, Y batch x n_rows with row stride
+ * ldy (elements).  Each output is summed from zero in stored order, so
+ * float32 results equal the reference's batched CPU kernel bit for bit.  The
+ * vectors are transposed into one n_cols x batch operand and multiplied by
+ * one SpMM (the matrix is read once), through scratch taken from the
+ * stream-ordered allocator of `stream`.
+ *
+ * Replaces CSRBatchedMatVec::eval_gpu (reference:
+ * src/sparse/csr_batched_matvec/csr_batched_matvec.cpp:186-226).
+ */
+msx_status msx_csr_batched_spmv(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                int64_t n_cols, int64_t nnz, const void *data,
+                                const void *indices, const void *indptr,
+                                int64_t batch, const void *X, int64_t ldx,
+                                void *Y, int64_t ldy, void *stream);
+
+/*
+ * Batched SpMM on the device: Y[b] = A X[b] for b < batch.  X[b] starts at
+ * X + b * x_batch (row-major n_cols x k, row stride ldx), Y[b] at
+ * Y + b * y_batch (n_rows x k, row stride ldy); strides in elements.  Summed
+ * like msx_csr_spmm.  No scratch.
+ *
+ * Replaces CSRBatchedMatMul::eval_gpu (reference:
+ * src/sparse/csr_batched_matmul/csr_batched_matmul.cpp).
+ */
+msx_status msx_csr_batched_spmm(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                int64_t n_cols, int64_t nnz, const void *data,
+                                const void *indices, const void *indptr,
+                                int64_t batch, int64_t k, const void *X,
+                                int64_t x_batch, int64_t ldx, void *Y,
+                                int64_t y_batch, int64_t ldy, void *stream);
+
+/*
  * Host (CPU) SpMV with host pointers, the `use_cpu()` device: rows are summed
  * sequentially in stored order, rows are split over `n_threads` std::threads
  * in nnz-balanced contiguous ranges (n_threads <= 0: the resolved worker
@@ -268,6 +302,29 @@ msx_status msx_csr_spmm_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
                             int64_t n_cols, int64_t nnz, const void *data,
                             const void *indices, const void *indptr,
                             int64_t k, const void *X, void *Y, int n_threads);
+
+/*
+ * Host (CPU) batched SpMV / SpMM, contiguous operands: X batch x n_cols and
+ * Y batch x n_rows (SpMV), X batch x n_cols x k and Y batch x n_rows x k
+ * (SpMM).  Work items are (batch, row) pairs split over `n_threads` threads in
+ * contiguous ranges balanced by row length (times k); each output is summed
+ * from zero in stored order.
+ *
+ * Replace csr_batched_matvec_cpu_impl (reference:
+ * src/sparse/csr_batched_matvec/csr_batched_matvec.cpp:82-146) and
+ * csr_batched_matmul_cpu_impl (reference:
+ * src/sparse/csr_batched_matmul/csr_batched_matmul.cpp:85-248).
+ */
+msx_status msx_csr_batched_spmv_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                    int64_t n_cols, int64_t nnz,
+                                    const void *data, const void *indices,
+                                    const void *indptr, int64_t batch,
+                                    const void *X, void *Y, int n_threads);
+msx_status msx_csr_batched_spmm_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                    int64_t n_cols, int64_t nnz,
+                                    const void *data, const void *indices,
+                                    const void *indptr, int64_t batch, int64_t k,
+                                    const void *X, void *Y, int n_threads);
 
 /*
  * CPU worker count resolved from the environment: MLX_SPARSE_CPU_THREADS,

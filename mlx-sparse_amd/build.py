@@ -81,7 +81,9 @@ def build(verbose: bool = True) -> Path:
     py_inc = sysconfig.get_paths()["include"]
     bind_srcs = [SRC / "bindings.cpp", SRC / "common" / "validate.cpp",
                  SRC / "sparse" / "csr_matvec" / "csr_matvec.cpp",
-                 SRC / "sparse" / "csr_matmul" / "csr_matmul.cpp"]
+                 SRC / "sparse" / "csr_matmul" / "csr_matmul.cpp",
+                 SRC / "sparse" / "csr_batched_matvec" / "csr_batched_matvec.cpp",
+                 SRC / "sparse" / "csr_batched_matmul" / "csr_batched_matmul.cpp"]
     bind_objs = []
     for s in bind_srcs:
         o = BUILD / ("bind_" + s.stem + ".o")

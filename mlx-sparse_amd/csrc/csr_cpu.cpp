@@ -330,6 +330,44 @@ void spmm(int64_t n, int64_t k, const void *data, const void *indices, const voi
   parallel_for(ranges, body);
 }
 
+// Batched: items (b, row), b < batch; batch b reads X + b * n_cols * k and
+// writes Y + b * n_rows * k.  Work per item = row length * max(k, 1).
+template <class V, class I>
+void batched(int64_t n, int64_t n_cols, int64_t batch, int64_t k, const void *data,
+             const void *indices, const void *indptr, const void *X, void *Y, int workers) {
+  const auto *d = static_cast<const typename V::S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *xv = static_cast<const typename V::S *>(X);
+  auto *yv = static_cast<typename V::S *>(Y);
+  using A = typename V::A;
+  const int64_t items = n * batch;
+  auto body = [&](Range r) {
+    std::vector<A> acc(static_cast<size_t>(std::max<int64_t>(k, 1)));
+    for (int64_t item = r.begin; item < r.end; ++item) {
+      const int64_t b = item / n, row = item - b * n;
+      const typename V::S *xb = xv + b * n_cols * k;
+      std::fill(acc.begin(), acc.end(), A{});
+      for (int64_t p = at(ip, row); p < at(ip, row + 1); ++p) {
+        const typename V::S v = d[p];
+        const typename V::S *xr = xb + at(ix, p) * k;
+        for (int64_t c = 0; c < k; ++c) acc[c] = add(acc[c], V::mul(v, xr[c]));
+      }
+      typename V::S *yr = yv + (b * n + row) * k;
+      for (int64_t c = 0; c < k; ++c) yr[c] = V::narrow(acc[c]);
+    }
+  };
+  if (workers <= 1 || items <= 0) return body({0, items});
+  std::vector<int64_t> work(static_cast<size_t>(items));
+  for (int64_t item = 0; item < items; ++item) {
+    const int64_t row = item % n;
+    work[item] = (at(ip, row + 1) - at(ip, row)) * std::max<int64_t>(k, 1);
+  }
+  const auto ranges = ranges_for_work(work, workers);
+  if (ranges.size() <= 1) return body({0, items});
+  parallel_for(ranges, body);
+}
+
 }  // namespace
 
 int worker_count() {
@@ -453,4 +491,59 @@ extern "C" msx_status msx_cpu_ranges(const int64_t *work, int64_t n, int parts, 
     }
     *n_ranges = static_cast<int64_t>(r.size());
   });
+}
+
+namespace {
+
+template <class V>
+void batched_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t batch, int64_t k,
+                const void *data, const void *indices, const void *indptr, const void *X, void *Y,
+                int workers) {
+  if (it == MSX_I64)
+    cpu::batched<V, int64_t>(n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers);
+  else
+    cpu::batched<V, int32_t>(n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers);
+}
+
+msx_status batched_cpu(const char *op, msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                       int64_t nnz, const void *data, const void *indices, const void *indptr,
+                       int64_t batch, int64_t k, const void *X, void *Y, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu(op, vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (batch < 0 || k < 0) return fail(MSX_EINVAL, std::string(op) + " shape dimensions must be non-negative.");
+  if (batch > 0 && n_rows > 0 && k > 0 && Y == nullptr)
+    return fail(MSX_EINVAL, std::string(op) + " Y is NULL.");
+  if (batch > 0 && n_cols > 0 && k > 0 && nnz > 0 && X == nullptr)
+    return fail(MSX_EINVAL, std::string(op) + " X is NULL.");
+  if (batch == 0 || n_rows == 0 || k == 0) return MSX_OK;
+  const int workers = n_threads > 0 ? n_threads : cpu::worker_count();
+  return guarded(op, [&] {
+    switch (vt) {
+    case MSX_F32: batched_vt<cpu::F32>(it, n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers); break;
+    case MSX_F16: batched_vt<cpu::F16>(it, n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers); break;
+    case MSX_BF16: batched_vt<cpu::BF16>(it, n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers); break;
+    case MSX_C64: batched_vt<cpu::C64>(it, n_rows, n_cols, batch, k, data, indices, indptr, X, Y, workers); break;
+    }
+  });
+}
+
+}  // namespace
+
+extern "C" msx_status msx_csr_batched_spmv_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                               int64_t n_cols, int64_t nnz, const void *data,
+                                               const void *indices, const void *indptr,
+                                               int64_t batch, const void *X, void *Y,
+                                               int n_threads) {
+  return batched_cpu("csr_batched_matvec", vt, it, n_rows, n_cols, nnz, data, indices, indptr,
+                     batch, 1, X, Y, n_threads);
+}
+
+extern "C" msx_status msx_csr_batched_spmm_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                               int64_t n_cols, int64_t nnz, const void *data,
+                                               const void *indices, const void *indptr,
+                                               int64_t batch, int64_t k, const void *X, void *Y,
+                                               int n_threads) {
+  return batched_cpu("csr_batched_matmul", vt, it, n_rows, n_cols, nnz, data, indices, indptr,
+                     batch, k, X, Y, n_threads);
 }

@@ -27,6 +27,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kMaxGrid = 1u << 20;
+constexpr int64_t kMaxBatchGrid = 65535;  // batches per launch (grid y extent)
 constexpr int kUnroll = 4;
 
 template <class S, int CW>
@@ -66,9 +67,12 @@ __global__ void __launch_bounds__(kThreads)
     spmm_rows(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
               const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
               int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
-              int64_t nnz, int64_t n_cols, int64_t k, int LR, int64_t n_col_tiles) {
+              int64_t nnz, int64_t n_cols, int64_t k, int LR, int64_t n_col_tiles, int64_t x_batch,
+              int64_t y_batch) {
   using S = typename V::Storage;
   using A = typename V::Acc;
+  X += blockIdx.y * x_batch;  // batch blockIdx.y (one for a plain SpMM)
+  Y += blockIdx.y * y_batch;
   const int rows_per_group = kThreads / LR;
   const int g = threadIdx.x / LR;
   const int l = threadIdx.x % LR;
@@ -136,9 +140,11 @@ __global__ void __launch_bounds__(kThreads)
     spmm_linetile(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                   const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
                   int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
-                  int64_t nnz, int64_t n_cols, int G) {
+                  int64_t nnz, int64_t n_cols, int G, int64_t x_batch, int64_t y_batch) {
   using S = typename V::Storage;
   using A = typename V::Acc;
+  X += blockIdx.y * x_batch;
+  Y += blockIdx.y * y_batch;
   constexpr int LR = 128 / (CW * static_cast<int>(sizeof(S)));  // lanes per row (one line)
   constexpr int kRowsPerGroup = kThreads / LR;
   const int xcd = static_cast<int>(blockIdx.x % kNumXcd);
@@ -206,8 +212,9 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 template <class V, class I>
 msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data_v,
-                      const void *indices_v, const void *indptr_v, int64_t k, const void *X_v,
-                      int64_t ldx, void *Y_v, int64_t ldy, hipStream_t stream) {
+                      const void *indices_v, const void *indptr_v, int64_t batch, int64_t k,
+                      const void *X_v, int64_t x_batch, int64_t ldx, void *Y_v, int64_t y_batch,
+                      int64_t ldy, hipStream_t stream) {
   using S = typename V::Storage;
   constexpr int CWV = static_cast<int>(16 / sizeof(S));
   const auto *data = static_cast<const S *>(data_v);
@@ -215,8 +222,8 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   const auto *indptr = static_cast<const I *>(indptr_v);
   const auto *X = static_cast<const S *>(X_v);
   auto *Y = static_cast<S *>(Y_v);
-  const bool vec = (k % CWV) == 0 && (ldx % CWV) == 0 && (ldy % CWV) == 0 && aligned16(X) &&
-                   aligned16(Y);
+  const bool vec = (k % CWV) == 0 && (ldx % CWV) == 0 && (ldy % CWV) == 0 &&
+                   (x_batch % CWV) == 0 && (y_batch % CWV) == 0 && aligned16(X) && aligned16(Y);
   // X rows of exactly two cache lines (k = 64 float32, 128 float16/bfloat16,
   // 32 complex64): one line per group of four XCDs.  Measured on the 3D
   // Poisson matrix at k = 64: 468 us against 493 us for spmm_rows; at four or
@@ -228,10 +235,15 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
     const int64_t n_rt = (n_rows + kThreads / LRT - 1) / (kThreads / LRT);
     const int64_t per_group = (n_rt + (kNumXcd / G) - 1) / (kNumXcd / G);
     const int64_t slots = std::max<int64_t>(1, std::min<int64_t>(per_group, kMaxGrid / kNumXcd));
-    hipLaunchKernelGGL((spmm_linetile<V, I, CWV>), dim3(static_cast<uint32_t>(slots * kNumXcd)),
-                       dim3(kThreads), 0, stream, data, indices, indptr, X, ldx, Y, ldy, n_rows, nnz,
-                       n_cols, G);
-    MSX_HIP_TRY(hipGetLastError());
+    // The grid's x extent is a multiple of 8, so workgroup (x, b) still runs
+    // on XCD x % 8 when batches are stacked along y.
+    for (int64_t b0 = 0; b0 < batch; b0 += kMaxBatchGrid) {
+      const uint32_t nb = static_cast<uint32_t>(std::min<int64_t>(batch - b0, kMaxBatchGrid));
+      hipLaunchKernelGGL((spmm_linetile<V, I, CWV>), dim3(static_cast<uint32_t>(slots * kNumXcd), nb),
+                         dim3(kThreads), 0, stream, data, indices, indptr, X + b0 * x_batch, ldx,
+                         Y + b0 * y_batch, ldy, n_rows, nnz, n_cols, G, x_batch, y_batch);
+      MSX_HIP_TRY(hipGetLastError());
+    }
     return MSX_OK;
   }
   const int CW = vec ? CWV : 1;
@@ -242,45 +254,66 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   const int64_t rows_per_group = kThreads / LR;
   const int64_t tiles = ((n_rows + rows_per_group - 1) / rows_per_group) * n_col_tiles;
   const uint32_t grid = static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(tiles, kMaxGrid)));
-  if (vec) {
-    hipLaunchKernelGGL((spmm_rows<V, I, CWV>), dim3(grid), dim3(kThreads), 0, stream, data,
-                       indices, indptr, X, ldx, Y, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles);
-  } else {
-    hipLaunchKernelGGL((spmm_rows<V, I, 1>), dim3(grid), dim3(kThreads), 0, stream, data, indices,
-                       indptr, X, ldx, Y, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles);
+  for (int64_t b0 = 0; b0 < batch; b0 += kMaxBatchGrid) {
+    const uint32_t nb = static_cast<uint32_t>(std::min<int64_t>(batch - b0, kMaxBatchGrid));
+    const S *Xb = X + b0 * x_batch;
+    S *Yb = Y + b0 * y_batch;
+    if (vec) {
+      hipLaunchKernelGGL((spmm_rows<V, I, CWV>), dim3(grid, nb), dim3(kThreads), 0, stream, data,
+                         indices, indptr, Xb, ldx, Yb, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles,
+                         x_batch, y_batch);
+    } else {
+      hipLaunchKernelGGL((spmm_rows<V, I, 1>), dim3(grid, nb), dim3(kThreads), 0, stream, data,
+                         indices, indptr, Xb, ldx, Yb, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles,
+                         x_batch, y_batch);
+    }
+    MSX_HIP_TRY(hipGetLastError());
   }
-  MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
 }
 
 template <class V>
 msx_status spmm_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
-                   const void *indices, const void *indptr, int64_t k, const void *X, int64_t ldx,
-                   void *Y, int64_t ldy, hipStream_t stream) {
+                   const void *indices, const void *indptr, int64_t batch, int64_t k, const void *X,
+                   int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
+                   hipStream_t stream) {
   if (it == MSX_I32)
-    return spmm_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
-                                  stream);
-  return spmm_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
-                                stream);
+    return spmm_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
+                                  ldx, Y, y_batch, ldy, stream);
+  return spmm_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
+                                ldx, Y, y_batch, ldy, stream);
 }
 
 }  // namespace
 
+msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                               int64_t nnz, const void *data, const void *indices,
+                               const void *indptr, int64_t batch, int64_t k, const void *X,
+                               int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
+                               hipStream_t stream) {
+  if (batch <= 0 || n_rows <= 0 || k <= 0) return MSX_OK;
+  switch (vt) {
+  case MSX_F32:
+    return spmm_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, stream);
+  case MSX_F16:
+    return spmm_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, stream);
+  case MSX_BF16:
+    return spmm_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                         Y, y_batch, ldy, stream);
+  case MSX_C64:
+    return spmm_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, stream);
+  }
+  return fail(MSX_ETYPE, "csr_matmul unsupported value dtype.");
+}
+
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,
                        const void *X, int64_t ldx, void *Y, int64_t ldy, hipStream_t stream) {
-  switch (vt) {
-  case MSX_F32:
-    return spmm_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
-  case MSX_F16:
-    return spmm_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
-  case MSX_BF16:
-    return spmm_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
-                         stream);
-  case MSX_C64:
-    return spmm_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, stream);
-  }
-  return fail(MSX_ETYPE, "csr_matmul unsupported value dtype.");
+  return launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, k, X, 0, ldx, Y,
+                             0, ldy, stream);
 }
 
 }  // namespace msx

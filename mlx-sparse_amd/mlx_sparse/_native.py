@@ -23,6 +23,16 @@ def csr_matmul(data, indices, indptr, rhs, shape: Shape2D, plan=None) -> torch.T
     return extension().csr_matmul(data, indices, indptr, rhs, shape[0], shape[1], plan=plan)
 
 
+def csr_batched_matvec(data, indices, indptr, rhs, shape: Shape2D) -> torch.Tensor:
+    """(reference: mlx_sparse/_native.py:218-228)"""
+    return extension().csr_batched_matvec(data, indices, indptr, rhs, shape[0], shape[1])
+
+
+def csr_batched_matmul(data, indices, indptr, rhs, shape: Shape2D) -> torch.Tensor:
+    """(reference: mlx_sparse/_native.py:325-335)"""
+    return extension().csr_batched_matmul(data, indices, indptr, rhs, shape[0], shape[1])
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

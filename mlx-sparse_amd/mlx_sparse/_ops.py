@@ -60,9 +60,8 @@ def _csr_matmul_rank2(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
 
 
 def _csr_matmul_batched(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
-    """``out[b] = A @ rhs[b]`` for every batch index, as ONE SpMM: the batch
-    is folded into the RHS columns, ``(B, n, k) -> (n, B*k)``, so the
-    matrix is streamed once instead of B times."""
+    """``out[b] = A @ rhs[b]`` over the flattened leading dimensions, through
+    the native batched SpMM (reference: mlx_sparse/_ops.py:986-1000)."""
     if a.data.dtype != rhs.dtype:
         raise TypeError(
             "csr_matmul requires sparse data and RHS to have the same dtype, "
@@ -70,10 +69,10 @@ def _csr_matmul_batched(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
         )
     batch_shape = tuple(int(d) for d in rhs.shape[:-2])
     k = int(rhs.shape[-1])
-    b = _prod(batch_shape)
-    folded = rhs.reshape(b, a.shape[1], k).permute(1, 0, 2).reshape(a.shape[1], b * k)
-    out = _csr_matmul_rank2(a, folded.contiguous())
-    return out.reshape(a.shape[0], b, k).permute(1, 0, 2).reshape(*batch_shape, a.shape[0], k)
+    flat = rhs.reshape(_prod(batch_shape), a.shape[1], k)
+    data, indices, indptr = a.buffers(rhs.device)
+    out = _native.csr_batched_matmul(data, indices, indptr, flat, a.shape)
+    return out.reshape(*batch_shape, a.shape[0], k)
 
 
 def csr_matmul(a: CSRArray, rhs) -> torch.Tensor:
@@ -101,18 +100,53 @@ def csr_matmul(a: CSRArray, rhs) -> torch.Tensor:
 
 
 def csr_batched_matvec(a: CSRArray, rhs) -> torch.Tensor:
-    """``out[..., :] = A @ rhs[..., :]`` for a batch of vectors
-    ``(..., n_cols)`` (reference: mlx_sparse/_ops.py csr_batched_matvec),
-    computed as one SpMM on the transposed batch."""
+    """Multiply a CSR sparse matrix by a batch of dense vectors: ``Y[b] = A @
+    X[b]`` for ``rhs`` of shape ``(..., n_cols)``; returns ``(..., n_rows)``
+    (reference: mlx_sparse/_ops.py:821-855).  Each output is summed from zero
+    in stored order, as the reference's batched kernels sum it.
+
+    Raises:
+        TypeError: ``a`` is not a CSRArray or the dtypes differ.
+        ValueError: ``rhs`` has rank < 2 or the wrong vector length.
+    """
     if not isinstance(a, CSRArray):
         raise TypeError(f"csr_batched_matvec expects CSRArray, got {type(a).__name__}.")
     rhs = ensure_array(rhs, device=default_torch_device())
-    if rhs.ndim < 1 or rhs.shape[-1] != a.shape[1]:
+    if rhs.ndim < 2:
         raise ValueError(
-            f"csr_batched_matvec RHS has sparse dimension {rhs.shape[-1] if rhs.ndim else None}, "
+            f"csr_batched_matvec expects rank-2 or higher RHS, got {tuple(rhs.shape)}."
+        )
+    if rhs.shape[-1] != a.shape[1]:
+        raise ValueError(
+            f"csr_batched_matvec RHS has vector dimension {rhs.shape[-1]}, "
             f"but sparse n_cols={a.shape[1]}."
+        )
+    if a.data.dtype != rhs.dtype:
+        raise TypeError(
+            "csr_batched_matvec requires sparse data and RHS to have the same dtype, "
+            f"got {a.data.dtype} and {rhs.dtype}."
         )
     batch_shape = tuple(int(d) for d in rhs.shape[:-1])
     flat = rhs.reshape(_prod(batch_shape), a.shape[1])
-    out = _csr_matmul_rank2(a, flat.transpose(0, 1).contiguous())
-    return out.transpose(0, 1).reshape(*batch_shape, a.shape[0])
+    data, indices, indptr = a.buffers(rhs.device)
+    out = _native.csr_batched_matvec(data, indices, indptr, flat, a.shape)
+    return out.reshape(*batch_shape, a.shape[0])
+
+
+def csr_batched_matmul(a: CSRArray, rhs) -> torch.Tensor:
+    """Multiply a CSR sparse matrix by a batch of dense matrices: ``rhs`` of
+    shape ``(..., n_cols, k)`` gives ``(..., n_rows, k)`` (reference:
+    mlx_sparse/_ops.py:1097-1115).  For rank-2 ``rhs`` use ``csr_matmul``."""
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_batched_matmul expects CSRArray, got {type(a).__name__}.")
+    rhs = ensure_array(rhs, device=default_torch_device())
+    if rhs.ndim < 3:
+        raise ValueError(
+            f"csr_batched_matmul expects rank-3 or higher RHS, got {tuple(rhs.shape)}."
+        )
+    if rhs.shape[-2] != a.shape[1]:
+        raise ValueError(
+            f"csr_batched_matmul RHS has sparse dimension {rhs.shape[-2]}, "
+            f"but sparse n_cols={a.shape[1]}."
+        )
+    return _csr_matmul_batched(a, rhs)

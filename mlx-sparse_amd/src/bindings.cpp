@@ -2,7 +2,8 @@
 //
 // Mirrors the reference nanobind module's entry points for this path
 // (reference: src/bindings.cpp:279-295 `_compiled_capabilities`,
-// :874-883 `csr_matvec`, :965-975 `csr_matmul`): same names and argument
+// :874-883 `csr_matvec`, :905-915 `csr_batched_matvec`, :965-975
+// `csr_matmul`, :998-1008 `csr_batched_matmul`): same names and argument
 // order (data, indices, indptr, x | rhs, n_rows, n_cols).  Arrays are torch
 // tensors; the module reads their pointer, dtype, shape, strides and device
 // through the tensor's Python attributes, so no torch headers are compiled
@@ -20,6 +21,8 @@
 #include "common/array_view.h"
 #include "common/validate.h"
 #include "msx_sparse.h"
+#include "sparse/csr_batched_matmul/csr_batched_matmul.h"
+#include "sparse/csr_batched_matvec/csr_batched_matvec.h"
 #include "sparse/csr_matmul/csr_matmul.h"
 #include "sparse/csr_matvec/csr_matvec.h"
 
@@ -65,7 +68,7 @@ ArrayView view_of(py::handle t) {
   v.dtype_name = dtype_name(t.attr("dtype"));
   v.dtype = dtype_of(v.dtype_name);
   v.ndim = t.attr("dim")().cast<int>();
-  if (v.ndim <= 2) {
+  if (v.ndim <= 3) {
     auto shape = t.attr("shape").cast<std::vector<int64_t>>();
     auto strides = t.attr("stride")().cast<std::vector<int64_t>>();
     for (int i = 0; i < v.ndim; ++i) {
@@ -206,6 +209,49 @@ py::object csr_matmul(py::handle data_o, py::handle indices_o, py::handle indptr
   return out;
 }
 
+py::object csr_batched_matvec(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                              py::handle rhs_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), rhs = contiguous(rhs_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr),
+                  vr = view_of(rhs);
+  if (vr.ndim != 2) msx::require_rank(vr, 2, "csr_batched_matvec rhs");
+  py::object out = empty_like_out(vd, data, py::make_tuple(vr.shape[0], std::max<int64_t>(n_rows, 0)));
+  const ArrayView vo = view_of(out);
+  msx::ExecContext ctx;
+  ctx.n_threads = n_threads;
+  ctx.stream = vd.device >= 0 ? stream_for(vd.device) : nullptr;
+  if (vd.device >= 0) {
+    msx::csr_batched_matvec(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_batched_matvec(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
+py::object csr_batched_matmul(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                              py::handle rhs_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), rhs = contiguous(rhs_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr),
+                  vr = view_of(rhs);
+  if (vr.ndim != 3) msx::require_rank(vr, 3, "csr_batched_matmul rhs");
+  py::object out = empty_like_out(
+      vd, data, py::make_tuple(vr.shape[0], std::max<int64_t>(n_rows, 0), vr.shape[2]));
+  const ArrayView vo = view_of(out);
+  msx::ExecContext ctx;
+  ctx.n_threads = n_threads;
+  ctx.stream = vd.device >= 0 ? stream_for(vd.device) : nullptr;
+  if (vd.device >= 0) {
+    msx::csr_batched_matmul(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_batched_matmul(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
 py::dict plan_info(const Plan &plan) {
   msx_plan_info info{};
   msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_info");
@@ -291,6 +337,13 @@ PYBIND11_MODULE(_ext, m) {
   m.def("csr_matmul", &csr_matmul, py::arg("data"), py::arg("indices"), py::arg("indptr"),
         py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"), py::arg("plan") = py::none(),
         py::arg("n_threads") = 0, "Multiply CSR buffers by a dense matrix.");
+  m.def("csr_batched_matvec", &csr_batched_matvec, py::arg("data"), py::arg("indices"),
+        py::arg("indptr"), py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0, "Multiply CSR buffers by a batch of dense vectors (batch, n_cols).");
+  m.def("csr_batched_matmul", &csr_batched_matmul, py::arg("data"), py::arg("indices"),
+        py::arg("indptr"), py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0,
+        "Multiply CSR buffers by a batch of dense matrices (batch, n_cols, k).");
   m.def("cpu_worker_count", &msx_cpu_worker_count, "Resolved CPU worker count.");
   m.def(
       "cpu_ranges",

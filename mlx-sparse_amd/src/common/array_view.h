@@ -15,19 +15,22 @@ struct ArrayView {
   void *ptr = nullptr;
   DType dtype = DType::Other;
   std::string dtype_name;  // framework spelling, for error texts
-  int ndim = 0;
-  int64_t shape[2] = {0, 0};
-  int64_t strides[2] = {1, 1};  // in elements
-  int device = -1;              // -1: host memory; >= 0: HIP device ordinal
+  int ndim = 0;                     // the layer handles ranks 0..3
+  int64_t shape[3] = {0, 0, 0};
+  int64_t strides[3] = {1, 1, 1};  // in elements
+  int device = -1;                 // -1: host memory; >= 0: HIP device ordinal
 
   int64_t size() const {
     int64_t s = 1;
-    for (int i = 0; i < ndim && i < 2; ++i) s *= shape[i];
+    for (int i = 0; i < ndim && i < 3; ++i) s *= shape[i];
     return ndim == 0 ? 1 : s;
   }
   bool contiguous() const {
-    if (ndim == 1) return shape[0] <= 1 || strides[0] == 1;
-    if (ndim == 2) return (shape[1] <= 1 || strides[1] == 1) && (shape[0] <= 1 || strides[0] == shape[1]);
+    int64_t expect = 1;
+    for (int i = ndim - 1; i >= 0; --i) {
+      if (shape[i] > 1 && strides[i] != expect) return false;
+      expect *= shape[i];
+    }
     return true;
   }
 };

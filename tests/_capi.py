@@ -58,6 +58,13 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_plan_export_panels.argtypes = [vp, vp, vp, vp]
         L.msx_csr_spmv.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
         L.msx_csr_spmm.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp, i64, vp, vp]
+        L.msx_csr_batched_spmv.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp,
+                                           i64, vp]
+        L.msx_csr_batched_spmm.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, i64, vp, i64,
+                                           i64, vp, i64, i64, vp]
+        L.msx_csr_batched_spmv_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp, ci]
+        L.msx_csr_batched_spmm_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, i64, vp,
+                                               vp, ci]
         L.msx_csr_spmv_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
         L.msx_csr_spmm_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp, ci]
         L.msx_cpu_worker_count.restype = ci
@@ -65,7 +72,9 @@ def lib() -> ctypes.CDLL:
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
                      "msx_csr_plan_destroy",
                      "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_plan_export_panels",
-                     "msx_csr_spmv", "msx_csr_spmm",
+                     "msx_csr_spmv", "msx_csr_spmm", "msx_csr_batched_spmv",
+                     "msx_csr_batched_spmm", "msx_csr_batched_spmv_cpu",
+                     "msx_csr_batched_spmm_cpu",
                      "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges"):
             getattr(L, name).restype = ci
         _lib = L
@@ -156,4 +165,32 @@ def spmm(data, indices, indptr, X, n_rows, n_cols, Y=None, ldx=None, ldy=None):
                             ldy if ldy is not None else Y.stride(0), None, _stream())
     if st != OK:
         raise RuntimeError(f"msx_csr_spmm: {st} {last_error()}")
+    return Y
+
+
+def batched_spmv(data, indices, indptr, X, n_rows, n_cols, Y=None, ldx=None, ldy=None):
+    """X: (batch, >= n_cols) rows of stride ldx; Y: (batch, >= n_rows)."""
+    batch = X.shape[0]
+    if Y is None:
+        Y = torch.empty((batch, n_rows), dtype=data.dtype, device=data.device)
+    st = lib().msx_csr_batched_spmv(VT[data.dtype], IT[indices.dtype], n_rows, n_cols,
+                                    data.numel(), _p(data), _p(indices), _p(indptr), batch,
+                                    _p(X), ldx if ldx is not None else X.stride(0), _p(Y),
+                                    ldy if ldy is not None else Y.stride(0), _stream())
+    if st != OK:
+        raise RuntimeError(f"msx_csr_batched_spmv: {st} {last_error()}")
+    return Y
+
+
+def batched_spmm(data, indices, indptr, X, n_rows, n_cols, Y=None):
+    """X: (batch, n_cols, k) with any batch/row strides of a torch view."""
+    batch, _, k = X.shape
+    if Y is None:
+        Y = torch.empty((batch, n_rows, k), dtype=data.dtype, device=data.device)
+    st = lib().msx_csr_batched_spmm(VT[data.dtype], IT[indices.dtype], n_rows, n_cols,
+                                    data.numel(), _p(data), _p(indices), _p(indptr), batch, k,
+                                    _p(X), X.stride(0), X.stride(1), _p(Y), Y.stride(0),
+                                    Y.stride(1), _stream())
+    if st != OK:
+        raise RuntimeError(f"msx_csr_batched_spmm: {st} {last_error()}")
     return Y

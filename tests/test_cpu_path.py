@@ -224,3 +224,75 @@ def test_is_available_and_no_fallback(ms, monkeypatch):
     monkeypatch.setattr(loader, "_ERROR", ImportError("simulated missing build"))
     with pytest.raises(RuntimeError, match="not built"):
         loader.extension()
+
+
+# -- batched right-hand sides (reference: src/sparse/csr_batched_matvec,
+#    src/sparse/csr_batched_matmul) -------------------------------------------------
+
+def _batched_want(oracle, data, indices, indptr, X, n_rows, vtype, k=None):
+    """Every output summed from zero in stored order: column b of one SpMM
+    over the transposed batch (vectors), or one SpMM per batch (matrices)."""
+    if k is None:
+        return np.ascontiguousarray(
+            oracle.csr_matmul(data, indices, indptr, np.ascontiguousarray(X.T), n_rows, vtype=vtype).T)
+    return np.stack([oracle.csr_matmul(data, indices, indptr, X[b], n_rows, vtype=vtype)
+                     for b in range(X.shape[0])])
+
+
+@pytest.mark.parametrize("vtype", ["float32", "float16", "bfloat16", "complex64"])
+@pytest.mark.parametrize("threads", [1, 5])
+def test_batched_native_cpu_equals_oracle(cpu, oracle, vtype, threads):
+    import _capi
+    from _util import storage
+
+    rng = np.random.default_rng(21)
+    n_rows, n_cols = 300, 250
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, np.int32)
+    vals = rng.standard_normal(nnz) + (1j * rng.standard_normal(nnz) if vtype == "complex64" else 0)
+    data = storage(vals, vtype)
+    for batch, k in ((1, None), (6, None), (3, 5), (4, 1)):
+        shape = (batch, n_cols) if k is None else (batch, n_cols, k)
+        xv = rng.standard_normal(shape) + (1j * rng.standard_normal(shape) if vtype == "complex64" else 0)
+        X = storage(xv, vtype)
+        want = _batched_want(oracle, data, indices, indptr, X, n_rows, vtype, k)
+        got = np.empty_like(want)
+        L, T = _capi.lib(), {"float32": 0, "float16": 1, "bfloat16": 2, "complex64": 3}[vtype]
+        ptr = lambda a: a.ctypes.data
+        if k is None:
+            st = L.msx_csr_batched_spmv_cpu(T, 0, n_rows, n_cols, nnz, ptr(data), ptr(indices),
+                                            ptr(indptr), batch, ptr(X), ptr(got), threads)
+        else:
+            st = L.msx_csr_batched_spmm_cpu(T, 0, n_rows, n_cols, nnz, ptr(data), ptr(indices),
+                                            ptr(indptr), batch, k, ptr(X), ptr(got), threads)
+        assert st == _capi.OK, _capi.last_error()
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_batched_api_on_cpu(cpu, oracle):
+    rng = np.random.default_rng(22)
+    indices, indptr, nnz = _random_csr(rng, 120, 90, np.int64)
+    data = rng.standard_normal(nnz).astype(np.float32)
+    A = cpu.csr_array((data, indices, indptr), shape=(120, 90))
+    X = rng.standard_normal((2, 3, 90)).astype(np.float32)
+    got = cpu.csr_batched_matvec(A, torch.from_numpy(X)).numpy()
+    assert got.shape == (2, 3, 120)
+    want = _batched_want(oracle, data, indices, indptr, X.reshape(6, 90), 120, "float32")
+    np.testing.assert_array_equal(got.reshape(6, 120), want)
+    M = rng.standard_normal((2, 2, 90, 4)).astype(np.float32)
+    got = cpu.csr_batched_matmul(A, torch.from_numpy(M)).numpy()
+    assert got.shape == (2, 2, 120, 4)
+    np.testing.assert_array_equal(got.reshape(4, 120, 4),
+                                  _batched_want(oracle, data, indices, indptr, M.reshape(4, 90, 4),
+                                                120, "float32", k=4))
+    np.testing.assert_array_equal((A @ torch.from_numpy(M)).numpy(), got)  # rank-4 csr_matmul
+    # reference error texts (mlx_sparse/_ops.py:821-855, :1097-1115)
+    with pytest.raises(ValueError, match="rank-2 or higher"):
+        cpu.csr_batched_matvec(A, torch.zeros(90))
+    with pytest.raises(ValueError, match="vector dimension 89"):
+        cpu.csr_batched_matvec(A, torch.zeros(2, 89))
+    with pytest.raises(TypeError, match="same dtype"):
+        cpu.csr_batched_matvec(A, torch.zeros(2, 90, dtype=torch.float16))
+    with pytest.raises(ValueError, match="rank-3 or higher"):
+        cpu.csr_batched_matmul(A, torch.zeros(90, 2))
+    with pytest.raises(ValueError, match="sparse dimension 91"):
+        cpu.csr_batched_matmul(A, torch.zeros(2, 91, 2))
