@@ -59,6 +59,84 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Narrow transposes for batches of at most kNarrow vectors (padded width
+// kpad, a multiple of the 16-byte vector): one thread per column of the
+// batch, 16-byte accesses on the transposed side, one coalesced access per
+// vector on the other - no LDS, every load and store fully used.
+constexpr int kNarrow = 32;
+
+template <class T>
+union Vec16 {
+  uint4 u;
+  T e[16 / sizeof(T)];
+};
+
+// Xt[c * kpad + b] = X[b * ldx + c] (b < batch), 0 for batch <= b < kpad.
+template <class T>
+__global__ void __launch_bounds__(kThreads)
+    gather_columns(const T *__restrict__ X, int64_t batch, int64_t kpad, int64_t n, int64_t ldx,
+                   T *__restrict__ Xt) {
+  constexpr int E = 16 / sizeof(T);
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < n;
+       c += static_cast<int64_t>(gridDim.x) * kThreads) {
+    uint4 *out = reinterpret_cast<uint4 *>(Xt + c * kpad);
+    for (int64_t q = 0; q < kpad / E; ++q) {
+      Vec16<T> v;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int64_t b = q * E + e;
+        v.e[e] = b < batch ? X[b * ldx + c] : T{};
+      }
+      out[q] = v.u;
+    }
+  }
+}
+
+// Y[b * ldy + r] = Yt[r * kpad + b] for b < batch.
+template <class T>
+__global__ void __launch_bounds__(kThreads)
+    scatter_rows(const T *__restrict__ Yt, int64_t batch, int64_t kpad, int64_t n, int64_t ldy,
+                 T *__restrict__ Y) {
+  constexpr int E = 16 / sizeof(T);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n;
+       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint4 *in = reinterpret_cast<const uint4 *>(Yt + r * kpad);
+    for (int64_t q = 0; q < kpad / E; ++q) {
+      Vec16<T> v;
+      v.u = in[q];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int64_t b = q * E + e;
+        if (b < batch) Y[b * ldy + r] = v.e[e];
+      }
+    }
+  }
+}
+
+template <class T>
+msx_status narrow_t(bool to_columns, const void *in, int64_t batch, int64_t kpad, int64_t n,
+                    int64_t ld, void *out, hipStream_t stream) {
+  if (n == 0) return MSX_OK;
+  const uint32_t grid = static_cast<uint32_t>(std::min((n + kThreads - 1) / kThreads, kMaxGrid));
+  if (to_columns)
+    hipLaunchKernelGGL((gather_columns<T>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const T *>(in), batch, kpad, n, ld, static_cast<T *>(out));
+  else
+    hipLaunchKernelGGL((scatter_rows<T>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const T *>(in), batch, kpad, n, ld, static_cast<T *>(out));
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+msx_status narrow(msx_vtype vt, bool to_columns, const void *in, int64_t batch, int64_t kpad,
+                  int64_t n, int64_t ld, void *out, hipStream_t stream) {
+  switch (value_bytes(vt)) {
+  case 2: return narrow_t<uint16_t>(to_columns, in, batch, kpad, n, ld, out, stream);
+  case 4: return narrow_t<uint32_t>(to_columns, in, batch, kpad, n, ld, out, stream);
+  default: return narrow_t<uint64_t>(to_columns, in, batch, kpad, n, ld, out, stream);
+  }
+}
+
 template <class T>
 msx_status transpose_t(const void *in, int64_t rows, int64_t rows_pad, int64_t cols, int64_t ldi,
                        void *out, int64_t ldo, hipStream_t stream) {
@@ -129,11 +207,15 @@ extern "C" msx_status msx_csr_batched_spmv(msx_vtype vt, msx_itype it, int64_t n
   char *scratch = nullptr;
   MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&scratch), bx + by, stream));
   void *Xt = scratch, *Yt = scratch + bx;
-  st = transpose(vt, X, batch, kpad, n_cols, ldx, Xt, kpad, stream);
+  const bool thin = kpad <= kNarrow;
+  st = thin ? narrow(vt, true, X, batch, kpad, n_cols, ldx, Xt, stream)
+            : transpose(vt, X, batch, kpad, n_cols, ldx, Xt, kpad, stream);
   if (st == MSX_OK)
     st = launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, kpad, Xt, 0,
                              kpad, Yt, 0, kpad, stream);
-  if (st == MSX_OK) st = transpose(vt, Yt, n_rows, n_rows, batch, kpad, Y, ldy, stream);
+  if (st == MSX_OK)
+    st = thin ? narrow(vt, false, Yt, batch, kpad, n_rows, ldy, Y, stream)
+              : transpose(vt, Yt, n_rows, n_rows, batch, kpad, Y, ldy, stream);
   const hipError_t e = hipFreeAsync(scratch, stream);
   if (st == MSX_OK && e != hipSuccess) return hip_fail(e, "csr_batched_matvec scratch release");
   return st;
