@@ -279,6 +279,107 @@ msx_status msx_csr_batched_spmm(msx_vtype vt, msx_itype it, int64_t n_rows,
                                 int64_t y_batch, int64_t ldy, void *stream);
 
 /*
+ * CSR of A^T (shape n_cols x n_rows, the CSC of A) into caller buffers:
+ * t_data and t_indices (nnz entries; t_indices holds row ids) and t_indptr
+ * (n_cols + 1).  Each column lists its entries by increasing row, as the
+ * reference's counting sort does.  Values with a column outside [0, n_cols)
+ * are left out: t_indptr[n_cols] counts the rest, and entries past it are
+ * unspecified.  Device: a stable radix sort, asynchronous on `stream`
+ * (scratch from its stream-ordered allocator); nnz < 2^31 - 1.
+ *
+ * Replaces CSRTranspose::eval_gpu / eval_cpu (reference:
+ * src/sparse/csr_transpose/csr_transpose.cpp), the structure behind
+ * CSRArray.transpose (mlx_sparse/_csr.py:252-275).
+ */
+msx_status msx_csr_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
+                             int64_t n_cols, int64_t nnz, const void *data,
+                             const void *indices, const void *indptr,
+                             void *t_data, void *t_indices, void *t_indptr,
+                             void *stream);
+msx_status msx_csr_transpose_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                 int64_t n_cols, int64_t nnz, const void *data,
+                                 const void *indices, const void *indptr,
+                                 void *t_data, void *t_indices, void *t_indptr);
+
+/*
+ * y = A^T x (x: n_rows, y: n_cols) and Y = A^T X (X: n_rows x k, row stride
+ * ldx; Y: n_cols x k, row stride ldy), without a transpose: every stored
+ * value adds its product into its column's output with a float atomic, so
+ * the order of additions is not fixed (results agree with a sequential sum
+ * to rounding).  float16/bfloat16 accumulate in float32 scratch.  For a
+ * deterministic result, transpose once (msx_csr_transpose) and multiply
+ * with msx_csr_spmv / msx_csr_spmm.
+ *
+ * Replace CSRMatVecTranspose::eval_gpu and CSRMatMulTranspose::eval_gpu
+ * (reference: src/sparse/csr_matvec_transpose/csr_matvec_transpose.metal:27-49,
+ * src/sparse/csr_matmul_transpose/); the VJP of csr_matvec / csr_matmul
+ * with respect to the dense operand (csr_matvec.cpp:232-259,
+ * csr_matmul.cpp:336-363), with conjugated values for complex64.
+ */
+msx_status msx_csr_spmv_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                  int64_t n_cols, int64_t nnz, const void *data,
+                                  const void *indices, const void *indptr,
+                                  const void *x, void *y, void *stream);
+msx_status msx_csr_spmm_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                  int64_t n_cols, int64_t nnz, const void *data,
+                                  const void *indices, const void *indptr,
+                                  int64_t k, const void *X, int64_t ldx,
+                                  void *Y, int64_t ldy, void *stream);
+
+/*
+ * Host (CPU) transposed products, contiguous operands, the reference's
+ * algorithm: with one worker every output is summed from zero over the rows
+ * in order; with W workers, rows are split by row length into W ranges, each
+ * accumulates its own partial output from zero, and the partials are added
+ * from zero in range order (reference: csr_matvec_transpose.cpp,
+ * csr_matvec_transpose_cpu_impl; csr_matmul_transpose.cpp,
+ * csr_matmul_transpose_cpu_impl).  Results depend on n_threads, as there.
+ */
+msx_status msx_csr_spmv_transpose_cpu(msx_vtype vt, msx_itype it,
+                                      int64_t n_rows, int64_t n_cols,
+                                      int64_t nnz, const void *data,
+                                      const void *indices, const void *indptr,
+                                      const void *x, void *y, int n_threads);
+msx_status msx_csr_spmm_transpose_cpu(msx_vtype vt, msx_itype it,
+                                      int64_t n_rows, int64_t n_cols,
+                                      int64_t nnz, const void *data,
+                                      const void *indices, const void *indptr,
+                                      int64_t k, const void *X, void *Y,
+                                      int n_threads);
+
+/*
+ * Value gradients of y = A x and Y = A X: out[p] = cot[row(p)] * x[col(p)],
+ * one rounding; out[p] = sum_q cot[row(p), q] * X[col(p), q], summed from zero
+ * in q order (cot: n_rows x k, row stride ldc).  Values with a column outside
+ * [0, n_cols) get zero.  For complex64 the caller passes conj(x) / conj(X)
+ * (the Hermitian rule of the reference VJPs).
+ *
+ * Replace csr_matvec_data_vjp and csr_matmul_data_vjp (reference:
+ * src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp,
+ * src/sparse/csr_matmul_data_vjp/csr_matmul_data_vjp.cpp).
+ */
+msx_status msx_csr_spmv_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                 int64_t n_cols, int64_t nnz, const void *indices,
+                                 const void *indptr, const void *x,
+                                 const void *cot, void *out, void *stream);
+msx_status msx_csr_spmm_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                 int64_t n_cols, int64_t nnz, const void *indices,
+                                 const void *indptr, int64_t k, const void *X,
+                                 int64_t ldx, const void *cot, int64_t ldc,
+                                 void *out, void *stream);
+msx_status msx_csr_spmv_data_vjp_cpu(msx_vtype vt, msx_itype it,
+                                     int64_t n_rows, int64_t n_cols,
+                                     int64_t nnz, const void *indices,
+                                     const void *indptr, const void *x,
+                                     const void *cot, void *out, int n_threads);
+msx_status msx_csr_spmm_data_vjp_cpu(msx_vtype vt, msx_itype it,
+                                     int64_t n_rows, int64_t n_cols,
+                                     int64_t nnz, const void *indices,
+                                     const void *indptr, int64_t k,
+                                     const void *X, const void *cot, void *out,
+                                     int n_threads);
+
+/*
  * Host (CPU) SpMV with host pointers, the `use_cpu()` device: rows are summed
  * sequentially in stored order, rows are split over `n_threads` std::threads
  * in nnz-balanced contiguous ranges (n_threads <= 0: the resolved worker

@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <exception>
 #include <limits>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -368,6 +369,132 @@ void batched(int64_t n, int64_t n_cols, int64_t batch, int64_t k, const void *da
   parallel_for(ranges, body);
 }
 
+// A^T X (k = 1: A^T x) as the reference computes it: serially, each output
+// from zero over the rows in order; with several workers, per-partition
+// partial outputs (rows split by row length) added from zero in partition
+// order.  Columns outside [0, n_cols) add nothing.
+template <class V, class I>
+void transpose_product(int64_t n_rows, int64_t n_cols, int64_t k, const void *data,
+                       const void *indices, const void *indptr, const void *X, void *Y,
+                       int workers) {
+  const auto *d = static_cast<const typename V::S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *xv = static_cast<const typename V::S *>(X);
+  auto *yv = static_cast<typename V::S *>(Y);
+  using A = typename V::A;
+  const int64_t out_size = n_cols * k;
+  auto rows_into = [&](A *acc, Range r) {
+    for (int64_t row = r.begin; row < r.end; ++row) {
+      const typename V::S *xr = xv + row * k;
+      for (int64_t p = at(ip, row); p < at(ip, row + 1); ++p) {
+        const int64_t col = at(ix, p);
+        if (col < 0 || col >= n_cols) continue;
+        for (int64_t q = 0; q < k; ++q) acc[col * k + q] = add(acc[col * k + q], V::mul(d[p], xr[q]));
+      }
+    }
+  };
+  std::vector<Range> ranges;
+  if (workers > 1 && n_rows > 0 && out_size > 0) ranges = ranges_for_work(row_work(ip, n_rows, 1), workers);
+  if (ranges.size() <= 1) {
+    std::vector<A> acc(static_cast<size_t>(out_size), A{});
+    rows_into(acc.data(), {0, n_rows});
+    for (int64_t i = 0; i < out_size; ++i) yv[i] = V::narrow(acc[i]);
+    return;
+  }
+  const size_t parts = ranges.size();
+  std::vector<A> partial(parts * static_cast<size_t>(out_size), A{});
+  std::vector<Range> indexed = ranges;
+  std::vector<std::thread> pool;
+  std::exception_ptr err;
+  std::mutex mu;
+  for (size_t w = 0; w < parts; ++w) {
+    pool.emplace_back([&, w] {
+      try {
+        rows_into(partial.data() + w * out_size, indexed[w]);
+      } catch (...) {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!err) err = std::current_exception();
+      }
+    });
+  }
+  for (auto &t : pool) t.join();
+  if (err) std::rethrow_exception(err);
+  auto reduce = [&](Range r) {
+    for (int64_t i = r.begin; i < r.end; ++i) {
+      A total{};
+      for (size_t w = 0; w < parts; ++w) total = add(total, partial[w * out_size + i]);
+      yv[i] = V::narrow(total);
+    }
+  };
+  const auto out_ranges = equal_ranges(out_size, workers);
+  if (out_ranges.size() <= 1) return reduce({0, out_size});
+  parallel_for(out_ranges, reduce);
+}
+
+// CSR of A^T by a counting sort: column counts, prefix, then the rows in
+// order, so every column lists its entries by increasing row.
+template <class V, class I>
+void transpose_csr(int64_t n_rows, int64_t n_cols, const void *data, const void *indices,
+                   const void *indptr, void *t_data, void *t_indices, void *t_indptr) {
+  const auto *d = static_cast<const typename V::S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  auto *td = static_cast<typename V::S *>(t_data);
+  auto *ti = static_cast<I *>(t_indices);
+  auto *tp = static_cast<I *>(t_indptr);
+  std::vector<int64_t> next(static_cast<size_t>(n_cols) + 1, 0);
+  for (int64_t row = 0; row < n_rows; ++row)
+    for (int64_t p = at(ip, row); p < at(ip, row + 1); ++p) {
+      const int64_t c = at(ix, p);
+      if (c >= 0 && c < n_cols) ++next[c + 1];
+    }
+  for (int64_t c = 0; c < n_cols; ++c) next[c + 1] += next[c];
+  for (int64_t c = 0; c <= n_cols; ++c) tp[c] = static_cast<I>(next[c]);
+  for (int64_t row = 0; row < n_rows; ++row)
+    for (int64_t p = at(ip, row); p < at(ip, row + 1); ++p) {
+      const int64_t c = at(ix, p);
+      if (c < 0 || c >= n_cols) continue;
+      const int64_t slot = next[c]++;
+      td[slot] = d[p];
+      ti[slot] = static_cast<I>(row);
+    }
+}
+
+// Value gradients: g[p] = sum_q cot[row, q] * X[col, q] from zero, or with
+// `single` (the SpMV rule) the one product cot[row] * x[col] - they differ in
+// the sign of a zero product.
+template <class V, class I>
+void data_vjp(int64_t n_rows, int64_t n_cols, int64_t k, bool single, const void *indices,
+              const void *indptr, const void *X, const void *cot, void *out, int workers) {
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *xv = static_cast<const typename V::S *>(X);
+  const auto *cv = static_cast<const typename V::S *>(cot);
+  auto *ov = static_cast<typename V::S *>(out);
+  using A = typename V::A;
+  auto body = [&](Range r) {
+    for (int64_t row = r.begin; row < r.end; ++row) {
+      for (int64_t p = at(ip, row); p < at(ip, row + 1); ++p) {
+        const int64_t col = at(ix, p);
+        A acc{};
+        if (col >= 0 && col < n_cols) {
+          if (single) {
+            acc = V::mul(cv[row], xv[col]);
+          } else {
+            for (int64_t q = 0; q < k; ++q) acc = add(acc, V::mul(cv[row * k + q], xv[col * k + q]));
+          }
+        }
+        ov[p] = V::narrow(acc);
+      }
+    }
+  };
+  if (workers <= 1 || n_rows <= 0) return body({0, n_rows});
+  const auto ranges = ranges_for_work(row_work(ip, n_rows, 1), workers);
+  if (ranges.size() <= 1) return body({0, n_rows});
+  parallel_for(ranges, body);
+}
+
 }  // namespace
 
 int worker_count() {
@@ -546,4 +673,127 @@ extern "C" msx_status msx_csr_batched_spmm_cpu(msx_vtype vt, msx_itype it, int64
                                                int n_threads) {
   return batched_cpu("csr_batched_matmul", vt, it, n_rows, n_cols, nnz, data, indices, indptr,
                      batch, k, X, Y, n_threads);
+}
+
+namespace {
+
+template <template <class, class> class Fn, class... Args>
+void dispatch_cpu(msx_vtype vt, msx_itype it, Args... args) {
+  const bool i64 = it == MSX_I64;
+  switch (vt) {
+  case MSX_F32: i64 ? Fn<cpu::F32, int64_t>::run(args...) : Fn<cpu::F32, int32_t>::run(args...); break;
+  case MSX_F16: i64 ? Fn<cpu::F16, int64_t>::run(args...) : Fn<cpu::F16, int32_t>::run(args...); break;
+  case MSX_BF16: i64 ? Fn<cpu::BF16, int64_t>::run(args...) : Fn<cpu::BF16, int32_t>::run(args...); break;
+  case MSX_C64: i64 ? Fn<cpu::C64, int64_t>::run(args...) : Fn<cpu::C64, int32_t>::run(args...); break;
+  }
+}
+
+template <class V, class I>
+struct TransposeProductCpu {
+  static void run(int64_t n_rows, int64_t n_cols, int64_t k, const void *data, const void *indices,
+                  const void *indptr, const void *X, void *Y, int workers) {
+    cpu::transpose_product<V, I>(n_rows, n_cols, k, data, indices, indptr, X, Y, workers);
+  }
+};
+
+template <class V, class I>
+struct TransposeCsrCpu {
+  static void run(int64_t n_rows, int64_t n_cols, const void *data, const void *indices,
+                  const void *indptr, void *t_data, void *t_indices, void *t_indptr) {
+    cpu::transpose_csr<V, I>(n_rows, n_cols, data, indices, indptr, t_data, t_indices, t_indptr);
+  }
+};
+
+template <class V, class I>
+struct DataVjpCpu {
+  static void run(int64_t n_rows, int64_t n_cols, int64_t k, bool single, const void *indices,
+                  const void *indptr, const void *X, const void *cot, void *out, int workers) {
+    cpu::data_vjp<V, I>(n_rows, n_cols, k, single, indices, indptr, X, cot, out, workers);
+  }
+};
+
+int resolve_workers(int n_threads) { return n_threads > 0 ? n_threads : cpu::worker_count(); }
+
+}  // namespace
+
+extern "C" msx_status msx_csr_transpose_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                            int64_t n_cols, int64_t nnz, const void *data,
+                                            const void *indices, const void *indptr, void *t_data,
+                                            void *t_indices, void *t_indptr) {
+  clear_error();
+  msx_status st = check_cpu("csr_transpose", vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (t_indptr == nullptr || (nnz > 0 && (t_data == nullptr || t_indices == nullptr)))
+    return fail(MSX_EINVAL, "csr_transpose output buffers must be non-NULL.");
+  return guarded("csr_transpose", [&] {
+    dispatch_cpu<TransposeCsrCpu>(vt, it, n_rows, n_cols, data, indices, indptr, t_data, t_indices,
+                                  t_indptr);
+  });
+}
+
+extern "C" msx_status msx_csr_spmv_transpose_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                 int64_t n_cols, int64_t nnz, const void *data,
+                                                 const void *indices, const void *indptr,
+                                                 const void *x, void *y, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matvec_transpose", vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (n_cols > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec_transpose y is NULL.");
+  if (n_rows > 0 && nnz > 0 && x == nullptr) return fail(MSX_EINVAL, "csr_matvec_transpose x is NULL.");
+  const int workers = resolve_workers(n_threads);
+  return guarded("csr_matvec_transpose", [&] {
+    dispatch_cpu<TransposeProductCpu>(vt, it, n_rows, n_cols, int64_t{1}, data, indices, indptr, x,
+                                      y, workers);
+  });
+}
+
+extern "C" msx_status msx_csr_spmm_transpose_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                 int64_t n_cols, int64_t nnz, const void *data,
+                                                 const void *indices, const void *indptr, int64_t k,
+                                                 const void *X, void *Y, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matmul_transpose", vt, it, n_rows, n_cols, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (k < 0) return fail(MSX_EINVAL, "csr_matmul_transpose rhs column count must be non-negative.");
+  if (n_cols > 0 && k > 0 && Y == nullptr) return fail(MSX_EINVAL, "csr_matmul_transpose Y is NULL.");
+  if (n_rows > 0 && nnz > 0 && k > 0 && X == nullptr)
+    return fail(MSX_EINVAL, "csr_matmul_transpose X is NULL.");
+  const int workers = resolve_workers(n_threads);
+  return guarded("csr_matmul_transpose", [&] {
+    dispatch_cpu<TransposeProductCpu>(vt, it, n_rows, n_cols, k, data, indices, indptr, X, Y,
+                                      workers);
+  });
+}
+
+extern "C" msx_status msx_csr_spmv_data_vjp_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                int64_t n_cols, int64_t nnz, const void *indices,
+                                                const void *indptr, const void *x, const void *cot,
+                                                void *out, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matvec_data_vjp", vt, it, n_rows, n_cols, nnz, indices, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (nnz > 0 && (out == nullptr || cot == nullptr || (n_cols > 0 && x == nullptr)))
+    return fail(MSX_EINVAL, "csr_matvec_data_vjp buffers must be non-NULL.");
+  const int workers = resolve_workers(n_threads);
+  return guarded("csr_matvec_data_vjp", [&] {
+    dispatch_cpu<DataVjpCpu>(vt, it, n_rows, n_cols, int64_t{1}, true, indices, indptr, x, cot,
+                             out, workers);
+  });
+}
+
+extern "C" msx_status msx_csr_spmm_data_vjp_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                int64_t n_cols, int64_t nnz, const void *indices,
+                                                const void *indptr, int64_t k, const void *X,
+                                                const void *cot, void *out, int n_threads) {
+  clear_error();
+  msx_status st = check_cpu("csr_matmul_data_vjp", vt, it, n_rows, n_cols, nnz, indices, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (k < 0) return fail(MSX_EINVAL, "csr_matmul_data_vjp rhs column count must be non-negative.");
+  if (nnz > 0 && (out == nullptr || (k > 0 && (cot == nullptr || (n_cols > 0 && X == nullptr)))))
+    return fail(MSX_EINVAL, "csr_matmul_data_vjp buffers must be non-NULL.");
+  const int workers = resolve_workers(n_threads);
+  return guarded("csr_matmul_data_vjp", [&] {
+    dispatch_cpu<DataVjpCpu>(vt, it, n_rows, n_cols, k, false, indices, indptr, X, cot, out,
+                             workers);
+  });
 }

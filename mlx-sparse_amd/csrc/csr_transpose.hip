@@ -1,0 +1,543 @@
+// csr_transpose.hip - the adjoint side of the path: the CSR transpose, the
+// transposed products A^T x / A^T X, and the value gradients of A x / A X.
+//
+//   msx_csr_transpose       CSR of A^T (= CSC of A), every column's entries
+//                           in row order (the reference's counting sort,
+//                           reference: src/sparse/csr_transpose/csr_transpose.cpp).
+//                           Built by a stable radix sort of (column,
+//                           position) pairs; fully asynchronous on `stream`.
+//   msx_csr_spmv_transpose  y = A^T x, and msx_csr_spmm_transpose Y = A^T X,
+//                           without a transpose: each stored value adds its
+//                           product to its column's output with a float
+//                           atomic (the reference's Metal kernels scatter the
+//                           same way, csr_matvec_transpose.metal:27-49).  The
+//                           order of those additions is not fixed, so the
+//                           result agrees with a sequential sum to rounding.
+//                           Deterministic transposed products come from
+//                           msx_csr_transpose followed by msx_csr_spmv/_spmm.
+//   msx_csr_spmv_data_vjp   g[p] = cot[row(p)] * x[col(p)], one rounding
+//                           (reference: csr_matvec_data_vjp.cpp,
+//                           csr_matvec_data_vjp_cpu_impl).
+//   msx_csr_spmm_data_vjp   g[p] = sum_c cot[row(p), c] * X[col(p), c] from
+//                           zero in c order (reference: csr_matmul_data_vjp.cpp).
+// Complex conjugation of an operand (the Hermitian adjoint) is the caller's.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <string>
+
+#include "msx_device.h"
+#include "msx_internal.h"
+#include "msx_sparse.h"
+
+namespace msx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int64_t kMaxGrid = int64_t{1} << 20;
+constexpr int64_t kIntMax = 2147483647;
+
+uint32_t grid_for(int64_t n) {
+  return static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, kMaxGrid)));
+}
+
+__device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+__device__ inline float amul(float a, float b) { return a * b; }
+__device__ inline c64 amul(c64 a, c64 b) { return vmul<C64>(a, b); }
+
+__device__ inline void atomic_acc(float *p, float v) { unsafeAtomicAdd(p, v); }
+__device__ inline void atomic_acc(c64 *p, c64 v) {
+  float *f = reinterpret_cast<float *>(p);
+  unsafeAtomicAdd(f, v.re);
+  unsafeAtomicAdd(f + 1, v.im);
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) fill(T *__restrict__ p, int64_t n, T v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    p[i] = v;
+}
+
+// acc[r * lda + q] = 0 for r < rows, q < k (padding columns untouched).
+template <class T>
+__global__ void __launch_bounds__(kThreads)
+    fill_rows(T *__restrict__ acc, int64_t rows, int64_t k, int64_t lda) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < rows * k;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t r = i / k;
+    acc[r * lda + (i - r * k)] = T{};
+  }
+}
+
+template <class V>
+__global__ void __launch_bounds__(kThreads)
+    narrow_all(const typename V::Acc *__restrict__ acc, int64_t n, typename V::Storage *__restrict__ y) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    y[i] = V::narrow(acc[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Transpose build.
+
+// key[p] = column of p (n_cols when out of range), row[p] = its row, pos[p] = p.
+template <class I>
+__global__ void __launch_bounds__(kThreads)
+    column_keys(const I *__restrict__ indices, const I *__restrict__ indptr, int64_t n_rows,
+                int64_t nnz, int64_t n_cols, uint32_t *__restrict__ key, I *__restrict__ row) {
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n_rows;
+       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+    for (int64_t p = s; p < e; ++p) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      key[p] = (c >= 0 && c < n_cols) ? static_cast<uint32_t>(c) : static_cast<uint32_t>(n_cols);
+      row[p] = static_cast<I>(r);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+    init_keys(int64_t nnz, uint32_t drop, uint32_t *__restrict__ key, uint32_t *__restrict__ pos) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; p < nnz;
+       p += static_cast<int64_t>(gridDim.x) * kThreads) {
+    key[p] = drop;
+    pos[p] = static_cast<uint32_t>(p);
+  }
+}
+
+// t_indptr[c] = first sorted index with key >= c, c in [0, n_cols].
+template <class I>
+__global__ void __launch_bounds__(kThreads)
+    column_starts(const uint32_t *__restrict__ sorted, int64_t nnz, int64_t n_cols,
+                  I *__restrict__ t_indptr) {
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c <= n_cols;
+       c += static_cast<int64_t>(gridDim.x) * kThreads) {
+    int64_t lo = 0, hi = nnz;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (static_cast<int64_t>(sorted[mid]) < c) lo = mid + 1; else hi = mid;
+    }
+    t_indptr[c] = static_cast<I>(lo);
+  }
+}
+
+template <class S, class I>
+__global__ void __launch_bounds__(kThreads)
+    transpose_gather(const S *__restrict__ data, const I *__restrict__ row,
+                     const uint32_t *__restrict__ key, const uint32_t *__restrict__ pos, int64_t nnz,
+                     int64_t n_cols, S *__restrict__ t_data, I *__restrict__ t_indices) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < nnz;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    if (static_cast<int64_t>(key[i]) >= n_cols) continue;  // dropped: past t_indptr[n_cols]
+    const int64_t p = clamp64(pos[i], 0, nnz - 1);
+    t_data[i] = data[p];
+    t_indices[i] = row[p];
+  }
+}
+
+int bits_for(uint64_t v) {
+  int b = 0;
+  while (b < 64 && (v >> b) != 0) ++b;
+  return std::max(1, b);
+}
+
+template <class S, class I>
+msx_status transpose_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                           const void *indices, const void *indptr, void *t_data, void *t_indices,
+                           void *t_indptr, hipStream_t stream) {
+  const auto *ip = static_cast<const I *>(indptr);
+  auto *tp = static_cast<I *>(t_indptr);
+  if (nnz == 0) {
+    hipLaunchKernelGGL((fill<I>), dim3(grid_for(n_cols + 1)), dim3(kThreads), 0, stream, tp,
+                       n_cols + 1, I{0});
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
+  // Scratch: 4 key/position arrays, the row of each value, the sort's temp.
+  const size_t b4 = (static_cast<size_t>(nnz) * 4 + 255) / 256 * 256;
+  const size_t bI = (static_cast<size_t>(nnz) * sizeof(I) + 255) / 256 * 256;
+  const int end_bit = bits_for(static_cast<uint64_t>(n_cols));  // keys <= n_cols
+  size_t sort_bytes = 0;
+  MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<int>(nnz), 0, end_bit, stream));
+  char *scratch = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&scratch), 4 * b4 + bI + sort_bytes, stream));
+  auto *key = reinterpret_cast<uint32_t *>(scratch);
+  auto *key_out = reinterpret_cast<uint32_t *>(scratch + b4);
+  auto *pos = reinterpret_cast<uint32_t *>(scratch + 2 * b4);
+  auto *pos_out = reinterpret_cast<uint32_t *>(scratch + 3 * b4);
+  auto *row = reinterpret_cast<I *>(scratch + 4 * b4);
+  void *sort_tmp = scratch + 4 * b4 + bI;
+  msx_status st = MSX_OK;
+  hipLaunchKernelGGL(init_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
+                     static_cast<uint32_t>(n_cols), key, pos);
+  hipLaunchKernelGGL((column_keys<I>), dim3(grid_for(n_rows)), dim3(kThreads), 0, stream,
+                     static_cast<const I *>(indices), ip, n_rows, nnz, n_cols, key, row);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipcub::DeviceRadixSort::SortPairs(sort_tmp, sort_bytes, key, key_out, pos, pos_out,
+                                           static_cast<int>(nnz), 0, end_bit, stream);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL((column_starts<I>), dim3(grid_for(n_cols + 1)), dim3(kThreads), 0, stream,
+                       key_out, nnz, n_cols, tp);
+    hipLaunchKernelGGL((transpose_gather<S, I>), dim3(grid_for(nnz)), dim3(kThreads), 0, stream,
+                       static_cast<const S *>(data), row, key_out, pos_out, nnz, n_cols,
+                       static_cast<S *>(t_data), static_cast<I *>(t_indices));
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) st = hip_fail(e, "csr_transpose");
+  const hipError_t ef = hipFreeAsync(scratch, stream);
+  if (st == MSX_OK && ef != hipSuccess) st = hip_fail(ef, "csr_transpose scratch release");
+  return st;
+}
+
+// ---------------------------------------------------------------------------
+// Transposed products by atomic scatter.  G lanes per row of A.
+
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    scatter_spmv(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
+                 typename V::Acc *__restrict__ acc, int64_t n_rows, int64_t nnz, int64_t n_cols,
+                 int G) {
+  using A = typename V::Acc;
+  const int64_t rows_per_block = kThreads / G;
+  const int j = threadIdx.x % G;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
+       row < n_rows; row += static_cast<int64_t>(gridDim.x) * rows_per_block) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    const A xr = V::widen(x[row]);
+    for (int64_t p = s + j; p < e; p += G) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      if (c >= 0 && c < n_cols) atomic_acc(acc + c, amul(V::widen(data[p]), xr));
+    }
+  }
+}
+
+// One wave per row of A; lanes over the k columns of X.
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    scatter_spmm(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
+                 int64_t ldx, typename V::Acc *__restrict__ acc, int64_t lda, int64_t n_rows,
+                 int64_t nnz, int64_t n_cols, int64_t k) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+       row < n_rows; row += waves) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    for (int64_t p = s; p < e; ++p) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      if (c < 0 || c >= n_cols) continue;
+      const typename V::Acc a = V::widen(data[p]);
+      for (int64_t q = lane; q < k; q += kWave)
+        atomic_acc(acc + c * lda + q, amul(a, V::widen(X[row * ldx + q])));
+    }
+  }
+}
+
+template <class V>
+__global__ void __launch_bounds__(kThreads)
+    narrow_rows(const typename V::Acc *__restrict__ acc, int64_t rows, int64_t k, int64_t lda,
+                typename V::Storage *__restrict__ Y, int64_t ldy) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < rows * k;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t r = i / k, q = i - r * k;
+    Y[r * ldy + q] = V::narrow(acc[r * lda + q]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Value gradients.  G lanes per row.
+
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    spmv_data_vjp(const I *__restrict__ indices, const I *__restrict__ indptr,
+                  const typename V::Storage *__restrict__ x,
+                  const typename V::Storage *__restrict__ cot, typename V::Storage *__restrict__ out,
+                  int64_t n_rows, int64_t nnz, int64_t n_cols, int G) {
+  using A = typename V::Acc;
+  const int64_t rows_per_block = kThreads / G;
+  const int j = threadIdx.x % G;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
+       row < n_rows; row += static_cast<int64_t>(gridDim.x) * rows_per_block) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    const A g = V::widen(cot[row]);
+    for (int64_t p = s + j; p < e; p += G) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      out[p] = V::narrow((c >= 0 && c < n_cols) ? amul(g, V::widen(x[c])) : vzero<A>());
+    }
+  }
+}
+
+template <class V, class I>
+__global__ void __launch_bounds__(kThreads)
+    spmm_data_vjp(const I *__restrict__ indices, const I *__restrict__ indptr,
+                  const typename V::Storage *__restrict__ X, int64_t ldx,
+                  const typename V::Storage *__restrict__ cot, int64_t ldc,
+                  typename V::Storage *__restrict__ out, int64_t n_rows, int64_t nnz,
+                  int64_t n_cols, int64_t k, int G) {
+  using A = typename V::Acc;
+  const int64_t rows_per_block = kThreads / G;
+  const int j = threadIdx.x % G;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
+       row < n_rows; row += static_cast<int64_t>(gridDim.x) * rows_per_block) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    const typename V::Storage *g = cot + row * ldc;
+    for (int64_t p = s + j; p < e; p += G) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      A acc = vzero<A>();
+      if (c >= 0 && c < n_cols) {
+        const typename V::Storage *xr = X + c * ldx;
+        for (int64_t q = 0; q < k; ++q) acc = vadd(acc, amul(V::widen(g[q]), V::widen(xr[q])));
+      }
+      out[p] = V::narrow(acc);
+    }
+  }
+}
+
+int lanes_for(int64_t n_rows, int64_t nnz) {
+  const int64_t avg = n_rows > 0 ? nnz / n_rows : 0;
+  int G = 1;
+  while (G < kWave && 2 * G <= avg) G <<= 1;
+  return G;
+}
+
+// Dispatch on value and index types.
+template <template <class, class> class Fn, class... Args>
+msx_status dispatch(msx_vtype vt, msx_itype it, Args... args) {
+  const bool i64 = it == MSX_I64;
+  switch (vt) {
+  case MSX_F32: return i64 ? Fn<F32, int64_t>::run(args...) : Fn<F32, int32_t>::run(args...);
+  case MSX_F16: return i64 ? Fn<F16, int64_t>::run(args...) : Fn<F16, int32_t>::run(args...);
+  case MSX_BF16: return i64 ? Fn<BF16, int64_t>::run(args...) : Fn<BF16, int32_t>::run(args...);
+  case MSX_C64: return i64 ? Fn<C64, int64_t>::run(args...) : Fn<C64, int32_t>::run(args...);
+  }
+  return fail(MSX_ETYPE, "unsupported value dtype.");
+}
+
+template <class V, class I>
+struct TransposeOp {
+  static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                        const void *indices, const void *indptr, void *t_data, void *t_indices,
+                        void *t_indptr, hipStream_t stream) {
+    return transpose_typed<typename V::Storage, I>(n_rows, n_cols, nnz, data, indices, indptr,
+                                                   t_data, t_indices, t_indptr, stream);
+  }
+};
+
+// Accumulators: the output itself when it holds the accumulator type
+// (float32, complex64), else float32 scratch narrowed at the end.
+template <class V, class I>
+struct SpmvTransposeOp {
+  static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                        const void *indices, const void *indptr, const void *x, void *y,
+                        hipStream_t stream) {
+    using S = typename V::Storage;
+    using A = typename V::Acc;
+    constexpr bool direct = sizeof(S) == sizeof(A);
+    A *acc = nullptr;
+    if (direct) {
+      acc = static_cast<A *>(y);
+    } else {
+      MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&acc), sizeof(A) * std::max<int64_t>(n_cols, 1), stream));
+    }
+    hipLaunchKernelGGL((fill<A>), dim3(grid_for(n_cols)), dim3(kThreads), 0, stream, acc, n_cols, A{});
+    const int G = lanes_for(n_rows, nnz);
+    hipLaunchKernelGGL((scatter_spmv<V, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+                       static_cast<const S *>(data), static_cast<const I *>(indices),
+                       static_cast<const I *>(indptr), static_cast<const S *>(x), acc, n_rows, nnz,
+                       n_cols, G);
+    if (!direct)
+      hipLaunchKernelGGL((narrow_all<V>), dim3(grid_for(n_cols)), dim3(kThreads), 0, stream, acc,
+                         n_cols, static_cast<S *>(y));
+    hipError_t e = hipGetLastError();
+    if (!direct) {
+      const hipError_t ef = hipFreeAsync(acc, stream);
+      if (e == hipSuccess) e = ef;
+    }
+    if (e != hipSuccess) return hip_fail(e, "csr_matvec_transpose");
+    return MSX_OK;
+  }
+};
+
+template <class V, class I>
+struct SpmmTransposeOp {
+  static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                        const void *indices, const void *indptr, int64_t k, const void *X,
+                        int64_t ldx, void *Y, int64_t ldy, hipStream_t stream) {
+    using S = typename V::Storage;
+    using A = typename V::Acc;
+    constexpr bool direct = sizeof(S) == sizeof(A);
+    A *acc = nullptr;
+    int64_t lda = ldy;
+    if (direct) {
+      acc = static_cast<A *>(Y);
+    } else {
+      lda = k;
+      MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&acc),
+                                 sizeof(A) * std::max<int64_t>(n_cols * k, 1), stream));
+    }
+    hipLaunchKernelGGL((fill_rows<A>), dim3(grid_for(n_cols * k)), dim3(kThreads), 0, stream, acc,
+                       n_cols, k, lda);
+    hipLaunchKernelGGL((scatter_spmm<V, I>), dim3(grid_for(n_rows * kWave)), dim3(kThreads), 0,
+                       stream, static_cast<const S *>(data), static_cast<const I *>(indices),
+                       static_cast<const I *>(indptr), static_cast<const S *>(X), ldx, acc, lda,
+                       n_rows, nnz, n_cols, k);
+    if (!direct)
+      hipLaunchKernelGGL((narrow_rows<V>), dim3(grid_for(n_cols * k)), dim3(kThreads), 0, stream,
+                         acc, n_cols, k, lda, static_cast<S *>(Y), ldy);
+    hipError_t e = hipGetLastError();
+    if (!direct) {
+      const hipError_t ef = hipFreeAsync(acc, stream);
+      if (e == hipSuccess) e = ef;
+    }
+    if (e != hipSuccess) return hip_fail(e, "csr_matmul_transpose");
+    return MSX_OK;
+  }
+};
+
+template <class V, class I>
+struct SpmvDataVjpOp {
+  static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *indices,
+                        const void *indptr, const void *x, const void *cot, void *out,
+                        hipStream_t stream) {
+    using S = typename V::Storage;
+    const int G = lanes_for(n_rows, nnz);
+    hipLaunchKernelGGL((spmv_data_vjp<V, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+                       static_cast<const I *>(indices), static_cast<const I *>(indptr),
+                       static_cast<const S *>(x), static_cast<const S *>(cot), static_cast<S *>(out),
+                       n_rows, nnz, n_cols, G);
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
+};
+
+template <class V, class I>
+struct SpmmDataVjpOp {
+  static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *indices,
+                        const void *indptr, int64_t k, const void *X, int64_t ldx, const void *cot,
+                        int64_t ldc, void *out, hipStream_t stream) {
+    using S = typename V::Storage;
+    const int G = lanes_for(n_rows, nnz);
+    hipLaunchKernelGGL((spmm_data_vjp<V, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+                       static_cast<const I *>(indices), static_cast<const I *>(indptr),
+                       static_cast<const S *>(X), ldx, static_cast<const S *>(cot), ldc,
+                       static_cast<S *>(out), n_rows, nnz, n_cols, k, G);
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
+};
+
+msx_status check_csr(const char *op, msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                     int64_t nnz, const void *indices, const void *indptr) {
+  if (!valid_itype(it)) return fail(MSX_ETYPE, std::string(op) + " requires int32 or int64 indices.");
+  if (!valid_vtype(vt)) return fail(MSX_ETYPE, std::string(op) + " unsupported value dtype.");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0)
+    return fail(MSX_EINVAL, std::string(op) + " shape dimensions must be non-negative.");
+  if (n_rows >= kIntMax || n_cols >= kIntMax)
+    return fail(MSX_EINVAL, std::string(op) + " shape dimensions must fit in int32.");
+  if (nnz >= kIntMax)
+    return fail(MSX_EINVAL, std::string(op) + " supports at most 2^31 - 2 stored values.");
+  if (indptr == nullptr) return fail(MSX_EINVAL, std::string(op) + " indptr is NULL.");
+  if (nnz > 0 && indices == nullptr)
+    return fail(MSX_EINVAL, std::string(op) + " indices must be non-NULL when nnz > 0.");
+  return MSX_OK;
+}
+
+}  // namespace
+}  // namespace msx
+
+using namespace msx;
+
+extern "C" msx_status msx_csr_transpose(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                                        int64_t nnz, const void *data, const void *indices,
+                                        const void *indptr, void *t_data, void *t_indices,
+                                        void *t_indptr, void *stream) {
+  clear_error();
+  msx_status st = check_csr("csr_transpose", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (t_indptr == nullptr || (nnz > 0 && (data == nullptr || t_data == nullptr || t_indices == nullptr)))
+    return fail(MSX_EINVAL, "csr_transpose output buffers must be non-NULL.");
+  return dispatch<TransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, t_data,
+                               t_indices, t_indptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_spmv_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                             int64_t n_cols, int64_t nnz, const void *data,
+                                             const void *indices, const void *indptr,
+                                             const void *x, void *y, void *stream) {
+  clear_error();
+  msx_status st = check_csr("csr_matvec_transpose", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (n_cols > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec_transpose y is NULL.");
+  if (nnz > 0 && (data == nullptr || x == nullptr))
+    return fail(MSX_EINVAL, "csr_matvec_transpose data and x must be non-NULL.");
+  if (n_cols == 0) return MSX_OK;
+  return dispatch<SpmvTransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, x, y,
+                                   static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_spmm_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                             int64_t n_cols, int64_t nnz, const void *data,
+                                             const void *indices, const void *indptr, int64_t k,
+                                             const void *X, int64_t ldx, void *Y, int64_t ldy,
+                                             void *stream) {
+  clear_error();
+  msx_status st = check_csr("csr_matmul_transpose", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (k < 0 || k >= kIntMax) return fail(MSX_EINVAL, "csr_matmul_transpose rhs column count must fit in int32.");
+  if (ldx < k || ldy < k)
+    return fail(MSX_EINVAL, "csr_matmul_transpose leading dimensions must be at least the column count.");
+  if (n_cols > 0 && k > 0 && Y == nullptr) return fail(MSX_EINVAL, "csr_matmul_transpose Y is NULL.");
+  if (nnz > 0 && k > 0 && (data == nullptr || X == nullptr))
+    return fail(MSX_EINVAL, "csr_matmul_transpose data and X must be non-NULL.");
+  if (n_cols == 0 || k == 0) return MSX_OK;
+  return dispatch<SpmmTransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx,
+                                   Y, ldy, static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_spmv_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                            int64_t n_cols, int64_t nnz, const void *indices,
+                                            const void *indptr, const void *x, const void *cot,
+                                            void *out, void *stream) {
+  clear_error();
+  msx_status st = check_csr("csr_matvec_data_vjp", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (nnz > 0 && (out == nullptr || cot == nullptr || (n_cols > 0 && x == nullptr)))
+    return fail(MSX_EINVAL, "csr_matvec_data_vjp buffers must be non-NULL.");
+  if (nnz == 0 || n_rows == 0) return MSX_OK;
+  return dispatch<SpmvDataVjpOp>(vt, it, n_rows, n_cols, nnz, indices, indptr, x, cot, out,
+                                 static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_spmm_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                            int64_t n_cols, int64_t nnz, const void *indices,
+                                            const void *indptr, int64_t k, const void *X,
+                                            int64_t ldx, const void *cot, int64_t ldc, void *out,
+                                            void *stream) {
+  clear_error();
+  msx_status st = check_csr("csr_matmul_data_vjp", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (k < 0 || k >= kIntMax) return fail(MSX_EINVAL, "csr_matmul_data_vjp rhs column count must fit in int32.");
+  if (ldx < k || ldc < k)
+    return fail(MSX_EINVAL, "csr_matmul_data_vjp leading dimensions must be at least the column count.");
+  if (nnz > 0 && (out == nullptr || (k > 0 && (cot == nullptr || (n_cols > 0 && X == nullptr)))))
+    return fail(MSX_EINVAL, "csr_matmul_data_vjp buffers must be non-NULL.");
+  if (nnz == 0 || n_rows == 0) return MSX_OK;
+  return dispatch<SpmmDataVjpOp>(vt, it, n_rows, n_cols, nnz, indices, indptr, k, X, ldx, cot, ldc,
+                                 out, static_cast<hipStream_t>(stream));
+}

@@ -18,7 +18,13 @@
  *     float16/bfloat16 -> float32 with operands widened before the multiply
  *     and one rounding at the end (src/common/common.h:52-79);
  *   - worker-count resolution and range partitioning
- *     (src/common/cpu_parallel.cpp:46-253, cpu_parallel.h:134-164).
+ *     (src/common/cpu_parallel.cpp:46-253, cpu_parallel.h:134-164);
+ *   - the adjoint side: the CSR transpose by counting sort
+ *     (src/sparse/csr_transpose/csr_transpose.cpp, csr_transpose_cpu_impl),
+ *     the transposed products with their per-range partial outputs added in
+ *     range order (src/sparse/csr_matvec_transpose/csr_matvec_transpose.cpp,
+ *     csr_matmul_transpose/csr_matmul_transpose.cpp, *_cpu_impl) and the
+ *     value gradients (csr_matvec_data_vjp.cpp, csr_matmul_data_vjp.cpp).
  *
  * Built with -ffp-contract=off so every product and every sum is rounded on
  * its own, as the reference's separate multiply_accumulate / `+=` are.
@@ -482,4 +488,151 @@ void oracle_narrow_array(int kind, const float *src, uint16_t *dst, int64_t n) {
 void oracle_widen_array(int kind, const uint16_t *src, float *dst, int64_t n) {
   for (int64_t i = 0; i < n; ++i)
     dst[i] = kind == 0 ? oracle_f16_to_f32(src[i]) : oracle_bf16_to_f32(src[i]);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Adjoint side.  Accumulators as above; columns outside [0, n_cols) are
+ * skipped (the reference indexes with them unchecked). */
+
+static inline int col_ok(int64_t c, int64_t n_cols) { return c >= 0 && c < n_cols; }
+
+/* Rows [r0, r1) of A^T X added into acc (n_cols * k, float or cf32). */
+static void transpose_rows(int vt, int it, const void *data, const void *indices, const void *indptr,
+                           const void *X, int64_t n_cols, int64_t k, int64_t r0, int64_t r1,
+                           void *acc) {
+  for (int64_t r = r0; r < r1; ++r) {
+    int64_t b = load_index(it, indptr, r), e = load_index(it, indptr, r + 1);
+    for (int64_t p = b; p < e; ++p) {
+      int64_t c = load_index(it, indices, p);
+      if (!col_ok(c, n_cols)) continue;
+      for (int64_t q = 0; q < k; ++q) {
+        if (vt == V_C64) {
+          cf32 *a = (cf32 *)acc + c * k + q;
+          *a = add_c64(*a, mul_c64(((const cf32 *)data)[p], ((const cf32 *)X)[r * k + q]));
+        } else {
+          float *a = (float *)acc + c * k + q;
+          *a = *a + mul_f32(widen(vt, data, p), widen(vt, X, r * k + q));
+        }
+      }
+    }
+  }
+}
+
+/* A^T X (k = 1: A^T x).  One worker: every output from zero over the rows
+ * in order.  W workers: the rows split by row length (the SpMV ranges),
+ * each range's partial output from zero, partials added from zero in range
+ * order.  Returns 0 on success. */
+int oracle_csr_transpose_product(int vt, int it, int64_t n_rows, int64_t n_cols, int64_t k,
+                                 const void *data, const void *indices, const void *indptr,
+                                 const void *X, void *Y, int n_threads) {
+  int workers = n_threads > 0 ? n_threads : oracle_cpu_worker_count();
+  int64_t out = n_cols * k;
+  size_t esz = vt == V_C64 ? sizeof(cf32) : sizeof(float);
+  int64_t m = 1;
+  int64_t *ranges = NULL;
+  if (workers > 1 && n_rows > 0 && out > 0) {
+    int64_t *work = (int64_t *)malloc((size_t)n_rows * sizeof(int64_t));
+    ranges = (int64_t *)malloc((size_t)workers * 2 * sizeof(int64_t));
+    if (!work || !ranges) {
+      free(work);
+      free(ranges);
+      return -1;
+    }
+    for (int64_t r = 0; r < n_rows; ++r)
+      work[r] = load_index(it, indptr, r + 1) - load_index(it, indptr, r);
+    m = oracle_cpu_ranges(work, n_rows, workers, ranges);
+    free(work);
+    if (m < 1) m = 1;
+  }
+  void *partial = calloc((size_t)(m * (out > 0 ? out : 1)), esz);
+  if (!partial) {
+    free(ranges);
+    return -1;
+  }
+  if (m <= 1) {
+    transpose_rows(vt, it, data, indices, indptr, X, n_cols, k, 0, n_rows, partial);
+  } else {
+    for (int64_t w = 0; w < m; ++w)
+      transpose_rows(vt, it, data, indices, indptr, X, n_cols, k, ranges[2 * w], ranges[2 * w + 1],
+                     (char *)partial + (size_t)(w * out) * esz);
+  }
+  for (int64_t i = 0; i < out; ++i) {
+    if (vt == V_C64) {
+      cf32 t = {0.0f, 0.0f};
+      if (m <= 1) t = ((cf32 *)partial)[i];
+      else
+        for (int64_t w = 0; w < m; ++w) t = add_c64(t, ((cf32 *)partial)[w * out + i]);
+      ((cf32 *)Y)[i] = t;
+    } else {
+      float t = 0.0f;
+      if (m <= 1) t = ((float *)partial)[i];
+      else
+        for (int64_t w = 0; w < m; ++w) t = t + ((float *)partial)[w * out + i];
+      narrow_store(vt, Y, i, t);
+    }
+  }
+  free(partial);
+  free(ranges);
+  return 0;
+}
+
+/* CSR of A^T: column counts, prefix sums, then rows in order. */
+int oracle_csr_transpose(int vt, int it, int64_t n_rows, int64_t n_cols, const void *data,
+                         const void *indices, const void *indptr, void *t_data, void *t_indices,
+                         void *t_indptr) {
+  size_t esz = vt == V_C64 ? 8 : (vt == V_F32 ? 4 : 2);
+  int64_t *next = (int64_t *)calloc((size_t)n_cols + 1, sizeof(int64_t));
+  if (!next) return -1;
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t p = load_index(it, indptr, r); p < load_index(it, indptr, r + 1); ++p) {
+      int64_t c = load_index(it, indices, p);
+      if (col_ok(c, n_cols)) next[c + 1]++;
+    }
+  for (int64_t c = 0; c < n_cols; ++c) next[c + 1] += next[c];
+  for (int64_t c = 0; c <= n_cols; ++c) {
+    if (it == I_I64) ((int64_t *)t_indptr)[c] = next[c];
+    else ((int32_t *)t_indptr)[c] = (int32_t)next[c];
+  }
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t p = load_index(it, indptr, r); p < load_index(it, indptr, r + 1); ++p) {
+      int64_t c = load_index(it, indices, p);
+      if (!col_ok(c, n_cols)) continue;
+      int64_t slot = next[c]++;
+      memcpy((char *)t_data + (size_t)slot * esz, (const char *)data + (size_t)p * esz, esz);
+      if (it == I_I64) ((int64_t *)t_indices)[slot] = r;
+      else ((int32_t *)t_indices)[slot] = (int32_t)r;
+    }
+  free(next);
+  return 0;
+}
+
+/* Value gradients.  single != 0: out[p] = cot[row] * x[col] (one product,
+ * the SpMV rule); else out[p] = sum_q cot[row, q] * X[col, q] from zero. */
+int oracle_csr_data_vjp(int vt, int it, int64_t n_rows, int64_t n_cols, int64_t k, int single,
+                        const void *indices, const void *indptr, const void *X, const void *cot,
+                        void *out) {
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t p = load_index(it, indptr, r); p < load_index(it, indptr, r + 1); ++p) {
+      int64_t c = load_index(it, indices, p);
+      if (vt == V_C64) {
+        cf32 acc = {0.0f, 0.0f};
+        if (col_ok(c, n_cols)) {
+          if (single) acc = mul_c64(((const cf32 *)cot)[r], ((const cf32 *)X)[c]);
+          else
+            for (int64_t q = 0; q < k; ++q)
+              acc = add_c64(acc, mul_c64(((const cf32 *)cot)[r * k + q], ((const cf32 *)X)[c * k + q]));
+        }
+        ((cf32 *)out)[p] = acc;
+      } else {
+        float acc = 0.0f;
+        if (col_ok(c, n_cols)) {
+          if (single) acc = mul_f32(widen(vt, cot, r), widen(vt, X, c));
+          else
+            for (int64_t q = 0; q < k; ++q)
+              acc = acc + mul_f32(widen(vt, cot, r * k + q), widen(vt, X, c * k + q));
+        }
+        narrow_store(vt, out, p, acc);
+      }
+    }
+  return 0;
 }

@@ -3,7 +3,9 @@
 ctypes front end of ``csr_oracle.c`` (a plain-C restatement of mlx-sparse's
 CPU kernels, reference: src/sparse/csr_matvec/csr_matvec.cpp:79-168,
 src/sparse/csr_matmul/csr_matmul.cpp:83-222, src/common/common.h:52-79,
-src/common/cpu_parallel.cpp:46-253).  Only ``tests/``,
+src/common/cpu_parallel.cpp:46-253, and the adjoint side:
+src/sparse/csr_transpose, csr_matvec_transpose, csr_matmul_transpose,
+csr_matvec_data_vjp, csr_matmul_data_vjp).  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
 this module, always as the checker or the timed CPU baseline, never as the
 product path.
@@ -23,6 +25,14 @@ Parity status of each function (the checks live in tests/test_oracle_*.py):
   SpMVs; the bit pattern of MLX's complex product is un-vendored.
 - ``cpu_ranges``/``cpu_worker_count``: pinned against a naive re-derivation
   and environment cases.
+- ``csr_transpose``: pinned against SciPy's ``tocsc`` (same stable order)
+  and a dense transpose.
+- ``csr_transpose_product``: float32 pinned against float64 brute force, the
+  adjoint identity <A x, y> = <x, A^T y>, single-product closed forms and the
+  transpose-then-SpMV route on matrices whose columns hold one value; the
+  W-worker partial order pinned on a case where it changes the rounding.
+- ``csr_data_vjp``: pinned against finite differences of the dense product
+  (exact for float32 on small integers) and the single-product rule.
 """
 
 from __future__ import annotations
@@ -74,6 +84,13 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_narrow_array.restype = None
         _lib.oracle_widen_array.argtypes = [ci, vp, vp, i64]
         _lib.oracle_widen_array.restype = None
+        _lib.oracle_csr_transpose_product.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp,
+                                                      ci]
+        _lib.oracle_csr_transpose_product.restype = ci
+        _lib.oracle_csr_transpose.argtypes = [ci, ci, i64, i64, vp, vp, vp, vp, vp, vp]
+        _lib.oracle_csr_transpose.restype = ci
+        _lib.oracle_csr_data_vjp.argtypes = [ci, ci, i64, i64, i64, ci, vp, vp, vp, vp, vp]
+        _lib.oracle_csr_data_vjp.restype = ci
     return _lib
 
 
@@ -127,6 +144,68 @@ def csr_matmul(data, indices, indptr, X, n_rows: int, *, vtype: str | None = Non
     if rc != 0:
         raise MemoryError("oracle_csr_matmul failed")
     return Y
+
+
+def csr_transpose_product(data, indices, indptr, X, n_rows: int, n_cols: int, *,
+                          vtype: str | None = None, n_threads: int = 1) -> np.ndarray:
+    """A^T x (X rank 1) or A^T X (rank 2, row-major): one worker sums every
+    output from zero over the rows in order; W workers keep one partial
+    output per row range (ranges by row length) and add the partials from
+    zero in range order (reference csr_matvec_transpose.cpp:89-153,
+    csr_matmul_transpose.cpp:94-159).  Complex values are not conjugated."""
+    vt, data, indices, indptr = _prep(data, indices, indptr, vtype)
+    X = np.ascontiguousarray(X, dtype=_STORAGE[vt])
+    k = 1 if X.ndim == 1 else X.shape[1]
+    shape = (n_cols,) if X.ndim == 1 else (n_cols, k)
+    Y = np.empty(shape, dtype=_STORAGE[vt])
+    rc = lib().oracle_csr_transpose_product(VTYPES[vt], ITYPES[indices.dtype], n_rows, n_cols,
+                                            k, _ptr(data), _ptr(indices), _ptr(indptr), _ptr(X),
+                                            _ptr(Y), n_threads)
+    if rc != 0:
+        raise MemoryError("oracle_csr_transpose_product failed")
+    return Y
+
+
+def csr_transpose(data, indices, indptr, n_rows: int, n_cols: int, *,
+                  vtype: str | None = None):
+    """CSR of A^T by counting sort: column counts, prefix sums, then the
+    stored values scattered in row order (reference
+    csr_transpose.cpp, csr_transpose_cpu_impl).  Returns (data, indices,
+    indptr) of the (n_cols, n_rows) transpose."""
+    vt, data, indices, indptr = _prep(data, indices, indptr, vtype)
+    nnz = int(indptr[n_rows]) if n_rows > 0 else 0
+    t_data = np.empty(max(nnz, 0), dtype=_STORAGE[vt])
+    t_indices = np.empty(max(nnz, 0), dtype=indices.dtype)
+    t_indptr = np.empty(n_cols + 1, dtype=indices.dtype)
+    rc = lib().oracle_csr_transpose(VTYPES[vt], ITYPES[indices.dtype], n_rows, n_cols,
+                                    _ptr(data), _ptr(indices), _ptr(indptr), _ptr(t_data),
+                                    _ptr(t_indices), _ptr(t_indptr))
+    if rc != 0:
+        raise MemoryError("oracle_csr_transpose failed")
+    end = int(t_indptr[n_cols])
+    return t_data[:end], t_indices[:end], t_indptr
+
+
+def csr_data_vjp(indices, indptr, X, cot, n_rows: int, n_cols: int, nnz: int, *,
+                 vtype: str | None = None) -> np.ndarray:
+    """Gradient of the stored values.  X rank 1 (SpMV): g[p] = cot[row] *
+    x[col], one product (reference csr_matvec_data_vjp.cpp).  X rank 2:
+    g[p] = sum_q cot[row, q] * X[col, q] from zero (csr_matmul_data_vjp.cpp).
+    No conjugation: complex callers pass conj(x)."""
+    X = np.asarray(X)
+    vt = _vtype_of(X, vtype)
+    indices = np.ascontiguousarray(indices)
+    indptr = np.ascontiguousarray(indptr)
+    X = np.ascontiguousarray(X, dtype=_STORAGE[vt])
+    cot = np.ascontiguousarray(cot, dtype=_STORAGE[vt])
+    single = 1 if X.ndim == 1 else 0
+    k = 1 if X.ndim == 1 else X.shape[1]
+    out = np.zeros(nnz, dtype=_STORAGE[vt])
+    rc = lib().oracle_csr_data_vjp(VTYPES[vt], ITYPES[indices.dtype], n_rows, n_cols, k, single,
+                                   _ptr(indices), _ptr(indptr), _ptr(X), _ptr(cot), _ptr(out))
+    if rc != 0:
+        raise MemoryError("oracle_csr_data_vjp failed")
+    return out
 
 
 def cpu_ranges(work, parts: int) -> list[tuple[int, int]]:

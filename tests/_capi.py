@@ -67,6 +67,20 @@ def lib() -> ctypes.CDLL:
                                                vp, ci]
         L.msx_csr_spmv_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
         L.msx_csr_spmm_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp, ci]
+        L.msx_csr_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmv_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmm_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp,
+                                             i64, vp]
+        L.msx_csr_spmv_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
+        L.msx_csr_spmm_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp,
+                                                 ci]
+        L.msx_csr_spmv_data_vjp.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmm_data_vjp.argtypes = [ci, ci, i64, i64, i64, vp, vp, i64, vp, i64, vp, i64,
+                                            vp, vp]
+        L.msx_csr_spmv_data_vjp_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
+        L.msx_csr_spmm_data_vjp_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, i64, vp, vp, vp,
+                                                ci]
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
@@ -75,7 +89,12 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_spmv", "msx_csr_spmm", "msx_csr_batched_spmv",
                      "msx_csr_batched_spmm", "msx_csr_batched_spmv_cpu",
                      "msx_csr_batched_spmm_cpu",
-                     "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges"):
+                     "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges",
+                     "msx_csr_transpose", "msx_csr_transpose_cpu", "msx_csr_spmv_transpose",
+                     "msx_csr_spmm_transpose", "msx_csr_spmv_transpose_cpu",
+                     "msx_csr_spmm_transpose_cpu", "msx_csr_spmv_data_vjp",
+                     "msx_csr_spmm_data_vjp", "msx_csr_spmv_data_vjp_cpu",
+                     "msx_csr_spmm_data_vjp_cpu"):
             getattr(L, name).restype = ci
         _lib = L
     return _lib
@@ -194,3 +213,84 @@ def batched_spmm(data, indices, indptr, X, n_rows, n_cols, Y=None):
     if st != OK:
         raise RuntimeError(f"msx_csr_batched_spmm: {st} {last_error()}")
     return Y
+
+
+def _check(st, name):
+    if st != OK:
+        raise RuntimeError(f"{name}: {st} {last_error()}")
+
+
+def _is_cpu(t):
+    return t.device.type == "cpu"
+
+
+def transpose(data, indices, indptr, n_rows, n_cols):
+    """CSR of A^T: (t_data, t_indices, t_indptr) on data's device."""
+    nnz = data.numel()
+    td = torch.empty(nnz, dtype=data.dtype, device=data.device)
+    ti = torch.empty(nnz, dtype=indices.dtype, device=data.device)
+    tp = torch.empty(n_cols + 1, dtype=indptr.dtype, device=data.device)
+    args = (VT[data.dtype], IT[indices.dtype], n_rows, n_cols, nnz, _p(data), _p(indices),
+            _p(indptr), _p(td), _p(ti), _p(tp))
+    if _is_cpu(data):
+        _check(lib().msx_csr_transpose_cpu(*args), "msx_csr_transpose_cpu")
+    else:
+        _check(lib().msx_csr_transpose(*args, _stream()), "msx_csr_transpose")
+    return td, ti, tp
+
+
+def spmv_transpose(data, indices, indptr, x, n_rows, n_cols, n_threads=1):
+    y = torch.empty(n_cols, dtype=data.dtype, device=data.device)
+    head = (VT[data.dtype], IT[indices.dtype], n_rows, n_cols, data.numel(), _p(data),
+            _p(indices), _p(indptr), _p(x), _p(y))
+    if _is_cpu(data):
+        _check(lib().msx_csr_spmv_transpose_cpu(*head, n_threads), "msx_csr_spmv_transpose_cpu")
+    else:
+        _check(lib().msx_csr_spmv_transpose(*head, _stream()), "msx_csr_spmv_transpose")
+    return y
+
+
+def spmm_transpose(data, indices, indptr, X, n_rows, n_cols, n_threads=1, Y=None, ldy=None):
+    k = X.shape[1]
+    if Y is None:
+        Y = torch.empty((n_cols, k), dtype=data.dtype, device=data.device)
+    head = (VT[data.dtype], IT[indices.dtype], n_rows, n_cols, data.numel(), _p(data),
+            _p(indices), _p(indptr), k, _p(X))
+    if _is_cpu(data):
+        _check(lib().msx_csr_spmm_transpose_cpu(*head, _p(Y), n_threads),
+               "msx_csr_spmm_transpose_cpu")
+    else:
+        _check(lib().msx_csr_spmm_transpose(*head, X.stride(0), _p(Y),
+                                            ldy if ldy is not None else Y.stride(0), _stream()),
+               "msx_csr_spmm_transpose")
+    return Y
+
+
+def spmv_data_vjp(indices, indptr, x, cot, n_rows, n_cols, n_threads=1):
+    nnz = indices.numel()
+    out = torch.empty(nnz, dtype=x.dtype, device=x.device)
+    head = (VT[x.dtype], IT[indices.dtype], n_rows, n_cols, nnz, _p(indices), _p(indptr),
+            _p(x), _p(cot), _p(out))
+    if _is_cpu(x):
+        _check(lib().msx_csr_spmv_data_vjp_cpu(*head, n_threads), "msx_csr_spmv_data_vjp_cpu")
+    else:
+        _check(lib().msx_csr_spmv_data_vjp(*head, _stream()), "msx_csr_spmv_data_vjp")
+    return out
+
+
+def spmm_data_vjp(indices, indptr, X, cot, n_rows, n_cols, n_threads=1):
+    nnz = indices.numel()
+    k = X.shape[1]
+    out = torch.empty(nnz, dtype=X.dtype, device=X.device)
+    it = IT[indices.dtype]
+    if _is_cpu(X):
+        _check(lib().msx_csr_spmm_data_vjp_cpu(VT[X.dtype], it, n_rows, n_cols, nnz,
+                                               _p(indices), _p(indptr), k, _p(X), _p(cot),
+                                               _p(out), n_threads),
+               "msx_csr_spmm_data_vjp_cpu")
+    else:
+        _check(lib().msx_csr_spmm_data_vjp(VT[X.dtype], it, n_rows, n_cols, nnz, _p(indices),
+                                           _p(indptr), k, _p(X), X.stride(0), _p(cot),
+                                           cot.stride(0), _p(out), _stream()),
+               "msx_csr_spmm_data_vjp")
+    return out
