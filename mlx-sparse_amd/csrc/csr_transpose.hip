@@ -282,29 +282,79 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// One wave per block.  The wave takes 64 / G rows at a time, G lanes per row
+// (lane = one stored value; long rows take several rounds).  X and cot are
+// read in column tiles of kVjpTile: the wave loads each active value's X row
+// segment and each row's cot segment with coalesced loads (two rows per
+// instruction) into LDS, then every lane adds its tile's products in q order
+// from LDS, so each value's sum runs from zero over q = 0 .. k-1 in order.
+constexpr int kVjpTile = 32;
+
 template <class V, class I>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kWave)
     spmm_data_vjp(const I *__restrict__ indices, const I *__restrict__ indptr,
                   const typename V::Storage *__restrict__ X, int64_t ldx,
                   const typename V::Storage *__restrict__ cot, int64_t ldc,
                   typename V::Storage *__restrict__ out, int64_t n_rows, int64_t nnz,
                   int64_t n_cols, int64_t k, int G) {
   using A = typename V::Acc;
-  const int64_t rows_per_block = kThreads / G;
-  const int j = threadIdx.x % G;
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
-       row < n_rows; row += static_cast<int64_t>(gridDim.x) * rows_per_block) {
-    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
-    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
-    const typename V::Storage *g = cot + row * ldc;
-    for (int64_t p = s + j; p < e; p += G) {
-      const int64_t c = static_cast<int64_t>(indices[p]);
-      A acc = vzero<A>();
-      if (c >= 0 && c < n_cols) {
-        const typename V::Storage *xr = X + c * ldx;
-        for (int64_t q = 0; q < k; ++q) acc = vadd(acc, amul(V::widen(g[q]), V::widen(xr[q])));
+  __shared__ A xs[kWave][kVjpTile + 1];
+  __shared__ A cs[kWave][kVjpTile + 1];
+  __shared__ int cl[kWave];  // column of each lane's value, -1 when none
+  const int lane = threadIdx.x;
+  const int R = kWave / G;
+  const int g = lane / G, j = lane - g * G;
+  const int half = lane >> 5, qq = lane & 31;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * R; r0 < n_rows;
+       r0 += static_cast<int64_t>(gridDim.x) * R) {
+    const int64_t row = r0 + g;
+    int64_t s = 0, e = 0;
+    if (row < n_rows) {
+      s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+      e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    }
+    const int rows_here = static_cast<int>(r0 + R <= n_rows ? R : n_rows - r0);
+    for (int64_t base = 0;; base += G) {
+      const int64_t p = s + base + j;
+      const bool act = p < e;
+      const uint64_t mask = __ballot(act);
+      if (mask == 0) break;  // wave-uniform
+      int c = -1;
+      if (act) {
+        const int64_t cv = static_cast<int64_t>(indices[p]);
+        c = (cv >= 0 && cv < n_cols) ? static_cast<int>(cv) : -1;
       }
-      out[p] = V::narrow(acc);
+      cl[lane] = c;
+      __syncthreads();
+      A acc = vzero<A>();
+      for (int64_t q0 = 0; q0 < k; q0 += kVjpTile) {
+        const int qn = static_cast<int>(k - q0 < kVjpTile ? k - q0 : kVjpTile);
+        // X row segments of the active values (two per instruction) and the
+        // cot segments of the group's rows: every load is issued before the
+        // first LDS store, so a wave keeps them all in flight.
+        // Slots a lane does not read (no value, dropped column, q >= qn)
+        // hold zeros.
+        using S = typename V::Storage;
+        S xv[kWave / 2], cv[kWave / 2];
+#pragma unroll
+        for (int t = 0; t < kWave / 2; ++t) {
+          const int cc = cl[2 * t + half];
+          xv[t] = (cc >= 0 && qq < qn) ? X[static_cast<int64_t>(cc) * ldx + q0 + qq] : S{};
+          const int gi = 2 * t + half;
+          cv[t] = (gi < rows_here && qq < qn) ? cot[(r0 + gi) * ldc + q0 + qq] : S{};
+        }
+#pragma unroll
+        for (int t = 0; t < kWave / 2; ++t) {
+          xs[2 * t + half][qq] = V::widen(xv[t]);
+          cs[2 * t + half][qq] = V::widen(cv[t]);
+        }
+        __syncthreads();
+        if (c >= 0)
+          for (int q = 0; q < qn; ++q) acc = vadd(acc, amul(cs[g][q], xs[lane][q]));
+        __syncthreads();
+      }
+      if (act) out[p] = V::narrow(acc);
+      __syncthreads();  // cl is rewritten by the next round
     }
   }
 }
@@ -433,7 +483,9 @@ struct SpmmDataVjpOp {
                         int64_t ldc, void *out, hipStream_t stream) {
     using S = typename V::Storage;
     const int G = lanes_for(n_rows, nnz);
-    hipLaunchKernelGGL((spmm_data_vjp<V, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+    const int64_t groups = (n_rows + kWave / G - 1) / (kWave / G);
+    const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(std::max<int64_t>(groups, 1), kMaxGrid));
+    hipLaunchKernelGGL((spmm_data_vjp<V, I>), dim3(grid), dim3(kWave), 0, stream,
                        static_cast<const I *>(indices), static_cast<const I *>(indptr),
                        static_cast<const S *>(X), ldx, static_cast<const S *>(cot), ldc,
                        static_cast<S *>(out), n_rows, nnz, n_cols, k, G);

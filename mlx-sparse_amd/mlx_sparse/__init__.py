@@ -8,7 +8,14 @@ from __future__ import annotations
 from mlx_sparse import runtime
 from mlx_sparse._csr import CSRArray, csr_array
 from mlx_sparse._device import default_torch_device, use_cpu, use_device, use_gpu
-from mlx_sparse._ops import csr_batched_matmul, csr_batched_matvec, csr_matmul, csr_matvec
+from mlx_sparse._ops import (
+    csr_batched_matmul,
+    csr_batched_matvec,
+    csr_matmul,
+    csr_matmul_transpose,
+    csr_matvec,
+    csr_matvec_transpose,
+)
 from mlx_sparse._typing import INDEX_DTYPES, VALUE_DTYPES, is_available
 
 
@@ -29,7 +36,9 @@ __all__ = [
     "csr_batched_matmul",
     "csr_batched_matvec",
     "csr_matmul",
+    "csr_matmul_transpose",
     "csr_matvec",
+    "csr_matvec_transpose",
     "default_torch_device",
     "is_available",
     "runtime",

@@ -130,6 +130,68 @@ class CSRArray:
             return csr_matmul(self, rhs)
         raise ValueError(f"CSR matmul expects rank-1 or higher RHS, got {tuple(rhs.shape)}.")
 
+    # -- transpose and conjugate -------------------------------------------
+    def _transpose_on(self, device) -> "CSRArray":
+        """CSR of the transpose, computed on ``device`` (cached: the array is
+        immutable)."""
+        device = torch.device(device)
+        data, indices, indptr = self.buffers(device)
+        key = ("T", str(data.device))
+        hit = self._cache.get(key)
+        if hit is None:
+            from mlx_sparse import _native
+
+            t_data, t_indices, t_indptr = _native.csr_transpose(data.detach(), indices, indptr,
+                                                                self.shape)
+            hit = CSRArray(
+                data=t_data,
+                indices=t_indices,
+                indptr=t_indptr,
+                shape=(self.shape[1], self.shape[0]),
+                sorted_indices=True,
+                has_canonical_format=self.has_canonical_format,
+            )
+            self._cache[key] = hit
+        return hit
+
+    def transpose(self) -> "CSRArray":
+        """Transpose, returning a ``CSRArray`` of shape ``(n_cols, n_rows)``
+        with ``sorted_indices=True`` (each row lists its values by increasing
+        column, duplicates in stored order) and the source's
+        ``has_canonical_format`` (reference: mlx_sparse/_csr.py:252-275).
+        Computed on the selected device; the values are not differentiable
+        through it, as in the reference."""
+        from mlx_sparse._device import default_torch_device
+
+        return self._transpose_on(default_torch_device())
+
+    @property
+    def T(self) -> "CSRArray":
+        """Transposed matrix. Alias for :meth:`transpose`."""
+        return self.transpose()
+
+    def conj(self) -> "CSRArray":
+        """Complex-conjugate the stored values; the structure is shared
+        (reference: mlx_sparse/_csr.py:362-379)."""
+        data = self.data.conj().resolve_conj() if self.data.is_complex() else self.data
+        return CSRArray(
+            data=data,
+            indices=self.indices,
+            indptr=self.indptr,
+            shape=self.shape,
+            sorted_indices=self.sorted_indices,
+            has_canonical_format=self.has_canonical_format,
+        )
+
+    def conjugate(self) -> "CSRArray":
+        """Alias for :meth:`conj`."""
+        return self.conj()
+
+    @property
+    def H(self) -> "CSRArray":
+        """Hermitian (conjugate) transpose, ``conj().T``."""
+        return self.conj().transpose()
+
     def todense(self) -> torch.Tensor:
         """Dense copy (duplicates summed), on the buffers' device."""
         n_rows, n_cols = self.shape

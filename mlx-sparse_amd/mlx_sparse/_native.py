@@ -33,6 +33,34 @@ def csr_batched_matmul(data, indices, indptr, rhs, shape: Shape2D) -> torch.Tens
     return extension().csr_batched_matmul(data, indices, indptr, rhs, shape[0], shape[1])
 
 
+def csr_transpose(data, indices, indptr, shape: Shape2D):
+    """CSR buffers of A^T, shape (n_cols, n_rows) (reference:
+    mlx_sparse/_native.py:464-473)."""
+    return tuple(extension().csr_transpose(data, indices, indptr, shape[0], shape[1]))
+
+
+def csr_matvec_transpose(data, indices, indptr, x, shape: Shape2D) -> torch.Tensor:
+    """A^T x, without conjugation (reference: mlx_sparse/_native.py:260-270)."""
+    return extension().csr_matvec_transpose(data, indices, indptr, x, shape[0], shape[1])
+
+
+def csr_matmul_transpose(data, indices, indptr, rhs, shape: Shape2D) -> torch.Tensor:
+    """A^T X, without conjugation (reference: mlx_sparse/_native.py:367-377)."""
+    return extension().csr_matmul_transpose(data, indices, indptr, rhs, shape[0], shape[1])
+
+
+def csr_matvec_data_vjp(indices, indptr, x, cotangent, shape: Shape2D) -> torch.Tensor:
+    """cot[row(p)] * x[col(p)] per stored value (reference:
+    src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp)."""
+    return extension().csr_matvec_data_vjp(indices, indptr, x, cotangent, shape[0], shape[1])
+
+
+def csr_matmul_data_vjp(indices, indptr, rhs, cotangent, shape: Shape2D) -> torch.Tensor:
+    """sum_q cot[row(p), q] * X[col(p), q] per stored value (reference:
+    src/sparse/csr_matmul_data_vjp/csr_matmul_data_vjp.cpp)."""
+    return extension().csr_matmul_data_vjp(indices, indptr, rhs, cotangent, shape[0], shape[1])
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

@@ -29,6 +29,19 @@ def _prod(shape) -> int:
     return int(math.prod(int(d) for d in shape))
 
 
+def _tracked(*tensors: torch.Tensor) -> bool:
+    """True when the product must carry derivatives: reverse mode (grad
+    enabled and an operand requires grad), forward mode (a dual level is
+    open) or a torch.func transform (vmap, grad, jvp) is active."""
+    if torch._C._are_functorch_transforms_active():
+        return True
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return True
+    from torch.autograd import forward_ad
+
+    return forward_ad._current_level >= 0
+
+
 def csr_matvec(a: CSRArray, x) -> torch.Tensor:
     """Multiply a CSR sparse matrix by a dense vector: ``y = A @ x``.
 
@@ -49,12 +62,20 @@ def csr_matvec(a: CSRArray, x) -> torch.Tensor:
     device = default_torch_device()
     x = ensure_array(x, device=device)
     validate_csr_matvec_inputs(a.data, a.indices, a.indptr, x, a.shape)
+    if _tracked(a.data, x):
+        from mlx_sparse._autograd import CSRMatVec
+
+        return CSRMatVec.apply(a.data.to(x.device), x, a, True)
     data, indices, indptr = a.buffers(device)
     return _native.csr_matvec(data, indices, indptr, x, a.shape, plan=a.plan(device))
 
 
 def _csr_matmul_rank2(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
     validate_csr_matmul_inputs(a.data, a.indices, a.indptr, rhs, a.shape)
+    if _tracked(a.data, rhs):
+        from mlx_sparse._autograd import CSRMatMul
+
+        return CSRMatMul.apply(a.data.to(rhs.device), rhs, a, True)
     data, indices, indptr = a.buffers(rhs.device)
     return _native.csr_matmul(data, indices, indptr, rhs, a.shape, plan=None)
 
@@ -69,6 +90,17 @@ def _csr_matmul_batched(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
         )
     batch_shape = tuple(int(d) for d in rhs.shape[:-2])
     k = int(rhs.shape[-1])
+    if _tracked(a.data, rhs):
+        # one rank-2 product over the batch laid side by side: every output
+        # is still summed from zero in stored order, so the values equal the
+        # batched kernel's, and the rank-2 rules give the derivatives
+        from mlx_sparse._autograd import CSRMatMul
+
+        B = _prod(batch_shape)
+        wide = rhs.reshape(B, a.shape[1], k).permute(1, 0, 2).reshape(a.shape[1], B * k)
+        out = CSRMatMul.apply(a.data.to(rhs.device), wide, a, True)
+        out = out.reshape(a.shape[0], B, k).permute(1, 0, 2)
+        return out.reshape(*batch_shape, a.shape[0], k)
     flat = rhs.reshape(_prod(batch_shape), a.shape[1], k)
     data, indices, indptr = a.buffers(rhs.device)
     out = _native.csr_batched_matmul(data, indices, indptr, flat, a.shape)
@@ -128,6 +160,13 @@ def csr_batched_matvec(a: CSRArray, rhs) -> torch.Tensor:
         )
     batch_shape = tuple(int(d) for d in rhs.shape[:-1])
     flat = rhs.reshape(_prod(batch_shape), a.shape[1])
+    if _tracked(a.data, rhs):
+        # the batch as the columns of one rank-2 product (zero-start stored
+        # order, as the batched kernel sums)
+        from mlx_sparse._autograd import CSRMatMul
+
+        out = CSRMatMul.apply(a.data.to(rhs.device), flat.transpose(0, 1), a, True)
+        return out.transpose(0, 1).reshape(*batch_shape, a.shape[0])
     data, indices, indptr = a.buffers(rhs.device)
     out = _native.csr_batched_matvec(data, indices, indptr, flat, a.shape)
     return out.reshape(*batch_shape, a.shape[0])
@@ -150,3 +189,39 @@ def csr_batched_matmul(a: CSRArray, rhs) -> torch.Tensor:
             f"but sparse n_cols={a.shape[1]}."
         )
     return _csr_matmul_batched(a, rhs)
+
+
+def csr_matvec_transpose(a: CSRArray, x) -> torch.Tensor:
+    """``A^T x`` without materialising the transpose (no conjugation), for
+    ``x`` of shape ``(n_rows,)`` (reference: mlx_sparse/_native.py:260-270).
+    GPU: atomic scatter over A's rows; CPU: per-range partial outputs added in
+    range order, as in the reference.  For ``A.T @ x`` through the
+    materialised transpose use ``a.T @ x``."""
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_matvec_transpose expects CSRArray, got {type(a).__name__}.")
+    device = default_torch_device()
+    x = ensure_array(x, device=device)
+    if x.ndim != 1 or x.shape[0] != a.shape[0]:
+        raise ValueError(
+            f"csr_matvec_transpose expects x of shape ({a.shape[0]},), got {tuple(x.shape)}.")
+    if x.dtype != a.data.dtype:
+        raise TypeError("csr_matvec_transpose requires data and x to have the same dtype.")
+    data, indices, indptr = a.buffers(device)
+    return _native.csr_matvec_transpose(data, indices, indptr, x, a.shape)
+
+
+def csr_matmul_transpose(a: CSRArray, rhs) -> torch.Tensor:
+    """``A^T X`` without materialising the transpose, for ``rhs`` of shape
+    ``(n_rows, k)`` (reference: mlx_sparse/_native.py:367-377)."""
+    if not isinstance(a, CSRArray):
+        raise TypeError(f"csr_matmul_transpose expects CSRArray, got {type(a).__name__}.")
+    device = default_torch_device()
+    rhs = ensure_array(rhs, device=device)
+    if rhs.ndim != 2 or rhs.shape[0] != a.shape[0]:
+        raise ValueError(
+            f"csr_matmul_transpose expects rhs of shape ({a.shape[0]}, k), "
+            f"got {tuple(rhs.shape)}.")
+    if rhs.dtype != a.data.dtype:
+        raise TypeError("csr_matmul_transpose requires data and rhs to have the same dtype.")
+    data, indices, indptr = a.buffers(device)
+    return _native.csr_matmul_transpose(data, indices, indptr, rhs, a.shape)

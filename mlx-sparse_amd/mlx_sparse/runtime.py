@@ -9,7 +9,10 @@ cached row-block plan of the GPU SpMV; without it a plan-free kernel runs.
 gathers: "auto" (default: panels when the columns are scattered over an x of
 more than 8 MB and the matrix qualifies, else XCD slices), "off", "on" (XCD
 column slices) or "panels" (LDS column panels); it applies to plans built
-while it is set.
+while it is set.  ``GPU_ADJOINT`` (new) routes the A^H products of the
+gradients on the GPU: "atomic" (scatter over A's rows), "transpose" (a
+cached CSR of A^H, multiplied by the forward kernels) or "auto" (default:
+scatter on a matrix's first adjoint product, cached transpose after).
 """
 
 from __future__ import annotations
@@ -21,8 +24,9 @@ from collections.abc import Iterator, Mapping
 from typing import Any
 
 _ENV = {"n_threads": "MLX_SPARSE_CPU_THREADS", "gpu_plan": "MLX_SPARSE_GPU_PLAN",
-        "gpu_slice": "MLX_SPARSE_GPU_SLICE"}
+        "gpu_slice": "MLX_SPARSE_GPU_SLICE", "gpu_adjoint": "MLX_SPARSE_GPU_ADJOINT"}
 _SLICE = {"auto": 0, "off": 1, "on": 2, "panels": 3}
+_ADJOINT = ("auto", "atomic", "transpose")
 _MISSING = object()
 
 
@@ -30,6 +34,7 @@ class RuntimeOption(str, enum.Enum):
     N_THREADS = "n_threads"
     GPU_PLAN = "gpu_plan"
     GPU_SLICE = "gpu_slice"  # "auto" | "off" | "on" | "panels": reordered copy of plans
+    GPU_ADJOINT = "gpu_adjoint"  # "auto" | "atomic" | "transpose": route of A^H products
 
 
 def _parse_threads(value: Any) -> int | str:
@@ -67,6 +72,9 @@ def get(option: RuntimeOption | str) -> Any:
             return "auto"
     if key == "gpu_slice":
         return _SLICE.get((raw or "auto").strip().lower(), 0)
+    if key == "gpu_adjoint":
+        v = (raw or "auto").strip().lower()
+        return v if v in _ADJOINT else "auto"
     return True if raw is None else _parse_bool(raw)
 
 
@@ -80,6 +88,11 @@ def _normalize_option(option) -> str:
 
 
 def _encode(key: str, value: Any) -> str | None:
+    if key == "gpu_adjoint":
+        v = str(value).strip().lower()
+        if v not in _ADJOINT:
+            raise ValueError(f"gpu_adjoint must be one of {list(_ADJOINT)}, got {value!r}.")
+        return v
     if key == "gpu_slice":
         v = str(value).strip().lower()
         if v not in _SLICE:
@@ -166,6 +179,7 @@ def info() -> dict[str, Any]:
         "n_threads_source": source,
         "gpu_plan": get(RuntimeOption.GPU_PLAN),
         "gpu_slice": get(RuntimeOption.GPU_SLICE),
+        "gpu_adjoint": get(RuntimeOption.GPU_ADJOINT),
         "device": str(default_torch_device()),
         "extension": extension_available(),
         "gpu": gpu_name,

@@ -3,7 +3,10 @@
 // Mirrors the reference nanobind module's entry points for this path
 // (reference: src/bindings.cpp:279-295 `_compiled_capabilities`,
 // :874-883 `csr_matvec`, :905-915 `csr_batched_matvec`, :965-975
-// `csr_matmul`, :998-1008 `csr_batched_matmul`): same names and argument
+// `csr_matmul`, :998-1008 `csr_batched_matmul`, :661-665 `csr_transpose`,
+// :942-947 `csr_matvec_transpose`, :1035-1040 `csr_matmul_transpose`; the
+// value gradients, internal to the reference's VJPs, are bound as
+// `csr_matvec_data_vjp` / `csr_matmul_data_vjp`): same names and argument
 // order (data, indices, indptr, x | rhs, n_rows, n_cols).  Arrays are torch
 // tensors; the module reads their pointer, dtype, shape, strides and device
 // through the tensor's Python attributes, so no torch headers are compiled
@@ -21,6 +24,7 @@
 #include "common/array_view.h"
 #include "common/validate.h"
 #include "msx_sparse.h"
+#include "sparse/csr_adjoint/csr_adjoint.h"
 #include "sparse/csr_batched_matmul/csr_batched_matmul.h"
 #include "sparse/csr_batched_matvec/csr_batched_matvec.h"
 #include "sparse/csr_matmul/csr_matmul.h"
@@ -252,6 +256,108 @@ py::object csr_batched_matmul(py::handle data_o, py::handle indices_o, py::handl
   return out;
 }
 
+msx::ExecContext context_for(const ArrayView &v, int n_threads) {
+  msx::ExecContext ctx;
+  ctx.n_threads = n_threads;
+  ctx.stream = v.device >= 0 ? stream_for(v.device) : nullptr;
+  return ctx;
+}
+
+py::tuple csr_transpose(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                        int64_t n_rows, int64_t n_cols) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr);
+  if (vd.ndim != 1) msx::require_rank(vd, 1, "csr_transpose data");
+  if (vi.ndim != 1) msx::require_rank(vi, 1, "csr_transpose indices");
+  py::object od = empty_like_out(vd, data, py::make_tuple(vd.shape[0]));
+  py::object oi = empty_like_out(vi, indices, py::make_tuple(vi.shape[0]));
+  py::object op = empty_like_out(vp, indptr, py::make_tuple(std::max<int64_t>(n_cols, 0) + 1));
+  const ArrayView vod = view_of(od), voi = view_of(oi), vop = view_of(op);
+  const msx::ExecContext ctx = context_for(vd, 0);
+  if (vd.device >= 0) {
+    msx::csr_transpose(vd, vi, vp, vod, voi, vop, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_transpose(vd, vi, vp, vod, voi, vop, n_rows, n_cols, ctx);
+  }
+  return py::make_tuple(od, oi, op);
+}
+
+py::object csr_matvec_transpose(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                                py::handle x_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), x = contiguous(x_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vx = view_of(x);
+  py::object out = empty_like_out(vd, data, py::make_tuple(std::max<int64_t>(n_cols, 0)));
+  const ArrayView vo = view_of(out);
+  const msx::ExecContext ctx = context_for(vd, n_threads);
+  if (vd.device >= 0) {
+    msx::csr_matvec_transpose(vd, vi, vp, vx, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matvec_transpose(vd, vi, vp, vx, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
+py::object csr_matmul_transpose(py::handle data_o, py::handle indices_o, py::handle indptr_o,
+                                py::handle rhs_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), rhs = contiguous(rhs_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr),
+                  vr = view_of(rhs);
+  if (vr.ndim != 2) msx::require_rank(vr, 2, "csr_matmul_transpose rhs");
+  py::object out =
+      empty_like_out(vd, data, py::make_tuple(std::max<int64_t>(n_cols, 0), vr.shape[1]));
+  const ArrayView vo = view_of(out);
+  const msx::ExecContext ctx = context_for(vd, n_threads);
+  if (vd.device >= 0) {
+    msx::csr_matmul_transpose(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matmul_transpose(vd, vi, vp, vr, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
+py::object csr_matvec_data_vjp(py::handle indices_o, py::handle indptr_o, py::handle x_o,
+                               py::handle cot_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object indices = contiguous(indices_o), indptr = contiguous(indptr_o), x = contiguous(x_o),
+             cot = contiguous(cot_o);
+  const ArrayView vi = view_of(indices), vp = view_of(indptr), vx = view_of(x), vc = view_of(cot);
+  if (vi.ndim != 1) msx::require_rank(vi, 1, "csr_matvec_data_vjp indices");
+  py::object out = empty_like_out(vx, x, py::make_tuple(vi.shape[0]));
+  const ArrayView vo = view_of(out);
+  const msx::ExecContext ctx = context_for(vx, n_threads);
+  if (vx.device >= 0) {
+    msx::csr_matvec_data_vjp(vi, vp, vx, vc, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matvec_data_vjp(vi, vp, vx, vc, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
+py::object csr_matmul_data_vjp(py::handle indices_o, py::handle indptr_o, py::handle rhs_o,
+                               py::handle cot_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+  py::object indices = contiguous(indices_o), indptr = contiguous(indptr_o),
+             rhs = contiguous(rhs_o), cot = contiguous(cot_o);
+  const ArrayView vi = view_of(indices), vp = view_of(indptr), vr = view_of(rhs),
+                  vc = view_of(cot);
+  if (vi.ndim != 1) msx::require_rank(vi, 1, "csr_matmul_data_vjp indices");
+  py::object out = empty_like_out(vr, rhs, py::make_tuple(vi.shape[0]));
+  const ArrayView vo = view_of(out);
+  const msx::ExecContext ctx = context_for(vr, n_threads);
+  if (vr.device >= 0) {
+    msx::csr_matmul_data_vjp(vi, vp, vr, vc, vo, n_rows, n_cols, ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    msx::csr_matmul_data_vjp(vi, vp, vr, vc, vo, n_rows, n_cols, ctx);
+  }
+  return out;
+}
+
 py::dict plan_info(const Plan &plan) {
   msx_plan_info info{};
   msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_info");
@@ -344,6 +450,21 @@ PYBIND11_MODULE(_ext, m) {
         py::arg("indptr"), py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"),
         py::arg("n_threads") = 0,
         "Multiply CSR buffers by a batch of dense matrices (batch, n_cols, k).");
+  m.def("csr_transpose", &csr_transpose, py::arg("data"), py::arg("indices"), py::arg("indptr"),
+        py::arg("n_rows"), py::arg("n_cols"),
+        "CSR buffers of the transpose: (data, indices, indptr), shape (n_cols, n_rows).");
+  m.def("csr_matvec_transpose", &csr_matvec_transpose, py::arg("data"), py::arg("indices"),
+        py::arg("indptr"), py::arg("x"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0, "A^T x for CSR buffers of shape (n_rows, n_cols).");
+  m.def("csr_matmul_transpose", &csr_matmul_transpose, py::arg("data"), py::arg("indices"),
+        py::arg("indptr"), py::arg("rhs"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0, "A^T X for CSR buffers of shape (n_rows, n_cols).");
+  m.def("csr_matvec_data_vjp", &csr_matvec_data_vjp, py::arg("indices"), py::arg("indptr"),
+        py::arg("x"), py::arg("cotangent"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0, "Gradient of A x with respect to the stored values.");
+  m.def("csr_matmul_data_vjp", &csr_matmul_data_vjp, py::arg("indices"), py::arg("indptr"),
+        py::arg("rhs"), py::arg("cotangent"), py::arg("n_rows"), py::arg("n_cols"),
+        py::arg("n_threads") = 0, "Gradient of A X with respect to the stored values.");
   m.def("cpu_worker_count", &msx_cpu_worker_count, "Resolved CPU worker count.");
   m.def(
       "cpu_ranges",
