@@ -25,6 +25,9 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
   headline matrix;
 - ``batched_spmv``: 8 vectors at once on the same Poisson matrix (native
   batched entry point), against 8 single SpMVs;
+- ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
+  the cached transpose, the transpose build, the SpMV value gradient and one
+  autograd step (forward + ``A^T g``);
 - ``cpu_baseline``: the C restatement of the reference CPU kernel
   (oracle/, ``-O3`` without ``-march=native``), threads split like the
   reference, timed on this host's cores on the same matrix.
@@ -151,6 +154,63 @@ def cpu_baseline(m, x, seconds: float = 12.0) -> dict:
     }
 
 
+def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
+    """The adjoint path on the headline matrix, HIP events around back-to-back
+    calls (the transpose and the f16 products take stream-ordered scratch):
+
+    - ``A^T x`` by atomic scatter (msx_csr_spmv_transpose), compulsory bytes
+      as the SpMV's;
+    - the CSR transpose build (radix sort; read and write nnz*(4+4) + (n+1)*4);
+    - ``A^T x`` as SpMV over the cached transpose with its own plan;
+    - the SpMV value gradient (indices + indptr + x + cot read, nnz*4 written);
+    - one autograd step ``(A @ x).backward(g)`` with x requiring grad
+      (forward SpMV + A^T g over the cached transpose, "auto" route warm)."""
+    n_rows, n_cols = m.shape
+    data, indices, indptr = A.buffers(x.device)
+    g = torch.randn(n_rows, device=x.device, generator=torch.Generator(x.device).manual_seed(4))
+    out = {"workload": "random16 n=4194304 nnz=67108864 f32/i32 (the headline matrix)"}
+    scatter = lambda: ext.csr_matvec_transpose(data, indices, indptr, g, n_rows, n_cols)
+    for _ in range(3):
+        scatter()
+    t = _events_time(scatter, 20)
+    out["atomic_us"] = round(t * 1e3, 1)
+    out["atomic_frac"] = round(spmv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    build = lambda: ext.csr_transpose(data, indices, indptr, n_rows, n_cols)
+    build()
+    t = _events_time(build, 5)
+    tb = 2 * (m.nnz * 8 + (n_cols + 1) * 4)
+    out["transpose_build_us"] = round(t * 1e3, 1)
+    out["transpose_build_frac"] = round(tb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    T = A.T
+    td, ti, tp = T.buffers(x.device)
+    tplan = T.plan(x.device)
+    cached = lambda: ext.csr_matvec(td, ti, tp, g, n_cols, n_rows, plan=tplan)
+    for _ in range(3):
+        cached()
+    t = _events_time(cached, 20)
+    out["cached_transpose_us"] = round(t * 1e3, 1)
+    out["cached_transpose_frac"] = round(spmv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    vjp = lambda: ext.csr_matvec_data_vjp(indices, indptr, x, g, n_rows, n_cols)
+    for _ in range(3):
+        vjp()
+    t = _events_time(vjp, 20)
+    vb = m.nnz * 8 + (n_rows + 1) * 4 + 4 * (n_rows + n_cols)
+    out["data_vjp_us"] = round(t * 1e3, 1)
+    out["data_vjp_frac"] = round(vb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    xr = x.clone().requires_grad_()
+
+    def train_step():
+        xr.grad = None
+        (A @ xr).backward(g)
+
+    for _ in range(3):
+        train_step()
+    t = _events_time(train_step, 20)
+    out["autograd_step_us"] = round(t * 1e3, 1)
+    log(f"adjoint: {out}")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,6 +218,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
+    ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
@@ -283,6 +344,11 @@ def main() -> int:
                  "frac": round(cold_gbs / HBM_PEAK_GBS, 4)},
     }
     del y
+
+    # ---- adjoint path on the headline matrix ---------------------------------------
+    if not args.no_adjoint:
+        result["adjoint"] = adjoint_leg(ext, A, m, x, nbytes)
+        torch.cuda.empty_cache()
 
     # ---- SpMM k=64 on the 3D Poisson matrix --------------------------------------
     if not args.no_spmm:

@@ -85,16 +85,20 @@ __global__ void __launch_bounds__(kThreads)
 // ---------------------------------------------------------------------------
 // Transpose build.
 
-// key[p] = column of p (n_cols when out of range), row[p] = its row, pos[p] = p.
+// key[p] = column of p (n_cols when out of range), row[p] = its row; G
+// lanes per row.
 template <class I>
 __global__ void __launch_bounds__(kThreads)
     column_keys(const I *__restrict__ indices, const I *__restrict__ indptr, int64_t n_rows,
-                int64_t nnz, int64_t n_cols, uint32_t *__restrict__ key, I *__restrict__ row) {
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n_rows;
-       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+                int64_t nnz, int64_t n_cols, int G, uint32_t *__restrict__ key,
+                I *__restrict__ row) {
+  const int64_t rows_per_block = kThreads / G;
+  const int j = threadIdx.x % G;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
+       r < n_rows; r += static_cast<int64_t>(gridDim.x) * rows_per_block) {
     const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
     const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
-    for (int64_t p = s; p < e; ++p) {
+    for (int64_t p = s + j; p < e; p += G) {
       const int64_t c = static_cast<int64_t>(indices[p]);
       key[p] = (c >= 0 && c < n_cols) ? static_cast<uint32_t>(c) : static_cast<uint32_t>(n_cols);
       row[p] = static_cast<I>(r);
@@ -141,6 +145,106 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Packed path (values of at most 4 bytes): the sort carries (row << 32) |
+// value bits, so the transposed arrays come out of one coalesced pass.
+// key[p] = column of p (n_cols when out of range), val[p] = packed pair;
+// G lanes per row.
+template <class S, class I>
+__global__ void __launch_bounds__(kThreads)
+    packed_keys(const S *__restrict__ data, const I *__restrict__ indices,
+                const I *__restrict__ indptr, int64_t n_rows, int64_t nnz, int64_t n_cols, int G,
+                uint32_t *__restrict__ key, uint64_t *__restrict__ val) {
+  static_assert(sizeof(S) <= 4, "packed transpose holds values of at most 4 bytes");
+  const int64_t rows_per_block = kThreads / G;
+  const int j = threadIdx.x % G;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / G;
+       r < n_rows; r += static_cast<int64_t>(gridDim.x) * rows_per_block) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+    for (int64_t p = s + j; p < e; p += G) {
+      const int64_t c = static_cast<int64_t>(indices[p]);
+      key[p] = (c >= 0 && c < n_cols) ? static_cast<uint32_t>(c) : static_cast<uint32_t>(n_cols);
+      uint32_t bits = 0;
+      __builtin_memcpy(&bits, &data[p], sizeof(S));
+      val[p] = (static_cast<uint64_t>(r) << 32) | bits;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+    drop_keys(int64_t nnz, uint32_t drop, uint32_t *__restrict__ key) {
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; p < nnz;
+       p += static_cast<int64_t>(gridDim.x) * kThreads)
+    key[p] = drop;
+}
+
+// Sorted pairs -> t_data, t_indices, and t_indptr[c] = first sorted index
+// with key >= c, written by the index where the key crosses c.
+template <class S, class I>
+__global__ void __launch_bounds__(kThreads)
+    packed_unpack(const uint32_t *__restrict__ key, const uint64_t *__restrict__ val, int64_t nnz,
+                  int64_t n_cols, S *__restrict__ t_data, I *__restrict__ t_indices,
+                  I *__restrict__ t_indptr) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i <= nnz;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t prev = i == 0 ? -1 : static_cast<int64_t>(key[i - 1]);
+    const int64_t cur = i == nnz ? n_cols : static_cast<int64_t>(key[i]);
+    for (int64_t c = prev + 1; c <= cur && c <= n_cols; ++c) t_indptr[c] = static_cast<I>(i);
+    if (i < nnz && cur < n_cols) {
+      const uint64_t v = val[i];
+      const uint32_t bits = static_cast<uint32_t>(v);
+      S d;
+      __builtin_memcpy(&d, &bits, sizeof(S));
+      t_data[i] = d;
+      t_indices[i] = static_cast<I>(v >> 32);
+    }
+  }
+}
+
+int lanes_for(int64_t n_rows, int64_t nnz);
+
+template <class S, class I>
+msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                            const void *indices, const void *indptr, void *t_data,
+                            void *t_indices, void *t_indptr, int end_bit, hipStream_t stream) {
+  const size_t b4 = (static_cast<size_t>(nnz) * 4 + 255) / 256 * 256;
+  const size_t b8 = (static_cast<size_t>(nnz) * 8 + 255) / 256 * 256;
+  size_t sort_bytes = 0;
+  MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint64_t *>(nullptr),
+                                                 static_cast<uint64_t *>(nullptr),
+                                                 static_cast<int>(nnz), 0, end_bit, stream));
+  char *scratch = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&scratch), 2 * b4 + 2 * b8 + sort_bytes, stream));
+  auto *key = reinterpret_cast<uint32_t *>(scratch);
+  auto *key_out = reinterpret_cast<uint32_t *>(scratch + b4);
+  auto *val = reinterpret_cast<uint64_t *>(scratch + 2 * b4);
+  auto *val_out = reinterpret_cast<uint64_t *>(scratch + 2 * b4 + b8);
+  void *sort_tmp = scratch + 2 * b4 + 2 * b8;
+  const int G = lanes_for(n_rows, nnz);
+  hipLaunchKernelGGL(drop_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
+                     static_cast<uint32_t>(n_cols), key);
+  hipLaunchKernelGGL((packed_keys<S, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+                     static_cast<const S *>(data), static_cast<const I *>(indices),
+                     static_cast<const I *>(indptr), n_rows, nnz, n_cols, G, key, val);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipcub::DeviceRadixSort::SortPairs(sort_tmp, sort_bytes, key, key_out, val, val_out,
+                                           static_cast<int>(nnz), 0, end_bit, stream);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL((packed_unpack<S, I>), dim3(grid_for(nnz + 1)), dim3(kThreads), 0, stream,
+                       key_out, val_out, nnz, n_cols, static_cast<S *>(t_data),
+                       static_cast<I *>(t_indices), static_cast<I *>(t_indptr));
+    e = hipGetLastError();
+  }
+  msx_status st = MSX_OK;
+  if (e != hipSuccess) st = hip_fail(e, "csr_transpose");
+  const hipError_t ef = hipFreeAsync(scratch, stream);
+  if (st == MSX_OK && ef != hipSuccess) st = hip_fail(ef, "csr_transpose scratch release");
+  return st;
+}
+
 int bits_for(uint64_t v) {
   int b = 0;
   while (b < 64 && (v >> b) != 0) ++b;
@@ -159,10 +263,14 @@ msx_status transpose_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const vo
     MSX_HIP_TRY(hipGetLastError());
     return MSX_OK;
   }
+  const int end_bit = bits_for(static_cast<uint64_t>(n_cols));  // keys <= n_cols
+  if constexpr (sizeof(S) <= 4)
+    return transpose_packed<S, I>(n_rows, n_cols, nnz, data, indices, indptr, t_data, t_indices,
+                                  t_indptr, end_bit, stream);
+  // Wider values: sort (column, position), then gather values and rows.
   // Scratch: 4 key/position arrays, the row of each value, the sort's temp.
   const size_t b4 = (static_cast<size_t>(nnz) * 4 + 255) / 256 * 256;
   const size_t bI = (static_cast<size_t>(nnz) * sizeof(I) + 255) / 256 * 256;
-  const int end_bit = bits_for(static_cast<uint64_t>(n_cols));  // keys <= n_cols
   size_t sort_bytes = 0;
   MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint32_t *>(nullptr),
                                                  static_cast<uint32_t *>(nullptr),
@@ -180,8 +288,9 @@ msx_status transpose_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const vo
   msx_status st = MSX_OK;
   hipLaunchKernelGGL(init_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
                      static_cast<uint32_t>(n_cols), key, pos);
-  hipLaunchKernelGGL((column_keys<I>), dim3(grid_for(n_rows)), dim3(kThreads), 0, stream,
-                     static_cast<const I *>(indices), ip, n_rows, nnz, n_cols, key, row);
+  const int G = lanes_for(n_rows, nnz);
+  hipLaunchKernelGGL((column_keys<I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+                     static_cast<const I *>(indices), ip, n_rows, nnz, n_cols, G, key, row);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess)
     e = hipcub::DeviceRadixSort::SortPairs(sort_tmp, sort_bytes, key, key_out, pos, pos_out,

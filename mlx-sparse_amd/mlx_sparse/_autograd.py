@@ -51,7 +51,8 @@ def _adjoint_csr(a, data: torch.Tensor):
         a._cache[seen] = a._cache.get(seen, 0) + 1
         if a._cache[seen] < 2:
             return None
-    hit = a.conj()._transpose_on(device)
+    # real values: A^H is A^T, shared with the array's own cached transpose
+    hit = a.conj()._transpose_on(device) if a.data.is_complex() else a._transpose_on(device)
     a._cache[key] = hit
     return hit
 
