@@ -91,6 +91,18 @@ def _distinct_sorted_columns(lengths: np.ndarray, n_cols: int, rng) -> tuple[np.
     """Per-row distinct sorted columns, uniform without replacement: draw with
     replacement, drop duplicates, redraw the shortfall until none is left."""
     n = lengths.shape[0]
+    # Rows holding more than an eighth of the columns are drawn directly
+    # without replacement: redrawing duplicates would need many rounds there.
+    wide = np.flatnonzero(lengths > n_cols // 8)
+    if wide.size:
+        narrow = lengths.copy()
+        narrow[wide] = 0
+        rows, cols = _distinct_sorted_columns(narrow, n_cols, rng)
+        extra = [np.sort(rng.choice(n_cols, size=int(lengths[r]), replace=False)) for r in wide]
+        rows = np.concatenate([rows] + [np.full(e.size, r, np.int64) for r, e in zip(wide, extra)])
+        cols = np.concatenate([cols] + [e.astype(np.int64) for e in extra])
+        order = np.argsort(rows * n_cols + cols, kind="stable")
+        return rows[order], cols[order]
     rows = np.repeat(np.arange(n, dtype=np.int64), lengths)
     cols = rng.integers(0, n_cols, size=rows.shape[0], dtype=np.int64)
     while True:
