@@ -25,6 +25,9 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
   headline matrix;
 - ``batched_spmv``: 8 vectors at once on the same Poisson matrix (native
   batched entry point), against 8 single SpMVs;
+- ``cg``: conjugate gradients (device-resident loop) on the Poisson matrix,
+  time per iteration against its bytes, and the single-threaded reference
+  loop on the host;
 - ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
   the cached transpose, the transpose build, the SpMV value gradient and one
   autograd step (forward + ``A^T g``);
@@ -211,6 +214,53 @@ def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
     return out
 
 
+def cg_leg(dev) -> dict:
+    """Conjugate gradients (``linalg.cg``, device-resident loop) on the 3D
+    Poisson matrix 128^3, b = 1, x0 = 0, rtol = 1e-6.  Bytes per iteration:
+    the SpMV's compulsory bytes plus 11 float vectors of n (p.ap reads p, ap;
+    the update reads x, p, r, ap and writes x, r; the direction reads r, p and
+    writes p).  The CPU figure is the oracle's single-threaded restatement of
+    the reference CPU loop (cg.cpp:75-246) on the same system, 20 iterations."""
+    import mlx_sparse as ms
+    from mlx_sparse import linalg, synthetic
+    from oracle import oracle as orc
+
+    p = synthetic.poisson_3d(128)
+    n = p.shape[0]
+    P = ms.csr_array((p.data, p.indices, p.indptr), shape=p.shape, canonical=True)
+    b = torch.ones(n, device=dev)
+    P.plan(dev)
+    x, info = linalg.cg(P, b, rtol=1e-6, return_info=True)  # warm-up (plan, allocator)
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        x, info = linalg.cg(P, b, rtol=1e-6, return_info=True)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    solve_s = statistics.median(times)
+    its = info.iterations
+    per_it = solve_s / max(its, 1)
+    it_bytes = synthetic.compulsory_bytes(p.nnz, n, n, 4, 4) + 11 * 4 * n
+    t0 = time.perf_counter()
+    _, cinfo, _, cits = orc.csr_cg(p.data, p.indices, p.indptr, np.ones(n, np.float32),
+                                   rtol=1e-6, maxiter=20)
+    cpu_per_it = (time.perf_counter() - t0) / max(cits, 1)
+    out = {
+        "workload": "poisson3d 128^3 n=2097152 nnz=14581760 f32/i32, b=1, x0=0, rtol=1e-6",
+        "info": info.status, "iterations": its, "residual": info.residual_norm,
+        "solve_ms": round(solve_s * 1e3, 2), "us_per_iteration": round(per_it * 1e6, 1),
+        "bytes_per_iteration": it_bytes,
+        "gbs": round(it_bytes / per_it / 1e9, 1),
+        "frac": round(it_bytes / per_it / 1e9 / HBM_PEAK_GBS, 4),
+        "cpu_us_per_iteration": round(cpu_per_it * 1e6, 1),
+        "cpu_sample": "oracle CG (one thread, the reference loop), 20 iterations",
+        "speedup_per_iteration": round(cpu_per_it / per_it, 1),
+    }
+    log(f"cg: {out}")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +269,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
     ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg")
+    ap.add_argument("--no-cg", action="store_true", help="skip the conjugate gradient leg")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
@@ -410,6 +461,11 @@ def main() -> int:
         }
         log(f"batched spmv x{B}: {bat_ms * 1e3:.1f} us ({B * spmv_ms * 1e3:.1f} us as {B} SpMVs)")
         del P, Xp, xp, pd, pi, pp, pplan, Vb
+
+    # ---- conjugate gradients on the Poisson matrix --------------------------------
+    if not args.no_cg:
+        result["cg"] = cg_leg(dev)
+        torch.cuda.empty_cache()
 
     # ---- CPU baseline (reference CPU kernel restated in C) -------------------------
     if not args.no_cpu:

@@ -380,6 +380,74 @@ msx_status msx_csr_spmm_data_vjp_cpu(msx_vtype vt, msx_itype it,
                                      int n_threads);
 
 /*
+ * Result of an iterative solve.  info: 0 converged (||r|| <= max(atol,
+ * rtol * ||b||)); > 0 the iteration budget ran out (maxiter, or 1 when
+ * maxiter is 0); -1 near-zero denominator; -2 non-positive preconditioned
+ * product r.z; -3 non-finite scalar or vector.  residual: norm of the final
+ * residual; iterations: completed iterations.
+ */
+typedef struct msx_solver_result {
+  int32_t info;
+  int32_t iterations;
+  float residual;
+  int32_t reserved;
+} msx_solver_result;
+
+/*
+ * Conjugate gradients for a square symmetric positive-definite float32 CSR
+ * matrix (n x n): x from x0 (device pointers; x0 and x may not overlap).
+ * Device-wide: the path's SpMV with `plan` (nullable; a plan from
+ * msx_csr_plan_create[_bound] for this matrix) and fused vector kernels,
+ * scalars kept on the device; the host reads the solver state between
+ * batches of iterations, so the call returns when the solve is over
+ * (`stream` is synchronised; scratch from its stream-ordered allocator).
+ * Dot products are double sums added per workgroup in a fixed order, so
+ * results are reproducible run to run; they agree with the sequential CPU
+ * loop to rounding.
+ *
+ * Replaces CSRCG::eval_gpu (reference: src/linalg/cg/cg.cpp:277-327, the
+ * single-threadgroup kernel csr_cg in cg.metal) with the arithmetic of
+ * csr_cg_cpu_impl (cg.cpp:75-246): float SpMV summed from zero, double dot
+ * products and updates, the same tolerance and status rules.
+ */
+msx_status msx_csr_cg(msx_itype it, int64_t n, int64_t nnz, const float *data,
+                      const void *indices, const void *indptr, const float *b,
+                      const float *x0, float *x, float rtol, float atol,
+                      int64_t maxiter, const msx_csr_plan *plan,
+                      msx_solver_result *result, void *stream);
+
+/*
+ * Jacobi-preconditioned CG (z = inv_diag * r), float scalars from double
+ * sums and float vector updates.  Replaces CSRPCGJacobi::eval_gpu
+ * (reference: src/preconditioners/pcg/pcg.cpp, pcg.metal:18) with the
+ * arithmetic of csr_pcg_jacobi_cpu_impl (pcg.cpp:71-236).
+ */
+msx_status msx_csr_pcg_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                              const float *data, const void *indices,
+                              const void *indptr, const float *b,
+                              const float *x0, const float *inv_diag, float *x,
+                              float rtol, float atol, int64_t maxiter,
+                              const msx_csr_plan *plan,
+                              msx_solver_result *result, void *stream);
+
+/*
+ * Host (CPU) solvers, host pointers: the reference's sequential loops
+ * (csr_cg_cpu_impl, cg.cpp:75-246; csr_pcg_jacobi_cpu_impl,
+ * pcg.cpp:71-236), one thread.
+ */
+msx_status msx_csr_cg_cpu(msx_itype it, int64_t n, int64_t nnz,
+                          const float *data, const void *indices,
+                          const void *indptr, const float *b, const float *x0,
+                          float *x, float rtol, float atol, int64_t maxiter,
+                          msx_solver_result *result);
+msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                  const float *data, const void *indices,
+                                  const void *indptr, const float *b,
+                                  const float *x0, const float *inv_diag,
+                                  float *x, float rtol, float atol,
+                                  int64_t maxiter, msx_solver_result *result);
+
+/*
  * Host (CPU) SpMV with host pointers, the `use_cpu()` device: rows are summed
  * sequentially in stored order, rows are split over `n_threads` std::threads
  * in nnz-balanced contiguous ranges (n_threads <= 0: the resolved worker

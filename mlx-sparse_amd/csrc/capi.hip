@@ -62,6 +62,8 @@ msx_status check_common(const char *op, msx_vtype vt, msx_itype it, int64_t n_ro
   return MSX_OK;
 }
 
+}  // namespace
+
 msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, msx_itype it,
                       int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
                       const void *indices) {
@@ -78,7 +80,6 @@ msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, ms
   return MSX_OK;
 }
 
-}  // namespace
 }  // namespace msx
 
 using namespace msx;

@@ -103,6 +103,13 @@ struct msx_csr_plan {
 
 namespace msx {
 
+// A plan passed with a matrix must have been built for it (same index type,
+// rows and values; a bound plan also the same buffers, value type and
+// columns) on the current device (capi.hip).
+msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, msx_itype it,
+                      int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                      const void *indices);
+
 // Launchers (csr_spmv.hip / csr_spmm.hip).  Arguments are already checked.
 msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr,

@@ -5,7 +5,7 @@ hand-written gfx950 HIP kernels behind the C ABI in ``include/msx_sparse.h``.
 
 from __future__ import annotations
 
-from mlx_sparse import runtime
+from mlx_sparse import linalg, runtime
 from mlx_sparse._csr import CSRArray, csr_array
 from mlx_sparse._device import default_torch_device, use_cpu, use_device, use_gpu
 from mlx_sparse._ops import (
@@ -41,6 +41,7 @@ __all__ = [
     "csr_matvec_transpose",
     "default_torch_device",
     "is_available",
+    "linalg",
     "runtime",
     "use_cpu",
     "use_device",

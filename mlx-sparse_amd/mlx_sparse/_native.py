@@ -61,6 +61,20 @@ def csr_matmul_data_vjp(indices, indptr, rhs, cotangent, shape: Shape2D) -> torc
     return extension().csr_matmul_data_vjp(indices, indptr, rhs, cotangent, shape[0], shape[1])
 
 
+def csr_cg(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
+           maxiter: int, plan=None):
+    """(x, info, residual, iterations) (reference: mlx_sparse/_native.py:883-905)."""
+    return extension().csr_cg(data, indices, indptr, b, x0, shape[0], shape[1], rtol, atol,
+                              maxiter, plan=plan)
+
+
+def csr_pcg_jacobi(data, indices, indptr, b, x0, inv_diag, shape: Shape2D, *, rtol: float,
+                   atol: float, maxiter: int, plan=None):
+    """(x, info, residual, iterations) (reference: mlx_sparse/_native.py:1139-1166)."""
+    return extension().csr_pcg_jacobi(data, indices, indptr, b, x0, inv_diag, shape[0], shape[1],
+                                      rtol, atol, maxiter, plan=plan)
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

@@ -1,0 +1,95 @@
+"""Conjugate gradients (reference: mlx_sparse/linalg/_iterative.py:69-323 ``cg``;
+native loops src/linalg/cg/cg.cpp, src/preconditioners/pcg/pcg.cpp).
+
+On the GPU the whole loop runs on the device (``msx_csr_cg``): the path's SpMV
+with the matrix's cached plan, fused vector passes, scalars on the device.
+With ``use_cpu()`` the reference's sequential loop runs natively.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import mlx_sparse._native as _native
+from mlx_sparse._csr import CSRArray
+from mlx_sparse._device import default_torch_device
+from mlx_sparse._validation import ensure_array
+from mlx_sparse.linalg import preconditioners as _pc
+from mlx_sparse.linalg._info import finish
+
+
+def _float32_csr(A) -> CSRArray:
+    if not isinstance(A, CSRArray):
+        if isinstance(A, torch.Tensor):
+            raise TypeError("sparse iterative solvers expect a CSRArray; use torch.linalg for "
+                            "dense arrays.")
+        raise TypeError(f"sparse iterative solvers expect a CSRArray, got {type(A).__name__}.")
+    if A.shape[0] != A.shape[1]:
+        raise ValueError(f"cg requires a square matrix, got {A.shape}.")
+    if A.dtype != torch.float32:
+        if A.dtype.is_complex:
+            raise TypeError("sparse iterative solvers currently use float32 values.")
+        A = CSRArray(A.data.to(torch.float32), A.indices, A.indptr, A.shape,
+                     A.sorted_indices, A.has_canonical_format)
+    return A
+
+
+def _float32_vector(x, device) -> torch.Tensor:
+    t = ensure_array(x, device=device)
+    if t.is_complex():
+        raise TypeError("sparse iterative solvers currently use float32 values.")
+    return t.to(torch.float32).contiguous()
+
+
+def cg(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, maxiter: int | None = None,
+       M=None, callback=None, return_info: bool = False):
+    """Solve a sparse SPD system ``A @ x = b`` with conjugate gradients.
+
+    Stops when ``||r|| <= max(atol, rtol * ||b||)``.  ``maxiter`` defaults to
+    ``10 * n``.  ``M``: ``None`` or ``preconditioners.identity`` (plain CG),
+    ``preconditioners.diagonal`` / ``jacobi`` (Jacobi-preconditioned CG), or a
+    rank-1 inverse diagonal.
+
+    Returns ``(x, info)``: ``info`` 0 converged; > 0 the iteration count at
+    which the budget ran out; < 0 breakdown (-1 near-zero denominator, -2
+    non-positive preconditioned product, -3 non-finite).  With
+    ``return_info=True`` a :class:`SolverInfo` replaces the integer.
+    """
+    csr = _float32_csr(A)
+    device = default_torch_device()
+    rhs = _float32_vector(b, device)
+    if rhs.ndim != 1:
+        raise ValueError(f"right-hand side must be rank-1, got {tuple(rhs.shape)}.")
+    if rhs.shape[0] != csr.shape[0]:
+        raise ValueError(f"b has length {rhs.shape[0]}, expected {csr.shape[0]}.")
+    if x0 is None:
+        guess = torch.zeros(csr.shape[1], dtype=torch.float32, device=device)
+    else:
+        guess = _float32_vector(x0, device)
+        if guess.ndim != 1 or guess.shape[0] != csr.shape[1]:
+            raise ValueError(f"x0 must have shape ({csr.shape[1]},), got {tuple(guess.shape)}.")
+    maxiter_value = 10 * csr.shape[1] if maxiter is None else int(maxiter)
+    if maxiter_value < 0:
+        raise ValueError("maxiter must be non-negative.")
+    data, indices, indptr = csr.buffers(device)
+    plan = csr.plan(device)
+    kind = None
+    inv_diag = None
+    if M is not None:
+        pc = _pc.aspreconditioner(M, csr)
+        kind = pc.kind
+        if isinstance(pc, _pc.DiagonalPreconditioner):
+            if pc.inverse_diagonal.shape[0] != csr.shape[0]:
+                raise ValueError("preconditioner size does not match the matrix.")
+            inv_diag = pc.inverse_diagonal.to(device=device, dtype=torch.float32).contiguous()
+    if inv_diag is None:
+        x, info, residual, iterations = _native.csr_cg(
+            data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
+            maxiter=maxiter_value, plan=plan)
+    else:
+        x, info, residual, iterations = _native.csr_pcg_jacobi(
+            data, indices, indptr, rhs, guess, inv_diag, csr.shape, rtol=float(rtol),
+            atol=float(atol), maxiter=maxiter_value, plan=plan)
+    return finish(x, info, residual, iterations, solver="cg", return_info=bool(return_info),
+                  callback=callback, rtol=float(rtol), atol=float(atol), maxiter=maxiter_value,
+                  preconditioner=kind)

@@ -24,6 +24,7 @@
 #include "common/array_view.h"
 #include "common/validate.h"
 #include "msx_sparse.h"
+#include "linalg/csr_cg.h"
 #include "sparse/csr_adjoint/csr_adjoint.h"
 #include "sparse/csr_batched_matmul/csr_batched_matmul.h"
 #include "sparse/csr_batched_matvec/csr_batched_matvec.h"
@@ -358,6 +359,36 @@ py::object csr_matmul_data_vjp(py::handle indices_o, py::handle indptr_o, py::ha
   return out;
 }
 
+py::tuple solve_cg(py::handle data_o, py::handle indices_o, py::handle indptr_o, py::handle b_o,
+                   py::handle x0_o, py::object inv_diag_o, int64_t n_rows, int64_t n_cols,
+                   float rtol, float atol, int64_t maxiter, py::object plan) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), b = contiguous(b_o), x0 = contiguous(x0_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vb = view_of(b),
+                  vx0 = view_of(x0);
+  py::object inv;
+  ArrayView vinv;
+  if (!inv_diag_o.is_none()) {
+    inv = contiguous(inv_diag_o);
+    vinv = view_of(inv);
+  }
+  if (vb.ndim != 1) msx::require_rank(vb, 1, inv_diag_o.is_none() ? "csr_cg b" : "csr_pcg_jacobi b");
+  py::object x = empty_like_out(vb, b, py::make_tuple(vb.shape[0]));
+  const ArrayView vx = view_of(x);
+  const msx::ExecContext ctx = context_for(vd, 0);
+  msx_solver_result res{};
+  const ArrayView *pinv = inv_diag_o.is_none() ? nullptr : &vinv;
+  if (vd.device >= 0) {
+    res = msx::csr_cg(vd, vi, vp, vb, vx0, pinv, vx, n_rows, n_cols, rtol, atol, maxiter,
+                      plan_ptr(plan), ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    res = msx::csr_cg(vd, vi, vp, vb, vx0, pinv, vx, n_rows, n_cols, rtol, atol, maxiter, nullptr,
+                      ctx);
+  }
+  return py::make_tuple(x, res.info, res.residual, res.iterations);
+}
+
 py::dict plan_info(const Plan &plan) {
   msx_plan_info info{};
   msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_info");
@@ -465,6 +496,29 @@ PYBIND11_MODULE(_ext, m) {
   m.def("csr_matmul_data_vjp", &csr_matmul_data_vjp, py::arg("indices"), py::arg("indptr"),
         py::arg("rhs"), py::arg("cotangent"), py::arg("n_rows"), py::arg("n_cols"),
         py::arg("n_threads") = 0, "Gradient of A X with respect to the stored values.");
+  m.def(
+      "csr_cg",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         int64_t n_rows, int64_t n_cols, float rtol, float atol, int64_t maxiter, py::object plan) {
+        return solve_cg(data, indices, indptr, b, x0, py::none(), n_rows, n_cols, rtol, atol,
+                        maxiter, plan);
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("maxiter"),
+      py::arg("plan") = py::none(),
+      "Conjugate gradients: (x, info, residual, iterations).");
+  m.def(
+      "csr_pcg_jacobi",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         py::handle inv_diag, int64_t n_rows, int64_t n_cols, float rtol, float atol,
+         int64_t maxiter, py::object plan) {
+        return solve_cg(data, indices, indptr, b, x0, py::reinterpret_borrow<py::object>(inv_diag),
+                        n_rows, n_cols, rtol, atol, maxiter, plan);
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
+      py::arg("atol"), py::arg("maxiter"), py::arg("plan") = py::none(),
+      "Jacobi-preconditioned conjugate gradients: (x, info, residual, iterations).");
   m.def("cpu_worker_count", &msx_cpu_worker_count, "Resolved CPU worker count.");
   m.def(
       "cpu_ranges",

@@ -24,7 +24,12 @@
  *     the transposed products with their per-range partial outputs added in
  *     range order (src/sparse/csr_matvec_transpose/csr_matvec_transpose.cpp,
  *     csr_matmul_transpose/csr_matmul_transpose.cpp, *_cpu_impl) and the
- *     value gradients (csr_matvec_data_vjp.cpp, csr_matmul_data_vjp.cpp).
+ *     value gradients (csr_matvec_data_vjp.cpp, csr_matmul_data_vjp.cpp);
+ *   - the conjugate gradient solver (src/linalg/cg/cg.cpp:75-246,
+ *     csr_cg_cpu_impl) with its float SpMV summed from zero
+ *     (src/linalg/common/common.h:35-45, csr_spmv_float), and the
+ *     Jacobi-preconditioned CG (src/preconditioners/pcg/pcg.cpp:71-236,
+ *     csr_pcg_jacobi_cpu_impl), float32 values only.
  *
  * Built with -ffp-contract=off so every product and every sum is rounded on
  * its own, as the reference's separate multiply_accumulate / `+=` are.
@@ -39,7 +44,9 @@
  */
 #define _GNU_SOURCE
 #include <errno.h>
+#include <float.h>
 #include <limits.h>
+#include <math.h>
 #include <pthread.h>
 #include <sched.h>
 #include <stdint.h>
@@ -634,5 +641,288 @@ int oracle_csr_data_vjp(int vt, int it, int64_t n_rows, int64_t n_cols, int64_t 
         narrow_store(vt, out, p, acc);
       }
     }
+  return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Krylov solvers (float32).  The solver SpMV sums each row from 0.0f in
+ * stored order; scalars and dot products are double unless noted. */
+
+static void cg_spmv(int it, int64_t n, const float *data, const void *indices, const void *indptr,
+                    const float *x, float *out) {
+  for (int64_t r = 0; r < n; ++r) {
+    float acc = 0.0f;
+    for (int64_t p = load_index(it, indptr, r); p < load_index(it, indptr, r + 1); ++p) {
+      const int64_t c = load_index(it, indices, p);
+      if (c >= 0 && c < n) acc = acc + data[p] * x[c];
+    }
+    out[r] = acc;
+  }
+}
+
+static int fin(float v) { return isfinite(v); }
+
+/* Conjugate gradients: x from x0; info 0 converged, maxiter (or 1 when
+ * maxiter is 0) when the budget ran out, -1 near-zero denominator, -3
+ * non-finite.  residual = float(sqrt(r.r)), iterations = completed steps. */
+int oracle_csr_cg(int it, int64_t n, const float *data, const void *indices, const void *indptr,
+                  const float *b, const float *x0, float *x, float rtol, float atol,
+                  int64_t maxiter, int32_t *info, float *residual, int32_t *iterations) {
+  float *r = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+  float *p = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+  float *ap = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+  if (!r || !p || !ap) {
+    free(r);
+    free(p);
+    free(ap);
+    return -1;
+  }
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  cg_spmv(it, n, data, indices, indptr, x, ap);
+  double b_norm2 = 0.0, rr = 0.0;
+  int finite = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    r[i] = b[i] - ap[i];
+    p[i] = r[i];
+    b_norm2 += (double)b[i] * (double)b[i];
+    rr += (double)r[i] * (double)r[i];
+    finite = finite && fin(r[i]) && fin(p[i]) && fin(ap[i]) && fin(b[i]) && fin(x[i]);
+  }
+  const float residual_norm = (float)sqrt(rr > 0.0 ? rr : 0.0);
+  const float b_norm = (float)sqrt(b_norm2 > 0.0 ? b_norm2 : 0.0);
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  const float eps = FLT_EPSILON;
+  int32_t status;
+  int32_t completed = 0;
+  if (!finite || !isfinite(rr) || !fin(residual_norm) || !fin(b_norm)) {
+    *info = -3;
+    *residual = residual_norm;
+    *iterations = 0;
+    goto done;
+  }
+  if (residual_norm <= tol) {
+    *info = 0;
+    *residual = residual_norm;
+    *iterations = 0;
+    goto done;
+  }
+  status = maxiter > 0 ? (int32_t)maxiter : 1;
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    cg_spmv(it, n, data, indices, indptr, p, ap);
+    double denom = 0.0;
+    finite = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      denom += (double)p[i] * (double)ap[i];
+      finite = finite && fin(p[i]) && fin(ap[i]);
+    }
+    if (!finite || !isfinite(denom)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (fabs(denom) <= (double)eps) {
+      double p2 = 0.0, ap2 = 0.0;
+      for (int64_t i = 0; i < n; ++i) {
+        p2 += (double)p[i] * (double)p[i];
+        ap2 += (double)ap[i] * (double)ap[i];
+      }
+      const double prod = p2 * ap2;
+      const double scale = sqrt(prod > 0.0 ? prod : 0.0);
+      const double grown = (double)eps * (double)eps * (scale > 1.0 ? scale : 1.0);
+      const double dtol = (double)eps < grown ? (double)eps : grown;
+      if (!isfinite(scale)) {
+        status = -3;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+      if (fabs(denom) <= dtol) {
+        status = -1;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+    }
+    const double alpha = rr / denom;
+    if (!isfinite(alpha)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    finite = 1;
+    double rr_new = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+      const double xc = (double)x[i] + alpha * (double)p[i];
+      const double rc = (double)r[i] - alpha * (double)ap[i];
+      const float xf = (float)xc, rf = (float)rc;
+      if (!isfinite(xc) || !isfinite(rc) || !fin(xf) || !fin(rf)) {
+        finite = 0;
+        continue;
+      }
+      x[i] = xf;
+      r[i] = rf;
+      rr_new += (double)rf * (double)rf;
+    }
+    const float r_norm = (float)sqrt(rr_new > 0.0 ? rr_new : 0.0);
+    completed = (int32_t)k;
+    if (!finite || !isfinite(rr_new) || !fin(r_norm)) {
+      status = -3;
+      break;
+    }
+    if (r_norm <= tol) {
+      status = 0;
+      rr = rr_new;
+      break;
+    }
+    const double beta = rr_new / rr;
+    if (!isfinite(beta)) {
+      status = -3;
+      break;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+      const double pc = (double)r[i] + beta * (double)p[i];
+      const float pf = (float)pc;
+      if (!isfinite(pc) || !fin(pf)) {
+        status = -3;
+        break;
+      }
+      p[i] = pf;
+    }
+    if (status < 0) break;
+    rr = rr_new;
+  }
+  *info = status;
+  *residual = (float)sqrt(rr > 0.0 ? rr : 0.0);
+  *iterations = completed;
+done:
+  free(r);
+  free(p);
+  free(ap);
+  return 0;
+}
+
+static float dot_f(const float *a, const float *b, int64_t n) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) acc += (double)a[i] * (double)b[i];
+  return (float)acc;
+}
+
+/* Jacobi-preconditioned CG (z = inv_diag * r): float scalars from double
+ * sums, float vector updates; info -2 for a non-positive r.z. */
+int oracle_csr_pcg_jacobi(int it, int64_t n, const float *data, const void *indices,
+                          const void *indptr, const float *b, const float *x0,
+                          const float *inv_diag, float *x, float rtol, float atol,
+                          int64_t maxiter, int32_t *info, float *residual, int32_t *iterations) {
+  const size_t bytes = (size_t)(n > 0 ? n : 1) * sizeof(float);
+  float *r = (float *)malloc(bytes), *z = (float *)malloc(bytes), *p = (float *)malloc(bytes);
+  float *ap = (float *)malloc(bytes);
+  if (!r || !z || !p || !ap) {
+    free(r);
+    free(z);
+    free(p);
+    free(ap);
+    return -1;
+  }
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  cg_spmv(it, n, data, indices, indptr, x, ap);
+  double b_norm2 = 0.0;
+  int finite = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    const float ri = b[i] - ap[i];
+    const float zi = inv_diag[i] * ri;
+    r[i] = ri;
+    z[i] = zi;
+    p[i] = zi;
+    b_norm2 += (double)b[i] * (double)b[i];
+    finite = finite && fin(ri) && fin(zi) && fin(inv_diag[i]);
+  }
+  float true_rr = dot_f(r, r, n);
+  float rho = dot_f(r, z, n);
+  const float b_norm = (float)sqrt(b_norm2 > 0.0 ? b_norm2 : 0.0);
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  const float true_residual = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+  const float eps = FLT_EPSILON;
+  int32_t status, completed = 0;
+  if (!finite || !fin(true_rr) || !fin(rho)) {
+    *info = -3;
+    *residual = true_residual;
+    *iterations = 0;
+    goto done;
+  }
+  if (true_residual <= tol) {
+    *info = 0;
+    *residual = true_residual;
+    *iterations = 0;
+    goto done;
+  }
+  if (rho <= 0.0f) {
+    *info = -2;
+    *residual = true_residual;
+    *iterations = 0;
+    goto done;
+  }
+  status = maxiter > 0 ? (int32_t)maxiter : 1;
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    cg_spmv(it, n, data, indices, indptr, p, ap);
+    const float denom = dot_f(p, ap, n);
+    const float p2 = dot_f(p, p, n);
+    const float ap2 = dot_f(ap, ap, n);
+    const float prod = p2 * ap2;
+    const float scale = sqrtf(prod > 0.0f ? prod : 0.0f);
+    const float dtol = eps * (scale > 1.0f ? scale : 1.0f);
+    if (!fin(denom) || !fin(scale) || fabsf(denom) <= dtol) {
+      status = -1;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    const float alpha = rho / denom;
+    if (!fin(alpha)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    double acc = 0.0;
+    finite = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      x[i] = x[i] + alpha * p[i];
+      const float ri = r[i] - alpha * ap[i];
+      const float zi = inv_diag[i] * ri;
+      r[i] = ri;
+      z[i] = zi;
+      acc += (double)ri * (double)ri;
+      finite = finite && fin(x[i]) && fin(ri) && fin(zi);
+    }
+    true_rr = (float)acc;
+    const float r_norm = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+    completed = (int32_t)k;
+    if (!finite || !fin(true_rr) || !fin(r_norm)) {
+      status = -3;
+      break;
+    }
+    if (r_norm <= tol) {
+      status = 0;
+      break;
+    }
+    const float rho_new = dot_f(r, z, n);
+    if (!fin(rho_new) || rho_new <= 0.0f) {
+      status = -2;
+      break;
+    }
+    const float beta = rho_new / rho;
+    if (!fin(beta)) {
+      status = -3;
+      break;
+    }
+    for (int64_t i = 0; i < n; ++i) p[i] = z[i] + beta * p[i];
+    rho = rho_new;
+  }
+  *info = status;
+  *residual = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+  *iterations = completed;
+done:
+  free(r);
+  free(z);
+  free(p);
+  free(ap);
   return 0;
 }

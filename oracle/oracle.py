@@ -33,6 +33,11 @@ Parity status of each function (the checks live in tests/test_oracle_*.py):
   W-worker partial order pinned on a case where it changes the rounding.
 - ``csr_data_vjp``: pinned against finite differences of the dense product
   (exact for float32 on small integers) and the single-product rule.
+- ``csr_cg`` / ``csr_pcg_jacobi``: pinned against a dense float64 solve
+  (SPD systems), the CG closed form on a diagonal system (one iteration per
+  distinct eigenvalue), SciPy's ``cg`` iteration counts on the same
+  systems, and the status rules (zero right-hand side, maxiter = 0,
+  non-finite input, indefinite matrix, non-positive preconditioner).
 """
 
 from __future__ import annotations
@@ -91,6 +96,12 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_transpose.restype = ci
         _lib.oracle_csr_data_vjp.argtypes = [ci, ci, i64, i64, i64, ci, vp, vp, vp, vp, vp]
         _lib.oracle_csr_data_vjp.restype = ci
+        f32 = ctypes.c_float
+        _lib.oracle_csr_cg.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp, vp, vp]
+        _lib.oracle_csr_cg.restype = ci
+        _lib.oracle_csr_pcg_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32, i64,
+                                               vp, vp, vp]
+        _lib.oracle_csr_pcg_jacobi.restype = ci
     return _lib
 
 
@@ -206,6 +217,52 @@ def csr_data_vjp(indices, indptr, X, cot, n_rows: int, n_cols: int, nnz: int, *,
     if rc != 0:
         raise MemoryError("oracle_csr_data_vjp failed")
     return out
+
+
+def _solver_inputs(data, indices, indptr, b, x0):
+    data = np.ascontiguousarray(data, dtype=np.float32)
+    indices = np.ascontiguousarray(indices)
+    indptr = np.ascontiguousarray(indptr)
+    if indices.dtype != indptr.dtype or indices.dtype not in ITYPES:
+        raise TypeError("oracle: indices/indptr must share int32 or int64")
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    n = b.shape[0]
+    x0 = np.zeros(n, np.float32) if x0 is None else np.ascontiguousarray(x0, dtype=np.float32)
+    return data, indices, indptr, b, x0, n
+
+
+def csr_cg(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: float = 0.0,
+           maxiter: int | None = None):
+    """Conjugate gradients on a square float32 CSR matrix (reference
+    src/linalg/cg/cg.cpp:75-246).  Returns (x, info, residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_cg(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices), _ptr(indptr),
+                             _ptr(b), _ptr(x0), _ptr(x), rtol, atol, maxiter, ctypes.addressof(info),
+                             ctypes.addressof(res), ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_cg failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_pcg_jacobi(data, indices, indptr, b, inv_diag, x0=None, *, rtol: float = 1e-5,
+                   atol: float = 0.0, maxiter: int | None = None):
+    """Jacobi-preconditioned CG (reference src/preconditioners/pcg/pcg.cpp:71-236).
+    Returns (x, info, residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    inv_diag = np.ascontiguousarray(inv_diag, dtype=np.float32)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_pcg_jacobi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                     _ptr(indptr), _ptr(b), _ptr(x0), _ptr(inv_diag), _ptr(x),
+                                     rtol, atol, maxiter, ctypes.addressof(info),
+                                     ctypes.addressof(res), ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_pcg_jacobi failed")
+    return x, info.value, res.value, its.value
 
 
 def cpu_ranges(work, parts: int) -> list[tuple[int, int]]:

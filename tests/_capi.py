@@ -33,6 +33,11 @@ class PlanOptions(ctypes.Structure):
 SLICE_AUTO, SLICE_OFF, SLICE_ON, SLICE_PANELS = 0, 1, 2, 3
 
 
+class SolverResult(ctypes.Structure):
+    _fields_ = [("info", ctypes.c_int32), ("iterations", ctypes.c_int32),
+                ("residual", ctypes.c_float), ("reserved", ctypes.c_int32)]
+
+
 def declared_functions() -> list[str]:
     text = HEADER.read_text()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(msx_\w+)\s*\(", text, re.M)))
@@ -81,6 +86,13 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_spmv_data_vjp_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
         L.msx_csr_spmm_data_vjp_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, i64, vp, vp, vp,
                                                 ci]
+        f32 = ctypes.c_float
+        L.msx_csr_cg.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp, vp, vp]
+        L.msx_csr_pcg_jacobi.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32, i64,
+                                         vp, vp, vp]
+        L.msx_csr_cg_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp]
+        L.msx_csr_pcg_jacobi_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                             i64, vp]
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
@@ -94,7 +106,8 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_spmm_transpose", "msx_csr_spmv_transpose_cpu",
                      "msx_csr_spmm_transpose_cpu", "msx_csr_spmv_data_vjp",
                      "msx_csr_spmm_data_vjp", "msx_csr_spmv_data_vjp_cpu",
-                     "msx_csr_spmm_data_vjp_cpu"):
+                     "msx_csr_spmm_data_vjp_cpu", "msx_csr_cg", "msx_csr_pcg_jacobi",
+                     "msx_csr_cg_cpu", "msx_csr_pcg_jacobi_cpu"):
             getattr(L, name).restype = ci
         _lib = L
     return _lib
@@ -294,3 +307,35 @@ def spmm_data_vjp(indices, indptr, X, cot, n_rows, n_cols, n_threads=1):
                                            cot.stride(0), _p(out), _stream()),
                "msx_csr_spmm_data_vjp")
     return out
+
+
+def cg(data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxiter=None, plan=None,
+       inv_diag=None):
+    """(x, info, residual, iterations) through msx_csr_cg[_cpu] or the
+    Jacobi-preconditioned variant when inv_diag is given."""
+    n = b.numel()
+    x0 = torch.zeros_like(b) if x0 is None else x0
+    x = torch.empty_like(b)
+    maxiter = 10 * n if maxiter is None else maxiter
+    res = SolverResult()
+    it = IT[indices.dtype]
+    L = lib()
+    if b.device.type == "cpu":
+        if inv_diag is None:
+            st = L.msx_csr_cg_cpu(it, n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b),
+                                  _p(x0), _p(x), rtol, atol, maxiter, ctypes.byref(res))
+        else:
+            st = L.msx_csr_pcg_jacobi_cpu(it, n, data.numel(), _p(data), _p(indices), _p(indptr),
+                                          _p(b), _p(x0), _p(inv_diag), _p(x), rtol, atol, maxiter,
+                                          ctypes.byref(res))
+    else:
+        pp = plan.ptr if plan else None
+        if inv_diag is None:
+            st = L.msx_csr_cg(it, n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b),
+                              _p(x0), _p(x), rtol, atol, maxiter, pp, ctypes.byref(res), _stream())
+        else:
+            st = L.msx_csr_pcg_jacobi(it, n, data.numel(), _p(data), _p(indices), _p(indptr),
+                                      _p(b), _p(x0), _p(inv_diag), _p(x), rtol, atol, maxiter, pp,
+                                      ctypes.byref(res), _stream())
+    _check(st, "msx_csr_cg")
+    return x, res.info, res.residual, res.iterations
