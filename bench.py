@@ -28,6 +28,8 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``cg``: conjugate gradients (device-resident loop) on the Poisson matrix,
   time per iteration against its bytes, and the single-threaded reference
   loop on the host;
+- ``mtx`` (with ``--mtx PATH``): SpMV on a Matrix Market matrix read by the
+  native reader (``mmread``);
 - ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
   the cached transpose, the transpose build, the SpMV value gradient and one
   autograd step (forward + ``A^T g``);
@@ -214,6 +216,36 @@ def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
     return out
 
 
+def mtx_leg(ext, path: str, dev) -> dict:
+    """SpMV on a Matrix Market file read with ``mmread`` (native reader):
+    ingestion time, then the cached-plan SpMV timed like the headline step,
+    against the matrix's compulsory bytes."""
+    import mlx_sparse as ms
+    from mlx_sparse import synthetic
+
+    t0 = time.perf_counter()
+    A = ms.mmread(path)
+    torch.cuda.synchronize()
+    read_s = time.perf_counter() - t0
+    if A.dtype != torch.float32:
+        return {"file": path, "skipped": f"dtype {A.dtype}"}
+    n_rows, n_cols = A.shape
+    x = torch.linspace(-1, 1, n_cols, device=dev)
+    data, indices, indptr = A.buffers(dev)
+    plan = A.plan(dev)
+    info = plan.info()
+    spmv_ms, _ = _graph_time(lambda: ext.csr_matvec(data, indices, indptr, x, n_rows, n_cols,
+                                                    plan=plan))
+    nbytes = synthetic.compulsory_bytes(A.nnz, n_rows, n_cols, 4, indices.element_size())
+    kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
+    out = {"file": os.path.basename(path), "shape": [n_rows, n_cols], "nnz": A.nnz,
+           "read_s": round(read_s, 3), "plan": kind, "kernel_us": round(spmv_ms * 1e3, 2),
+           "gbs": round(nbytes / (spmv_ms * 1e-3) / 1e9, 1),
+           "frac": round(nbytes / (spmv_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"mtx: {out}")
+    return out
+
+
 def cg_leg(dev) -> dict:
     """Conjugate gradients (``linalg.cg``, device-resident loop) on the 3D
     Poisson matrix 128^3, b = 1, x0 = 0, rtol = 1e-6.  Bytes per iteration:
@@ -270,6 +302,8 @@ def main() -> int:
     ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
     ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg")
     ap.add_argument("--no-cg", action="store_true", help="skip the conjugate gradient leg")
+    ap.add_argument("--mtx", default=None,
+                    help="also time SpMV on a Matrix Market file (e.g. a SuiteSparse matrix)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
@@ -461,6 +495,11 @@ def main() -> int:
         }
         log(f"batched spmv x{B}: {bat_ms * 1e3:.1f} us ({B * spmv_ms * 1e3:.1f} us as {B} SpMVs)")
         del P, Xp, xp, pd, pi, pp, pplan, Vb
+
+    # ---- a Matrix Market matrix, when given -------------------------------------
+    if args.mtx:
+        result["mtx"] = mtx_leg(ext, args.mtx, dev)
+        torch.cuda.empty_cache()
 
     # ---- conjugate gradients on the Poisson matrix --------------------------------
     if not args.no_cg:

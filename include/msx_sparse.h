@@ -448,6 +448,51 @@ msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
                                   int64_t maxiter, msx_solver_result *result);
 
 /*
+ * Matrix Market files (the text format of the SuiteSparse collection).
+ * Header fields: format 0 coordinate / 1 array; field 0 real, 1 integer,
+ * 2 complex, 3 pattern; symmetry 0 general, 1 symmetric, 2 skew-symmetric,
+ * 3 hermitian.  entries: data lines; nnz_bound: stored values after the
+ * symmetric kinds are expanded, at most.
+ *
+ * The reference reads these files with scipy.io.mmread (its tests,
+ * tests/test_suitesparse_collection.py:36-47, fixtures
+ * tests/fixtures/suitesparse/HB/*.mtx) and builds the array with from_scipy
+ * (mlx_sparse/_construct.py:854-975).
+ */
+typedef struct msx_mm_info {
+  int64_t n_rows;
+  int64_t n_cols;
+  int64_t entries;
+  int64_t nnz_bound;
+  int32_t format;
+  int32_t field;
+  int32_t symmetry;
+  int32_t reserved;
+} msx_mm_info;
+
+msx_status msx_mm_info_read(const char *path, msx_mm_info *info);
+
+/*
+ * A coordinate (or array) file as canonical CSR in host buffers of capacity
+ * `capacity` values (data, indices) and n_rows + 1 (indptr): symmetric kinds
+ * expanded (skew: negated mirror, hermitian: conjugated mirror), rows sorted
+ * by column, duplicates summed in double in file order, each value rounded
+ * once to `vt` (bfloat16 through float32, as from_scipy does).  *nnz gets
+ * the stored values.  Pattern files store 1.  n_threads <= 0: the resolved
+ * worker count.
+ */
+msx_status msx_mm_read_csr(const char *path, msx_vtype vt, msx_itype it,
+                           int64_t capacity, void *data, void *indices,
+                           void *indptr, int64_t *nnz, int n_threads);
+
+/*
+ * A file as a dense row-major n_rows x n_cols array (capacity values):
+ * array files directly, coordinate files with zeros elsewhere.
+ */
+msx_status msx_mm_read_dense(const char *path, msx_vtype vt, int64_t capacity,
+                             void *out, int n_threads);
+
+/*
  * Host (CPU) SpMV with host pointers, the `use_cpu()` device: rows are summed
  * sequentially in stored order, rows are split over `n_threads` std::threads
  * in nnz-balanced contiguous ranges (n_threads <= 0: the resolved worker

@@ -8,6 +8,7 @@ from __future__ import annotations
 from mlx_sparse import linalg, runtime
 from mlx_sparse._csr import CSRArray, csr_array
 from mlx_sparse._device import default_torch_device, use_cpu, use_device, use_gpu
+from mlx_sparse._io import from_scipy, mminfo, mmread
 from mlx_sparse._ops import (
     csr_batched_matmul,
     csr_batched_matvec,
@@ -40,8 +41,11 @@ __all__ = [
     "csr_matvec",
     "csr_matvec_transpose",
     "default_torch_device",
+    "from_scipy",
     "is_available",
     "linalg",
+    "mminfo",
+    "mmread",
     "runtime",
     "use_cpu",
     "use_device",

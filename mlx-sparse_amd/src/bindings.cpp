@@ -389,6 +389,75 @@ py::tuple solve_cg(py::handle data_o, py::handle indices_o, py::handle indptr_o,
   return py::make_tuple(x, res.info, res.residual, res.iterations);
 }
 
+py::dict mm_info(const std::string &path) {
+  msx_mm_info info{};
+  msx::check_status(msx_mm_info_read(path.c_str(), &info), "mmread");
+  static const char *formats[] = {"coordinate", "array"};
+  static const char *fields[] = {"real", "integer", "complex", "pattern"};
+  static const char *syms[] = {"general", "symmetric", "skew-symmetric", "hermitian"};
+  py::dict d;
+  d["rows"] = info.n_rows;
+  d["cols"] = info.n_cols;
+  d["entries"] = info.entries;
+  d["nnz_bound"] = info.nnz_bound;
+  d["format"] = formats[info.format];
+  d["field"] = fields[info.field];
+  d["symmetry"] = syms[info.symmetry];
+  return d;
+}
+
+py::object host_empty(int64_t n, py::object dtype) {
+  py::dict kw;
+  kw["dtype"] = dtype;
+  return torch().attr("empty")(py::make_tuple(n), **kw);
+}
+
+// (data, indices, indptr, shape) of a Matrix Market file as canonical CSR
+// host tensors.
+py::tuple mm_read_csr(const std::string &path, py::object dtype, py::object index_dtype,
+                      int n_threads) {
+  msx_mm_info info{};
+  msx::check_status(msx_mm_info_read(path.c_str(), &info), "mmread");
+  const std::string vname = dtype_name(dtype), iname = dtype_name(index_dtype);
+  const DType vd = dtype_of(vname), id = dtype_of(iname);
+  if (!msx::is_value_dtype(vd))
+    throw std::invalid_argument("mmread dtype must be float32, float16, bfloat16 or complex64.");
+  if (id != DType::Int32 && id != DType::Int64)
+    throw std::invalid_argument("mmread index_dtype must be int32 or int64.");
+  py::object data = host_empty(std::max<int64_t>(info.nnz_bound, 1), dtype);
+  py::object indices = host_empty(std::max<int64_t>(info.nnz_bound, 1), index_dtype);
+  py::object indptr = host_empty(info.n_rows + 1, index_dtype);
+  const ArrayView vdv = view_of(data), viv = view_of(indices), vpv = view_of(indptr);
+  int64_t nnz = 0;
+  {
+    py::gil_scoped_release nogil;
+    msx::check_status(msx_mm_read_csr(path.c_str(), msx::to_vtype(vd), msx::to_itype(id),
+                                      info.nnz_bound, vdv.ptr, viv.ptr, vpv.ptr, &nnz, n_threads),
+                      "mmread");
+  }
+  py::object sl = py::module_::import("builtins").attr("slice")(0, nnz);
+  return py::make_tuple(data.attr("__getitem__")(sl).attr("clone")(),
+                        indices.attr("__getitem__")(sl).attr("clone")(), indptr,
+                        py::make_tuple(info.n_rows, info.n_cols));
+}
+
+py::object mm_read_dense(const std::string &path, py::object dtype, int n_threads) {
+  msx_mm_info info{};
+  msx::check_status(msx_mm_info_read(path.c_str(), &info), "mmread");
+  const DType vd = dtype_of(dtype_name(dtype));
+  if (!msx::is_value_dtype(vd))
+    throw std::invalid_argument("mmread dtype must be float32, float16, bfloat16 or complex64.");
+  py::object out = host_empty(info.n_rows * info.n_cols, dtype);
+  const ArrayView vo = view_of(out);
+  {
+    py::gil_scoped_release nogil;
+    msx::check_status(msx_mm_read_dense(path.c_str(), msx::to_vtype(vd), info.n_rows * info.n_cols,
+                                        vo.ptr, n_threads),
+                      "mmread");
+  }
+  return out.attr("reshape")(info.n_rows, info.n_cols);
+}
+
 py::dict plan_info(const Plan &plan) {
   msx_plan_info info{};
   msx::check_status(msx_csr_plan_info(plan.p, &info), "csr_plan_info");
@@ -519,6 +588,12 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
       py::arg("atol"), py::arg("maxiter"), py::arg("plan") = py::none(),
       "Jacobi-preconditioned conjugate gradients: (x, info, residual, iterations).");
+  m.def("mm_info", &mm_info, py::arg("path"), "Header of a Matrix Market file.");
+  m.def("mm_read_csr", &mm_read_csr, py::arg("path"), py::arg("dtype"), py::arg("index_dtype"),
+        py::arg("n_threads") = 0,
+        "Matrix Market file -> (data, indices, indptr, shape), canonical CSR host tensors.");
+  m.def("mm_read_dense", &mm_read_dense, py::arg("path"), py::arg("dtype"),
+        py::arg("n_threads") = 0, "Matrix Market file -> dense row-major host tensor.");
   m.def("cpu_worker_count", &msx_cpu_worker_count, "Resolved CPU worker count.");
   m.def(
       "cpu_ranges",
