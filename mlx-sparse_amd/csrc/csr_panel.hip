@@ -35,6 +35,10 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kUnroll = 4;
+constexpr int kWavesPerGroup = kThreads / kWave;
+// Panel runs one pass-2 wave gathers per batch (16 waves x 8 = 128 panels,
+// the count of a 16.8 MB float32 x).
+constexpr int kRunsPerWave = 8;
 
 __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -49,33 +53,6 @@ template <class S>
 struct alignas(4 * sizeof(S)) Four {
   S v[4];
 };
-
-// Workgroup-wide exclusive scan of one u32 per thread; returns the total.
-__device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t *wsum, uint32_t *excl) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  uint32_t inc = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = __shfl_up(inc, d, kWave);
-    if (lane >= d) inc += o;
-  }
-  if (lane == kWave - 1) wsum[wave] = inc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t s = 0;
-    for (int i = 0; i < kThreads / kWave; ++i) {
-      const uint32_t t = wsum[i];
-      wsum[i] = s;
-      s += t;
-    }
-    wsum[kThreads / kWave] = s;
-  }
-  __syncthreads();
-  *excl = wsum[wave] + inc - v;
-  const uint32_t total = wsum[kThreads / kWave];
-  __syncthreads();  // wsum is reused by the next call
-  return total;
-}
 
 template <class V>
 __global__ void __launch_bounds__(kThreads)
@@ -138,8 +115,8 @@ __global__ void __launch_bounds__(kThreads)
     prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
 }
 
-// NU products per thread cover a whole tile (TW = NU * kThreads words) in
-// one batch; a tile never holds more values than words.
+// NU products per lane per batch: a wave's share of a tile (TW / 16 words on
+// average) usually takes one batch.
 template <class V, class I>
 __global__ void __launch_bounds__(kThreads)
     panel_rows(const typename V::Acc *__restrict__ prod, const uint16_t *__restrict__ dest,
@@ -151,55 +128,61 @@ __global__ void __launch_bounds__(kThreads)
   constexpr int TW = 65536 / static_cast<int>(sizeof(A));
   constexpr int NU = TW / kThreads;
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  A *buf = reinterpret_cast<A *>(lds_raw);                   // TW words
-  uint32_t *pre = reinterpret_cast<uint32_t *>(buf + TW);    // P + 1
-  uint32_t *start = pre + (P + 1);                           // P
-  uint32_t *wsum = start + P;                                // kThreads / kWave + 1
+  A *buf = reinterpret_cast<A *>(lds_raw);  // TW words
   const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
-
-  // Segment (q, T) of every panel: starts and a prefix of their lengths.
-  uint32_t total = 0;
-  for (int q0 = 0; q0 < P; q0 += kThreads) {
-    const int q = q0 + threadIdx.x;
-    uint32_t len = 0;
-    if (q < P) {
-      const uint32_t s = seg[static_cast<int64_t>(q) * n_tiles + T];
-      const uint32_t e = seg[static_cast<int64_t>(q) * n_tiles + T + 1];
-      start[q] = s;
-      len = e > s ? e - s : 0u;
-    }
-    uint32_t ex;
-    const uint32_t tot = block_exclusive_scan(len, wsum, &ex);
-    if (q < P) pre[q] = total + ex;
-    total += tot;
-  }
-  if (threadIdx.x == 0) pre[P] = total;
-  if (zero_fill)
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  if (zero_fill) {
     for (int i = threadIdx.x; i < TW; i += kThreads) buf[i] = vzero<A>();
-  __syncthreads();
+    __syncthreads();
+  }
 
-  for (uint32_t j0 = 0; j0 < total; j0 += NU * kThreads) {
-    A pv[NU];
-    uint32_t dv[NU];
+  // Wave w owns panels qb + w + 16k (k < kRunsPerWave) of each batch of
+  // 16 * kRunsPerWave panels.  Their segments (q, T) are concatenated: the
+  // run starts and the prefix of their lengths are wave-uniform, so a lane
+  // finds the run of its element j with kRunsPerWave - 1 scalar compares and
+  // every load address is known before the first load is issued.  Each run
+  // is read by consecutive lanes (coalesced).
+  for (int qb = 0; qb < P; qb += kWavesPerGroup * kRunsPerWave) {
+    uint32_t st[kRunsPerWave], pre[kRunsPerWave + 1];
+    pre[0] = 0;
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const uint32_t j = j0 + u * kThreads + threadIdx.x;
-      dv[u] = 0xFFFFFFFFu;
-      pv[u] = vzero<A>();
-      if (j < total) {
-        int lo = 0, hi = P;  // last panel whose prefix is <= j
-        while (hi - lo > 1) {
-          const int mid = (lo + hi) >> 1;
-          if (pre[mid] <= j) lo = mid; else hi = mid;
-        }
-        const uint32_t idx = start[lo] + (j - pre[lo]);
-        pv[u] = prod[idx];
-        dv[u] = dest[idx];
+    for (int k = 0; k < kRunsPerWave; ++k) {
+      const int q = qb + wave + kWavesPerGroup * k;
+      uint32_t s = 0, e = 0;
+      if (q < P) {
+        s = seg[static_cast<int64_t>(q) * n_tiles + T];
+        e = seg[static_cast<int64_t>(q) * n_tiles + T + 1];
       }
+      st[k] = s;
+      pre[k + 1] = pre[k] + (e > s ? e - s : 0u);
     }
+    const uint32_t total = pre[kRunsPerWave];
+    for (uint32_t j0 = 0; j0 < total; j0 += NU * kWave) {
+      A pv[NU];
+      uint32_t dv[NU];
 #pragma unroll
-    for (int u = 0; u < NU; ++u)
-      if (dv[u] < static_cast<uint32_t>(TW)) buf[dv[u]] = pv[u];
+      for (int u = 0; u < NU; ++u) {
+        const uint32_t j = j0 + u * kWave + lane;
+        dv[u] = 0xFFFFFFFFu;
+        pv[u] = vzero<A>();
+        if (j < total) {
+          uint32_t base = st[0], p0 = 0;
+#pragma unroll
+          for (int k = 1; k < kRunsPerWave; ++k)
+            if (j >= pre[k]) {
+              base = st[k];
+              p0 = pre[k];
+            }
+          const uint32_t idx = base + (j - p0);
+          pv[u] = prod[idx];
+          dv[u] = dest[idx];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        if (dv[u] < static_cast<uint32_t>(TW)) buf[dv[u]] = pv[u];
+    }
   }
   __syncthreads();
 
@@ -230,8 +213,7 @@ size_t pass1_lds(const msx_csr_plan *p) {
 
 template <class A>
 size_t pass2_lds(const msx_csr_plan *p) {
-  return sizeof(A) * static_cast<size_t>(p->tile_words) +
-         sizeof(uint32_t) * (2 * static_cast<size_t>(p->n_panels) + 1 + kThreads / kWave + 1);
+  return sizeof(A) * static_cast<size_t>(p->tile_words);
 }
 
 // Both passes take more than 64 KB of dynamic LDS.  The limit is raised
