@@ -103,7 +103,9 @@ typedef struct msx_plan_info {
   int64_t n_panels;    /* 0, or the number of LDS column panels */
   int64_t panel_width; /* columns per panel */
   int64_t n_tiles;     /* row tiles of a panel plan */
-  int64_t panel_values;/* values placed in the panel copy (short rows, valid columns) */
+  int64_t panel_values;/* entries of the panel copy: values of short rows with valid
+                          columns, each (panel, tile) segment padded to a
+                          multiple of 4 */
   int64_t panel_bytes; /* device bytes of the panel copy and its product buffer */
 } msx_plan_info;
 
@@ -203,7 +205,8 @@ msx_status msx_csr_plan_export(const msx_csr_plan *plan,
  *   seg_begin:       n_panels * n_tiles + 1 int64 - start of segment
  *                    (panel p, tile t) at index p * n_tiles + t of the
  *                    panel copy, whose values are ordered by (panel, tile,
- *                    stored position); the last entry is panel_values.
+ *                    stored position), each segment padded to a multiple
+ *                    of 4 entries; the last entry is panel_values.
  * MSX_EINVAL when the plan has no panels.  No reference counterpart: a
  * layout check of this library's own plans.
  */

@@ -170,10 +170,14 @@ __global__ void __launch_bounds__(kThreads)
     prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
 }
 
-__device__ inline float load_product(const float *p) { return __builtin_nontemporal_load(p); }
-__device__ inline c64 load_product(const c64 *p) { return nt_load(p); }
+// Four products of a segment (16-byte aligned: segments are padded to
+// multiples of 4 entries).
+template <class A>
+struct alignas(4 * sizeof(A)) ProdQuad {
+  A v[4];
+};
 
-// NU products per lane per batch: a wave's share of a tile (TW / 16 words on
+// NQ quads per lane per batch: a wave's share of a tile (TW / 16 words on
 // average) usually takes one batch.
 template <class V, class I>
 __global__ void __launch_bounds__(kThreads)
@@ -184,23 +188,34 @@ __global__ void __launch_bounds__(kThreads)
                typename V::Storage *__restrict__ y, int zero_fill) {
   using A = typename V::Acc;
   constexpr int TW = 65536 / static_cast<int>(sizeof(A));
-  constexpr int NU = TW / kThreads;
+  constexpr int NQ = TW / kThreads / 4;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   A *buf = reinterpret_cast<A *>(lds_raw);  // TW words
   const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  // The row bounds of the thread's first row are loaded now; their latency
+  // overlaps the product loads.
+  const int64_t r0 = clamp64(tile_begin[T], 0, n_rows);
+  const int64_t r1 = clamp64(tile_end[T], r0, n_rows);
+  const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+  int64_t s_first = 0, e_first = 0;
+  if (r0 + threadIdx.x < r1) {
+    s_first = static_cast<int64_t>(indptr[r0 + threadIdx.x]);
+    e_first = static_cast<int64_t>(indptr[r0 + threadIdx.x + 1]);
+  }
   if (zero_fill) {
     for (int i = threadIdx.x; i < TW; i += kThreads) buf[i] = vzero<A>();
     __syncthreads();
   }
 
   // Wave w owns panels qb + w + 16k (k < kRunsPerWave) of each batch of
-  // 16 * kRunsPerWave panels.  Their segments (q, T) are concatenated: the
-  // run starts and the prefix of their lengths are wave-uniform, so a lane
-  // finds the run of its element j with kRunsPerWave - 1 scalar compares and
-  // every load address is known before the first load is issued.  Each run
-  // is read by consecutive lanes (coalesced).
+  // 16 * kRunsPerWave panels.  Their segments (q, T) are concatenated in
+  // quads: the run starts and the prefix of their quad counts are
+  // wave-uniform, so a lane finds the run of its quad j with
+  // kRunsPerWave - 1 scalar compares and every load address is known before
+  // the first load is issued.  Consecutive lanes read consecutive quads.
+  const auto *pq = reinterpret_cast<const ProdQuad<A> *>(prod);
   for (int qb = 0; qb < P; qb += kWavesPerGroup * kRunsPerWave) {
     uint32_t st[kRunsPerWave], pre[kRunsPerWave + 1];
     pre[0] = 0;
@@ -212,18 +227,17 @@ __global__ void __launch_bounds__(kThreads)
         s = seg[static_cast<int64_t>(q) * n_tiles + T];
         e = seg[static_cast<int64_t>(q) * n_tiles + T + 1];
       }
-      st[k] = s;
-      pre[k + 1] = pre[k] + (e > s ? e - s : 0u);
+      st[k] = s / 4;
+      pre[k + 1] = pre[k] + (e > s ? (e - s) / 4 : 0u);
     }
     const uint32_t total = pre[kRunsPerWave];
-    for (uint32_t j0 = 0; j0 < total; j0 += NU * kWave) {
-      A pv[NU];
-      uint32_t dv[NU];
+    for (uint32_t j0 = 0; j0 < total; j0 += NQ * kWave) {
+      ProdQuad<A> pv[NQ];
+      uint2 dv[NQ];
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
+      for (int u = 0; u < NQ; ++u) {
         const uint32_t j = j0 + u * kWave + lane;
-        dv[u] = 0xFFFFFFFFu;
-        pv[u] = vzero<A>();
+        dv[u] = uint2{0xFFFFFFFFu, 0xFFFFFFFFu};
         if (j < total) {
           uint32_t base = st[0], p0 = 0;
 #pragma unroll
@@ -232,24 +246,30 @@ __global__ void __launch_bounds__(kThreads)
               base = st[k];
               p0 = pre[k];
             }
-          const uint32_t idx = base + (j - p0);
-          pv[u] = load_product(prod + idx);
-          dv[u] = __builtin_nontemporal_load(dest + idx);
+          const uint32_t quad = base + (j - p0);
+          pv[u] = nt_load(pq + quad);
+          dv[u] = nt_load(reinterpret_cast<const uint2 *>(dest) + quad);
         }
       }
 #pragma unroll
-      for (int u = 0; u < NU; ++u)
-        if (dv[u] < static_cast<uint32_t>(TW)) buf[dv[u]] = pv[u];
+      for (int u = 0; u < NQ; ++u) {
+        const uint32_t d[4] = {dv[u].x & 0xFFFFu, dv[u].x >> 16, dv[u].y & 0xFFFFu, dv[u].y >> 16};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (d[e] < static_cast<uint32_t>(TW)) buf[d[e]] = pv[u].v[e];
+      }
     }
   }
   __syncthreads();
 
-  const int64_t r0 = clamp64(tile_begin[T], 0, n_rows);
-  const int64_t r1 = clamp64(tile_end[T], r0, n_rows);
-  const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
   for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
-    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
-    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+    int64_t s = s_first, e = e_first;
+    if (r != r0 + threadIdx.x) {
+      s = static_cast<int64_t>(indptr[r]);
+      e = static_cast<int64_t>(indptr[r + 1]);
+    }
+    s = clamp64(s, 0, nnz);
+    e = clamp64(e, s, nnz);
     const int64_t base = clamp64((s - b0) + (r - r0), 0, TW);
     const int len = static_cast<int>(std::min<int64_t>(e - s, TW - base));
     const A *v = buf + base;

@@ -14,7 +14,10 @@
 //           words, so a tile holds at most H + W = TW words.
 //   copy    the values of short rows whose column lies in [0, n_cols),
 //           ordered by (panel, tile, stored position).  Segment (q, t) - the
-//           values of tile t in panel q - starts at seg[q * n_tiles + t].
+//           values of tile t in panel q - starts at seg[q * n_tiles + t] and
+//           is padded to a multiple of 4 entries (value 0, column 0, word
+//           0xFFFF, which no tile has), so every segment starts on a 16-byte
+//           boundary of the product buffer and pass 2 reads whole quads.
 //           Each value keeps its column inside the panel (u16) and its LDS
 //           word in the tile, dest = (p - first value of the tile) +
 //           (row - first row of the tile) (u16): a row's values sit at
@@ -24,7 +27,8 @@
 // per-value sort keys q * n_tiles + t (values dropped from the copy get the
 // key n_panels * n_tiles, which sorts last), a stable radix sort of
 // (key, position) pairs, segment starts by binary search over the sorted
-// keys, then a gather of the values.  The host reads two small arrays: the
+// keys, padded starts by a prefix sum of the rounded lengths, then a
+// gather of the values to their padded places.  The host reads two small arrays: the
 // tile count and the panel boundaries, which size the copy and split pass 1
 // into about one workgroup per CU.
 #include <hip/hip_runtime.h>
@@ -163,18 +167,33 @@ __global__ void __launch_bounds__(kThreads)
     out[q] = seg[q * n_tiles];
 }
 
+// len[k] = segment k's length rounded up to a multiple of 4; len[n_keys] = 0.
+__global__ void __launch_bounds__(kThreads)
+    padded_lengths(const uint32_t *__restrict__ seg, int64_t n_keys, uint32_t *__restrict__ len) {
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k <= n_keys;
+       k += static_cast<int64_t>(gridDim.x) * kThreads)
+    len[k] = k < n_keys ? (seg[k + 1] - seg[k] + 3u) & ~3u : 0u;
+}
+
+// Sorted value i (key k) goes to pseg[k] + (i - seg[k]).
 template <class S>
 __global__ void __launch_bounds__(kThreads)
     panel_gather(const S *__restrict__ data, const uint32_t *__restrict__ pos,
-                 const uint32_t *__restrict__ aux, int64_t n_values, int64_t nnz, S *__restrict__ out_data,
+                 const uint32_t *__restrict__ sorted_key, const uint32_t *__restrict__ seg,
+                 const uint32_t *__restrict__ pseg, const uint32_t *__restrict__ aux, int64_t n_kept,
+                 int64_t n_keys, int64_t nnz, int64_t n_values, S *__restrict__ out_data,
                  uint16_t *__restrict__ out_col, uint16_t *__restrict__ out_dest) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n_values;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n_kept;
        i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t k = sorted_key[i];
+    if (k >= n_keys) continue;
+    const int64_t at = static_cast<int64_t>(pseg[k]) + (i - static_cast<int64_t>(seg[k]));
+    if (at < 0 || at >= n_values) continue;
     const int64_t p = clamp64(pos[i], 0, nnz - 1);
-    out_data[i] = data[p];
+    out_data[at] = data[p];
     const uint32_t a = aux[p];
-    out_col[i] = static_cast<uint16_t>(a & 0xFFFFu);
-    out_dest[i] = static_cast<uint16_t>(a >> 16);
+    out_col[at] = static_cast<uint16_t>(a & 0xFFFFu);
+    out_dest[at] = static_cast<uint16_t>(a >> 16);
   }
 }
 
@@ -296,9 +315,25 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   if (!tmp.alloc(&sort_tmp, sort_bytes)) return no_memory();
   MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(sort_tmp, sort_bytes, key, key_out, pos, pos_out,
                                                  static_cast<int>(nnz), 0, end_bit, stream));
+  uint32_t *seg_raw = nullptr, *plen = nullptr;
+  if (!tmp.alloc(&seg_raw, sizeof(uint32_t) * (n_keys + 1)) ||
+      !tmp.alloc(&plen, sizeof(uint32_t) * (n_keys + 1)))
+    return no_memory();
   hipLaunchKernelGGL(segment_starts, dim3(grid_for(n_keys + 1)), dim3(kThreads), 0, stream, key_out,
-                     nnz, n_keys, p->pn_seg);
+                     nnz, n_keys, seg_raw);
   MSX_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(padded_lengths, dim3(grid_for(n_keys + 1)), dim3(kThreads), 0, stream, seg_raw,
+                     n_keys, plen);
+  MSX_HIP_TRY(hipGetLastError());
+  size_t pscan_bytes = 0;
+  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, pscan_bytes, plen, p->pn_seg,
+                                               static_cast<int>(n_keys + 1), stream));
+  void *pscan_tmp = nullptr;
+  if (!tmp.alloc(&pscan_tmp, pscan_bytes)) return no_memory();
+  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(pscan_tmp, pscan_bytes, plen, p->pn_seg,
+                                               static_cast<int>(n_keys + 1), stream));
+  uint32_t n_kept_u = 0;
+  MSX_HIP_TRY(hipMemcpyAsync(&n_kept_u, seg_raw + n_keys, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
   uint32_t *pbound = nullptr;
   if (!tmp.alloc(&pbound, sizeof(uint32_t) * (P + 1))) return no_memory();
   hipLaunchKernelGGL(panel_bounds, dim3(grid_for(P + 1)), dim3(kThreads), 0, stream, p->pn_seg, P,
@@ -310,6 +345,7 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   MSX_HIP_TRY(hipMemcpyAsync(&lost, dropped, sizeof(lost), hipMemcpyDeviceToHost, stream));
   MSX_HIP_TRY(hipStreamSynchronize(stream));
   const int64_t n_values = pb[P];
+  const int64_t n_kept = n_kept_u;
 
   // Pass-1 chunks: about one per CU (C in total, at least kMinChunk values
   // each), never across a panel boundary.  Panel q gets round(C * len / total)
@@ -324,7 +360,7 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
     if (b <= a) continue;
     const int64_t c = std::max<int64_t>(1, (2 * C * (b - a) + n_values) / (2 * n_values));
     for (int64_t i = 0; i < c; ++i) {
-      cbeg.push_back(a + (b - a) * i / c);
+      cbeg.push_back(a + (((b - a) * i / c) & ~int64_t{3}));
       cpan.push_back(static_cast<int32_t>(q));
     }
   }
@@ -347,8 +383,13 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   p->pn_col = reinterpret_cast<uint16_t *>(base + b_data);
   p->pn_dest = reinterpret_cast<uint16_t *>(base + b_data + b_u16);
   p->pn_prod = base + b_data + 2 * b_u16;
-  hipLaunchKernelGGL((panel_gather<S>), dim3(grid_for(n_values)), dim3(kThreads), 0, stream, data,
-                     pos_out, aux, n_values, nnz, static_cast<S *>(p->pn_data), p->pn_col, p->pn_dest);
+  // Padding entries: value 0, column 0, word 0xFFFF.
+  MSX_HIP_TRY(hipMemsetAsync(p->pn_data, 0, b_data, stream));
+  MSX_HIP_TRY(hipMemsetAsync(p->pn_col, 0, b_u16, stream));
+  MSX_HIP_TRY(hipMemsetAsync(p->pn_dest, 0xFF, b_u16, stream));
+  hipLaunchKernelGGL((panel_gather<S>), dim3(grid_for(n_kept)), dim3(kThreads), 0, stream, data,
+                     pos_out, key_out, seg_raw, p->pn_seg, aux, n_kept, n_keys, nnz, n_values,
+                     static_cast<S *>(p->pn_data), p->pn_col, p->pn_dest);
   MSX_HIP_TRY(hipGetLastError());
   MSX_HIP_TRY(hipMemcpyAsync(p->pn_chunk_begin, cbeg.data(), sizeof(int64_t) * cbeg.size(),
                              hipMemcpyHostToDevice, stream));
@@ -382,7 +423,8 @@ bool panels_eligible(const msx_csr_plan *p) {
   if (P > kMaxPanels || H <= 0) return false;
   // Tiles: key windows of the word range, plus one break per long row.
   const int64_t tiles_max = (p->nnz + p->n_rows) / H + 2 + p->n_long;
-  return P * tiles_max + 1 < (int64_t{1} << 32);
+  // Segment keys and padded copy offsets are 32-bit.
+  return P * tiles_max + 1 < (int64_t{1} << 32) && p->nnz + 3 * P * tiles_max < (int64_t{1} << 32);
 }
 
 msx_status build_panels(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,

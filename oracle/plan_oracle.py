@@ -28,8 +28,9 @@ The column-panel layout of a bound plan (csr_panel_build.hip; exported by
   clamped to [0, nnz]; a tile runs to the next tile start or long row;
 - every value p of a short row with a column c in [0, n_cols) and an LDS word
   (p - s(first row of its tile)) + (r - first row) below TW gets the segment
-  key floor(c / PW) * n_tiles + tile; ``seg_begin[k]`` is the number of such
-  values with a key below k (k = 0 .. n_panels * n_tiles).
+  key floor(c / PW) * n_tiles + tile; segment k holds the values with key k
+  padded to a multiple of 4 entries, so ``seg_begin[k]`` is the sum over
+  keys k' < k of ceil(count(k') / 4) * 4 (k = 0 .. n_panels * n_tiles).
 
 Pinned by ``panel_layout_loop`` (plain per-row loops) and by the tile and
 segment invariants in the same test file.
@@ -125,8 +126,8 @@ def panel_layout(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int = 256)
     dest = (pos - s[first]) + (r_of - first)
     c = idx[pos] if len(pos) else np.zeros(0, np.int64)
     ok = (c >= 0) & (c < n_cols) & (dest >= 0) & (dest < TW)
-    keys = np.sort((c[ok] // PW) * n_tiles + T[ok])
-    seg = np.searchsorted(keys, np.arange(P * n_tiles + 1), side="left").astype(np.int64)
+    counts = np.bincount((c[ok] // PW) * n_tiles + T[ok], minlength=P * n_tiles)
+    seg = np.concatenate([[0], np.cumsum((counts + 3) // 4 * 4)]).astype(np.int64)
     return tile_begin.astype(np.int64), tile_end.astype(np.int64), seg
 
 
@@ -167,6 +168,6 @@ def panel_layout_loop(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int =
                     counts[(c // PW) * n_tiles + t] += 1
     seg = [0]
     for v in counts:
-        seg.append(seg[-1] + v)
+        seg.append(seg[-1] + 4 * ((v + 3) // 4))
     return (np.array([a for a, _ in tiles], np.int64), np.array([b for _, b in tiles], np.int64),
             np.array(seg, np.int64))

@@ -198,7 +198,7 @@ def test_out_of_range_columns_add_nothing():
     sliced = _capi.Plan(p, 2, 6, data=d, indices=i, n_cols=3, slice_mode=_capi.SLICE_ON)
     assert sliced.info().n_slices == 8
     panels = _capi.Plan(p, 2, 6, data=d, indices=i, n_cols=3, slice_mode=_capi.SLICE_PANELS)
-    assert panels.info().n_panels == 1 and panels.info().panel_values == 3
+    assert panels.info().n_panels == 1 and panels.info().panel_values == 4  # 3 values + 1 pad
     for plan in (_capi.Plan(p, 2, 6), None, sliced, panels):
         y = _capi.spmv(d, i, p, to_torch(x, None, DEV), 2, 3, plan=plan)
         torch.cuda.synchronize()
@@ -295,7 +295,10 @@ def test_configs_full_size(name):
         # row is summed in stored order, so the result equals the oracle
         plan = _capi.Plan(p, m.shape[0], m.nnz, data=d, indices=i, n_cols=m.shape[1])
         info = plan.info()
-        assert info.n_panels == 128 and info.n_slices == 0 and info.panel_values == m.nnz
+        assert info.n_panels == 128 and info.n_slices == 0
+        # every (panel, tile) segment is padded to a multiple of 4 entries
+        assert info.panel_values % 4 == 0
+        assert m.nnz <= info.panel_values < m.nnz + 4 * info.n_panels * info.n_tiles
         for _ in range(2):
             y = _capi.spmv(d, i, p, xt, m.shape[0], m.shape[1], plan=plan)
             torch.cuda.synchronize()

@@ -109,15 +109,18 @@ def test_panel_layout_invariants(kind, acc_bytes):
         assert (p[b] - p[a]) + (b - a) <= TW  # products + one word per row fit
     np.testing.assert_array_equal(covered, (lengths <= W).astype(int))
     assert np.all(tb[1:] >= te[:-1])
-    # segments partition the valid short-row values by (panel, tile)
+    # segments partition the valid short-row values by (panel, tile), each
+    # padded to a multiple of 4 entries
     n_tiles, P = len(tb), -(-n_cols // PW)
     assert len(seg) == P * n_tiles + 1 and seg[0] == 0 and np.all(np.diff(seg) >= 0)
+    assert np.all(seg % 4 == 0)
     counts = np.zeros(P * n_tiles, np.int64)
     for t, (a, b) in enumerate(zip(tb, te)):
         cols = idx[p[a]:p[b]]
         cols = cols[(cols >= 0) & (cols < n_cols)]
         np.add.at(counts, (cols // PW) * n_tiles + t, 1)
-    np.testing.assert_array_equal(np.diff(seg), counts)
+    np.testing.assert_array_equal(np.diff(seg), -(-counts // 4) * 4)
+    assert np.all(np.diff(seg) - counts < 4)
     short_vals = sum(int(((idx[p[r]:p[r + 1]] >= 0) & (idx[p[r]:p[r + 1]] < n_cols)).sum())
                      for r in np.flatnonzero(lengths <= W))
-    assert seg[-1] == short_vals
+    assert counts.sum() == short_vals
