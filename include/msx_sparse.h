@@ -459,7 +459,7 @@ msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
  *
  * The reference reads these files with scipy.io.mmread (its tests,
  * tests/test_suitesparse_collection.py:36-47, fixtures
- * tests/fixtures/suitesparse/HB/*.mtx) and builds the array with from_scipy
+ * tests/fixtures/suitesparse/HB/ with its .mtx files) and builds the array with from_scipy
  * (mlx_sparse/_construct.py:854-975).
  */
 typedef struct msx_mm_info {
