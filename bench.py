@@ -414,7 +414,7 @@ def main() -> int:
                    "plan": {"kind": plan_kind,
                             **{k: info[k] for k in ("block_nnz", "n_blocks", "n_long_rows",
                                                     "n_slices", "n_panels", "n_tiles",
-                                                    "plan_bytes")}}},
+                                                    "panel_values", "plan_bytes")}}},
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 2),
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
