@@ -33,6 +33,11 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
   the cached transpose, the transpose build, the SpMV value gradient and one
   autograd step (forward + ``A^T g``);
+- ``configs`` (with ``--configs``): SpMV on every configuration of the
+  benchmark definition (2D Laplacian, power law with int64 indices, 3D
+  Poisson, the banded matrix in float32 / bfloat16 / float16 / complex64)
+  and SpMM at k = 8 / 64 / 256 (Poisson) and k = 64 (float16 banded),
+  graph-replay and cold timed against each one's compulsory bytes;
 - ``cpu_baseline``: the C restatement of the reference CPU kernel
   (oracle/, ``-O3`` without ``-march=native``), threads split like the
   reference, timed on this host's cores on the same matrix.
@@ -293,6 +298,75 @@ def cg_leg(dev) -> dict:
     return out
 
 
+def configs_leg(ext, dev, scratch) -> list:
+    """SpMV / SpMM on each benchmark configuration through the cached bound
+    plan (AUTO's choice), timed like the headline (graph replay) and cold
+    (1 GiB written between calls), against the compulsory bytes
+    nnz*(value+index) + indptr + x once + y once (X, Y at width k)."""
+    import mlx_sparse as ms
+    from mlx_sparse import synthetic
+
+    cases = []
+    rows = []
+
+    def run(name, m, data, X, k=None, complex_values=False):
+        n_rows, n_cols = m.shape
+        A = ms.csr_array((data, torch.from_numpy(m.indices), torch.from_numpy(m.indptr)),
+                         shape=m.shape)
+        d, i, p = A.buffers(dev)
+        plan = A.plan(dev)
+        info = plan.info()
+        if k is None:
+            fn = lambda: ext.csr_matvec(d, i, p, X, n_rows, n_cols, plan=plan)
+        else:
+            fn = lambda: ext.csr_matmul(d, i, p, X, n_rows, n_cols)
+        t, _ = _graph_time(fn, calls=10 if k else 20)
+        cold = _cold_time(fn, 10, scratch)
+        vb, ib = data.element_size(), m.indices.dtype.itemsize
+        nbytes = synthetic.compulsory_bytes(m.nnz, n_rows, n_cols, vb, ib, k=k or 1)
+        nflops = synthetic.flops(m.nnz, k or 1, complex_values)
+        kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
+        row = {"case": name, "nnz": m.nnz, "op": "spmv" if k is None else f"spmm k={k}",
+               "plan": kind if k is None else "none", "long_rows": info["n_long_rows"],
+               "kernel_us": round(t * 1e3, 2), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
+               "frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "gflops": round(nflops / (t * 1e-3) / 1e9, 1),
+               "cold_us": round(cold * 1e3, 2),
+               "cold_frac": round(nbytes / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"config: {row}")
+        rows.append(row)
+        del A, d, i, p, plan
+        torch.cuda.empty_cache()
+
+    def vec(n, seed, low=-1.0, high=1.0):
+        return torch.from_numpy(synthetic.uniform(n, low, high, seed=seed)).to(dev)
+
+    m = synthetic.laplacian_2d(1024)
+    run("cfg1 laplacian2d 1024^2 f32/i32", m, torch.from_numpy(m.data), vec(m.shape[1], 1))
+    m = synthetic.power_law(1 << 21, 2.0, 200_000, seed=0)
+    run("cfg3 powerlaw zipf2 n=2^21 f32/i64", m, torch.from_numpy(m.data),
+        vec(m.shape[1], 1, 0.0, 1.0))
+    m = synthetic.poisson_3d(128)
+    run("cfg4 poisson3d 128^3 f32/i32", m, torch.from_numpy(m.data), vec(m.shape[1], 1))
+    for k in (8, 64, 256):
+        X = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=k)).to(dev)
+        run("cfg4 poisson3d 128^3 f32/i32", m, torch.from_numpy(m.data), X, k=k)
+        del X
+    m = synthetic.banded(1 << 20, 32, 0.65, 70.0, seed=0)
+    d32 = torch.from_numpy(m.data)
+    x32 = vec(m.shape[1], 1)
+    run("cfg5 banded hb32 f32/i32", m, d32, x32)
+    for dt, nm in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        run(f"cfg5 banded hb32 {nm}/i32", m, d32.to(dt), x32.to(dt))
+    Xh = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=64)).to(dev).to(torch.float16)
+    run("cfg5 banded hb32 f16/i32", m, d32.to(torch.float16), Xh, k=64)
+    del Xh
+    cv = torch.from_numpy(synthetic.complex_values(m, seed=3))
+    xc = torch.complex(vec(m.shape[1], 4), vec(m.shape[1], 5))
+    run("cfg5 banded hb32 c64/i32", m, cv, xc, complex_values=True)
+    return rows
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,6 +378,8 @@ def main() -> int:
     ap.add_argument("--no-cg", action="store_true", help="skip the conjugate gradient leg")
     ap.add_argument("--mtx", default=None,
                     help="also time SpMV on a Matrix Market file (e.g. a SuiteSparse matrix)")
+    ap.add_argument("--configs", action="store_true",
+                    help="also time SpMV/SpMM on every benchmark configuration")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
@@ -499,6 +575,11 @@ def main() -> int:
     # ---- a Matrix Market matrix, when given -------------------------------------
     if args.mtx:
         result["mtx"] = mtx_leg(ext, args.mtx, dev)
+        torch.cuda.empty_cache()
+
+    # ---- every benchmark configuration, when asked ----------------------------------
+    if args.configs:
+        result["configs"] = configs_leg(ext, dev, scratch)
         torch.cuda.empty_cache()
 
     # ---- conjugate gradients on the Poisson matrix --------------------------------

@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(kThreads)
 // chunks of kChunk values (all loads of a chunk issued before any use);
 // within a chunk each row's run is summed in stored order by one lane and
 // added to the row's running sum, so segments of any length fit LDS.
-template <class V>
+template <class V, int AUX>
 __global__ void __launch_bounds__(kThreads)
     spmv_sliced(const typename V::Storage *__restrict__ s_data, const uint32_t *__restrict__ s_col,
                 const uint32_t *__restrict__ s_seg, const typename V::Storage *__restrict__ x,
@@ -258,8 +258,8 @@ __global__ void __launch_bounds__(kThreads)
       for (int j = 0; j <= QPL; ++j) {
         const int q = lane + j * kWave;
         if (q < nq) {
-          cq[j] = load_quad<uint32_t>(rc, static_cast<uint32_t>(q) * 16u);
-          dq[j] = load_quad<S>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+          cq[j] = load_quad<uint32_t, AUX>(rc, static_cast<uint32_t>(q) * 16u);
+          dq[j] = load_quad<S, AUX>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
         }
       }
       S xv[QPL + 1][4];
@@ -421,7 +421,11 @@ void launch_v(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream)
   const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
   const int64_t total = (n_super + kWavesPerGroup - 1) / kWavesPerGroup * kSlices;
   const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(total, kMaxGrid / kSlices * kSlices));
-  hipLaunchKernelGGL((spmv_sliced<V>), dim3(grid), dim3(kThreads), 0, stream,
+  // Copies larger than the Infinity Cache are streamed non-temporally.
+  const bool stream_nt =
+      static_cast<uint64_t>(p->nnz) * (sizeof(S) + sizeof(uint32_t)) > kInfinityCacheBytes;
+  auto kernel = stream_nt ? spmv_sliced<V, kCacheStream> : spmv_sliced<V, kCacheDefault>;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const S *>(p->s_data), p->s_col, p->s_seg, static_cast<const S *>(x),
                      static_cast<A *>(p->s_partial), p->n_rows, p->nnz, p->s_indptr,
                      p->itype == MSX_I64 ? 8 : 4, p->slice_width, p->col_bits);

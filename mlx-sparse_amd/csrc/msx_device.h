@@ -140,15 +140,23 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t nu
                                            static_cast<int>(n), kBufferFlags);
 }
 
+// Cache policy of a buffer load: kCacheDefault, or kCacheStream for data
+// read once per call (the non-temporal bit, so it does not displace reused
+// lines from L2).
+constexpr int kCacheDefault = 0;
+constexpr int kCacheStream = 2;
+// MI355X's Infinity Cache (memory-side, shared by all XCDs).
+constexpr uint64_t kInfinityCacheBytes = uint64_t{256} << 20;
+
 // Load N bytes (8, 16 or 32) at byte offset `off` from a buffer.
-template <int N>
+template <int N, int AUX = kCacheDefault>
 struct BufLoad;
 
-template <>
-struct BufLoad<8> {
+template <int AUX>
+struct BufLoad<8, AUX> {
   using T = uint64_t;
   __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
     return static_cast<uint64_t>(v[0]) | (static_cast<uint64_t>(v[1]) << 32);
   }
 };
@@ -160,21 +168,21 @@ struct u32x8 {
   uint32_t w[8];
 };
 
-template <>
-struct BufLoad<16> {
+template <int AUX>
+struct BufLoad<16, AUX> {
   using T = u32x4;
   __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
     return u32x4{{v[0], v[1], v[2], v[3]}};
   }
 };
 
-template <>
-struct BufLoad<32> {
+template <int AUX>
+struct BufLoad<32, AUX> {
   using T = u32x8;
   __device__ static inline T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    auto a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    auto b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+    auto a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+    auto b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, AUX);
     return u32x8{{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}};
   }
 };
@@ -186,10 +194,10 @@ struct Quad {
   E v[4];
 };
 
-template <class E>
+template <class E, int AUX = kCacheDefault>
 __device__ inline Quad<E> load_quad(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   static_assert(sizeof(E) == 2 || sizeof(E) == 4 || sizeof(E) == 8, "element size");
-  auto raw = BufLoad<4 * sizeof(E)>::load(r, byte_off);
+  auto raw = BufLoad<4 * sizeof(E), AUX>::load(r, byte_off);
   return __builtin_bit_cast(Quad<E>, raw);
 }
 
