@@ -70,7 +70,9 @@ typedef struct msx_csr_plan msx_csr_plan;
 typedef enum msx_slice_mode {
   MSX_SLICE_AUTO = 0,  /* when x exceeds 8 MB and most blocks' columns span
                           over a quarter of the columns: panels if the matrix
-                          qualifies, else XCD slices */
+                          qualifies and its short rows hold at least 65536
+                          values per compute unit, else XCD slices if x is
+                          16 MB or more, else row blocks */
   MSX_SLICE_OFF = 1,   /* row blocks only */
   MSX_SLICE_ON = 2,    /* XCD column slices */
   MSX_SLICE_PANELS = 3 /* LDS column panels (two-pass SpMV) */
@@ -141,8 +143,8 @@ msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
  * Build a plan bound to one matrix's values (`data`, `indices`, `indptr`,
  * all device pointers) on `stream`: the row blocks of msx_csr_plan_create,
  * plus, for scattered gathers, one of two reordered copies of the short
- * rows' values (`opts->slice_mode`; AUTO picks when x is over 8 MB and the
- * columns are scattered):
+ * rows' values (`opts->slice_mode`; AUTO picks as described at
+ * MSX_SLICE_AUTO):
  *   XCD slices - the values of each 256-row block reordered into 8 column
  *     slices; slice s runs on the workgroups the hardware places on XCD s,
  *     so each XCD gathers from one eighth of x, which stays in its L2;
@@ -154,7 +156,7 @@ msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
  *     one tile's products into LDS by stored position and sums each row in
  *     stored order, so short rows equal the reference CPU kernel bit for bit.
  *     Needs nnz < 2^31 and at most 2048 panels; MSX_SLICE_PANELS on a matrix
- *     outside those limits fails with MSX_EINVAL, AUTO falls back to slices.
+ *     outside those limits fails with MSX_EINVAL.
  * Long rows keep the row-block path in every mode.  `opts` may be NULL
  * (defaults).  Synchronises `stream`.
  *

@@ -415,6 +415,15 @@ msx_status build_v(msx_csr_plan *p, const void *data, const void *indices, const
 
 }  // namespace
 
+int64_t panels_min_values(int device) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  return static_cast<int64_t>(std::max(cus, 1)) * kMinChunk;
+}
+
 bool panels_eligible(const msx_csr_plan *p) {
   if (p->n_cols < 1 || p->n_rows < 1 || p->nnz < 1 || p->nnz >= (int64_t{1} << 31) - 1) return false;
   const int64_t a = acc_bytes(p->vtype);

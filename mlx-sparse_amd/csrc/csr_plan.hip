@@ -358,9 +358,22 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   auto s = static_cast<hipStream_t>(stream);
   int mode = opts->slice_mode;
   if (mode == MSX_SLICE_AUTO) {
+    // Scattered short rows over a large x: LDS panels when the short rows
+    // hold enough values to give every compute unit a pass-1 chunk (the
+    // 4M-row random matrix: 302 -> 221 us against 930 us in row blocks);
+    // XCD slices when x is 16 MB or more and panels are not possible.
+    // Otherwise row blocks: the power-law matrix (x 8.4 MB, about half of
+    // its values in long rows) runs 218 us in row blocks, 236 us sliced and
+    // 257 us in panels.
     bool scattered = false;
-    st = probe_scattered(p, indices, s, &scattered);
-    mode = !scattered ? MSX_SLICE_OFF : (panels_eligible(p) ? MSX_SLICE_PANELS : MSX_SLICE_ON);
+    int64_t short_values = 0;
+    st = probe_scattered(p, indices, s, &scattered, &short_values);
+    const int64_t x_bytes = n_cols * static_cast<int64_t>(value_bytes(vt));
+    mode = MSX_SLICE_OFF;
+    if (scattered && panels_eligible(p) && short_values >= panels_min_values(p->device))
+      mode = MSX_SLICE_PANELS;
+    else if (scattered && x_bytes >= (int64_t{16} << 20))
+      mode = MSX_SLICE_ON;
   }
   if (st == MSX_OK && mode == MSX_SLICE_PANELS && p->n_blocks > 0) {
     if (!panels_eligible(p))

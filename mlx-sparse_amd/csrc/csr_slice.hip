@@ -73,17 +73,19 @@ __device__ inline BlockRange block_range(const int32_t *bounds, const int64_t *b
 }
 
 // ---------------------------------------------------------------------------
-// Probe: count short blocks whose valid columns span more than n_cols / 4.
+// Probe: count short blocks whose valid columns span more than n_cols / 4
+// (counter[0]) and the values of all short blocks (counter[1]).
 template <class I, int W>
 __global__ void __launch_bounds__(kThreads)
     slice_probe(const I *__restrict__ indices, const int32_t *__restrict__ bounds,
                 const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
-                int64_t n_cols, unsigned long long *__restrict__ scattered) {
+                int64_t n_cols, unsigned long long *__restrict__ counter) {
   const int lane = threadIdx.x % kWave;
   const int64_t b = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + threadIdx.x / kWave;
   if (b >= n_bounds) return;
   const BlockRange br = block_range<W>(bounds, bounds_nnz, b, nnz);
   if (!br.valid || br.p1 <= br.p0) return;
+  if (lane == 0) atomicAdd(counter + 1, static_cast<unsigned long long>(br.p1 - br.p0));
   int64_t lo = INT64_MAX, hi = -1;
   for (int64_t p = br.p0 + lane; p < br.p1; p += kWave) {
     const int64_t c = static_cast<int64_t>(indices[p]);
@@ -98,7 +100,7 @@ __global__ void __launch_bounds__(kThreads)
     lo = ol < lo ? ol : lo;
     hi = oh > hi ? oh : hi;
   }
-  if (lane == 0 && hi >= lo && hi - lo > n_cols / 4) atomicAdd(scattered, 1ull);
+  if (lane == 0 && hi >= lo && hi - lo > n_cols / 4) atomicAdd(counter, 1ull);
 }
 
 // ---------------------------------------------------------------------------
@@ -338,34 +340,35 @@ int bits_for(int64_t v) {  // smallest b with v <= 2^b
 
 template <class I, int W>
 msx_status probe_typed(const msx_csr_plan *p, const void *indices, hipStream_t stream,
-                       bool *scattered) {
+                       bool *scattered, int64_t *short_values) {
   const int64_t groups = (p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
   unsigned long long *counter = nullptr;
-  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&counter), sizeof(*counter), stream));
-  MSX_HIP_TRY(hipMemsetAsync(counter, 0, sizeof(*counter), stream));
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&counter), 2 * sizeof(*counter), stream));
+  MSX_HIP_TRY(hipMemsetAsync(counter, 0, 2 * sizeof(*counter), stream));
   hipLaunchKernelGGL((slice_probe<I, W>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
                      stream, static_cast<const I *>(indices), p->bounds, p->bounds_nnz,
                      p->n_bounds, p->nnz, p->n_cols, counter);
-  unsigned long long count = 0;
+  unsigned long long count[2] = {0, 0};
   hipError_t e = hipGetLastError();
   if (e == hipSuccess)
-    e = hipMemcpyAsync(&count, counter, sizeof(count), hipMemcpyDeviceToHost, stream);
+    e = hipMemcpyAsync(count, counter, sizeof(count), hipMemcpyDeviceToHost, stream);
   if (e == hipSuccess) e = hipStreamSynchronize(stream);
   (void)hipFreeAsync(counter, stream);
   if (e != hipSuccess) return hip_fail(e, "slice probe");
-  *scattered = 2 * static_cast<int64_t>(count) > p->n_blocks;  // else mostly local
+  *scattered = 2 * static_cast<int64_t>(count[0]) > p->n_blocks;  // else mostly local
+  *short_values = static_cast<int64_t>(count[1]);
   return MSX_OK;
 }
 
 template <class I>
 msx_status probe_w(const msx_csr_plan *p, const void *indices, hipStream_t stream,
-                   bool *scattered) {
+                   bool *scattered, int64_t *short_values) {
   switch (p->block_nnz) {
-  case 64: return probe_typed<I, 64>(p, indices, stream, scattered);
-  case 128: return probe_typed<I, 128>(p, indices, stream, scattered);
-  case 256: return probe_typed<I, 256>(p, indices, stream, scattered);
-  case 512: return probe_typed<I, 512>(p, indices, stream, scattered);
-  default: return probe_typed<I, 1024>(p, indices, stream, scattered);
+  case 64: return probe_typed<I, 64>(p, indices, stream, scattered, short_values);
+  case 128: return probe_typed<I, 128>(p, indices, stream, scattered, short_values);
+  case 256: return probe_typed<I, 256>(p, indices, stream, scattered, short_values);
+  case 512: return probe_typed<I, 512>(p, indices, stream, scattered, short_values);
+  default: return probe_typed<I, 1024>(p, indices, stream, scattered, short_values);
   }
 }
 
@@ -449,12 +452,13 @@ msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, 
 }
 
 msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,
-                           bool *scattered) {
+                           bool *scattered, int64_t *short_values) {
   *scattered = false;
+  *short_values = 0;
   const int64_t x_bytes = p->n_cols * static_cast<int64_t>(value_bytes(p->vtype));
   if (x_bytes < (int64_t{8} << 20) || p->n_bounds == 0 || p->n_blocks == 0) return MSX_OK;
-  return p->itype == MSX_I32 ? probe_w<int32_t>(p, indices, stream, scattered)
-                             : probe_w<int64_t>(p, indices, stream, scattered);
+  return p->itype == MSX_I32 ? probe_w<int32_t>(p, indices, stream, scattered, short_values)
+                             : probe_w<int64_t>(p, indices, stream, scattered, short_values);
 }
 
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream) {

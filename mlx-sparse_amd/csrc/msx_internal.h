@@ -120,9 +120,13 @@ msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, 
                         hipStream_t stream);
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream);
 // True when the short blocks' columns are scattered over an x of more than
-// 8 MB (the AUTO rule for a reordered copy).  Synchronises `stream`.
+// 8 MB (the AUTO rule for a reordered copy); also the number of values in
+// short blocks.  Synchronises `stream`.
 msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,
-                           bool *scattered);
+                           bool *scattered, int64_t *short_values);
+// Minimum short-row values of an AUTO panel plan: one pass-1 chunk
+// (csr_panel_build.hip, kMinChunk) per compute unit of `device`.
+int64_t panels_min_values(int device);
 
 // Panel plans (csr_panel_build.hip / csr_panel.hip).
 bool panels_eligible(const msx_csr_plan *p);

@@ -365,6 +365,23 @@ def test_auto_selection_and_binding():
     plan = _capi.Plan(p, g.shape[0], g.nnz, data=d, indices=i, n_cols=g.shape[1])
     assert plan.info().n_slices == 0 and plan.info().n_panels == 0
     plan.close()
+    # scattered, but too few short-row values to give each of the 256 compute
+    # units a 65536-value pass-1 chunk: row blocks at x = 8.4 MB, XCD slices
+    # from x = 16 MB on
+    for n, kind in ((1 << 21, "blocks"), (1 << 22, "slices")):
+        f = s.random_fixed_row(n, 2, seed=8)
+        d, i, p = _upload(f.data, f.indices, f.indptr, "float32")
+        plan = _capi.Plan(p, f.shape[0], f.nnz, data=d, indices=i, n_cols=f.shape[1])
+        info = plan.info()
+        assert info.n_panels == 0 and info.n_slices == (8 if kind == "slices" else 0), kind
+        xf = s.uniform(f.shape[1], -1, 1, 9)
+        y = _capi.spmv(d, i, p, to_torch(xf, None, DEV), f.shape[0], f.shape[1], plan=plan)
+        torch.cuda.synchronize()
+        want = orc.csr_matvec(f.data, f.indices, f.indptr, xf, f.shape[0], n_threads=8)
+        assert_rows_close(to_numpy(y), want,
+                          orc.row_scale(f.data, f.indices, f.indptr, xf, f.shape[0]), "float32",
+                          f"auto {kind}")
+        plan.close()
 
 
 def test_sliced_through_api(gpu):
