@@ -319,7 +319,7 @@ def configs_leg(ext, dev, scratch) -> list:
         if k is None:
             fn = lambda: ext.csr_matvec(d, i, p, X, n_rows, n_cols, plan=plan)
         else:
-            fn = lambda: ext.csr_matmul(d, i, p, X, n_rows, n_cols)
+            fn = lambda: ext.csr_matmul(d, i, p, X, n_rows, n_cols, plan=plan)
         t, _ = _graph_time(fn, calls=10 if k else 20)
         cold = _cold_time(fn, 10, scratch)
         vb, ib = data.element_size(), m.indices.dtype.itemsize
@@ -327,7 +327,7 @@ def configs_leg(ext, dev, scratch) -> list:
         nflops = synthetic.flops(m.nnz, k or 1, complex_values)
         kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
         row = {"case": name, "nnz": m.nnz, "op": "spmv" if k is None else f"spmm k={k}",
-               "plan": kind if k is None else "none", "long_rows": info["n_long_rows"],
+               "plan": kind, "window_rows": info["window_rows"], "long_rows": info["n_long_rows"],
                "kernel_us": round(t * 1e3, 2), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
                "frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "gflops": round(nflops / (t * 1e-3) / 1e9, 1),
@@ -524,11 +524,12 @@ def main() -> int:
         pplan = P.plan(dev)
         spmv_ms, _ = _graph_time(lambda: ext.csr_matvec(pd, pi, pp, xp, p.shape[0], p.shape[1],
                                                         plan=pplan))
-        spmm_ms, _ = _graph_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1]),
-                                 calls=10)
+        spmm_ms, _ = _graph_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1],
+                                                        plan=pplan), calls=10)
         for _ in range(3):
             P @ Xp
-        spmm_cold = _cold_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1]), 15, scratch)
+        spmm_cold = _cold_time(lambda: ext.csr_matmul(pd, pi, pp, Xp, p.shape[0], p.shape[1],
+                                                      plan=pplan), 15, scratch)
         f_spmv = synthetic.flops(p.nnz)
         f_spmm = synthetic.flops(p.nnz, 64)
         b_spmm = synthetic.compulsory_bytes(p.nnz, p.shape[0], p.shape[1], 4, 4, k=64)

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 2
+#define MSX_ABI_VERSION 3
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -109,6 +109,9 @@ typedef struct msx_plan_info {
                           columns, each (panel, tile) segment padded to a
                           multiple of 4 */
   int64_t panel_bytes; /* device bytes of the panel copy and its product buffer */
+  int64_t window_rows; /* bound plans: the widest column window (in rows of X)
+                          of the plan's 64-row tiles, 0 when none; SpMM
+                          stages each tile's window of X in LDS when it fits */
 } msx_plan_info;
 
 /* ABI version of the loaded library (MSX_ABI_VERSION at build time). */
@@ -237,7 +240,9 @@ msx_status msx_csr_spmv(msx_vtype vt, msx_itype it, int64_t n_rows,
  * Y[i, c] = sum_p data[p] * X[indices[p], c] for c in [0, k), with X an
  * n_cols x k row-major matrix of leading dimension ldx (>= k) and Y an
  * n_rows x k row-major matrix of leading dimension ldy (>= k).  Device
- * pointers.  `plan` is accepted for symmetry and may be NULL.
+ * pointers.  `plan` may be NULL; a bound plan of the matrix lets the SpMM
+ * stage each 64-row tile's column window of X in LDS when every window fits
+ * (banded matrices), reading X from HBM about once.
  *
  * Replaces CSRMatMul::eval_gpu (reference:
  * src/sparse/csr_matmul/csr_matmul.cpp:260-300) and the Metal kernels

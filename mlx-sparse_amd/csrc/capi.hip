@@ -136,6 +136,6 @@ extern "C" msx_status msx_csr_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, i
   st = check_plan("csr_matmul", plan, vt, it, n_rows, n_cols, nnz, data, indices);
   if (st != MSX_OK) return st;
   if (n_rows == 0 || k == 0) return MSX_OK;
-  return launch_spmm(vt, it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy,
+  return launch_spmm(vt, it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, plan,
                      static_cast<hipStream_t>(stream));
 }

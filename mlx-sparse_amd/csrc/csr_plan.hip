@@ -319,6 +319,7 @@ void release(msx_csr_plan *p) {
   if (p->s_base) (void)hipFree(p->s_base);
   if (p->pn_base) (void)hipFree(p->pn_base);
   if (p->pn_meta) (void)hipFree(p->pn_meta);
+  if (p->win) (void)hipFree(p->win);
   delete p;
 }
 
@@ -385,6 +386,7 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   } else if (st == MSX_OK && mode == MSX_SLICE_ON && p->n_blocks > 0) {
     st = build_slices(p, data, indices, indptr, s);
   }
+  if (st == MSX_OK) st = build_windows(p, indices, indptr, s);
   if (st != MSX_OK) {
     release(p);
     return st;
@@ -420,7 +422,8 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->n_long_rows = plan->n_long;
   info->n_chunks = plan->n_chunks;
   info->device = plan->device;
-  info->plan_bytes = static_cast<int64_t>(plan->bytes + plan->s_bytes + plan->pn_bytes);
+  info->plan_bytes =
+      static_cast<int64_t>(plan->bytes + plan->s_bytes + plan->pn_bytes + plan->win_bytes);
   info->n_slices = plan->n_slices;
   info->slice_width = plan->slice_width;
   info->slice_bytes = static_cast<int64_t>(plan->s_bytes);
@@ -429,6 +432,7 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->n_tiles = plan->n_tiles;
   info->panel_values = plan->pn_values;
   info->panel_bytes = static_cast<int64_t>(plan->pn_bytes);
+  info->window_rows = plan->win_rows_max;
   return MSX_OK;
 }
 

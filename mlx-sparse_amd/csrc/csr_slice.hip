@@ -424,9 +424,9 @@ void launch_v(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream)
   const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
   const int64_t total = (n_super + kWavesPerGroup - 1) / kWavesPerGroup * kSlices;
   const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(total, kMaxGrid / kSlices * kSlices));
-  // Copies larger than the Infinity Cache are streamed non-temporally.
+  // Copies that cannot stay in the Infinity Cache are streamed non-temporally.
   const bool stream_nt =
-      static_cast<uint64_t>(p->nnz) * (sizeof(S) + sizeof(uint32_t)) > kInfinityCacheBytes;
+      static_cast<uint64_t>(p->nnz) * (sizeof(S) + sizeof(uint32_t)) > kStreamNtBytes;
   auto kernel = stream_nt ? spmv_sliced<V, kCacheStream> : spmv_sliced<V, kCacheDefault>;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const S *>(p->s_data), p->s_col, p->s_seg, static_cast<const S *>(x),

@@ -74,23 +74,22 @@ __device__ inline c64 shfl_idx(c64 v, int src, int width) {
   return c64{__shfl(v.re, src, width), __shfl(v.im, src, width)};
 }
 
-// Y-row segment [col, col + CW) of row [s, e): sum from zero in stored order.
-// The row's group is LR lanes wide (lane l of it); every lane of the group
-// calls this with the same s and e.  SHUF: LR >= kChunk, a chunk of kChunk
+// Y-row segment of row [s, e): sum from zero in stored order; fetch(c)
+// returns the lane's CW values of X row c.  The row's group is LR lanes wide
+// (lane l of it); every lane of the group calls this with the same s and e.  SHUF: LR >= kChunk, a chunk of kChunk
 // values is loaded one value per lane and shared by shuffles; otherwise every
 // lane loads the values itself, kUnrollDirect per step (narrow groups, small
 // k: measured faster there than whole chunks).  Columns outside [0, n_cols)
 // add nothing.
-template <class V, class I, int CW, bool SHUF>
+template <class V, class I, int CW, bool SHUF, class Fetch>
 __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
-                                   const I *__restrict__ indices, const typename V::Storage *__restrict__ X,
-                                   int64_t ldx, int64_t n_cols, int64_t s, int64_t e, int64_t col, int l,
-                                   int LR, typename V::Acc (&acc)[CW]) {
+                                   const I *__restrict__ indices, Fetch fetch, int64_t n_cols,
+                                   int64_t s, int64_t e, int l, int LR,
+                                   typename V::Acc (&acc)[CW]) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   // Positions stay 64-bit: 32-bit ones measured 15 % slower here (the
   // address arithmetic of the index and value loads).
-  const auto *Xc = X + col;
 #pragma unroll
   for (int c = 0; c < CW; ++c) acc[c] = vzero<A>();
   if constexpr (!SHUF) {
@@ -108,21 +107,21 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
       }
 #pragma unroll
       for (int u = 0; u < kUnrollDirect; ++u)
-        if (cu[u] >= 0) xv[u] = load_vec<S, CW>(Xc + static_cast<int64_t>(cu[u]) * ldx);
+        if (cu[u] >= 0) xv[u] = fetch(cu[u]);
 #pragma unroll
       for (int u = 0; u < kUnrollDirect; ++u)
         if (cu[u] >= 0) {
 #pragma unroll
-          for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(au[u], xv[u].v[c]));
+          for (int c = 0; c < CW; ++c) acc[c] = vmadd<V>(acc[c], au[u], xv[u].v[c]);
         }
     }
     for (; p < e; ++p) {
       const I c = indices[p];
       if (static_cast<uint64_t>(static_cast<int64_t>(c)) < static_cast<uint64_t>(n_cols)) {
         const A a = V::widen(data[p]);
-        const Vec<S, CW> xv = load_vec<S, CW>(Xc + static_cast<int64_t>(c) * ldx);
+        const Vec<S, CW> xv = fetch(static_cast<int>(c));
 #pragma unroll
-        for (int q = 0; q < CW; ++q) acc[q] = vadd(acc[q], vmul_acc<V>(a, xv.v[q]));
+        for (int q = 0; q < CW; ++q) acc[q] = vmadd<V>(acc[q], a, xv.v[q]);
       }
     }
     return;
@@ -145,12 +144,12 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
     Vec<S, CW> xv[kChunk];
 #pragma unroll
     for (int u = 0; u < kChunk; ++u)
-      if (cu[u] >= 0) xv[u] = load_vec<S, CW>(Xc + static_cast<int64_t>(cu[u]) * ldx);
+      if (cu[u] >= 0) xv[u] = fetch(cu[u]);
 #pragma unroll
     for (int u = 0; u < kChunk; ++u)
       if (cu[u] >= 0) {
 #pragma unroll
-        for (int c = 0; c < CW; ++c) acc[c] = vadd(acc[c], vmul_acc<V>(au[u], xv[u].v[c]));
+        for (int c = 0; c < CW; ++c) acc[c] = vmadd<V>(acc[c], au[u], xv[u].v[c]);
       }
   }
 }
@@ -182,7 +181,10 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
     A acc[CW];
     // Lanes past k still take part in the shuffles; they read column 0.
-    row_segment<V, I, CW, SHUF>(data, indices, X, ldx, n_cols, s, e, col < k ? col : 0, l, LR, acc);
+    const S *Xc = X + (col < k ? col : 0);
+    row_segment<V, I, CW, SHUF>(
+        data, indices, [&](int c) { return load_vec<S, CW>(Xc + static_cast<int64_t>(c) * ldx); },
+        n_cols, s, e, l, LR, acc);
     if (col >= k) continue;
     Vec<S, CW> out;
 #pragma unroll
@@ -227,11 +229,192 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
     const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
     A acc[CW];
-    row_segment<V, I, CW, true>(data, indices, X, ldx, n_cols, s, e, col, l, LR, acc);
+    const S *Xc = X + col;
+    row_segment<V, I, CW, true>(
+        data, indices, [&](int c) { return load_vec<S, CW>(Xc + static_cast<int64_t>(c) * ldx); },
+        n_cols, s, e, l, LR, acc);
     Vec<S, CW> out;
 #pragma unroll
     for (int c = 0; c < CW; ++c) out.v[c] = V::narrow(acc[c]);
     store_vec<S, CW>(Y + row * ldy + col, out);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Column windows.  A bound plan records, for each tile of kWinRows
+// consecutive rows, the lowest and highest valid column of its values.  On a
+// banded matrix (half-bandwidth 32) a tile's values touch about 100 rows of
+// X, yet each row gathers one X row per value (about 43): staging the
+// window once per workgroup with coalesced loads and gathering from LDS
+// reads X from L2 about three times per tile instead of once per value.
+constexpr int kWinRows = 32;
+constexpr int64_t kWinLdsBytes = 65536;  // LDS of one workgroup's window
+
+template <class I>
+__global__ void __launch_bounds__(kThreads)
+    window_bounds(const I *__restrict__ indices, const I *__restrict__ indptr, int64_t n_rows,
+                  int64_t nnz, int64_t n_cols, int64_t n_win, int32_t *__restrict__ win,
+                  unsigned long long *__restrict__ widest) {
+  // widest[0]: window rows, widest[1]: values of a tile
+  const int lane = threadIdx.x % kWave;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (t >= n_win) return;
+  const int64_t r0 = t * kWinRows;
+  const int64_t r1 = std::min<int64_t>(r0 + kWinRows, n_rows);
+  const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+  const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0, nnz);
+  int64_t lo = INT64_MAX, hi = -1;
+  for (int64_t p = p0 + lane; p < p1; p += kWave) {
+    const int64_t c = static_cast<int64_t>(indices[p]);
+    if (static_cast<uint64_t>(c) < static_cast<uint64_t>(n_cols)) {
+      lo = c < lo ? c : lo;
+      hi = c > hi ? c : hi;
+    }
+  }
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) {
+    const int64_t ol = __shfl_xor(lo, d, kWave);
+    const int64_t oh = __shfl_xor(hi, d, kWave);
+    lo = ol < lo ? ol : lo;
+    hi = oh > hi ? oh : hi;
+  }
+  if (lane == 0) {
+    const bool any = hi >= lo;
+    win[2 * t] = any ? static_cast<int32_t>(lo) : 1;
+    win[2 * t + 1] = any ? static_cast<int32_t>(hi) : 0;
+    if (any) atomicMax(widest, static_cast<unsigned long long>(hi - lo + 1));
+    atomicMax(widest + 1, static_cast<unsigned long long>(p1 - p0));
+  }
+}
+
+// One workgroup per row tile.  Staged in LDS with loads all issued at once:
+// X rows [lo, hi] of the tile's window (LR lanes of 16 bytes, the whole k),
+// the tile's columns and widened values (its positions [p0, p1)), and its
+// row pointers.  Each row is then summed from zero in stored order, as in
+// spmm_rows, from LDS only.  A column outside the window (the indices
+// changed after the plan was built) is read from X directly, and a row
+// outside [p0, p1) (non-monotone indptr) or a tile with more values than
+// staged takes the global path, so the result never depends on the plan.
+template <class V, class I, int CW>
+__global__ void __launch_bounds__(kThreads)
+    spmm_window(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
+                int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
+                int64_t nnz, int64_t n_cols, int64_t k, int LR, const int32_t *__restrict__ win,
+                int64_t n_win, int64_t win_rows_cap, int64_t tile_nnz_cap) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  static_assert(CW * sizeof(S) == 16, "window rows are staged in 16-byte lanes");
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  // Layout (the launcher sizes it alike): X window, row pointers, columns
+  // and values in their storage type (counts rounded to a multiple of 4, so
+  // every array stays aligned).
+  const int64_t cap4 = (tile_nnz_cap + 3) & ~int64_t{3};
+  uint4 *xs = reinterpret_cast<uint4 *>(lds_raw);                  // win_rows_cap * LR
+  int64_t *rptr = reinterpret_cast<int64_t *>(xs + win_rows_cap * LR);  // kWinRows + 1 (+1)
+  int32_t *cols = reinterpret_cast<int32_t *>(rptr + kWinRows + 2);     // cap4
+  S *vals = reinterpret_cast<S *>(cols + cap4);                         // cap4
+  const int g = threadIdx.x / LR;
+  const int l = threadIdx.x % LR;
+  const int lg = __builtin_ctz(static_cast<unsigned>(LR));  // LR is a power of two
+  const int rows_per_pass = kThreads / LR;
+  const int64_t col = static_cast<int64_t>(l) * CW;
+  const S *Xc = X + (col < k ? col : 0);
+  for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_win; t += gridDim.x) {
+    const int64_t lo = win[2 * t];
+    const int64_t nw = std::min<int64_t>(
+        win_rows_cap, std::max<int64_t>(0, static_cast<int64_t>(win[2 * t + 1]) - lo + 1));
+    const int64_t r0 = t * kWinRows;
+    const int64_t r1 = std::min<int64_t>(r0 + kWinRows, n_rows);
+    const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+    const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0, nnz);
+    const bool staged = p1 - p0 <= tile_nnz_cap;
+    for (int64_t q = threadIdx.x; q < nw * LR; q += kThreads) {
+      const int64_t wr = q / LR;
+      const int64_t wc = (q - wr * LR) * CW;
+      if (wc < k) xs[q] = *reinterpret_cast<const uint4 *>(X + (lo + wr) * ldx + wc);
+    }
+    // cols[q]: the value's row in the window (>= 0); -1 for a column
+    // outside [0, n_cols) (adds nothing); -2 - c for a valid column c
+    // outside the window (read from X).
+    if (staged) {
+      for (int64_t q = threadIdx.x; q < p1 - p0; q += kThreads) {
+        const int64_t c = static_cast<int64_t>(indices[p0 + q]);
+        const int64_t w = c - lo;
+        int32_t code = -1;
+        if (static_cast<uint64_t>(c) < static_cast<uint64_t>(n_cols))
+          code = static_cast<uint64_t>(w) < static_cast<uint64_t>(nw) ? static_cast<int32_t>(w)
+                                                                       : static_cast<int32_t>(-2 - c);
+        cols[q] = code;
+        vals[q] = data[p0 + q];
+      }
+    }
+    for (int64_t q = threadIdx.x; q <= r1 - r0; q += kThreads)
+      rptr[q] = static_cast<int64_t>(indptr[r0 + q]);
+    __syncthreads();
+    auto fetch = [&](int c) {
+      const int64_t w = static_cast<int64_t>(c) - lo;
+      if (static_cast<uint64_t>(w) < static_cast<uint64_t>(nw))
+        return __builtin_bit_cast(Vec<S, CW>, xs[w * LR + l]);
+      return load_vec<S, CW>(Xc + static_cast<int64_t>(c) * ldx);
+    };
+    for (int64_t row = r0 + g; row < r1; row += rows_per_pass) {
+      const int64_t s = clamp64(rptr[row - r0], 0, nnz);
+      const int64_t e = clamp64(rptr[row - r0 + 1], s, nnz);
+      A acc[CW];
+#pragma unroll
+      for (int c = 0; c < CW; ++c) acc[c] = vzero<A>();
+      if (staged && s >= p0 && e <= p1) {
+        // Window reads for four values at a time, no branch on the common
+        // path; the rare out-of-window column is read from X afterwards.
+        auto step = [&](int code, A a, const Vec<S, CW> &lv) {
+          if (code == -1) return;  // column outside [0, n_cols)
+          Vec<S, CW> xv = lv;
+          if (code < -1) xv = load_vec<S, CW>(Xc + static_cast<int64_t>(-2 - code) * ldx);
+#pragma unroll
+          for (int c = 0; c < CW; ++c) acc[c] = vmadd<V>(acc[c], a, xv.v[c]);
+        };
+        int64_t q = s - p0;
+        const int64_t qe = e - p0;
+        for (; q + 4 <= qe; q += 4) {
+          int code[4];
+          A au[4];
+          Vec<S, CW> lv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            code[u] = cols[q + u];
+            au[u] = V::widen(vals[q + u]);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            lv[u] = __builtin_bit_cast(Vec<S, CW>, xs[((code[u] > 0 ? code[u] : 0) << lg) + l]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) step(code[u], au[u], lv[u]);
+        }
+        for (; q < qe; ++q) {
+          const int code = cols[q];
+          step(code, V::widen(vals[q]),
+               __builtin_bit_cast(Vec<S, CW>, xs[((code > 0 ? code : 0) << lg) + l]));
+        }
+      } else {
+        for (int64_t p = s; p < e; ++p) {
+          const int64_t c = static_cast<int64_t>(indices[p]);
+          if (static_cast<uint64_t>(c) < static_cast<uint64_t>(n_cols)) {
+            const A a = V::widen(data[p]);
+            const Vec<S, CW> xv = fetch(static_cast<int>(c));
+#pragma unroll
+            for (int cc = 0; cc < CW; ++cc) acc[cc] = vmadd<V>(acc[cc], a, xv.v[cc]);
+          }
+        }
+      }
+      if (col < k) {
+        Vec<S, CW> out;
+#pragma unroll
+        for (int c = 0; c < CW; ++c) out.v[c] = V::narrow(acc[c]);
+        store_vec<S, CW>(Y + row * ldy + col, out);
+      }
+    }
+    __syncthreads();  // the next tile overwrites the staged data
   }
 }
 
@@ -243,7 +426,7 @@ template <class V, class I>
 msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data_v,
                       const void *indices_v, const void *indptr_v, int64_t batch, int64_t k,
                       const void *X_v, int64_t x_batch, int64_t ldx, void *Y_v, int64_t y_batch,
-                      int64_t ldy, hipStream_t stream) {
+                      int64_t ldy, const msx_csr_plan *plan, hipStream_t stream) {
   using S = typename V::Storage;
   constexpr int CWV = static_cast<int>(16 / sizeof(S));
   const auto *data = static_cast<const S *>(data_v);
@@ -258,6 +441,26 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // Poisson matrix at k = 64: 468 us against 493 us for spmm_rows; at four or
   // eight lines per row the extra reads of the matrix cancel the gain.
   const int64_t row_bytes = k * static_cast<int64_t>(sizeof(S));
+  // Column windows of a bound plan: every tile's window of X, its values
+  // and row pointers in LDS.
+  if (vec && batch == 1 && plan != nullptr && plan->win_rows_max > 0 &&
+      plan->n_win == (n_rows + kWinRows - 1) / kWinRows && k <= int64_t{kWave} * CWV) {
+    int LR = 1;
+    while (LR * CWV < k) LR <<= 1;
+    const int64_t tile_cap = plan->win_nnz_max;
+    const int64_t cap4 = (tile_cap + 3) & ~int64_t{3};
+    const int64_t lds = plan->win_rows_max * LR * 16 + (kWinRows + 2) * 8 +
+                        cap4 * static_cast<int64_t>(sizeof(typename V::Storage) + 4);
+    if (lds <= kWinLdsBytes) {
+      const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(plan->n_win, kMaxGrid));
+      hipLaunchKernelGGL((spmm_window<V, I, CWV>), dim3(grid), dim3(kThreads),
+                         static_cast<size_t>(lds), stream, data, indices, indptr, X, ldx, Y, ldy,
+                         n_rows, nnz, n_cols, k, LR, plan->win, plan->n_win, plan->win_rows_max,
+                         tile_cap);
+      MSX_HIP_TRY(hipGetLastError());
+      return MSX_OK;
+    }
+  }
   const int G = static_cast<int>(row_bytes / 128);
   if (vec && row_bytes == 256) {
     constexpr int LRT = 128 / 16;
@@ -307,14 +510,68 @@ template <class V>
 msx_status spmm_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
                    const void *indices, const void *indptr, int64_t batch, int64_t k, const void *X,
                    int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
-                   hipStream_t stream) {
+                   const msx_csr_plan *plan, hipStream_t stream) {
   if (it == MSX_I32)
     return spmm_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
-                                  ldx, Y, y_batch, ldy, stream);
+                                  ldx, Y, y_batch, ldy, plan, stream);
   return spmm_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
-                                ldx, Y, y_batch, ldy, stream);
+                                ldx, Y, y_batch, ldy, plan, stream);
 }
 
+template <class I>
+msx_status windows_typed(msx_csr_plan *p, const void *indices, const void *indptr,
+                         hipStream_t stream) {
+  const int64_t n_win = (p->n_rows + kWinRows - 1) / kWinRows;
+  if (n_win == 0 || p->nnz == 0) return MSX_OK;
+  const size_t b_win = (static_cast<size_t>(2 * n_win) * sizeof(int32_t) + 255) / 256 * 256;
+  char *base = nullptr;
+  if (hipMalloc(&base, b_win + 256) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MSX_ENOMEM, "msx_csr_plan_create_bound: device allocation of the column windows failed.");
+  }
+  p->win = reinterpret_cast<int32_t *>(base);
+  p->win_bytes = b_win + 256;
+  auto *widest = reinterpret_cast<unsigned long long *>(base + b_win);
+  MSX_HIP_TRY(hipMemsetAsync(widest, 0, 2 * sizeof(*widest), stream));
+  const int64_t groups = (n_win + kThreads / kWave - 1) / (kThreads / kWave);
+  hipLaunchKernelGGL((window_bounds<I>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
+                     stream, static_cast<const I *>(indices), static_cast<const I *>(indptr),
+                     p->n_rows, p->nnz, p->n_cols, n_win, p->win, widest);
+  MSX_HIP_TRY(hipGetLastError());
+  unsigned long long w[2] = {0, 0};
+  MSX_HIP_TRY(hipMemcpyAsync(w, widest, sizeof(w), hipMemcpyDeviceToHost, stream));
+  MSX_HIP_TRY(hipStreamSynchronize(stream));
+  p->n_win = n_win;
+  p->win_rows_max = static_cast<int64_t>(w[0]);
+  p->win_nnz_max = static_cast<int64_t>(w[1]);
+  return MSX_OK;
+}
+
+}  // namespace
+
+namespace {
+msx_status spmm_dispatch(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                         const void *data, const void *indices, const void *indptr, int64_t batch,
+                         int64_t k, const void *X, int64_t x_batch, int64_t ldx, void *Y,
+                         int64_t y_batch, int64_t ldy, const msx_csr_plan *plan,
+                         hipStream_t stream) {
+  if (batch <= 0 || n_rows <= 0 || k <= 0) return MSX_OK;
+  switch (vt) {
+  case MSX_F32:
+    return spmm_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, plan, stream);
+  case MSX_F16:
+    return spmm_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, plan, stream);
+  case MSX_BF16:
+    return spmm_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                         Y, y_batch, ldy, plan, stream);
+  case MSX_C64:
+    return spmm_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
+                        Y, y_batch, ldy, plan, stream);
+  }
+  return fail(MSX_ETYPE, "csr_matmul unsupported value dtype.");
+}
 }  // namespace
 
 msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
@@ -322,29 +579,22 @@ msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64
                                const void *indptr, int64_t batch, int64_t k, const void *X,
                                int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
                                hipStream_t stream) {
-  if (batch <= 0 || n_rows <= 0 || k <= 0) return MSX_OK;
-  switch (vt) {
-  case MSX_F32:
-    return spmm_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
-                        Y, y_batch, ldy, stream);
-  case MSX_F16:
-    return spmm_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
-                        Y, y_batch, ldy, stream);
-  case MSX_BF16:
-    return spmm_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
-                         Y, y_batch, ldy, stream);
-  case MSX_C64:
-    return spmm_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch, ldx,
-                        Y, y_batch, ldy, stream);
-  }
-  return fail(MSX_ETYPE, "csr_matmul unsupported value dtype.");
+  return spmm_dispatch(vt, it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
+                       ldx, Y, y_batch, ldy, nullptr, stream);
+}
+
+msx_status build_windows(msx_csr_plan *p, const void *indices, const void *indptr,
+                         hipStream_t stream) {
+  return p->itype == MSX_I32 ? windows_typed<int32_t>(p, indices, indptr, stream)
+                             : windows_typed<int64_t>(p, indices, indptr, stream);
 }
 
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,
-                       const void *X, int64_t ldx, void *Y, int64_t ldy, hipStream_t stream) {
-  return launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, k, X, 0, ldx, Y,
-                             0, ldy, stream);
+                       const void *X, int64_t ldx, void *Y, int64_t ldy, const msx_csr_plan *plan,
+                       hipStream_t stream) {
+  return spmm_dispatch(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, k, X, 0, ldx, Y, 0,
+                       ldy, plan, stream);
 }
 
 }  // namespace msx

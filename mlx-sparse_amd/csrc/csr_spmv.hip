@@ -322,12 +322,13 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // Misaligned streams cannot use the quad loads of the plan kernels (the
   // long-row kernel reads the caller's arrays even on a sliced plan).
   const bool use_plan = plan != nullptr && quads_ok;
-  // Matrices whose value and index streams exceed the Infinity Cache are
-  // read with the non-temporal policy (banded 44.7M values: 140 -> 122 us);
-  // smaller ones stay cache-resident between calls, which the policy would
-  // give up (3D Poisson 128^3: 42 -> 47 us).
+  // Matrices whose value and index streams cannot stay in the Infinity
+  // Cache are read with the non-temporal policy (banded 44.7M values, f32:
+  // 140 -> 122 us, bf16: 160 -> 147 us); smaller ones stay cache-resident
+  // between calls, which the policy would give up (3D Poisson 128^3:
+  // 42 -> 47 us).
   const bool stream_nt =
-      static_cast<uint64_t>(nnz) * (sizeof(S) + sizeof(I)) > kInfinityCacheBytes;
+      static_cast<uint64_t>(nnz) * (sizeof(S) + sizeof(I)) > kStreamNtBytes;
   if (use_plan && plan->n_panels > 0) {
     MSX_HIP_TRY_ST(launch_spmv_panels(plan, indptr, x, y, stream));
   } else if (use_plan && plan->n_slices > 0) {

@@ -108,7 +108,26 @@ __device__ inline c64 vmul_acc<C64>(c64 a, c64 b) {
 }
 
 __device__ inline float vadd(float a, float b) { return a + b; }
+
+// acc + a * x with the reference's rounding (the product rounded to the
+// accumulator type, then added).  float16: the product of two binary16
+// values has at most 22 significant bits and an exponent inside binary32's
+// normal range, so it is exact in float32 and one fused multiply-add gives
+// the same bits; gfx950 does it in one v_fma_mix_f32 that also widens x.
+template <class V>
+__device__ inline typename V::Acc vmadd(typename V::Acc acc, typename V::Acc a,
+                                        typename V::Storage x);
 __device__ inline c64 vadd(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
+
+template <class V>
+__device__ inline typename V::Acc vmadd(typename V::Acc acc, typename V::Acc a,
+                                        typename V::Storage x) {
+  return vadd(acc, vmul_acc<V>(a, x));
+}
+template <>
+__device__ inline float vmadd<F16>(float acc, float a, uint16_t x) {
+  return __builtin_fmaf(a, half_bits_to_float(x), acc);
+}
 
 template <class A>
 __device__ inline A vzero() {
@@ -145,8 +164,10 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t nu
 // lines from L2).
 constexpr int kCacheDefault = 0;
 constexpr int kCacheStream = 2;
-// MI355X's Infinity Cache (memory-side, shared by all XCDs).
-constexpr uint64_t kInfinityCacheBytes = uint64_t{256} << 20;
+// Matrix streams above this size are read with kCacheStream: they cannot
+// stay in MI355X's 256 MB Infinity Cache (memory-side, shared by all XCDs)
+// next to x, y and the plan between calls.  Three quarters of the cache.
+constexpr uint64_t kStreamNtBytes = uint64_t{192} << 20;
 
 // Load N bytes (8, 16 or 32) at byte offset `off` from a buffer.
 template <int N, int AUX = kCacheDefault>

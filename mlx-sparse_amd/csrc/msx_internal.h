@@ -99,6 +99,16 @@ struct msx_csr_plan {
   void *pn_base;              // allocation of pn_data, pn_col, pn_dest, pn_prod
   void *pn_meta;              // allocation of the tile, segment and chunk arrays
   size_t pn_bytes;
+  // Column windows of bound plans (csr_spmm.hip): for row tile t (rows
+  // [64t, 64t + 64)), win[2t] and win[2t + 1] are the lowest and highest
+  // valid column of its values (1 and 0 when it has none).  win_rows_max is
+  // the widest window in rows of X (0 when the plan has no windows);
+  // win_nnz_max the most values of a tile.
+  int64_t n_win;
+  int64_t win_rows_max;
+  int64_t win_nnz_max;
+  int32_t *win;
+  size_t win_bytes;
 };
 
 namespace msx {
@@ -146,6 +156,10 @@ msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64
                                hipStream_t stream);
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,
-                       const void *X, int64_t ldx, void *Y, int64_t ldy, hipStream_t stream);
+                       const void *X, int64_t ldx, void *Y, int64_t ldy, const msx_csr_plan *plan,
+                       hipStream_t stream);
+// Column windows of a bound plan (csr_spmm.hip).  Synchronises `stream`.
+msx_status build_windows(msx_csr_plan *p, const void *indices, const void *indptr,
+                         hipStream_t stream);
 
 }  // namespace msx

@@ -73,7 +73,7 @@ def rmatmat(a, data: torch.Tensor, G: torch.Tensor) -> torch.Tensor:
     ah = _adjoint_csr(a, data)
     if ah is not None:
         d, i, p = ah.buffers(data.device)
-        return _native.csr_matmul(d, i, p, G, ah.shape)
+        return _native.csr_matmul(d, i, p, G, ah.shape, plan=ah.plan(data.device))
     return _native.csr_matmul_transpose(_conj(data), indices, indptr, G, a.shape)
 
 

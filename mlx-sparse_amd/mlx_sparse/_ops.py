@@ -77,7 +77,8 @@ def _csr_matmul_rank2(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:
 
         return CSRMatMul.apply(a.data.to(rhs.device), rhs, a, True)
     data, indices, indptr = a.buffers(rhs.device)
-    return _native.csr_matmul(data, indices, indptr, rhs, a.shape, plan=None)
+    # the cached bound plan carries the column windows of the row tiles
+    return _native.csr_matmul(data, indices, indptr, rhs, a.shape, plan=a.plan(rhs.device))
 
 
 def _csr_matmul_batched(a: CSRArray, rhs: torch.Tensor) -> torch.Tensor:

@@ -481,6 +481,7 @@ py::dict plan_info(const Plan &plan) {
   d["n_tiles"] = info.n_tiles;
   d["panel_values"] = info.panel_values;
   d["panel_bytes"] = info.panel_bytes;
+  d["window_rows"] = info.window_rows;
   return d;
 }
 

@@ -22,7 +22,7 @@ class PlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in (
         "n_rows", "nnz", "block_nnz", "block_rows", "chunk_nnz", "n_blocks", "n_bounds", "n_long_rows",
         "n_chunks", "device", "plan_bytes", "n_slices", "slice_width", "slice_bytes",
-        "n_panels", "panel_width", "n_tiles", "panel_values", "panel_bytes")]
+        "n_panels", "panel_width", "n_tiles", "panel_values", "panel_bytes", "window_rows")]
 
 
 class PlanOptions(ctypes.Structure):
@@ -187,14 +187,16 @@ def spmv(data, indices, indptr, x, n_rows, n_cols, plan: Plan | None = None, y=N
     return y
 
 
-def spmm(data, indices, indptr, X, n_rows, n_cols, Y=None, ldx=None, ldy=None):
+def spmm(data, indices, indptr, X, n_rows, n_cols, Y=None, ldx=None, ldy=None,
+         plan: Plan | None = None):
     k = X.shape[1]
     if Y is None:
         Y = torch.empty((n_rows, k), dtype=data.dtype, device=data.device)
     st = lib().msx_csr_spmm(VT[data.dtype], IT[indices.dtype], n_rows, n_cols, data.numel(),
                             _p(data), _p(indices), _p(indptr), k, _p(X),
                             ldx if ldx is not None else X.stride(0), _p(Y),
-                            ldy if ldy is not None else Y.stride(0), None, _stream())
+                            ldy if ldy is not None else Y.stride(0),
+                            plan.ptr if plan is not None else None, _stream())
     if st != OK:
         raise RuntimeError(f"msx_csr_spmm: {st} {last_error()}")
     return Y

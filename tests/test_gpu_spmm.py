@@ -171,3 +171,87 @@ def test_poisson_spmm_k64_full_size():
                        m.shape[1], plan=plan)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(to_numpy(y), got[:, c])
+
+
+# -- column windows of bound plans (banded matrices) ---------------------------------
+
+
+def _banded(n, half_band, seed, vtype, index_dtype=np.int32):
+    from mlx_sparse import synthetic
+
+    m = synthetic.banded(n, half_band, 0.65, 10.0, seed=seed, index_dtype=index_dtype)
+    rng = np.random.default_rng(seed)
+    return m, _values(rng, m.nnz, vtype)
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("k", [4, 8, 32, 64, 128, 256])
+def test_window_spmm_matches_oracle_and_plan_free(vtype, k):
+    """A bound plan of a banded matrix records each 64-row tile's column
+    window; the SpMM then gathers X from LDS.  Same sums as without the plan
+    (bit for bit, every type) and as the oracle (float32 bit for bit)."""
+    n, hb = 3001, 12  # n not a multiple of the 64-row tile
+    m, data = _banded(n, hb, seed=k, vtype=vtype)
+    rng = np.random.default_rng(100 + k)
+    X = _values(rng, (n, k), vtype)
+    d, i, p = to_torch(data, vtype, DEV), to_torch(m.indices, None, DEV), to_torch(m.indptr, None, DEV)
+    plan = _capi.Plan(p, n, m.nnz, data=d, indices=i, n_cols=n)
+    w = plan.info().window_rows
+    assert 32 <= w <= 32 + 2 * hb, w  # a full tile plus the band on each side
+    Xt = to_torch(X, vtype, DEV)
+    got = _capi.spmm(d, i, p, Xt, n, n, plan=plan)
+    ref = _capi.spmm(d, i, p, Xt, n, n)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_numpy(got), to_numpy(ref))
+    want = orc.csr_matmul(data, m.indices, m.indptr, X, n, vtype=vtype, n_threads=8)
+    if vtype == "float32":
+        np.testing.assert_array_equal(to_numpy(got), want)
+    else:
+        scale = orc.row_scale(data, m.indices, m.indptr, X, n, vtype=vtype)
+        assert_rows_close(to_numpy(got), want, scale, vtype, f"window {vtype} k={k}")
+    plan.close()
+
+
+def test_window_spmm_columns_outside_the_recorded_window():
+    """Columns moved after the plan was built (same buffers) and columns out
+    of range: values outside a tile's recorded window are read from X
+    directly, so the product still equals the oracle."""
+    n, k = 2000, 32
+    m, data = _banded(n, 6, seed=3, vtype="float32", index_dtype=np.int64)
+    rng = np.random.default_rng(5)
+    X = _values(rng, (n, k), "float32")
+    d, i, p = to_torch(data, "float32", DEV), to_torch(m.indices, None, DEV), to_torch(m.indptr, None, DEV)
+    plan = _capi.Plan(p, n, m.nnz, data=d, indices=i, n_cols=n)
+    assert plan.info().window_rows > 0
+    moved = m.indices.copy()
+    moved[::97] = (moved[::97] + n // 2) % n  # far outside each tile's window
+    moved[5] = n + 7                          # out of range: adds nothing
+    i.copy_(to_torch(moved, None, DEV))
+    got = _capi.spmm(d, i, p, to_torch(X, "float32", DEV), n, n, plan=plan)
+    torch.cuda.synchronize()
+    # the GPU skips the out-of-range entry (the reference would read past X):
+    # the oracle gets the matrix without it
+    keep = (moved >= 0) & (moved < n)
+    rows = np.repeat(np.arange(n), np.diff(m.indptr))
+    kept_indptr = np.concatenate([[0], np.cumsum(np.bincount(rows[keep], minlength=n))])
+    want = orc.csr_matmul(data[keep], moved[keep], kept_indptr.astype(np.int64), X, n,
+                          vtype="float32", n_threads=8)
+    np.testing.assert_array_equal(to_numpy(got), want)
+    plan.close()
+
+
+def test_window_not_used_when_too_wide():
+    """A random matrix's tiles span all columns: the window does not fit LDS
+    and the SpMM keeps the global-gather kernels (same result either way)."""
+    rng = np.random.default_rng(11)
+    indices, indptr, nnz = _matrix(rng, 4000, 20000, 20, np.int32)
+    data = _values(rng, nnz, "float32")
+    d, i, p = to_torch(data, "float32", DEV), to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    plan = _capi.Plan(p, 4000, nnz, data=d, indices=i, n_cols=20000)
+    assert plan.info().window_rows > 10000
+    X = _values(rng, (20000, 64), "float32")
+    got = _capi.spmm(d, i, p, to_torch(X, "float32", DEV), 4000, 20000, plan=plan)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(
+        to_numpy(got), orc.csr_matmul(data, indices, indptr, X, 4000, vtype="float32", n_threads=8))
+    plan.close()
