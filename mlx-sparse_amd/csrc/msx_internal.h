@@ -100,7 +100,7 @@ struct msx_csr_plan {
   void *pn_meta;              // allocation of the tile, segment and chunk arrays
   size_t pn_bytes;
   // Column windows of bound plans (csr_spmm.hip): for row tile t (rows
-  // [64t, 64t + 64)), win[2t] and win[2t + 1] are the lowest and highest
+  // [32t, 32t + 32)), win[2t] and win[2t + 1] are the lowest and highest
   // valid column of its values (1 and 0 when it has none).  win_rows_max is
   // the widest window in rows of X (0 when the plan has no windows);
   // win_nnz_max the most values of a tile.
@@ -129,9 +129,9 @@ msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_col
 msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                         hipStream_t stream);
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream);
-// True when the short blocks' columns are scattered over an x of more than
-// 8 MB (the AUTO rule for a reordered copy); also the number of values in
-// short blocks.  Synchronises `stream`.
+// True when most short blocks have valid columns spread over more than a
+// quarter of x (the AUTO rule's test for a reordered copy); also the number
+// of values in short blocks.  Synchronises `stream`.
 msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,
                            bool *scattered, int64_t *short_values);
 // Minimum short-row values of an AUTO panel plan: one pass-1 chunk
