@@ -79,7 +79,9 @@ typedef enum msx_slice_mode {
 } msx_slice_mode;
 
 typedef struct msx_plan_options {
-  int64_t block_nnz;  /* W: 0 = default (256), else a power of two in [64, 1024] */
+  int64_t block_nnz;  /* W: 0 = default (512 when rows average 20 or more
+                         values and the values are not complex64, else 256),
+                         else a power of two in [64, 1024] */
   int32_t slice_mode; /* msx_slice_mode */
   int32_t reserved;   /* must be 0 */
 } msx_plan_options;
@@ -129,7 +131,8 @@ msx_status msx_device_count(int *count);
  * blocks (consecutive rows processed by one wavefront) and long rows (split
  * into chunks processed by whole workgroups, then summed in chunk order).
  * Synchronises `stream` once to read the block counts.  `block_nnz` selects
- * W (0 = library default 256; otherwise a power of two in [64, 1024]).
+ * W (0 = library default: 512 when nnz >= 20 * n_rows, else 256; otherwise
+ * a power of two in [64, 1024]).
  * The plan holds scratch for long-row chunk sums: calls sharing one plan
  * must be ordered (one stream) - concurrent calls on a shared plan race.
  *

@@ -73,12 +73,15 @@ __global__ void __launch_bounds__(kThreads)
                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
                 typename V::Storage *__restrict__ y, const int32_t *__restrict__ bounds,
                 const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
-                int64_t n_cols) {
+                int64_t n_cols, uint32_t x_bytes) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   // A block spans < 2W values; with the 4-aligned start, <= W/2 + 1 quads.
+  // The lanes hold the first QPL * 64 of them (W/2 when W >= 128); the one
+  // quad that can lie past those is summed by a separate tail step, so the
+  // registers of a whole third chunk are not spent on it.
   constexpr int kQuads = W / 2 + 1;
-  constexpr int QPL = (kQuads + kWave - 1) / kWave;
+  constexpr int QPL = (W / 2 + kWave - 1) / kWave;
   constexpr int kCap = 4 * kQuads;  // products staged per wave
   __shared__ A lds_prod[kWavesPerGroup][kCap];
   __shared__ int32_t lds_ptr[kWavesPerGroup][kBlockRows + 1];
@@ -105,39 +108,67 @@ __global__ void __launch_bounds__(kThreads)
     const int nq = static_cast<int>((p1 - a0 + 3) >> 2);
 
     // Row pointers of the block, relative to a0 and clamped into the block.
+    // Every load below is unconditional: lanes with nothing to load address
+    // past the end of a descriptor and read zero, so a wave issues all of
+    // its loads before it waits on any.
+    const auto rr = make_rsrc(indptr + r0, static_cast<uint64_t>(m + 1) * sizeof(I));
     int32_t rp[(kBlockRows + kWave) / kWave];
 #pragma unroll
     for (int k = 0; k < (kBlockRows + kWave) / kWave; ++k) {
       const int i = lane + k * kWave;
-      rp[k] = 0;
-      if (i <= m) rp[k] = static_cast<int32_t>(clamp64(static_cast<int64_t>(indptr[r0 + i]), p0, p1) - a0);
+      const int64_t v = static_cast<int64_t>(buffer_index<I>(rr, static_cast<uint32_t>(i) * sizeof(I)));
+      rp[k] = i <= m ? static_cast<int32_t>(clamp64(v, p0, p1) - a0) : 0;
     }
 
     // Phase 1: all quads of the block, then all gathers, then products.
-    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(nnz - a0) * sizeof(I));
-    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
+    // The descriptors end at p1, so quads past the block read zero.
+    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(p1 - a0) * sizeof(I));
+    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(p1 - a0) * sizeof(S));
     Quad<I> iq[QPL];
     Quad<S> dq[QPL];
 #pragma unroll
     for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
-      if (q < nq) {
-        iq[k] = load_quad<I, AUX>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
-        dq[k] = load_quad<S, AUX>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
-      }
+      const uint32_t q = static_cast<uint32_t>(lane + k * kWave);
+      iq[k] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
+      dq[k] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
     }
-    S xv[QPL][4];
+    A xv[QPL][4];
+    if (x_bytes != 0) {
+      const auto rx = make_rsrc(x, x_bytes);
+      GatherRaw<S> raw[QPL][4];
 #pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
+      for (int k = 0; k < QPL; ++k) {
+        const int q = lane + k * kWave;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t pos = a0 + 4 * q + e;
-        const int64_t col = static_cast<int64_t>(iq[k].v[e]);
-        xv[k][e] = S{};
-        if (q < nq && pos >= p0 && pos < p1 &&
-            static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
-          xv[k][e] = x[col];
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = a0 + 4 * q + e;
+          const int64_t col = static_cast<int64_t>(iq[k].v[e]);
+          const bool ok = q < nq && pos >= p0 && pos < p1 &&
+                          static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+          raw[k][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(col), ok);
+        }
+      }
+      // every gather is issued before the first is used
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < QPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[k][e] = gather_widen<V>(raw[k][e], static_cast<uint32_t>(iq[k].v[e]));
+    } else {  // x beyond a descriptor's reach: clamped global loads
+#pragma unroll
+      for (int k = 0; k < QPL; ++k) {
+        const int q = lane + k * kWave;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = a0 + 4 * q + e;
+          const int64_t col = static_cast<int64_t>(iq[k].v[e]);
+          const bool ok = q < nq && pos >= p0 && pos < p1 &&
+                          static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+          A v = vzero<A>();
+          if (n_cols > 0) v = V::widen(x[ok ? col : 0]);  // wave-uniform test
+          xv[k][e] = ok ? v : vzero<A>();
+        }
       }
     }
 #pragma unroll
@@ -148,9 +179,22 @@ __global__ void __launch_bounds__(kThreads)
         for (int e = 0; e < 4; ++e) {
           const int64_t pos = a0 + 4 * q + e;
           A pv = vzero<A>();
-          if (pos >= p0 && pos < p1) pv = vmul<V>(dq[k].v[e], xv[k][e]);
+          if (pos >= p0 && pos < p1) pv = vmul_acc<V>(xv[k][e], dq[k].v[e]);
           prod[4 * q + e] = pv;
         }
+      }
+    }
+    if (nq > QPL * kWave) {  // wave-uniform: the block's last quad, one value per lane
+      const int q = QPL * kWave;
+      const int64_t pos = a0 + 4 * q + lane;
+      if (lane < 4) {
+        A pv = vzero<A>();
+        if (pos >= p0 && pos < p1) {
+          const int64_t col = static_cast<int64_t>(indices[pos]);
+          if (static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+            pv = vmul<V>(data[pos], x[col]);
+        }
+        prod[4 * q + lane] = pv;
       }
     }
 #pragma unroll
@@ -304,6 +348,11 @@ uint32_t grid_for(int64_t tiles) {
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+uint32_t gather_bytes(const void *x, int64_t n_cols, size_t elem) {
+  const uint64_t b = (static_cast<uint64_t>(n_cols) * elem + 3) & ~uint64_t{3};
+  return n_cols > 0 && b <= kGatherMaxBytes && aligned(x, 4) ? static_cast<uint32_t>(b) : 0u;
+}
+
 template <class V, class I>
 msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data_v,
                       const void *indices_v, const void *indptr_v, const void *x_v, void *y_v,
@@ -329,6 +378,9 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   // 42 -> 47 us).
   const bool stream_nt =
       static_cast<uint64_t>(nnz) * (sizeof(S) + sizeof(I)) > kStreamNtBytes;
+  // x through a buffer descriptor when it fits one and is dword-aligned
+  // (0: clamped global loads).
+  const uint32_t x_bytes = gather_bytes(x, n_cols, sizeof(S));
   if (use_plan && plan->n_panels > 0) {
     MSX_HIP_TRY_ST(launch_spmv_panels(plan, indptr, x, y, stream));
   } else if (use_plan && plan->n_slices > 0) {
@@ -342,11 +394,11 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
     if (stream_nt)                                                                             \
       hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheStream>), grid, block, 0, stream, data,  \
                          indices, indptr, x, y, plan->bounds, plan->bounds_nnz, plan->n_bounds, \
-                         nnz, n_cols);                                                         \
+                         nnz, n_cols, x_bytes);                                                \
     else                                                                                       \
       hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheDefault>), grid, block, 0, stream, data, \
                          indices, indptr, x, y, plan->bounds, plan->bounds_nnz, plan->n_bounds, \
-                         nnz, n_cols);                                                         \
+                         nnz, n_cols, x_bytes);                                                \
   } while (0)
       switch (plan->block_nnz) {
       case 64: MSX_SPMV_BLOCKS(64); break;

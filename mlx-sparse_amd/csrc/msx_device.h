@@ -12,6 +12,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include "msx_sparse.h"
@@ -157,6 +159,54 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t nu
   const uint32_t n = num_bytes > 0xfffffffcull ? 0xfffffffcu : static_cast<uint32_t>(num_bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
                                            static_cast<int>(n), kBufferFlags);
+}
+
+// Gathers through a descriptor over x.  `x_bytes` is x's size rounded up to
+// a dword (at most kGatherMaxBytes); a lane whose element is invalid loads
+// from offset x_bytes, past the buffer, and reads zero.  The load therefore
+// needs no branch: a conditional load per gather makes the compiler wait for
+// each one before issuing the next.  16-bit elements are read as the aligned
+// dword that holds them (x is then 4-byte aligned), so each gather fills its
+// own 32-bit register.
+constexpr uint64_t kGatherMaxBytes = 0xfffffff0ull;
+
+// Raw bits of x[col] (the holding dword for 16-bit elements), zero when !ok.
+template <class S>
+using GatherRaw = typename std::conditional<sizeof(S) == 8, uint64_t, uint32_t>::type;
+
+template <class S>
+__device__ inline GatherRaw<S> gather_raw(__amdgpu_buffer_rsrc_t rx, uint32_t x_bytes,
+                                          uint32_t col, bool ok) {
+  if constexpr (sizeof(S) == 2) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? (col * 2u) & ~3u : x_bytes, 0, 0);
+  } else if constexpr (sizeof(S) == 4) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? col * 4u : x_bytes, 0, 0);
+  } else {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b64(rx, ok ? col * 8u : x_bytes, 0, 0);
+    return static_cast<uint64_t>(w[0]) | (static_cast<uint64_t>(w[1]) << 32);
+  }
+}
+
+// The accumulator value of a gathered element.
+template <class V>
+__device__ inline typename V::Acc gather_widen(GatherRaw<typename V::Storage> raw, uint32_t col) {
+  using S = typename V::Storage;
+  if constexpr (sizeof(S) == 2) {
+    return V::widen(static_cast<S>(raw >> ((col & 1u) * 16u)));
+  } else {
+    return V::widen(__builtin_bit_cast(S, raw));
+  }
+}
+
+// One index (int32 or int64) at byte offset `off` of a buffer; zero past it.
+template <class I>
+__device__ inline I buffer_index(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(I) == 4) {
+    return static_cast<I>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return static_cast<I>(static_cast<uint64_t>(w[0]) | (static_cast<uint64_t>(w[1]) << 32));
+  }
 }
 
 // Cache policy of a buffer load: kCacheDefault, or kCacheStream for data

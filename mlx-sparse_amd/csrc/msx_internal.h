@@ -32,6 +32,12 @@ bool valid_itype(int it);
 // fall in (block nnz < 2W); R: short blocks never cross a multiple of R rows;
 // C: chunk length of long rows.
 constexpr int64_t kDefaultBlockNnz = 256;
+// Default W for rows averaging kWideBlockMean or more values: larger blocks
+// keep more bytes in flight per wavefront (banded matrix, 42.6 values per
+// row, f32: 103 -> 98 us; bf16: 112 -> 96 us), while short rows lose with
+// them (3D Poisson, 7 per row: 35 -> 40 us).
+constexpr int64_t kWideBlockNnz = 512;
+constexpr int64_t kWideBlockMean = 20;
 constexpr int64_t kBlockRows = 256;
 constexpr int64_t kChunkNnz = 4096;
 // Column slices of a sliced plan: one per XCD.

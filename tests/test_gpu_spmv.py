@@ -148,7 +148,7 @@ def test_long_rows_and_fixup(vtype):
     n_rows, n_cols = lengths.size, 70000
     indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, np.int32)
     _check_spmv(_values(rng, nnz, vtype), indices, indptr, _values(rng, n_cols, vtype), n_rows,
-                n_cols, vtype, what=f"long/{vtype}")
+                n_cols, vtype, plan_w=256, what=f"long/{vtype}")
 
 
 @pytest.mark.parametrize("W", [64, 128, 256, 512, 1024])
@@ -170,6 +170,25 @@ def test_plan_bins_bit_exact(W):
         info = plan.info()
         assert info.n_bounds == want[0].size - 1 and info.n_long_rows == want[1].size
         assert info.n_blocks == info.n_bounds - info.n_long_rows
+        plan.close()
+
+
+def test_default_block_nnz_follows_mean_row_length():
+    # W = 0 asks for the default: 512 when rows average 20 values or more
+    for per_row, want_w in ((19, 256), (20, 512), (0, 256)):
+        indptr = np.arange(1001, dtype=np.int64) * per_row
+        p = torch.from_numpy(indptr.astype(np.int32)).to(DEV)
+        plan = _capi.Plan(p, 1000, int(indptr[-1]))
+        assert plan.info().block_nnz == want_w
+        np.testing.assert_array_equal(plan.export()[0], plan_oracle.plan(indptr, W=want_w)[0])
+        plan.close()
+    # a bound complex64 plan keeps 256 (its wide blocks would halve occupancy)
+    idx = torch.zeros(20000, dtype=torch.int32, device=DEV)
+    p = torch.arange(0, 20001, 20, dtype=torch.int32, device=DEV)
+    for dtype, want_w in ((torch.complex64, 256), (torch.float32, 512), (torch.bfloat16, 512)):
+        plan = _capi.Plan(p, 1000, 20000, data=torch.zeros(20000, dtype=dtype, device=DEV),
+                          indices=idx, n_cols=4, slice_mode=_capi.SLICE_OFF)
+        assert plan.info().block_nnz == want_w, dtype
         plan.close()
 
 
@@ -220,6 +239,37 @@ def test_misaligned_buffers_use_plan_free_path():
     want = orc.csr_matvec(data[1:], indices, indptr, x, 2000)
     assert_rows_close(to_numpy(y), want, orc.row_scale(data[1:], indices, indptr, x, 2000),
                       "float32", "misaligned")
+
+
+@pytest.mark.parametrize("vtype", ["float16", "bfloat16", "float32"])
+def test_x_gathers_at_any_alignment(vtype):
+    """The short-block kernel reads 16-bit x elements as the dword that holds
+    them when x is dword-aligned, and with plain element loads otherwise (x at
+    a 2-byte offset).  n_cols is odd and the last column is used, so the last
+    element sits in the low half of a dword whose high half is past x."""
+    rng = np.random.default_rng(17)
+    n_rows, n_cols = 3000, 2001
+    lengths = rng.integers(0, 40, n_rows)
+    indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, np.int32)
+    indices[::7] = n_cols - 1
+    data = _values(rng, nnz, vtype)
+    x_full = _values(rng, n_cols + 1, vtype)
+    d, i, p = _upload(data, indices, indptr, vtype)
+    plan = _capi.Plan(p, n_rows, nnz)
+    lengths = np.diff(indptr.astype(np.int64))
+    xt_full = to_torch(x_full, vtype, DEV)
+    for off in (0, 1):
+        x = x_full[off:off + n_cols]
+        xt = xt_full[off:off + n_cols]
+        assert (xt.data_ptr() % 4 == 0) == (off == 0 or vtype == "float32")
+        y = _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan)
+        torch.cuda.synchronize()
+        want = orc.csr_matvec(data, indices, indptr, x, n_rows, vtype=vtype)
+        assert_rows_close(to_numpy(y), want, orc.row_scale(data, indices, indptr, x, n_rows, vtype=vtype),
+                          vtype, f"x offset {off}",
+                          exact=orc.row_exact(data, indices, indptr, x, n_rows, vtype=vtype),
+                          lengths=lengths)
+    plan.close()
 
 
 def test_repeat_calls_bitwise_identical():
