@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(kThreads)
                 const uint32_t *__restrict__ s_seg, const typename V::Storage *__restrict__ x,
                 typename V::Acc *__restrict__ partial, int64_t n_rows, int64_t nnz,
                 const void *__restrict__ indptr_v, int index_bytes, int64_t slice_width,
-                int col_bits) {
+                int col_bits, uint64_t x_bytes_total) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   constexpr int QPL = 4;
@@ -227,6 +227,13 @@ __global__ void __launch_bounds__(kThreads)
   const int s = static_cast<int>(blockIdx.x % kSlices);
   const S *xs = x + static_cast<int64_t>(s) * slice_width;
   A *part = partial + static_cast<int64_t>(s) * n_rows;
+  // This slice of x through a descriptor (x_bytes_total == 0: x is not
+  // dword-aligned or too large for one, and the gathers are plain loads).
+  const uint64_t s_off = static_cast<uint64_t>(s) * slice_width * sizeof(S);
+  const uint64_t s_len = x_bytes_total > s_off
+      ? std::min<uint64_t>(slice_width * sizeof(S), x_bytes_total - s_off) : 0;
+  const uint32_t xs_bytes = static_cast<uint32_t>((s_len + 3) & ~uint64_t{3});
+  const auto rxs = make_rsrc(xs, xs_bytes);
   const int64_t n_super = (n_rows + kRows - 1) / kRows;
 
   for (int64_t g = blockIdx.x / kSlices; g * kWavesPerGroup < n_super; g += gridDim.x / kSlices) {
@@ -247,47 +254,59 @@ __global__ void __launch_bounds__(kThreads)
       re[i] = 0;
     }
     wave_lds_sync();
-    for (int64_t c_lo = lo; c_lo < hi; c_lo += kChunk) {
-      const int64_t c_hi = std::min<int64_t>(c_lo + kChunk, hi);
+    // Chunks start on quad boundaries, so a chunk is at most QPL quads per
+    // lane; the descriptors end at the chunk's last value, so every load is
+    // unconditional (lanes past it read zero) and a wave issues all of its
+    // loads before it waits on any.
+    for (int64_t a0 = lo & ~int64_t{3}; a0 < hi; a0 += kChunk) {
+      const int64_t c_lo = std::max(lo, a0);
+      const int64_t c_hi = std::min<int64_t>(a0 + kChunk, hi);
       const int cnt = static_cast<int>(c_hi - c_lo);
-      const int64_t a0 = c_lo & ~int64_t{3};
-      const int nq = static_cast<int>((c_hi - a0 + 3) >> 2);
-      const auto rc = make_rsrc(s_col + a0, static_cast<uint64_t>(nnz - a0) * sizeof(uint32_t));
-      const auto rd = make_rsrc(s_data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
-      Quad<uint32_t> cq[QPL + 1];
-      Quad<S> dq[QPL + 1];
+      const auto rc = make_rsrc(s_col + a0, static_cast<uint64_t>(c_hi - a0) * sizeof(uint32_t));
+      const auto rd = make_rsrc(s_data + a0, static_cast<uint64_t>(c_hi - a0) * sizeof(S));
+      Quad<uint32_t> cq[QPL];
+      Quad<S> dq[QPL];
 #pragma unroll
-      for (int j = 0; j <= QPL; ++j) {
-        const int q = lane + j * kWave;
-        if (q < nq) {
-          cq[j] = load_quad<uint32_t, AUX>(rc, static_cast<uint32_t>(q) * 16u);
-          dq[j] = load_quad<S, AUX>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
-        }
+      for (int j = 0; j < QPL; ++j) {
+        const uint32_t q = static_cast<uint32_t>(lane + j * kWave);
+        cq[j] = load_quad<uint32_t, AUX>(rc, q * 16u);
+        dq[j] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
       }
-      S xv[QPL + 1][4];
+      A xv[QPL][4];
+      if (x_bytes_total != 0) {
+        GatherRaw<S> raw[QPL][4];
 #pragma unroll
-      for (int j = 0; j <= QPL; ++j) {
-        const int q = lane + j * kWave;
+        for (int j = 0; j < QPL; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t pos = a0 + 4 * q + e;
-          xv[j][e] = S{};
-          if (q < nq && pos >= c_lo && pos < c_hi) xv[j][e] = xs[cq[j].v[e] & col_mask];
-        }
+          for (int e = 0; e < 4; ++e) {
+            const int64_t pos = a0 + 4 * (lane + j * kWave) + e;
+            raw[j][e] = gather_raw<S>(rxs, xs_bytes, cq[j].v[e] & col_mask, pos >= c_lo && pos < c_hi);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < QPL; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[j][e] = gather_widen<V>(raw[j][e], cq[j].v[e] & col_mask);
+      } else {
+#pragma unroll
+        for (int j = 0; j < QPL; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t pos = a0 + 4 * (lane + j * kWave) + e;
+            xv[j][e] = vzero<A>();
+            if (pos >= c_lo && pos < c_hi) xv[j][e] = V::widen(xs[cq[j].v[e] & col_mask]);
+          }
       }
       // rows of this chunk: rowid[0] .. rowid[cnt-1] (ascending)
 #pragma unroll
-      for (int j = 0; j <= QPL; ++j) {
-        const int q = lane + j * kWave;
-        if (q < nq) {
+      for (int j = 0; j < QPL; ++j) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int64_t pos = a0 + 4 * q + e;
-            if (pos >= c_lo && pos < c_hi) {
-              const int t = static_cast<int>(pos - c_lo);
-              prod[t] = vmul<V>(dq[j].v[e], xv[j][e]);
-              rowid[t] = static_cast<uint8_t>((cq[j].v[e] >> col_bits) & (kRows - 1));
-            }
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = a0 + 4 * (lane + j * kWave) + e;
+          if (pos >= c_lo && pos < c_hi) {
+            const int t = static_cast<int>(pos - c_lo);
+            prod[t] = vmul_acc<V>(xv[j][e], dq[j].v[e]);
+            rowid[t] = static_cast<uint8_t>((cq[j].v[e] >> col_bits) & (kRows - 1));
           }
         }
       }
@@ -428,10 +447,14 @@ void launch_v(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream)
   const bool stream_nt =
       static_cast<uint64_t>(p->nnz) * (sizeof(S) + sizeof(uint32_t)) > kStreamNtBytes;
   auto kernel = stream_nt ? spmv_sliced<V, kCacheStream> : spmv_sliced<V, kCacheDefault>;
+  // Each slice's descriptor must reach its last byte: x below 4 GB, dword-aligned.
+  const uint64_t xb = static_cast<uint64_t>(p->n_cols) * sizeof(S);
+  const uint64_t x_bytes =
+      xb <= kGatherMaxBytes && reinterpret_cast<uintptr_t>(x) % 4 == 0 ? xb : 0;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const S *>(p->s_data), p->s_col, p->s_seg, static_cast<const S *>(x),
                      static_cast<A *>(p->s_partial), p->n_rows, p->nnz, p->s_indptr,
-                     p->itype == MSX_I64 ? 8 : 4, p->slice_width, p->col_bits);
+                     p->itype == MSX_I64 ? 8 : 4, p->slice_width, p->col_bits, x_bytes);
   const uint32_t mgrid = static_cast<uint32_t>(
       std::max<int64_t>(1, std::min<int64_t>((p->n_rows + kThreads - 1) / kThreads, kMaxGrid)));
   hipLaunchKernelGGL((slice_merge<V>), dim3(mgrid), dim3(kThreads), 0, stream,

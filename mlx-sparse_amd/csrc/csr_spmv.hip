@@ -253,7 +253,7 @@ __global__ void __launch_bounds__(kThreads)
               typename V::Storage *__restrict__ y, const int32_t *__restrict__ long_rows,
               const int32_t *__restrict__ long_chunk_begin, const int32_t *__restrict__ chunk_row,
               typename V::Acc *__restrict__ partials, int64_t n_chunks, int64_t nnz,
-              int64_t n_cols, int64_t C) {
+              int64_t n_cols, int64_t C, uint32_t x_bytes) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   __shared__ A lds4[kWavesPerGroup];
@@ -268,19 +268,58 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t q1 = std::min(q0 + C, re);
     const int64_t a0 = q0 & ~int64_t{3};
     const int nq = static_cast<int>((q1 - a0 + 3) >> 2);
-    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(nnz - a0) * sizeof(I));
-    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(nnz - a0) * sizeof(S));
+    // The descriptors end at q1: quads past the chunk read zero.
+    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(q1 - a0) * sizeof(I));
+    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(q1 - a0) * sizeof(S));
     A acc = vzero<A>();
-#pragma unroll 2
-    for (int q = threadIdx.x; q < nq; q += kThreads) {
-      const Quad<I> iq = load_quad<I, AUX>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
-      const Quad<S> dq = load_quad<S, AUX>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+    if (x_bytes != 0) {
+      // Two quads per thread and step; their loads and all 8 gathers are
+      // unconditional (out-of-range lanes read zero), so a step costs two
+      // dependent round trips.  Sums run over q in order, as below.
+      const auto rx = make_rsrc(x, x_bytes);
+      for (int q = threadIdx.x; q < nq; q += 2 * kThreads) {
+        Quad<I> iq[2];
+        Quad<S> dq[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t pos = a0 + 4 * q + e;
-        const int64_t col = static_cast<int64_t>(iq.v[e]);
-        if (pos >= q0 && pos < q1 && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
-          acc = vadd(acc, vmul<V>(dq.v[e], x[col]));
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t qq = static_cast<uint32_t>(q + u * kThreads);
+          iq[u] = load_quad<I, AUX>(ri, qq * 4u * sizeof(I));
+          dq[u] = load_quad<S, AUX>(rd, qq * 4u * sizeof(S));
+        }
+        GatherRaw<S> raw[2][4];
+        bool ok[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t pos = a0 + 4 * (q + u * kThreads) + e;
+            const int64_t col = static_cast<int64_t>(iq[u].v[e]);
+            ok[u][e] = pos >= q0 && pos < q1 &&
+                       static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+            raw[u][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(col), ok[u][e]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const A xv = gather_widen<V>(raw[u][e], static_cast<uint32_t>(iq[u].v[e]));
+            const A sum = vadd(acc, vmul_acc<V>(xv, dq[u].v[e]));
+            acc = ok[u][e] ? sum : acc;
+          }
+      }
+    } else {  // x beyond a descriptor's reach
+#pragma unroll 2
+      for (int q = threadIdx.x; q < nq; q += kThreads) {
+        const Quad<I> iq = load_quad<I, AUX>(ri, static_cast<uint32_t>(q) * 4u * sizeof(I));
+        const Quad<S> dq = load_quad<S, AUX>(rd, static_cast<uint32_t>(q) * 4u * sizeof(S));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = a0 + 4 * q + e;
+          const int64_t col = static_cast<int64_t>(iq.v[e]);
+          if (pos >= q0 && pos < q1 && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
+            acc = vadd(acc, vmul<V>(dq.v[e], x[col]));
+        }
       }
     }
     const A total = block_sum(acc, lds4);
@@ -418,7 +457,7 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
                          stream, data, indices, indptr, x, y, plan->long_rows,
                          plan->long_chunk_begin, plan->chunk_row,
                          static_cast<A *>(plan->partials), plan->n_chunks, nnz, n_cols,
-                         plan->chunk_nnz);
+                         plan->chunk_nnz, x_bytes);
       MSX_HIP_TRY(hipGetLastError());
       if (plan->n_chunks > plan->n_long) {
         const int64_t groups = (plan->n_long + kWavesPerGroup - 1) / kWavesPerGroup;
