@@ -250,40 +250,76 @@ __global__ void __launch_bounds__(kThreads)
 constexpr int kWinRows = 32;
 constexpr int64_t kWinLdsBytes = 65536;  // LDS of one workgroup's window
 
+// A tile with more values than this can never be staged (4-byte columns
+// alone would fill the 64 KB), so its window is not scanned: it is recorded
+// empty and its value count disables the window kernel for the matrix.
+constexpr int64_t kWinScanMax = 16384;
+
 template <class I>
 __global__ void __launch_bounds__(kThreads)
     window_bounds(const I *__restrict__ indices, const I *__restrict__ indptr, int64_t n_rows,
                   int64_t nnz, int64_t n_cols, int64_t n_win, int32_t *__restrict__ win,
                   unsigned long long *__restrict__ widest) {
-  // widest[0]: window rows, widest[1]: values of a tile
+  // widest[0]: window rows, widest[1]: values of a tile; one atomic per
+  // workgroup (a wave per tile would serialise tens of thousands on them)
+  __shared__ unsigned long long wg_max[2][kThreads / kWave];
   const int lane = threadIdx.x % kWave;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
-  if (t >= n_win) return;
-  const int64_t r0 = t * kWinRows;
-  const int64_t r1 = std::min<int64_t>(r0 + kWinRows, n_rows);
-  const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
-  const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0, nnz);
-  int64_t lo = INT64_MAX, hi = -1;
-  for (int64_t p = p0 + lane; p < p1; p += kWave) {
-    const int64_t c = static_cast<int64_t>(indices[p]);
-    if (static_cast<uint64_t>(c) < static_cast<uint64_t>(n_cols)) {
-      lo = c < lo ? c : lo;
-      hi = c > hi ? c : hi;
-    }
-  }
+  const int wave = threadIdx.x / kWave;
+  unsigned long long w_rows = 0, w_vals = 0;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave; t < n_win;
+       t += static_cast<int64_t>(gridDim.x) * (kThreads / kWave)) {
+    const int64_t r0 = t * kWinRows;
+    const int64_t r1 = std::min<int64_t>(r0 + kWinRows, n_rows);
+    const int64_t p0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+    const int64_t p1 = clamp64(static_cast<int64_t>(indptr[r1]), p0, nnz);
+    const int64_t cnt = p1 - p0;
+    w_vals = std::max<unsigned long long>(w_vals, static_cast<unsigned long long>(cnt));
+    int64_t lo = INT64_MAX, hi = -1;
+    if (cnt <= kWinScanMax) {
+      // four unconditional loads per lane and step (past the tile: zero, masked)
+      const auto rr = make_rsrc(indices + p0, static_cast<uint64_t>(cnt) * sizeof(I));
+      for (int64_t b = 0; b < cnt; b += 4 * kWave) {
+        I c[4];
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) {
-    const int64_t ol = __shfl_xor(lo, d, kWave);
-    const int64_t oh = __shfl_xor(hi, d, kWave);
-    lo = ol < lo ? ol : lo;
-    hi = oh > hi ? oh : hi;
+        for (int u = 0; u < 4; ++u)
+          c[u] = buffer_index<I>(rr, static_cast<uint32_t>(b + lane + u * kWave) * sizeof(I));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t v = static_cast<int64_t>(c[u]);
+          if (b + lane + u * kWave < cnt && static_cast<uint64_t>(v) < static_cast<uint64_t>(n_cols)) {
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+          }
+        }
+      }
+#pragma unroll
+      for (int d = kWave / 2; d >= 1; d >>= 1) {
+        const int64_t ol = __shfl_xor(lo, d, kWave);
+        const int64_t oh = __shfl_xor(hi, d, kWave);
+        lo = ol < lo ? ol : lo;
+        hi = oh > hi ? oh : hi;
+      }
+    }
+    const bool any = hi >= lo;
+    if (lane == 0) {
+      win[2 * t] = any ? static_cast<int32_t>(lo) : 1;
+      win[2 * t + 1] = any ? static_cast<int32_t>(hi) : 0;
+    }
+    if (any) w_rows = std::max<unsigned long long>(w_rows, static_cast<unsigned long long>(hi - lo + 1));
   }
   if (lane == 0) {
-    const bool any = hi >= lo;
-    win[2 * t] = any ? static_cast<int32_t>(lo) : 1;
-    win[2 * t + 1] = any ? static_cast<int32_t>(hi) : 0;
-    if (any) atomicMax(widest, static_cast<unsigned long long>(hi - lo + 1));
-    atomicMax(widest + 1, static_cast<unsigned long long>(p1 - p0));
+    wg_max[0][wave] = w_rows;
+    wg_max[1][wave] = w_vals;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long a = 0, b = 0;
+    for (int w = 0; w < kThreads / kWave; ++w) {
+      a = std::max(a, wg_max[0][w]);
+      b = std::max(b, wg_max[1][w]);
+    }
+    if (a > 0) atomicMax(widest, a);
+    if (b > 0) atomicMax(widest + 1, b);
   }
 }
 
@@ -533,7 +569,8 @@ msx_status windows_typed(msx_csr_plan *p, const void *indices, const void *indpt
   p->win_bytes = b_win + 256;
   auto *widest = reinterpret_cast<unsigned long long *>(base + b_win);
   MSX_HIP_TRY(hipMemsetAsync(widest, 0, 2 * sizeof(*widest), stream));
-  const int64_t groups = (n_win + kThreads / kWave - 1) / (kThreads / kWave);
+  const int64_t groups =
+      std::min<int64_t>((n_win + kThreads / kWave - 1) / (kThreads / kWave), 2048);
   hipLaunchKernelGGL((window_bounds<I>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
                      stream, static_cast<const I *>(indices), static_cast<const I *>(indptr),
                      p->n_rows, p->nnz, p->n_cols, n_win, p->win, widest);

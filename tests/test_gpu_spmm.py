@@ -187,10 +187,10 @@ def _banded(n, half_band, seed, vtype, index_dtype=np.int32):
 @pytest.mark.parametrize("vtype", VTYPES)
 @pytest.mark.parametrize("k", [4, 8, 32, 64, 128, 256])
 def test_window_spmm_matches_oracle_and_plan_free(vtype, k):
-    """A bound plan of a banded matrix records each 64-row tile's column
+    """A bound plan of a banded matrix records each 32-row tile's column
     window; the SpMM then gathers X from LDS.  Same sums as without the plan
     (bit for bit, every type) and as the oracle (float32 bit for bit)."""
-    n, hb = 3001, 12  # n not a multiple of the 64-row tile
+    n, hb = 3001, 12  # n not a multiple of the 32-row tile
     m, data = _banded(n, hb, seed=k, vtype=vtype)
     rng = np.random.default_rng(100 + k)
     X = _values(rng, (n, k), vtype)
@@ -237,6 +237,31 @@ def test_window_spmm_columns_outside_the_recorded_window():
     want = orc.csr_matmul(data[keep], moved[keep], kept_indptr.astype(np.int64), X, n,
                           vtype="float32", n_threads=8)
     np.testing.assert_array_equal(to_numpy(got), want)
+    plan.close()
+
+
+def test_window_tile_too_full_to_scan():
+    """A tile holding more values than LDS could ever stage (one row of
+    20,000 values) is not scanned: the other tiles keep their narrow windows,
+    the window kernel is off for the matrix, and the product is unchanged."""
+    n, hb, k = 30001, 6, 32
+    rng = np.random.default_rng(4)
+    rows = [np.arange(max(0, r - hb), min(n, r + hb + 1)) for r in range(n)]
+    rows[100] = np.sort(rng.choice(n, 20000, replace=False))
+    indptr = np.concatenate([[0], np.cumsum([r.size for r in rows])]).astype(np.int32)
+    indices = np.concatenate(rows).astype(np.int32)
+    data = _values(rng, indices.size, "float32")
+    d, i, p = to_torch(data, "float32", DEV), to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    plan = _capi.Plan(p, n, indices.size, data=d, indices=i, n_cols=n)
+    assert 0 < plan.info().window_rows <= 32 + 2 * hb
+    X = _values(rng, (n, k), "float32")
+    Xt = to_torch(X, "float32", DEV)
+    got = _capi.spmm(d, i, p, Xt, n, n, plan=plan)
+    ref = _capi.spmm(d, i, p, Xt, n, n)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_numpy(got), to_numpy(ref))
+    np.testing.assert_array_equal(
+        to_numpy(got), orc.csr_matmul(data, indices, indptr, X, n, vtype="float32", n_threads=8))
     plan.close()
 
 
