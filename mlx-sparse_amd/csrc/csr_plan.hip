@@ -321,6 +321,7 @@ void release(msx_csr_plan *p) {
   if (p->pn_base) (void)hipFree(p->pn_base);
   if (p->pn_meta) (void)hipFree(p->pn_meta);
   if (p->win) (void)hipFree(p->win);
+  if (p->ls_base) (void)hipFree(p->ls_base);
   delete p;
 }
 
@@ -392,6 +393,7 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
     st = build_slices(p, data, indices, indptr, s);
   }
   if (st == MSX_OK) st = build_windows(p, indices, indptr, s);
+  if (st == MSX_OK) st = build_long_slices(p, indices, indptr, s);
   if (st != MSX_OK) {
     release(p);
     return st;
@@ -428,7 +430,8 @@ extern "C" msx_status msx_csr_plan_info(const msx_csr_plan *plan, msx_plan_info 
   info->n_chunks = plan->n_chunks;
   info->device = plan->device;
   info->plan_bytes =
-      static_cast<int64_t>(plan->bytes + plan->s_bytes + plan->pn_bytes + plan->win_bytes);
+      static_cast<int64_t>(plan->bytes + plan->s_bytes + plan->pn_bytes + plan->win_bytes +
+                           plan->ls_bytes);
   info->n_slices = plan->n_slices;
   info->slice_width = plan->slice_width;
   info->slice_bytes = static_cast<int64_t>(plan->s_bytes);

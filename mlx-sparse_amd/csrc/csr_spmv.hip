@@ -450,6 +450,11 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
       MSX_HIP_TRY(hipGetLastError());
     }
   }
+  if (use_plan && plan->n_chunks > 0 && plan->ls_units > 0 && x_bytes != 0) {
+    // long rows cut at the XCD column slices (sorted columns, x >= 4 MB)
+    MSX_HIP_TRY_ST(launch_long_sliced(plan, data, indices, x, y, x_bytes, stream_nt, stream));
+    return MSX_OK;
+  }
   if (use_plan) {
     if (plan->n_chunks > 0) {
       auto long_kernel = stream_nt ? spmv_long<V, I, kCacheStream> : spmv_long<V, I, kCacheDefault>;

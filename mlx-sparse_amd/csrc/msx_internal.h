@@ -115,6 +115,22 @@ struct msx_csr_plan {
   int64_t win_nnz_max;
   int32_t *win;
   size_t win_bytes;
+  // XCD-sliced long rows (csr_long_slice.hip); ls_units == 0 when unused.
+  // Bound plans whose long rows all hold sorted columns cut each long row at
+  // the kSlices column-slice boundaries into pieces of at most
+  // kLongPieceMax values.  Pieces are grouped by slice ([ls_slice_begin[s],
+  // ls_slice_begin[s + 1])) and carry the accumulator slot they write;
+  // long row li owns slots [ls_row_slot[li], ls_row_slot[li + 1]).
+  int64_t ls_units;
+  int64_t ls_slice_max;     // most pieces of one slice
+  int64_t *ls_begin;        // ls_units: first position of the piece
+  int32_t *ls_len;          // ls_units: values in the piece
+  int32_t *ls_slot;         // ls_units: accumulator slot of the piece
+  int32_t *ls_slice_begin;  // kSlices + 1
+  int32_t *ls_row_slot;     // n_long + 1
+  void *ls_partial;         // ls_units accumulators
+  void *ls_base;
+  size_t ls_bytes;
 };
 
 namespace msx {
@@ -164,6 +180,16 @@ msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_col
                        const void *data, const void *indices, const void *indptr, int64_t k,
                        const void *X, int64_t ldx, void *Y, int64_t ldy, const msx_csr_plan *plan,
                        hipStream_t stream);
+// XCD-sliced long rows of a bound plan (csr_long_slice.hip): built when
+// x is at least 4 MB and every long row's columns are sorted; otherwise the
+// plan keeps ls_units == 0.  Synchronises `stream`.
+msx_status build_long_slices(msx_csr_plan *p, const void *indices, const void *indptr,
+                             hipStream_t stream);
+// Long rows of such a plan: y[row] for every long row.  x_bytes as for the
+// short-block kernel (x's size rounded up to a dword, nonzero).
+msx_status launch_long_sliced(const msx_csr_plan *p, const void *data, const void *indices,
+                              const void *x, void *y, uint32_t x_bytes, bool stream_nt,
+                              hipStream_t stream);
 // Column windows of a bound plan (csr_spmm.hip).  Synchronises `stream`.
 msx_status build_windows(msx_csr_plan *p, const void *indices, const void *indptr,
                          hipStream_t stream);

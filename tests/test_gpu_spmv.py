@@ -151,6 +151,55 @@ def test_long_rows_and_fixup(vtype):
                 n_cols, vtype, plan_w=256, what=f"long/{vtype}")
 
 
+@pytest.mark.parametrize("vtype", VTYPES)
+def test_long_rows_sliced_by_column(vtype):
+    """A bound plan with x of 4 MB or more cuts long rows with sorted columns
+    at the 8 XCD column slices (pieces of at most 1020 values, each slice's
+    pieces on its own XCD); a long row with unsorted columns keeps the
+    chunked long-row kernel.  Both match the oracle; an out-of-range column
+    at the end of a sorted long row adds nothing."""
+    rng = np.random.default_rng(31)
+    n_rows, n_cols = 3000, 2_200_000
+    lengths = rng.integers(0, 20, n_rows)
+    special = {17: 300, 400: 1021, 401: 1020, 1200: 5000, 2000: 40000, 2999: 200000, 5: 257}
+    for r, L in special.items():
+        lengths[r] = L
+    cols = []
+    for L in lengths:
+        c = np.unique(rng.integers(0, n_cols, int(L * 1.2) + 8))
+        cols.append(np.sort(rng.permutation(c)[:L]))
+    cols[1200][-1] = n_cols + 5  # out of range, still sorted
+    indptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    indices = np.concatenate(cols).astype(np.int32)
+    nnz = int(indptr[-1])
+    data = _values(rng, nnz, vtype)
+    x = _values(rng, n_cols, vtype)
+    keep = indices < n_cols
+    rows = np.repeat(np.arange(n_rows), lengths)
+    k_indptr = np.concatenate([[0], np.cumsum(np.bincount(rows[keep], minlength=n_rows))]).astype(np.int32)
+    want = orc.csr_matvec(data[keep], indices[keep], k_indptr, x, n_rows, vtype=vtype, n_threads=8)
+    scale = orc.row_scale(data[keep], indices[keep], k_indptr, x, n_rows, vtype=vtype)
+    exact = orc.row_exact(data[keep], indices[keep], k_indptr, x, n_rows, vtype=vtype)
+    xt = to_torch(x, vtype, DEV)
+    p = to_torch(indptr, None, DEV)
+    sizes = []
+    for label in ("sorted", "unsorted"):
+        if label == "unsorted":  # one long row loses its order: same sums, other kernel
+            a, b = int(indptr[2000]), int(indptr[2000]) + 1
+            indices[[a, b]] = indices[[b, a]]
+            data[[a, b]] = data[[b, a]]
+        d, i = to_torch(data, vtype, DEV), to_torch(indices, None, DEV)
+        plan = _capi.Plan(p, n_rows, nnz, data=d, indices=i, n_cols=n_cols,
+                          slice_mode=_capi.SLICE_OFF)
+        sizes.append(plan.info().plan_bytes)
+        y = _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan)
+        torch.cuda.synchronize()
+        assert_rows_close(to_numpy(y), want, scale, vtype, f"{label} long rows", exact=exact,
+                          lengths=lengths, min_len_exempt=LONG_ROW_EXEMPT)
+        plan.close()
+    assert sizes[0] > sizes[1]  # only the sorted plan holds the slice pieces
+
+
 @pytest.mark.parametrize("W", [64, 128, 256, 512, 1024])
 def test_plan_bins_bit_exact(W):
     rng = np.random.default_rng(W)
