@@ -21,6 +21,7 @@
 
 #include "msx_device.h"
 #include "msx_internal.h"
+#include "msx_long_slice.h"
 
 namespace msx {
 namespace {
@@ -28,10 +29,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / kWave;
 constexpr uint32_t kMaxGrid = 1u << 20;
-// A piece starts anywhere, so with its 4-aligned start it spans at most
-// kLongPieceMax + 3 positions: 256 quads, four per lane.
-constexpr int kLongPieceMax = 1020;
-constexpr int kPieceQuads = 4;
 // x must be at least this large for the slicing to pay: below it, x fits
 // one XCD's L2 anyway.
 constexpr int64_t kLongSliceMinX = int64_t{4} << 20;
@@ -99,55 +96,8 @@ __global__ void __launch_bounds__(kThreads)
                      const int32_t *__restrict__ ls_slot,
                      const int32_t *__restrict__ ls_slice_begin,
                      typename V::Acc *__restrict__ partial) {
-  using S = typename V::Storage;
-  using A = typename V::Acc;
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int s = static_cast<int>(blockIdx.x % kSlices);  // this workgroup's XCD
-  const int64_t u1 = ls_slice_begin[s + 1];
-  const int64_t step = static_cast<int64_t>(gridDim.x / kSlices) * kWavesPerGroup;
-  const auto rx = make_rsrc(x, x_bytes);
-  for (int64_t u = ls_slice_begin[s] + static_cast<int64_t>(blockIdx.x / kSlices) * kWavesPerGroup + wave;
-       u < u1; u += step) {
-    const int64_t pb = ls_begin[u];
-    const int64_t pe = pb + ls_len[u];
-    const int64_t a0 = pb & ~int64_t{3};
-    // descriptors end at the piece: later quads read zero
-    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(pe - a0) * sizeof(I));
-    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(pe - a0) * sizeof(S));
-    Quad<I> iq[kPieceQuads];
-    Quad<S> dq[kPieceQuads];
-#pragma unroll
-    for (int j = 0; j < kPieceQuads; ++j) {
-      const uint32_t q = static_cast<uint32_t>(lane + j * kWave);
-      iq[j] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
-      dq[j] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
-    }
-    GatherRaw<S> raw[kPieceQuads][4];
-    bool ok[kPieceQuads][4];
-#pragma unroll
-    for (int j = 0; j < kPieceQuads; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t pos = a0 + 4 * (lane + j * kWave) + e;
-        const int64_t col = static_cast<int64_t>(iq[j].v[e]);
-        ok[j][e] = pos >= pb && pos < pe && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
-        raw[j][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(col), ok[j][e]);
-      }
-    __builtin_amdgcn_sched_barrier(0);
-    A acc = vzero<A>();
-#pragma unroll
-    for (int j = 0; j < kPieceQuads; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const A xv = gather_widen<V>(raw[j][e], static_cast<uint32_t>(iq[j].v[e]));
-        const A sum = vadd(acc, vmul_acc<V>(xv, dq[j].v[e]));
-        acc = ok[j][e] ? sum : acc;
-      }
-#pragma unroll
-    for (int d = kWave / 2; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
-    if (lane == 0) partial[ls_slot[u]] = acc;
-  }
+  long_pieces<V, I, AUX>(data, indices, x, x_bytes, n_cols, ls_begin, ls_len, ls_slot,
+                         ls_slice_begin, partial, blockIdx.x, gridDim.x);
 }
 
 // One wave per long row: its slots in a fixed-order tree.
@@ -268,6 +218,16 @@ msx_status build_typed(msx_csr_plan *p, const void *indices, const void *indptr,
   return MSX_OK;
 }
 
+template <class V>
+void launch_fixup(const msx_csr_plan *p, void *y, hipStream_t stream) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  const int64_t groups = (p->n_long + kWavesPerGroup - 1) / kWavesPerGroup;
+  hipLaunchKernelGGL((long_sliced_fixup<V>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
+                     stream, static_cast<S *>(y), p->long_rows, p->ls_row_slot,
+                     static_cast<const A *>(p->ls_partial), p->n_long);
+}
+
 template <class V, class I>
 void launch_typed(const msx_csr_plan *p, const void *data, const void *indices, const void *x,
                   void *y, uint32_t x_bytes, bool stream_nt, hipStream_t stream) {
@@ -281,10 +241,7 @@ void launch_typed(const msx_csr_plan *p, const void *data, const void *indices, 
                      static_cast<const I *>(indices), static_cast<const S *>(x), x_bytes, p->n_cols,
                      p->ls_begin, p->ls_len, p->ls_slot, p->ls_slice_begin,
                      static_cast<A *>(p->ls_partial));
-  const int64_t groups = (p->n_long + kWavesPerGroup - 1) / kWavesPerGroup;
-  hipLaunchKernelGGL((long_sliced_fixup<V>), dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0,
-                     stream, static_cast<S *>(y), p->long_rows, p->ls_row_slot,
-                     static_cast<const A *>(p->ls_partial), p->n_long);
+  launch_fixup<V>(p, y, stream);
 }
 
 template <class V>
@@ -312,6 +269,17 @@ msx_status launch_long_sliced(const msx_csr_plan *p, const void *data, const voi
   case MSX_F16: launch_v<F16>(p, data, indices, x, y, x_bytes, stream_nt, stream); break;
   case MSX_BF16: launch_v<BF16>(p, data, indices, x, y, x_bytes, stream_nt, stream); break;
   case MSX_C64: launch_v<C64>(p, data, indices, x, y, x_bytes, stream_nt, stream); break;
+  }
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+msx_status launch_long_sliced_fixup(const msx_csr_plan *p, void *y, hipStream_t stream) {
+  switch (p->vtype) {
+  case MSX_F32: launch_fixup<F32>(p, y, stream); break;
+  case MSX_F16: launch_fixup<F16>(p, y, stream); break;
+  case MSX_BF16: launch_fixup<BF16>(p, y, stream); break;
+  case MSX_C64: launch_fixup<C64>(p, y, stream); break;
   }
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;

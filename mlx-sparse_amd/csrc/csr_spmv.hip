@@ -34,6 +34,7 @@
 
 #include "msx_device.h"
 #include "msx_internal.h"
+#include "msx_long_slice.h"
 
 namespace msx {
 namespace {
@@ -67,13 +68,28 @@ __device__ inline void wave_lds_sync() {
 // indices, values) -> x gathers -> LDS -> y.
 constexpr int kBlockRows = 256;  // R; equals the plan's block_rows
 
-template <class V, class I, int W, int AUX>
+// FUSE: the XCD-sliced long-row pieces ride in the same launch.  The first
+// `long_groups` workgroups (a multiple of 8, so workgroup g still runs on
+// XCD g % 8) sum long-row pieces, the rest walk the short blocks; the two
+// halves gather from different places (one slice of x per XCD, all of x),
+// so they overlap instead of running back to back.
+template <class V, class I, int W, int AUX, bool FUSE>
 __global__ void __launch_bounds__(kThreads)
     spmv_blocks(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
                 typename V::Storage *__restrict__ y, const int32_t *__restrict__ bounds,
                 const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
-                int64_t n_cols, uint32_t x_bytes) {
+                int64_t n_cols, uint32_t x_bytes, uint32_t long_groups,
+                const int64_t *__restrict__ ls_begin, const int32_t *__restrict__ ls_len,
+                const int32_t *__restrict__ ls_slot, const int32_t *__restrict__ ls_slice_begin,
+                typename V::Acc *__restrict__ ls_partial) {
+  if constexpr (FUSE) {
+    if (blockIdx.x < long_groups) {
+      long_pieces<V, I, AUX>(data, indices, x, x_bytes, n_cols, ls_begin, ls_len, ls_slot,
+                             ls_slice_begin, ls_partial, blockIdx.x, long_groups);
+      return;
+    }
+  }
   using S = typename V::Storage;
   using A = typename V::Acc;
   // A block spans < 2W values; with the 4-aligned start, <= W/2 + 1 quads.
@@ -93,8 +109,10 @@ __global__ void __launch_bounds__(kThreads)
   A *prod = lds_prod[wave];
   int32_t *rptr = lds_ptr[wave];
 
-  const uint32_t first = xcd_remap(blockIdx.x, gridDim.x);
-  for (int64_t wg = first; wg * kWavesPerGroup < n_bounds; wg += gridDim.x) {
+  const uint32_t gid = FUSE ? blockIdx.x - long_groups : blockIdx.x;
+  const uint32_t ngroups = FUSE ? gridDim.x - long_groups : gridDim.x;
+  const uint32_t first = xcd_remap(gid, ngroups);
+  for (int64_t wg = first; wg * kWavesPerGroup < n_bounds; wg += ngroups) {
     const int64_t b = wg * kWavesPerGroup + wave;
     if (b >= n_bounds) break;
     const uint32_t e0 = static_cast<uint32_t>(bounds[b]);
@@ -425,19 +443,39 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   } else if (use_plan && plan->n_slices > 0) {
     MSX_HIP_TRY_ST(launch_spmv_sliced(plan, x, y, stream));
   } else if (use_plan) {
+    // Sliced long-row pieces ride in the same launch as the short blocks.
+    const bool fuse = plan->n_chunks > 0 && plan->ls_units > 0 && x_bytes != 0;
     if (plan->n_bounds > plan->n_long) {
       const int64_t groups = (plan->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
-      const dim3 grid(grid_for(groups)), block(kThreads);
+      const uint32_t long_groups =
+          fuse ? static_cast<uint32_t>(kSlices * std::max<int64_t>(1, std::min<int64_t>(
+                     (plan->ls_slice_max + kWavesPerGroup - 1) / kWavesPerGroup, kMaxGrid / 64)))
+               : 0u;
+      const dim3 grid(long_groups + std::min(grid_for(groups), kMaxGrid - long_groups)),
+          block(kThreads);
+      A *ls_partial = static_cast<A *>(plan->ls_partial);
 #define MSX_SPMV_BLOCKS(WV)                                                                   \
   do {                                                                                         \
-    if (stream_nt)                                                                             \
-      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheStream>), grid, block, 0, stream, data,  \
-                         indices, indptr, x, y, plan->bounds, plan->bounds_nnz, plan->n_bounds, \
-                         nnz, n_cols, x_bytes);                                                \
+    if (fuse && stream_nt)                                                                     \
+      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheStream, true>), grid, block, 0, stream,   \
+                         data, indices, indptr, x, y, plan->bounds, plan->bounds_nnz,          \
+                         plan->n_bounds, nnz, n_cols, x_bytes, long_groups, plan->ls_begin,    \
+                         plan->ls_len, plan->ls_slot, plan->ls_slice_begin, ls_partial);       \
+    else if (fuse)                                                                             \
+      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheDefault, true>), grid, block, 0, stream,  \
+                         data, indices, indptr, x, y, plan->bounds, plan->bounds_nnz,          \
+                         plan->n_bounds, nnz, n_cols, x_bytes, long_groups, plan->ls_begin,    \
+                         plan->ls_len, plan->ls_slot, plan->ls_slice_begin, ls_partial);       \
+    else if (stream_nt)                                                                        \
+      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheStream, false>), grid, block, 0, stream, \
+                         data, indices, indptr, x, y, plan->bounds, plan->bounds_nnz,          \
+                         plan->n_bounds, nnz, n_cols, x_bytes, 0u, nullptr, nullptr, nullptr,  \
+                         nullptr, nullptr);                                                    \
     else                                                                                       \
-      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheDefault>), grid, block, 0, stream, data, \
-                         indices, indptr, x, y, plan->bounds, plan->bounds_nnz, plan->n_bounds, \
-                         nnz, n_cols, x_bytes);                                                \
+      hipLaunchKernelGGL((spmv_blocks<V, I, WV, kCacheDefault, false>), grid, block, 0, stream, \
+                         data, indices, indptr, x, y, plan->bounds, plan->bounds_nnz,          \
+                         plan->n_bounds, nnz, n_cols, x_bytes, 0u, nullptr, nullptr, nullptr,  \
+                         nullptr, nullptr);                                                    \
   } while (0)
       switch (plan->block_nnz) {
       case 64: MSX_SPMV_BLOCKS(64); break;
@@ -448,6 +486,10 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
       }
 #undef MSX_SPMV_BLOCKS
       MSX_HIP_TRY(hipGetLastError());
+      if (fuse) {
+        MSX_HIP_TRY_ST(launch_long_sliced_fixup(plan, y, stream));
+        return MSX_OK;
+      }
     }
   }
   if (use_plan && plan->n_chunks > 0 && plan->ls_units > 0 && x_bytes != 0) {

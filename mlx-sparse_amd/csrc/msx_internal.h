@@ -190,6 +190,9 @@ msx_status build_long_slices(msx_csr_plan *p, const void *indices, const void *i
 msx_status launch_long_sliced(const msx_csr_plan *p, const void *data, const void *indices,
                               const void *x, void *y, uint32_t x_bytes, bool stream_nt,
                               hipStream_t stream);
+// Only the fixup of those long rows, after their pieces were summed by the
+// fused short-block kernel (csr_spmv.hip).
+msx_status launch_long_sliced_fixup(const msx_csr_plan *p, void *y, hipStream_t stream);
 // Column windows of a bound plan (csr_spmm.hip).  Synchronises `stream`.
 msx_status build_windows(msx_csr_plan *p, const void *indices, const void *indptr,
                          hipStream_t stream);
