@@ -80,27 +80,58 @@ __global__ void __launch_bounds__(kThreads)
     slice_probe(const I *__restrict__ indices, const int32_t *__restrict__ bounds,
                 const int64_t *__restrict__ bounds_nnz, int64_t n_bounds, int64_t nnz,
                 int64_t n_cols, unsigned long long *__restrict__ counter) {
+  // Each wave walks blocks with a stride of the grid and keeps its counts in
+  // registers; one atomic per counter and workgroup (an atomic per block
+  // serialises hundreds of thousands of them on two addresses).
+  __shared__ unsigned long long wg_count[2][kWavesPerGroup];
   const int lane = threadIdx.x % kWave;
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + threadIdx.x / kWave;
-  if (b >= n_bounds) return;
-  const BlockRange br = block_range<W>(bounds, bounds_nnz, b, nnz);
-  if (!br.valid || br.p1 <= br.p0) return;
-  if (lane == 0) atomicAdd(counter + 1, static_cast<unsigned long long>(br.p1 - br.p0));
-  int64_t lo = INT64_MAX, hi = -1;
-  for (int64_t p = br.p0 + lane; p < br.p1; p += kWave) {
-    const int64_t c = static_cast<int64_t>(indices[p]);
-    if (static_cast<uint64_t>(c) < static_cast<uint64_t>(n_cols)) {
-      lo = c < lo ? c : lo;
-      hi = c > hi ? c : hi;
+  const int wave = threadIdx.x / kWave;
+  unsigned long long scattered = 0, values = 0;
+  for (int64_t b = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + wave; b < n_bounds;
+       b += static_cast<int64_t>(gridDim.x) * kWavesPerGroup) {
+    const BlockRange br = block_range<W>(bounds, bounds_nnz, b, nnz);
+    if (!br.valid || br.p1 <= br.p0) continue;
+    values += static_cast<unsigned long long>(br.p1 - br.p0);
+    int64_t lo = INT64_MAX, hi = -1;
+    // a block holds < 2W values: four unconditional loads per lane and step
+    const auto rr = make_rsrc(indices + br.p0, static_cast<uint64_t>(br.p1 - br.p0) * sizeof(I));
+    for (int64_t q = 0; q < br.p1 - br.p0; q += 4 * kWave) {
+      I c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        c[u] = buffer_index<I>(rr, static_cast<uint32_t>(q + lane + u * kWave) * sizeof(I));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t v = static_cast<int64_t>(c[u]);
+        if (q + lane + u * kWave < br.p1 - br.p0 &&
+            static_cast<uint64_t>(v) < static_cast<uint64_t>(n_cols)) {
+          lo = v < lo ? v : lo;
+          hi = v > hi ? v : hi;
+        }
+      }
     }
+    for (int d = kWave / 2; d >= 1; d >>= 1) {
+      const int64_t ol = __shfl_xor(lo, d, kWave);
+      const int64_t oh = __shfl_xor(hi, d, kWave);
+      lo = ol < lo ? ol : lo;
+      hi = oh > hi ? oh : hi;
+    }
+    if (hi >= lo && hi - lo > n_cols / 4) ++scattered;
   }
-  for (int d = kWave / 2; d >= 1; d >>= 1) {
-    const int64_t ol = __shfl_xor(lo, d, kWave);
-    const int64_t oh = __shfl_xor(hi, d, kWave);
-    lo = ol < lo ? ol : lo;
-    hi = oh > hi ? oh : hi;
+  if (lane == 0) {
+    wg_count[0][wave] = scattered;
+    wg_count[1][wave] = values;
   }
-  if (lane == 0 && hi >= lo && hi - lo > n_cols / 4) atomicAdd(counter, 1ull);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long a = 0, v = 0;
+    for (int w = 0; w < kWavesPerGroup; ++w) {
+      a += wg_count[0][w];
+      v += wg_count[1][w];
+    }
+    if (a > 0) atomicAdd(counter, a);
+    if (v > 0) atomicAdd(counter + 1, v);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -360,7 +391,7 @@ int bits_for(int64_t v) {  // smallest b with v <= 2^b
 template <class I, int W>
 msx_status probe_typed(const msx_csr_plan *p, const void *indices, hipStream_t stream,
                        bool *scattered, int64_t *short_values) {
-  const int64_t groups = (p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup;
+  const int64_t groups = std::min<int64_t>((p->n_bounds + kWavesPerGroup - 1) / kWavesPerGroup, 2048);
   unsigned long long *counter = nullptr;
   MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&counter), 2 * sizeof(*counter), stream));
   MSX_HIP_TRY(hipMemsetAsync(counter, 0, 2 * sizeof(*counter), stream));
