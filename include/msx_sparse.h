@@ -163,8 +163,13 @@ msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
  *     stored order, so short rows equal the reference CPU kernel bit for bit.
  *     Needs nnz < 2^31 and at most 2048 panels; MSX_SLICE_PANELS on a matrix
  *     outside those limits fails with MSX_EINVAL.
- * Long rows keep the row-block path in every mode.  `opts` may be NULL
- * (defaults).  Synchronises `stream`.
+ * Long rows keep the row-block path in every mode.  When x is at least
+ * 4 MB and every long row holds sorted columns, the plan also records each
+ * long row's 8 column-slice stretches (pieces of at most 1020 values): the
+ * pieces of slice s are summed on XCD s, in the same launch as the short
+ * blocks, and a fixed-order tree adds a row's pieces.  Every bound plan
+ * also records the column window of each 32-row tile (see msx_csr_spmm).
+ * `opts` may be NULL (defaults).  Synchronises `stream`.
  *
  * A bound plan reads the matrix from its own copy: msx_csr_spmv must be
  * given the same data/indices/indptr pointers it was built from (other
