@@ -84,9 +84,15 @@ __device__ void write_partials(double (&v)[kSlots], double *part) {
 __device__ void read_totals(const double *part, int nparts, double (&t)[kSlots]) {
   __shared__ double sh[kSlots][kCgThreads / kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  // all kSlots loads first (clamped index, no branch), then the sums
+  const bool mine = static_cast<int>(threadIdx.x) < nparts;
+  const int idx = mine ? static_cast<int>(threadIdx.x) : 0;
+  double v[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) v[k] = part[k * kCgMaxBlocks + idx];
+#pragma unroll
   for (int k = 0; k < kSlots; ++k) {
-    const double v = static_cast<int>(threadIdx.x) < nparts ? part[k * kCgMaxBlocks + threadIdx.x] : 0.0;
-    const double w = wave_sum(v);
+    const double w = wave_sum(mine ? v[k] : 0.0);
     if (lane == 0) sh[k][wave] = w;
   }
   __syncthreads();
@@ -105,14 +111,25 @@ __device__ inline void stop(CgState *st, int32_t status, int32_t completed) {
 }
 
 // Grid-stride over [0, n) with kUnroll coalesced elements per round.
+// A thread whose kUnroll elements all lie below n runs them without a
+// per-element test, so the compiler issues all of their loads before the
+// first use (a test per element made it wait for each load in turn); the
+// last, partial group tests each element.
 #define MSX_CG_LOOP(...)                                                                    \
   {                                                                                          \
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;                     \
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n; \
          base += kUnroll * stride) {                                                         \
-      _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                  \
-        const int64_t i = base + u * stride;                                                 \
-        if (i < n) { __VA_ARGS__ }                                                                  \
+      if (base + (kUnroll - 1) * stride < n) {                                               \
+        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
+          const int64_t i = base + u * stride;                                               \
+          __VA_ARGS__                                                                        \
+        }                                                                                    \
+      } else {                                                                               \
+        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
+          const int64_t i = base + u * stride;                                               \
+          if (i < n) { __VA_ARGS__ }                                                         \
+        }                                                                                    \
       }                                                                                      \
     }                                                                                        \
   }
@@ -218,18 +235,37 @@ __global__ void __launch_bounds__(kCgThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
-    const double xc = static_cast<double>(x[i]) + alpha * static_cast<double>(p[i]);
-    const double rc = static_cast<double>(r[i]) - alpha * static_cast<double>(ap[i]);
-    const float xf = static_cast<float>(xc), rf = static_cast<float>(rc);
-    if (!fin(xc) || !fin(rc) || !fin(xf) || !fin(rf)) {
-      v[3] += 1.0;
-    } else {
-      x[i] = xf;
-      r[i] = rf;
-      v[0] += static_cast<double>(rf) * static_cast<double>(rf);
+  // All loads of a thread's kUnroll elements first (an index past n reads
+  // element `base` instead), then the arithmetic and the stores: written as
+  // one loop body, the compiler waited for each element's loads in turn.
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+       base += kUnroll * stride) {
+    float xo[kUnroll], ro[kUnroll], pv[kUnroll], av[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = base + u * stride < n ? base + u * stride : base;
+      xo[u] = x[j];
+      ro[u] = r[j];
+      pv[u] = p[j];
+      av[u] = ap[j];
     }
-  })
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * stride;
+      if (i >= n) break;
+      const double xc = static_cast<double>(xo[u]) + alpha * static_cast<double>(pv[u]);
+      const double rc = static_cast<double>(ro[u]) - alpha * static_cast<double>(av[u]);
+      const float xf = static_cast<float>(xc), rf = static_cast<float>(rc);
+      if (!fin(xc) || !fin(rc) || !fin(xf) || !fin(rf)) {
+        v[3] += 1.0;
+      } else {
+        x[i] = xf;
+        r[i] = rf;
+        v[0] += static_cast<double>(rf) * static_cast<double>(rf);
+      }
+    }
+  }
   write_partials(v, part);
 }
 
@@ -261,12 +297,27 @@ __global__ void __launch_bounds__(kCgThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
-    const double pc = static_cast<double>(r[i]) + beta * static_cast<double>(p[i]);
-    const float pf = static_cast<float>(pc);
-    if (!fin(pc) || !fin(pf)) v[3] += 1.0;
-    else p[i] = pf;
-  })
+  // loads first, then arithmetic and stores, as in cg_update
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+       base += kUnroll * stride) {
+    float rv[kUnroll], pv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = base + u * stride < n ? base + u * stride : base;
+      rv[u] = r[j];
+      pv[u] = p[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * stride;
+      if (i >= n) break;
+      const double pc = static_cast<double>(rv[u]) + beta * static_cast<double>(pv[u]);
+      const float pf = static_cast<float>(pc);
+      if (!fin(pc) || !fin(pf)) v[3] += 1.0;
+      else p[i] = pf;
+    }
+  }
   write_partials(v, part);
   if (lead) {
     st->completed = it;
