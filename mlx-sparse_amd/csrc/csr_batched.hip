@@ -113,11 +113,82 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// The same transposes with the number of 16-byte vectors per column, Q, a
+// constant: every load of a thread is issued before its first store (with
+// a runtime Q the compiler waited for each vector's loads in turn).  A lane
+// past `batch` loads element batch - 1 and stores zero.
+template <class T, int Q>
+__global__ void __launch_bounds__(kThreads)
+    gather_columns_q(const T *__restrict__ X, int64_t batch, int64_t n, int64_t ldx,
+                     T *__restrict__ Xt) {
+  constexpr int E = 16 / sizeof(T);
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < n;
+       c += static_cast<int64_t>(gridDim.x) * kThreads) {
+    Vec16<T> v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int64_t b = q * E + e;
+        const T t = X[(b < batch ? b : batch - 1) * ldx + c];
+        v[q].e[e] = b < batch ? t : T{};
+      }
+    uint4 *out = reinterpret_cast<uint4 *>(Xt + c * (Q * E));
+#pragma unroll
+    for (int q = 0; q < Q; ++q) out[q] = v[q].u;
+  }
+}
+
+template <class T, int Q>
+__global__ void __launch_bounds__(kThreads)
+    scatter_rows_q(const T *__restrict__ Yt, int64_t batch, int64_t n, int64_t ldy,
+                   T *__restrict__ Y) {
+  constexpr int E = 16 / sizeof(T);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n;
+       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint4 *in = reinterpret_cast<const uint4 *>(Yt + r * (Q * E));
+    Vec16<T> v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) v[q].u = in[q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int64_t b = q * E + e;
+        if (b < batch) Y[b * ldy + r] = v[q].e[e];
+      }
+  }
+}
+
+template <class T, int Q>
+void narrow_q(bool to_columns, const void *in, int64_t batch, int64_t n, int64_t ld, void *out,
+              uint32_t grid, hipStream_t stream) {
+  if (to_columns)
+    hipLaunchKernelGGL((gather_columns_q<T, Q>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const T *>(in), batch, n, ld, static_cast<T *>(out));
+  else
+    hipLaunchKernelGGL((scatter_rows_q<T, Q>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const T *>(in), batch, n, ld, static_cast<T *>(out));
+}
+
 template <class T>
 msx_status narrow_t(bool to_columns, const void *in, int64_t batch, int64_t kpad, int64_t n,
                     int64_t ld, void *out, hipStream_t stream) {
-  if (n == 0) return MSX_OK;
+  if (n == 0 || batch <= 0) return MSX_OK;
   const uint32_t grid = static_cast<uint32_t>(std::min((n + kThreads - 1) / kThreads, kMaxGrid));
+  constexpr int64_t E = 16 / sizeof(T);
+  bool done = true;
+  switch (kpad / E) {
+  case 1: narrow_q<T, 1>(to_columns, in, batch, n, ld, out, grid, stream); break;
+  case 2: narrow_q<T, 2>(to_columns, in, batch, n, ld, out, grid, stream); break;
+  case 4: narrow_q<T, 4>(to_columns, in, batch, n, ld, out, grid, stream); break;
+  case 8: narrow_q<T, 8>(to_columns, in, batch, n, ld, out, grid, stream); break;
+  default: done = false; break;  // other widths: the kernels with a runtime width
+  }
+  if (done) {
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
   if (to_columns)
     hipLaunchKernelGGL((gather_columns<T>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const T *>(in), batch, kpad, n, ld, static_cast<T *>(out));

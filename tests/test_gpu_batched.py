@@ -57,7 +57,7 @@ def test_batched_spmv_parity_and_strides(vtype, index_dtype):
     indices, indptr, nnz = _matrix(rng, n_rows, n_cols, index_dtype)
     data = _values(rng, nnz, vtype)
     d, i, p = (to_torch(a, vtype if a is data else None, DEV) for a in (data, indices, indptr))
-    for batch in (1, 2, 3, 8, 17):
+    for batch in (1, 2, 3, 8, 16, 17, 32):  # 16-byte vectors per column: 1, 2, 4, 8 and others
         X = _values(rng, (batch, n_cols + 5), vtype)  # row stride n_cols + 5
         want = _want_vectors(data, indices, indptr, np.ascontiguousarray(X[:, :n_cols]), n_rows,
                              vtype)
