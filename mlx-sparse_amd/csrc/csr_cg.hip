@@ -433,17 +433,35 @@ __global__ void __launch_bounds__(kCgThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
-    const float xi = x[i] + alpha * p[i];
-    const float ri = r[i] - alpha * ap[i];
-    const float zi = inv_diag[i] * ri;
-    x[i] = xi;
-    r[i] = ri;
-    z[i] = zi;
-    v[0] += static_cast<double>(ri) * static_cast<double>(ri);
-    v[1] += static_cast<double>(ri) * static_cast<double>(zi);
-    if (!(fin(xi) && fin(ri) && fin(zi))) v[3] += 1.0;
-  })
+  // loads first, then arithmetic and stores, as in cg_update
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+       base += kUnroll * stride) {
+    float xo[kUnroll], po[kUnroll], ro[kUnroll], ao[kUnroll], dv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = base + u * stride < n ? base + u * stride : base;
+      xo[u] = x[j];
+      po[u] = p[j];
+      ro[u] = r[j];
+      ao[u] = ap[j];
+      dv[u] = inv_diag[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * stride;
+      if (i >= n) break;
+      const float xi = xo[u] + alpha * po[u];
+      const float ri = ro[u] - alpha * ao[u];
+      const float zi = dv[u] * ri;
+      x[i] = xi;
+      r[i] = ri;
+      z[i] = zi;
+      v[0] += static_cast<double>(ri) * static_cast<double>(ri);
+      v[1] += static_cast<double>(ri) * static_cast<double>(zi);
+      if (!(fin(xi) && fin(ri) && fin(zi))) v[3] += 1.0;
+    }
+  }
   write_partials(v, part);
 }
 
@@ -472,7 +490,23 @@ __global__ void __launch_bounds__(kCgThreads)
     if (lead) stop(st, verdict, it);
     return;
   }
-  MSX_CG_LOOP({ p[i] = z[i] + beta * p[i]; })
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+       base += kUnroll * stride) {  // loads first, as in cg_update
+    float zv[kUnroll], pv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = base + u * stride < n ? base + u * stride : base;
+      zv[u] = z[j];
+      pv[u] = p[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * stride;
+      if (i >= n) break;
+      p[i] = zv[u] + beta * pv[u];
+    }
+  }
   if (lead) st->rr_next = rho_new;
 }
 
