@@ -387,10 +387,34 @@ __global__ void __launch_bounds__(kThreads)
     if (row < n_rows) {
       const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
       const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
-      for (int64_t q = s + j; q < e; q += G) {
-        const int64_t col = static_cast<int64_t>(indices[q]);
-        if (static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols))
-          acc = vadd(acc, vmul<V>(data[q], x[col]));
+      // Four values per lane and step in the row's stored order; every load
+      // is unconditional (positions past the row read the step's first
+      // value, invalid columns read x[0]) and masked afterwards, so a step
+      // costs two dependent round trips instead of two per value.
+      if (n_cols > 0) {
+        for (int64_t q0 = s + j; q0 < e; q0 += 4 * G) {
+          I c[4];
+          typename V::Storage d[4], xv[4];
+          bool ok[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int64_t q = q0 + u * G;
+            const int64_t qc = q < e ? q : q0;
+            c[u] = indices[qc];
+            d[u] = data[qc];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int64_t col = static_cast<int64_t>(c[u]);
+            ok[u] = q0 + u * G < e && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+            xv[u] = x[ok[u] ? col : 0];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const A sum = vadd(acc, vmul<V>(d[u], xv[u]));
+            acc = ok[u] ? sum : acc;
+          }
+        }
       }
     }
     for (int d = G >> 1; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
