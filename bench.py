@@ -33,14 +33,16 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
   the cached transpose, the transpose build, the SpMV value gradient and one
   autograd step (forward + ``A^T g``);
-- ``configs`` (with ``--configs``): SpMV on every configuration of the
-  benchmark definition (2D Laplacian, power law with int64 indices, 3D
-  Poisson, the banded matrix in float32 / bfloat16 / float16 / complex64)
-  and SpMM at k = 8 / 64 / 256 (Poisson) and k = 64 (float16 banded),
-  graph-replay and cold timed against each one's compulsory bytes;
-- ``cpu_baseline``: the C restatement of the reference CPU kernel
-  (oracle/, ``-O3`` without ``-march=native``), threads split like the
-  reference, timed on this host's cores on the same matrix.
+- ``configs`` (skipped with ``--no-configs``): SpMV on every configuration
+  of the benchmark definition (the headline, 2D Laplacian, power law with
+  int64 indices, 3D Poisson, the banded matrix in float32 / bfloat16 /
+  float16 / complex64) and SpMM at k = 8 / 64 / 256 (Poisson) and k = 64
+  (float16 and bfloat16 banded), graph-replay (warm) and cold timed against
+  each one's compulsory bytes, with the plan kind and its footprint;
+- ``cpu_baseline``: the product's CPU path (``ms.use_cpu()``, the C++
+  restatement of the reference CPU kernel in csrc/csr_cpu.cpp, ``-O3``
+  without ``-march=native``) on the headline matrix, at the reference-resolved
+  worker count and at one thread, on this host's cores, with the CPU model.
 """
 
 from __future__ import annotations
@@ -128,39 +130,76 @@ def _cold_time(fn, iters: int, scratch: torch.Tensor) -> float:
     return statistics.median(times)
 
 
-def cpu_baseline(m, x, seconds: float = 12.0) -> dict:
-    """Time the oracle's reference-CPU restatement on a bounded sample."""
-    from oracle import oracle as orc
-
-    threads = orc.cpu_worker_count()
-    for _ in range(2):
-        orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=threads)
-    samples = []
-    t_end = time.perf_counter() + seconds
-    while len(samples) < 10 or (time.perf_counter() < t_end and len(samples) < 30):
-        t0 = time.perf_counter()
-        orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=threads)
-        samples.append(time.perf_counter() - t0)
-    med = statistics.median(samples)
-    from mlx_sparse import synthetic
-
-    nbytes = synthetic.compulsory_bytes(m.nnz, m.shape[0], m.shape[1], 4, 4)
-    model = ""
+def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def _median_wall(fn, seconds: float, lo: int = 10, hi: int = 30) -> tuple[float, int]:
+    """Median wall seconds per call after 3 warm-up calls, over at least
+    ``lo`` calls (and up to ``hi`` while ``seconds`` last)."""
+    for _ in range(3):
+        fn()
+    samples = []
+    t_end = time.perf_counter() + seconds
+    while len(samples) < lo or (time.perf_counter() < t_end and len(samples) < hi):
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+    return statistics.median(samples), len(samples)
+
+
+def cpu_baseline(m, x, seconds: float = 10.0) -> dict:
+    """The product's CPU path, ``ms.use_cpu()`` then ``A @ x`` on the same
+    matrix: the C++ restatement of the reference CPU kernel
+    (csrc/csr_cpu.cpp: stored-order row sums, the O(n) row-work prepass,
+    nnz-balanced ranges, std::threads spawned per call; reference
+    csr_matvec.cpp:116-168, cpu_parallel.h:50-97), at the reference-resolved
+    worker count and at one thread.  The oracle's C restatement is timed
+    beside it as a cross-check (3 calls)."""
+    import mlx_sparse as ms
+    from mlx_sparse import runtime, synthetic
+    from oracle import oracle as orc
+
+    nbytes = synthetic.compulsory_bytes(m.nnz, m.shape[0], m.shape[1], 4, 4)
+    prev = ms.default_torch_device()
+    ms.use_cpu()
+    try:
+        A = ms.csr_array((torch.from_numpy(m.data), torch.from_numpy(m.indices),
+                          torch.from_numpy(m.indptr)), shape=m.shape)
+        xc = torch.from_numpy(x)
+        assert A.data.device.type == "cpu"
+        threads = runtime.resolve_n_threads()[0]
+        med, n = _median_wall(lambda: A @ xc, seconds)
+        with runtime.context(n_threads=1):
+            med1, n1 = _median_wall(lambda: A @ xc, seconds, lo=10, hi=10)
+    finally:
+        if prev.type == "cuda":
+            ms.use_gpu(prev.index or 0)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        orc.csr_matvec(m.data, m.indices, m.indptr, x, m.shape[0], n_threads=threads)
+    oracle_ms = (time.perf_counter() - t0) / 3 * 1e3
+    model = _cpu_model()
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(samples)} full SpMV calls on the same matrix, median "
-                   f"{med * 1e3:.1f} ms; gcc -O3 -ffp-contract=off, no -march=native; "
-                   f"{threads} threads of {len(os.sched_getaffinity(0))} in affinity; {model}"),
+        "ms": round(med * 1e3, 2),
+        "threads_1": {"value": round(nbytes / med1 / 1e9, 3), "unit": "GB/s",
+                      "ms": round(med1 * 1e3, 2)},
+        "cpu_model": model,
+        "affinity_cores": len(os.sched_getaffinity(0)),
+        "oracle_check_ms": round(oracle_ms, 2),
+        "sample": (f"ms.use_cpu() A @ x on the headline matrix, median of {n} calls at "
+                   f"{threads} threads and {n1} at 1 thread; g++ -O3 -ffp-contract=off, "
+                   f"no -march=native"),
     }
 
 
@@ -327,7 +366,9 @@ def configs_leg(ext, dev, scratch) -> list:
         nflops = synthetic.flops(m.nnz, k or 1, complex_values)
         kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
         row = {"case": name, "nnz": m.nnz, "op": "spmv" if k is None else f"spmm k={k}",
-               "plan": kind, "window_rows": info["window_rows"], "long_rows": info["n_long_rows"],
+               "plan": kind, "plan_bytes": info["plan_bytes"], "block_nnz": info["block_nnz"],
+               "window_rows": info["window_rows"], "long_rows": info["n_long_rows"],
+               "compulsory_bytes": nbytes, "flops": nflops,
                "kernel_us": round(t * 1e3, 2), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
                "frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "gflops": round(nflops / (t * 1e-3) / 1e9, 1),
@@ -358,9 +399,10 @@ def configs_leg(ext, dev, scratch) -> list:
     run("cfg5 banded hb32 f32/i32", m, d32, x32)
     for dt, nm in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
         run(f"cfg5 banded hb32 {nm}/i32", m, d32.to(dt), x32.to(dt))
-    Xh = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=64)).to(dev).to(torch.float16)
-    run("cfg5 banded hb32 f16/i32", m, d32.to(torch.float16), Xh, k=64)
-    del Xh
+    X64 = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=64)).to(dev)
+    for dt, nm in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+        run(f"cfg5 banded hb32 {nm}/i32", m, d32.to(dt), X64.to(dt), k=64)
+    del X64
     cv = torch.from_numpy(synthetic.complex_values(m, seed=3))
     xc = torch.complex(vec(m.shape[1], 4), vec(m.shape[1], 5))
     run("cfg5 banded hb32 c64/i32", m, cv, xc, complex_values=True)
@@ -378,8 +420,8 @@ def main() -> int:
     ap.add_argument("--no-cg", action="store_true", help="skip the conjugate gradient leg")
     ap.add_argument("--mtx", default=None,
                     help="also time SpMV on a Matrix Market file (e.g. a SuiteSparse matrix)")
-    ap.add_argument("--configs", action="store_true",
-                    help="also time SpMV/SpMM on every benchmark configuration")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the SpMV/SpMM rows of the other benchmark configurations")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
@@ -500,6 +542,7 @@ def main() -> int:
                                 "slices": "spmv_sliced<F32> + slice_merge<F32>"}.get(
                                     plan_kind, f"spmv_blocks<F32,int,{info['block_nnz']}>"),
                      "kernel_us": round(kern_ms * 1e3, 2),
+                     "plan_bytes": info["plan_bytes"],
                      "timing": "HIP-graph replay of 20 calls x 10, HIP events"},
         "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),
                  "frac": round(cold_gbs / HBM_PEAK_GBS, 4)},
@@ -578,9 +621,18 @@ def main() -> int:
         result["mtx"] = mtx_leg(ext, args.mtx, dev)
         torch.cuda.empty_cache()
 
-    # ---- every benchmark configuration, when asked ----------------------------------
-    if args.configs:
-        result["configs"] = configs_leg(ext, dev, scratch)
+    # ---- every benchmark configuration -------------------------------------------------
+    if not args.no_configs:
+        head = {"case": "cfg2 random16 n=2^22 f32/i32 (headline)", "nnz": m.nnz, "op": "spmv",
+                "plan": plan_kind, "plan_bytes": info["plan_bytes"],
+                "block_nnz": info["block_nnz"], "window_rows": info["window_rows"],
+                "long_rows": info["n_long_rows"], "compulsory_bytes": nbytes, "flops": nflops,
+                "kernel_us": round(kern_ms * 1e3, 2), "gbs": round(achieved, 1),
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "gflops": round(nflops / (kern_ms * 1e-3) / 1e9, 1),
+                "cold_us": round(cold_ms * 1e3, 2),
+                "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4)}
+        result["configs"] = [head] + configs_leg(ext, dev, scratch)
         torch.cuda.empty_cache()
 
     # ---- conjugate gradients on the Poisson matrix --------------------------------

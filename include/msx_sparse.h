@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 3
+#define MSX_ABI_VERSION 4
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -173,8 +173,9 @@ msx_status msx_csr_plan_create(msx_itype it, int64_t n_rows, int64_t nnz,
  *
  * A bound plan reads the matrix from its own copy: msx_csr_spmv must be
  * given the same data/indices/indptr pointers it was built from (other
- * pointers are rejected with MSX_EINVAL), and the values must not change
- * while the plan is in use.  Replaces, like msx_csr_plan_create, the
+ * pointers are rejected with MSX_EINVAL).  When the values change, call
+ * msx_csr_plan_refresh before the next product; when indices or indptr
+ * change, build a new plan.  Replaces, like msx_csr_plan_create, the
  * reference's per-launch kernel choice (reference:
  * src/sparse/csr_matvec/csr_matvec.cpp:291-296).
  */
@@ -184,6 +185,24 @@ msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it,
                                      const void *indices, const void *indptr,
                                      const msx_plan_options *opts,
                                      void *stream, msx_csr_plan **out);
+
+/*
+ * The values of a bound plan's matrix changed (in place, or copied to a new
+ * buffer `data`), its indices and indptr did not: rewrite the plan's own
+ * copies of the values (the XCD-sliced or panel copy) from `data` on
+ * `stream`, asynchronously, and bind the plan to `data` from now on.  A
+ * gather through the layout the plan already holds: O(nnz), no allocation
+ * and no re-sort (the headline matrix: one pass over its values instead of
+ * the 20 ms build).  Row-block plans hold no values: a no-op.  Calls that
+ * share the plan must be ordered after this one (same stream).
+ *
+ * No reference counterpart: the reference's arrays are immutable
+ * (reference: mlx_sparse/_csr.py:33), so its kernels always read the
+ * current values; torch tensors are not, and this keeps a cached plan right
+ * after an optimizer updates the values in place.
+ */
+msx_status msx_csr_plan_refresh(msx_csr_plan *plan, const void *data,
+                                void *stream);
 
 /* Release a plan (NULL is accepted).  Synchronises the plan's device. */
 msx_status msx_csr_plan_destroy(msx_csr_plan *plan);
@@ -231,7 +250,8 @@ msx_status msx_csr_plan_export_panels(const msx_csr_plan *plan,
  * y[i] = sum_{p = indptr[i]}^{indptr[i+1]-1} data[p] * x[indices[p]]
  * for i in [0, n_rows).  All pointers are device pointers.  `plan` may be
  * NULL (a plan-free kernel sized from nnz / n_rows is used); a non-NULL plan
- * must have been built from this `indptr`.
+ * must have been built from this `indptr` buffer (the same pointer; another
+ * buffer is rejected with MSX_EINVAL, whatever it holds).
  *
  * Replaces CSRMatVec::eval_gpu (reference:
  * src/sparse/csr_matvec/csr_matvec.cpp:278-317) and the Metal kernels
@@ -318,6 +338,34 @@ msx_status msx_csr_transpose_cpu(msx_vtype vt, msx_itype it, int64_t n_rows,
                                  int64_t n_cols, int64_t nnz, const void *data,
                                  const void *indices, const void *indptr,
                                  void *t_data, void *t_indices, void *t_indptr);
+
+/*
+ * The structure of A^T (t_indices, t_indptr exactly as msx_csr_transpose
+ * writes them) and, per entry i < t_indptr[n_cols], the stored position of
+ * A it holds: t_pos[i] (int32); entries past t_indptr[n_cols] (values with
+ * a column outside [0, n_cols)) get -1.  Asynchronous on `stream` (scratch
+ * from its stream-ordered allocator); nnz < 2^31 - 1.
+ *
+ * With msx_csr_transpose_values this refreshes a cached transpose after A's
+ * values changed in place; no reference counterpart (the reference's arrays
+ * are immutable, reference: mlx_sparse/_csr.py:33; the structure is the one
+ * of CSRTranspose, src/sparse/csr_transpose/csr_transpose.cpp).
+ */
+msx_status msx_csr_transpose_positions(msx_itype it, int64_t n_rows,
+                                       int64_t n_cols, int64_t nnz,
+                                       const void *indices, const void *indptr,
+                                       int32_t *t_pos, void *t_indices,
+                                       void *t_indptr, void *stream);
+
+/*
+ * t_data[i] = data[t_pos[i]] for i < nnz whose t_pos[i] lies in [0, nnz)
+ * (complex conjugated when `conjugate` is nonzero and vt is complex64, which
+ * gives the values of A^H); other entries are left alone.  Device pointers,
+ * asynchronous on `stream`.
+ */
+msx_status msx_csr_transpose_values(msx_vtype vt, int64_t nnz,
+                                    const void *data, const int32_t *t_pos,
+                                    int conjugate, void *t_data, void *stream);
 
 /*
  * y = A^T x (x: n_rows, y: n_cols) and Y = A^T X (X: n_rows x k, row stride

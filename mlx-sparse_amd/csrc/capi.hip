@@ -66,12 +66,16 @@ msx_status check_common(const char *op, msx_vtype vt, msx_itype it, int64_t n_ro
 
 msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, msx_itype it,
                       int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
-                      const void *indices) {
+                      const void *indices, const void *indptr) {
   if (plan == nullptr) return MSX_OK;
   if (plan->itype != it || plan->n_rows != n_rows || plan->nnz != nnz)
     return fail(MSX_EINVAL, std::string(op) + ": plan was built for a different matrix.");
-  if (plan->bound_data != nullptr && (plan->bound_data != data || plan->bound_indices != indices ||
-                                      plan->vtype != vt || plan->n_cols != n_cols))
+  // The row blocks come from one indptr buffer: another buffer (even of the
+  // same length and nnz) may hold other rows.
+  if (plan->indptr != indptr)
+    return fail(MSX_EINVAL, std::string(op) + ": plan was built from another indptr buffer.");
+  if (plan->bound && (plan->bound_data != data || plan->bound_indices != indices ||
+                      plan->vtype != vt || plan->n_cols != n_cols))
     return fail(MSX_EINVAL, std::string(op) + ": plan is bound to other data/indices buffers.");
   int dev = -1;
   MSX_HIP_TRY(hipGetDevice(&dev));
@@ -113,7 +117,7 @@ extern "C" msx_status msx_csr_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, i
   if (st != MSX_OK) return st;
   if (n_rows > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec y is NULL.");
   if (n_cols > 0 && nnz > 0 && x == nullptr) return fail(MSX_EINVAL, "csr_matvec x is NULL.");
-  st = check_plan("csr_matvec", plan, vt, it, n_rows, n_cols, nnz, data, indices);
+  st = check_plan("csr_matvec", plan, vt, it, n_rows, n_cols, nnz, data, indices, indptr);
   if (st != MSX_OK) return st;
   if (n_rows == 0) return MSX_OK;
   return launch_spmv(vt, it, n_rows, n_cols, nnz, data, indices, indptr, x, y, plan,
@@ -133,7 +137,7 @@ extern "C" msx_status msx_csr_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, i
   if (n_rows > 0 && k > 0 && Y == nullptr) return fail(MSX_EINVAL, "csr_matmul Y is NULL.");
   if (n_cols > 0 && k > 0 && nnz > 0 && X == nullptr)
     return fail(MSX_EINVAL, "csr_matmul X is NULL.");
-  st = check_plan("csr_matmul", plan, vt, it, n_rows, n_cols, nnz, data, indices);
+  st = check_plan("csr_matmul", plan, vt, it, n_rows, n_cols, nnz, data, indices, indptr);
   if (st != MSX_OK) return st;
   if (n_rows == 0 || k == 0) return MSX_OK;
   return launch_spmm(vt, it, n_rows, n_cols, nnz, data, indices, indptr, k, X, ldx, Y, ldy, plan,

@@ -687,7 +687,7 @@ extern "C" msx_status msx_csr_cg(msx_itype it, int64_t n, int64_t nnz, const flo
   clear_error();
   msx_status st = check("csr_cg", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
   if (st != MSX_OK) return st;
-  st = check_plan("csr_cg", plan, MSX_F32, it, n, n, nnz, data, indices);
+  st = check_plan("csr_cg", plan, MSX_F32, it, n, n, nnz, data, indices, indptr);
   if (st != MSX_OK) return st;
   const Solve s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
                 blocks_for(n)};
@@ -705,7 +705,7 @@ extern "C" msx_status msx_csr_pcg_jacobi(msx_itype it, int64_t n, int64_t nnz, c
       check("csr_pcg_jacobi", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
   if (st != MSX_OK) return st;
   if (inv_diag == nullptr) return fail(MSX_EINVAL, "csr_pcg_jacobi inverse diagonal is NULL.");
-  st = check_plan("csr_pcg_jacobi", plan, MSX_F32, it, n, n, nnz, data, indices);
+  st = check_plan("csr_pcg_jacobi", plan, MSX_F32, it, n, n, nnz, data, indices, indptr);
   if (st != MSX_OK) return st;
   const Solve s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
                 blocks_for(n)};

@@ -197,6 +197,42 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Refresh of the copy's values after the matrix's values changed (same
+// indices and indptr): one workgroup per tile.  The tile's rows fill a map
+// from LDS word to (row - first row of the tile); an entry with word d then
+// came from position b0 + d - map[d], the inverse of dest = (p - b0) +
+// (row - r0).  Every panel's segment of the tile is regathered; padding
+// entries (word 0xFFFF, outside every tile) keep their zero.
+template <class S, class I>
+__global__ void __launch_bounds__(kThreads)
+    panel_refresh(const S *__restrict__ data, const I *__restrict__ indptr, int64_t nnz,
+                  const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
+                  const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles, int64_t TW,
+                  const uint16_t *__restrict__ dest, S *__restrict__ out) {
+  __shared__ uint16_t row_of[kTileBytes / 4];  // TW <= 16384 words
+  const int64_t t = blockIdx.x;
+  const int64_t r0 = tile_begin[t], r1 = tile_end[t];
+  const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
+  for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+    for (int64_t p = s; p < e; ++p) {
+      const int64_t w = (p - b0) + (r - r0);
+      if (w >= 0 && w < TW) row_of[w] = static_cast<uint16_t>(r - r0);
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  for (int64_t q = wave; q < n_panels; q += kThreads / kWave) {
+    const int64_t a = seg[q * n_tiles + t], b = seg[q * n_tiles + t + 1];
+    for (int64_t e = a + lane; e < b; e += kWave) {
+      const int64_t d = dest[e];
+      if (d >= TW) continue;
+      out[e] = data[clamp64(b0 + d - row_of[d], 0, nnz - 1)];
+    }
+  }
+}
+
 int bits_for(uint64_t v) {
   int b = 0;
   while (b < 64 && (v >> b) != 0) ++b;
@@ -406,6 +442,24 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   return prepare_spmv_panels(p);
 }
 
+template <class V, class I>
+msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  using S = typename V::Storage;
+  if (p->n_tiles == 0 || p->pn_values == 0) return MSX_OK;
+  hipLaunchKernelGGL((panel_refresh<S, I>), dim3(static_cast<uint32_t>(p->n_tiles)), dim3(kThreads), 0,
+                     stream, static_cast<const S *>(data), static_cast<const I *>(p->indptr), p->nnz,
+                     p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels, p->n_tiles,
+                     p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+template <class V>
+msx_status refresh_v(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  return p->itype == MSX_I32 ? refresh_typed<V, int32_t>(p, data, stream)
+                             : refresh_typed<V, int64_t>(p, data, stream);
+}
+
 template <class V>
 msx_status build_v(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                    hipStream_t stream) {
@@ -445,6 +499,16 @@ msx_status build_panels(msx_csr_plan *p, const void *data, const void *indices, 
   case MSX_C64: return build_v<C64>(p, data, indices, indptr, stream);
   }
   return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+}
+
+msx_status refresh_panels(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  switch (p->vtype) {
+  case MSX_F32: return refresh_v<F32>(p, data, stream);
+  case MSX_F16: return refresh_v<F16>(p, data, stream);
+  case MSX_BF16: return refresh_v<BF16>(p, data, stream);
+  case MSX_C64: return refresh_v<C64>(p, data, stream);
+  }
+  return fail(MSX_ETYPE, "msx_csr_plan_refresh unsupported value dtype.");
 }
 
 }  // namespace msx

@@ -298,6 +298,7 @@ msx_status create_plan(msx_itype it, int64_t n_rows, int64_t nnz, const void *in
   p->block_rows = kBlockRows;
   p->chunk_nnz = kChunkNnz;
   p->slice_mode = MSX_SLICE_OFF;
+  p->indptr = indptr;
   hipError_t e = hipGetDevice(&p->device);
   if (e != hipSuccess) {
     delete p;
@@ -360,6 +361,7 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   p->vtype = vt;
   p->n_cols = n_cols;
   p->slice_mode = opts->slice_mode;
+  p->bound = true;
   p->bound_data = data;
   p->bound_indices = indices;
   auto s = static_cast<hipStream_t>(stream);
@@ -400,6 +402,23 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   }
   *out = p;
   return MSX_OK;
+}
+
+extern "C" msx_status msx_csr_plan_refresh(msx_csr_plan *plan, const void *data, void *stream) {
+  clear_error();
+  if (plan == nullptr) return fail(MSX_EINVAL, "msx_csr_plan_refresh: plan is NULL.");
+  if (!plan->bound) return MSX_OK;  // row blocks hold no values
+  if (plan->nnz > 0 && data == nullptr)
+    return fail(MSX_EINVAL, "msx_csr_plan_refresh: data is NULL.");
+  int dev = -1;
+  MSX_HIP_TRY(hipGetDevice(&dev));
+  if (dev != plan->device)
+    return fail(MSX_EINVAL, "msx_csr_plan_refresh: plan lives on another device.");
+  auto s = static_cast<hipStream_t>(stream);
+  msx_status st = refresh_slices(plan, data, s);
+  if (st == MSX_OK && plan->n_panels > 0) st = refresh_panels(plan, data, s);
+  if (st == MSX_OK) plan->bound_data = data;
+  return st;
 }
 
 extern "C" msx_status msx_csr_plan_destroy(msx_csr_plan *plan) {

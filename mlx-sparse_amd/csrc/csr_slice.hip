@@ -140,14 +140,16 @@ __global__ void __launch_bounds__(kThreads)
 // stably reordered there by slice, seg[k][s] .. seg[k][s+1] relative to P0.
 // Dropped: values of long rows (summed by spmv_long on the caller's arrays)
 // and values whose column is outside [0, n_cols) (they add nothing).  One
-// wave per super-block: a counting pass, then a stable scatter.
+// wave per super-block: a counting pass, then a stable scatter.  With
+// `values_only` (a refresh after the values changed: same indices and
+// indptr, so the same order) only s_data is written.
 template <class V, class I>
 __global__ void __launch_bounds__(kThreads)
     slice_build(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                 const I *__restrict__ indptr, int64_t n_rows, int64_t nnz, int64_t n_cols,
                 int64_t long_len, int64_t slice_width, int col_bits,
                 typename V::Storage *__restrict__ s_data, uint32_t *__restrict__ s_col,
-                uint32_t *__restrict__ s_seg) {
+                uint32_t *__restrict__ s_seg, bool values_only) {
   __shared__ int64_t lds_rp[kWavesPerGroup][kRows + 1];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -194,7 +196,7 @@ __global__ void __launch_bounds__(kThreads)
   start[0] = 0;
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) start[s + 1] = start[s] + count[s];
-  if (lane <= kSlices) {
+  if (lane <= kSlices && !values_only) {
     int64_t v = 0;
 #pragma unroll
     for (int s = 0; s <= kSlices; ++s) v = lane == s ? start[s] : v;
@@ -218,8 +220,9 @@ __global__ void __launch_bounds__(kThreads)
     }
     if (dest >= 0) {
       s_data[P0 + dest] = data[P0 + e];
-      s_col[P0 + dest] = (static_cast<uint32_t>(row) << col_bits) |
-                         static_cast<uint32_t>(col - static_cast<int64_t>(sl) * slice_width);
+      if (!values_only)
+        s_col[P0 + dest] = (static_cast<uint32_t>(row) << col_bits) |
+                           static_cast<uint32_t>(col - static_cast<int64_t>(sl) * slice_width);
     }
   }
 }
@@ -452,12 +455,32 @@ msx_status build_typed(msx_csr_plan *p, const void *data, const void *indices, c
   hipLaunchKernelGGL((slice_build<V, I>), dim3(static_cast<uint32_t>(bgroups)), dim3(kThreads), 0,
                      stream, static_cast<const S *>(data), static_cast<const I *>(indices),
                      static_cast<const I *>(indptr), p->n_rows, p->nnz, p->n_cols, p->block_nnz,
-                     width, col_bits, static_cast<S *>(p->s_data), p->s_col, p->s_seg);
+                     width, col_bits, static_cast<S *>(p->s_data), p->s_col, p->s_seg, false);
   MSX_HIP_TRY(hipGetLastError());
   MSX_HIP_TRY(hipStreamSynchronize(stream));
   p->n_slices = kSlices;
   p->s_indptr = indptr;
   return MSX_OK;
+}
+
+template <class V, class I>
+msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  using S = typename V::Storage;
+  const int64_t n_super = (p->n_rows + kRows - 1) / kRows;
+  const int64_t bgroups = (n_super + kWavesPerGroup - 1) / kWavesPerGroup;
+  hipLaunchKernelGGL((slice_build<V, I>), dim3(static_cast<uint32_t>(bgroups)), dim3(kThreads), 0,
+                     stream, static_cast<const S *>(data), static_cast<const I *>(p->bound_indices),
+                     static_cast<const I *>(p->s_indptr), p->n_rows, p->nnz, p->n_cols,
+                     p->block_nnz, p->slice_width, p->col_bits, static_cast<S *>(p->s_data),
+                     p->s_col, p->s_seg, true);
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
+template <class V>
+msx_status refresh_v(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  return p->itype == MSX_I32 ? refresh_typed<V, int32_t>(p, data, stream)
+                             : refresh_typed<V, int64_t>(p, data, stream);
 }
 
 template <class V>
@@ -503,6 +526,17 @@ msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, 
   case MSX_C64: return build_v<C64>(p, data, indices, indptr, stream);
   }
   return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+}
+
+msx_status refresh_slices(msx_csr_plan *p, const void *data, hipStream_t stream) {
+  if (p->n_slices == 0) return MSX_OK;
+  switch (p->vtype) {
+  case MSX_F32: return refresh_v<F32>(p, data, stream);
+  case MSX_F16: return refresh_v<F16>(p, data, stream);
+  case MSX_BF16: return refresh_v<BF16>(p, data, stream);
+  case MSX_C64: return refresh_v<C64>(p, data, stream);
+  }
+  return fail(MSX_ETYPE, "msx_csr_plan_refresh unsupported value dtype.");
 }
 
 msx_status probe_scattered(const msx_csr_plan *p, const void *indices, hipStream_t stream,

@@ -56,6 +56,29 @@ __device__ inline void atomic_acc(c64 *p, c64 v) {
   unsafeAtomicAdd(f + 1, v.im);
 }
 
+// out[i] = src[pos[i]] (conjugated on request) for pos[i] in [0, n_src);
+// entries with another position are left alone.
+template <class S>
+__global__ void __launch_bounds__(kThreads)
+    gather_positions(const S *__restrict__ src, int64_t n_src, const int32_t *__restrict__ pos,
+                     int64_t count, bool conjugate, S *__restrict__ out) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t p = pos[i];
+    if (p < 0 || p >= n_src) continue;
+    S v = src[p];
+    if constexpr (sizeof(S) == 8) {
+      if (conjugate) {
+        uint64_t bits = 0;
+        __builtin_memcpy(&bits, &v, 8);
+        bits ^= uint64_t{1} << 63;  // sign of the imaginary part (the high float)
+        __builtin_memcpy(&v, &bits, 8);
+      }
+    }
+    out[i] = v;
+  }
+}
+
 template <class T>
 __global__ void __launch_bounds__(kThreads) fill(T *__restrict__ p, int64_t n, T v) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
@@ -148,8 +171,9 @@ __global__ void __launch_bounds__(kThreads)
 // Packed path (values of at most 4 bytes): the sort carries (row << 32) |
 // value bits, so the transposed arrays come out of one coalesced pass.
 // key[p] = column of p (n_cols when out of range), val[p] = packed pair;
-// G lanes per row.
-template <class S, class I>
+// G lanes per row.  With kPos the "value" of p is p itself (int32): the
+// transpose then lists, per entry, the position of A it came from.
+template <class S, class I, bool kPos = false>
 __global__ void __launch_bounds__(kThreads)
     packed_keys(const S *__restrict__ data, const I *__restrict__ indices,
                 const I *__restrict__ indptr, int64_t n_rows, int64_t nnz, int64_t n_cols, int G,
@@ -165,7 +189,10 @@ __global__ void __launch_bounds__(kThreads)
       const int64_t c = static_cast<int64_t>(indices[p]);
       key[p] = (c >= 0 && c < n_cols) ? static_cast<uint32_t>(c) : static_cast<uint32_t>(n_cols);
       uint32_t bits = 0;
-      __builtin_memcpy(&bits, &data[p], sizeof(S));
+      if constexpr (kPos)
+        bits = static_cast<uint32_t>(p);
+      else
+        __builtin_memcpy(&bits, &data[p], sizeof(S));
       val[p] = (static_cast<uint64_t>(r) << 32) | bits;
     }
   }
@@ -179,8 +206,9 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Sorted pairs -> t_data, t_indices, and t_indptr[c] = first sorted index
-// with key >= c, written by the index where the key crosses c.
-template <class S, class I>
+// with key >= c, written by the index where the key crosses c.  With kPos
+// the entries past t_indptr[n_cols] (dropped values) get position -1.
+template <class S, class I, bool kPos = false>
 __global__ void __launch_bounds__(kThreads)
     packed_unpack(const uint32_t *__restrict__ key, const uint64_t *__restrict__ val, int64_t nnz,
                   int64_t n_cols, S *__restrict__ t_data, I *__restrict__ t_indices,
@@ -197,13 +225,15 @@ __global__ void __launch_bounds__(kThreads)
       __builtin_memcpy(&d, &bits, sizeof(S));
       t_data[i] = d;
       t_indices[i] = static_cast<I>(v >> 32);
+    } else if constexpr (kPos) {
+      if (i < nnz) t_data[i] = S(-1);
     }
   }
 }
 
 int lanes_for(int64_t n_rows, int64_t nnz);
 
-template <class S, class I>
+template <class S, class I, bool kPos = false>
 msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
                             const void *indices, const void *indptr, void *t_data,
                             void *t_indices, void *t_indptr, int end_bit, hipStream_t stream) {
@@ -225,7 +255,7 @@ msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const v
   const int G = lanes_for(n_rows, nnz);
   hipLaunchKernelGGL(drop_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
                      static_cast<uint32_t>(n_cols), key);
-  hipLaunchKernelGGL((packed_keys<S, I>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL((packed_keys<S, I, kPos>), dim3(grid_for(n_rows * G)), dim3(kThreads), 0, stream,
                      static_cast<const S *>(data), static_cast<const I *>(indices),
                      static_cast<const I *>(indptr), n_rows, nnz, n_cols, G, key, val);
   hipError_t e = hipGetLastError();
@@ -233,7 +263,7 @@ msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const v
     e = hipcub::DeviceRadixSort::SortPairs(sort_tmp, sort_bytes, key, key_out, val, val_out,
                                            static_cast<int>(nnz), 0, end_bit, stream);
   if (e == hipSuccess) {
-    hipLaunchKernelGGL((packed_unpack<S, I>), dim3(grid_for(nnz + 1)), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((packed_unpack<S, I, kPos>), dim3(grid_for(nnz + 1)), dim3(kThreads), 0, stream,
                        key_out, val_out, nnz, n_cols, static_cast<S *>(t_data),
                        static_cast<I *>(t_indices), static_cast<I *>(t_indptr));
     e = hipGetLastError();
@@ -635,6 +665,70 @@ extern "C" msx_status msx_csr_transpose(msx_vtype vt, msx_itype it, int64_t n_ro
     return fail(MSX_EINVAL, "csr_transpose output buffers must be non-NULL.");
   return dispatch<TransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, t_data,
                                t_indices, t_indptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_transpose_positions(msx_itype it, int64_t n_rows, int64_t n_cols,
+                                                  int64_t nnz, const void *indices,
+                                                  const void *indptr, int32_t *t_pos,
+                                                  void *t_indices, void *t_indptr, void *stream) {
+  clear_error();
+  msx_status st =
+      check_csr("csr_transpose_positions", MSX_F32, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (t_indptr == nullptr || (nnz > 0 && (t_pos == nullptr || t_indices == nullptr)))
+    return fail(MSX_EINVAL, "csr_transpose_positions output buffers must be non-NULL.");
+  auto s = static_cast<hipStream_t>(stream);
+  if (nnz == 0) {
+    if (it == MSX_I64)
+      hipLaunchKernelGGL((fill<int64_t>), dim3(grid_for(n_cols + 1)), dim3(kThreads), 0, s,
+                         static_cast<int64_t *>(t_indptr), n_cols + 1, int64_t{0});
+    else
+      hipLaunchKernelGGL((fill<int32_t>), dim3(grid_for(n_cols + 1)), dim3(kThreads), 0, s,
+                         static_cast<int32_t *>(t_indptr), n_cols + 1, int32_t{0});
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
+  const int end_bit = bits_for(static_cast<uint64_t>(n_cols));
+  return it == MSX_I64
+             ? transpose_packed<int32_t, int64_t, true>(n_rows, n_cols, nnz, nullptr, indices,
+                                                         indptr, t_pos, t_indices, t_indptr,
+                                                         end_bit, s)
+             : transpose_packed<int32_t, int32_t, true>(n_rows, n_cols, nnz, nullptr, indices,
+                                                         indptr, t_pos, t_indices, t_indptr,
+                                                         end_bit, s);
+}
+
+extern "C" msx_status msx_csr_transpose_values(msx_vtype vt, int64_t nnz, const void *data,
+                                               const int32_t *t_pos, int conjugate, void *t_data,
+                                               void *stream) {
+  clear_error();
+  if (!valid_vtype(vt)) return fail(MSX_ETYPE, "csr_transpose_values unsupported value dtype.");
+  if (nnz < 0 || nnz >= kIntMax)
+    return fail(MSX_EINVAL, "csr_transpose_values supports 0 to 2^31 - 2 stored values.");
+  if (nnz > 0 && (data == nullptr || t_pos == nullptr || t_data == nullptr))
+    return fail(MSX_EINVAL, "csr_transpose_values buffers must be non-NULL.");
+  if (nnz == 0) return MSX_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  const bool conj = conjugate != 0 && vt == MSX_C64;
+  switch (value_bytes(vt)) {
+  case 2:
+    hipLaunchKernelGGL((gather_positions<uint16_t>), dim3(grid_for(nnz)), dim3(kThreads), 0, s,
+                       static_cast<const uint16_t *>(data), nnz, t_pos, nnz, false,
+                       static_cast<uint16_t *>(t_data));
+    break;
+  case 4:
+    hipLaunchKernelGGL((gather_positions<uint32_t>), dim3(grid_for(nnz)), dim3(kThreads), 0, s,
+                       static_cast<const uint32_t *>(data), nnz, t_pos, nnz, false,
+                       static_cast<uint32_t *>(t_data));
+    break;
+  default:
+    hipLaunchKernelGGL((gather_positions<uint64_t>), dim3(grid_for(nnz)), dim3(kThreads), 0, s,
+                       static_cast<const uint64_t *>(data), nnz, t_pos, nnz, conj,
+                       static_cast<uint64_t *>(t_data));
+    break;
+  }
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
 }
 
 extern "C" msx_status msx_csr_spmv_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,

@@ -73,7 +73,9 @@ struct msx_csr_plan {
   int n_slices;
   int64_t slice_width;
   int col_bits;
-  const void *bound_data;     // the buffers a bound plan was built from
+  const void *indptr;         // the row pointers the plan was built from
+  bool bound;                 // built by msx_csr_plan_create_bound
+  const void *bound_data;     // the buffers a bound plan was built from (data: as last refreshed)
   const void *bound_indices;
   void *s_data;               // values reordered by slice inside each short block
   uint32_t *s_col;            // (row_in_block << col_bits) | column_in_slice
@@ -136,11 +138,11 @@ struct msx_csr_plan {
 namespace msx {
 
 // A plan passed with a matrix must have been built for it (same index type,
-// rows and values; a bound plan also the same buffers, value type and
-// columns) on the current device (capi.hip).
+// rows, values and indptr buffer; a bound plan also the same data and
+// indices buffers, value type and columns) on the current device (capi.hip).
 msx_status check_plan(const char *op, const msx_csr_plan *plan, msx_vtype vt, msx_itype it,
                       int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
-                      const void *indices);
+                      const void *indices, const void *indptr);
 
 // Launchers (csr_spmv.hip / csr_spmm.hip).  Arguments are already checked.
 msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
@@ -151,6 +153,10 @@ msx_status launch_spmv(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_col
 msx_status build_slices(msx_csr_plan *p, const void *data, const void *indices, const void *indptr,
                         hipStream_t stream);
 msx_status launch_spmv_sliced(const msx_csr_plan *p, const void *x, void *y, hipStream_t stream);
+// Rewrite the values of a plan's sliced / panel copy from `data` (the
+// matrix's values changed; its indices and indptr did not).  Asynchronous.
+msx_status refresh_slices(msx_csr_plan *p, const void *data, hipStream_t stream);
+msx_status refresh_panels(msx_csr_plan *p, const void *data, hipStream_t stream);
 // True when most short blocks have valid columns spread over more than a
 // quarter of x (the AUTO rule's test for a reordered copy); also the number
 // of values in short blocks.  Synchronises `stream`.

@@ -35,26 +35,34 @@ def _conj(t: torch.Tensor) -> torch.Tensor:
 
 
 def _adjoint_csr(a, data: torch.Tensor):
-    """Cached CSR of A^H on data's device (None when the route is atomic)."""
+    """CSR of A^H on data's device (None when the route is atomic): the
+    array's cached (conjugate) transpose, which follows in-place updates of
+    its values (``CSRArray._transpose_on``)."""
     from mlx_sparse import runtime
 
     device = data.device
     if device.type != "cuda":
         return None
     mode = runtime.get(runtime.RuntimeOption.GPU_ADJOINT)
-    key = ("adjoint", str(device))
-    hit = a._cache.get(key)
-    if hit is not None or mode == "atomic":
-        return hit
+    if mode == "atomic":
+        return None
     if mode == "auto":
         seen = ("adjoint_calls", str(device))
         a._cache[seen] = a._cache.get(seen, 0) + 1
         if a._cache[seen] < 2:
             return None
     # real values: A^H is A^T, shared with the array's own cached transpose
-    hit = a.conj()._transpose_on(device) if a.data.is_complex() else a._transpose_on(device)
-    a._cache[key] = hit
-    return hit
+    return a._transpose_on(device, conjugate=a.data.is_complex())
+
+
+def _own_plan(a, data: torch.Tensor):
+    """``a``'s plan when ``data`` is the very buffer the plan is bound to
+    (``a``'s values, contiguous on their device), else None: values
+    elsewhere run plan-free."""
+    bufs = a.buffers(data.device)
+    if data.data_ptr() != bufs[0].data_ptr() or not data.is_contiguous():
+        return None
+    return a.plan(data.device)
 
 
 def rmatvec(a, data: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
@@ -95,7 +103,7 @@ class CSRMatVec(torch.autograd.Function):
     @staticmethod
     def forward(data, x, a, planned=True):
         _, indices, indptr = a.buffers(data.device)
-        plan = a.plan(data.device) if planned else None
+        plan = _own_plan(a, data) if planned else None
         return _native.csr_matvec(data, indices, indptr, x, a.shape, plan=plan)
 
     @staticmethod
@@ -145,7 +153,8 @@ class CSRMatMul(torch.autograd.Function):
     @staticmethod
     def forward(data, X, a, planned=True):
         _, indices, indptr = a.buffers(data.device)
-        return _native.csr_matmul(data, indices, indptr, X, a.shape)
+        plan = _own_plan(a, data) if planned else None
+        return _native.csr_matmul(data, indices, indptr, X, a.shape, plan=plan)
 
     @staticmethod
     def setup_context(ctx, inputs, output):

@@ -1,10 +1,23 @@
 """CSR container (reference: mlx_sparse/_csr.py:33-129 ``CSRArray``,
 :502-552 ``__matmul__``, :627-730 ``csr_array``).
 
-``CSRArray`` is an immutable dataclass over three torch tensors.  Because it
-is immutable it can cache, per device, copies of its buffers and the GPU
-row-block plan built from ``indptr`` (built on first use, released with the
-array).
+``CSRArray`` is a frozen dataclass over three torch tensors.  It caches, per
+device, copies of its buffers, the GPU plan bound to them and its transpose
+(built on first use, released with the array).  The reference's arrays are
+immutable; torch tensors are not, so every cache entry records what it was
+built from - each tensor's storage address and version counter, which every
+in-place operation bumps - and is brought up to date on its next use:
+
+- new values (``A.data`` updated in place, e.g. by an optimizer step): device
+  copies are copied again, the plan's reordered copy of the values is
+  rewritten through the layout it holds (``CSRPlan.refresh``, one pass over
+  the values), and a cached transpose gets its values regathered through
+  the stored position of every entry (computed once), as a new array that
+  takes over the old one's plan;
+- new ``indices`` or ``indptr``: plans and transposes are built again.
+
+Writes that torch does not count (through ``.data``, DLPack or raw
+pointers) are not seen.
 """
 
 from __future__ import annotations
@@ -21,6 +34,16 @@ from mlx_sparse._validation import (
     validate_csr_metadata,
     validate_csr_values,
 )
+
+
+def _stamp(t: torch.Tensor) -> tuple[int, int]:
+    """Storage address and version counter of a tensor: what a cache entry
+    built from it must still match.  Inference tensors keep no version
+    counter; they count as unchanged while their storage is."""
+    try:
+        return (t.data_ptr(), t._version)
+    except RuntimeError:
+        return (t.data_ptr(), -1)
 
 
 @dataclass(frozen=True, slots=True)
@@ -79,21 +102,32 @@ class CSRArray:
         )
 
     # -- device copies and plans -----------------------------------------
+    def _stamps(self) -> tuple:
+        return (_stamp(self.data), _stamp(self.indices), _stamp(self.indptr))
+
     def buffers(self, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """``(data, indices, indptr)`` contiguous on ``device`` (cached)."""
+        """``(data, indices, indptr)`` contiguous on ``device`` (cached; a
+        tensor already contiguous on ``device`` is used as it is, a copy is
+        made again when its source changed)."""
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
         key = ("buffers", str(device))
+        now = self._stamps()
         hit = self._cache.get(key)
-        if hit is None:
-            hit = tuple(t.to(device).contiguous() for t in (self.data, self.indices, self.indptr))
-            self._cache[key] = hit
-        return hit
+        if hit is not None and hit[0] == now:
+            return hit[1]
+        old_stamps, old = hit if hit is not None else ((None,) * 3, (None,) * 3)
+        bufs = tuple(
+            o if o is not None and was == cur else t.to(device).contiguous()
+            for t, o, was, cur in zip((self.data, self.indices, self.indptr), old, old_stamps, now))
+        self._cache[key] = (now, bufs)
+        return bufs
 
     def plan(self, device=None):
-        """The GPU row-block plan for ``device`` (None on the CPU, or when the
-        ``gpu_plan`` runtime option is off).  Built once, then cached."""
+        """The GPU plan for ``device``, bound to :meth:`buffers` (None on the
+        CPU, or when the ``gpu_plan`` runtime option is off).  Built once;
+        refreshed when the values changed, rebuilt when the structure did."""
         from mlx_sparse import runtime
 
         device = torch.device(device) if device is not None else self.device
@@ -101,16 +135,35 @@ class CSRArray:
             return None
         data, indices, indptr = self.buffers(device)
         key = ("plan", str(indptr.device))
+        now = self._stamps()
         hit = self._cache.get(key)
-        if hit is None:
-            from mlx_sparse import _native
+        if hit is not None:
+            built, plan = hit
+            if built[1:] == now[1:]:
+                if built[0] != now[0]:
+                    plan.refresh(data)
+                    self._cache[key] = (now, plan)
+                return plan
+        from mlx_sparse import _native
 
-            # bound to this immutable matrix: may hold a column-sliced copy
-            hit = _native.csr_plan(indptr, self.shape[0], self.nnz, data=data, indices=indices,
-                                   n_cols=self.shape[1],
-                                   slice_mode=int(runtime.get(runtime.RuntimeOption.GPU_SLICE)))
-            self._cache[key] = hit
-        return hit
+        # bound to these buffers: may hold a reordered copy of the values
+        plan = _native.csr_plan(indptr, self.shape[0], self.nnz, data=data, indices=indices,
+                                n_cols=self.shape[1],
+                                slice_mode=int(runtime.get(runtime.RuntimeOption.GPU_SLICE)))
+        self._cache[key] = (now, plan)
+        return plan
+
+    def _with_values(self, data: torch.Tensor) -> "CSRArray":
+        """The same structure with other values, taking over this array's
+        GPU plans (each is rebound to ``data`` on its next use, as after an
+        in-place update); this array builds new ones if it is used again."""
+        out = CSRArray(data=data, indices=self.indices, indptr=self.indptr, shape=self.shape,
+                       sorted_indices=self.sorted_indices,
+                       has_canonical_format=self.has_canonical_format)
+        for key in [k for k in self._cache if k[0] == "plan"]:
+            built, plan = self._cache.pop(key)
+            out._cache[key] = (((None, None),) + tuple(built[1:]), plan)
+        return out
 
     # -- operators ---------------------------------------------------------
     def __matmul__(self, rhs):
@@ -131,28 +184,45 @@ class CSRArray:
         raise ValueError(f"CSR matmul expects rank-1 or higher RHS, got {tuple(rhs.shape)}.")
 
     # -- transpose and conjugate -------------------------------------------
-    def _transpose_on(self, device) -> "CSRArray":
-        """CSR of the transpose, computed on ``device`` (cached: the array is
-        immutable)."""
+    def _transpose_on(self, device, conjugate: bool = False) -> "CSRArray":
+        """CSR of the transpose (of the conjugate transpose with
+        ``conjugate``), computed on ``device``.  Cached while this array is
+        unchanged; after new values, the cached transpose's values are
+        regathered on the GPU through the stored position of each of its
+        entries (computed on the first such update), as a new array."""
+        from mlx_sparse import _native
+
         device = torch.device(device)
         data, indices, indptr = self.buffers(device)
-        key = ("T", str(data.device))
+        key = ("H" if conjugate else "T", str(data.device))
+        now = self._stamps()
         hit = self._cache.get(key)
-        if hit is None:
-            from mlx_sparse import _native
-
-            t_data, t_indices, t_indptr = _native.csr_transpose(data.detach(), indices, indptr,
-                                                                self.shape)
-            hit = CSRArray(
-                data=t_data,
-                indices=t_indices,
-                indptr=t_indptr,
-                shape=(self.shape[1], self.shape[0]),
-                sorted_indices=True,
-                has_canonical_format=self.has_canonical_format,
-            )
-            self._cache[key] = hit
-        return hit
+        if hit is not None:
+            built, T, pos = hit
+            if built == now:
+                return T
+            if built[1:] == now[1:] and data.device.type == "cuda":
+                if pos is None:
+                    pos = _native.csr_transpose_positions(indices, indptr, self.shape)[0]
+                t_data = torch.empty_like(T.data)
+                _native.csr_transpose_values(data.detach(), pos, conjugate, t_data)
+                T = T._with_values(t_data)
+                self._cache[key] = (now, T, pos)
+                return T
+        src = data.detach()
+        if conjugate:
+            src = src.conj().resolve_conj()
+        t_data, t_indices, t_indptr = _native.csr_transpose(src, indices, indptr, self.shape)
+        T = CSRArray(
+            data=t_data,
+            indices=t_indices,
+            indptr=t_indptr,
+            shape=(self.shape[1], self.shape[0]),
+            sorted_indices=True,
+            has_canonical_format=self.has_canonical_format,
+        )
+        self._cache[key] = (now, T, None)
+        return T
 
     def transpose(self) -> "CSRArray":
         """Transpose, returning a ``CSRArray`` of shape ``(n_cols, n_rows)``
@@ -189,8 +259,11 @@ class CSRArray:
 
     @property
     def H(self) -> "CSRArray":
-        """Hermitian (conjugate) transpose, ``conj().T``."""
-        return self.conj().transpose()
+        """Hermitian (conjugate) transpose, ``conj().T``: for real values the
+        transpose itself; both are cached like :meth:`transpose`."""
+        from mlx_sparse._device import default_torch_device
+
+        return self._transpose_on(default_torch_device(), conjugate=self.data.is_complex())
 
     def todense(self) -> torch.Tensor:
         """Dense copy (duplicates summed), on the buffers' device."""

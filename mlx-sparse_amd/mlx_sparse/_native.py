@@ -39,6 +39,17 @@ def csr_transpose(data, indices, indptr, shape: Shape2D):
     return tuple(extension().csr_transpose(data, indices, indptr, shape[0], shape[1]))
 
 
+def csr_transpose_positions(indices, indptr, shape: Shape2D):
+    """(t_pos, t_indices, t_indptr): the structure of A^T and, per entry, the
+    position of A it holds (int32; -1 for dropped values).  GPU only."""
+    return tuple(extension().csr_transpose_positions(indices, indptr, shape[0], shape[1]))
+
+
+def csr_transpose_values(data, positions, conjugate: bool, out) -> None:
+    """out[i] = data[positions[i]] (conjugated on request), in place.  GPU only."""
+    extension().csr_transpose_values(data, positions, conjugate, out)
+
+
 def csr_matvec_transpose(data, indices, indptr, x, shape: Shape2D) -> torch.Tensor:
     """A^T x, without conjugation (reference: mlx_sparse/_native.py:260-270)."""
     return extension().csr_matvec_transpose(data, indices, indptr, x, shape[0], shape[1])

@@ -159,6 +159,27 @@ std::shared_ptr<Plan> make_plan(py::handle indptr_obj, int64_t n_rows, int64_t n
   return plan;
 }
 
+// The matrix's values changed (indices and indptr did not): rewrite the
+// bound plan's copies from `data` and keep `data` alive in its place.
+void plan_refresh(Plan &plan, py::handle data_obj) {
+  if (plan.bound.is_none()) return;  // row blocks hold no values
+  py::tuple bound = plan.bound.cast<py::tuple>();
+  const ArrayView vd = view_of(data_obj), vi = view_of(bound[1]);
+  msx::require_rank(vd, 1, "csr_plan_refresh data");
+  msx::require_same_value_dtype(vd, view_of(bound[0]), "csr_plan_refresh data", "plan data");
+  msx::require_size(vd, plan.nnz, "csr_plan_refresh data");
+  msx::require_same_device({&vd, &vi}, "csr_plan_refresh");
+  msx::require_contiguous(vd, "csr_plan_refresh data");
+  void *stream = stream_for(vd.device);
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_plan_refresh(plan.p, vd.ptr, stream);
+  }
+  msx::check_status(st, "csr_plan_refresh");
+  plan.bound = py::make_tuple(py::reinterpret_borrow<py::object>(data_obj), bound[1], bound[2]);
+}
+
 const msx_csr_plan *plan_ptr(const py::object &plan) {
   if (plan.is_none()) return nullptr;
   return plan.cast<std::shared_ptr<Plan>>()->p;
@@ -283,6 +304,60 @@ py::tuple csr_transpose(py::handle data_o, py::handle indices_o, py::handle indp
     msx::csr_transpose(vd, vi, vp, vod, voi, vop, n_rows, n_cols, ctx);
   }
   return py::make_tuple(od, oi, op);
+}
+
+// (t_pos, t_indices, t_indptr): the transpose's structure and, per entry,
+// the position of A it holds (GPU operands).
+py::tuple csr_transpose_positions(py::handle indices_o, py::handle indptr_o, int64_t n_rows,
+                                  int64_t n_cols) {
+  py::object indices = contiguous(indices_o), indptr = contiguous(indptr_o);
+  const ArrayView vi = view_of(indices), vp = view_of(indptr);
+  if (vi.ndim != 1) msx::require_rank(vi, 1, "csr_transpose_positions indices");
+  msx::require_same_index_dtype(vi, vp, "csr_transpose_positions indices",
+                                "csr_transpose_positions indptr");
+  msx::require_size(vp, n_rows + 1, "csr_transpose_positions indptr");
+  msx::require_same_device({&vi, &vp}, "csr_transpose_positions");
+  if (vi.device < 0) throw std::invalid_argument("csr_transpose_positions needs GPU tensors.");
+  py::dict kw;
+  kw["dtype"] = torch().attr("int32");
+  kw["device"] = indices.attr("device");
+  py::object pos = torch().attr("empty")(py::make_tuple(vi.shape[0]), **kw);
+  py::object oi = empty_like_out(vi, indices, py::make_tuple(vi.shape[0]));
+  py::object op = empty_like_out(vp, indptr, py::make_tuple(std::max<int64_t>(n_cols, 0) + 1));
+  const ArrayView vpos = view_of(pos), voi = view_of(oi), vop = view_of(op);
+  void *stream = stream_for(vi.device);
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_transpose_positions(msx::to_itype(vi.dtype), n_rows, n_cols, vi.shape[0], vi.ptr,
+                                     vp.ptr, static_cast<int32_t *>(vpos.ptr), voi.ptr, vop.ptr,
+                                     stream);
+  }
+  msx::check_status(st, "csr_transpose_positions");
+  return py::make_tuple(pos, oi, op);
+}
+
+// out[i] = data[t_pos[i]] (conjugated on request), in place (GPU operands).
+void csr_transpose_values(py::handle data_o, py::handle pos_o, bool conjugate, py::handle out_o) {
+  py::object data = contiguous(data_o), pos = contiguous(pos_o);
+  const ArrayView vd = view_of(data), vpos = view_of(pos), vo = view_of(out_o);
+  msx::require_rank(vd, 1, "csr_transpose_values data");
+  msx::require_same_value_dtype(vd, vo, "csr_transpose_values data", "csr_transpose_values out");
+  if (vpos.dtype != DType::Int32) throw std::invalid_argument("csr_transpose_values positions must be int32.");
+  msx::require_size(vpos, vd.shape[0], "csr_transpose_values positions");
+  msx::require_size(vo, vd.shape[0], "csr_transpose_values out");
+  msx::require_contiguous(vo, "csr_transpose_values out");
+  msx::require_same_device({&vd, &vpos, &vo}, "csr_transpose_values");
+  if (vd.device < 0) throw std::invalid_argument("csr_transpose_values needs GPU tensors.");
+  void *stream = stream_for(vd.device);
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_transpose_values(msx::to_vtype(vd.dtype), vd.shape[0], vd.ptr,
+                                  static_cast<const int32_t *>(vpos.ptr), conjugate ? 1 : 0,
+                                  vo.ptr, stream);
+  }
+  msx::check_status(st, "csr_transpose_values");
 }
 
 py::object csr_matvec_transpose(py::handle data_o, py::handle indices_o, py::handle indptr_o,
@@ -528,6 +603,9 @@ PYBIND11_MODULE(_ext, m) {
       .def_readonly("index_dtype", &Plan::index_dtype)
       .def_readonly("device", &Plan::device)
       .def("info", &plan_info, "Plan summary (block and long-row counts, sizes).")
+      .def("refresh", &plan_refresh, py::arg("data"),
+           "The values changed (indices and indptr did not): rewrite the plan's copies "
+           "from data, which the plan is bound to from now on.")
       .def("export", &plan_export,
            "Host copies (int64 tensors) of bounds, long_rows and long_chunk_begin.");
 
@@ -554,6 +632,13 @@ PYBIND11_MODULE(_ext, m) {
   m.def("csr_transpose", &csr_transpose, py::arg("data"), py::arg("indices"), py::arg("indptr"),
         py::arg("n_rows"), py::arg("n_cols"),
         "CSR buffers of the transpose: (data, indices, indptr), shape (n_cols, n_rows).");
+  m.def("csr_transpose_positions", &csr_transpose_positions, py::arg("indices"),
+        py::arg("indptr"), py::arg("n_rows"), py::arg("n_cols"),
+        "(t_pos, t_indices, t_indptr): the transpose's structure and the position of A each "
+        "entry holds (int32, -1 past t_indptr[n_cols]).");
+  m.def("csr_transpose_values", &csr_transpose_values, py::arg("data"), py::arg("positions"),
+        py::arg("conjugate"), py::arg("out"),
+        "out[i] = data[positions[i]] (conjugated on request), in place.");
   m.def("csr_matvec_transpose", &csr_matvec_transpose, py::arg("data"), py::arg("indices"),
         py::arg("indptr"), py::arg("x"), py::arg("n_rows"), py::arg("n_cols"),
         py::arg("n_threads") = 0, "A^T x for CSR buffers of shape (n_rows, n_cols).");

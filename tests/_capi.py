@@ -58,6 +58,9 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_plan_create_bound.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp,
                                                 ctypes.POINTER(PlanOptions), vp, ctypes.POINTER(vp)]
         L.msx_csr_plan_destroy.argtypes = [vp]
+        L.msx_csr_plan_refresh.argtypes = [vp, vp, vp]
+        L.msx_csr_transpose_positions.argtypes = [ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_transpose_values.argtypes = [ci, i64, vp, vp, ci, vp, vp]
         L.msx_csr_plan_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
         L.msx_csr_plan_export.argtypes = [vp, vp, vp, vp]
         L.msx_csr_plan_export_panels.argtypes = [vp, vp, vp, vp]
@@ -96,7 +99,8 @@ def lib() -> ctypes.CDLL:
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
-                     "msx_csr_plan_destroy",
+                     "msx_csr_plan_destroy", "msx_csr_plan_refresh",
+                     "msx_csr_transpose_positions", "msx_csr_transpose_values",
                      "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_plan_export_panels",
                      "msx_csr_spmv", "msx_csr_spmm", "msx_csr_batched_spmv",
                      "msx_csr_batched_spmm", "msx_csr_batched_spmv_cpu",
@@ -154,6 +158,14 @@ class Plan:
         st = lib().msx_csr_plan_export(self.ptr, _p(blocks), _p(longs), _p(chunks))
         assert st == OK, last_error()
         return blocks.numpy(), longs[: info.n_long_rows].numpy(), chunks.numpy()
+
+    def refresh(self, data):
+        """The values changed: rewrite the plan's copies from ``data``."""
+        st = lib().msx_csr_plan_refresh(self.ptr, _p(data), _stream())
+        if st != OK:
+            raise RuntimeError(f"plan_refresh: {st} {last_error()}")
+        if getattr(self, "_keep", None) is not None:
+            self._keep = (data,) + self._keep[1:]
 
     def export_panels(self):
         info = self.info()
@@ -252,6 +264,25 @@ def transpose(data, indices, indptr, n_rows, n_cols):
     else:
         _check(lib().msx_csr_transpose(*args, _stream()), "msx_csr_transpose")
     return td, ti, tp
+
+
+def transpose_positions(indices, indptr, n_rows, n_cols):
+    """(t_pos int32, t_indices, t_indptr) of A^T on the GPU."""
+    nnz = indices.numel()
+    pos = torch.empty(nnz, dtype=torch.int32, device=indices.device)
+    ti = torch.empty(nnz, dtype=indices.dtype, device=indices.device)
+    tp = torch.empty(n_cols + 1, dtype=indptr.dtype, device=indices.device)
+    _check(lib().msx_csr_transpose_positions(IT[indices.dtype], n_rows, n_cols, nnz, _p(indices),
+                                             _p(indptr), _p(pos), _p(ti), _p(tp), _stream()),
+           "msx_csr_transpose_positions")
+    return pos, ti, tp
+
+
+def transpose_values(data, pos, out, conjugate=False):
+    _check(lib().msx_csr_transpose_values(VT[data.dtype], data.numel(), _p(data), _p(pos),
+                                          1 if conjugate else 0, _p(out), _stream()),
+           "msx_csr_transpose_values")
+    return out
 
 
 def spmv_transpose(data, indices, indptr, x, n_rows, n_cols, n_threads=1):

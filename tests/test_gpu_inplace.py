@@ -1,0 +1,310 @@
+"""Cached matrix state follows in-place updates of the values.
+
+torch tensors are mutable, unlike the reference's arrays
+(reference: mlx_sparse/_csr.py:33): after ``A.data`` changes in place (an
+optimizer step on the values), a product must use the new values, whatever
+the array cached - a bound plan's reordered copy (XCD slices, LDS panels),
+device copies, the transpose and the adjoint.  Every result below is
+checked against the oracle on the new values: bit for bit where both sides
+sum a row in stored order (panel plans, row blocks of short rows, the
+transpose's SpMV), within tol * sum|a*x| elsewhere.
+
+Also: a plan is bound to the indptr buffer it was built from (a same-nnz
+matrix with other rows is rejected), and a bound plan given new values
+without a refresh is rejected.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _capi
+from _util import TORCH, assert_rows_close, storage, to_numpy, to_torch
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+VTYPES = ["float32", "float16", "bfloat16", "complex64"]
+
+
+def _values(rng, n, vtype):
+    v = rng.standard_normal(n)
+    if vtype == "complex64":
+        v = v + 1j * rng.standard_normal(n)
+    return storage(v, vtype)
+
+
+def _random_csr(rng, n_rows, n_cols, max_len, index_dtype=np.int32):
+    lengths = rng.integers(0, max_len, n_rows)
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    indices = rng.integers(0, n_cols, int(indptr[-1]))
+    return indices.astype(index_dtype), indptr.astype(index_dtype), lengths
+
+
+def _short_rows_equal(got, want, lengths, W, vtype, what):
+    short = lengths <= W
+    g, w = got[short], want[short]
+    if vtype == "complex64":
+        g, w = g.view(np.float32), w.view(np.float32)
+    np.testing.assert_array_equal(g, w, err_msg=what)
+
+
+# -- the C ABI: msx_csr_plan_refresh ---------------------------------------------------
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("mode", [_capi.SLICE_PANELS, _capi.SLICE_ON])
+def test_plan_refresh_rewrites_the_copy(vtype, mode):
+    rng = np.random.default_rng(11)
+    n_rows, n_cols = 20_000, 300_000
+    indices, indptr, lengths = _random_csr(rng, n_rows, n_cols, 40)
+    lengths[5] = 0
+    nnz = int(indptr[-1])
+    data0, data1 = _values(rng, nnz, vtype), _values(rng, nnz, vtype)
+    x = _values(rng, n_cols, vtype)
+    d = to_torch(data0, vtype, DEV)
+    i, p = to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    xt = to_torch(x, vtype, DEV)
+    plan = _capi.Plan(p, n_rows, nnz, data=d, indices=i, n_cols=n_cols, slice_mode=mode)
+    info = plan.info()
+    assert (info.n_panels > 0) if mode == _capi.SLICE_PANELS else (info.n_slices == 8)
+    for step, new in enumerate((data1, data0, data1)):
+        # in place, same buffer
+        d.copy_(to_torch(new, vtype, DEV))
+        plan.refresh(d)
+        y = to_numpy(_capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan))
+        want = orc.csr_matvec(new, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+        scale = orc.row_scale(new, indices, indptr, x, n_rows, vtype=vtype)
+        assert_rows_close(y, want, scale, vtype, f"refresh {step} {vtype}")
+        if mode == _capi.SLICE_PANELS:
+            _short_rows_equal(y, want, lengths, info.block_nnz, vtype, f"panels {step}")
+    # a new buffer: rejected until the plan is refreshed with it, then bound to it
+    d2 = to_torch(data0, vtype, DEV)
+    with pytest.raises(RuntimeError, match="bound to other"):
+        _capi.spmv(d2, i, p, xt, n_rows, n_cols, plan=plan)
+    plan.refresh(d2)
+    y = to_numpy(_capi.spmv(d2, i, p, xt, n_rows, n_cols, plan=plan))
+    want = orc.csr_matvec(data0, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+    assert_rows_close(y, want, orc.row_scale(data0, indices, indptr, x, n_rows, vtype=vtype),
+                      vtype, "rebound")
+    with pytest.raises(RuntimeError, match="bound to other"):
+        _capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan)
+    plan.close()
+
+
+def test_plan_is_bound_to_its_indptr_buffer():
+    """Same n_rows and nnz, other rows: both plan kinds reject the matrix."""
+    rng = np.random.default_rng(3)
+    n_rows, n_cols = 5000, 4000
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, 20)
+    nnz = int(indptr[-1])
+    other = indptr.copy()
+    other[1:-1] = np.sort(rng.integers(0, nnz, n_rows - 1))  # same nnz, other rows
+    d = torch.ones(nnz, device=DEV)
+    i = to_torch(indices, None, DEV)
+    p, p2 = to_torch(indptr, None, DEV), to_torch(other, None, DEV)
+    x = torch.ones(n_cols, device=DEV)
+    for plan in (_capi.Plan(p, n_rows, nnz), _capi.Plan(p, n_rows, nnz, data=d, indices=i,
+                                                        n_cols=n_cols)):
+        with pytest.raises(RuntimeError, match="another indptr"):
+            _capi.spmv(d, i, p2, x, n_rows, n_cols, plan=plan)
+        st = _capi.lib().msx_csr_spmv(0, 0, n_rows, n_cols, nnz, d.data_ptr(), i.data_ptr(),
+                                      p2.data_ptr(), x.data_ptr(),
+                                      torch.empty(n_rows, device=DEV).data_ptr(), plan.ptr,
+                                      _capi._stream())
+        assert st == _capi.EINVAL
+        y = _capi.spmv(d, i, p, x, n_rows, n_cols, plan=plan)  # its own indptr still works
+        np.testing.assert_array_equal(to_numpy(y), np.diff(indptr).astype(np.float32))
+        plan.close()
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+def test_transpose_positions_and_values(vtype):
+    """msx_csr_transpose_positions lists, per entry of A^T, the position of
+    A it holds: gathering A's values through it equals msx_csr_transpose and
+    the oracle's transpose bit for bit (conjugated for A^H)."""
+    rng = np.random.default_rng(5)
+    n_rows, n_cols = 3000, 2500
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, 30)
+    indices[7] = n_cols + 3  # out of range: dropped from the transpose
+    nnz = int(indptr[-1])
+    data = _values(rng, nnz, vtype)
+    d = to_torch(data, vtype, DEV)
+    i, p = to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    pos, ti, tp = _capi.transpose_positions(i, p, n_rows, n_cols)
+    td, ti2, tp2 = _capi.transpose(d, i, p, n_rows, n_cols)
+    kept = int(tp[-1].item())
+    assert kept == nnz - 1
+    assert torch.equal(tp, tp2) and torch.equal(ti[:kept], ti2[:kept])
+    assert torch.all(pos[kept:] == -1)
+    out = torch.zeros_like(d)
+    _capi.transpose_values(d, pos, out)
+    np.testing.assert_array_equal(to_numpy(out[:kept]), to_numpy(td[:kept]))
+    ot, oi, op = orc.csr_transpose(data, indices, indptr, n_rows, n_cols, vtype=vtype)
+    np.testing.assert_array_equal(to_numpy(out[:kept]), ot)
+    if vtype == "complex64":
+        _capi.transpose_values(d, pos, out, conjugate=True)
+        np.testing.assert_array_equal(to_numpy(out[:kept]), np.conj(ot))
+
+
+# -- the drop-in API: in-place updates of A.data ------------------------------------------
+
+def _sgd(A, step):
+    with torch.no_grad():
+        A.data.mul_(0.5).add_(step)
+
+
+def _check_forward_and_adjoint(ms, A, m_indices, m_indptr, shape, x, g, what, exact):
+    n_rows, n_cols = shape
+    data = A.data.detach().cpu().numpy()
+    xn, gn = x.cpu().numpy(), g.cpu().numpy()
+    y = (A @ x).cpu().numpy()
+    want = orc.csr_matvec(data, m_indices, m_indptr, xn, n_rows, n_threads=8)
+    if exact:
+        np.testing.assert_array_equal(y, want, err_msg=f"{what}: A @ x")
+    assert_rows_close(y, want, orc.row_scale(data, m_indices, m_indptr, xn, n_rows), "float32",
+                      f"{what}: A @ x")
+    # x.grad = A^T g, checked against the oracle's transpose and its SpMV
+    xr = x.clone().requires_grad_()
+    (A @ xr).backward(g)
+    td, ti, tp = orc.csr_transpose(data, m_indices, m_indptr, n_rows, n_cols)
+    want_t = orc.csr_matvec(td, ti, tp, gn, n_cols, n_threads=8)
+    assert_rows_close(xr.grad.cpu().numpy(), want_t, orc.row_scale(td, ti, tp, gn, n_cols),
+                      "float32", f"{what}: x.grad")
+    # A.T follows the new values too; on a panel plan its SpMV sums every
+    # row in stored order
+    yt = (A.T @ g).cpu().numpy()
+    if exact:
+        np.testing.assert_array_equal(yt, want_t, err_msg=f"{what}: A.T @ g")
+    assert_rows_close(yt, want_t, orc.row_scale(td, ti, tp, gn, n_cols), "float32",
+                      f"{what}: A.T @ g")
+
+
+@pytest.mark.parametrize("slice_mode", ["auto", "on"])
+def test_inplace_update_on_a_bound_plan(gpu, slice_mode):
+    """The panel plan AUTO builds for a 2M-row random matrix (16 per row) and
+    the XCD-sliced plan: A @ x, x.grad and A.T @ g after SGD-style updates."""
+    from mlx_sparse import runtime, synthetic
+
+    ms = gpu
+    m = synthetic.random_fixed_row(1 << 21, 16, seed=9)
+    x = torch.from_numpy(synthetic.uniform(m.shape[1], -1, 1, seed=2)).to(DEV)
+    g = torch.from_numpy(synthetic.uniform(m.shape[0], -1, 1, seed=3)).to(DEV)
+    with runtime.context(gpu_slice=slice_mode, gpu_adjoint="auto"):
+        A = ms.csr_array((m.data, m.indices, m.indptr), shape=m.shape)
+        info = A.plan().info()
+        if slice_mode == "auto":
+            assert info["n_panels"] > 0
+        else:
+            assert info["n_slices"] == 8
+        exact = slice_mode == "auto"  # panels sum every short row in stored order
+        _check_forward_and_adjoint(ms, A, m.indices, m.indptr, m.shape, x, g, "initial", exact)
+        plan = A.plan()
+        for k in range(2):
+            _sgd(A, 0.25 * (k + 1))
+            _check_forward_and_adjoint(ms, A, m.indices, m.indptr, m.shape, x, g,
+                                       f"after update {k}", exact)
+            assert A.plan() is plan  # refreshed, not rebuilt
+
+
+def test_inplace_update_trained_values_small_matrix(gpu):
+    """Row blocks, gradients of the values themselves: three SGD steps on a
+    requires-grad A.data under gpu_adjoint="auto" (atomic first, then the
+    cached transpose, then the refreshed transpose); every step's forward
+    and x.grad are checked against the oracle on that step's values."""
+    from mlx_sparse import runtime
+
+    ms = gpu
+    rng = np.random.default_rng(17)
+    n_rows, n_cols = 3000, 2000
+    indices, indptr, lengths = _random_csr(rng, n_rows, n_cols, 30)
+    data = torch.from_numpy(rng.standard_normal(int(indptr[-1])).astype(np.float32)).to(DEV)
+    data.requires_grad_()
+    A = ms.csr_array((data, indices, indptr), shape=(n_rows, n_cols))
+    x = torch.from_numpy(rng.uniform(-1, 1, n_cols).astype(np.float32)).to(DEV)
+    g = torch.from_numpy(rng.uniform(-1, 1, n_rows).astype(np.float32)).to(DEV)
+    with runtime.context(gpu_adjoint="auto"):
+        for step in range(3):
+            vals = A.data.detach().cpu().numpy()
+            xr = x.clone().requires_grad_()
+            y = A @ xr
+            want = orc.csr_matvec(vals, indices, indptr, x.cpu().numpy(), n_rows)
+            np.testing.assert_array_equal(y.detach().cpu().numpy(), want)
+            y.backward(g)
+            td, ti, tp = orc.csr_transpose(vals, indices, indptr, n_rows, n_cols)
+            gn = g.cpu().numpy()
+            want_t = orc.csr_matvec(td, ti, tp, gn, n_cols)
+            assert_rows_close(xr.grad.cpu().numpy(), want_t, orc.row_scale(td, ti, tp, gn, n_cols),
+                              "float32", f"step {step}: x.grad")
+            want_d = orc.csr_data_vjp(indices, indptr, x.cpu().numpy(), gn, n_rows, n_cols,
+                                      int(indptr[-1]))
+            np.testing.assert_array_equal(A.data.grad.cpu().numpy(), want_d)
+            with torch.no_grad():
+                A.data.sub_(0.5 * A.data.grad)
+            A.data.grad = None
+
+
+def test_inplace_update_of_a_host_array_used_on_the_gpu(gpu):
+    """Values held on the host: the device copy is made again after an
+    in-place update, and a tracked product with those values runs plan-free
+    instead of failing on the plan's binding."""
+    ms = gpu
+    rng = np.random.default_rng(23)
+    n_rows, n_cols = 1000, 800
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, 12)
+    data = torch.from_numpy(rng.standard_normal(int(indptr[-1])).astype(np.float32))
+    A = ms.CSRArray(data=data, indices=torch.from_numpy(indices), indptr=torch.from_numpy(indptr),
+                    shape=(n_rows, n_cols))
+    assert A.data.device.type == "cpu"
+    x = torch.from_numpy(rng.uniform(-1, 1, n_cols).astype(np.float32)).to(DEV)
+    for step in range(2):
+        vals = A.data.numpy().copy()
+        want = orc.csr_matvec(vals, indices, indptr, x.cpu().numpy(), n_rows)
+        scale = orc.row_scale(vals, indices, indptr, x.cpu().numpy(), n_rows)
+        np.testing.assert_array_equal((A @ x).cpu().numpy(), want)
+        xr = x.clone().requires_grad_()
+        # tracked with values copied from the host: the plan-free kernel
+        # (several lanes per row) runs instead of the plan
+        assert_rows_close((A @ xr).detach().cpu().numpy(), want, scale, "float32",
+                          f"tracked step {step}")
+        A.data.mul_(-2.0)
+    # non-contiguous values with requires_grad: plan-free, same result
+    base = torch.from_numpy(np.repeat(rng.standard_normal(int(indptr[-1])).astype(np.float32), 2))
+    strided = base.to(DEV)[::2].requires_grad_()
+    B = ms.CSRArray(data=strided, indices=torch.from_numpy(indices).to(DEV),
+                    indptr=torch.from_numpy(indptr).to(DEV), shape=(n_rows, n_cols))
+    vals = strided.detach().cpu().numpy()
+    want = orc.csr_matvec(vals, indices, indptr, x.cpu().numpy(), n_rows)
+    assert_rows_close((B @ x).detach().cpu().numpy(), want,
+                      orc.row_scale(vals, indices, indptr, x.cpu().numpy(), n_rows), "float32",
+                      "non-contiguous tracked values")
+
+
+def test_hermitian_transpose_is_cached_and_follows_updates(gpu):
+    ms = gpu
+    rng = np.random.default_rng(29)
+    n_rows, n_cols = 1500, 1200
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, 20)
+    nnz = int(indptr[-1])
+    for dtype in (torch.float32, torch.complex64):
+        v = rng.standard_normal(nnz) + (1j * rng.standard_normal(nnz) if dtype == torch.complex64 else 0)
+        A = ms.csr_array((torch.as_tensor(v).to(dtype), indices, indptr), shape=(n_rows, n_cols))
+        H1 = A.H
+        assert A.H is H1  # cached
+        if dtype == torch.float32:
+            assert A.T is H1  # real values: A^H is A^T
+        with torch.no_grad():
+            A.data.mul_(3.0)
+        H2 = A.H
+        vals = A.data.cpu().numpy()
+        ot, oi, op = orc.csr_transpose(vals, indices, indptr, n_rows, n_cols)
+        np.testing.assert_array_equal(H2.data.cpu().numpy(), np.conj(ot))
+        np.testing.assert_array_equal(H2.indptr.cpu().numpy(), op)
+        g = torch.as_tensor(rng.standard_normal(n_rows)).to(DEV, dtype)
+        y = (H2 @ g).cpu().numpy()
+        want = orc.csr_matvec(np.conj(ot), oi, op, g.cpu().numpy(), n_cols)
+        assert_rows_close(y, want, orc.row_scale(np.conj(ot), oi, op, g.cpu().numpy(), n_cols),
+                          "complex64" if dtype == torch.complex64 else "float32", "A.H @ g")
