@@ -393,6 +393,26 @@ msx_status msx_csr_spmm_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,
                                   void *Y, int64_t ldy, void *stream);
 
 /*
+ * msx_csr_spmv_transpose without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No reference counterpart.
+ * Same arguments and results as msx_csr_spmv_transpose; float16/bfloat16
+ * accumulate in a fixed float32 scratch array inside the library instead of
+ * stream-ordered scratch, so they need n_cols <= 8388608 (32 MiB; larger
+ * n_cols fail with MSX_EINVAL).  Each GPU holds its own scratch array from
+ * the first such call until the process ends, and every call on that GPU
+ * uses it: calls that overlap on one GPU (different streams, or different
+ * host threads) race.  float32 and complex64 accumulate in y, as in
+ * msx_csr_spmv_transpose, and use no scratch.
+ */
+msx_status msx_csr_spmv_transpose_noalloc(msx_vtype vt, msx_itype it,
+                                          int64_t n_rows, int64_t n_cols,
+                                          int64_t nnz, const void *data,
+                                          const void *indices,
+                                          const void *indptr, const void *x,
+                                          void *y, void *stream);
+
+/*
  * Host (CPU) transposed products, contiguous operands, the reference's
  * algorithm: with one worker every output is summed from zero over the rows
  * in order; with W workers, rows are split by row length into W ranges, each

@@ -25,6 +25,7 @@
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "msx_device.h"
@@ -40,6 +41,39 @@ constexpr int64_t kIntMax = 2147483647;
 
 uint32_t grid_for(int64_t n) {
   return static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, kMaxGrid)));
+}
+
+// Allocation-free transposed SpMV (msx_csr_spmv_transpose_noalloc): the
+// float32 accumulators of 16-bit values live in this file-scope device array
+// instead of stream-ordered scratch.  Each GPU the library runs on holds its
+// own copy (32 MiB) until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): it passes the address hipGetSymbolAddress gives for the current
+// device (noalloc_scratch below).
+constexpr int64_t kNoAllocAccMax = int64_t{1} << 23;  // float32 accumulators
+static __device__ __align__(256) float scratch[kNoAllocAccMax];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first
+// call made with that device current and kept.
+msx_status noalloc_scratch(float **out) {
+  int dev = -1;
+  MSX_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MSX_EINVAL, "csr_matvec_transpose_noalloc supports device ordinals below 64.");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(MSX_EHIP, "hipGetSymbolAddress(scratch) returned NULL.");
+    g_scratch_ptr[dev] = static_cast<float *>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return MSX_OK;
 }
 
 __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
@@ -245,13 +279,13 @@ msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const v
                                                  static_cast<uint64_t *>(nullptr),
                                                  static_cast<uint64_t *>(nullptr),
                                                  static_cast<int>(nnz), 0, end_bit, stream));
-  char *scratch = nullptr;
-  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&scratch), 2 * b4 + 2 * b8 + sort_bytes, stream));
-  auto *key = reinterpret_cast<uint32_t *>(scratch);
-  auto *key_out = reinterpret_cast<uint32_t *>(scratch + b4);
-  auto *val = reinterpret_cast<uint64_t *>(scratch + 2 * b4);
-  auto *val_out = reinterpret_cast<uint64_t *>(scratch + 2 * b4 + b8);
-  void *sort_tmp = scratch + 2 * b4 + 2 * b8;
+  char *work = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&work), 2 * b4 + 2 * b8 + sort_bytes, stream));
+  auto *key = reinterpret_cast<uint32_t *>(work);
+  auto *key_out = reinterpret_cast<uint32_t *>(work + b4);
+  auto *val = reinterpret_cast<uint64_t *>(work + 2 * b4);
+  auto *val_out = reinterpret_cast<uint64_t *>(work + 2 * b4 + b8);
+  void *sort_tmp = work + 2 * b4 + 2 * b8;
   const int G = lanes_for(n_rows, nnz);
   hipLaunchKernelGGL(drop_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
                      static_cast<uint32_t>(n_cols), key);
@@ -270,7 +304,7 @@ msx_status transpose_packed(int64_t n_rows, int64_t n_cols, int64_t nnz, const v
   }
   msx_status st = MSX_OK;
   if (e != hipSuccess) st = hip_fail(e, "csr_transpose");
-  const hipError_t ef = hipFreeAsync(scratch, stream);
+  const hipError_t ef = hipFreeAsync(work, stream);
   if (st == MSX_OK && ef != hipSuccess) st = hip_fail(ef, "csr_transpose scratch release");
   return st;
 }
@@ -307,14 +341,14 @@ msx_status transpose_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const vo
                                                  static_cast<uint32_t *>(nullptr),
                                                  static_cast<uint32_t *>(nullptr),
                                                  static_cast<int>(nnz), 0, end_bit, stream));
-  char *scratch = nullptr;
-  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&scratch), 4 * b4 + bI + sort_bytes, stream));
-  auto *key = reinterpret_cast<uint32_t *>(scratch);
-  auto *key_out = reinterpret_cast<uint32_t *>(scratch + b4);
-  auto *pos = reinterpret_cast<uint32_t *>(scratch + 2 * b4);
-  auto *pos_out = reinterpret_cast<uint32_t *>(scratch + 3 * b4);
-  auto *row = reinterpret_cast<I *>(scratch + 4 * b4);
-  void *sort_tmp = scratch + 4 * b4 + bI;
+  char *work = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&work), 4 * b4 + bI + sort_bytes, stream));
+  auto *key = reinterpret_cast<uint32_t *>(work);
+  auto *key_out = reinterpret_cast<uint32_t *>(work + b4);
+  auto *pos = reinterpret_cast<uint32_t *>(work + 2 * b4);
+  auto *pos_out = reinterpret_cast<uint32_t *>(work + 3 * b4);
+  auto *row = reinterpret_cast<I *>(work + 4 * b4);
+  void *sort_tmp = work + 4 * b4 + bI;
   msx_status st = MSX_OK;
   hipLaunchKernelGGL(init_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
                      static_cast<uint32_t>(n_cols), key, pos);
@@ -334,7 +368,7 @@ msx_status transpose_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const vo
     e = hipGetLastError();
   }
   if (e != hipSuccess) st = hip_fail(e, "csr_transpose");
-  const hipError_t ef = hipFreeAsync(scratch, stream);
+  const hipError_t ef = hipFreeAsync(work, stream);
   if (st == MSX_OK && ef != hipSuccess) st = hip_fail(ef, "csr_transpose scratch release");
   return st;
 }
@@ -529,18 +563,23 @@ struct TransposeOp {
 };
 
 // Accumulators: the output itself when it holds the accumulator type
-// (float32, complex64), else float32 scratch narrowed at the end.
+// (float32, complex64), else float32 scratch narrowed at the end: `fixed`
+// (n_cols floats the caller provides) when non-NULL, else stream-ordered
+// scratch.
 template <class V, class I>
 struct SpmvTransposeOp {
   static msx_status run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
                         const void *indices, const void *indptr, const void *x, void *y,
-                        hipStream_t stream) {
+                        float *fixed, hipStream_t stream) {
     using S = typename V::Storage;
     using A = typename V::Acc;
     constexpr bool direct = sizeof(S) == sizeof(A);
+    const bool owned = !direct && fixed == nullptr;
     A *acc = nullptr;
     if (direct) {
       acc = static_cast<A *>(y);
+    } else if (fixed != nullptr) {
+      acc = reinterpret_cast<A *>(fixed);
     } else {
       MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&acc), sizeof(A) * std::max<int64_t>(n_cols, 1), stream));
     }
@@ -554,7 +593,7 @@ struct SpmvTransposeOp {
       hipLaunchKernelGGL((narrow_all<V>), dim3(grid_for(n_cols)), dim3(kThreads), 0, stream, acc,
                          n_cols, static_cast<S *>(y));
     hipError_t e = hipGetLastError();
-    if (!direct) {
+    if (owned) {
       const hipError_t ef = hipFreeAsync(acc, stream);
       if (e == hipSuccess) e = ef;
     }
@@ -743,6 +782,33 @@ extern "C" msx_status msx_csr_spmv_transpose(msx_vtype vt, msx_itype it, int64_t
     return fail(MSX_EINVAL, "csr_matvec_transpose data and x must be non-NULL.");
   if (n_cols == 0) return MSX_OK;
   return dispatch<SpmvTransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, x, y,
+                                   static_cast<float *>(nullptr), static_cast<hipStream_t>(stream));
+}
+
+extern "C" msx_status msx_csr_spmv_transpose_noalloc(msx_vtype vt, msx_itype it, int64_t n_rows,
+                                                     int64_t n_cols, int64_t nnz, const void *data,
+                                                     const void *indices, const void *indptr,
+                                                     const void *x, void *y, void *stream) {
+  clear_error();
+  msx_status st =
+      check_csr("csr_matvec_transpose_noalloc", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  if (n_cols > 0 && y == nullptr) return fail(MSX_EINVAL, "csr_matvec_transpose_noalloc y is NULL.");
+  if (nnz > 0 && (data == nullptr || x == nullptr))
+    return fail(MSX_EINVAL, "csr_matvec_transpose_noalloc data and x must be non-NULL.");
+  const bool wide_acc = vt == MSX_F16 || vt == MSX_BF16;  // float32 accumulators in `scratch`
+  if (wide_acc && n_cols > kNoAllocAccMax)
+    return fail(MSX_EINVAL, "csr_matvec_transpose_noalloc: float16/bfloat16 need n_cols <= " +
+                                std::to_string(kNoAllocAccMax) +
+                                " (the 32 MiB allocation-free scratch), got " +
+                                std::to_string(n_cols) + ".");
+  float *fixed = nullptr;
+  if (wide_acc) {
+    st = noalloc_scratch(&fixed);
+    if (st != MSX_OK) return st;
+  }
+  if (n_cols == 0) return MSX_OK;
+  return dispatch<SpmvTransposeOp>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, x, y, fixed,
                                    static_cast<hipStream_t>(stream));
 }
 

@@ -78,6 +78,8 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
         L.msx_csr_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
         L.msx_csr_spmv_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmv_transpose_noalloc.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp,
+                                                     vp]
         L.msx_csr_spmm_transpose.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp,
                                              i64, vp]
         L.msx_csr_spmv_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
@@ -107,6 +109,7 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_batched_spmm_cpu",
                      "msx_csr_spmv_cpu", "msx_csr_spmm_cpu", "msx_cpu_ranges",
                      "msx_csr_transpose", "msx_csr_transpose_cpu", "msx_csr_spmv_transpose",
+                     "msx_csr_spmv_transpose_noalloc",
                      "msx_csr_spmm_transpose", "msx_csr_spmv_transpose_cpu",
                      "msx_csr_spmm_transpose_cpu", "msx_csr_spmv_data_vjp",
                      "msx_csr_spmm_data_vjp", "msx_csr_spmv_data_vjp_cpu",
