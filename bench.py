@@ -28,6 +28,8 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``cg``: conjugate gradients (device-resident loop) on the Poisson matrix,
   time per iteration against its bytes, and the single-threaded reference
   loop on the host;
+- ``krylov``: BiCGSTAB and MINRES (device-resident loops) at n = 128^3, the
+  same figures;
 - ``mtx`` (with ``--mtx PATH``): SpMV on a Matrix Market matrix read by the
   native reader (``mmread``);
 - ``adjoint``: on the headline matrix, ``A^T x`` by atomic scatter and over
@@ -337,38 +339,166 @@ def cg_leg(dev) -> dict:
     return out
 
 
-def configs_leg(ext, dev, scratch) -> list:
-    """SpMV / SpMM on each benchmark configuration through the cached bound
-    plan (AUTO's choice), timed like the headline (graph replay) and cold
-    (1 GiB written between calls), against the compulsory bytes
-    nnz*(value+index) + indptr + x once + y once (X, Y at width k)."""
+# Benchmark configurations: short id -> (label,
+# matrix generator, value type, rhs width k or None, complex values).  The
+# matrix generators are seeded; x ~ U[-1, 1] (cfg3: U[0, 1]), X ~ N(0, 1).
+CASES = {
+    "cfg1": ("cfg1 laplacian2d 1024^2 f32/i32", "laplacian", torch.float32, None),
+    "cfg2": ("cfg2 random16 n=2^22 f32/i32", "random16", torch.float32, None),
+    "cfg3": ("cfg3 powerlaw zipf2 n=2^21 f32/i64", "powerlaw", torch.float32, None),
+    "cfg4": ("cfg4 poisson3d 128^3 f32/i32", "poisson", torch.float32, None),
+    "cfg4-k8": ("cfg4 poisson3d 128^3 f32/i32", "poisson", torch.float32, 8),
+    "cfg4-k64": ("cfg4 poisson3d 128^3 f32/i32", "poisson", torch.float32, 64),
+    "cfg4-k256": ("cfg4 poisson3d 128^3 f32/i32", "poisson", torch.float32, 256),
+    "cfg5-f32": ("cfg5 banded hb32 f32/i32", "banded", torch.float32, None),
+    "cfg5-bf16": ("cfg5 banded hb32 bf16/i32", "banded", torch.bfloat16, None),
+    "cfg5-f16": ("cfg5 banded hb32 f16/i32", "banded", torch.float16, None),
+    "cfg5-f16-k64": ("cfg5 banded hb32 f16/i32", "banded", torch.float16, 64),
+    "cfg5-bf16-k64": ("cfg5 banded hb32 bf16/i32", "banded", torch.bfloat16, 64),
+    "cfg5-c64": ("cfg5 banded hb32 c64/i32", "banded", torch.complex64, None),
+}
+
+
+def _matrix(kind: str):
+    from mlx_sparse import synthetic
+
+    if kind == "laplacian":
+        return synthetic.laplacian_2d(1024)
+    if kind == "random16":
+        return synthetic.random_fixed_row(1 << 22, 16, seed=0)
+    if kind == "powerlaw":
+        return synthetic.power_law(1 << 21, 2.0, 200_000, seed=0)
+    if kind == "poisson":
+        return synthetic.poisson_3d(128)
+    return synthetic.banded(1 << 20, 32, 0.65, 70.0, seed=0)
+
+
+def _operands(case: str, m, dev):
+    """(values, x or X) of a case on ``dev``."""
+    from mlx_sparse import synthetic
+
+    _, kind, dt, k = CASES[case]
+    n = m.shape[1]
+    if dt == torch.complex64:
+        data = torch.from_numpy(synthetic.complex_values(m, seed=3))
+        x = torch.complex(torch.from_numpy(synthetic.uniform(n, -1.0, 1.0, seed=4)),
+                          torch.from_numpy(synthetic.uniform(n, -1.0, 1.0, seed=5)))
+        return data, x.to(dev)
+    data = torch.from_numpy(m.data).to(dt)
+    if k is not None:
+        return data, torch.from_numpy(synthetic.normal(n, seed=2, k=k)).to(dev).to(dt)
+    low = 0.0 if kind == "powerlaw" else -1.0
+    return data, torch.from_numpy(synthetic.uniform(n, low, 1.0, seed=1)).to(dev).to(dt)
+
+
+def _case_call(ext, case: str, m, data, X, dev):
+    """(call, info, compulsory bytes, flops, keep-alive) of a case through its
+    cached bound plan (AUTO's choice)."""
     import mlx_sparse as ms
     from mlx_sparse import synthetic
 
-    cases = []
-    rows = []
+    _, _, dt, k = CASES[case]
+    n_rows, n_cols = m.shape
+    A = ms.csr_array((data, torch.from_numpy(m.indices), torch.from_numpy(m.indptr)),
+                     shape=m.shape)
+    d, i, p = A.buffers(dev)
+    plan = A.plan(dev)
+    if k is None:
+        fn = lambda: ext.csr_matvec(d, i, p, X, n_rows, n_cols, plan=plan)
+    else:
+        fn = lambda: ext.csr_matmul(d, i, p, X, n_rows, n_cols, plan=plan)
+    vb, ib = data.element_size(), m.indices.dtype.itemsize
+    nbytes = synthetic.compulsory_bytes(m.nnz, n_rows, n_cols, vb, ib, k=k or 1)
+    nflops = synthetic.flops(m.nnz, k or 1, dt == torch.complex64)
+    return fn, plan.info(), nbytes, nflops, (A, d, i, p, plan)
 
-    def run(name, m, data, X, k=None, complex_values=False):
-        n_rows, n_cols = m.shape
-        A = ms.csr_array((data, torch.from_numpy(m.indices), torch.from_numpy(m.indptr)),
-                         shape=m.shape)
-        d, i, p = A.buffers(dev)
-        plan = A.plan(dev)
-        info = plan.info()
-        if k is None:
-            fn = lambda: ext.csr_matvec(d, i, p, X, n_rows, n_cols, plan=plan)
-        else:
-            fn = lambda: ext.csr_matmul(d, i, p, X, n_rows, n_cols, plan=plan)
+
+def _kind(info) -> str:
+    return "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
+
+
+def krylov_leg(dev) -> dict:
+    """BiCGSTAB and MINRES (device-resident loops) at n = 128^3: MINRES on
+    the 3D Poisson matrix with shift -1, BiCGSTAB on a nonsymmetric
+    convection-diffusion variant of it (x-direction off-diagonals -1.3 and
+    -0.7, diagonal 8); b ~ U[-1, 1], rtol 1e-5.  Bytes per iteration: two
+    SpMVs' compulsory bytes plus the vector passes (BiCGSTAB 20, MINRES 18
+    float vectors of n).  The CPU figure is the oracle's single-threaded
+    restatement of the reference loop on the same system."""
+    import mlx_sparse as ms
+    from mlx_sparse import linalg, synthetic
+    from oracle import oracle as orc
+
+    m = synthetic.poisson_3d(128)
+    n = m.shape[0]
+    rows = np.repeat(np.arange(n), np.diff(m.indptr))
+    cols = m.indices.astype(np.int64)
+    conv = m.data.copy()
+    conv[cols == rows + 1] = -0.7
+    conv[cols == rows - 1] = -1.3
+    conv[cols == rows] = 8.0
+    b_np = synthetic.uniform(n, -1.0, 1.0, seed=7)
+    b = torch.from_numpy(b_np).to(dev)
+    spmv_bytes = synthetic.compulsory_bytes(m.nnz, n, n, 4, 4)
+    out = {"workload": "n=2097152 (128^3) f32/i32, b~U[-1,1], rtol=1e-5"}
+    for name, data, kw, nvec, f in (("minres", m.data, {"shift": -1.0}, 18, orc.csr_minres),
+                                    ("bicgstab", conv, {}, 20, orc.csr_bicgstab)):
+        A = ms.csr_array((data, m.indices, m.indptr), shape=m.shape, canonical=True)
+        solver = getattr(linalg, name)
+        solver(A, b, rtol=1e-5, maxiter=500, **kw)  # plan, allocator
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            x, info = solver(A, b, rtol=1e-5, maxiter=500, return_info=True, **kw)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        solve_s = statistics.median(times)
+        its = max(info.iterations, 1)
+        it_bytes = 2 * spmv_bytes + nvec * 4 * n
+        t0 = time.perf_counter()
+        _, cinfo, _, cits = f(data, m.indices, m.indptr, b_np, rtol=1e-5, maxiter=500, **kw)
+        cpu_it = (time.perf_counter() - t0) / max(cits, 1)
+        out[name] = {"matrix": "poisson3d + shift -1" if name == "minres" else
+                     "convection-diffusion variant of poisson3d",
+                     "info": info.status, "iterations": info.iterations,
+                     "residual": info.residual_norm, "solve_ms": round(solve_s * 1e3, 2),
+                     "us_per_iteration": round(solve_s / its * 1e6, 1),
+                     "bytes_per_iteration": it_bytes,
+                     "gbs": round(it_bytes / (solve_s / its) / 1e9, 1),
+                     "frac": round(it_bytes / (solve_s / its) / 1e9 / HBM_PEAK_GBS, 4),
+                     "cpu_us_per_iteration": round(cpu_it * 1e6, 1),
+                     "cpu_iterations": cits,
+                     "speedup_per_iteration": round(cpu_it / (solve_s / its), 1)}
+        log(f"{name}: {out[name]}")
+        del A
+        torch.cuda.empty_cache()
+    return out
+
+
+def configs_leg(ext, dev, scratch) -> list:
+    """SpMV / SpMM on each benchmark configuration but the headline, through
+    the cached bound plan (AUTO's choice), timed like the headline (graph
+    replay) and cold (1 GiB written between calls), against the compulsory
+    bytes nnz*(value+index) + indptr + x once + y once (X, Y at width k)."""
+    rows = []
+    m_kind, m = None, None
+    for case, (label, kind, dt, k) in CASES.items():
+        if case == "cfg2":
+            continue  # the headline leg
+        if kind != m_kind:
+            m, m_kind = None, None
+            torch.cuda.empty_cache()
+            m, m_kind = _matrix(kind), kind
+        data, X = _operands(case, m, dev)
+        fn, info, nbytes, nflops, keep = _case_call(ext, case, m, data, X, dev)
         t, _ = _graph_time(fn, calls=10 if k else 20)
         cold = _cold_time(fn, 10, scratch)
-        vb, ib = data.element_size(), m.indices.dtype.itemsize
-        nbytes = synthetic.compulsory_bytes(m.nnz, n_rows, n_cols, vb, ib, k=k or 1)
-        nflops = synthetic.flops(m.nnz, k or 1, complex_values)
-        kind = "panels" if info.get("n_panels") else ("slices" if info.get("n_slices") else "blocks")
-        row = {"case": name, "nnz": m.nnz, "op": "spmv" if k is None else f"spmm k={k}",
-               "plan": kind, "plan_bytes": info["plan_bytes"], "block_nnz": info["block_nnz"],
-               "window_rows": info["window_rows"], "long_rows": info["n_long_rows"],
-               "compulsory_bytes": nbytes, "flops": nflops,
+        row = {"case": label, "id": case, "nnz": m.nnz,
+               "op": "spmv" if k is None else f"spmm k={k}",
+               "plan": _kind(info), "plan_bytes": info["plan_bytes"],
+               "block_nnz": info["block_nnz"], "window_rows": info["window_rows"],
+               "long_rows": info["n_long_rows"], "compulsory_bytes": nbytes, "flops": nflops,
                "kernel_us": round(t * 1e3, 2), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
                "frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "gflops": round(nflops / (t * 1e-3) / 1e9, 1),
@@ -376,37 +506,30 @@ def configs_leg(ext, dev, scratch) -> list:
                "cold_frac": round(nbytes / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"config: {row}")
         rows.append(row)
-        del A, d, i, p, plan
+        del fn, keep, data, X
         torch.cuda.empty_cache()
-
-    def vec(n, seed, low=-1.0, high=1.0):
-        return torch.from_numpy(synthetic.uniform(n, low, high, seed=seed)).to(dev)
-
-    m = synthetic.laplacian_2d(1024)
-    run("cfg1 laplacian2d 1024^2 f32/i32", m, torch.from_numpy(m.data), vec(m.shape[1], 1))
-    m = synthetic.power_law(1 << 21, 2.0, 200_000, seed=0)
-    run("cfg3 powerlaw zipf2 n=2^21 f32/i64", m, torch.from_numpy(m.data),
-        vec(m.shape[1], 1, 0.0, 1.0))
-    m = synthetic.poisson_3d(128)
-    run("cfg4 poisson3d 128^3 f32/i32", m, torch.from_numpy(m.data), vec(m.shape[1], 1))
-    for k in (8, 64, 256):
-        X = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=k)).to(dev)
-        run("cfg4 poisson3d 128^3 f32/i32", m, torch.from_numpy(m.data), X, k=k)
-        del X
-    m = synthetic.banded(1 << 20, 32, 0.65, 70.0, seed=0)
-    d32 = torch.from_numpy(m.data)
-    x32 = vec(m.shape[1], 1)
-    run("cfg5 banded hb32 f32/i32", m, d32, x32)
-    for dt, nm in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
-        run(f"cfg5 banded hb32 {nm}/i32", m, d32.to(dt), x32.to(dt))
-    X64 = torch.from_numpy(synthetic.normal(m.shape[1], seed=2, k=64)).to(dev)
-    for dt, nm in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
-        run(f"cfg5 banded hb32 {nm}/i32", m, d32.to(dt), X64.to(dt), k=64)
-    del X64
-    cv = torch.from_numpy(synthetic.complex_values(m, seed=3))
-    xc = torch.complex(vec(m.shape[1], 4), vec(m.shape[1], 5))
-    run("cfg5 banded hb32 c64/i32", m, cv, xc, complex_values=True)
     return rows
+
+
+def profile_case(ext, dev, case: str, calls: int) -> dict:
+    """One configuration alone, for rocprofv3 (kernel trace or counters):
+    a 1 GiB copy of known traffic (the counters' scale), then ``calls``
+    back-to-back calls through the case's bound plan, synchronised."""
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+    label, kind, dt, k = CASES[case]
+    m = _matrix(kind)
+    data, X = _operands(case, m, dev)
+    fn, info, nbytes, nflops, keep = _case_call(ext, case, m, data, X, dev)
+    torch.cuda.synchronize()
+    t_ms = _events_time(fn, calls)
+    return {"profile_case": case, "label": label, "calls": calls, "nnz": m.nnz,
+            "plan": _kind(info), "compulsory_bytes": nbytes, "flops": nflops,
+            "events_us_per_call": round(t_ms * 1e3, 2)}
 
 
 def main() -> int:
@@ -418,6 +541,7 @@ def main() -> int:
     ap.add_argument("--no-spmm", action="store_true", help="skip the SpMM leg")
     ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg")
     ap.add_argument("--no-cg", action="store_true", help="skip the conjugate gradient leg")
+    ap.add_argument("--no-krylov", action="store_true", help="skip the BiCGSTAB / MINRES leg")
     ap.add_argument("--mtx", default=None,
                     help="also time SpMV on a Matrix Market file (e.g. a SuiteSparse matrix)")
     ap.add_argument("--no-configs", action="store_true",
@@ -425,6 +549,9 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 1 GiB once (a kernel of known traffic for counter scaling)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "spmv_random16_traffic.txt"))
+    ap.add_argument("--profile-case", default=None, choices=sorted(CASES),
+                    help="run only this configuration (calls back to back, for rocprofv3)")
+    ap.add_argument("--calls", type=int, default=10, help="calls of --profile-case")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -442,6 +569,9 @@ def main() -> int:
     ext = extension()
     ms.use_gpu(0)
     dev = torch.device("cuda", 0)
+    if args.profile_case:
+        print(json.dumps(profile_case(ext, dev, args.profile_case, args.calls)), flush=True)
+        return 0
     if args.calibrate:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -624,7 +754,7 @@ def main() -> int:
     # ---- every benchmark configuration -------------------------------------------------
     if not args.no_configs:
         head = {"case": "cfg2 random16 n=2^22 f32/i32 (headline)", "nnz": m.nnz, "op": "spmv",
-                "plan": plan_kind, "plan_bytes": info["plan_bytes"],
+                "id": "cfg2", "plan": plan_kind, "plan_bytes": info["plan_bytes"],
                 "block_nnz": info["block_nnz"], "window_rows": info["window_rows"],
                 "long_rows": info["n_long_rows"], "compulsory_bytes": nbytes, "flops": nflops,
                 "kernel_us": round(kern_ms * 1e3, 2), "gbs": round(achieved, 1),
@@ -638,6 +768,11 @@ def main() -> int:
     # ---- conjugate gradients on the Poisson matrix --------------------------------
     if not args.no_cg:
         result["cg"] = cg_leg(dev)
+        torch.cuda.empty_cache()
+
+    # ---- BiCGSTAB and MINRES at the same size -----------------------------------------
+    if not args.no_krylov:
+        result["krylov"] = krylov_leg(dev)
         torch.cuda.empty_cache()
 
     # ---- CPU baseline (reference CPU kernel restated in C) -------------------------

@@ -517,6 +517,50 @@ msx_status msx_csr_pcg_jacobi(msx_itype it, int64_t n, int64_t nnz,
                               msx_solver_result *result, void *stream);
 
 /*
+ * BiCGSTAB for a square float32 CSR matrix (n x n, not necessarily
+ * symmetric): x from x0 (device pointers; x0 and x may not overlap).  Runs
+ * on the device like msx_csr_cg: per iteration two SpMVs of the path with
+ * `plan` (nullable) and fused vector passes; the scalars stay on the device
+ * and the host reads the solver state between batches of iterations and
+ * when a residual estimate falls under the tolerance (the reference then
+ * confirms it on the true residual b - A x, computed here on the device).
+ * `stream` is synchronised; scratch comes from its stream-ordered
+ * allocator.  Status and residual as msx_solver_result describes
+ * (-1: near-zero rho, alpha denominator or omega).
+ *
+ * Replaces CSRBiCGSTAB::eval_gpu (reference:
+ * src/linalg/bicgstab/bicgstab.cpp:388-436, the single-threadgroup kernel
+ * of bicgstab.metal:54-320) with the arithmetic of csr_bicgstab_cpu_impl
+ * (bicgstab.cpp:80-362).
+ */
+msx_status msx_csr_bicgstab(msx_itype it, int64_t n, int64_t nnz,
+                            const float *data, const void *indices,
+                            const void *indptr, const float *b, const float *x0,
+                            float *x, float rtol, float atol, int64_t maxiter,
+                            const msx_csr_plan *plan, msx_solver_result *result,
+                            void *stream);
+
+/*
+ * MINRES for (A - shift I) x = b with A square symmetric (possibly
+ * indefinite) float32 CSR: x from x0 (device pointers).  Per iteration two
+ * SpMVs (A v for the Lanczos step, A x for the true residual the reference
+ * tests every iteration) and fused vector passes; the Givens recurrences
+ * run redundantly in every workgroup from the same sums.  `stream` is
+ * synchronised; scratch from its stream-ordered allocator.  residual: the
+ * true residual ||b - (A - shift I) x||.
+ *
+ * Replaces CSRMINRES::eval_gpu (reference: src/linalg/minres/minres.cpp,
+ * the single-threadgroup kernels of minres.metal:71-140) with the
+ * arithmetic of csr_minres_cpu_impl (minres.cpp:93-312).
+ */
+msx_status msx_csr_minres(msx_itype it, int64_t n, int64_t nnz,
+                          const float *data, const void *indices,
+                          const void *indptr, const float *b, const float *x0,
+                          float *x, float rtol, float atol, int64_t maxiter,
+                          float shift, const msx_csr_plan *plan,
+                          msx_solver_result *result, void *stream);
+
+/*
  * Host (CPU) solvers, host pointers: the reference's sequential loops
  * (csr_cg_cpu_impl, cg.cpp:75-246; csr_pcg_jacobi_cpu_impl,
  * pcg.cpp:71-236), one thread.
@@ -532,6 +576,20 @@ msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
                                   const float *x0, const float *inv_diag,
                                   float *x, float rtol, float atol,
                                   int64_t maxiter, msx_solver_result *result);
+/* csr_bicgstab_cpu_impl (bicgstab.cpp:80-362) and csr_minres_cpu_impl
+ * (minres.cpp:93-312), one thread. */
+msx_status msx_csr_bicgstab_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                const float *data, const void *indices,
+                                const void *indptr, const float *b,
+                                const float *x0, float *x, float rtol,
+                                float atol, int64_t maxiter,
+                                msx_solver_result *result);
+msx_status msx_csr_minres_cpu(msx_itype it, int64_t n, int64_t nnz,
+                              const float *data, const void *indices,
+                              const void *indptr, const float *b,
+                              const float *x0, float *x, float rtol,
+                              float atol, int64_t maxiter, float shift,
+                              msx_solver_result *result);
 
 /*
  * Matrix Market files (the text format of the SuiteSparse collection).

@@ -85,7 +85,7 @@ def build(verbose: bool = True) -> Path:
                  SRC / "sparse" / "csr_batched_matvec" / "csr_batched_matvec.cpp",
                  SRC / "sparse" / "csr_batched_matmul" / "csr_batched_matmul.cpp",
                  SRC / "sparse" / "csr_adjoint" / "csr_adjoint.cpp",
-                 SRC / "linalg" / "csr_cg.cpp"]
+                 SRC / "linalg" / "csr_cg.cpp", SRC / "linalg" / "csr_krylov.cpp"]
     bind_objs = []
     for s in bind_srcs:
         o = BUILD / ("bind_" + s.stem + ".o")

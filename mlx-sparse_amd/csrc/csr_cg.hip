@@ -33,15 +33,13 @@
 
 #include "msx_device.h"
 #include "msx_internal.h"
+#include "msx_solver.h"
 #include "msx_sparse.h"
 
 namespace msx {
 namespace {
 
-constexpr int kCgThreads = 512;
-constexpr int kCgMaxBlocks = 512;  // two workgroups per CU at most (partials re-read by each)
-constexpr int kSlots = 4;          // partial sums per pass (slot 3 counts non-finite values)
-constexpr int kUnroll = 4;         // independent loads in flight per thread
+using namespace solver;  // slot 3 of every pass counts non-finite values
 
 struct CgState {
   double rr;       // CG: r.r of the current residual; PCG: rho = r.z (a float)
@@ -53,97 +51,22 @@ struct CgState {
   int32_t running;    // 1 while iterating
 };
 
-__device__ inline bool fin(float v) { return isfinite(v); }
-__device__ inline bool fin(double v) { return isfinite(v); }
-
-__device__ inline double wave_sum(double v) {
-  // butterfly: every lane ends with the same value (each level adds a
-  // commutative pair)
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
-// Workgroup sums of v[] -> part[k * kCgMaxBlocks + blockIdx.x].
-__device__ void write_partials(double (&v)[kSlots], double *part) {
-  __shared__ double sh[kSlots][kCgThreads / kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  for (int k = 0; k < kSlots; ++k) {
-    const double w = wave_sum(v[k]);
-    if (lane == 0) sh[k][wave] = w;
-  }
-  __syncthreads();
-  if (threadIdx.x < kSlots) {
-    double s = 0.0;
-    for (int w = 0; w < kCgThreads / kWave; ++w) s += sh[threadIdx.x][w];
-    part[threadIdx.x * kCgMaxBlocks + blockIdx.x] = s;
-  }
-}
-
-// Totals of the previous pass's `nparts` partials, the same bits in every
-// workgroup (fixed order, written by an earlier kernel).
-__device__ void read_totals(const double *part, int nparts, double (&t)[kSlots]) {
-  __shared__ double sh[kSlots][kCgThreads / kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  // all kSlots loads first (clamped index, no branch), then the sums
-  const bool mine = static_cast<int>(threadIdx.x) < nparts;
-  const int idx = mine ? static_cast<int>(threadIdx.x) : 0;
-  double v[kSlots];
-#pragma unroll
-  for (int k = 0; k < kSlots; ++k) v[k] = part[k * kCgMaxBlocks + idx];
-#pragma unroll
-  for (int k = 0; k < kSlots; ++k) {
-    const double w = wave_sum(mine ? v[k] : 0.0);
-    if (lane == 0) sh[k][wave] = w;
-  }
-  __syncthreads();
-  for (int k = 0; k < kSlots; ++k) {
-    double s = 0.0;
-    for (int w = 0; w < kCgThreads / kWave; ++w) s += sh[k][w];
-    t[k] = s;
-  }
-  __syncthreads();
-}
-
 __device__ inline void stop(CgState *st, int32_t status, int32_t completed) {
   st->status = status;
   st->completed = completed;
   st->running = 0;
 }
 
-// Grid-stride over [0, n) with kUnroll coalesced elements per round.
-// A thread whose kUnroll elements all lie below n runs them without a
-// per-element test, so the compiler issues all of their loads before the
-// first use (a test per element made it wait for each load in turn); the
-// last, partial group tests each element.
-#define MSX_CG_LOOP(...)                                                                    \
-  {                                                                                          \
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;                     \
-    for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n; \
-         base += kUnroll * stride) {                                                         \
-      if (base + (kUnroll - 1) * stride < n) {                                               \
-        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
-          const int64_t i = base + u * stride;                                               \
-          __VA_ARGS__                                                                        \
-        }                                                                                    \
-      } else {                                                                               \
-        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
-          const int64_t i = base + u * stride;                                               \
-          if (i < n) { __VA_ARGS__ }                                                         \
-        }                                                                                    \
-      }                                                                                      \
-    }                                                                                        \
-  }
-
 // ---------------------------------------------------------------------------
 // Plain CG (cg.cpp:75-246).  Passes: start -> [SpMV, alpha, update,
 // direction] x it -> finish.  alpha consumes the previous direction pass,
 // update the alpha pass, direction the update pass.
 
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_start(const float *__restrict__ b, const float *__restrict__ x, const float *__restrict__ ap,
              float *__restrict__ r, float *__restrict__ p, int64_t n, double *part) {
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
+  MSX_SOLVER_LOOP({
     const float ri = b[i] - ap[i];
     r[i] = ri;
     p[i] = ri;
@@ -155,15 +78,15 @@ __global__ void __launch_bounds__(kCgThreads)
 }
 
 // One workgroup: the start decision (cg.cpp:122-145).
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_decide_start(const double *part, int nparts, float rtol, float atol, int64_t maxiter,
                     CgState *st) {
   double t[kSlots];
   read_totals(part, nparts, t);
   if (threadIdx.x != 0) return;
   const double rr = t[1];
-  const float residual_norm = static_cast<float>(sqrt(fmax(rr, 0.0)));
-  const float b_norm = static_cast<float>(sqrt(fmax(t[0], 0.0)));
+  const float residual_norm = static_cast<float>(sqrt(max0(rr)));
+  const float b_norm = static_cast<float>(sqrt(max0(t[0])));
   const float scaled = rtol * b_norm;
   st->tol = atol > scaled ? atol : scaled;
   st->rr = rr;
@@ -183,7 +106,7 @@ __global__ void __launch_bounds__(kCgThreads)
 // p.ap, p.p, ap.ap, non-finite p/ap.  From the second iteration on, first
 // checks the previous direction pass (any non-finite p stops with -3) and
 // commits the residual norm it left.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_alpha(const float *__restrict__ p, const float *__restrict__ ap, int64_t n, int32_t it,
              const double *dir_part, double *part, int nparts, CgState *st) {
   if (!st->running) return;
@@ -197,7 +120,7 @@ __global__ void __launch_bounds__(kCgThreads)
     if (blockIdx.x == 0 && threadIdx.x == 0) st->rr = st->rr_next;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
+  MSX_SOLVER_LOOP({
     const double pd = p[i], ad = ap[i];
     v[0] += pd * ad;
     v[1] += pd * pd;
@@ -209,7 +132,7 @@ __global__ void __launch_bounds__(kCgThreads)
 
 // alpha from the alpha pass (cg.cpp:158-199), then x += alpha p and
 // r -= alpha ap in double, rounded once; r.r and non-finite counts.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_update(float *__restrict__ x, float *__restrict__ r, const float *__restrict__ p,
               const float *__restrict__ ap, int64_t n, int32_t it, const double *alpha_part,
               double *part, int nparts, CgState *st) {
@@ -223,7 +146,7 @@ __global__ void __launch_bounds__(kCgThreads)
   if (t[3] != 0.0 || !fin(denom)) {
     verdict = -3;
   } else if (fabs(denom) <= eps) {
-    const double scale = sqrt(fmax(t[1] * t[2], 0.0));
+    const double scale = sqrt(max0(t[1] * t[2]));
     const double dtol = fmin(eps, eps * eps * fmax(1.0, scale));
     if (!fin(scale)) verdict = -3;
     else if (fabs(denom) <= dtol) verdict = -1;
@@ -238,8 +161,8 @@ __global__ void __launch_bounds__(kCgThreads)
   // All loads of a thread's kUnroll elements first (an index past n reads
   // element `base` instead), then the arithmetic and the stores: written as
   // one loop body, the compiler waited for each element's loads in turn.
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
        base += kUnroll * stride) {
     float xo[kUnroll], ro[kUnroll], pv[kUnroll], av[kUnroll];
 #pragma unroll
@@ -271,7 +194,7 @@ __global__ void __launch_bounds__(kCgThreads)
 
 // Convergence and beta from the update pass (cg.cpp:200-238), then
 // p = r + beta p; non-finite p values are counted for the next alpha pass.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_direction(const float *__restrict__ r, float *__restrict__ p, int64_t n, int32_t it,
                  const double *upd_part, double *part, int nparts, CgState *st) {
   if (!st->running) return;
@@ -279,7 +202,7 @@ __global__ void __launch_bounds__(kCgThreads)
   read_totals(upd_part, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const double rr_new = t[0];
-  const float r_norm = static_cast<float>(sqrt(fmax(rr_new, 0.0)));
+  const float r_norm = static_cast<float>(sqrt(max0(rr_new)));
   if (t[3] != 0.0 || !fin(rr_new) || !fin(r_norm)) {
     if (lead) stop(st, -3, it);
     return;
@@ -298,8 +221,8 @@ __global__ void __launch_bounds__(kCgThreads)
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
   // loads first, then arithmetic and stores, as in cg_update
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
        base += kUnroll * stride) {
     float rv[kUnroll], pv[kUnroll];
 #pragma unroll
@@ -327,7 +250,7 @@ __global__ void __launch_bounds__(kCgThreads)
 
 // One workgroup, after the last launched iteration: settles the check the
 // final direction pass left open.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     cg_finish(const double *dir_part, int nparts, CgState *st) {
   if (!st->running) return;
   double t[kSlots];
@@ -347,12 +270,12 @@ __global__ void __launch_bounds__(kCgThreads)
 
 __device__ inline float to_f(double v) { return static_cast<float>(v); }
 
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     pcg_start(const float *__restrict__ b, const float *__restrict__ ap,
               const float *__restrict__ inv_diag, float *__restrict__ r, float *__restrict__ z,
               float *__restrict__ p, int64_t n, double *part) {
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
+  MSX_SOLVER_LOOP({
     const float ri = b[i] - ap[i];
     const float zi = inv_diag[i] * ri;
     r[i] = ri;
@@ -366,20 +289,20 @@ __global__ void __launch_bounds__(kCgThreads)
   write_partials(v, part);
 }
 
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     pcg_decide_start(const double *part, int nparts, float rtol, float atol, int64_t maxiter,
                      CgState *st) {
   double t[kSlots];
   read_totals(part, nparts, t);
   if (threadIdx.x != 0) return;
   const float true_rr = to_f(t[1]), rho = to_f(t[2]);
-  const float b_norm = static_cast<float>(sqrt(fmax(t[0], 0.0)));
+  const float b_norm = static_cast<float>(sqrt(max0(t[0])));
   const float scaled = rtol * b_norm;
   st->tol = atol > scaled ? atol : scaled;
   st->true_rr = true_rr;
   st->rr = rho;
   st->rr_next = rho;
-  const float true_residual = sqrtf(fmaxf(true_rr, 0.0f));
+  const float true_residual = sqrtf(max0(true_rr));
   if (t[3] != 0.0 || !fin(true_rr) || !fin(rho)) {
     stop(st, -3, 0);
   } else if (true_residual <= st->tol) {
@@ -393,13 +316,13 @@ __global__ void __launch_bounds__(kCgThreads)
   }
 }
 
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     pcg_alpha(const float *__restrict__ p, const float *__restrict__ ap, int64_t n, int32_t it,
               double *part, CgState *st) {
   if (!st->running) return;
   if (it > 1 && blockIdx.x == 0 && threadIdx.x == 0) st->rr = st->rr_next;
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_CG_LOOP({
+  MSX_SOLVER_LOOP({
     const double pd = p[i], ad = ap[i];
     v[0] += pd * ad;
     v[1] += pd * pd;
@@ -410,7 +333,7 @@ __global__ void __launch_bounds__(kCgThreads)
 
 // alpha (pcg.cpp:165-184), then x += alpha p; r -= alpha ap; z = inv_diag r;
 // r.r and r.z.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     pcg_update(float *__restrict__ x, float *__restrict__ r, float *__restrict__ z,
                const float *__restrict__ p, const float *__restrict__ ap,
                const float *__restrict__ inv_diag, int64_t n, int32_t it,
@@ -421,7 +344,7 @@ __global__ void __launch_bounds__(kCgThreads)
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const float eps = FLT_EPSILON;
   const float denom = to_f(t[0]), p2 = to_f(t[1]), ap2 = to_f(t[2]);
-  const float scale = sqrtf(fmaxf(p2 * ap2, 0.0f));
+  const float scale = sqrtf(max0(p2 * ap2));
   const float dtol = eps * fmaxf(1.0f, scale);
   if (!fin(denom) || !fin(scale) || fabsf(denom) <= dtol) {
     if (lead) stop(st, -1, it - 1);
@@ -434,8 +357,8 @@ __global__ void __launch_bounds__(kCgThreads)
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
   // loads first, then arithmetic and stores, as in cg_update
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
        base += kUnroll * stride) {
     float xo[kUnroll], po[kUnroll], ro[kUnroll], ao[kUnroll], dv[kUnroll];
 #pragma unroll
@@ -466,7 +389,7 @@ __global__ void __launch_bounds__(kCgThreads)
 }
 
 // Convergence, rho and beta (pcg.cpp:186-232), then p = z + beta p.
-__global__ void __launch_bounds__(kCgThreads)
+__global__ void __launch_bounds__(kSolverThreads)
     pcg_direction(const float *__restrict__ z, float *__restrict__ p, int64_t n, int32_t it,
                   const double *upd_part, int nparts, CgState *st) {
   if (!st->running) return;
@@ -474,7 +397,7 @@ __global__ void __launch_bounds__(kCgThreads)
   read_totals(upd_part, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const float true_rr = to_f(t[0]);
-  const float r_norm = sqrtf(fmaxf(true_rr, 0.0f));
+  const float r_norm = sqrtf(max0(true_rr));
   int32_t verdict = 1;
   if (t[3] != 0.0 || !fin(true_rr) || !fin(r_norm)) verdict = -3;
   else if (r_norm <= st->tol) verdict = 0;
@@ -490,8 +413,8 @@ __global__ void __launch_bounds__(kCgThreads)
     if (lead) stop(st, verdict, it);
     return;
   }
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCgThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; base < n;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
        base += kUnroll * stride) {  // loads first, as in cg_update
     float zv[kUnroll], pv[kUnroll];
 #pragma unroll
@@ -514,11 +437,10 @@ __global__ void pcg_finish(CgState *st) {
   if (threadIdx.x == 0 && st->running) st->running = 0;
 }
 
-#undef MSX_CG_LOOP
 
 __global__ void copy_vec(const float *__restrict__ src, float *__restrict__ dst, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kCgThreads + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * kCgThreads)
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kSolverThreads)
     dst[i] = src[i];
 }
 
@@ -585,7 +507,7 @@ msx_status solve(const Solve &s, const float *b, const float *x0, const float *i
   const int64_t n = s.n;
   const size_t vec = (static_cast<size_t>(n) * sizeof(float) + 255) / 256 * 256;
   const size_t state_bytes = 256;
-  const size_t part_bytes = sizeof(double) * kSlots * kCgMaxBlocks;
+  const size_t part_bytes = sizeof(double) * kSlots * kSolverMaxBlocks;
   const int nvec = pcg ? 4 : 3;  // r, p, ap (+ z)
   Scratch sc;
   sc.stream = s.stream;
@@ -602,7 +524,7 @@ msx_status solve(const Solve &s, const float *b, const float *x0, const float *i
   auto *dir_part = reinterpret_cast<double *>(sc.base + nvec * vec + state_bytes + 2 * part_bytes);
   const int nparts = static_cast<int>(s.blocks);
   CgState host{};
-  const dim3 grid(s.blocks), block(kCgThreads);
+  const dim3 grid(s.blocks), block(kSolverThreads);
 
   hipLaunchKernelGGL(copy_vec, grid, block, 0, s.stream, x0, x, n);
   MSX_HIP_TRY(hipGetLastError());
@@ -668,11 +590,6 @@ msx_status check(const char *op, msx_itype it, int64_t n, int64_t nnz, const voi
   return MSX_OK;
 }
 
-uint32_t blocks_for(int64_t n) {
-  const int64_t per_block = static_cast<int64_t>(kUnroll) * kCgThreads;
-  return static_cast<uint32_t>(
-      std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kCgMaxBlocks)));
-}
 
 }  // namespace
 }  // namespace msx

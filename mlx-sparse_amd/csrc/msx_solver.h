@@ -1,0 +1,112 @@
+// msx_solver.h - device-side building blocks of the Krylov solver loops
+// (csr_cg.hip, csr_krylov.hip): workgroup sizes, the reproducible
+// partial-sum protocol and the grid-stride loop with loads in flight.
+//
+// Sums: each workgroup reduces its grid-stride share in double and writes
+// one partial per slot; every workgroup of the NEXT pass adds those
+// partials in workgroup order, so all workgroups see the same bits and
+// take the same scalar decisions, and no workgroup waits on another inside
+// a kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "msx_device.h"
+
+namespace msx {
+namespace solver {
+
+constexpr int kSolverThreads = 512;
+constexpr int kSolverMaxBlocks = 512;  // two workgroups per CU at most (partials re-read by each)
+constexpr int kSlots = 4;              // partial sums per pass
+constexpr int kUnroll = 4;             // independent loads in flight per thread
+
+__device__ inline bool fin(float v) { return isfinite(v); }
+__device__ inline bool fin(double v) { return isfinite(v); }
+
+// std::max(v, 0) of the reference loops: a NaN stays NaN (fmax would drop it).
+__device__ inline double max0(double v) { return v < 0.0 ? 0.0 : v; }
+__device__ inline float max0(float v) { return v < 0.0f ? 0.0f : v; }
+
+__device__ inline double wave_sum(double v) {
+  // butterfly: every lane ends with the same value (each level adds a
+  // commutative pair)
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Workgroup sums of v[] -> part[k * kSolverMaxBlocks + blockIdx.x].
+__device__ inline void write_partials(double (&v)[kSlots], double *part) {
+  __shared__ double sh[kSlots][kSolverThreads / kWave];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int k = 0; k < kSlots; ++k) {
+    const double w = wave_sum(v[k]);
+    if (lane == 0) sh[k][wave] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x < kSlots) {
+    double s = 0.0;
+    for (int w = 0; w < kSolverThreads / kWave; ++w) s += sh[threadIdx.x][w];
+    part[threadIdx.x * kSolverMaxBlocks + blockIdx.x] = s;
+  }
+}
+
+// Totals of the previous pass's `nparts` partials, the same bits in every
+// workgroup (fixed order, written by an earlier kernel).
+__device__ inline void read_totals(const double *part, int nparts, double (&t)[kSlots]) {
+  __shared__ double sh[kSlots][kSolverThreads / kWave];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  // all kSlots loads first (clamped index, no branch), then the sums
+  const bool mine = static_cast<int>(threadIdx.x) < nparts;
+  const int idx = mine ? static_cast<int>(threadIdx.x) : 0;
+  double v[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) v[k] = part[k * kSolverMaxBlocks + idx];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) {
+    const double w = wave_sum(mine ? v[k] : 0.0);
+    if (lane == 0) sh[k][wave] = w;
+  }
+  __syncthreads();
+  for (int k = 0; k < kSlots; ++k) {
+    double s = 0.0;
+    for (int w = 0; w < kSolverThreads / kWave; ++w) s += sh[k][w];
+    t[k] = s;
+  }
+  __syncthreads();
+}
+
+// Grid-stride over [0, n) with kUnroll coalesced elements per round.
+// A thread whose kUnroll elements all lie below n runs them without a
+// per-element test, so the compiler issues all of their loads before the
+// first use (a test per element made it wait for each load in turn); the
+// last, partial group tests each element.
+#define MSX_SOLVER_LOOP(...)                                                                    \
+  {                                                                                          \
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;                     \
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n; \
+         base += kUnroll * stride) {                                                         \
+      if (base + (kUnroll - 1) * stride < n) {                                               \
+        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
+          const int64_t i = base + u * stride;                                               \
+          __VA_ARGS__                                                                        \
+        }                                                                                    \
+      } else {                                                                               \
+        _Pragma("unroll") for (int u = 0; u < kUnroll; ++u) {                                \
+          const int64_t i = base + u * stride;                                               \
+          if (i < n) { __VA_ARGS__ }                                                         \
+        }                                                                                    \
+      }                                                                                      \
+    }                                                                                        \
+  }
+
+// Workgroups of a solver pass over n elements (kUnroll per thread and round).
+inline uint32_t blocks_for(int64_t n) {
+  const int64_t per_block = static_cast<int64_t>(kUnroll) * kSolverThreads;
+  const int64_t blocks = (n + per_block - 1) / per_block;
+  return static_cast<uint32_t>(blocks < 1 ? 1 : (blocks > kSolverMaxBlocks ? kSolverMaxBlocks : blocks));
+}
+
+}  // namespace solver
+}  // namespace msx

@@ -86,6 +86,21 @@ def csr_pcg_jacobi(data, indices, indptr, b, x0, inv_diag, shape: Shape2D, *, rt
                                       rtol, atol, maxiter, plan=plan)
 
 
+def csr_bicgstab(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
+                 maxiter: int, plan=None):
+    """(x, info, residual, iterations) (reference: mlx_sparse/_native.py csr_bicgstab)."""
+    return extension().csr_bicgstab(data, indices, indptr, b, x0, shape[0], shape[1], rtol, atol,
+                                    maxiter, plan=plan)
+
+
+def csr_minres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
+               maxiter: int, shift: float = 0.0, plan=None):
+    """(x, info, residual, iterations) of (A - shift I) x = b (reference:
+    mlx_sparse/_native.py csr_minres)."""
+    return extension().csr_minres(data, indices, indptr, b, x0, shape[0], shape[1], rtol, atol,
+                                  maxiter, shift, plan=plan)
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

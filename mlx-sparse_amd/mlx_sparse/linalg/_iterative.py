@@ -1,9 +1,12 @@
-"""Conjugate gradients (reference: mlx_sparse/linalg/_iterative.py:69-323 ``cg``;
-native loops src/linalg/cg/cg.cpp, src/preconditioners/pcg/pcg.cpp).
+"""Krylov solvers on the path's SpMV (reference: mlx_sparse/linalg/_iterative.py:
+69-323 ``cg``, :328-640 ``bicgstab``, :993-1145 ``minres``; native loops
+src/linalg/cg/cg.cpp, src/preconditioners/pcg/pcg.cpp,
+src/linalg/bicgstab/bicgstab.cpp, src/linalg/minres/minres.cpp).
 
-On the GPU the whole loop runs on the device (``msx_csr_cg``): the path's SpMV
-with the matrix's cached plan, fused vector passes, scalars on the device.
-With ``use_cpu()`` the reference's sequential loop runs natively.
+On the GPU each loop runs on the device (``msx_csr_cg``, ``msx_csr_bicgstab``,
+``msx_csr_minres``): the path's SpMV with the matrix's cached plan, fused
+vector passes, scalars on the device.  With ``use_cpu()`` the reference's
+sequential loops run natively.
 """
 
 from __future__ import annotations
@@ -18,14 +21,14 @@ from mlx_sparse.linalg import preconditioners as _pc
 from mlx_sparse.linalg._info import finish
 
 
-def _float32_csr(A) -> CSRArray:
+def _float32_csr(A, solver: str = "cg") -> CSRArray:
     if not isinstance(A, CSRArray):
         if isinstance(A, torch.Tensor):
             raise TypeError("sparse iterative solvers expect a CSRArray; use torch.linalg for "
                             "dense arrays.")
         raise TypeError(f"sparse iterative solvers expect a CSRArray, got {type(A).__name__}.")
     if A.shape[0] != A.shape[1]:
-        raise ValueError(f"cg requires a square matrix, got {A.shape}.")
+        raise ValueError(f"{solver} requires a square matrix, got {A.shape}.")
     if A.dtype != torch.float32:
         if A.dtype.is_complex:
             raise TypeError("sparse iterative solvers currently use float32 values.")
@@ -91,5 +94,116 @@ def cg(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, maxiter: int | N
             data, indices, indptr, rhs, guess, inv_diag, csr.shape, rtol=float(rtol),
             atol=float(atol), maxiter=maxiter_value, plan=plan)
     return finish(x, info, residual, iterations, solver="cg", return_info=bool(return_info),
+                  callback=callback, rtol=float(rtol), atol=float(atol), maxiter=maxiter_value,
+                  preconditioner=kind)
+
+
+def _finite_scalar(name: str, value) -> float:
+    scalar = float(value)
+    if scalar != scalar or scalar in (float("inf"), float("-inf")):
+        raise ValueError(f"{name} must be finite.")
+    return scalar
+
+
+def _normalize_tolerances(rtol, tol, atol) -> tuple[float, float]:
+    """SciPy's ``tol`` alias of ``rtol`` (reference:
+    mlx_sparse/linalg/_iterative.py:46-66)."""
+    if rtol is None and tol is None:
+        rtol_value = 1e-5
+    elif rtol is None:
+        rtol_value = _finite_scalar("tol", tol)
+    else:
+        rtol_value = _finite_scalar("rtol", rtol)
+        if tol is not None and _finite_scalar("tol", tol) != rtol_value:
+            raise ValueError("tol is a compatibility alias for rtol; do not set both.")
+    atol_value = _finite_scalar("atol", atol)
+    if rtol_value < 0.0:
+        raise ValueError("rtol must be non-negative.")
+    if atol_value < 0.0:
+        raise ValueError("atol must be non-negative.")
+    return float(rtol_value), float(atol_value)
+
+
+def _system(A, b, x0, maxiter, solver: str):
+    """(csr, rhs, guess, maxiter, device) of a square float32 system."""
+    csr = _float32_csr(A, solver)
+    device = default_torch_device()
+    rhs = _float32_vector(b, device)
+    if rhs.ndim != 1:
+        raise ValueError(f"right-hand side must be rank-1, got {tuple(rhs.shape)}.")
+    if rhs.shape[0] != csr.shape[0]:
+        raise ValueError(f"b has length {rhs.shape[0]}, expected {csr.shape[0]}.")
+    if x0 is None:
+        guess = torch.zeros(csr.shape[1], dtype=torch.float32, device=device)
+    else:
+        guess = _float32_vector(x0, device)
+        if guess.ndim != 1 or guess.shape[0] != csr.shape[1]:
+            raise ValueError(f"x0 must have shape ({csr.shape[1]},), got {tuple(guess.shape)}.")
+    maxiter_value = 10 * csr.shape[1] if maxiter is None else int(maxiter)
+    if maxiter_value < 0:
+        raise ValueError("maxiter must be non-negative.")
+    return csr, rhs, guess, maxiter_value, device
+
+
+def _plain_preconditioner(M, csr, solver: str):
+    """The preconditioner kind when ``M`` is None or the identity; other
+    kinds raise (this build runs BiCGSTAB and MINRES unpreconditioned)."""
+    if M is None:
+        return None
+    pc = _pc.aspreconditioner(M, csr)
+    if isinstance(pc, _pc.IdentityPreconditioner):
+        return pc.kind
+    raise TypeError(f"{solver} in this build supports only the identity preconditioner "
+                    f"(M=None or preconditioners.identity); got {pc.kind}.")
+
+
+def bicgstab(A, b, x0=None, *, rtol: float | None = None, atol: float = 0.0,
+             tol: float | None = None, maxiter: int | None = None, M=None, callback=None,
+             return_info: bool = False):
+    """Solve a square (non-symmetric) sparse system ``A @ x = b`` with
+    BiCGSTAB (reference: mlx_sparse/linalg/_iterative.py:328-640).
+
+    Two SpMVs per iteration; convergence is confirmed on the true residual
+    ``||b - A @ x|| <= max(rtol * ||b||, atol)``.  ``rtol`` defaults to
+    ``1e-5``; ``tol`` is SciPy's alias for it (both may be given only when
+    equal).  ``maxiter`` defaults to ``10 * n``.
+
+    Returns ``(x, info)``: ``info`` 0 converged, > 0 the iteration budget
+    ran out, -1 breakdown (near-zero ``rho``, ``alpha`` denominator or
+    ``omega``), -3 non-finite values.  With ``return_info=True`` a
+    :class:`SolverInfo` replaces the integer.
+    """
+    rtol_value, atol_value = _normalize_tolerances(rtol, tol, atol)
+    csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "bicgstab")
+    kind = _plain_preconditioner(M, csr, "bicgstab")
+    data, indices, indptr = csr.buffers(device)
+    x, info, residual, iterations = _native.csr_bicgstab(
+        data, indices, indptr, rhs, guess, csr.shape, rtol=rtol_value, atol=atol_value,
+        maxiter=maxiter_value, plan=csr.plan(device))
+    return finish(x, info, residual, iterations, solver="bicgstab", return_info=bool(return_info),
+                  callback=callback, rtol=rtol_value, atol=atol_value, maxiter=maxiter_value,
+                  preconditioner=kind)
+
+
+def minres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, shift: float = 0.0,
+           maxiter: int | None = None, M=None, check_preconditioner: bool = True,
+           callback=None, return_info: bool = False):
+    """Solve a symmetric (possibly indefinite) sparse system
+    ``(A - shift * I) @ x = b`` with MINRES (reference:
+    mlx_sparse/linalg/_iterative.py:993-1145; SciPy's ``shift`` convention).
+
+    Two SpMVs per iteration (the Lanczos step and the true residual the
+    reference tests every iteration).  Stops when
+    ``||b - (A - shift I) x|| <= max(rtol * ||b||, atol)``.  ``maxiter``
+    defaults to ``10 * n``.  Returns ``(x, info)`` as :func:`bicgstab` does.
+    """
+    csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "minres")
+    shift_value = _finite_scalar("shift", shift)
+    kind = _plain_preconditioner(M, csr, "minres")
+    data, indices, indptr = csr.buffers(device)
+    x, info, residual, iterations = _native.csr_minres(
+        data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
+        maxiter=maxiter_value, shift=shift_value, plan=csr.plan(device))
+    return finish(x, info, residual, iterations, solver="minres", return_info=bool(return_info),
                   callback=callback, rtol=float(rtol), atol=float(atol), maxiter=maxiter_value,
                   preconditioner=kind)

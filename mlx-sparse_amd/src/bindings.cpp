@@ -25,6 +25,7 @@
 #include "common/validate.h"
 #include "msx_sparse.h"
 #include "linalg/csr_cg.h"
+#include "linalg/csr_krylov.h"
 #include "sparse/csr_adjoint/csr_adjoint.h"
 #include "sparse/csr_batched_matmul/csr_batched_matmul.h"
 #include "sparse/csr_batched_matvec/csr_batched_matvec.h"
@@ -464,6 +465,31 @@ py::tuple solve_cg(py::handle data_o, py::handle indices_o, py::handle indptr_o,
   return py::make_tuple(x, res.info, res.residual, res.iterations);
 }
 
+py::tuple solve_krylov(msx::Krylov kind, py::handle data_o, py::handle indices_o,
+                       py::handle indptr_o, py::handle b_o, py::handle x0_o, int64_t n_rows,
+                       int64_t n_cols, float rtol, float atol, int64_t maxiter, float shift,
+                       py::object plan) {
+  py::object data = contiguous(data_o), indices = contiguous(indices_o),
+             indptr = contiguous(indptr_o), b = contiguous(b_o), x0 = contiguous(x0_o);
+  const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vb = view_of(b),
+                  vx0 = view_of(x0);
+  if (vb.ndim != 1)
+    msx::require_rank(vb, 1, kind == msx::Krylov::BiCGSTAB ? "csr_bicgstab b" : "csr_minres b");
+  py::object x = empty_like_out(vb, b, py::make_tuple(vb.shape[0]));
+  const ArrayView vx = view_of(x);
+  const msx::ExecContext ctx = context_for(vd, 0);
+  msx_solver_result res{};
+  if (vd.device >= 0) {
+    res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
+                          shift, plan_ptr(plan), ctx);
+  } else {
+    py::gil_scoped_release nogil;
+    res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
+                          shift, nullptr, ctx);
+  }
+  return py::make_tuple(x, res.info, res.residual, res.iterations);
+}
+
 py::dict mm_info(const std::string &path) {
   msx_mm_info info{};
   msx::check_status(msx_mm_info_read(path.c_str(), &info), "mmread");
@@ -674,6 +700,28 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
       py::arg("atol"), py::arg("maxiter"), py::arg("plan") = py::none(),
       "Jacobi-preconditioned conjugate gradients: (x, info, residual, iterations).");
+  m.def(
+      "csr_bicgstab",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         int64_t n_rows, int64_t n_cols, float rtol, float atol, int64_t maxiter, py::object plan) {
+        return solve_krylov(msx::Krylov::BiCGSTAB, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, 0.0f, plan);
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("maxiter"),
+      py::arg("plan") = py::none(), "BiCGSTAB: (x, info, residual, iterations).");
+  m.def(
+      "csr_minres",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         int64_t n_rows, int64_t n_cols, float rtol, float atol, int64_t maxiter, float shift,
+         py::object plan) {
+        return solve_krylov(msx::Krylov::MINRES, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, shift, plan);
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("maxiter"),
+      py::arg("shift") = 0.0f, py::arg("plan") = py::none(),
+      "MINRES on (A - shift I) x = b: (x, info, residual, iterations).");
   m.def("mm_info", &mm_info, py::arg("path"), "Header of a Matrix Market file.");
   m.def("mm_read_csr", &mm_read_csr, py::arg("path"), py::arg("dtype"), py::arg("index_dtype"),
         py::arg("n_threads") = 0,

@@ -29,7 +29,10 @@
  *     csr_cg_cpu_impl) with its float SpMV summed from zero
  *     (src/linalg/common/common.h:35-45, csr_spmv_float), and the
  *     Jacobi-preconditioned CG (src/preconditioners/pcg/pcg.cpp:71-236,
- *     csr_pcg_jacobi_cpu_impl), float32 values only.
+ *     csr_pcg_jacobi_cpu_impl), float32 values only;
+ *   - BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
+ *     and MINRES with its shift (src/linalg/minres/minres.cpp:68-312,
+ *     csr_minres_cpu_impl), float32.
  *
  * Built with -ffp-contract=off so every product and every sum is rounded on
  * its own, as the reference's separate multiply_accumulate / `+=` are.
@@ -662,6 +665,10 @@ static void cg_spmv(int it, int64_t n, const float *data, const void *indices, c
 
 static int fin(float v) { return isfinite(v); }
 
+/* std::max(v, 0) of the reference: a NaN stays NaN. */
+static double max0(double v) { return v < 0.0 ? 0.0 : v; }
+static float max0f(float v) { return v < 0.0f ? 0.0f : v; }
+
 /* Conjugate gradients: x from x0; info 0 converged, maxiter (or 1 when
  * maxiter is 0) when the budget ran out, -1 near-zero denominator, -3
  * non-finite.  residual = float(sqrt(r.r)), iterations = completed steps. */
@@ -688,8 +695,8 @@ int oracle_csr_cg(int it, int64_t n, const float *data, const void *indices, con
     rr += (double)r[i] * (double)r[i];
     finite = finite && fin(r[i]) && fin(p[i]) && fin(ap[i]) && fin(b[i]) && fin(x[i]);
   }
-  const float residual_norm = (float)sqrt(rr > 0.0 ? rr : 0.0);
-  const float b_norm = (float)sqrt(b_norm2 > 0.0 ? b_norm2 : 0.0);
+  const float residual_norm = (float)sqrt(max0(rr));
+  const float b_norm = (float)sqrt(max0(b_norm2));
   const float scaled = rtol * b_norm;
   const float tol = atol > scaled ? atol : scaled;
   const float eps = FLT_EPSILON;
@@ -728,7 +735,7 @@ int oracle_csr_cg(int it, int64_t n, const float *data, const void *indices, con
         ap2 += (double)ap[i] * (double)ap[i];
       }
       const double prod = p2 * ap2;
-      const double scale = sqrt(prod > 0.0 ? prod : 0.0);
+      const double scale = sqrt(max0(prod));
       const double grown = (double)eps * (double)eps * (scale > 1.0 ? scale : 1.0);
       const double dtol = (double)eps < grown ? (double)eps : grown;
       if (!isfinite(scale)) {
@@ -762,7 +769,7 @@ int oracle_csr_cg(int it, int64_t n, const float *data, const void *indices, con
       r[i] = rf;
       rr_new += (double)rf * (double)rf;
     }
-    const float r_norm = (float)sqrt(rr_new > 0.0 ? rr_new : 0.0);
+    const float r_norm = (float)sqrt(max0(rr_new));
     completed = (int32_t)k;
     if (!finite || !isfinite(rr_new) || !fin(r_norm)) {
       status = -3;
@@ -791,7 +798,7 @@ int oracle_csr_cg(int it, int64_t n, const float *data, const void *indices, con
     rr = rr_new;
   }
   *info = status;
-  *residual = (float)sqrt(rr > 0.0 ? rr : 0.0);
+  *residual = (float)sqrt(max0(rr));
   *iterations = completed;
 done:
   free(r);
@@ -837,10 +844,10 @@ int oracle_csr_pcg_jacobi(int it, int64_t n, const float *data, const void *indi
   }
   float true_rr = dot_f(r, r, n);
   float rho = dot_f(r, z, n);
-  const float b_norm = (float)sqrt(b_norm2 > 0.0 ? b_norm2 : 0.0);
+  const float b_norm = (float)sqrt(max0(b_norm2));
   const float scaled = rtol * b_norm;
   const float tol = atol > scaled ? atol : scaled;
-  const float true_residual = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+  const float true_residual = sqrtf(max0f(true_rr));
   const float eps = FLT_EPSILON;
   int32_t status, completed = 0;
   if (!finite || !fin(true_rr) || !fin(rho)) {
@@ -868,7 +875,7 @@ int oracle_csr_pcg_jacobi(int it, int64_t n, const float *data, const void *indi
     const float p2 = dot_f(p, p, n);
     const float ap2 = dot_f(ap, ap, n);
     const float prod = p2 * ap2;
-    const float scale = sqrtf(prod > 0.0f ? prod : 0.0f);
+    const float scale = sqrtf(max0f(prod));
     const float dtol = eps * (scale > 1.0f ? scale : 1.0f);
     if (!fin(denom) || !fin(scale) || fabsf(denom) <= dtol) {
       status = -1;
@@ -893,7 +900,7 @@ int oracle_csr_pcg_jacobi(int it, int64_t n, const float *data, const void *indi
       finite = finite && fin(x[i]) && fin(ri) && fin(zi);
     }
     true_rr = (float)acc;
-    const float r_norm = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+    const float r_norm = sqrtf(max0f(true_rr));
     completed = (int32_t)k;
     if (!finite || !fin(true_rr) || !fin(r_norm)) {
       status = -3;
@@ -917,12 +924,404 @@ int oracle_csr_pcg_jacobi(int it, int64_t n, const float *data, const void *indi
     rho = rho_new;
   }
   *info = status;
-  *residual = sqrtf(true_rr > 0.0f ? true_rr : 0.0f);
+  *residual = sqrtf(max0f(true_rr));
   *iterations = completed;
 done:
   free(r);
   free(z);
   free(p);
   free(ap);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
+ * and MINRES (src/linalg/minres/minres.cpp:68-312, csr_minres_cpu_impl),
+ * float32, the solver SpMV summed from zero.  Dot products are sequential
+ * double sums; scalars double; vectors float, each update rounded once. */
+
+static double dot_d(const float *a, const float *b, int64_t n) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) acc += (double)a[i] * (double)b[i];
+  return acc;
+}
+
+/* bicgstab.cpp:43-49 */
+static int near_zero_dot(double value, double lhs_norm2, double rhs_norm2) {
+  const double prod = lhs_norm2 * rhs_norm2;
+  const double scale = sqrt(max0(prod));
+  const double tol = (double)FLT_EPSILON * (scale > 1.0 ? scale : 1.0);
+  return !isfinite(scale) || fabs(value) <= tol;
+}
+
+/* dst = b - A x (bicgstab.cpp:130-149): returns float(sqrt(sum dst^2)) and
+ * *finite (every dst, A x and x entry, the sum and the norm finite). */
+static float bi_true_residual(int it, int64_t n, const float *data, const void *indices,
+                              const void *indptr, const float *b, const float *x, float *ax,
+                              float *dst, int *finite) {
+  cg_spmv(it, n, data, indices, indptr, x, ax);
+  double rr = 0.0;
+  int ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    const float ri = b[i] - ax[i];
+    ok = ok && fin(ri) && fin(ax[i]) && fin(x[i]);
+    dst[i] = ri;
+    rr += (double)ri * (double)ri;
+  }
+  const float norm = (float)sqrt(max0(rr));
+  *finite = ok && isfinite(rr) && fin(norm);
+  return norm;
+}
+
+int oracle_csr_bicgstab(int it, int64_t n, const float *data, const void *indices,
+                        const void *indptr, const float *b, const float *x0, float *x, float rtol,
+                        float atol, int64_t maxiter, int32_t *info, float *residual,
+                        int32_t *iterations) {
+  const size_t bytes = (size_t)(n > 0 ? n : 1) * sizeof(float);
+  float *r = (float *)malloc(bytes), *r_hat = (float *)malloc(bytes), *p = (float *)malloc(bytes);
+  float *v = (float *)malloc(bytes), *s = (float *)malloc(bytes), *t = (float *)malloc(bytes);
+  float *ax = (float *)malloc(bytes);
+  int32_t status = 0, completed = 0;
+  float residual_norm = 0.0f;
+  if (!r || !r_hat || !p || !v || !s || !t || !ax) {
+    free(r); free(r_hat); free(p); free(v); free(s); free(t); free(ax);
+    return -1;
+  }
+  memset(p, 0, bytes);
+  memset(v, 0, bytes);
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  double b_norm2 = 0.0;
+  int setup_finite = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    b_norm2 += (double)b[i] * (double)b[i];
+    setup_finite = setup_finite && fin(b[i]) && fin(x[i]);
+  }
+  const float b_norm = (float)sqrt(max0(b_norm2));
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  int finite = 1;
+  residual_norm = bi_true_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
+  memcpy(r_hat, r, (size_t)n * sizeof(float));
+  if (!setup_finite || !fin(b_norm) || !fin(tol) || !finite) {
+    status = -3;
+    goto done;
+  }
+  if (residual_norm <= tol) {
+    status = 0;
+    goto done;
+  }
+  status = maxiter > 0 ? (int32_t)maxiter : 1;
+  double rho_prev = 1.0, alpha = 1.0, omega = 1.0;
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    const double rho = dot_d(r_hat, r, n);
+    const double r_hat_norm2 = dot_d(r_hat, r_hat, n);
+    const double r_norm2 = dot_d(r, r, n);
+    if (!isfinite(rho) || !isfinite(r_hat_norm2) || !isfinite(r_norm2)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (near_zero_dot(rho, r_hat_norm2, r_norm2)) {
+      status = -1;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (k == 1) {
+      memcpy(p, r, (size_t)n * sizeof(float));
+    } else {
+      if (fabs(omega) <= (double)FLT_EPSILON) {
+        status = -1;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+      const double beta = (rho / rho_prev) * (alpha / omega);
+      if (!isfinite(beta)) {
+        status = -3;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+      int ok = 1;
+      for (int64_t i = 0; i < n; ++i) {
+        const double pi = (double)r[i] + beta * ((double)p[i] - omega * (double)v[i]);
+        p[i] = (float)pi;
+        ok = ok && isfinite(pi) && fin(p[i]);
+      }
+      if (!ok) {
+        status = -3;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+    }
+    cg_spmv(it, n, data, indices, indptr, p, v);
+    const double alpha_den = dot_d(r_hat, v, n);
+    const double v_norm2 = dot_d(v, v, n);
+    if (!isfinite(alpha_den) || !isfinite(v_norm2)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (near_zero_dot(alpha_den, r_hat_norm2, v_norm2)) {
+      status = -1;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    alpha = rho / alpha_den;
+    if (!isfinite(alpha)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    double s_norm2 = 0.0;
+    int ok = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      const double si = (double)r[i] - alpha * (double)v[i];
+      const double xi = (double)x[i] + alpha * (double)p[i];
+      s[i] = (float)si;
+      x[i] = (float)xi;
+      s_norm2 += si * si;
+      ok = ok && isfinite(si) && isfinite(xi) && fin(s[i]) && fin(x[i]);
+    }
+    completed = (int32_t)k;
+    const float s_norm = (float)sqrt(max0(s_norm2));
+    if (!ok || !isfinite(s_norm2) || !fin(s_norm)) {
+      status = -3;
+      break;
+    }
+    if (s_norm <= tol) {
+      int tf = 1;
+      const float true_norm = bi_true_residual(it, n, data, indices, indptr, b, x, ax, ax, &tf);
+      if (!tf) {
+        status = -3;
+        residual_norm = true_norm;
+        break;
+      }
+      if (true_norm <= tol) {
+        status = 0;
+        residual_norm = true_norm;
+        break;
+      }
+    }
+    cg_spmv(it, n, data, indices, indptr, s, t);
+    const double omega_num = dot_d(t, s, n);
+    const double omega_den = dot_d(t, t, n);
+    if (!isfinite(omega_num) || !isfinite(omega_den)) {
+      status = -3;
+      break;
+    }
+    if (near_zero_dot(omega_den, omega_den, 1.0)) {
+      status = -1;
+      break;
+    }
+    omega = omega_num / omega_den;
+    if (!isfinite(omega)) {
+      status = -3;
+      break;
+    }
+    double r_norm2_new = 0.0;
+    ok = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      const double xi = (double)x[i] + omega * (double)s[i];
+      const double ri = (double)s[i] - omega * (double)t[i];
+      x[i] = (float)xi;
+      r[i] = (float)ri;
+      r_norm2_new += ri * ri;
+      ok = ok && isfinite(xi) && isfinite(ri) && fin(x[i]) && fin(r[i]);
+    }
+    residual_norm = (float)sqrt(max0(r_norm2_new));
+    if (!ok || !isfinite(r_norm2_new) || !fin(residual_norm)) {
+      status = -3;
+      break;
+    }
+    if (residual_norm <= tol) {
+      int tf = 1;
+      const float true_norm = bi_true_residual(it, n, data, indices, indptr, b, x, ax, r, &tf);
+      if (!tf) {
+        status = -3;
+        residual_norm = true_norm;
+        break;
+      }
+      residual_norm = true_norm;
+      if (true_norm <= tol) {
+        status = 0;
+        break;
+      }
+    }
+    if (fabs(omega) <= (double)FLT_EPSILON) {
+      status = -1;
+      break;
+    }
+    rho_prev = rho;
+  }
+  if (status > 0 || status == -1) {
+    int tf = 1;
+    const float true_norm = bi_true_residual(it, n, data, indices, indptr, b, x, ax, r, &tf);
+    residual_norm = true_norm;
+    if (!tf) status = -3;
+    else if (true_norm <= tol) status = 0;
+  }
+done:
+  *info = status;
+  *residual = residual_norm;
+  *iterations = completed;
+  free(r); free(r_hat); free(p); free(v); free(s); free(t); free(ax);
+  return 0;
+}
+
+/* (A - shift I) x residual (minres.cpp:68-91): work = A x, then
+ * ai = work - shift x, ri = b - ai in float; *finite: every ai, ri and the
+ * norm finite. */
+static float mr_true_residual(int it, int64_t n, const float *data, const void *indices,
+                              const void *indptr, const float *b, const float *x, float *work,
+                              float shift, int *finite) {
+  cg_spmv(it, n, data, indices, indptr, x, work);
+  double rr = 0.0;
+  int ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    const float ai = work[i] - shift * x[i];
+    const float ri = b[i] - ai;
+    rr += (double)ri * (double)ri;
+    ok = ok && fin(ai) && fin(ri);
+  }
+  const float norm = (float)sqrt(max0(rr));
+  *finite = ok && fin(norm);
+  return norm;
+}
+
+int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
+                      const void *indptr, const float *b, const float *x0, float *x, float rtol,
+                      float atol, int64_t maxiter, float shift, int32_t *info, float *residual,
+                      int32_t *iterations) {
+  const size_t bytes = (size_t)(n > 0 ? n : 1) * sizeof(float);
+  float *r1 = (float *)calloc(1, bytes), *r2 = (float *)calloc(1, bytes);
+  float *y = (float *)calloc(1, bytes), *v = (float *)calloc(1, bytes);
+  float *w = (float *)calloc(1, bytes), *w2 = (float *)calloc(1, bytes);
+  float *av = (float *)calloc(1, bytes);
+  if (!r1 || !r2 || !y || !v || !w || !w2 || !av) {
+    free(r1); free(r2); free(y); free(v); free(w); free(w2); free(av);
+    return -1;
+  }
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  double b_norm2 = 0.0;
+  for (int64_t i = 0; i < n; ++i) b_norm2 += (double)b[i] * (double)b[i];
+  const float b_norm = (float)sqrt(max0(b_norm2));
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  int32_t status = maxiter > 0 ? (int32_t)maxiter : 1;
+  int32_t completed = 0;
+  /* the finite flag of minres.cpp:161-165 is reset by the residual helper */
+  int finite = 1;
+  float true_residual = mr_true_residual(it, n, data, indices, indptr, b, x, av, shift, &finite);
+  if (!finite) {
+    status = -3;
+    goto done;
+  }
+  if (true_residual <= tol) {
+    status = 0;
+    goto done;
+  }
+  if (maxiter == 0) goto done;
+  for (int64_t i = 0; i < n; ++i) {
+    const float ai = av[i] - shift * x[i];
+    const float ri = b[i] - ai;
+    r2[i] = ri;
+    y[i] = ri;
+  }
+  double beta_inner = (double)(float)dot_d(r2, y, n);
+  if (!isfinite(beta_inner) || beta_inner <= 0.0) {
+    status = -1;
+    goto done;
+  }
+  const double eps = (double)FLT_EPSILON;
+  double beta = sqrt(beta_inner), oldb = 0.0, dbar = 0.0, epsln = 0.0, phibar = beta;
+  double cs = -1.0, sn = 0.0;
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    if (!isfinite(beta) || beta <= eps) {
+      status = -1;
+      break;
+    }
+    const double inv_beta = 1.0 / beta;
+    for (int64_t i = 0; i < n; ++i) v[i] = (float)(inv_beta * (double)y[i]);
+    cg_spmv(it, n, data, indices, indptr, v, av);
+    for (int64_t i = 0; i < n; ++i) av[i] = av[i] - shift * v[i];
+    if (k >= 2) {
+      if (!isfinite(oldb) || fabs(oldb) <= eps) {
+        status = -1;
+        break;
+      }
+      const float prev_scale = (float)(beta / oldb);
+      for (int64_t i = 0; i < n; ++i) av[i] = av[i] - prev_scale * r1[i];
+    }
+    const double alfa = (double)(float)dot_d(v, av, n);
+    if (!isfinite(alfa)) {
+      status = -3;
+      break;
+    }
+    const float diag_scale = (float)(alfa / beta);
+    for (int64_t i = 0; i < n; ++i) av[i] = av[i] - diag_scale * r2[i];
+    /* r1 <- r2, r2 <- av, y = r2 (the old r1 becomes scratch) */
+    float *old_r1 = r1;
+    r1 = r2;
+    r2 = av;
+    av = old_r1;
+    memcpy(y, r2, (size_t)n * sizeof(float));
+    oldb = beta;
+    beta_inner = (double)(float)dot_d(r2, y, n);
+    if (!isfinite(beta_inner) || beta_inner < 0.0) {
+      status = -1;
+      break;
+    }
+    beta = sqrt(max0(beta_inner));
+    const double oldeps = epsln;
+    const double delta = cs * dbar + sn * alfa;
+    const double gbar = sn * dbar - cs * alfa;
+    epsln = sn * beta;
+    dbar = -cs * beta;
+    double gamma = hypot(gbar, beta);
+    if (!isfinite(gamma)) {
+      status = -3;
+      break;
+    }
+    gamma = gamma > eps ? gamma : eps;
+    cs = gbar / gamma;
+    sn = beta / gamma;
+    const double phi = cs * phibar;
+    phibar = sn * phibar;
+    if (!isfinite(phi) || !isfinite(phibar)) {
+      status = -3;
+      break;
+    }
+    int ok = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      const float prev_w1 = w2[i];
+      const float prev_w2 = w[i];
+      w2[i] = prev_w2;
+      w[i] = (float)(((double)v[i] - oldeps * (double)prev_w1 - delta * (double)prev_w2) / gamma);
+      x[i] = x[i] + (float)(phi * (double)w[i]);
+      ok = ok && fin(w[i]) && fin(x[i]);
+    }
+    completed = (int32_t)k;
+    if (!ok) {
+      status = -3;
+      break;
+    }
+    true_residual = mr_true_residual(it, n, data, indices, indptr, b, x, av, shift, &finite);
+    if (!finite) {
+      status = -3;
+      break;
+    }
+    if (true_residual <= tol) {
+      status = 0;
+      break;
+    }
+    if (beta <= eps) {
+      status = -1;
+      break;
+    }
+  }
+done:
+  *info = status;
+  *residual = true_residual;
+  *iterations = completed;
+  free(r1); free(r2); free(y); free(v); free(w); free(w2); free(av);
   return 0;
 }

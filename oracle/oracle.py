@@ -102,6 +102,12 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_pcg_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32, i64,
                                                vp, vp, vp]
         _lib.oracle_csr_pcg_jacobi.restype = ci
+        _lib.oracle_csr_bicgstab.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp,
+                                             vp, vp]
+        _lib.oracle_csr_bicgstab.restype = ci
+        _lib.oracle_csr_minres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
+                                           vp, vp, vp]
+        _lib.oracle_csr_minres.restype = ci
     return _lib
 
 
@@ -262,6 +268,42 @@ def csr_pcg_jacobi(data, indices, indptr, b, inv_diag, x0=None, *, rtol: float =
                                      ctypes.addressof(res), ctypes.addressof(its))
     if rc != 0:
         raise MemoryError("oracle_csr_pcg_jacobi failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_bicgstab(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: float = 0.0,
+                 maxiter: int | None = None):
+    """BiCGSTAB on a square float32 CSR matrix (reference
+    src/linalg/bicgstab/bicgstab.cpp:80-362).  Returns (x, info, residual,
+    iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_bicgstab(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                   _ptr(indptr), _ptr(b), _ptr(x0), _ptr(x), rtol, atol, maxiter,
+                                   ctypes.addressof(info), ctypes.addressof(res),
+                                   ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_bicgstab failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_minres(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: float = 0.0,
+               maxiter: int | None = None, shift: float = 0.0):
+    """MINRES on (A - shift I) x = b, A square symmetric float32 CSR
+    (reference src/linalg/minres/minres.cpp:68-312).  Returns (x, info,
+    residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_minres(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                 _ptr(indptr), _ptr(b), _ptr(x0), _ptr(x), rtol, atol, maxiter,
+                                 shift, ctypes.addressof(info), ctypes.addressof(res),
+                                 ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_minres failed")
     return x, info.value, res.value, its.value
 
 

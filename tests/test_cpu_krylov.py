@@ -1,0 +1,136 @@
+"""Native CPU BiCGSTAB and MINRES (msx_csr_bicgstab_cpu, msx_csr_minres_cpu)
+against the oracle through the C ABI - the same sequential loops, so x,
+info, residual and iteration count agree bit for bit - and the drop-in API
+``linalg.bicgstab`` / ``linalg.minres`` on the CPU device, with the
+reference's own test systems and argument rules
+(tests/test_linalg_bicgstab.py, tests/test_linalg_minres.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _capi
+from test_oracle_krylov import (INDEF, NONSYM, _csr, convection_2d, convection_diffusion,
+                                laplacian_2d)
+
+
+def _run(kind, A, b, index_dtype=np.int32, x0=None, **kw):
+    d, i, p = (torch.from_numpy(np.ascontiguousarray(a))
+               for a in (A.data.astype(np.float32), A.indices.astype(index_dtype),
+                         A.indptr.astype(index_dtype)))
+    return _capi.krylov(kind, d, i, p, torch.from_numpy(b),
+                        None if x0 is None else torch.from_numpy(x0), **kw)
+
+
+def _oracle(oracle, kind, A, b, index_dtype=np.int32, **kw):
+    args = (A.data.astype(np.float32), A.indices.astype(index_dtype),
+            A.indptr.astype(index_dtype), b)
+    return (oracle.csr_bicgstab if kind == "bicgstab" else oracle.csr_minres)(*args, **kw)
+
+
+def _same(got, want):
+    x, info, res, its = got
+    wx, winfo, wres, wits = want
+    assert (info, its) == (winfo, wits)
+    assert np.float32(res).tobytes() == np.float32(wres).tobytes()
+    assert x.numpy().tobytes() == wx.tobytes()
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_bicgstab_cpu_equals_oracle(oracle, index_dtype):
+    import scipy.sparse as sp
+
+    A = convection_2d(24)
+    b = np.random.default_rng(4).uniform(-1, 1, A.shape[0]).astype(np.float32)
+    for kw in ({"rtol": 1e-4}, {"rtol": 1e-6}, {"rtol": 1e-3, "atol": 0.05},
+               {"maxiter": 5, "rtol": 1e-9}, {"maxiter": 0}):
+        _same(_run("bicgstab", A, b, index_dtype, **kw),
+              _oracle(oracle, "bicgstab", A, b, index_dtype, **kw))
+    x0 = np.full(A.shape[0], 0.25, np.float32)
+    _same(_run("bicgstab", A, b, x0=x0, rtol=1e-4), oracle.csr_bicgstab(
+        A.data, A.indices, A.indptr, b, x0, rtol=1e-4))
+    B = sp.csr_matrix(np.diag([1.0, 2.0]).astype(np.float32))
+    _same(_run("bicgstab", B, np.ones(2, np.float32)),
+          _oracle(oracle, "bicgstab", B, np.ones(2, np.float32)))
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_minres_cpu_equals_oracle(oracle, index_dtype):
+    A = laplacian_2d(20)
+    b = np.random.default_rng(8).uniform(-1, 1, A.shape[0]).astype(np.float32)
+    for kw in ({"rtol": 1e-4, "shift": 1.3}, {"rtol": 1e-5}, {"rtol": 1e-9, "maxiter": 9},
+               {"maxiter": 0}, {"rtol": 1e-3, "atol": 0.02, "shift": -0.5}):
+        _same(_run("minres", A, b, index_dtype, **kw),
+              _oracle(oracle, "minres", A, b, index_dtype, **kw))
+
+
+def test_cpu_status_cases_equal_oracle(oracle):
+    import scipy.sparse as sp
+
+    A = sp.csr_matrix(NONSYM)
+    S = sp.csr_matrix(INDEF)
+    bad = np.ones(4, np.float32)
+    bad[2] = np.nan
+    for kind, M in (("bicgstab", A), ("minres", S)):
+        for b, kw in ((np.zeros(4, np.float32), {}), (np.ones(4, np.float32), {"maxiter": 0}),
+                      (bad, {})):
+            _same(_run(kind, M, b, **kw), _oracle(oracle, kind, M, b, **kw))
+    zero = sp.csr_matrix((np.zeros(3, np.float32), np.arange(3), np.arange(4)), shape=(3, 3))
+    got = _run("bicgstab", zero, np.array([1.0, 0.0, 0.0], np.float32), maxiter=8)
+    assert got[1] < 0
+    _same(got, _oracle(oracle, "bicgstab", zero, np.array([1.0, 0.0, 0.0], np.float32),
+                       maxiter=8))
+
+
+def test_api_on_cpu_reference_systems(cpu):
+    ms = cpu
+    from mlx_sparse import linalg
+
+    def csr(dense):
+        d, i, p = _csr(dense)
+        return ms.csr_array((d, i, p), shape=dense.shape, canonical=True)
+
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    x, info = linalg.bicgstab(csr(NONSYM), b, rtol=1e-6, atol=1e-7, maxiter=64)
+    assert info == 0
+    np.testing.assert_allclose(x.numpy(), np.linalg.solve(NONSYM, b), rtol=3e-5, atol=3e-5)
+    A = convection_diffusion()
+    x, info = linalg.bicgstab(csr(A), np.linspace(0.25, 1.5, 6, dtype=np.float32), tol=1e-5,
+                              atol=1e-7, maxiter=80, return_info=True)
+    assert info.solver == "bicgstab" and info.status == 0
+    assert info.convergence_reason == "converged" and info.breakdown_reason is None
+    assert info.rtol == 1e-5 and info.atol == 1e-7 and info.maxiter == 80
+    with pytest.raises(ValueError, match="tol is a compatibility alias"):
+        linalg.bicgstab(csr(A), np.ones(6, np.float32), rtol=1e-5, tol=1e-6)
+    _, info = linalg.bicgstab(csr(A), np.ones(6, np.float32), maxiter=0, return_info=True)
+    assert info.status > 0 and info.convergence_reason == "iteration_limit"
+    assert info.iterations == 0
+    bi = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    x, info = linalg.minres(csr(INDEF), bi, rtol=1e-6, atol=1e-7, maxiter=64)
+    assert info == 0
+    np.testing.assert_allclose(x.numpy(), np.linalg.solve(INDEF, bi), rtol=5e-5, atol=5e-5)
+    dense = np.array([[4.0, 1.0, 0.0], [1.0, 2.5, 0.5], [0.0, 0.5, 3.0]], np.float32)
+    x, info = linalg.minres(csr(dense), np.array([1.0, -2.0, 0.5], np.float32), shift=0.75,
+                            rtol=1e-6, atol=1e-7, maxiter=64)
+    assert info == 0
+    np.testing.assert_allclose(x.numpy(), np.linalg.solve(dense - 0.75 * np.eye(3),
+                                                          [1.0, -2.0, 0.5]), rtol=2e-5, atol=2e-5)
+    with pytest.raises(ValueError, match="shift must be finite"):
+        linalg.minres(csr(dense), np.ones(3, np.float32), shift=float("inf"))
+    from mlx_sparse.linalg import preconditioners
+
+    with pytest.raises(TypeError, match="identity preconditioner"):
+        linalg.minres(csr(dense), np.ones(3, np.float32), M=preconditioners.jacobi(csr(dense)))
+    x, info = linalg.bicgstab(csr(NONSYM), b, M=preconditioners.identity((4, 4)), rtol=1e-6)
+    assert info == 0
+
+
+def test_cpu_krylov_errors():
+    d = torch.ones(1)
+    i = torch.zeros(1, dtype=torch.int32)
+    p = torch.tensor([0, 1], dtype=torch.int32)
+    for kind in ("bicgstab", "minres"):
+        with pytest.raises(RuntimeError, match="maxiter must be non-negative"):
+            _capi.krylov(kind, d, i, p, torch.ones(1), maxiter=-1)

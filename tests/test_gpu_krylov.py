@@ -1,0 +1,230 @@
+"""HIP BiCGSTAB and MINRES (msx_csr_bicgstab, msx_csr_minres) against the
+oracle through the C ABI, and through ``linalg.bicgstab`` / ``linalg.minres``.
+
+The device loops follow the reference's arithmetic (float SpMV from zero,
+double dot products and scalars, vector updates rounded once) but add their
+dot products per workgroup, so the rounding of the double sums differs from
+the sequential loop.  The bar:
+
+- status equal to the oracle's, iteration count within two (a different
+  rounding of a double sum can move the crossing of the tolerance);
+- x solves the system as well as the oracle's: error against the float64
+  dense solution within rtol * cond, true residual under the tolerance,
+  reported residual equal to the true one to float32 rounding;
+- the status cases (zero right-hand side, exact x0, maxiter 0 and short
+  budgets, non-finite input, breakdown) give the oracle's status,
+  iterations and residual;
+- a solve is reproducible (two runs give the same bits), on every SpMV route
+  (row blocks, LDS panels, no plan);
+- the reference's own GPU test systems (tests/test_linalg_bicgstab.py:306-333,
+  tests/test_linalg_minres.py:57-93).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+import torch
+
+import _capi
+from oracle import oracle as orc
+from test_oracle_krylov import INDEF, NONSYM, convection_2d, laplacian_2d
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def convection_3d(g, wind=0.3):
+    one = sp.diags([-1 - wind, 2, -1 + wind], [-1, 0, 1], shape=(g, g))
+    eye = sp.identity(g)
+    A = (sp.kron(sp.kron(one, eye), eye) + sp.kron(sp.kron(eye, one), eye)
+         + sp.kron(sp.kron(eye, eye), one)).tocsr()
+    A.sort_indices()
+    return A.astype(np.float32)
+
+
+def _args(A, index_dtype=np.int32):
+    return (A.data.astype(np.float32), A.indices.astype(index_dtype),
+            A.indptr.astype(index_dtype))
+
+
+def _gpu(kind, A, b, index_dtype=np.int32, slice_mode=None, plan=True, x0=None, **kw):
+    d, i, p = (torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in _args(A, index_dtype))
+    pl = _capi.Plan(p, A.shape[0], d.numel(), data=d, indices=i, n_cols=A.shape[1],
+                    slice_mode=slice_mode) if plan else None
+    out = _capi.krylov(kind, d, i, p, torch.from_numpy(b).to(DEV),
+                       None if x0 is None else torch.from_numpy(x0).to(DEV), plan=pl, **kw)
+    torch.cuda.synchronize()
+    info = pl.info() if pl else None
+    return (out[0].cpu().numpy(),) + tuple(out[1:]) + ((info.n_panels if info else 0),)
+
+
+def _oracle(kind, A, b, index_dtype=np.int32, **kw):
+    f = orc.csr_bicgstab if kind == "bicgstab" else orc.csr_minres
+    return f(*_args(A, index_dtype), b, **kw)
+
+
+def _solution_checks(kind, A, b, x, res, rtol, shift=0.0):
+    A64 = A.astype(np.float64).toarray() - shift * np.eye(A.shape[0])
+    exact = np.linalg.solve(A64, b.astype(np.float64))
+    cond = np.linalg.cond(A64)
+    assert np.linalg.norm(x - exact) <= 4 * cond * rtol * np.linalg.norm(exact)
+    true_res = np.linalg.norm(b.astype(np.float64) - A64 @ x.astype(np.float64))
+    assert res <= rtol * np.linalg.norm(b) * (1 + 1e-5), (kind, res)
+    assert abs(true_res - res) <= 1e-5 * np.linalg.norm(b) + 1e-3 * res
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_bicgstab_matches_oracle(index_dtype):
+    A = convection_2d(32)
+    b = np.random.default_rng(4).uniform(-1, 1, A.shape[0]).astype(np.float32)
+    rtol = 1e-4
+    print(f"bicgstab convection 32^2 {np.dtype(index_dtype).name}", flush=True)
+    x, info, res, its, _ = _gpu("bicgstab", A, b, index_dtype, rtol=rtol)
+    wx, winfo, wres, wits = _oracle("bicgstab", A, b, index_dtype, rtol=rtol)
+    assert info == winfo == 0 and abs(its - wits) <= 2, (its, wits)
+    _solution_checks("bicgstab", A, b, x, res, rtol)
+
+
+@pytest.mark.parametrize("shift", [0.0, 1.3])
+def test_minres_matches_oracle(shift):
+    A = laplacian_2d(24)
+    b = np.random.default_rng(8).uniform(-1, 1, A.shape[0]).astype(np.float32)
+    rtol = 1e-4
+    print(f"minres laplacian 24^2 shift={shift}", flush=True)
+    x, info, res, its, _ = _gpu("minres", A, b, rtol=rtol, shift=shift)
+    wx, winfo, wres, wits = _oracle("minres", A, b, rtol=rtol, shift=shift)
+    assert info == winfo == 0 and abs(its - wits) <= 2, (its, wits)
+    _solution_checks("minres", A, b, x, res, rtol, shift=shift)
+
+
+@pytest.mark.parametrize("mode", ["blocks", "panels", "none"])
+def test_every_spmv_route_and_reproducible(mode):
+    A = convection_3d(40)
+    n = A.shape[0]
+    b = np.random.default_rng(9).uniform(-1, 1, n).astype(np.float32)
+    kw = {"plan": mode != "none",
+          "slice_mode": {"blocks": _capi.SLICE_OFF, "panels": _capi.SLICE_PANELS,
+                         "none": None}[mode]}
+    for kind in ("bicgstab", "minres"):
+        M = A if kind == "bicgstab" else laplacian_2d(200)
+        bb = b if kind == "bicgstab" else np.random.default_rng(3).uniform(
+            -1, 1, M.shape[0]).astype(np.float32)
+        print(f"{kind} route={mode} n={M.shape[0]}", flush=True)
+        x1, info1, res1, its1, panels = _gpu(kind, M, bb, rtol=1e-4, **kw)
+        x2, info2, res2, its2, _ = _gpu(kind, M, bb, rtol=1e-4, **kw)
+        if mode == "panels":
+            assert panels > 0
+        assert (info1, its1) == (info2, its2) and res1 == res2 and x1.tobytes() == x2.tobytes()
+        wx, winfo, wres, wits = _oracle(kind, M, bb, rtol=1e-4)
+        assert info1 == winfo == 0 and abs(its1 - wits) <= max(2, wits // 50), (its1, wits)
+        ref = np.linalg.norm(wx.astype(np.float64))
+        assert np.linalg.norm(x1.astype(np.float64) - wx) <= 1e-2 * ref
+
+
+def test_status_cases_match_oracle():
+    A, S = sp.csr_matrix(NONSYM), sp.csr_matrix(INDEF)
+    bad = np.ones(4, np.float32)
+    bad[2] = np.nan
+    exact = np.linalg.solve(NONSYM, np.arange(1, 5, dtype=np.float32)).astype(np.float32)
+    bx = (NONSYM.astype(np.float64) @ exact).astype(np.float32)
+    cases = [(np.zeros(4, np.float32), {}), (np.ones(4, np.float32), {"maxiter": 0}),
+             (np.ones(4, np.float32), {"maxiter": 1, "rtol": 1e-9}), (bad, {})]
+    for kind, M in (("bicgstab", A), ("minres", S)):
+        for b, kw in cases:
+            x, info, res, its, _ = _gpu(kind, M, b, **kw)
+            wx, winfo, wres, wits = _oracle(kind, M, b, **kw)
+            print(f"{kind} status case {kw}: gpu {info, its, res} oracle {winfo, wits, wres}",
+                  flush=True)
+            assert (info, its) == (winfo, wits)
+            assert np.isnan(res) == np.isnan(wres)
+            if not np.isnan(wres):
+                assert abs(res - wres) <= 1e-6 * max(1.0, abs(wres))
+    x, info, res, its, _ = _gpu("bicgstab", A, bx, x0=exact, rtol=1e-7, atol=1e-7)
+    assert (info, its) == (0, 0) and x.tobytes() == exact.tobytes()
+    zero = sp.csr_matrix((np.zeros(3, np.float32), np.arange(3), np.arange(4)), shape=(3, 3))
+    b1 = np.array([1.0, 0.0, 0.0], np.float32)
+    got = _gpu("bicgstab", zero, b1, maxiter=8)
+    want = _oracle("bicgstab", zero, b1, maxiter=8)
+    assert got[1] == want[1] < 0 and got[3] == want[3]
+
+
+def test_hand_computed_and_closed_forms():
+    x, info, res, its, _ = _gpu("bicgstab", sp.csr_matrix(np.diag([1.0, 2.0]).astype(np.float32)),
+                                np.ones(2, np.float32), rtol=1e-5)
+    assert (info, its) == (0, 2)
+    np.testing.assert_allclose(x, [1.0, 0.5], rtol=1e-6, atol=1e-7)
+    rng = np.random.default_rng(3)
+    n, eigs = 40, [2.0, 5.0, -1.0]
+    diag = np.array([eigs[j % 3] for j in range(n)])
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    dense = ((Q * diag) @ Q.T).astype(np.float32)
+    dense = (dense + dense.T) / 2
+    b = rng.uniform(-1, 1, n).astype(np.float32)
+    x, info, res, its, _ = _gpu("minres", sp.csr_matrix(dense), b, rtol=1e-4)
+    assert (info, its) == (0, 3)
+
+
+def test_api_on_gpu_reference_systems(gpu):
+    """The reference's GPU tests (test_linalg_bicgstab.py:306-333,
+    test_linalg_minres.py:57-93) through linalg on the device."""
+    ms = gpu
+    from mlx_sparse import linalg
+
+    def csr(dense):
+        A = sp.csr_matrix(dense.astype(np.float32))
+        return ms.csr_array((A.data, A.indices.astype(np.int32), A.indptr.astype(np.int32)),
+                            shape=dense.shape, canonical=True)
+
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    x, info = linalg.bicgstab(csr(NONSYM), b, rtol=1e-6, atol=1e-7, maxiter=80)
+    assert info == 0 and x.device.type == "cuda"
+    xn = x.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(NONSYM @ xn - b) / max(np.linalg.norm(b), 1.0) < 2e-6
+    bi = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    x, info = linalg.minres(csr(INDEF), bi, rtol=1e-6, atol=1e-7, maxiter=64)
+    assert info == 0
+    np.testing.assert_allclose(x.cpu().numpy(), np.linalg.solve(INDEF, bi), rtol=5e-5, atol=5e-5)
+    x, info = linalg.minres(csr(np.diag([0.0, 2.0, 3.0, -4.0])),
+                            np.array([0.0, 4.0, -3.0, 8.0], np.float32), rtol=1e-7, atol=1e-7,
+                            maxiter=32, return_info=True)
+    assert info.status == 0 and info.solver == "minres"
+
+
+def test_full_size_minres_and_bicgstab(gpu):
+    """Both loops at the SpMM benchmark's size (n = 128^3) on the device
+    with the matrix's cached plan, against the oracle: MINRES on the 3D
+    Poisson matrix with shift -1 (A + I), BiCGSTAB on a nonsymmetric
+    convection-diffusion variant of it (x-direction off-diagonals -1.3 and
+    -0.7, diagonal 8).  In float32 the reference's loops stagnate near a
+    relative residual of 1e-3 on the plain Poisson matrix (MINRES) or break
+    down (BiCGSTAB, rho = 0 against r_hat = b), so these are the systems
+    both converge on."""
+    ms = gpu
+    from mlx_sparse import linalg, synthetic
+
+    m = synthetic.poisson_3d(128)
+    n = m.shape[0]
+    rows = np.repeat(np.arange(n), np.diff(m.indptr))
+    cols = m.indices.astype(np.int64)
+    conv = m.data.copy()
+    conv[cols == rows + 1] = -0.7
+    conv[cols == rows - 1] = -1.3
+    conv[cols == rows] = 8.0
+    b_np = synthetic.uniform(n, -1.0, 1.0, seed=7)
+    b = torch.from_numpy(b_np).to(DEV)
+    for name, data, kw in (("minres", m.data, {"shift": -1.0}), ("bicgstab", conv, {})):
+        A = ms.csr_array((data, m.indices, m.indptr), shape=m.shape, canonical=True)
+        solver = getattr(linalg, name)
+        x, info = solver(A, b, rtol=1e-5, maxiter=500, return_info=True, **kw)
+        wx, winfo, wres, wits = _oracle(name, sp.csr_matrix((data, m.indices, m.indptr),
+                                                            shape=m.shape), b_np, rtol=1e-5,
+                                        maxiter=500, **kw)
+        print(f"{name}: gpu status {info.status} iterations {info.iterations} residual "
+              f"{info.residual_norm:.5g}; oracle {winfo} {wits} {wres:.5g}", flush=True)
+        assert info.status == winfo == 0 and abs(info.iterations - wits) <= 2
+        assert info.residual_norm <= 1e-5 * np.linalg.norm(b_np) * (1 + 1e-5)
+        ref = np.linalg.norm(wx.astype(np.float64))
+        assert np.linalg.norm(x.cpu().numpy().astype(np.float64) - wx) <= 1e-4 * ref
