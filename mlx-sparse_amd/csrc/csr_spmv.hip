@@ -53,6 +53,29 @@ __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+// Offset from a0 of a row pointer clamped into its block [p0, p1].  With
+// int32 row pointers p0, p1 and a0 are row-pointer values too, so the clamp
+// runs in 32 bits.
+__device__ inline int32_t block_offset(int32_t v, int64_t p0, int64_t p1, int64_t a0) {
+  return std::min(std::max(v, static_cast<int32_t>(p0)), static_cast<int32_t>(p1)) -
+         static_cast<int32_t>(a0);
+}
+__device__ inline int32_t block_offset(int64_t v, int64_t p0, int64_t p1, int64_t a0) {
+  return static_cast<int32_t>(clamp64(v, p0, p1) - a0);
+}
+
+// 0 <= col < n_cols.  An int32 column compares as unsigned against
+// lim32 = min(n_cols, 2^31), which also rejects negative columns.
+__device__ inline bool col_ok(int32_t col, int64_t, uint32_t lim32) {
+  return static_cast<uint32_t>(col) < lim32;
+}
+__device__ inline bool col_ok(int64_t col, int64_t n_cols, uint32_t) {
+  return static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+}
+__host__ __device__ inline uint32_t col_limit32(int64_t n_cols) {
+  return n_cols >= 0x80000000LL ? 0x80000000u : (n_cols > 0 ? static_cast<uint32_t>(n_cols) : 0u);
+}
+
 __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -108,6 +131,7 @@ __global__ void __launch_bounds__(kThreads)
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   A *prod = lds_prod[wave];
   int32_t *rptr = lds_ptr[wave];
+  const uint32_t lim32 = col_limit32(n_cols);
 
   const uint32_t gid = FUSE ? blockIdx.x - long_groups : blockIdx.x;
   const uint32_t ngroups = FUSE ? gridDim.x - long_groups : gridDim.x;
@@ -123,47 +147,54 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t p0 = clamp64(bounds_nnz[b], 0, nnz);
     const int64_t p1 = clamp64(bounds_nnz[b + 1], p0, std::min<int64_t>(nnz, p0 + 2 * W - 1));
     const int64_t a0 = p0 & ~int64_t{3};
+    // The block's values lie at offsets [p0 - a0, p1 - a0) from a0, in nq
+    // quads (fewer than W/2 + 2).  Products are staged for every loaded
+    // position; phase 2 reads only the row ranges, which lie inside the
+    // block, so the positions around it need no mask.
     const int nq = static_cast<int>((p1 - a0 + 3) >> 2);
 
     // Row pointers of the block, relative to a0 and clamped into the block.
-    // Every load below is unconditional: lanes with nothing to load address
-    // past the end of a descriptor and read zero, so a wave issues all of
-    // its loads before it waits on any.
+    // Chunks of 64 past the block's m + 1 entries are skipped (a
+    // wave-uniform test); the loads that are issued are unconditional, lanes
+    // past the end read zero through the descriptor.
     const auto rr = make_rsrc(indptr + r0, static_cast<uint64_t>(m + 1) * sizeof(I));
-    int32_t rp[(kBlockRows + kWave) / kWave];
+    constexpr int kRpChunks = (kBlockRows + kWave) / kWave;
+    int32_t rp[kRpChunks];
 #pragma unroll
-    for (int k = 0; k < (kBlockRows + kWave) / kWave; ++k) {
-      const int i = lane + k * kWave;
-      const int64_t v = static_cast<int64_t>(buffer_index<I>(rr, static_cast<uint32_t>(i) * sizeof(I)));
-      rp[k] = i <= m ? static_cast<int32_t>(clamp64(v, p0, p1) - a0) : 0;
+    for (int k = 0; k < kRpChunks; ++k) {
+      rp[k] = 0;
+      if (k == 0 || k * kWave <= m) {
+        const int i = lane + k * kWave;
+        rp[k] = block_offset(buffer_index<I>(rr, static_cast<uint32_t>(i) * sizeof(I)), p0, p1, a0);
+      }
     }
 
     // Phase 1: all quads of the block, then all gathers, then products.
-    // The descriptors end at p1, so quads past the block read zero.
+    // The descriptors end at p1, so quads past the block read zero; chunks
+    // of 64 quads past nq are skipped.
     const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(p1 - a0) * sizeof(I));
     const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(p1 - a0) * sizeof(S));
-    Quad<I> iq[QPL];
-    Quad<S> dq[QPL];
+    Quad<I> iq[QPL] = {};
+    Quad<S> dq[QPL] = {};
 #pragma unroll
     for (int k = 0; k < QPL; ++k) {
-      const uint32_t q = static_cast<uint32_t>(lane + k * kWave);
-      iq[k] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
-      dq[k] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
+      if (k == 0 || k * kWave < nq) {
+        const uint32_t q = static_cast<uint32_t>(lane + k * kWave);
+        iq[k] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
+        dq[k] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
+      }
     }
     A xv[QPL][4];
     if (x_bytes != 0) {
       const auto rx = make_rsrc(x, x_bytes);
-      GatherRaw<S> raw[QPL][4];
+      GatherRaw<S> raw[QPL][4] = {};
 #pragma unroll
       for (int k = 0; k < QPL; ++k) {
-        const int q = lane + k * kWave;
+        if (k == 0 || k * kWave < nq) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t pos = a0 + 4 * q + e;
-          const int64_t col = static_cast<int64_t>(iq[k].v[e]);
-          const bool ok = q < nq && pos >= p0 && pos < p1 &&
-                          static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
-          raw[k][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(col), ok);
+          for (int e = 0; e < 4; ++e)
+            raw[k][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(iq[k].v[e]),
+                                      col_ok(iq[k].v[e], n_cols, lim32));
         }
       }
       // every gather is issued before the first is used
@@ -176,29 +207,27 @@ __global__ void __launch_bounds__(kThreads)
     } else {  // x beyond a descriptor's reach: clamped global loads
 #pragma unroll
       for (int k = 0; k < QPL; ++k) {
-        const int q = lane + k * kWave;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t pos = a0 + 4 * q + e;
-          const int64_t col = static_cast<int64_t>(iq[k].v[e]);
-          const bool ok = q < nq && pos >= p0 && pos < p1 &&
-                          static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
-          A v = vzero<A>();
-          if (n_cols > 0) v = V::widen(x[ok ? col : 0]);  // wave-uniform test
-          xv[k][e] = ok ? v : vzero<A>();
+          xv[k][e] = vzero<A>();
+          if (k == 0 || k * kWave < nq) {
+            const I col = iq[k].v[e];
+            const bool ok = col_ok(col, n_cols, lim32);
+            A v = vzero<A>();
+            if (n_cols > 0) v = V::widen(x[ok ? static_cast<int64_t>(col) : 0]);  // wave-uniform test
+            xv[k][e] = v;
+          }
         }
       }
     }
 #pragma unroll
     for (int k = 0; k < QPL; ++k) {
       const int q = lane + k * kWave;
-      if (q < nq) {
+      if ((k == 0 || k * kWave < nq) && (W >= 128 || q < kQuads)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t pos = a0 + 4 * q + e;
-          A pv = vzero<A>();
-          if (pos >= p0 && pos < p1) pv = vmul_acc<V>(xv[k][e], dq[k].v[e]);
-          prod[4 * q + e] = pv;
+          const A pv = vmul_acc<V>(xv[k][e], dq[k].v[e]);
+          prod[4 * q + e] = col_ok(iq[k].v[e], n_cols, lim32) ? pv : vzero<A>();
         }
       }
     }
@@ -216,9 +245,9 @@ __global__ void __launch_bounds__(kThreads)
       }
     }
 #pragma unroll
-    for (int k = 0; k < (kBlockRows + kWave) / kWave; ++k) {
+    for (int k = 0; k < kRpChunks; ++k) {
       const int i = lane + k * kWave;
-      if (i <= m) rptr[i] = rp[k];
+      if ((k == 0 || k * kWave <= m) && i <= m) rptr[i] = rp[k];
     }
     wave_lds_sync();
 
