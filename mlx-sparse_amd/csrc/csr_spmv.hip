@@ -91,6 +91,96 @@ __device__ inline void wave_lds_sync() {
 // indices, values) -> x gathers -> LDS -> y.
 constexpr int kBlockRows = 256;  // R; equals the plan's block_rows
 
+// Phase 1 of a short block, NC chunks of 64 quads (4 values per lane per
+// load): all index/value quads, then all gathers, then the products staged
+// in LDS.  The loads are unconditional - the descriptors end at p1, so
+// quads past the block read zero - which lets the compiler issue every one
+// before it waits on any; a load under a branch would be waited on inside
+// it.  Products are staged for every loaded position: phase 2 reads only the
+// row ranges, which lie inside the block.
+template <class V, class I, int W, int AUX, int NC>
+__device__ __forceinline__ void block_products(const typename V::Storage *__restrict__ data,
+                                               const I *__restrict__ indices,
+                                               const typename V::Storage *__restrict__ x,
+                                               int64_t a0, int64_t p1, int64_t n_cols,
+                                               uint32_t lim32, uint32_t x_bytes, int lane,
+                                               typename V::Acc *prod) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  constexpr int kQuads = W / 2 + 1;
+  const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(p1 - a0) * sizeof(I));
+  const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(p1 - a0) * sizeof(S));
+  Quad<I> iq[NC];
+  Quad<S> dq[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const uint32_t q = static_cast<uint32_t>(lane + k * kWave);
+    iq[k] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
+    dq[k] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
+  }
+  A xv[NC][4];
+  if (x_bytes != 0) {
+    const auto rx = make_rsrc(x, x_bytes);
+    GatherRaw<S> raw[NC][4];
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        raw[k][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(iq[k].v[e]),
+                                  col_ok(iq[k].v[e], n_cols, lim32));
+    // every gather is issued before the first is used
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[k][e] = gather_widen<V>(raw[k][e], static_cast<uint32_t>(iq[k].v[e]));
+  } else {  // x beyond a descriptor's reach: clamped global loads
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const I col = iq[k].v[e];
+        const bool ok = col_ok(col, n_cols, lim32);
+        A v = vzero<A>();
+        if (n_cols > 0) v = V::widen(x[ok ? static_cast<int64_t>(col) : 0]);  // wave-uniform test
+        xv[k][e] = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int q = lane + k * kWave;
+    if (W >= 128 || q < kQuads) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const A pv = vmul_acc<V>(xv[k][e], dq[k].v[e]);
+        prod[4 * q + e] = col_ok(iq[k].v[e], n_cols, lim32) ? pv : vzero<A>();
+      }
+    }
+  }
+}
+
+// block_products for the block's chunk count nch <= NC (a wave-uniform
+// dispatch, so each case is straight-line code).
+template <class V, class I, int W, int AUX, int NC>
+__device__ __forceinline__ void block_products_n(int nch,
+                                                 const typename V::Storage *__restrict__ data,
+                                                 const I *__restrict__ indices,
+                                                 const typename V::Storage *__restrict__ x,
+                                                 int64_t a0, int64_t p1, int64_t n_cols,
+                                                 uint32_t lim32, uint32_t x_bytes, int lane,
+                                                 typename V::Acc *prod) {
+  if constexpr (NC > 0) {
+    if (nch >= NC)
+      block_products<V, I, W, AUX, NC>(data, indices, x, a0, p1, n_cols, lim32, x_bytes, lane,
+                                       prod);
+    else
+      block_products_n<V, I, W, AUX, NC - 1>(nch, data, indices, x, a0, p1, n_cols, lim32,
+                                             x_bytes, lane, prod);
+  }
+}
+
 // FUSE: the XCD-sliced long-row pieces ride in the same launch.  The first
 // `long_groups` workgroups (a multiple of 8, so workgroup g still runs on
 // XCD g % 8) sum long-row pieces, the rest walk the short blocks; the two
@@ -148,89 +238,22 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t p1 = clamp64(bounds_nnz[b + 1], p0, std::min<int64_t>(nnz, p0 + 2 * W - 1));
     const int64_t a0 = p0 & ~int64_t{3};
     // The block's values lie at offsets [p0 - a0, p1 - a0) from a0, in nq
-    // quads (fewer than W/2 + 2).  Products are staged for every loaded
-    // position; phase 2 reads only the row ranges, which lie inside the
-    // block, so the positions around it need no mask.
+    // quads (fewer than W/2 + 2).
     const int nq = static_cast<int>((p1 - a0 + 3) >> 2);
 
-    // Row pointers of the block, relative to a0 and clamped into the block.
-    // Chunks of 64 past the block's m + 1 entries are skipped (a
-    // wave-uniform test); the loads that are issued are unconditional, lanes
-    // past the end read zero through the descriptor.
+    // Row pointers of the block (lanes past its m + 1 entries read zero
+    // through the descriptor); clamped into the block after phase 1.
     const auto rr = make_rsrc(indptr + r0, static_cast<uint64_t>(m + 1) * sizeof(I));
     constexpr int kRpChunks = (kBlockRows + kWave) / kWave;
-    int32_t rp[kRpChunks];
+    I rpv[kRpChunks];
 #pragma unroll
-    for (int k = 0; k < kRpChunks; ++k) {
-      rp[k] = 0;
-      if (k == 0 || k * kWave <= m) {
-        const int i = lane + k * kWave;
-        rp[k] = block_offset(buffer_index<I>(rr, static_cast<uint32_t>(i) * sizeof(I)), p0, p1, a0);
-      }
-    }
+    for (int k = 0; k < kRpChunks; ++k)
+      rpv[k] = buffer_index<I>(rr, static_cast<uint32_t>(lane + k * kWave) * sizeof(I));
 
-    // Phase 1: all quads of the block, then all gathers, then products.
-    // The descriptors end at p1, so quads past the block read zero; chunks
-    // of 64 quads past nq are skipped.
-    const auto ri = make_rsrc(indices + a0, static_cast<uint64_t>(p1 - a0) * sizeof(I));
-    const auto rd = make_rsrc(data + a0, static_cast<uint64_t>(p1 - a0) * sizeof(S));
-    Quad<I> iq[QPL] = {};
-    Quad<S> dq[QPL] = {};
-#pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      if (k == 0 || k * kWave < nq) {
-        const uint32_t q = static_cast<uint32_t>(lane + k * kWave);
-        iq[k] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
-        dq[k] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
-      }
-    }
-    A xv[QPL][4];
-    if (x_bytes != 0) {
-      const auto rx = make_rsrc(x, x_bytes);
-      GatherRaw<S> raw[QPL][4] = {};
-#pragma unroll
-      for (int k = 0; k < QPL; ++k) {
-        if (k == 0 || k * kWave < nq) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            raw[k][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(iq[k].v[e]),
-                                      col_ok(iq[k].v[e], n_cols, lim32));
-        }
-      }
-      // every gather is issued before the first is used
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int k = 0; k < QPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xv[k][e] = gather_widen<V>(raw[k][e], static_cast<uint32_t>(iq[k].v[e]));
-    } else {  // x beyond a descriptor's reach: clamped global loads
-#pragma unroll
-      for (int k = 0; k < QPL; ++k) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          xv[k][e] = vzero<A>();
-          if (k == 0 || k * kWave < nq) {
-            const I col = iq[k].v[e];
-            const bool ok = col_ok(col, n_cols, lim32);
-            A v = vzero<A>();
-            if (n_cols > 0) v = V::widen(x[ok ? static_cast<int64_t>(col) : 0]);  // wave-uniform test
-            xv[k][e] = v;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int q = lane + k * kWave;
-      if ((k == 0 || k * kWave < nq) && (W >= 128 || q < kQuads)) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const A pv = vmul_acc<V>(xv[k][e], dq[k].v[e]);
-          prod[4 * q + e] = col_ok(iq[k].v[e], n_cols, lim32) ? pv : vzero<A>();
-        }
-      }
-    }
+    // Phase 1 over the chunks of 64 quads the block occupies.
+    const int nch = std::min(QPL, (nq + kWave - 1) / kWave);
+    block_products_n<V, I, W, AUX, QPL>(nch, data, indices, x, a0, p1, n_cols, lim32, x_bytes,
+                                        lane, prod);
     if (nq > QPL * kWave) {  // wave-uniform: the block's last quad, one value per lane
       const int q = QPL * kWave;
       const int64_t pos = a0 + 4 * q + lane;
@@ -247,7 +270,9 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int k = 0; k < kRpChunks; ++k) {
       const int i = lane + k * kWave;
-      if ((k == 0 || k * kWave <= m) && i <= m) rptr[i] = rp[k];
+      if (k == 0 || k * kWave <= m) {  // wave-uniform
+        if (i <= m) rptr[i] = block_offset(rpv[k], p0, p1, a0);
+      }
     }
     wave_lds_sync();
 
