@@ -179,13 +179,18 @@ struct alignas(4 * sizeof(A)) ProdQuad {
 
 // NQ quads per lane per batch: a wave's share of a tile (TW / 16 words on
 // average) usually takes one batch.
-template <class V, class I>
+// Rows of a tile are virtual rows delimited by rowptr: the matrix's rows
+// (RP = the index type, indptr) or, with LONG, short rows and chunks of
+// long rows (RP = uint32_t, the plan's virtual-row starts); vslot then
+// names each one's row, or -1 for a chunk, whose sum goes to partial.
+template <class V, class RP, bool LONG>
 __global__ void __launch_bounds__(kThreads)
     panel_rows(const typename V::Acc *__restrict__ prod, const uint16_t *__restrict__ dest,
                const uint32_t *__restrict__ seg, int64_t n_tiles, int P,
                const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
-               const I *__restrict__ indptr, int64_t n_rows, int64_t nnz,
-               typename V::Storage *__restrict__ y, int zero_fill) {
+               const RP *__restrict__ indptr, int64_t n_rows, int64_t nnz,
+               typename V::Storage *__restrict__ y, int zero_fill,
+               const int32_t *__restrict__ vslot, typename V::Acc *__restrict__ partial) {
   using A = typename V::Acc;
   constexpr int TW = 65536 / static_cast<int>(sizeof(A));
   constexpr int NQ = TW / kThreads / 4;
@@ -200,9 +205,11 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t r1 = clamp64(tile_end[T], r0, n_rows);
   const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
   int64_t s_first = 0, e_first = 0;
+  int32_t slot_first = 0;
   if (r0 + threadIdx.x < r1) {
     s_first = static_cast<int64_t>(indptr[r0 + threadIdx.x]);
     e_first = static_cast<int64_t>(indptr[r0 + threadIdx.x + 1]);
+    if constexpr (LONG) slot_first = vslot[r0 + threadIdx.x];
   }
   if (zero_fill) {
     for (int i = threadIdx.x; i < TW; i += kThreads) buf[i] = vzero<A>();
@@ -264,10 +271,13 @@ __global__ void __launch_bounds__(kThreads)
 
   for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
     int64_t s = s_first, e = e_first;
+    int32_t slot = slot_first;
     if (r != r0 + threadIdx.x) {
       s = static_cast<int64_t>(indptr[r]);
       e = static_cast<int64_t>(indptr[r + 1]);
+      if constexpr (LONG) slot = vslot[r];
     }
+    if constexpr (!LONG) slot = static_cast<int32_t>(r);
     s = clamp64(s, 0, nnz);
     e = clamp64(e, s, nnz);
     const int64_t base = clamp64((s - b0) + (r - r0), 0, TW);
@@ -275,12 +285,62 @@ __global__ void __launch_bounds__(kThreads)
     const A *v = buf + base;
     A acc = vzero<A>();
     int i = 0;
-    if (len >= 1 && len <= 4) {
+    // a chunk of a long row sums from zero, like the long row it belongs to
+    if (len >= 1 && len <= 4 && slot >= 0) {
       acc = v[0];
       i = 1;
     }
+    // stored order; eight LDS reads are issued before their adds
+    for (; i + 8 <= len; i += 8) {
+      A t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = v[i + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = vadd(acc, t[u]);
+    }
     for (; i < len; ++i) acc = vadd(acc, v[i]);
-    y[r] = V::narrow(acc);
+    if (slot >= 0)
+      y[slot] = V::narrow(acc);
+    else
+      partial[r] = acc;
+  }
+}
+
+// Long rows of a virtual-row layout: one 256-thread workgroup per long row
+// adds its chunk sums - each thread a strided share (four loads in flight),
+// then a butterfly per wave and the four wave sums in order - so the
+// result is the same on every call.
+constexpr int kFixupThreads = 256;
+
+template <class V>
+__global__ void __launch_bounds__(kFixupThreads)
+    panel_long_fixup(const typename V::Acc *__restrict__ partial, const uint32_t *__restrict__ vbase,
+                     const int32_t *__restrict__ long_rows, int64_t n_long, int64_t n_rows,
+                     typename V::Storage *__restrict__ y) {
+  using A = typename V::Acc;
+  __shared__ A wave_sum[kFixupThreads / kWave];
+  const int64_t r = long_rows[blockIdx.x];
+  if (r < 0 || r >= n_rows) return;  // uniform across the workgroup
+  const int64_t a = vbase[r], b = vbase[r + 1];
+  A acc = vzero<A>();
+  int64_t k = a + threadIdx.x;
+  for (; k + 3 * kFixupThreads < b; k += 4 * kFixupThreads) {
+    A t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) t[u] = partial[k + u * kFixupThreads];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = vadd(acc, t[u]);
+  }
+  for (; k < b; k += kFixupThreads) acc = vadd(acc, partial[k]);
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) acc = vadd(acc, shfl_xor(acc, d));
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (lane == 0) wave_sum[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    A total = wave_sum[0];
+    for (int w = 1; w < kFixupThreads / kWave; ++w) total = vadd(total, wave_sum[w]);
+    y[r] = V::narrow(total);
   }
 }
 
@@ -303,7 +363,10 @@ msx_status prepare_typed(const msx_csr_plan *p) {
   MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_products<V>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(pass1_lds<A>(p))));
-  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_rows<V, I>),
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_rows<V, I, false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(pass2_lds<A>(p))));
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_rows<V, uint32_t, true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(pass2_lds<A>(p))));
   return MSX_OK;
@@ -326,11 +389,25 @@ msx_status launch_typed(const msx_csr_plan *p, const void *indptr, const void *x
                      p->pn_values, static_cast<int>(p->panel_width));
   MSX_HIP_TRY(hipGetLastError());
   const size_t lds2 = pass2_lds<A>(p);
-  hipLaunchKernelGGL((panel_rows<V, I>), dim3(static_cast<uint32_t>(p->n_tiles)), dim3(kThreads), lds2,
-                     stream, static_cast<const A *>(p->pn_prod), p->pn_dest, p->pn_seg, p->n_tiles,
-                     static_cast<int>(p->n_panels), p->pn_tile_begin, p->pn_tile_end,
-                     static_cast<const I *>(indptr), p->n_rows, p->nnz, static_cast<S *>(y),
-                     p->pn_dropped ? 1 : 0);
+  if (p->pn_vstart == nullptr) {
+    hipLaunchKernelGGL((panel_rows<V, I, false>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                       dim3(kThreads), lds2, stream, static_cast<const A *>(p->pn_prod), p->pn_dest,
+                       p->pn_seg, p->n_tiles, static_cast<int>(p->n_panels), p->pn_tile_begin,
+                       p->pn_tile_end, static_cast<const I *>(indptr), p->n_rows, p->nnz,
+                       static_cast<S *>(y), p->pn_dropped ? 1 : 0, nullptr, nullptr);
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
+  // Long rows: pass 2 writes their chunk sums, the fixup adds them.
+  hipLaunchKernelGGL((panel_rows<V, uint32_t, true>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                     dim3(kThreads), lds2, stream, static_cast<const A *>(p->pn_prod), p->pn_dest,
+                     p->pn_seg, p->n_tiles, static_cast<int>(p->n_panels), p->pn_tile_begin,
+                     p->pn_tile_end, p->pn_vstart, p->pn_vrows, p->nnz, static_cast<S *>(y),
+                     p->pn_dropped ? 1 : 0, p->pn_vslot, static_cast<A *>(p->pn_partial));
+  MSX_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL((panel_long_fixup<V>), dim3(static_cast<uint32_t>(p->n_long)),
+                     dim3(kFixupThreads), 0, stream, static_cast<const A *>(p->pn_partial), p->pn_vbase,
+                     p->long_rows, p->n_long, p->n_rows, static_cast<S *>(y));
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
 }

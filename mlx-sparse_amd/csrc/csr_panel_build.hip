@@ -43,6 +43,12 @@
 namespace msx {
 namespace {
 
+#define MSX_TRY_STATUS(expr)     \
+  do {                           \
+    msx_status _s = (expr);      \
+    if (_s != MSX_OK) return _s; \
+  } while (0)
+
 constexpr int kThreads = 256;
 constexpr int64_t kMaxGrid = int64_t{1} << 20;
 constexpr int64_t kPanelBytes = 131072;  // x panel in LDS during pass 1
@@ -60,44 +66,96 @@ __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// The plan's long-row rule (csr_plan.hip, classify): raw offsets, len > W.
-template <class I>
-__device__ inline bool row_long(const I *indptr, int64_t r, int64_t W) {
-  return static_cast<int64_t>(indptr[r + 1]) - static_cast<int64_t>(indptr[r]) > W;
-}
+// Virtual rows.  A row is long when it holds more than W values (the
+// row-block plan's rule, csr_plan.hip classify: raw offsets, len > W).  A
+// short row is one virtual row; a long row with its values clamped to
+// [s, e) is max(1, ceil((e - s) / C)) virtual rows of C = min(W, 64)
+// values (the last one shorter).  Every virtual row then holds at most W
+// values, and a chunk, summed by one thread of pass 2, at most 64.
+constexpr int64_t kLongChunk = 64;
+
+__host__ __device__ inline int64_t long_chunk(int64_t W) { return W < kLongChunk ? W : kLongChunk; }
 
 template <class I>
-__device__ inline int64_t tile_key(const I *indptr, int64_t r, int64_t nnz, int64_t H) {
-  return (clamp64(static_cast<int64_t>(indptr[r]), 0, nnz) + r) / H;
+__device__ inline int64_t virtual_count(const I *indptr, int64_t r, int64_t nnz, int64_t W) {
+  const int64_t b = static_cast<int64_t>(indptr[r]);
+  const int64_t e = static_cast<int64_t>(indptr[r + 1]);
+  if (e - b <= W) return 1;
+  const int64_t C = long_chunk(W);
+  const int64_t cs = clamp64(b, 0, nnz);
+  const int64_t ce = clamp64(e, cs, nnz);
+  return std::max<int64_t>(1, (ce - cs + C - 1) / C);
 }
 
-// flag[r] = 1 when short row r starts a tile; flag[n] = 0.
+// count[r] = virtual rows of row r; count[n] = 0.
 template <class I>
 __global__ void __launch_bounds__(kThreads)
-    tile_flags(const I *__restrict__ indptr, int64_t n, int64_t nnz, int64_t W, int64_t H,
-               uint32_t *__restrict__ flag) {
+    vrow_counts(const I *__restrict__ indptr, int64_t n, int64_t nnz, int64_t W,
+                uint32_t *__restrict__ count) {
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r <= n;
+       r += static_cast<int64_t>(gridDim.x) * kThreads)
+    count[r] = r < n ? static_cast<uint32_t>(virtual_count(indptr, r, nnz, W)) : 0u;
+}
+
+// vstart / vslot of the virtual rows of row r (vbase: exclusive prefix of
+// the counts); vstart[n_v] = clamped indptr[n].
+template <class I>
+__global__ void __launch_bounds__(kThreads)
+    vrow_fill(const I *__restrict__ indptr, int64_t n, int64_t nnz, int64_t W,
+              const uint32_t *__restrict__ vbase, uint32_t *__restrict__ vstart,
+              int32_t *__restrict__ vslot) {
+  const int64_t C = long_chunk(W);
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r <= n;
        r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t v = vbase[r];
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
+    if (r == n) {
+      vstart[v] = static_cast<uint32_t>(s);
+      continue;
+    }
+    const int64_t c = vbase[r + 1] - v;
+    const bool is_long = static_cast<int64_t>(indptr[r + 1]) - static_cast<int64_t>(indptr[r]) > W;
+    for (int64_t k = 0; k < c; ++k) {
+      vstart[v + k] = static_cast<uint32_t>(std::min<int64_t>(s + k * C, nnz));
+      vslot[v + k] = is_long ? -1 : static_cast<int32_t>(r);
+    }
+  }
+}
+
+// Row-pointer value of virtual row v clamped to [0, nnz]: indptr when the
+// virtual rows are the rows, vstart otherwise.
+template <class RP>
+__device__ inline int64_t vpos(const RP *rowptr, int64_t v, int64_t nnz) {
+  return clamp64(static_cast<int64_t>(rowptr[v]), 0, nnz);
+}
+
+template <class RP>
+__device__ inline int64_t tile_key(const RP *rowptr, int64_t v, int64_t nnz, int64_t H) {
+  return (vpos(rowptr, v, nnz) + v) / H;
+}
+
+// flag[v] = 1 when virtual row v starts a tile; flag[n_v] = 0.
+template <class RP>
+__global__ void __launch_bounds__(kThreads)
+    tile_flags(const RP *__restrict__ rowptr, int64_t nv, int64_t nnz, int64_t H,
+               uint32_t *__restrict__ flag) {
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; v <= nv;
+       v += static_cast<int64_t>(gridDim.x) * kThreads) {
     bool f = false;
-    if (r < n && !row_long(indptr, r, W))
-      f = r == 0 || row_long(indptr, r - 1, W) ||
-          tile_key(indptr, r, nnz, H) != tile_key(indptr, r - 1, nnz, H);
-    flag[r] = f ? 1u : 0u;
+    if (v < nv) f = v == 0 || tile_key(rowptr, v, nnz, H) != tile_key(rowptr, v - 1, nnz, H);
+    flag[v] = f ? 1u : 0u;
   }
 }
 
 // tile_begin / tile_end from the flags and their exclusive prefix sum.
-template <class I>
 __global__ void __launch_bounds__(kThreads)
-    tile_bounds(const I *__restrict__ indptr, int64_t n, int64_t W, const uint32_t *__restrict__ flag,
-                const uint32_t *__restrict__ tid, int32_t *__restrict__ tile_begin,
-                int32_t *__restrict__ tile_end) {
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n;
-       r += static_cast<int64_t>(gridDim.x) * kThreads) {
-    if (row_long(indptr, r, W)) continue;
-    const uint32_t t = tid[r] + flag[r] - 1u;
-    if (flag[r]) tile_begin[t] = static_cast<int32_t>(r);
-    if (r == n - 1 || row_long(indptr, r + 1, W) || flag[r + 1]) tile_end[t] = static_cast<int32_t>(r + 1);
+    tile_bounds(int64_t nv, const uint32_t *__restrict__ flag, const uint32_t *__restrict__ tid,
+                int32_t *__restrict__ tile_begin, int32_t *__restrict__ tile_end) {
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; v < nv;
+       v += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint32_t t = tid[v] + flag[v] - 1u;
+    if (flag[v]) tile_begin[t] = static_cast<int32_t>(v);
+    if (v == nv - 1 || flag[v + 1]) tile_end[t] = static_cast<int32_t>(v + 1);
   }
 }
 
@@ -110,28 +168,27 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// One thread per short row: sort key and (column in panel | dest << 16) of
-// each of its values.  Values with a column outside [0, n_cols) keep the
-// drop key and are counted.
-template <class I>
+// One thread per virtual row: sort key and (column in panel | dest << 16)
+// of each of its values.  Values with a column outside [0, n_cols) keep
+// the drop key and are counted.
+template <class I, class RP>
 __global__ void __launch_bounds__(kThreads)
-    panel_keys(const I *__restrict__ indices, const I *__restrict__ indptr, int64_t n, int64_t nnz,
-               int64_t n_cols, int64_t W, int64_t PW, int64_t TW, uint32_t n_tiles,
+    panel_keys(const I *__restrict__ indices, const RP *__restrict__ rowptr, int64_t nv,
+               int64_t nnz, int64_t n_cols, int64_t PW, int64_t TW, uint32_t n_tiles,
                const uint32_t *__restrict__ flag, const uint32_t *__restrict__ tid,
                const int32_t *__restrict__ tile_begin, uint32_t *__restrict__ key,
                uint32_t *__restrict__ aux, unsigned long long *__restrict__ dropped) {
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; r < n;
-       r += static_cast<int64_t>(gridDim.x) * kThreads) {
-    if (row_long(indptr, r, W)) continue;
-    const uint32_t t = tid[r] + flag[r] - 1u;
-    const int64_t r0 = tile_begin[t];
-    const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
-    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
-    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; v < nv;
+       v += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint32_t t = tid[v] + flag[v] - 1u;
+    const int64_t v0 = tile_begin[t];
+    const int64_t b0 = vpos(rowptr, v0, nnz);
+    const int64_t s = vpos(rowptr, v, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, nnz);
     unsigned long long lost = 0;
     for (int64_t p = s; p < e; ++p) {
       const int64_t c = static_cast<int64_t>(indices[p]);
-      const int64_t dest = (p - b0) + (r - r0);
+      const int64_t dest = (p - b0) + (v - v0);
       if (c >= 0 && c < n_cols && dest >= 0 && dest < TW) {
         const int64_t q = c / PW;
         key[p] = static_cast<uint32_t>(q * n_tiles + t);
@@ -198,27 +255,27 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Refresh of the copy's values after the matrix's values changed (same
-// indices and indptr): one workgroup per tile.  The tile's rows fill a map
-// from LDS word to (row - first row of the tile); an entry with word d then
-// came from position b0 + d - map[d], the inverse of dest = (p - b0) +
-// (row - r0).  Every panel's segment of the tile is regathered; padding
-// entries (word 0xFFFF, outside every tile) keep their zero.
-template <class S, class I>
+// indices and indptr): one workgroup per tile.  The tile's virtual rows fill
+// a map from LDS word to (virtual row - first of the tile); an entry with
+// word d then came from position b0 + d - map[d], the inverse of dest =
+// (p - b0) + (v - v0).  Every panel's segment of the tile is regathered;
+// padding entries (word 0xFFFF, outside every tile) keep their zero.
+template <class S, class RP>
 __global__ void __launch_bounds__(kThreads)
-    panel_refresh(const S *__restrict__ data, const I *__restrict__ indptr, int64_t nnz,
+    panel_refresh(const S *__restrict__ data, const RP *__restrict__ rowptr, int64_t nnz,
                   const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
                   const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles, int64_t TW,
                   const uint16_t *__restrict__ dest, S *__restrict__ out) {
   __shared__ uint16_t row_of[kTileBytes / 4];  // TW <= 16384 words
   const int64_t t = blockIdx.x;
-  const int64_t r0 = tile_begin[t], r1 = tile_end[t];
-  const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
-  for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
-    const int64_t s = clamp64(static_cast<int64_t>(indptr[r]), 0, nnz);
-    const int64_t e = clamp64(static_cast<int64_t>(indptr[r + 1]), s, nnz);
+  const int64_t v0 = tile_begin[t], v1 = tile_end[t];
+  const int64_t b0 = vpos(rowptr, v0, nnz);
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads) {
+    const int64_t s = vpos(rowptr, v, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, nnz);
     for (int64_t p = s; p < e; ++p) {
-      const int64_t w = (p - b0) + (r - r0);
-      if (w >= 0 && w < TW) row_of[w] = static_cast<uint16_t>(r - r0);
+      const int64_t w = (p - b0) + (v - v0);
+      if (w >= 0 && w < TW) row_of[w] = static_cast<uint16_t>(v - v0);
     }
   }
   __syncthreads();
@@ -266,35 +323,44 @@ msx_status no_memory() {
   return fail(MSX_ENOMEM, "msx_csr_plan_create_bound: device allocation of the panel copy failed.");
 }
 
-template <class V, class I>
-msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_v,
-                       const void *indptr_v, hipStream_t stream) {
+// Exclusive prefix sum of n + 1 counts (the last one 0) into out; returns
+// the total through *total (host).
+msx_status exclusive_scan(Scratch &tmp, const uint32_t *in, uint32_t *out, int64_t n,
+                          uint32_t *total, hipStream_t stream) {
+  size_t bytes = 0;
+  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, in, out, static_cast<int>(n + 1), stream));
+  void *scratch = nullptr;
+  if (!tmp.alloc(&scratch, bytes)) return no_memory();
+  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(scratch, bytes, in, out, static_cast<int>(n + 1), stream));
+  MSX_HIP_TRY(hipMemcpyAsync(total, out + n, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+  MSX_HIP_TRY(hipStreamSynchronize(stream));
+  return MSX_OK;
+}
+
+// The layout over nv virtual rows delimited by rowptr (RP = the index type
+// when the virtual rows are the rows, uint32_t for the virtual-row starts).
+template <class V, class I, class RP>
+msx_status build_layout(msx_csr_plan *p, const typename V::Storage *data, const I *indices,
+                        const RP *rowptr, int64_t nv, hipStream_t stream) {
   using S = typename V::Storage;
   using A = typename V::Acc;
-  const auto *data = static_cast<const S *>(data_v);
-  const auto *indices = static_cast<const I *>(indices_v);
-  const auto *indptr = static_cast<const I *>(indptr_v);
-  const int64_t n = p->n_rows, nnz = p->nnz, W = p->block_nnz;
+  const int64_t nnz = p->nnz, W = p->block_nnz;
   const int64_t PW = kPanelBytes / static_cast<int64_t>(sizeof(A));
   const int64_t TW = kTileBytes / static_cast<int64_t>(sizeof(A));
   const int64_t H = TW - W;
   const int64_t P = (p->n_cols + PW - 1) / PW;
+  const int64_t n = nv;
   Scratch tmp{{}, stream};
 
   // Tiles.
   uint32_t *flag = nullptr, *tid = nullptr;
   if (!tmp.alloc(&flag, sizeof(uint32_t) * (n + 1)) || !tmp.alloc(&tid, sizeof(uint32_t) * (n + 1)))
     return no_memory();
-  hipLaunchKernelGGL((tile_flags<I>), dim3(grid_for(n + 1)), dim3(kThreads), 0, stream, indptr, n,
-                     nnz, W, H, flag);
+  hipLaunchKernelGGL((tile_flags<RP>), dim3(grid_for(n + 1)), dim3(kThreads), 0, stream, rowptr, n,
+                     nnz, H, flag);
   MSX_HIP_TRY(hipGetLastError());
-  size_t scan_bytes = 0;
-  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, flag, tid, static_cast<int>(n + 1), stream));
-  void *scan_tmp = nullptr;
-  if (!tmp.alloc(&scan_tmp, scan_bytes)) return no_memory();
-  MSX_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(scan_tmp, scan_bytes, flag, tid, static_cast<int>(n + 1), stream));
   uint32_t n_tiles_u = 0;
-  MSX_HIP_TRY(hipMemcpyAsync(&n_tiles_u, tid + n, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+  MSX_TRY_STATUS(exclusive_scan(tmp, flag, tid, n, &n_tiles_u, stream));
   MSX_HIP_TRY(hipStreamSynchronize(stream));
   const int64_t n_tiles = n_tiles_u;
   if (n_tiles == 0) return MSX_OK;
@@ -324,8 +390,8 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   p->pn_seg = reinterpret_cast<uint32_t *>(meta + 2 * b_tb);
   p->pn_chunk_begin = reinterpret_cast<int64_t *>(meta + 2 * b_tb + b_seg);
   p->pn_chunk_panel = reinterpret_cast<int32_t *>(meta + 2 * b_tb + b_seg + b_cb);
-  hipLaunchKernelGGL((tile_bounds<I>), dim3(grid_for(n)), dim3(kThreads), 0, stream, indptr, n, W, flag,
-                     tid, p->pn_tile_begin, p->pn_tile_end);
+  hipLaunchKernelGGL(tile_bounds, dim3(grid_for(n)), dim3(kThreads), 0, stream, n, flag, tid,
+                     p->pn_tile_begin, p->pn_tile_end);
   MSX_HIP_TRY(hipGetLastError());
 
   // Keys, stable sort, segment starts.
@@ -339,8 +405,8 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   hipLaunchKernelGGL(fill_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, nnz,
                      static_cast<uint32_t>(n_keys), key, pos);
   MSX_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL((panel_keys<I>), dim3(grid_for(n)), dim3(kThreads), 0, stream, indices, indptr, n,
-                     nnz, p->n_cols, W, PW, TW, static_cast<uint32_t>(n_tiles), flag, tid,
+  hipLaunchKernelGGL((panel_keys<I, RP>), dim3(grid_for(n)), dim3(kThreads), 0, stream, indices,
+                     rowptr, n, nnz, p->n_cols, PW, TW, static_cast<uint32_t>(n_tiles), flag, tid,
                      p->pn_tile_begin, key, aux, dropped);
   MSX_HIP_TRY(hipGetLastError());
   const int end_bit = bits_for(static_cast<uint64_t>(n_keys));
@@ -383,18 +449,37 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   const int64_t n_values = pb[P];
   const int64_t n_kept = n_kept_u;
 
-  // Pass-1 chunks: about one per CU (C in total, at least kMinChunk values
-  // each), never across a panel boundary.  Panel q gets round(C * len / total)
-  // chunks, at least one: a panel holding a few values more than its share
-  // must not add a chunk, or the grid spills into a second, nearly empty
-  // round of workgroups.  The total stays within C + P / 2 + 1 <= CUs + P.
+  // Pass-1 chunks: one workgroup per CU fits (its x panel fills the LDS),
+  // so the grid is C = min(CUs, values / kMinChunk) chunks - never more, or
+  // it spills into a second, nearly empty round - split at panel
+  // boundaries: panel q gets floor(C * len / total) chunks, at least one,
+  // and the chunks left over go to the largest remainders.  With more
+  // non-empty panels than C, each gets one.
   const int64_t C = std::max<int64_t>(1, std::min<int64_t>(cus, n_values / kMinChunk));
+  std::vector<int64_t> per(static_cast<size_t>(P), 0), rem(static_cast<size_t>(P), -1);
+  int64_t given = 0;
+  for (int64_t q = 0; q < P; ++q) {
+    const int64_t len = static_cast<int64_t>(pb[q + 1]) - static_cast<int64_t>(pb[q]);
+    if (len <= 0) continue;
+    per[q] = std::max<int64_t>(1, C * len / n_values);
+    rem[q] = C * len % n_values;
+    given += per[q];
+  }
+  while (given < C) {
+    int64_t best = -1;
+    for (int64_t q = 0; q < P; ++q)
+      if (rem[q] >= 0 && (best < 0 || rem[q] > rem[best])) best = q;
+    if (best < 0) break;
+    ++per[best];
+    rem[best] = -1;
+    ++given;
+  }
   std::vector<int64_t> cbeg;
   std::vector<int32_t> cpan;
   for (int64_t q = 0; q < P; ++q) {
     const int64_t a = pb[q], b = pb[q + 1];
     if (b <= a) continue;
-    const int64_t c = std::max<int64_t>(1, (2 * C * (b - a) + n_values) / (2 * n_values));
+    const int64_t c = per[q];
     for (int64_t i = 0; i < c; ++i) {
       cbeg.push_back(a + (((b - a) * i / c) & ~int64_t{3}));
       cpan.push_back(static_cast<int32_t>(q));
@@ -439,17 +524,72 @@ msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_
   p->pn_values = n_values;
   p->pn_chunks = n_chunks;
   p->pn_dropped = lost != 0;
+  p->pn_vrows = nv;
   return prepare_spmv_panels(p);
+}
+
+template <class V, class I>
+msx_status build_typed(msx_csr_plan *p, const void *data_v, const void *indices_v,
+                       const void *indptr_v, hipStream_t stream) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  const auto *data = static_cast<const S *>(data_v);
+  const auto *indices = static_cast<const I *>(indices_v);
+  const auto *indptr = static_cast<const I *>(indptr_v);
+  const int64_t n = p->n_rows, nnz = p->nnz, W = p->block_nnz;
+  if (p->n_long == 0) return build_layout<V, I, I>(p, data, indices, indptr, n, stream);
+
+  // Virtual rows: long rows cut into chunks of W values.
+  uint32_t nv_u = 0;
+  uint32_t *count = nullptr, *vbase = nullptr;
+  {
+    Scratch tmp{{}, stream};
+    if (!tmp.alloc(&count, sizeof(uint32_t) * (n + 1)) || !tmp.alloc(&vbase, sizeof(uint32_t) * (n + 1)))
+      return no_memory();
+    hipLaunchKernelGGL((vrow_counts<I>), dim3(grid_for(n + 1)), dim3(kThreads), 0, stream, indptr, n,
+                       nnz, W, count);
+    MSX_HIP_TRY(hipGetLastError());
+    MSX_TRY_STATUS(exclusive_scan(tmp, count, vbase, n, &nv_u, stream));
+    const int64_t nv = nv_u;
+    const size_t b_base = round256(sizeof(uint32_t) * (n + 1));
+    const size_t b_start = round256(sizeof(uint32_t) * (nv + 1));
+    const size_t b_slot = round256(sizeof(int32_t) * std::max<int64_t>(nv, 1));
+    const size_t b_part = round256(sizeof(A) * std::max<int64_t>(nv, 1));
+    char *vm = nullptr;
+    if (hipMalloc(&vm, b_base + b_start + b_slot + b_part) != hipSuccess) {
+      (void)hipGetLastError();
+      return no_memory();
+    }
+    p->pn_vmeta = vm;
+    p->pn_bytes += b_base + b_start + b_slot + b_part;
+    p->pn_vbase = reinterpret_cast<uint32_t *>(vm);
+    p->pn_vstart = reinterpret_cast<uint32_t *>(vm + b_base);
+    p->pn_vslot = reinterpret_cast<int32_t *>(vm + b_base + b_start);
+    p->pn_partial = vm + b_base + b_start + b_slot;
+    MSX_HIP_TRY(hipMemcpyAsync(p->pn_vbase, vbase, sizeof(uint32_t) * (n + 1),
+                               hipMemcpyDeviceToDevice, stream));
+    hipLaunchKernelGGL((vrow_fill<I>), dim3(grid_for(n + 1)), dim3(kThreads), 0, stream, indptr, n,
+                       nnz, W, p->pn_vbase, p->pn_vstart, p->pn_vslot);
+    MSX_HIP_TRY(hipGetLastError());
+  }
+  return build_layout<V, I, uint32_t>(p, data, indices, p->pn_vstart, nv_u, stream);
 }
 
 template <class V, class I>
 msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) {
   using S = typename V::Storage;
   if (p->n_tiles == 0 || p->pn_values == 0) return MSX_OK;
-  hipLaunchKernelGGL((panel_refresh<S, I>), dim3(static_cast<uint32_t>(p->n_tiles)), dim3(kThreads), 0,
-                     stream, static_cast<const S *>(data), static_cast<const I *>(p->indptr), p->nnz,
-                     p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels, p->n_tiles,
-                     p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
+  if (p->pn_vstart != nullptr)
+    hipLaunchKernelGGL((panel_refresh<S, uint32_t>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                       dim3(kThreads), 0, stream, static_cast<const S *>(data), p->pn_vstart, p->nnz,
+                       p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels, p->n_tiles,
+                       p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
+  else
+    hipLaunchKernelGGL((panel_refresh<S, I>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                       dim3(kThreads), 0, stream, static_cast<const S *>(data),
+                       static_cast<const I *>(p->indptr), p->nnz, p->pn_tile_begin, p->pn_tile_end,
+                       p->pn_seg, p->n_panels, p->n_tiles, p->tile_words, p->pn_dest,
+                       static_cast<S *>(p->pn_data));
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
 }
@@ -484,8 +624,11 @@ bool panels_eligible(const msx_csr_plan *p) {
   const int64_t PW = kPanelBytes / a, TW = kTileBytes / a, H = TW - p->block_nnz;
   const int64_t P = (p->n_cols + PW - 1) / PW;
   if (P > kMaxPanels || H <= 0) return false;
-  // Tiles: key windows of the word range, plus one break per long row.
-  const int64_t tiles_max = (p->nnz + p->n_rows) / H + 2 + p->n_long;
+  // Virtual rows (int32 tile bounds): the rows plus the extra chunks of
+  // long rows.  Tiles: key windows of the word range.
+  const int64_t nv_max = p->n_rows + p->nnz / long_chunk(p->block_nnz) + p->n_long;
+  const int64_t tiles_max = (p->nnz + nv_max) / H + 2;
+  if (nv_max >= (int64_t{1} << 31) - 1) return false;
   // Segment keys and padded copy offsets are 32-bit.
   return P * tiles_max + 1 < (int64_t{1} << 32) && p->nnz + 3 * P * tiles_max < (int64_t{1} << 32);
 }

@@ -321,6 +321,7 @@ void release(msx_csr_plan *p) {
   if (p->s_base) (void)hipFree(p->s_base);
   if (p->pn_base) (void)hipFree(p->pn_base);
   if (p->pn_meta) (void)hipFree(p->pn_meta);
+  if (p->pn_vmeta) (void)hipFree(p->pn_vmeta);
   if (p->win) (void)hipFree(p->win);
   if (p->ls_base) (void)hipFree(p->ls_base);
   delete p;
@@ -367,19 +368,18 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
   auto s = static_cast<hipStream_t>(stream);
   int mode = opts->slice_mode;
   if (mode == MSX_SLICE_AUTO) {
-    // Scattered short rows over a large x: LDS panels when the short rows
-    // hold enough values to give every compute unit a pass-1 chunk (the
-    // 4M-row random matrix: 302 -> 221 us against 930 us in row blocks);
-    // XCD slices when x is 16 MB or more and panels are not possible.
-    // Otherwise row blocks: the power-law matrix (x 8.4 MB, about half of
-    // its values in long rows) runs 218 us in row blocks, 236 us sliced and
-    // 257 us in panels.
+    // Scattered short rows over a large x: LDS panels (long rows ride in
+    // them as 64-value virtual rows) when the matrix holds enough values to
+    // give every compute unit a pass-1 chunk - the 4M-row random matrix:
+    // 221 us against 930 us in row blocks; the power-law matrix (x 8.4 MB,
+    // about half of its values in long rows): 92 us against 157 us; XCD
+    // slices when x is 16 MB or more and panels are not possible.
     bool scattered = false;
     int64_t short_values = 0;
     st = probe_scattered(p, indices, s, &scattered, &short_values);
     const int64_t x_bytes = n_cols * static_cast<int64_t>(value_bytes(vt));
     mode = MSX_SLICE_OFF;
-    if (scattered && panels_eligible(p) && short_values >= panels_min_values(p->device))
+    if (scattered && panels_eligible(p) && p->nnz >= panels_min_values(p->device))
       mode = MSX_SLICE_PANELS;
     else if (scattered && x_bytes >= (int64_t{16} << 20))
       mode = MSX_SLICE_ON;
@@ -395,7 +395,8 @@ extern "C" msx_status msx_csr_plan_create_bound(msx_vtype vt, msx_itype it, int6
     st = build_slices(p, data, indices, indptr, s);
   }
   if (st == MSX_OK) st = build_windows(p, indices, indptr, s);
-  if (st == MSX_OK) st = build_long_slices(p, indices, indptr, s);
+  // long rows in a panel layout need no sliced pieces
+  if (st == MSX_OK && p->pn_vstart == nullptr) st = build_long_slices(p, indices, indptr, s);
   if (st != MSX_OK) {
     release(p);
     return st;

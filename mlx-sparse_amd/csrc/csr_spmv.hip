@@ -64,18 +64,6 @@ __device__ inline int32_t block_offset(int64_t v, int64_t p0, int64_t p1, int64_
   return static_cast<int32_t>(clamp64(v, p0, p1) - a0);
 }
 
-// 0 <= col < n_cols.  An int32 column compares as unsigned against
-// lim32 = min(n_cols, 2^31), which also rejects negative columns.
-__device__ inline bool col_ok(int32_t col, int64_t, uint32_t lim32) {
-  return static_cast<uint32_t>(col) < lim32;
-}
-__device__ inline bool col_ok(int64_t col, int64_t n_cols, uint32_t) {
-  return static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
-}
-__host__ __device__ inline uint32_t col_limit32(int64_t n_cols) {
-  return n_cols >= 0x80000000LL ? 0x80000000u : (n_cols > 0 ? static_cast<uint32_t>(n_cols) : 0u);
-}
-
 __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -196,14 +184,27 @@ __global__ void __launch_bounds__(kThreads)
                 const int64_t *__restrict__ ls_begin, const int32_t *__restrict__ ls_len,
                 const int32_t *__restrict__ ls_slot, const int32_t *__restrict__ ls_slice_begin,
                 typename V::Acc *__restrict__ ls_partial) {
+  // FUSE: workgroups come in octets (workgroup g runs on XCD g % 8); the
+  // long_groups / 8 long-piece octets are spread evenly through the grid,
+  // so both kinds of work run side by side for the whole launch.
+  uint32_t gid = blockIdx.x;
+  uint32_t ngroups = gridDim.x;
   if constexpr (FUSE) {
-    if (blockIdx.x < long_groups) {
+    const uint64_t n_oct = gridDim.x / kNumXcd;
+    const uint64_t long_oct = long_groups / kNumXcd;
+    const uint64_t oct = blockIdx.x / kNumXcd;
+    const uint64_t before = oct * long_oct / n_oct;  // long octets before this one
+    const bool is_long = (oct + 1) * long_oct / n_oct > before;
+    if (is_long) {
       long_pieces<V, I, AUX>(data, indices, x, x_bytes, n_cols, ls_begin, ls_len, ls_slot,
-                             ls_slice_begin, ls_partial, blockIdx.x, long_groups);
+                             ls_slice_begin, ls_partial,
+                             static_cast<uint32_t>(before) * kNumXcd + blockIdx.x % kNumXcd,
+                             long_groups);
       return;
     }
+    gid = static_cast<uint32_t>(oct - before) * kNumXcd + blockIdx.x % kNumXcd;
+    ngroups = gridDim.x - long_groups;
   }
-  using S = typename V::Storage;
   using A = typename V::Acc;
   // A block spans < 2W values; with the 4-aligned start, <= W/2 + 1 quads.
   // The lanes hold the first QPL * 64 of them (W/2 when W >= 128); the one
@@ -223,8 +224,6 @@ __global__ void __launch_bounds__(kThreads)
   int32_t *rptr = lds_ptr[wave];
   const uint32_t lim32 = col_limit32(n_cols);
 
-  const uint32_t gid = FUSE ? blockIdx.x - long_groups : blockIdx.x;
-  const uint32_t ngroups = FUSE ? gridDim.x - long_groups : gridDim.x;
   const uint32_t first = xcd_remap(gid, ngroups);
   for (int64_t wg = first; wg * kWavesPerGroup < n_bounds; wg += ngroups) {
     const int64_t b = wg * kWavesPerGroup + wave;
@@ -518,6 +517,7 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   const uint32_t x_bytes = gather_bytes(x, n_cols, sizeof(S));
   if (use_plan && plan->n_panels > 0) {
     MSX_HIP_TRY_ST(launch_spmv_panels(plan, indptr, x, y, stream));
+    if (plan->pn_vstart != nullptr) return MSX_OK;  // long rows are in the panel layout too
   } else if (use_plan && plan->n_slices > 0) {
     MSX_HIP_TRY_ST(launch_spmv_sliced(plan, x, y, stream));
   } else if (use_plan) {
@@ -529,8 +529,11 @@ msx_status spmv_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
           fuse ? static_cast<uint32_t>(kSlices * std::max<int64_t>(1, std::min<int64_t>(
                      (plan->ls_slice_max + kWavesPerGroup - 1) / kWavesPerGroup, kMaxGrid / 64)))
                : 0u;
-      const dim3 grid(long_groups + std::min(grid_for(groups), kMaxGrid - long_groups)),
-          block(kThreads);
+      // fused: the short-block workgroups are a multiple of 8 too, so the
+      // grid is whole octets
+      uint32_t short_groups = std::min(grid_for(groups), kMaxGrid - long_groups);
+      if (fuse) short_groups = (short_groups + kNumXcd - 1) / kNumXcd * kNumXcd;
+      const dim3 grid(long_groups + short_groups), block(kThreads);
       A *ls_partial = static_cast<A *>(plan->ls_partial);
 #define MSX_SPMV_BLOCKS(WV)                                                                   \
   do {                                                                                         \

@@ -170,6 +170,19 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint64_t nu
 // own 32-bit register.
 constexpr uint64_t kGatherMaxBytes = 0xfffffff0ull;
 
+// 0 <= col < n_cols.  An int32 column compares as unsigned against
+// lim32 = col_limit32(n_cols) = min(n_cols, 2^31), which also rejects
+// negative columns; an int64 column compares against n_cols.
+__device__ inline bool col_ok(int32_t col, int64_t, uint32_t lim32) {
+  return static_cast<uint32_t>(col) < lim32;
+}
+__device__ inline bool col_ok(int64_t col, int64_t n_cols, uint32_t) {
+  return static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+}
+__host__ __device__ inline uint32_t col_limit32(int64_t n_cols) {
+  return n_cols >= 0x80000000LL ? 0x80000000u : (n_cols > 0 ? static_cast<uint32_t>(n_cols) : 0u);
+}
+
 // Raw bits of x[col] (the holding dword for 16-bit elements), zero when !ok.
 template <class S>
 using GatherRaw = typename std::conditional<sizeof(S) == 8, uint64_t, uint32_t>::type;

@@ -85,9 +85,10 @@ struct msx_csr_plan {
   void *s_base;
   size_t s_bytes;
   // Column panels (csr_panel.hip, csr_panel_build.hip); n_panels == 0 when
-  // the plan has none.  Values of short rows with a valid column, ordered by
-  // (panel, tile, stored position): segment (panel q, tile t) is
-  // [pn_seg[q * n_tiles + t], pn_seg[q * n_tiles + t + 1]).
+  // the plan has none.  The tiles are built over virtual rows: every short
+  // row, and every chunk of block_nnz values of a long row.  Values with a
+  // valid column, ordered by (panel, tile, stored position): segment (panel
+  // q, tile t) is [pn_seg[q * n_tiles + t], pn_seg[q * n_tiles + t + 1]).
   int64_t n_panels;
   int64_t panel_width;        // columns per panel (LDS-resident in pass 1)
   int64_t n_tiles;
@@ -106,6 +107,18 @@ struct msx_csr_plan {
   void *pn_prod;              // pn_values accumulator-type products (pass 1 -> pass 2)
   void *pn_base;              // allocation of pn_data, pn_col, pn_dest, pn_prod
   void *pn_meta;              // allocation of the tile, segment and chunk arrays
+  // Virtual rows when the matrix has long rows (all null otherwise: then the
+  // virtual rows are the rows, delimited by indptr).  Virtual row v spans
+  // values [pn_vstart[v], pn_vstart[v + 1]); pn_vslot[v] is its row when
+  // it is a short row, -1 for a chunk of a long row, whose sum pass 2
+  // writes to pn_partial[v]; long row r owns virtual rows
+  // [pn_vbase[r], pn_vbase[r + 1]).
+  int64_t pn_vrows;           // virtual rows (n_rows without long rows)
+  uint32_t *pn_vstart;        // pn_vrows + 1
+  int32_t *pn_vslot;          // pn_vrows
+  uint32_t *pn_vbase;         // n_rows + 1
+  void *pn_partial;           // pn_vrows accumulators
+  void *pn_vmeta;             // allocation of the four arrays above
   size_t pn_bytes;
   // Column windows of bound plans (csr_spmm.hip): for row tile t (rows
   // [32t, 32t + 32)), win[2t] and win[2t + 1] are the lowest and highest

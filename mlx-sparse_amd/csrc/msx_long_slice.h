@@ -38,6 +38,7 @@ __device__ __attribute__((always_inline)) inline void long_pieces(const typename
   const int64_t u1 = ls_slice_begin[s + 1];
   const int64_t step = static_cast<int64_t>(ngroups / kSlices) * kLongWavesPerGroup;
   const auto rx = make_rsrc(x, x_bytes);
+  const uint32_t lim32 = col_limit32(n_cols);
   for (int64_t u = ls_slice_begin[s] + static_cast<int64_t>(gid / kSlices) * kLongWavesPerGroup + wave;
        u < u1; u += step) {
     const int64_t pb = ls_begin[u];
@@ -54,15 +55,18 @@ __device__ __attribute__((always_inline)) inline void long_pieces(const typename
       iq[j] = load_quad<I, AUX>(ri, q * 4u * sizeof(I));
       dq[j] = load_quad<S, AUX>(rd, q * 4u * sizeof(S));
     }
+    // positions as offsets from a0: the piece is [lo, hi), hi <= 1023
+    const uint32_t lo = static_cast<uint32_t>(pb - a0);
+    const uint32_t span = static_cast<uint32_t>(pe - pb);
     GatherRaw<S> raw[kPieceQuads][4];
     bool ok[kPieceQuads][4];
 #pragma unroll
     for (int j = 0; j < kPieceQuads; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t pos = a0 + 4 * (lane + j * kWave) + e;
-        const int64_t col = static_cast<int64_t>(iq[j].v[e]);
-        ok[j][e] = pos >= pb && pos < pe && static_cast<uint64_t>(col) < static_cast<uint64_t>(n_cols);
+        const uint32_t off = 4u * static_cast<uint32_t>(lane + j * kWave) + e;
+        const I col = iq[j].v[e];
+        ok[j][e] = off - lo < span && col_ok(col, n_cols, lim32);
         raw[j][e] = gather_raw<S>(rx, x_bytes, static_cast<uint32_t>(col), ok[j][e]);
       }
     __builtin_amdgcn_sched_barrier(0);

@@ -23,14 +23,21 @@ The column-panel layout of a bound plan (csr_panel_build.hip; exported by
 - x is cut into panels of PW = 131072 / acc_bytes columns (acc_bytes = 4 for
   float32/float16/bfloat16, 8 for complex64); tiles hold at most
   TW = 65536 / acc_bytes LDS words; H = TW - W;
-- a short row (len(r) <= W) starts a tile when r == 0, row r-1 is long, or
-  floor((s(r) + r) / H) != floor((s(r-1) + r-1) / H), s(r) = indptr[r]
-  clamped to [0, nnz]; a tile runs to the next tile start or long row;
-- every value p of a short row with a column c in [0, n_cols) and an LDS word
-  (p - s(first row of its tile)) + (r - first row) below TW gets the segment
+- virtual rows: a short row (len(r) <= W) is one, spanning [s(r), e(r)),
+  s(r) = indptr[r] clamped to [0, nnz], e(r) = max(clamped indptr[r+1],
+  s(r)); a long row is max(1, ceil((e(r) - s(r)) / C)) of them,
+  C = min(W, 64), chunk k starting at min(s(r) + k C, nnz).  Virtual row v spans [vs(v), ve(v)),
+  ve(v) = max(vs(v+1), vs(v)) with vs(n_v) = s(n);
+- virtual row v starts a tile when v == 0 or
+  floor((vs(v) + v) / H) != floor((vs(v-1) + v-1) / H); a tile runs to the
+  next tile start (tile bounds are virtual-row numbers);
+- every value p of virtual row v with a column c in [0, n_cols) and an LDS
+  word (p - vs(first of its tile)) + (v - first) below TW gets the segment
   key floor(c / PW) * n_tiles + tile; segment k holds the values with key k
   padded to a multiple of 4 entries, so ``seg_begin[k]`` is the sum over
   keys k' < k of ceil(count(k') / 4) * 4 (k = 0 .. n_panels * n_tiles).
+
+Without long rows the virtual rows are the rows.
 
 Pinned by ``panel_layout_loop`` (plain per-row loops) and by the tile and
 segment invariants in the same test file.
@@ -42,6 +49,7 @@ import numpy as np
 
 
 LONG_FLAG = 1 << 31
+LONG_CHUNK = 64  # values per virtual row of a long row in the panel layout
 
 
 def plan(indptr, W: int = 256, R: int = 256, C: int = 4096):
@@ -94,6 +102,25 @@ def panel_constants(acc_bytes: int, W: int):
     return PW, TW, TW - W
 
 
+def virtual_rows(indptr, nnz: int, W: int = 256):
+    """(vs, ve, row) of the virtual rows: starts, ends and owning row."""
+    p = np.asarray(indptr, dtype=np.int64)
+    n = len(p) - 1
+    s = np.clip(p[:-1], 0, nnz)
+    e = np.maximum(np.clip(p[1:], 0, nnz), s)
+    long_ = (p[1:] - p[:-1]) > W
+    C = min(W, LONG_CHUNK)
+    count = np.where(long_, np.maximum(1, -(-(e - s) // C)), 1)
+    vbase = np.concatenate([[0], np.cumsum(count)]).astype(np.int64)
+    nv = int(vbase[-1])
+    row = np.repeat(np.arange(n, dtype=np.int64), count)
+    k = np.arange(nv, dtype=np.int64) - vbase[row]
+    vs = np.minimum(s[row] + k * C, nnz)
+    vs_full = np.concatenate([vs, [np.clip(p[n], 0, nnz)]]) if n > 0 else np.zeros(1, np.int64)
+    ve = np.maximum(vs_full[1:], vs)
+    return vs.astype(np.int64), ve.astype(np.int64), row
+
+
 def panel_layout(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int = 256):
     """Returns (tile_begin, tile_end, seg_begin) as int64 arrays."""
     PW, TW, H = panel_constants(acc_bytes, W)
@@ -102,28 +129,23 @@ def panel_layout(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int = 256)
     n, nnz = len(p) - 1, len(idx)
     if n == 0:
         return np.zeros(0, np.int64), np.zeros(0, np.int64), np.zeros(1, np.int64)
-    rows = np.arange(n, dtype=np.int64)
-    long_ = (p[1:] - p[:-1]) > W
-    s = np.clip(p[:-1], 0, nnz)
-    e = np.maximum(np.clip(p[1:], 0, nnz), s)
-    key = (s + rows) // H
-    start = ~long_.copy()
-    start[1:] &= long_[:-1] | (key[1:] != key[:-1])
-    tile_begin = rows[start]
-    nxt_break = np.ones(n, bool)
-    nxt_break[:-1] = long_[1:] | start[1:]
-    tile_end = rows[~long_ & nxt_break] + 1
+    vs, ve, _ = virtual_rows(p, nnz, W)
+    nv = len(vs)
+    v = np.arange(nv, dtype=np.int64)
+    key = (vs + v) // H
+    start = np.ones(nv, bool)
+    start[1:] = key[1:] != key[:-1]
+    tile_begin = v[start]
+    tile_end = np.concatenate([tile_begin[1:], [nv]])
     n_tiles = len(tile_begin)
     P = -(-n_cols // PW) if n_cols > 0 else 0
     tile_of = np.cumsum(start) - 1
-    short_rows = rows[~long_]
-    lens = (e - s)[~long_]
-    pos = np.concatenate([np.arange(a, b) for a, b in zip(s[~long_], e[~long_])]) \
-        if len(short_rows) else np.zeros(0, np.int64)
-    r_of = np.repeat(short_rows, lens)
-    T = tile_of[r_of]
+    lens = ve - vs
+    pos = np.concatenate([np.arange(a, b) for a, b in zip(vs, ve)]) if nv else np.zeros(0, np.int64)
+    v_of = np.repeat(v, lens)
+    T = tile_of[v_of]
     first = tile_begin[T]
-    dest = (pos - s[first]) + (r_of - first)
+    dest = (pos - vs[first]) + (v_of - first)
     c = idx[pos] if len(pos) else np.zeros(0, np.int64)
     ok = (c >= 0) & (c < n_cols) & (dest >= 0) & (dest < TW)
     counts = np.bincount((c[ok] // PW) * n_tiles + T[ok], minlength=P * n_tiles)
@@ -141,29 +163,36 @@ def panel_layout_loop(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int =
     def clamp(v):
         return min(max(v, 0), nnz)
 
-    tiles = []  # [first, last + 1]
-    prev_long, prev_key = True, None
+    starts = []  # virtual-row starts, then the end sentinel
     for r in range(n):
-        is_long = p[r + 1] - p[r] > W
-        key = (clamp(p[r]) + r) // H
-        if is_long:
-            prev_long = True
-            continue
-        if prev_long or key != prev_key:
-            tiles.append([r, r + 1])
+        s, e = clamp(p[r]), max(clamp(p[r + 1]), clamp(p[r]))
+        if p[r + 1] - p[r] > W:
+            C = min(W, LONG_CHUNK)
+            for k in range(max(1, (e - s + C - 1) // C)):
+                starts.append(min(s + k * C, nnz))
         else:
-            tiles[-1][1] = r + 1
-        prev_long, prev_key = False, key
+            starts.append(s)
+    nv = len(starts)
+    starts.append(clamp(p[n]) if n > 0 else 0)
+    tiles = []  # [first, last + 1]
+    prev_key = None
+    for v in range(nv):
+        key = (starts[v] + v) // H
+        if v == 0 or key != prev_key:
+            tiles.append([v, v + 1])
+        else:
+            tiles[-1][1] = v + 1
+        prev_key = key
     n_tiles = len(tiles)
     P = -(-n_cols // PW) if n_cols > 0 else 0
     counts = [0] * (P * n_tiles)
-    for t, (r0, r1) in enumerate(tiles):
-        b0 = clamp(p[r0])
-        for r in range(r0, r1):
-            s = clamp(p[r])
-            e = max(clamp(p[r + 1]), s)
+    for t, (v0, v1) in enumerate(tiles):
+        b0 = starts[v0]
+        for v in range(v0, v1):
+            s = starts[v]
+            e = max(starts[v + 1], s)
             for q in range(s, e):
-                c, dest = idx[q], (q - b0) + (r - r0)
+                c, dest = idx[q], (q - b0) + (v - v0)
                 if 0 <= c < n_cols and 0 <= dest < TW:
                     counts[(c // PW) * n_tiles + t] += 1
     seg = [0]

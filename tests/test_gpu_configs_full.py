@@ -131,16 +131,36 @@ def test_cfg2_random16_through_api(gpu):
     assert _kind(info) == "panels"
 
 
-def test_cfg3_power_law_int64(gpu):
-    """Row blocks plus the XCD-sliced long rows in the same launch (x is
-    8 MB, every long row sorted)."""
+@pytest.fixture(scope="module")
+def power_law():
     from mlx_sparse import synthetic
 
-    m = synthetic.power_law(1 << 21, 2.0, 200_000, seed=0)
+    return synthetic.power_law(1 << 21, 2.0, 200_000, seed=0)
+
+
+def test_cfg3_power_law_int64(gpu, power_law):
+    """LDS panels with the long rows as 64-value virtual rows (AUTO's
+    choice): every short row equal to the oracle."""
+    from mlx_sparse import synthetic
+
+    m = power_law
     assert m.indices.dtype == np.int64
     x = synthetic.uniform(m.shape[1], 0.0, 1.0, seed=1)
-    # rows of blocks summed one lane per row in stored order: equal
     info = _spmv_check(gpu, m, m.data, x, "float32", "cfg3 power law 2M", exact_max_len=256)
+    assert _kind(info) == "panels" and info["n_long_rows"] > 1000
+
+
+def test_cfg3_power_law_row_blocks(gpu, power_law):
+    """The same matrix with the panel copy off: row blocks plus the
+    XCD-sliced long rows in the same launch (x is 8 MB, every long row
+    sorted); rows of blocks summed one lane per row in stored order equal."""
+    from mlx_sparse import runtime, synthetic
+
+    m = power_law
+    x = synthetic.uniform(m.shape[1], 0.0, 1.0, seed=1)
+    with runtime.context(gpu_slice="off"):
+        info = _spmv_check(gpu, m, m.data, x, "float32", "cfg3 power law 2M blocks",
+                           exact_max_len=256)
     assert _kind(info) == "blocks" and info["n_long_rows"] > 1000
 
 

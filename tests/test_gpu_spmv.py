@@ -532,7 +532,7 @@ def test_panel_plan_parity(vtype, index_dtype):
     lengths[rng.random(n_rows) < 0.1] = 0
     few = rng.random(n_rows) < 0.1
     lengths[few] = rng.integers(1, 5, int(few.sum()))  # the 1..4-value rule
-    lengths[[17, 2000, 8999]] = [3000, 9000, 700]  # long rows keep the row-block path
+    lengths[[17, 2000, 8999]] = [3000, 9000, 700]  # long rows: chunks of W values in the tiles
     indices, indptr, nnz = _random_csr(rng, n_rows, n_cols, lengths, index_dtype)
     data, x = _values(rng, nnz, vtype), _values(rng, n_cols, vtype)
     data[::53] = storage(np.array([-0.0]), vtype)[0] if vtype != "complex64" else data[::53]
@@ -558,6 +558,18 @@ def test_panel_plan_parity(vtype, index_dtype):
             got = to_numpy(y)
             _assert_short_rows_equal(got, want, lengths, W, vtype, f"panels {vtype} W={W}")
             assert_rows_close(got, want, scale, vtype, f"panels {vtype} W={W}")
+        # new values in the same buffer: the copy (long-row chunks included)
+        # is regathered through the layout
+        data2 = _values(rng, nnz, vtype)
+        d.copy_(to_torch(data2, vtype, DEV))
+        plan.refresh(d)
+        want2 = orc.csr_matvec(data2, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+        scale2 = orc.row_scale(data2, indices, indptr, x, n_rows, vtype=vtype)
+        got = to_numpy(_capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan))
+        _assert_short_rows_equal(got, want2, lengths, W, vtype, f"panels refreshed {vtype} W={W}")
+        assert_rows_close(got, want2, scale2, vtype, f"panels refreshed {vtype} W={W}")
+        d.copy_(to_torch(data, vtype, DEV))
+        plan.refresh(d)
         plan.close()
 
 

@@ -100,27 +100,34 @@ def test_panel_layout_invariants(kind, acc_bytes):
     PW, TW, H = plan_oracle.panel_constants(acc_bytes, W)
     tb, te, seg = plan_oracle.panel_layout(p, idx, n_cols, acc_bytes, W)
     lengths = np.diff(p)
-    # every short row in exactly one tile; long rows in none
-    covered = np.zeros(len(lengths), int)
+    vs, ve, row = plan_oracle.virtual_rows(p, int(p[-1]), W)
+    nv = len(vs)
+    # virtual rows: at most W values each; a row's virtual rows are
+    # consecutive, cover its values in order, and only long rows have more
+    # than one
+    assert np.all(ve - vs <= W) and np.all(ve >= vs)
+    np.testing.assert_array_equal(np.bincount(row, ve - vs, minlength=len(lengths)), lengths)
+    per_row = np.bincount(row, minlength=len(lengths))
+    assert np.all(per_row[lengths <= W] == 1)
+    C = min(W, plan_oracle.LONG_CHUNK)
+    np.testing.assert_array_equal(per_row[lengths > W], -(-lengths[lengths > W] // C))
+    np.testing.assert_array_equal(vs[1:], ve[:-1])  # well-formed indptr: contiguous
+    # tiles partition the virtual rows; products + one word per virtual row fit
+    assert tb[0] == 0 and te[-1] == nv
+    np.testing.assert_array_equal(tb[1:], te[:-1])
     for a, b in zip(tb, te):
         assert a < b
-        covered[a:b] += 1
-        assert np.all(lengths[a:b] <= W)
-        assert (p[b] - p[a]) + (b - a) <= TW  # products + one word per row fit
-    np.testing.assert_array_equal(covered, (lengths <= W).astype(int))
-    assert np.all(tb[1:] >= te[:-1])
-    # segments partition the valid short-row values by (panel, tile), each
-    # padded to a multiple of 4 entries
+        assert (ve[b - 1] - vs[a]) + (b - a) <= TW
+    # segments partition the valid values by (panel, tile), each padded to a
+    # multiple of 4 entries
     n_tiles, P = len(tb), -(-n_cols // PW)
     assert len(seg) == P * n_tiles + 1 and seg[0] == 0 and np.all(np.diff(seg) >= 0)
     assert np.all(seg % 4 == 0)
     counts = np.zeros(P * n_tiles, np.int64)
     for t, (a, b) in enumerate(zip(tb, te)):
-        cols = idx[p[a]:p[b]]
+        cols = idx[vs[a]:ve[b - 1]]
         cols = cols[(cols >= 0) & (cols < n_cols)]
         np.add.at(counts, (cols // PW) * n_tiles + t, 1)
     np.testing.assert_array_equal(np.diff(seg), -(-counts // 4) * 4)
     assert np.all(np.diff(seg) - counts < 4)
-    short_vals = sum(int(((idx[p[r]:p[r + 1]] >= 0) & (idx[p[r]:p[r + 1]] < n_cols)).sum())
-                     for r in np.flatnonzero(lengths <= W))
-    assert counts.sum() == short_vals
+    assert counts.sum() == int(((idx >= 0) & (idx < n_cols)).sum())
