@@ -213,7 +213,9 @@ def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
       as the SpMV's;
     - the CSR transpose build (radix sort; read and write nnz*(4+4) + (n+1)*4);
     - ``A^T x`` as SpMV over the cached transpose with its own plan;
-    - the SpMV value gradient (indices + indptr + x + cot read, nnz*4 written);
+    - the SpMV value gradient (indices + indptr + x + cot read, nnz*4 written),
+      through the matrix's plan (its panel layout: what autograd uses) and
+      plan-free;
     - one autograd step ``(A @ x).backward(g)`` with x requiring grad
       (forward SpMV + A^T g over the cached transpose, "auto" route warm)."""
     n_rows, n_cols = m.shape
@@ -241,13 +243,15 @@ def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
     t = _events_time(cached, 20)
     out["cached_transpose_us"] = round(t * 1e3, 1)
     out["cached_transpose_frac"] = round(spmv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-    vjp = lambda: ext.csr_matvec_data_vjp(indices, indptr, x, g, n_rows, n_cols)
-    for _ in range(3):
-        vjp()
-    t = _events_time(vjp, 20)
     vb = m.nnz * 8 + (n_rows + 1) * 4 + 4 * (n_rows + n_cols)
-    out["data_vjp_us"] = round(t * 1e3, 1)
-    out["data_vjp_frac"] = round(vb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    plan = A.plan(x.device)
+    for key, pl in (("data_vjp", plan), ("data_vjp_planfree", None)):
+        vjp = lambda: ext.csr_matvec_data_vjp(indices, indptr, x, g, n_rows, n_cols, plan=pl)
+        for _ in range(3):
+            vjp()
+        t = _events_time(vjp, 20)
+        out[f"{key}_us"] = round(t * 1e3, 1)
+        out[f"{key}_frac"] = round(vb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     xr = x.clone().requires_grad_()
 
     def train_step():

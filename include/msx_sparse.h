@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 4
+#define MSX_ABI_VERSION 5
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -440,6 +440,13 @@ msx_status msx_csr_spmm_transpose_cpu(msx_vtype vt, msx_itype it,
  * [0, n_cols) get zero.  For complex64 the caller passes conj(x) / conj(X)
  * (the Hermitian rule of the reference VJPs).
  *
+ * msx_csr_spmv_data_vjp takes an optional plan of the matrix (NULL: none;
+ * otherwise checked as for msx_csr_spmv, except that a bound plan's values
+ * are not compared: the gradient does not read them).  A bound panel plan
+ * whose copy holds every value gathers x from LDS panels and uses the plan's
+ * product buffer as scratch, so calls that overlap on one plan race, as SpMV
+ * calls do.
+ *
  * Replace csr_matvec_data_vjp and csr_matmul_data_vjp (reference:
  * src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp,
  * src/sparse/csr_matmul_data_vjp/csr_matmul_data_vjp.cpp).
@@ -447,7 +454,8 @@ msx_status msx_csr_spmm_transpose_cpu(msx_vtype vt, msx_itype it,
 msx_status msx_csr_spmv_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
                                  int64_t n_cols, int64_t nnz, const void *indices,
                                  const void *indptr, const void *x,
-                                 const void *cot, void *out, void *stream);
+                                 const void *cot, void *out,
+                                 const msx_csr_plan *plan, void *stream);
 msx_status msx_csr_spmm_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
                                  int64_t n_cols, int64_t nnz, const void *indices,
                                  const void *indptr, int64_t k, const void *X,

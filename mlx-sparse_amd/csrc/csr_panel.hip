@@ -88,7 +88,9 @@ __device__ inline T nt_load(const T *p) {
 // Pass 1.  The first batch of value and column loads is issued before the x
 // panel is staged, so their latency overlaps the panel load; every later
 // batch is issued before the products of the previous one are formed.
-template <class V>
+// XONLY: the entry's x value itself (widened), not the product; the copy's
+// values are not read (the value gradient's gather of x).
+template <class V, bool XONLY = false>
 __global__ void __launch_bounds__(kThreads)
     panel_products(const typename V::Storage *__restrict__ data, const uint16_t *__restrict__ col,
                    const typename V::Storage *__restrict__ x, int64_t n_cols,
@@ -110,64 +112,70 @@ __global__ void __launch_bounds__(kThreads)
   const auto *d4 = reinterpret_cast<const Four<S> *>(data + a);
   const auto *k4 = reinterpret_cast<const uint2 *>(col + a);
   auto *o4 = reinterpret_cast<Four<A> *>(prod + a);
-  Four<S> d[kUnroll];
-  uint2 k[kUnroll];
+  // A valid copy has col < w; the mask keeps a corrupted one inside LDS.
+  const uint32_t mask = static_cast<uint32_t>(PW - 1);
+  auto term = [&](S dv, uint32_t cw) -> A {
+    if constexpr (XONLY) {
+      (void)dv;
+      return xs[cw & mask];
+    } else {
+      return amul(V::widen(dv), xs[cw & mask]);
+    }
+  };
+  auto quad = [&](const Four<S> &dd, uint2 kk) {
+    Four<A> o;
+    o.v[0] = term(dd.v[0], kk.x);
+    o.v[1] = term(dd.v[1], kk.x >> 16);
+    o.v[2] = term(dd.v[2], kk.y);
+    o.v[3] = term(dd.v[3], kk.y >> 16);
+    return o;
+  };
+  // x only: no values are loaded, so twice the column loads are kept in flight
+  constexpr int U = XONLY ? 2 * kUnroll : kUnroll;
+  Four<S> d[U] = {};
+  uint2 k[U];
   int64_t qd = threadIdx.x;
-  bool full = qd + (kUnroll - 1) * kThreads < nq;
+  bool full = qd + (U - 1) * kThreads < nq;
   if (full) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      d[u] = nt_load(d4 + qd + u * kThreads);
+    for (int u = 0; u < U; ++u) {
+      if constexpr (!XONLY) d[u] = nt_load(d4 + qd + u * kThreads);
       k[u] = nt_load(k4 + qd + u * kThreads);
     }
   }
   for (int i = threadIdx.x; i < w; i += kThreads) xs[i] = V::widen(x[c0 + i]);
   __syncthreads();
-  // A valid copy has col < w; the mask keeps a corrupted one inside LDS.
-  const uint32_t mask = static_cast<uint32_t>(PW - 1);
   for (int64_t i = b + threadIdx.x; i < a; i += kThreads)
-    prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
+    prod[i] = term(XONLY ? S{} : data[i], col[i]);
   while (full) {
-    Four<S> dc[kUnroll];
-    uint2 kc[kUnroll];
+    Four<S> dc[U];
+    uint2 kc[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       dc[u] = d[u];
       kc[u] = k[u];
     }
-    const int64_t next = qd + kUnroll * kThreads;
-    const bool full_next = next + (kUnroll - 1) * kThreads < nq;
+    const int64_t next = qd + U * kThreads;
+    const bool full_next = next + (U - 1) * kThreads < nq;
     if (full_next) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        d[u] = nt_load(d4 + next + u * kThreads);
+      for (int u = 0; u < U; ++u) {
+        if constexpr (!XONLY) d[u] = nt_load(d4 + next + u * kThreads);
         k[u] = nt_load(k4 + next + u * kThreads);
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      Four<A> o;
-      o.v[0] = amul(V::widen(dc[u].v[0]), xs[kc[u].x & mask]);
-      o.v[1] = amul(V::widen(dc[u].v[1]), xs[(kc[u].x >> 16) & mask]);
-      o.v[2] = amul(V::widen(dc[u].v[2]), xs[kc[u].y & mask]);
-      o.v[3] = amul(V::widen(dc[u].v[3]), xs[(kc[u].y >> 16) & mask]);
-      o4[qd + u * kThreads] = o;
-    }
+    for (int u = 0; u < U; ++u) o4[qd + u * kThreads] = quad(dc[u], kc[u]);
     qd = next;
     full = full_next;
   }
   for (; qd < nq; qd += kThreads) {
-    const Four<S> dd = d4[qd];
-    const uint2 kk = k4[qd];
-    Four<A> o;
-    o.v[0] = amul(V::widen(dd.v[0]), xs[kk.x & mask]);
-    o.v[1] = amul(V::widen(dd.v[1]), xs[(kk.x >> 16) & mask]);
-    o.v[2] = amul(V::widen(dd.v[2]), xs[kk.y & mask]);
-    o.v[3] = amul(V::widen(dd.v[3]), xs[(kk.y >> 16) & mask]);
-    o4[qd] = o;
+    Four<S> dd = {};
+    if constexpr (!XONLY) dd = d4[qd];
+    o4[qd] = quad(dd, k4[qd]);
   }
   for (int64_t i = a + 4 * nq + threadIdx.x; i < e; i += kThreads)
-    prod[i] = amul(V::widen(data[i]), xs[col[i] & mask]);
+    prod[i] = term(XONLY ? S{} : data[i], col[i]);
 }
 
 // Four products of a segment (16-byte aligned: segments are padded to
@@ -344,6 +352,104 @@ __global__ void __launch_bounds__(kFixupThreads)
   }
 }
 
+// Value gradient of y = A x over the panel layout (out[p] = cot[row(p)] *
+// x[col(p)], the same rounding as the plan-free kernel): the first pass is
+// panel_products<V, true>, which writes each entry's x value; this second
+// pass takes one workgroup per tile, like pass 2 of the SpMV.  It stages the
+// cotangent of each of the tile's virtual rows and, per value position, the
+// position's virtual row; places each entry's x value at its LDS word (the
+// segment runs read as in pass 2); then walks the tile's value positions in
+// order - position p of virtual row v0 + i has word (p - b0) + i - and
+// stores the gradients with coalesced writes.  Only for copies that dropped
+// no value (every position's word is then written).
+template <class V, class RP, bool LONG>
+__global__ void __launch_bounds__(kThreads)
+    panel_vjp_scatter(const typename V::Acc *__restrict__ xg, const uint16_t *__restrict__ dest,
+                      const uint32_t *__restrict__ seg, int64_t n_tiles, int P,
+                      const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
+                      const RP *__restrict__ rowptr, const int32_t *__restrict__ vslot, int64_t nv,
+                      int64_t nnz, int rows_cap, const typename V::Storage *__restrict__ cot,
+                      typename V::Storage *__restrict__ out) {
+  using A = typename V::Acc;
+  constexpr int TW = 65536 / static_cast<int>(sizeof(A));
+  constexpr int NQ = TW / kThreads / 4;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  A *xw = reinterpret_cast<A *>(lds_raw);                          // TW words
+  A *cotv = xw + TW;                                               // rows_cap
+  uint16_t *row_at = reinterpret_cast<uint16_t *>(cotv + ((rows_cap + 3) & ~3));  // TW positions
+  const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int64_t v0 = clamp64(tile_begin[T], 0, nv);
+  const int64_t v1 = clamp64(tile_end[T], v0, std::min<int64_t>(nv, v0 + rows_cap));
+  const int64_t b0 = clamp64(static_cast<int64_t>(rowptr[v0]), 0, nnz);
+  const int64_t b1 = clamp64(static_cast<int64_t>(rowptr[v1]), b0, std::min<int64_t>(nnz, b0 + TW));
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads) {
+    const int64_t s = clamp64(static_cast<int64_t>(rowptr[v]), b0, b1);
+    const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, b1);
+    int64_t r = v;
+    if constexpr (LONG) {
+      const int32_t slot = vslot[v];
+      r = slot >= 0 ? slot : -1 - static_cast<int64_t>(slot);
+    }
+    cotv[v - v0] = V::widen(cot[r]);
+    for (int64_t p = s; p < e; ++p) row_at[p - b0] = static_cast<uint16_t>(v - v0);
+  }
+
+  const auto *xq = reinterpret_cast<const ProdQuad<A> *>(xg);
+  for (int qb = 0; qb < P; qb += kWavesPerGroup * kRunsPerWave) {
+    uint32_t st[kRunsPerWave], pre[kRunsPerWave + 1];
+    pre[0] = 0;
+#pragma unroll
+    for (int k = 0; k < kRunsPerWave; ++k) {
+      const int q = qb + wave + kWavesPerGroup * k;
+      uint32_t s = 0, e = 0;
+      if (q < P) {
+        s = seg[static_cast<int64_t>(q) * n_tiles + T];
+        e = seg[static_cast<int64_t>(q) * n_tiles + T + 1];
+      }
+      st[k] = s / 4;
+      pre[k + 1] = pre[k] + (e > s ? (e - s) / 4 : 0u);
+    }
+    const uint32_t total = pre[kRunsPerWave];
+    for (uint32_t j0 = 0; j0 < total; j0 += NQ * kWave) {
+      ProdQuad<A> xv[NQ];
+      uint2 dv[NQ];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) {
+        const uint32_t j = j0 + u * kWave + lane;
+        dv[u] = uint2{0xFFFFFFFFu, 0xFFFFFFFFu};
+        if (j < total) {
+          uint32_t base = st[0], p0 = 0;
+#pragma unroll
+          for (int k = 1; k < kRunsPerWave; ++k)
+            if (j >= pre[k]) {
+              base = st[k];
+              p0 = pre[k];
+            }
+          const uint32_t quad = base + (j - p0);
+          xv[u] = nt_load(xq + quad);
+          dv[u] = nt_load(reinterpret_cast<const uint2 *>(dest) + quad);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) {
+        const uint32_t d[4] = {dv[u].x & 0xFFFFu, dv[u].x >> 16, dv[u].y & 0xFFFFu, dv[u].y >> 16};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (d[e] < static_cast<uint32_t>(TW)) xw[d[e]] = xv[u].v[e];
+      }
+    }
+  }
+  __syncthreads();
+
+  for (int64_t k = threadIdx.x; k < b1 - b0; k += kThreads) {
+    const int i = row_at[k];
+    const int64_t w = k + i;
+    if (i < rows_cap && w < TW) out[b0 + k] = V::narrow(amul(cotv[i], xw[w]));
+  }
+}
+
 template <class A>
 size_t pass1_lds(const msx_csr_plan *p) {
   return sizeof(A) * static_cast<size_t>(p->panel_width);
@@ -352,6 +458,18 @@ size_t pass1_lds(const msx_csr_plan *p) {
 template <class A>
 size_t pass2_lds(const msx_csr_plan *p) {
   return sizeof(A) * static_cast<size_t>(p->tile_words);
+}
+
+// LDS of one workgroup on gfx950.
+constexpr size_t kMaxLdsBytes = 163840;
+
+// Value-gradient pass 2: the x value of every word, a cotangent per virtual
+// row of the widest tile (rounded to 4), the virtual row of every position.
+template <class A>
+size_t vjp_lds(const msx_csr_plan *p) {
+  const size_t rows = sizeof(A) * static_cast<size_t>((p->pn_tile_rows_max + 3) & ~int64_t{3});
+  return sizeof(A) * static_cast<size_t>(p->tile_words) + rows +
+         sizeof(uint16_t) * static_cast<size_t>(p->tile_words);
 }
 
 // Both passes take more than 64 KB of dynamic LDS.  The limit is raised
@@ -369,6 +487,17 @@ msx_status prepare_typed(const msx_csr_plan *p) {
   MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_rows<V, uint32_t, true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(pass2_lds<A>(p))));
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_products<V, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(pass1_lds<A>(p))));
+  if (vjp_lds<A>(p) <= kMaxLdsBytes) {
+    MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_vjp_scatter<V, I, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(vjp_lds<A>(p))));
+    MSX_HIP_TRY(hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&panel_vjp_scatter<V, uint32_t, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(vjp_lds<A>(p))));
+  }
   return MSX_OK;
 }
 
@@ -412,6 +541,35 @@ msx_status launch_typed(const msx_csr_plan *p, const void *indptr, const void *x
   return MSX_OK;
 }
 
+template <class V, class I>
+msx_status vjp_typed(const msx_csr_plan *p, const void *indptr, const void *x, const void *cot,
+                     void *out, hipStream_t stream) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  hipLaunchKernelGGL((panel_products<V, true>), dim3(static_cast<uint32_t>(p->pn_chunks)),
+                     dim3(kThreads), pass1_lds<A>(p), stream, static_cast<const S *>(p->pn_data), p->pn_col,
+                     static_cast<const S *>(x), p->n_cols, static_cast<A *>(p->pn_prod),
+                     p->pn_chunk_begin, p->pn_chunk_panel, p->pn_values,
+                     static_cast<int>(p->panel_width));
+  MSX_HIP_TRY(hipGetLastError());
+  const size_t lds = vjp_lds<A>(p);
+  const int cap = static_cast<int>(p->pn_tile_rows_max);
+  if (p->pn_vstart == nullptr)
+    hipLaunchKernelGGL((panel_vjp_scatter<V, I, false>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                       dim3(kThreads), lds, stream, static_cast<const A *>(p->pn_prod), p->pn_dest,
+                       p->pn_seg, p->n_tiles, static_cast<int>(p->n_panels), p->pn_tile_begin,
+                       p->pn_tile_end, static_cast<const I *>(indptr), nullptr, p->n_rows, p->nnz,
+                       cap, static_cast<const S *>(cot), static_cast<S *>(out));
+  else
+    hipLaunchKernelGGL((panel_vjp_scatter<V, uint32_t, true>), dim3(static_cast<uint32_t>(p->n_tiles)),
+                       dim3(kThreads), lds, stream, static_cast<const A *>(p->pn_prod), p->pn_dest,
+                       p->pn_seg, p->n_tiles, static_cast<int>(p->n_panels), p->pn_tile_begin,
+                       p->pn_tile_end, p->pn_vstart, p->pn_vslot, p->pn_vrows, p->nnz, cap,
+                       static_cast<const S *>(cot), static_cast<S *>(out));
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
 template <class V>
 msx_status launch_v(const msx_csr_plan *p, const void *indptr, const void *x, void *y,
                     hipStream_t stream) {
@@ -429,6 +587,27 @@ msx_status prepare_spmv_panels(const msx_csr_plan *p) {
   case MSX_C64: return prepare_v<C64>(p);
   }
   return fail(MSX_ETYPE, "msx_csr_plan_create_bound unsupported value dtype.");
+}
+
+bool panel_data_vjp_fits(const msx_csr_plan *p) {
+  if (p->n_panels == 0 || p->pn_dropped) return false;
+  return (p->vtype == MSX_C64 ? vjp_lds<c64>(p) : vjp_lds<float>(p)) <= kMaxLdsBytes;
+}
+
+msx_status launch_panel_data_vjp(const msx_csr_plan *p, const void *indptr, const void *x,
+                                 const void *cot, void *out, hipStream_t stream) {
+  const bool i32 = p->itype == MSX_I32;
+  switch (p->vtype) {
+  case MSX_F32: return i32 ? vjp_typed<F32, int32_t>(p, indptr, x, cot, out, stream)
+                           : vjp_typed<F32, int64_t>(p, indptr, x, cot, out, stream);
+  case MSX_F16: return i32 ? vjp_typed<F16, int32_t>(p, indptr, x, cot, out, stream)
+                           : vjp_typed<F16, int64_t>(p, indptr, x, cot, out, stream);
+  case MSX_BF16: return i32 ? vjp_typed<BF16, int32_t>(p, indptr, x, cot, out, stream)
+                            : vjp_typed<BF16, int64_t>(p, indptr, x, cot, out, stream);
+  case MSX_C64: return i32 ? vjp_typed<C64, int32_t>(p, indptr, x, cot, out, stream)
+                           : vjp_typed<C64, int64_t>(p, indptr, x, cot, out, stream);
+  }
+  return fail(MSX_ETYPE, "csr_matvec_data_vjp unsupported value dtype.");
 }
 
 msx_status launch_spmv_panels(const msx_csr_plan *p, const void *indptr, const void *x, void *y,

@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(kThreads)
     const bool is_long = static_cast<int64_t>(indptr[r + 1]) - static_cast<int64_t>(indptr[r]) > W;
     for (int64_t k = 0; k < c; ++k) {
       vstart[v + k] = static_cast<uint32_t>(std::min<int64_t>(s + k * C, nnz));
-      vslot[v + k] = is_long ? -1 : static_cast<int32_t>(r);
+      vslot[v + k] = static_cast<int32_t>(is_long ? -1 - r : r);
     }
   }
 }
@@ -525,6 +525,17 @@ msx_status build_layout(msx_csr_plan *p, const typename V::Storage *data, const 
   p->pn_chunks = n_chunks;
   p->pn_dropped = lost != 0;
   p->pn_vrows = nv;
+  {  // the widest tile in virtual rows (sizes the value-gradient LDS)
+    std::vector<int32_t> tb(static_cast<size_t>(n_tiles)), te(static_cast<size_t>(n_tiles));
+    MSX_HIP_TRY(hipMemcpyAsync(tb.data(), p->pn_tile_begin, sizeof(int32_t) * n_tiles,
+                               hipMemcpyDeviceToHost, stream));
+    MSX_HIP_TRY(hipMemcpyAsync(te.data(), p->pn_tile_end, sizeof(int32_t) * n_tiles,
+                               hipMemcpyDeviceToHost, stream));
+    MSX_HIP_TRY(hipStreamSynchronize(stream));
+    int64_t widest = 1;
+    for (int64_t t = 0; t < n_tiles; ++t) widest = std::max<int64_t>(widest, int64_t{te[t]} - tb[t]);
+    p->pn_tile_rows_max = std::min<int64_t>(widest, TW);
+  }
   return prepare_spmv_panels(p);
 }
 

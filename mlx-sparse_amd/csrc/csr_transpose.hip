@@ -834,13 +834,22 @@ extern "C" msx_status msx_csr_spmm_transpose(msx_vtype vt, msx_itype it, int64_t
 extern "C" msx_status msx_csr_spmv_data_vjp(msx_vtype vt, msx_itype it, int64_t n_rows,
                                             int64_t n_cols, int64_t nnz, const void *indices,
                                             const void *indptr, const void *x, const void *cot,
-                                            void *out, void *stream) {
+                                            void *out, const msx_csr_plan *plan, void *stream) {
   clear_error();
   msx_status st = check_csr("csr_matvec_data_vjp", vt, it, n_rows, n_cols, nnz, indices, indptr);
+  if (st != MSX_OK) return st;
+  // The gradient does not read the values: a plan bound to this matrix is
+  // accepted whatever values it was bound to.
+  st = check_plan("csr_matvec_data_vjp", plan, vt, it, n_rows, n_cols, nnz,
+                  plan != nullptr ? plan->bound_data : nullptr, indices, indptr);
   if (st != MSX_OK) return st;
   if (nnz > 0 && (out == nullptr || cot == nullptr || (n_cols > 0 && x == nullptr)))
     return fail(MSX_EINVAL, "csr_matvec_data_vjp buffers must be non-NULL.");
   if (nnz == 0 || n_rows == 0) return MSX_OK;
+  // A panel plan turns the gather of x into LDS reads (two streaming passes)
+  // when its copy holds every value (no invalid column was dropped).
+  if (plan != nullptr && plan->bound && plan->vtype == vt && panel_data_vjp_fits(plan))
+    return launch_panel_data_vjp(plan, indptr, x, cot, out, static_cast<hipStream_t>(stream));
   return dispatch<SpmvDataVjpOp>(vt, it, n_rows, n_cols, nnz, indices, indptr, x, cot, out,
                                  static_cast<hipStream_t>(stream));
 }

@@ -110,10 +110,11 @@ struct msx_csr_plan {
   // Virtual rows when the matrix has long rows (all null otherwise: then the
   // virtual rows are the rows, delimited by indptr).  Virtual row v spans
   // values [pn_vstart[v], pn_vstart[v + 1]); pn_vslot[v] is its row when
-  // it is a short row, -1 for a chunk of a long row, whose sum pass 2
+  // it is a short row, -1 - r for a chunk of long row r, whose sum pass 2
   // writes to pn_partial[v]; long row r owns virtual rows
   // [pn_vbase[r], pn_vbase[r + 1]).
   int64_t pn_vrows;           // virtual rows (n_rows without long rows)
+  int64_t pn_tile_rows_max;   // most virtual rows of a tile
   uint32_t *pn_vstart;        // pn_vrows + 1
   int32_t *pn_vslot;          // pn_vrows
   uint32_t *pn_vbase;         // n_rows + 1
@@ -187,6 +188,11 @@ msx_status launch_spmv_panels(const msx_csr_plan *p, const void *indptr, const v
                               hipStream_t stream);
 // Raises the dynamic-LDS limit of the two panel kernels on the current device.
 msx_status prepare_spmv_panels(const msx_csr_plan *p);
+// Value gradient of y = A x through a panel plan of A (csr_panel.hip), for
+// plans whose copy holds every value and whose widest tile fits the LDS.
+bool panel_data_vjp_fits(const msx_csr_plan *p);
+msx_status launch_panel_data_vjp(const msx_csr_plan *p, const void *indptr, const void *x,
+                                 const void *cot, void *out, hipStream_t stream);
 
 // Y[b] = A X[b] for b < batch: X[b] at X + b * x_batch (row stride ldx),
 // Y[b] at Y + b * y_batch (row stride ldy), all in elements.

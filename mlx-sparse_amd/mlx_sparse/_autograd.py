@@ -253,7 +253,10 @@ class MatVecDataVjp(torch.autograd.Function):
     @staticmethod
     def forward(x, g, a):
         _, indices, indptr = a.buffers(x.device)
-        return _native.csr_matvec_data_vjp(indices, indptr, _conj(x), g.contiguous(), a.shape)
+        # the gradient does not read the values: the plan serves whatever
+        # values it is bound to
+        return _native.csr_matvec_data_vjp(indices, indptr, _conj(x), g.contiguous(), a.shape,
+                                           plan=a.plan(x.device))
 
     @staticmethod
     def setup_context(ctx, inputs, output):

@@ -60,10 +60,12 @@ def csr_matmul_transpose(data, indices, indptr, rhs, shape: Shape2D) -> torch.Te
     return extension().csr_matmul_transpose(data, indices, indptr, rhs, shape[0], shape[1])
 
 
-def csr_matvec_data_vjp(indices, indptr, x, cotangent, shape: Shape2D) -> torch.Tensor:
+def csr_matvec_data_vjp(indices, indptr, x, cotangent, shape: Shape2D, plan=None) -> torch.Tensor:
     """cot[row(p)] * x[col(p)] per stored value (reference:
-    src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp)."""
-    return extension().csr_matvec_data_vjp(indices, indptr, x, cotangent, shape[0], shape[1])
+    src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp); ``plan``: the
+    matrix's GPU plan, whose panel layout (if any) serves the gather of x."""
+    return extension().csr_matvec_data_vjp(indices, indptr, x, cotangent, shape[0], shape[1],
+                                           plan=plan)
 
 
 def csr_matmul_data_vjp(indices, indptr, rhs, cotangent, shape: Shape2D) -> torch.Tensor:

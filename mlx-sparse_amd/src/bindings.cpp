@@ -399,7 +399,8 @@ py::object csr_matmul_transpose(py::handle data_o, py::handle indices_o, py::han
 }
 
 py::object csr_matvec_data_vjp(py::handle indices_o, py::handle indptr_o, py::handle x_o,
-                               py::handle cot_o, int64_t n_rows, int64_t n_cols, int n_threads) {
+                               py::handle cot_o, int64_t n_rows, int64_t n_cols, int n_threads,
+                               const py::object &plan) {
   py::object indices = contiguous(indices_o), indptr = contiguous(indptr_o), x = contiguous(x_o),
              cot = contiguous(cot_o);
   const ArrayView vi = view_of(indices), vp = view_of(indptr), vx = view_of(x), vc = view_of(cot);
@@ -408,7 +409,7 @@ py::object csr_matvec_data_vjp(py::handle indices_o, py::handle indptr_o, py::ha
   const ArrayView vo = view_of(out);
   const msx::ExecContext ctx = context_for(vx, n_threads);
   if (vx.device >= 0) {
-    msx::csr_matvec_data_vjp(vi, vp, vx, vc, vo, n_rows, n_cols, ctx);
+    msx::csr_matvec_data_vjp(vi, vp, vx, vc, vo, n_rows, n_cols, ctx, plan_ptr(plan));
   } else {
     py::gil_scoped_release nogil;
     msx::csr_matvec_data_vjp(vi, vp, vx, vc, vo, n_rows, n_cols, ctx);
@@ -673,7 +674,9 @@ PYBIND11_MODULE(_ext, m) {
         py::arg("n_threads") = 0, "A^T X for CSR buffers of shape (n_rows, n_cols).");
   m.def("csr_matvec_data_vjp", &csr_matvec_data_vjp, py::arg("indices"), py::arg("indptr"),
         py::arg("x"), py::arg("cotangent"), py::arg("n_rows"), py::arg("n_cols"),
-        py::arg("n_threads") = 0, "Gradient of A x with respect to the stored values.");
+        py::arg("n_threads") = 0, py::arg("plan") = py::none(),
+        "Gradient of A x with respect to the stored values (a GPU plan of the matrix may "
+        "serve the gather of x).");
   m.def("csr_matmul_data_vjp", &csr_matmul_data_vjp, py::arg("indices"), py::arg("indptr"),
         py::arg("rhs"), py::arg("cotangent"), py::arg("n_rows"), py::arg("n_cols"),
         py::arg("n_threads") = 0, "Gradient of A X with respect to the stored values.");

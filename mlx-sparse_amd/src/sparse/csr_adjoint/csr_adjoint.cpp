@@ -129,7 +129,7 @@ void csr_matmul_transpose(const ArrayView &data, const ArrayView &indices,
 
 void csr_matvec_data_vjp(const ArrayView &indices, const ArrayView &indptr, const ArrayView &x,
                          const ArrayView &cotangent, const ArrayView &out, int64_t n_rows,
-                         int64_t n_cols, const ExecContext &ctx) {
+                         int64_t n_cols, const ExecContext &ctx, const msx_csr_plan *plan) {
   // reference: src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp,
   // csr_matvec_data_vjp
   const char *op = "csr_matvec_data_vjp";
@@ -153,7 +153,8 @@ void csr_matvec_data_vjp(const ArrayView &indices, const ArrayView &indptr, cons
   const msx_itype it = to_itype(indices.dtype);
   if (x.device >= 0)
     check_status(msx_csr_spmv_data_vjp(vt, it, n_rows, n_cols, indices.size(), indices.ptr,
-                                       indptr.ptr, x.ptr, cotangent.ptr, out.ptr, ctx.stream),
+                                       indptr.ptr, x.ptr, cotangent.ptr, out.ptr, plan,
+                                       ctx.stream),
                  op);
   else
     check_status(msx_csr_spmv_data_vjp_cpu(vt, it, n_rows, n_cols, indices.size(), indices.ptr,

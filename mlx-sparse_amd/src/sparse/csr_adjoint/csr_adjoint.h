@@ -32,9 +32,12 @@ void csr_matmul_transpose(const ArrayView &data, const ArrayView &indices,
 
 // out[p] = cot[row(p)] * x[col(p)] (reference:
 // src/sparse/csr_matvec_data_vjp/csr_matvec_data_vjp.cpp, csr_matvec_data_vjp).
+// plan: a GPU plan of the matrix (nullptr: none); a panel plan serves the
+// gather of x from LDS.
 void csr_matvec_data_vjp(const ArrayView &indices, const ArrayView &indptr, const ArrayView &x,
                          const ArrayView &cotangent, const ArrayView &out, int64_t n_rows,
-                         int64_t n_cols, const ExecContext &ctx);
+                         int64_t n_cols, const ExecContext &ctx,
+                         const msx_csr_plan *plan = nullptr);
 
 // out[p] = sum_q cot[row(p), q] * X[col(p), q] (reference:
 // src/sparse/csr_matmul_data_vjp/csr_matmul_data_vjp.cpp, csr_matmul_data_vjp).

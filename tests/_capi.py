@@ -85,7 +85,7 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_spmv_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
         L.msx_csr_spmm_transpose_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, i64, vp, vp,
                                                  ci]
-        L.msx_csr_spmv_data_vjp.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+        L.msx_csr_spmv_data_vjp.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]
         L.msx_csr_spmm_data_vjp.argtypes = [ci, ci, i64, i64, i64, vp, vp, i64, vp, i64, vp, i64,
                                             vp, vp]
         L.msx_csr_spmv_data_vjp_cpu.argtypes = [ci, ci, i64, i64, i64, vp, vp, vp, vp, vp, ci]
@@ -323,7 +323,7 @@ def spmm_transpose(data, indices, indptr, X, n_rows, n_cols, n_threads=1, Y=None
     return Y
 
 
-def spmv_data_vjp(indices, indptr, x, cot, n_rows, n_cols, n_threads=1):
+def spmv_data_vjp(indices, indptr, x, cot, n_rows, n_cols, n_threads=1, plan=None):
     nnz = indices.numel()
     out = torch.empty(nnz, dtype=x.dtype, device=x.device)
     head = (VT[x.dtype], IT[indices.dtype], n_rows, n_cols, nnz, _p(indices), _p(indptr),
@@ -331,7 +331,8 @@ def spmv_data_vjp(indices, indptr, x, cot, n_rows, n_cols, n_threads=1):
     if _is_cpu(x):
         _check(lib().msx_csr_spmv_data_vjp_cpu(*head, n_threads), "msx_csr_spmv_data_vjp_cpu")
     else:
-        _check(lib().msx_csr_spmv_data_vjp(*head, _stream()), "msx_csr_spmv_data_vjp")
+        _check(lib().msx_csr_spmv_data_vjp(*head, plan.ptr if plan is not None else None,
+                                           _stream()), "msx_csr_spmv_data_vjp")
     return out
 
 

@@ -188,6 +188,45 @@ def test_data_vjp_bit_exact(vtype, index_dtype):
 
 
 @pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("bad_cols", [False, True])
+def test_data_vjp_through_panel_plan(vtype, index_dtype, bad_cols):
+    """The value gradient through a panel plan (x gathered from LDS and
+    placed at the tiles' words, the gradient stored in position order):
+    equal to the oracle bit for bit, long rows (virtual rows) included.  A
+    copy that dropped invalid columns takes the plan-free kernel (zeros
+    there)."""
+    rng = np.random.default_rng(12)
+    n_rows, n_cols = 9000, 200_000
+    lengths = rng.integers(0, 40, n_rows)
+    lengths[[5, 4000, 8998]] = [3000, 9000, 700]
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    nnz = int(indptr[-1])
+    indices = rng.integers(0, n_cols, nnz)
+    if bad_cols:
+        indices[rng.random(nnz) < 0.002] = -1
+        indices[rng.random(nnz) < 0.002] = n_cols + 5
+    indices, indptr = indices.astype(index_dtype), indptr.astype(index_dtype)
+    data = _values(rng, nnz, vtype)
+    x = _values(rng, n_cols, vtype)
+    cot = _values(rng, n_rows, vtype)
+    want = orc.csr_data_vjp(indices, indptr, x, cot, n_rows, n_cols, nnz, vtype=vtype)
+    d, i, p = _dev(data, vtype), _dev(indices), _dev(indptr)
+    for W in (64, 256):
+        plan = _capi.Plan(p, n_rows, nnz, W, data=d, indices=i, n_cols=n_cols,
+                          slice_mode=_capi.SLICE_PANELS)
+        assert plan.info().n_panels > 0
+        print(f"data_vjp panels {vtype} {np.dtype(index_dtype).name} W={W} bad={bad_cols}",
+              flush=True)
+        for _ in range(2):
+            got = _capi.spmv_data_vjp(i, p, _dev(x, vtype), _dev(cot, vtype), n_rows, n_cols,
+                                      plan=plan)
+            np.testing.assert_array_equal(_bytes(to_numpy(got)), _bytes(want))
+        plan.close()
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
 def test_deterministic_route_equals_one_worker_reference(vtype):
     # transpose, then the zero-start stored-order SpMM with k = 1: every
     # output summed from zero over its column's values in row order, which
