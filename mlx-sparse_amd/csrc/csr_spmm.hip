@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "msx_device.h"
 #include "msx_internal.h"
@@ -454,6 +455,181 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Column windows on the matrix cores (float16 / bfloat16, k a multiple of
+// 16).  One 256-thread workgroup per 32-row tile: the tile's values are
+// scattered into a dense 32 x Kp block of its window in LDS (Kp: the
+// plan's widest window rounded up to 32 columns), the window's X rows are
+// staged transposed (each column's Kp values contiguous, so every MFMA
+// operand of a lane is one 16-byte read), and v_mfma_f32_16x16x32 forms
+// the 32 x k tile of Y with float32 accumulation (lane layout, checked on
+// gfx950: A lane l holds row l % 16, k = 8 (l / 16) + 0..7; B lane l holds
+// column l % 16, the same k; D lane l holds column l % 16, rows
+// 4 (l / 16) + 0..3).  A product of two 16-bit values is exact in float32;
+// the sums run in the matrix core's order, within the float16 / bfloat16
+// tolerance of the reference's stored-order sum.  A tile with a repeated
+// (row, column) pair, a column outside its window or row pointers outside
+// the tile's range takes the stored-order path from global memory instead
+// (its result then equals the reference's).
+typedef float MfmaAcc __attribute__((ext_vector_type(4)));
+
+template <class V>
+struct Mfma16;
+template <>
+struct Mfma16<F16> {
+  typedef _Float16 Vec8 __attribute__((ext_vector_type(8)));
+  __device__ static inline MfmaAcc mma(uint4 a, uint4 b, MfmaAcc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(Vec8, a),
+                                                  __builtin_bit_cast(Vec8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<BF16> {
+  typedef __bf16 Vec8 __attribute__((ext_vector_type(8)));
+  __device__ static inline MfmaAcc mma(uint4 a, uint4 b, MfmaAcc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(Vec8, a),
+                                                   __builtin_bit_cast(Vec8, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kMfmaPad = 8;  // halves of padding per LDS row (staggers the banks)
+
+// LDS bytes of spmm_window_mfma for a padded window Kp and k columns.
+__host__ __device__ inline int64_t mfma_window_lds(int64_t Kp, int64_t k) {
+  const int64_t stride = Kp + kMfmaPad;
+  return 2 * (kWinRows * stride + k * stride) + 8 * (kWinRows + 2) + 4 * kWinRows * (Kp / 32) + 16;
+}
+
+// k in {16, 32, 64, 128, 256}: LG = log2(k / 8), the 16-byte chunks of a row.
+template <class V, class I, int LG>
+__global__ void __launch_bounds__(kThreads)
+    spmm_window_mfma(const uint16_t *__restrict__ data, const I *__restrict__ indices,
+                     const I *__restrict__ indptr, const uint16_t *__restrict__ X, int64_t ldx,
+                     uint16_t *__restrict__ Y, int64_t ldy, int64_t n_rows, int64_t nnz,
+                     int64_t n_cols, const int32_t *__restrict__ win, int64_t n_win, int Kp) {
+  using A = typename V::Acc;
+  constexpr int CH = 1 << LG;  // 16-byte chunks per X / Y row
+  constexpr int K = 8 * CH;    // columns
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int stride = Kp + kMfmaPad;
+  uint16_t *ad = reinterpret_cast<uint16_t *>(lds_raw);              // kWinRows x stride
+  uint16_t *xt = ad + kWinRows * stride;                              // K x stride
+  int64_t *rptr = reinterpret_cast<int64_t *>(xt + K * stride);       // kWinRows + 1
+  uint32_t *seen = reinterpret_cast<uint32_t *>(rptr + kWinRows + 2);  // kWinRows x Kp / 32
+  int *flag = reinterpret_cast<int *>(seen + kWinRows * (Kp / 32));
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int words = Kp / 32;
+  // staging: thread tid owns column chunk c8 and X-row pair tid >> LG (+ steps)
+  const int c8 = (tid & (CH - 1)) * 8;
+  const int pair0 = tid >> LG;
+  constexpr int kPairsPerStep = kThreads >> LG;
+  for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_win; t += gridDim.x) {
+    const int64_t lo = win[2 * t];
+    const int nw = static_cast<int>(std::min<int64_t>(
+        Kp, std::max<int64_t>(0, static_cast<int64_t>(win[2 * t + 1]) - lo + 1)));
+    const int64_t r0 = t * kWinRows;
+    const int nr = static_cast<int>(std::min<int64_t>(kWinRows, n_rows - r0));
+    if (tid <= nr) rptr[tid] = clamp64(static_cast<int64_t>(indptr[r0 + tid]), 0, nnz);
+    for (int i = tid; i < kWinRows * stride / 8; i += kThreads)
+      reinterpret_cast<uint4 *>(ad)[i] = uint4{0, 0, 0, 0};
+    for (int i = tid; i < kWinRows * words; i += kThreads) seen[i] = 0;
+    if (tid == 0) *flag = 0;
+    // X window, transposed two rows at a time (one 4-byte LDS write per
+    // column); rows past the window or past x read as zero, so the padded
+    // part of K adds nothing.
+    for (int wr = 2 * pair0; wr < Kp; wr += 2 * kPairsPerStep) {
+      uint4 v0{0, 0, 0, 0}, v1{0, 0, 0, 0};
+      if (wr < nw && lo + wr < n_cols) v0 = *reinterpret_cast<const uint4 *>(X + (lo + wr) * ldx + c8);
+      if (wr + 1 < nw && lo + wr + 1 < n_cols)
+        v1 = *reinterpret_cast<const uint4 *>(X + (lo + wr + 1) * ldx + c8);
+      const uint32_t a4[4] = {v0.x, v0.y, v0.z, v0.w}, b4[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t lo16 = (a4[j / 2] >> (16 * (j & 1))) & 0xFFFFu;
+        const uint32_t hi16 = (b4[j / 2] >> (16 * (j & 1))) << 16;
+        *reinterpret_cast<uint32_t *>(xt + (c8 + j) * stride + wr) = lo16 | (hi16 & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+    // Values into the dense block: 8 threads per row, in stored order.
+    {
+      const int i = tid >> 3;
+      if (i < nr) {
+        const int64_t s = rptr[i];
+        const int64_t e = std::max<int64_t>(rptr[i + 1], s);
+        for (int64_t q = s + (tid & 7); q < e; q += 8) {
+          const int64_t c = static_cast<int64_t>(indices[q]);
+          if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols)) continue;  // adds nothing
+          const int64_t w = c - lo;
+          if (static_cast<uint64_t>(w) >= static_cast<uint64_t>(nw)) {
+            *flag = 1;
+            continue;
+          }
+          const uint32_t bit = 1u << (w & 31);
+          if (atomicOr(&seen[i * words + static_cast<int>(w >> 5)], bit) & bit) {
+            *flag = 1;  // repeated (row, column): keep the stored-order sum
+            continue;
+          }
+          ad[i * stride + static_cast<int>(w)] = data[q];
+        }
+        // row pointers outside the tile's range: keep the stored-order sum
+        if ((tid & 7) == 0 && (s < rptr[0] || rptr[i + 1] < s)) *flag = 1;
+      }
+    }
+    __syncthreads();
+    if (*flag) {
+      // Stored order from global memory, 8 columns per thread.
+      for (int q = tid; q < nr * CH; q += kThreads) {
+        const int i = q >> LG;
+        const int cc = (q & (CH - 1)) * 8;
+        const int64_t s = rptr[i];
+        const int64_t e = std::max<int64_t>(rptr[i + 1], s);
+        A acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = vzero<A>();
+        for (int64_t p = s; p < e; ++p) {
+          const int64_t c = static_cast<int64_t>(indices[p]);
+          if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols)) continue;
+          const A a = V::widen(data[p]);
+          const uint4 v = *reinterpret_cast<const uint4 *>(X + c * ldx + cc);
+          const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            acc[j] = vmadd<V>(acc[j], a, static_cast<uint16_t>(w4[j / 2] >> (16 * (j & 1))));
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = static_cast<uint32_t>(V::narrow(acc[2 * j])) |
+                 (static_cast<uint32_t>(V::narrow(acc[2 * j + 1])) << 16);
+        *reinterpret_cast<uint4 *>(Y + (r0 + i) * ldy + cc) = uint4{o[0], o[1], o[2], o[3]};
+      }
+      __syncthreads();
+      continue;
+    }
+    // Matrix cores: 2 x (K / 16) output blocks of 16 x 16 over the waves,
+    // stored straight to Y (a lane holds four rows of one column).
+    const int lr = lane % 16, lk = 8 * (lane / 16);
+    for (int blk = wave; blk < 2 * (K / 16); blk += kThreads / kWave) {
+      const int rb = blk & 1, cb = blk >> 1;
+      MfmaAcc acc = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t *arow = ad + (rb * 16 + lr) * stride + lk;
+      const uint16_t *bcol = xt + (cb * 16 + lr) * stride + lk;
+      for (int kk = 0; kk < Kp; kk += 32)
+        acc = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk),
+                             *reinterpret_cast<const uint4 *>(bcol + kk), acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = rb * 16 + 4 * (lane / 16) + v;
+        if (row < nr) Y[(r0 + row) * ldy + cb * 16 + lr] = V::narrow(acc[v]);
+      }
+    }
+    __syncthreads();  // the next tile overwrites the staged data
+  }
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 
@@ -479,6 +655,33 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
   const int64_t row_bytes = k * static_cast<int64_t>(sizeof(S));
   // Column windows of a bound plan: every tile's window of X, its values
   // and row pointers in LDS.
+  if constexpr (std::is_same_v<V, F16> || std::is_same_v<V, BF16>) {
+    // 16-bit values, k = 16 .. 256 a power of two: the matrix-core window
+    // kernel.
+    const int lg = k == 16 ? 1 : k == 32 ? 2 : k == 64 ? 3 : k == 128 ? 4 : k == 256 ? 5 : 0;
+    if (vec && batch == 1 && plan != nullptr && plan->win_rows_max > 0 &&
+        plan->n_win == (n_rows + kWinRows - 1) / kWinRows && lg > 0) {
+      const int64_t Kp = (plan->win_rows_max + 31) / 32 * 32;
+      const int64_t lds = mfma_window_lds(Kp, k);
+      if (lds <= kWinLdsBytes) {
+        const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(plan->n_win, kMaxGrid));
+        auto go = [&](auto kern) {
+          hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), static_cast<size_t>(lds), stream,
+                             data, indices, indptr, X, ldx, Y, ldy, n_rows, nnz, n_cols,
+                             plan->win, plan->n_win, static_cast<int>(Kp));
+        };
+        switch (lg) {
+        case 1: go(spmm_window_mfma<V, I, 1>); break;
+        case 2: go(spmm_window_mfma<V, I, 2>); break;
+        case 3: go(spmm_window_mfma<V, I, 3>); break;
+        case 4: go(spmm_window_mfma<V, I, 4>); break;
+        default: go(spmm_window_mfma<V, I, 5>); break;
+        }
+        MSX_HIP_TRY(hipGetLastError());
+        return MSX_OK;
+      }
+    }
+  }
   if (vec && batch == 1 && plan != nullptr && plan->win_rows_max > 0 &&
       plan->n_win == (n_rows + kWinRows - 1) / kWinRows && k <= int64_t{kWave} * CWV) {
     int LR = 1;

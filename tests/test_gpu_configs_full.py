@@ -197,12 +197,13 @@ def test_cfg5_banded_spmv(gpu, banded, vtype):
 
 @pytest.mark.parametrize("vtype", ["float16", "bfloat16"])
 def test_cfg5_banded_spmm_k64(gpu, banded, vtype):
-    """The column-window SpMM (each 32-row tile's window of X staged in
-    LDS): every output summed in stored order from zero, float32
-    accumulation, one rounding - equal to the oracle bit for bit."""
+    """The column-window SpMM on the matrix cores (each 32-row tile's
+    window densified in LDS, v_mfma_f32_16x16x32 with float32
+    accumulation, one rounding): within the 16-bit tolerance of the
+    oracle's stored-order sums."""
     from mlx_sparse import synthetic
 
     X = storage(synthetic.normal(banded.shape[1], seed=2, k=64), vtype)
     info = _spmm_check(gpu, banded, storage(banded.data, vtype), X, vtype,
-                       f"cfg5 banded {vtype} spmm k=64", exact=True)
+                       f"cfg5 banded {vtype} spmm k=64", exact=False)
     assert 0 < info["window_rows"] <= 32 + 2 * 32

@@ -189,7 +189,9 @@ def _banded(n, half_band, seed, vtype, index_dtype=np.int32):
 def test_window_spmm_matches_oracle_and_plan_free(vtype, k):
     """A bound plan of a banded matrix records each 32-row tile's column
     window; the SpMM then gathers X from LDS.  Same sums as without the plan
-    (bit for bit, every type) and as the oracle (float32 bit for bit)."""
+    (bit for bit) and as the oracle (float32 bit for bit) - except float16 /
+    bfloat16 with k a multiple of 16, which run on the matrix cores (float32
+    accumulation in the MFMA's order): within the 16-bit tolerance of both."""
     n, hb = 3001, 12  # n not a multiple of the 32-row tile
     m, data = _banded(n, hb, seed=k, vtype=vtype)
     rng = np.random.default_rng(100 + k)
@@ -202,13 +204,53 @@ def test_window_spmm_matches_oracle_and_plan_free(vtype, k):
     got = _capi.spmm(d, i, p, Xt, n, n, plan=plan)
     ref = _capi.spmm(d, i, p, Xt, n, n)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(to_numpy(got), to_numpy(ref))
     want = orc.csr_matmul(data, m.indices, m.indptr, X, n, vtype=vtype, n_threads=8)
+    scale = orc.row_scale(data, m.indices, m.indptr, X, n, vtype=vtype)
+    mfma = vtype in ("float16", "bfloat16") and k % 16 == 0
+    if mfma:
+        assert_rows_close(to_numpy(got), to_numpy(ref), scale, vtype, f"window mfma {vtype} k={k}")
+    else:
+        np.testing.assert_array_equal(to_numpy(got), to_numpy(ref))
     if vtype == "float32":
         np.testing.assert_array_equal(to_numpy(got), want)
     else:
-        scale = orc.row_scale(data, m.indices, m.indptr, X, n, vtype=vtype)
         assert_rows_close(to_numpy(got), want, scale, vtype, f"window {vtype} k={k}")
+    plan.close()
+
+
+@pytest.mark.parametrize("vtype", ["float16", "bfloat16"])
+def test_window_mfma_tiles_that_keep_stored_order(vtype):
+    """Tiles the matrix cores cannot take - a repeated (row, column) pair, a
+    column moved outside the tile's recorded window - are summed in stored
+    order from global memory, equal to the oracle bit for bit; the other
+    tiles stay within the 16-bit tolerance; out-of-range columns add
+    nothing."""
+    n, k = 2000, 64
+    m, data = _banded(n, 6, seed=9, vtype=vtype)
+    rng = np.random.default_rng(10)
+    X = _values(rng, (n, k), vtype)
+    idx = m.indices.copy()
+    d, i, p = to_torch(data, vtype, DEV), to_torch(idx, None, DEV), to_torch(m.indptr, None, DEV)
+    plan = _capi.Plan(p, n, m.nnz, data=d, indices=i, n_cols=n)
+    assert plan.info().window_rows > 0
+    ip = m.indptr.astype(np.int64)
+    r_dup, r_far = 100, 700  # tiles 3 and 21
+    idx[ip[r_dup] + 1] = idx[ip[r_dup]]             # repeated column in one row
+    idx[ip[r_far]] = (idx[ip[r_far]] + n // 2) % n   # far outside its tile's window
+    idx[ip[1500]] = n + 3                            # out of range: adds nothing
+    i.copy_(to_torch(idx, None, DEV))
+    got = to_numpy(_capi.spmm(d, i, p, to_torch(X, vtype, DEV), n, n, plan=plan))
+    keep = (idx >= 0) & (idx < n)
+    rows = np.repeat(np.arange(n), np.diff(ip))
+    kept_indptr = np.concatenate([[0], np.cumsum(np.bincount(rows[keep], minlength=n))])
+    kidx, kptr = idx[keep].astype(np.int64), kept_indptr.astype(np.int64)
+    want = orc.csr_matmul(data[keep], kidx, kptr, X, n, vtype=vtype, n_threads=8)
+    for r in (r_dup, r_far):
+        t = r // 32
+        np.testing.assert_array_equal(got[32 * t:32 * t + 32], want[32 * t:32 * t + 32],
+                                      err_msg=f"stored-order tile {t}")
+    scale = orc.row_scale(data[keep], kidx, kptr, X, n, vtype=vtype)
+    assert_rows_close(got, want, scale, vtype, f"window mfma {vtype} edited")
     plan.close()
 
 
