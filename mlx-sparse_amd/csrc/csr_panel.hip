@@ -85,11 +85,56 @@ __device__ inline T nt_load(const T *p) {
   }
 }
 
-// Pass 1.  The first batch of value and column loads is issued before the x
-// panel is staged, so their latency overlaps the panel load; every later
-// batch is issued before the products of the previous one are formed.
+// Stage panel [c0, c0 + w) of x into LDS, widened: 16-byte loads, eight per
+// thread issued before the first LDS store (the unaligned case and the tail
+// element by element).
+template <class V>
+__device__ inline void stage_panel(typename V::Acc *xs, const typename V::Storage *__restrict__ x,
+                                   int64_t c0, int w) {
+  using S = typename V::Storage;
+  constexpr int E = 16 / static_cast<int>(sizeof(S));
+  constexpr int L = 8;
+  const S *src = x + c0;
+  int done = 0;
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const int nv = w / E;
+    const auto *s4 = reinterpret_cast<const uint4 *>(src);
+    for (int v0 = 0; v0 < nv; v0 += L * kThreads) {
+      uint4 t[L];
+#pragma unroll
+      for (int u = 0; u < L; ++u) {
+        const int v = v0 + u * kThreads + static_cast<int>(threadIdx.x);
+        if (v < nv) t[u] = s4[v];
+      }
+#pragma unroll
+      for (int u = 0; u < L; ++u) {
+        const int v = v0 + u * kThreads + static_cast<int>(threadIdx.x);
+        if (v < nv) {
+          struct Pack {
+            S e[E];
+          };
+          const Pack pk = __builtin_bit_cast(Pack, t[u]);
+#pragma unroll
+          for (int k = 0; k < E; ++k) xs[v * E + k] = V::widen(pk.e[k]);
+        }
+      }
+    }
+    done = nv * E;
+  }
+  for (int i = done + static_cast<int>(threadIdx.x); i < w; i += kThreads) xs[i] = V::widen(src[i]);
+}
+
+// Pass 1.  Each workgroup owns one chunk of one panel and is the only one on
+// its compute unit (the panel fills the LDS), so the time until its panel of
+// x is staged is time its stream stands still: kPrefetch quads per lane of
+// the chunk are loaded before the panel, and formed once it is there.  The
+// rest streams in batches of U quads per lane.  Measured on the headline
+// shape: 152 -> 142 us against one prefetched batch of four and a staging
+// loop of single loads.
 // XONLY: the entry's x value itself (widened), not the product; the copy's
 // values are not read (the value gradient's gather of x).
+constexpr int kPrefetch = 8;
+
 template <class V, bool XONLY = false>
 __global__ void __launch_bounds__(kThreads)
     panel_products(const typename V::Storage *__restrict__ data, const uint16_t *__restrict__ col,
@@ -130,44 +175,35 @@ __global__ void __launch_bounds__(kThreads)
     o.v[3] = term(dd.v[3], kk.y >> 16);
     return o;
   };
+  const int64_t t0 = threadIdx.x;
+  Four<S> pd[kPrefetch] = {};
+  uint2 pk[kPrefetch] = {};
+#pragma unroll
+  for (int u = 0; u < kPrefetch; ++u)
+    if (t0 + u * kThreads < nq) {
+      if constexpr (!XONLY) pd[u] = nt_load(d4 + t0 + u * kThreads);
+      pk[u] = nt_load(k4 + t0 + u * kThreads);
+    }
+  stage_panel<V>(xs, x, c0, w);
+  __syncthreads();
+  for (int64_t i = b + threadIdx.x; i < a; i += kThreads)
+    prod[i] = term(XONLY ? S{} : data[i], col[i]);
+#pragma unroll
+  for (int u = 0; u < kPrefetch; ++u)
+    if (t0 + u * kThreads < nq) o4[t0 + u * kThreads] = quad(pd[u], pk[u]);
   // x only: no values are loaded, so twice the column loads are kept in flight
   constexpr int U = XONLY ? 2 * kUnroll : kUnroll;
-  Four<S> d[U] = {};
-  uint2 k[U];
-  int64_t qd = threadIdx.x;
-  bool full = qd + (U - 1) * kThreads < nq;
-  if (full) {
+  int64_t qd = t0 + kPrefetch * kThreads;
+  for (; qd + (U - 1) * kThreads < nq; qd += U * kThreads) {
+    Four<S> d[U] = {};
+    uint2 k[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if constexpr (!XONLY) d[u] = nt_load(d4 + qd + u * kThreads);
       k[u] = nt_load(k4 + qd + u * kThreads);
     }
-  }
-  for (int i = threadIdx.x; i < w; i += kThreads) xs[i] = V::widen(x[c0 + i]);
-  __syncthreads();
-  for (int64_t i = b + threadIdx.x; i < a; i += kThreads)
-    prod[i] = term(XONLY ? S{} : data[i], col[i]);
-  while (full) {
-    Four<S> dc[U];
-    uint2 kc[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      dc[u] = d[u];
-      kc[u] = k[u];
-    }
-    const int64_t next = qd + U * kThreads;
-    const bool full_next = next + (U - 1) * kThreads < nq;
-    if (full_next) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if constexpr (!XONLY) d[u] = nt_load(d4 + next + u * kThreads);
-        k[u] = nt_load(k4 + next + u * kThreads);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) o4[qd + u * kThreads] = quad(dc[u], kc[u]);
-    qd = next;
-    full = full_next;
+    for (int u = 0; u < U; ++u) o4[qd + u * kThreads] = quad(d[u], k[u]);
   }
   for (; qd < nq; qd += kThreads) {
     Four<S> dd = {};

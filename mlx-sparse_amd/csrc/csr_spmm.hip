@@ -127,7 +127,7 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
     }
     return;
   }
-  for (int64_t b = s; b < e; b += kChunk) {
+  auto chunk = [&](int64_t b) {
     int cu[kChunk];
     A au[kChunk];
     int ci = -1;
@@ -152,7 +152,11 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
 #pragma unroll
         for (int c = 0; c < CW; ++c) acc[c] = vmadd<V>(acc[c], au[u], xv[u].v[c]);
       }
-  }
+  };
+  // The first chunk outside the loop: rows of up to 8 values (stencils)
+  // then run straight-line code.
+  chunk(s);
+  for (int64_t b = s + kChunk; b < e; b += kChunk) chunk(b);
 }
 
 template <class V, class I, int CW, bool SHUF>
