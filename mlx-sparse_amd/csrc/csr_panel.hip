@@ -124,6 +124,17 @@ __device__ inline void stage_panel(typename V::Acc *xs, const typename V::Storag
   for (int i = done + static_cast<int>(threadIdx.x); i < w; i += kThreads) xs[i] = V::widen(src[i]);
 }
 
+// A store that is not read back soon (the value gradient).
+template <class T>
+__device__ inline void nt_store(T *p, T v) {
+  if constexpr (sizeof(T) == 8) {
+    using W = NtWord<8>::T;
+    __builtin_nontemporal_store(__builtin_bit_cast(W, v), reinterpret_cast<W *>(p));
+  } else {
+    __builtin_nontemporal_store(v, p);
+  }
+}
+
 // Pass 1.  Each workgroup owns one chunk of one panel and is the only one on
 // its compute unit (the panel fills the LDS), so the time until its panel of
 // x is staged is time its stream stands still: kPrefetch quads per lane of
@@ -391,13 +402,18 @@ __global__ void __launch_bounds__(kFixupThreads)
 // Value gradient of y = A x over the panel layout (out[p] = cot[row(p)] *
 // x[col(p)], the same rounding as the plan-free kernel): the first pass is
 // panel_products<V, true>, which writes each entry's x value; this second
-// pass takes one workgroup per tile, like pass 2 of the SpMV.  It stages the
-// cotangent of each of the tile's virtual rows and, per value position, the
-// position's virtual row; places each entry's x value at its LDS word (the
-// segment runs read as in pass 2); then walks the tile's value positions in
-// order - position p of virtual row v0 + i has word (p - b0) + i - and
-// stores the gradients with coalesced writes.  Only for copies that dropped
-// no value (every position's word is then written).
+// pass takes one workgroup per tile, like pass 2 of the SpMV.  In a tile's
+// LDS words, virtual row v0 + i holds its values at words (p - b0) + i and
+// one more word right after them, its gap.  Each row stores its cotangent
+// in its gap and sets the gap's bit in a bitmap; each entry's x value goes
+// to its word (the segment runs read as in pass 2).  Then the tile's words
+// are walked in order, 64 per wave step - one bitmap word per step: a
+// value word w's row i is the number of gaps before it (a prefix count per
+// bitmap word plus a popcount), its cotangent sits in the next gap, and
+// its gradient goes to position b0 + w - i, so the stores stay coalesced.
+// LDS: the words, TW / 8 bytes of bitmap and a count per bitmap word (67 KB
+// for 4-byte accumulators), so two workgroups share a compute unit.  Only
+// for copies that dropped no value (every value word is then written).
 template <class V, class RP, bool LONG>
 __global__ void __launch_bounds__(kThreads)
     panel_vjp_scatter(const typename V::Acc *__restrict__ xg, const uint16_t *__restrict__ dest,
@@ -409,10 +425,13 @@ __global__ void __launch_bounds__(kThreads)
   using A = typename V::Acc;
   constexpr int TW = 65536 / static_cast<int>(sizeof(A));
   constexpr int NQ = TW / kThreads / 4;
+  constexpr int NB = TW / 64;  // bitmap words
+  static_assert(NB <= kThreads, "one thread per bitmap word");
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  A *xw = reinterpret_cast<A *>(lds_raw);                          // TW words
-  A *cotv = xw + TW;                                               // rows_cap
-  uint16_t *row_at = reinterpret_cast<uint16_t *>(cotv + ((rows_cap + 3) & ~3));  // TW positions
+  A *xw = reinterpret_cast<A *>(lds_raw);                                        // TW words
+  unsigned long long *gap = reinterpret_cast<unsigned long long *>(xw + TW);     // NB
+  uint32_t *before = reinterpret_cast<uint32_t *>(gap + NB);                     // NB
+  uint32_t *wsum = before + NB;                                                  // one per wave
   const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
@@ -420,6 +439,10 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t v1 = clamp64(tile_end[T], v0, std::min<int64_t>(nv, v0 + rows_cap));
   const int64_t b0 = clamp64(static_cast<int64_t>(rowptr[v0]), 0, nnz);
   const int64_t b1 = clamp64(static_cast<int64_t>(rowptr[v1]), b0, std::min<int64_t>(nnz, b0 + TW));
+  if (threadIdx.x < NB) gap[threadIdx.x] = 0;
+  __syncthreads();
+
+  // Rows: the cotangent into the gap word, the gap's bit into the bitmap.
   for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads) {
     const int64_t s = clamp64(static_cast<int64_t>(rowptr[v]), b0, b1);
     const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, b1);
@@ -428,8 +451,11 @@ __global__ void __launch_bounds__(kThreads)
       const int32_t slot = vslot[v];
       r = slot >= 0 ? slot : -1 - static_cast<int64_t>(slot);
     }
-    cotv[v - v0] = V::widen(cot[r]);
-    for (int64_t p = s; p < e; ++p) row_at[p - b0] = static_cast<uint16_t>(v - v0);
+    const int64_t g = (e - b0) + (v - v0);
+    if (g < TW) {
+      xw[g] = V::widen(cot[r]);
+      atomicOr(&gap[g >> 6], 1ull << (g & 63));
+    }
   }
 
   const auto *xq = reinterpret_cast<const ProdQuad<A> *>(xg);
@@ -479,10 +505,53 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
 
-  for (int64_t k = threadIdx.x; k < b1 - b0; k += kThreads) {
-    const int i = row_at[k];
-    const int64_t w = k + i;
-    if (i < rows_cap && w < TW) out[b0 + k] = V::narrow(amul(cotv[i], xw[w]));
+  // Gaps before each bitmap word: a scan of the NB counts (a wave scan,
+  // then the wave totals in order).
+  {
+    uint32_t c = threadIdx.x < NB ? static_cast<uint32_t>(__popcll(gap[threadIdx.x])) : 0u;
+    uint32_t incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t t = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += t;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    uint32_t off = 0;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    if (threadIdx.x < NB) before[threadIdx.x] = off + incl - c;
+    __syncthreads();
+  }
+
+  // The walk: lane l of every wave step holds word w (w % 64 == l), so the
+  // gaps below it in its bitmap word are an mbcnt of that word.
+  const uint32_t npos = static_cast<uint32_t>(b1 - b0);
+  typename V::Storage *ob = out + b0;
+#pragma unroll
+  for (int j = 0; j < TW / kThreads; ++j) {
+    const int w = j * kThreads + static_cast<int>(threadIdx.x);
+    const int k = w >> 6;
+    const unsigned long long bits = gap[k];
+    const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(bhi, __builtin_amdgcn_mbcnt_lo(blo, 0u));
+    const unsigned long long rest = bits >> lane;  // bit 0: w itself
+    const uint32_t pos = static_cast<uint32_t>(w) - (before[k] + below);
+    if ((rest & 1ull) || pos >= npos) continue;  // a gap word, or past the tile's values
+    int g;
+    if (rest != 0) {
+      g = w + static_cast<int>(__builtin_ctzll(rest));
+    } else {  // the row's gap lies in a later bitmap word
+      g = -1;
+      for (int kk = k + 1; kk < NB; ++kk) {
+        const unsigned long long b = gap[kk];
+        if (b != 0) {
+          g = kk * 64 + static_cast<int>(__builtin_ctzll(b));
+          break;
+        }
+      }
+      if (g < 0) continue;
+    }
+    nt_store(ob + pos, V::narrow(amul(xw[g], xw[w])));
   }
 }
 
@@ -499,13 +568,13 @@ size_t pass2_lds(const msx_csr_plan *p) {
 // LDS of one workgroup on gfx950.
 constexpr size_t kMaxLdsBytes = 163840;
 
-// Value-gradient pass 2: the x value of every word, a cotangent per virtual
-// row of the widest tile (rounded to 4), the virtual row of every position.
+// Value-gradient pass 2: the words (x values and gap cotangents), the gap
+// bitmap, the gaps before each bitmap word, one count per wave.
 template <class A>
 size_t vjp_lds(const msx_csr_plan *p) {
-  const size_t rows = sizeof(A) * static_cast<size_t>((p->pn_tile_rows_max + 3) & ~int64_t{3});
-  return sizeof(A) * static_cast<size_t>(p->tile_words) + rows +
-         sizeof(uint16_t) * static_cast<size_t>(p->tile_words);
+  const size_t words = static_cast<size_t>(p->tile_words);
+  return sizeof(A) * words + (words / 64) * (sizeof(unsigned long long) + sizeof(uint32_t)) +
+         sizeof(uint32_t) * kWavesPerGroup;
 }
 
 // Both passes take more than 64 KB of dynamic LDS.  The limit is raised

@@ -53,10 +53,13 @@ __device__ inline Vec<S, CW> load_vec(const S *p) {
   }
 }
 
+// Y is written once and not read back by the kernel: 16-byte stores are
+// non-temporal.
 template <class S, int CW>
 __device__ inline void store_vec(S *p, const Vec<S, CW> &v) {
   if constexpr (CW * sizeof(S) == 16) {
-    *reinterpret_cast<uint4 *>(p) = __builtin_bit_cast(uint4, v);
+    using W = uint32_t __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(__builtin_bit_cast(W, v), reinterpret_cast<W *>(p));
   } else {
 #pragma unroll
     for (int c = 0; c < CW; ++c) p[c] = v.v[c];
