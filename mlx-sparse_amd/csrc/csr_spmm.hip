@@ -622,21 +622,45 @@ __global__ void __launch_bounds__(kThreads)
       continue;
     }
     // Matrix cores: 2 x (K / 16) output blocks of 16 x 16 over the waves,
-    // stored straight to Y (a lane holds four rows of one column).
+    // each wave keeping its blocks' accumulators (a lane holds four rows of
+    // one column); the tile then goes through LDS (the transposed-X area,
+    // free once every wave is done) and out as 16-byte row segments.
+    constexpr int kBlocks = 2 * (K / 16);
+    constexpr int kWaves = kThreads / kWave;
+    constexpr int kPerWave = (kBlocks + kWaves - 1) / kWaves;
     const int lr = lane % 16, lk = 8 * (lane / 16);
-    for (int blk = wave; blk < 2 * (K / 16); blk += kThreads / kWave) {
-      const int rb = blk & 1, cb = blk >> 1;
-      MfmaAcc acc = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t *arow = ad + (rb * 16 + lr) * stride + lk;
-      const uint16_t *bcol = xt + (cb * 16 + lr) * stride + lk;
-      for (int kk = 0; kk < Kp; kk += 32)
-        acc = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk),
-                             *reinterpret_cast<const uint4 *>(bcol + kk), acc);
+    MfmaAcc accs[kPerWave];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = rb * 16 + 4 * (lane / 16) + v;
-        if (row < nr) Y[(r0 + row) * ldy + cb * 16 + lr] = V::narrow(acc[v]);
+    for (int b = 0; b < kPerWave; ++b) {
+      const int blk = wave + kWaves * b;
+      accs[b] = MfmaAcc{0.f, 0.f, 0.f, 0.f};
+      if (blk < kBlocks) {
+        const int rb = blk & 1, cb = blk >> 1;
+        const uint16_t *arow = ad + (rb * 16 + lr) * stride + lk;
+        const uint16_t *bcol = xt + (cb * 16 + lr) * stride + lk;
+        for (int kk = 0; kk < Kp; kk += 32)
+          accs[b] = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk),
+                                   *reinterpret_cast<const uint4 *>(bcol + kk), accs[b]);
       }
+    }
+    __syncthreads();
+    uint16_t *yb = xt;  // kWinRows x K
+#pragma unroll
+    for (int b = 0; b < kPerWave; ++b) {
+      const int blk = wave + kWaves * b;
+      if (blk < kBlocks) {
+        const int rb = blk & 1, cb = blk >> 1;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          yb[(rb * 16 + 4 * (lane / 16) + v) * K + cb * 16 + lr] = V::narrow(accs[b][v]);
+      }
+    }
+    __syncthreads();
+    for (int q = tid; q < nr * CH; q += kThreads) {
+      const int i = q >> LG;
+      const int cc = (q & (CH - 1)) * 8;
+      *reinterpret_cast<uint4 *>(Y + (r0 + i) * ldy + cc) =
+          *reinterpret_cast<const uint4 *>(yb + i * K + cc);
     }
     __syncthreads();  // the next tile overwrites the staged data
   }
