@@ -267,7 +267,7 @@ extern "C" msx_status msx_csr_batched_spmv(msx_vtype vt, msx_itype it, int64_t n
   auto stream = static_cast<hipStream_t>(stream_v);
   if (batch == 1)  // one vector is a one-column SpMM, no transposes
     return launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, 1, X, 0, 1,
-                               Y, 0, 1, stream);
+                               Y, 0, 1, true, stream);
   // Columns padded so that a row of the transposed operands is a whole number
   // of 16-byte vectors (the SpMM's vector path); padding columns read zero.
   const int64_t sv = static_cast<int64_t>(value_bytes(vt));
@@ -283,7 +283,7 @@ extern "C" msx_status msx_csr_batched_spmv(msx_vtype vt, msx_itype it, int64_t n
             : transpose(vt, X, batch, kpad, n_cols, ldx, Xt, kpad, stream);
   if (st == MSX_OK)
     st = launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, kpad, Xt, 0,
-                             kpad, Yt, 0, kpad, stream);
+                             kpad, Yt, 0, kpad, false, stream);  // Yt is read back next
   if (st == MSX_OK)
     st = thin ? narrow(vt, false, Yt, batch, kpad, n_rows, ldy, Y, stream)
               : transpose(vt, Yt, n_rows, n_rows, batch, kpad, Y, ldy, stream);
@@ -312,5 +312,5 @@ extern "C" msx_status msx_csr_batched_spmm(msx_vtype vt, msx_itype it, int64_t n
   if (batch > 0 && n_cols > 0 && k > 0 && nnz > 0 && X == nullptr)
     return fail(MSX_EINVAL, "csr_batched_matmul X is NULL.");
   return launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X,
-                             x_batch, ldx, Y, y_batch, ldy, static_cast<hipStream_t>(stream));
+                             x_batch, ldx, Y, y_batch, ldy, true, static_cast<hipStream_t>(stream));
 }

@@ -195,12 +195,13 @@ msx_status launch_panel_data_vjp(const msx_csr_plan *p, const void *indptr, cons
                                  const void *cot, void *out, hipStream_t stream);
 
 // Y[b] = A X[b] for b < batch: X[b] at X + b * x_batch (row stride ldx),
-// Y[b] at Y + b * y_batch (row stride ldy), all in elements.
+// Y[b] at Y + b * y_batch (row stride ldy), all in elements.  y_nt: Y is
+// stored non-temporally (false when the caller reads it back right away).
 msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
                                int64_t nnz, const void *data, const void *indices,
                                const void *indptr, int64_t batch, int64_t k, const void *X,
                                int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
-                               hipStream_t stream);
+                               bool y_nt, hipStream_t stream);
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,
                        const void *X, int64_t ldx, void *Y, int64_t ldy, const msx_csr_plan *plan,
