@@ -56,13 +56,15 @@ __device__ inline Vec<S, CW> load_vec(const S *p) {
 // Y is written once and not read back by the kernel: 16-byte stores are
 // non-temporal (measured at k = 8 / 64 / 256 on the 3D Poisson matrix: 63 ->
 // 52, 362 -> 351, 1,694 -> 1,650 us), unless the caller reads Y again right
-// away (the batched SpMV's transposed intermediate: nt false).
-template <class S, int CW>
-__device__ inline void store_vec(S *p, const Vec<S, CW> &v, bool nt = true) {
+// away (the batched SpMV's transposed intermediate: NT false).  NT is a
+// template parameter: a runtime choice between the two stores is merged by
+// the compiler into one ordinary store.
+template <class S, int CW, bool NT = true>
+__device__ inline void store_vec(S *p, const Vec<S, CW> &v) {
   if constexpr (CW * sizeof(S) == 16) {
     using W = uint32_t __attribute__((ext_vector_type(4)));
     const W w = __builtin_bit_cast(W, v);
-    if (nt) __builtin_nontemporal_store(w, reinterpret_cast<W *>(p));
+    if constexpr (NT) __builtin_nontemporal_store(w, reinterpret_cast<W *>(p));
     else *reinterpret_cast<W *>(p) = w;
   } else {
 #pragma unroll
@@ -168,13 +170,13 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
 
 // LRT: the group width LR as a compile-time constant (a runtime width in
 // every shuffle and index measured 6 % slower at k = 256); 0 takes LR_rt.
-template <class V, class I, int CW, bool SHUF, int LRT = 0>
+template <class V, class I, int CW, bool SHUF, int LRT = 0, bool NTY = true>
 __global__ void __launch_bounds__(kThreads)
     spmm_rows(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
               const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
               int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
               int64_t nnz, int64_t n_cols, int64_t k, int LR_rt, int64_t n_col_tiles, int64_t x_batch,
-              int64_t y_batch, int y_nt) {
+              int64_t y_batch) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   const int LR = LRT > 0 ? LRT : LR_rt;
@@ -206,7 +208,7 @@ __global__ void __launch_bounds__(kThreads)
     Vec<S, CW> out;
 #pragma unroll
     for (int c = 0; c < CW; ++c) out.v[c] = V::narrow(acc[c]);
-    store_vec<S, CW>(Y + row * ldy + col, out, y_nt != 0);
+    store_vec<S, CW, NTY>(Y + row * ldy + col, out);
   }
 }
 
@@ -216,12 +218,12 @@ __global__ void __launch_bounds__(kThreads)
 // every X row in its L2, halving (G = 2) the X window that a stencil's far
 // neighbours need, at the cost of reading each row's indices/data G times.
 // Sums per column are in stored order, as in spmm_rows.
-template <class V, class I, int CW>
+template <class V, class I, int CW, bool NTY = true>
 __global__ void __launch_bounds__(kThreads)
     spmm_linetile(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                   const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
                   int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
-                  int64_t nnz, int64_t n_cols, int G, int64_t x_batch, int64_t y_batch, int y_nt) {
+                  int64_t nnz, int64_t n_cols, int G, int64_t x_batch, int64_t y_batch) {
   using S = typename V::Storage;
   using A = typename V::Acc;
   X += blockIdx.y * x_batch;
@@ -253,7 +255,7 @@ __global__ void __launch_bounds__(kThreads)
     Vec<S, CW> out;
 #pragma unroll
     for (int c = 0; c < CW; ++c) out.v[c] = V::narrow(acc[c]);
-    store_vec<S, CW>(Y + row * ldy + col, out, y_nt != 0);
+    store_vec<S, CW, NTY>(Y + row * ldy + col, out);
   }
 }
 
@@ -750,9 +752,10 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
     // on XCD x % 8 when batches are stacked along y.
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxBatchGrid) {
       const uint32_t nb = static_cast<uint32_t>(std::min<int64_t>(batch - b0, kMaxBatchGrid));
-      hipLaunchKernelGGL((spmm_linetile<V, I, CWV>), dim3(static_cast<uint32_t>(slots * kNumXcd), nb),
+      auto kern = y_nt ? spmm_linetile<V, I, CWV, true> : spmm_linetile<V, I, CWV, false>;
+      hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(slots * kNumXcd), nb),
                          dim3(kThreads), 0, stream, data, indices, indptr, X + b0 * x_batch, ldx,
-                         Y + b0 * y_batch, ldy, n_rows, nnz, n_cols, G, x_batch, y_batch, y_nt ? 1 : 0);
+                         Y + b0 * y_batch, ldy, n_rows, nnz, n_cols, G, x_batch, y_batch);
       MSX_HIP_TRY(hipGetLastError());
     }
     return MSX_OK;
@@ -771,19 +774,23 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
     S *Yb = Y + b0 * y_batch;
     auto launch = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid, nb), dim3(kThreads), 0, stream, data, indices, indptr, Xb,
-                         ldx, Yb, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles, x_batch, y_batch,
-                         y_nt ? 1 : 0);
+                         ldx, Yb, ldy, n_rows, nnz, n_cols, k, LR, n_col_tiles, x_batch, y_batch);
     };
     if (vec) {
-      switch (LR) {
-      case 1: launch(spmm_rows<V, I, CWV, false, 1>); break;
-      case 2: launch(spmm_rows<V, I, CWV, false, 2>); break;
-      case 4: launch(spmm_rows<V, I, CWV, false, 4>); break;
-      case 8: launch(spmm_rows<V, I, CWV, true, 8>); break;
-      case 16: launch(spmm_rows<V, I, CWV, true, 16>); break;
-      case 32: launch(spmm_rows<V, I, CWV, true, 32>); break;
-      default: launch(spmm_rows<V, I, CWV, true, 64>); break;
-      }
+      auto go = [&](auto nt) {
+        constexpr bool NT = decltype(nt)::value;
+        switch (LR) {
+        case 1: launch(spmm_rows<V, I, CWV, false, 1, NT>); break;
+        case 2: launch(spmm_rows<V, I, CWV, false, 2, NT>); break;
+        case 4: launch(spmm_rows<V, I, CWV, false, 4, NT>); break;
+        case 8: launch(spmm_rows<V, I, CWV, true, 8, NT>); break;
+        case 16: launch(spmm_rows<V, I, CWV, true, 16, NT>); break;
+        case 32: launch(spmm_rows<V, I, CWV, true, 32, NT>); break;
+        default: launch(spmm_rows<V, I, CWV, true, 64, NT>); break;
+        }
+      };
+      if (y_nt) go(std::true_type{});
+      else go(std::false_type{});
     } else {
       if (LR >= kChunk) launch(spmm_rows<V, I, 1, true>);
       else launch(spmm_rows<V, I, 1, false>);
