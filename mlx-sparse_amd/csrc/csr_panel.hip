@@ -39,6 +39,8 @@ constexpr int kWavesPerGroup = kThreads / kWave;
 // Panel runs one pass-2 wave gathers per batch (16 waves x 8 = 128 panels,
 // the count of a 16.8 MB float32 x).
 constexpr int kRunsPerWave = 8;
+// Row bounds each pass-2 thread loads before the tile's products.
+constexpr int kRowsAhead = 4;
 
 __device__ inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -254,17 +256,26 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  // The row bounds of the thread's first row are loaded now; their latency
-  // overlaps the product loads.
+  // The bounds of the thread's first kRowsAhead rows are loaded now; their
+  // latency overlaps the product loads (tiles of short rows hold up to a
+  // few thousand rows, and a bound loaded inside the sum loop would cost a
+  // dependent round trip per row).
   const int64_t r0 = clamp64(tile_begin[T], 0, n_rows);
   const int64_t r1 = clamp64(tile_end[T], r0, n_rows);
   const int64_t b0 = clamp64(static_cast<int64_t>(indptr[r0]), 0, nnz);
-  int64_t s_first = 0, e_first = 0;
-  int32_t slot_first = 0;
-  if (r0 + threadIdx.x < r1) {
-    s_first = static_cast<int64_t>(indptr[r0 + threadIdx.x]);
-    e_first = static_cast<int64_t>(indptr[r0 + threadIdx.x + 1]);
-    if constexpr (LONG) slot_first = vslot[r0 + threadIdx.x];
+  RP s_ahead[kRowsAhead], e_ahead[kRowsAhead];
+  int32_t slot_ahead[kRowsAhead];
+#pragma unroll
+  for (int k = 0; k < kRowsAhead; ++k) {
+    const int64_t r = r0 + threadIdx.x + static_cast<int64_t>(k) * kThreads;
+    s_ahead[k] = 0;
+    e_ahead[k] = 0;
+    slot_ahead[k] = 0;
+    if (r < r1) {
+      s_ahead[k] = indptr[r];
+      e_ahead[k] = indptr[r + 1];
+      if constexpr (LONG) slot_ahead[k] = vslot[r];
+    }
   }
   if (zero_fill) {
     for (int i = threadIdx.x; i < TW; i += kThreads) buf[i] = vzero<A>();
@@ -324,10 +335,25 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
 
-  for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads) {
-    int64_t s = s_first, e = e_first;
-    int32_t slot = slot_first;
-    if (r != r0 + threadIdx.x) {
+  int k_row = 0;
+  for (int64_t r = r0 + threadIdx.x; r < r1; r += kThreads, ++k_row) {
+    int64_t s, e;
+    int32_t slot = 0;
+    if (k_row < kRowsAhead) {
+      // a select over the prefetched rows (no dynamic register indexing)
+      RP sa = s_ahead[0], ea = e_ahead[0];
+      int32_t la = slot_ahead[0];
+#pragma unroll
+      for (int k = 1; k < kRowsAhead; ++k)
+        if (k_row == k) {
+          sa = s_ahead[k];
+          ea = e_ahead[k];
+          la = slot_ahead[k];
+        }
+      s = static_cast<int64_t>(sa);
+      e = static_cast<int64_t>(ea);
+      slot = la;
+    } else {
       s = static_cast<int64_t>(indptr[r]);
       e = static_cast<int64_t>(indptr[r + 1]);
       if constexpr (LONG) slot = vslot[r];
