@@ -490,12 +490,14 @@ __global__ void __launch_bounds__(kThreads)
 // the tile's range takes the stored-order path from global memory instead
 // (its result then equals the reference's).
 typedef float MfmaAcc __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 template <class V>
 struct Mfma16;
 template <>
 struct Mfma16<F16> {
   typedef _Float16 Vec8 __attribute__((ext_vector_type(8)));
+  static constexpr uint16_t kInfBits = 0x7C00;  // magnitude bits >= this: inf or NaN
   __device__ static inline MfmaAcc mma(uint4 a, uint4 b, MfmaAcc c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(Vec8, a),
                                                   __builtin_bit_cast(Vec8, b), c, 0, 0, 0);
@@ -504,23 +506,42 @@ struct Mfma16<F16> {
 template <>
 struct Mfma16<BF16> {
   typedef __bf16 Vec8 __attribute__((ext_vector_type(8)));
+  static constexpr uint16_t kInfBits = 0x7F80;
   __device__ static inline MfmaAcc mma(uint4 a, uint4 b, MfmaAcc c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(Vec8, a),
                                                    __builtin_bit_cast(Vec8, b), c, 0, 0, 0);
   }
 };
 
-constexpr int kMfmaPad = 8;  // halves of padding per LDS row (staggers the banks)
+// Halves of padding per LDS row of the dense block and of the output: with
+// Kp (or k) a multiple of 32 such a row is an odd number of 16-byte units
+// long, so 8 consecutive rows start in 8 different groups of 4 banks (of
+// 32) and stay 16-byte aligned for the operand reads.
+constexpr int kMfmaPad = 8;
+// Halves of padding per row of the transposed X window: an odd number of
+// 4-byte words per row, so the staging writes of 8 columns 8 apart land in
+// different banks.  Its operand reads are 4-byte reads.
+constexpr int kMfmaPadX = 2;
+
+// Halves of the transposed-X area, which afterwards holds the tile's output
+// (kWinRows rows of k + kMfmaPad halves).
+__host__ __device__ inline int64_t mfma_xt_halves(int64_t Kp, int64_t k) {
+  const int64_t a = k * (Kp + kMfmaPadX), b = kWinRows * (k + kMfmaPad);
+  return a > b ? a : b;
+}
 
 // LDS bytes of spmm_window_mfma for a padded window Kp and k columns.
 __host__ __device__ inline int64_t mfma_window_lds(int64_t Kp, int64_t k) {
-  const int64_t stride = Kp + kMfmaPad;
-  return 2 * (kWinRows * stride + k * stride) + 8 * (kWinRows + 2) + 4 * kWinRows * (Kp / 32) + 16;
+  return 2 * (kWinRows * (Kp + kMfmaPad) + mfma_xt_halves(Kp, k)) + 8 * (kWinRows + 2) +
+         4 * kWinRows * (Kp / 32) + 16;
 }
 
 // k in {16, 32, 64, 128, 256}: LG = log2(k / 8), the 16-byte chunks of a row.
+// Up to k = 64 the LDS admits 7 workgroups per CU; the register budget is
+// held to match.
 template <class V, class I, int LG>
 __global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
     spmm_window_mfma(const uint16_t *__restrict__ data, const I *__restrict__ indices,
                      const I *__restrict__ indptr, const uint16_t *__restrict__ X, int64_t ldx,
                      uint16_t *__restrict__ Y, int64_t ldy, int64_t n_rows, int64_t nnz,
@@ -529,10 +550,11 @@ __global__ void __launch_bounds__(kThreads)
   constexpr int CH = 1 << LG;  // 16-byte chunks per X / Y row
   constexpr int K = 8 * CH;    // columns
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const int stride = Kp + kMfmaPad;
+  const int stride = Kp + kMfmaPad;    // dense block rows
+  const int xstride = Kp + kMfmaPadX;  // transposed X rows
   uint16_t *ad = reinterpret_cast<uint16_t *>(lds_raw);              // kWinRows x stride
-  uint16_t *xt = ad + kWinRows * stride;                              // K x stride
-  int64_t *rptr = reinterpret_cast<int64_t *>(xt + K * stride);       // kWinRows + 1
+  uint16_t *xt = ad + kWinRows * stride;                              // K x xstride
+  int64_t *rptr = reinterpret_cast<int64_t *>(xt + mfma_xt_halves(Kp, K));  // kWinRows + 1
   uint32_t *seen = reinterpret_cast<uint32_t *>(rptr + kWinRows + 2);  // kWinRows x Kp / 32
   int *flag = reinterpret_cast<int *>(seen + kWinRows * (Kp / 32));
   const int tid = threadIdx.x;
@@ -555,46 +577,76 @@ __global__ void __launch_bounds__(kThreads)
     for (int i = tid; i < kWinRows * words; i += kThreads) seen[i] = 0;
     if (tid == 0) *flag = 0;
     // X window, transposed two rows at a time (one 4-byte LDS write per
-    // column); rows past the window or past x read as zero, so the padded
-    // part of K adds nothing.
+    // column, packed by a byte permute); rows past the window or past x read
+    // as zero, so the padded part of K adds nothing.  A non-finite X value
+    // in the window would reach every row of the tile through a zero of the
+    // dense block (0 x inf), so such a tile keeps the stored-order sum: the
+    // largest magnitude bits seen are kept per half.
+    u16x2 big = {0, 0};
     for (int wr = 2 * pair0; wr < Kp; wr += 2 * kPairsPerStep) {
       uint4 v0{0, 0, 0, 0}, v1{0, 0, 0, 0};
       if (wr < nw && lo + wr < n_cols) v0 = *reinterpret_cast<const uint4 *>(X + (lo + wr) * ldx + c8);
       if (wr + 1 < nw && lo + wr + 1 < n_cols)
         v1 = *reinterpret_cast<const uint4 *>(X + (lo + wr + 1) * ldx + c8);
       const uint32_t a4[4] = {v0.x, v0.y, v0.z, v0.w}, b4[4] = {v1.x, v1.y, v1.z, v1.w};
+      uint16_t *dst = xt + c8 * xstride + wr;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t lo16 = (a4[j / 2] >> (16 * (j & 1))) & 0xFFFFu;
-        const uint32_t hi16 = (b4[j / 2] >> (16 * (j & 1))) << 16;
-        *reinterpret_cast<uint32_t *>(xt + (c8 + j) * stride + wr) = lo16 | (hi16 & 0xFFFF0000u);
+      for (int j = 0; j < 4; ++j) {
+        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, a4[j] & 0x7FFF7FFFu));
+        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, b4[j] & 0x7FFF7FFFu));
+        // column c8 + 2j: (row wr, row wr + 1) = low halves; c8 + 2j + 1: high halves
+        *reinterpret_cast<uint32_t *>(dst + (2 * j) * xstride) =
+            __builtin_amdgcn_perm(b4[j], a4[j], 0x05040100u);
+        *reinterpret_cast<uint32_t *>(dst + (2 * j + 1) * xstride) =
+            __builtin_amdgcn_perm(b4[j], a4[j], 0x07060302u);
       }
     }
+    const bool nonfinite = (big.x > big.y ? big.x : big.y) >= Mfma16<V>::kInfBits;
     __syncthreads();
-    // Values into the dense block: 8 threads per row, in stored order.
-    {
-      const int i = tid >> 3;
-      if (i < nr) {
-        const int64_t s = rptr[i];
-        const int64_t e = std::max<int64_t>(rptr[i + 1], s);
-        for (int64_t q = s + (tid & 7); q < e; q += 8) {
-          const int64_t c = static_cast<int64_t>(indices[q]);
-          if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols)) continue;  // adds nothing
+    if (nonfinite) *flag = 1;  // after the barrier that follows the flag's reset
+    // Values into the dense block, in stored order: 8 threads per row, each
+    // taking kU entries (8 apart) per step, all loaded before the first is
+    // placed (one memory round trip per step).
+    const int ri = tid >> 3;
+    if (ri < nr) {
+      const int64_t rs = rptr[ri];
+      const int64_t re = std::max<int64_t>(rptr[ri + 1], rs);
+      constexpr int kU = 4;
+      I cu[kU];
+      uint16_t du[kU];
+      auto load_entries = [&](int64_t qb) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int64_t q = qb + 8 * u;
+          cu[u] = q < re ? indices[q] : I{-1};
+          du[u] = q < re ? data[q] : uint16_t{0};
+        }
+      };
+      auto place = [&]() {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int64_t c = static_cast<int64_t>(cu[u]);
+          // past the row, or out of range: adds nothing
+          if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols)) continue;
           const int64_t w = c - lo;
           if (static_cast<uint64_t>(w) >= static_cast<uint64_t>(nw)) {
             *flag = 1;
             continue;
           }
           const uint32_t bit = 1u << (w & 31);
-          if (atomicOr(&seen[i * words + static_cast<int>(w >> 5)], bit) & bit) {
+          if (atomicOr(&seen[ri * words + static_cast<int>(w >> 5)], bit) & bit) {
             *flag = 1;  // repeated (row, column): keep the stored-order sum
             continue;
           }
-          ad[i * stride + static_cast<int>(w)] = data[q];
+          ad[ri * stride + static_cast<int>(w)] = du[u];
         }
-        // row pointers outside the tile's range: keep the stored-order sum
-        if ((tid & 7) == 0 && (s < rptr[0] || rptr[i + 1] < s)) *flag = 1;
+      };
+      for (int64_t qb = rs + (tid & 7); qb < re; qb += 8 * kU) {
+        load_entries(qb);
+        place();
       }
+      // row pointers that decrease or leave the tile's range: stored order
+      if ((tid & 7) == 0 && (rs < rptr[0] || rptr[ri + 1] < rs)) *flag = 1;
     }
     __syncthreads();
     if (*flag) {
@@ -643,14 +695,16 @@ __global__ void __launch_bounds__(kThreads)
       if (blk < kBlocks) {
         const int rb = blk & 1, cb = blk >> 1;
         const uint16_t *arow = ad + (rb * 16 + lr) * stride + lk;
-        const uint16_t *bcol = xt + (cb * 16 + lr) * stride + lk;
-        for (int kk = 0; kk < Kp; kk += 32)
-          accs[b] = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk),
-                                   *reinterpret_cast<const uint4 *>(bcol + kk), accs[b]);
+        const uint32_t *bcol = reinterpret_cast<const uint32_t *>(xt + (cb * 16 + lr) * xstride + lk);
+        for (int kk = 0; kk < Kp; kk += 32) {
+          const uint4 bv{bcol[kk / 2], bcol[kk / 2 + 1], bcol[kk / 2 + 2], bcol[kk / 2 + 3]};
+          accs[b] = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk), bv, accs[b]);
+        }
       }
     }
     __syncthreads();
-    uint16_t *yb = xt;  // kWinRows x K
+    constexpr int KY = K + kMfmaPad;  // output row stride (staggers the banks)
+    uint16_t *yb = xt;                // kWinRows x KY
 #pragma unroll
     for (int b = 0; b < kPerWave; ++b) {
       const int blk = wave + kWaves * b;
@@ -658,7 +712,7 @@ __global__ void __launch_bounds__(kThreads)
         const int rb = blk & 1, cb = blk >> 1;
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          yb[(rb * 16 + 4 * (lane / 16) + v) * K + cb * 16 + lr] = V::narrow(accs[b][v]);
+          yb[(rb * 16 + 4 * (lane / 16) + v) * KY + cb * 16 + lr] = V::narrow(accs[b][v]);
       }
     }
     __syncthreads();
@@ -666,7 +720,7 @@ __global__ void __launch_bounds__(kThreads)
       const int i = q >> LG;
       const int cc = (q & (CH - 1)) * 8;
       *reinterpret_cast<uint4 *>(Y + (r0 + i) * ldy + cc) =
-          *reinterpret_cast<const uint4 *>(yb + i * K + cc);
+          *reinterpret_cast<const uint4 *>(yb + i * KY + cc);
     }
     __syncthreads();  // the next tile overwrites the staged data
   }

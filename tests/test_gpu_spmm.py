@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import _capi
-from _util import assert_rows_close, storage, to_numpy, to_torch
+from _util import assert_rows_close, storage, to_numpy, to_torch, widen
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -251,6 +251,44 @@ def test_window_mfma_tiles_that_keep_stored_order(vtype):
                                       err_msg=f"stored-order tile {t}")
     scale = orc.row_scale(data[keep], kidx, kptr, X, n, vtype=vtype)
     assert_rows_close(got, want, scale, vtype, f"window mfma {vtype} edited")
+    plan.close()
+
+
+@pytest.mark.parametrize("vtype", ["float16", "bfloat16"])
+def test_window_mfma_nonfinite_x_and_unsorted_rows(vtype):
+    """An infinite or NaN X value inside a tile's window would reach every
+    row of the tile through the zeros of its dense block (0 x inf), so that
+    tile keeps the stored-order sum: equal to the oracle bit for bit, finite
+    in the rows that do not read it.  A row whose columns decrease (no
+    repeated pair) stays on the matrix cores, within the 16-bit tolerance."""
+    n, k = 3000, 64
+    m, data = _banded(n, 8, seed=21, vtype=vtype)
+    rng = np.random.default_rng(22)
+    X = _values(rng, (n, k), vtype).copy()
+    ip = m.indptr.astype(np.int64)
+    idx = m.indices.copy()
+    r_rev = 1000  # tile 31: its row's columns reversed
+    idx[ip[r_rev]:ip[r_rev + 1]] = idx[ip[r_rev]:ip[r_rev + 1]][::-1].copy()
+    c_inf, c_nan = 455, 2001  # tiles 14 and 62
+    X[c_inf, 3] = storage(np.array([np.inf]), vtype)[0]
+    X[c_nan, 40] = storage(np.array([np.nan]), vtype)[0]
+    d, i, p = to_torch(data, vtype, DEV), to_torch(idx, None, DEV), to_torch(m.indptr, None, DEV)
+    plan = _capi.Plan(p, n, m.nnz, data=d, indices=i, n_cols=n)
+    assert plan.info().window_rows > 0
+    got = to_numpy(_capi.spmm(d, i, p, to_torch(X, vtype, DEV), n, n, plan=plan))
+    torch.cuda.synchronize()
+    want = orc.csr_matmul(data, idx.astype(np.int64), ip, X, n, vtype=vtype, n_threads=8)
+    for c in (c_inf, c_nan):
+        t = c // 32
+        g, w = widen(got[32 * t:32 * t + 32], vtype), widen(want[32 * t:32 * t + 32], vtype)
+        assert np.array_equal(g, w, equal_nan=True), f"stored-order tile {t}"
+        readers = np.unique(np.repeat(np.arange(n), np.diff(ip))[idx == c])
+        others = np.setdiff1d(np.arange(32 * t, 32 * t + 32), readers)
+        assert len(others) > 0 and np.isfinite(widen(got[others], vtype)).all()
+    finite = np.isfinite(widen(want, vtype)).all(axis=1)
+    Xf = np.where(np.isfinite(widen(X, vtype)), X, storage(np.zeros(1), vtype)[0])
+    scale = orc.row_scale(data, idx.astype(np.int64), ip, Xf, n, vtype=vtype)
+    assert_rows_close(got[finite], want[finite], scale[finite], vtype, f"window mfma {vtype} non-finite")
     plan.close()
 
 
