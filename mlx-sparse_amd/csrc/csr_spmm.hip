@@ -518,6 +518,22 @@ struct Mfma16<BF16> {
 // long, so 8 consecutive rows start in 8 different groups of 4 banks (of
 // 32) and stay 16-byte aligned for the operand reads.
 constexpr int kMfmaPad = 8;
+
+// DPP moves within rows of 16 lanes (pure VALU): lane i takes lane i - 1
+// (row_shr:1), or lane (i - 9) mod 16 (row_ror:9: lanes 0 and 8 take lanes 7
+// and 15, the last lane of their group of 8).
+template <int CTRL>
+__device__ inline int64_t dpp_move(int64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, 0xF, 0xF, false);
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+template <int CTRL>
+__device__ inline int32_t dpp_move(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppShr1 = 0x111, kDppRor9 = 0x129;
 // Halves of padding per row of the transposed X window: an odd number of
 // 4-byte words per row, so the staging writes of 8 columns 8 apart land in
 // different banks.  Its operand reads are 4-byte reads.
@@ -574,8 +590,10 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
     if (tid <= nr) rptr[tid] = clamp64(static_cast<int64_t>(indptr[r0 + tid]), 0, nnz);
     for (int i = tid; i < kWinRows * stride / 8; i += kThreads)
       reinterpret_cast<uint4 *>(ad)[i] = uint4{0, 0, 0, 0};
-    for (int i = tid; i < kWinRows * words; i += kThreads) seen[i] = 0;
-    if (tid == 0) *flag = 0;
+    if (tid == 0) {
+      flag[0] = 0;  // the tile keeps the stored-order sum
+      flag[1] = 0;  // some row's columns do not increase
+    }
     // X window, transposed two rows at a time (one 4-byte LDS write per
     // column, packed by a byte permute); rows past the window or past x read
     // as zero, so the padded part of K adds nothing.  A non-finite X value
@@ -603,17 +621,25 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
     }
     const bool nonfinite = (big.x > big.y ? big.x : big.y) >= Mfma16<V>::kInfBits;
     __syncthreads();
-    if (nonfinite) *flag = 1;  // after the barrier that follows the flag's reset
-    // Values into the dense block, in stored order: 8 threads per row, each
-    // taking kU entries (8 apart) per step, all loaded before the first is
-    // placed (one memory round trip per step).
-    const int ri = tid >> 3;
+    if (nonfinite) flag[0] = 1;  // after the barrier that follows the flags' reset
+    // Values into the dense block, in stored order: 8 threads per row (lanes
+    // 8 g .. 8 g + 7 of a wave), each taking kU entries (8 apart) per step,
+    // all loaded before the first is placed (one memory round trip per
+    // step).  Each entry's column is compared with the entry before it
+    // (moved across lanes by DPP): when every row's columns increase, no
+    // (row, column) pair repeats and the entries go straight to the block.
+    const int ri = tid >> 3, j8 = tid & 7;
+    int64_t rs = 0, re = 0;
     if (ri < nr) {
-      const int64_t rs = rptr[ri];
-      const int64_t re = std::max<int64_t>(rptr[ri + 1], rs);
+      rs = rptr[ri];
+      re = std::max<int64_t>(rptr[ri + 1], rs);
+    }
+    if (ri < nr) {
       constexpr int kU = 4;
       I cu[kU];
       uint16_t du[kU];
+      bool unsorted = false;
+      I carry = I{0};  // the previous step's last column of the lane
       auto load_entries = [&](int64_t qb) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
@@ -622,34 +648,59 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
           du[u] = q < re ? data[q] : uint16_t{0};
         }
       };
-      auto place = [&]() {
+      auto place = [&](int64_t qb) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
+          const int64_t q = qb + 8 * u;
+          // the entry before q: lane j8 - 1's, or for j8 = 0 lane 7's of the
+          // step before.  Both moves run on every lane (a lane reads only
+          // lanes that run the move with it).
+          const I from_left = dpp_move<kDppShr1>(cu[u]);
+          const I from_last = dpp_move<kDppRor9>(u > 0 ? cu[u > 0 ? u - 1 : 0] : carry);
+          const I before = j8 > 0 ? from_left : from_last;
+          if (q < re && q > rs && static_cast<int64_t>(cu[u]) <= static_cast<int64_t>(before))
+            unsorted = true;
           const int64_t c = static_cast<int64_t>(cu[u]);
           // past the row, or out of range: adds nothing
           if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols)) continue;
           const int64_t w = c - lo;
           if (static_cast<uint64_t>(w) >= static_cast<uint64_t>(nw)) {
-            *flag = 1;
-            continue;
-          }
-          const uint32_t bit = 1u << (w & 31);
-          if (atomicOr(&seen[ri * words + static_cast<int>(w >> 5)], bit) & bit) {
-            *flag = 1;  // repeated (row, column): keep the stored-order sum
+            flag[0] = 1;
             continue;
           }
           ad[ri * stride + static_cast<int>(w)] = du[u];
         }
+        carry = cu[kU - 1];
       };
-      for (int64_t qb = rs + (tid & 7); qb < re; qb += 8 * kU) {
+      // the same number of steps on the row's 8 lanes (the moves read them)
+      for (int64_t qb = rs + j8; qb - j8 < re; qb += 8 * kU) {
         load_entries(qb);
-        place();
+        place(qb);
       }
+      if (unsorted) flag[1] = 1;
       // row pointers that decrease or leave the tile's range: stored order
-      if ((tid & 7) == 0 && (rs < rptr[0] || rptr[ri + 1] < rs)) *flag = 1;
+      if (j8 == 0 && (rs < rptr[0] || rptr[ri + 1] < rs)) flag[0] = 1;
     }
     __syncthreads();
-    if (*flag) {
+    if (flag[1] && !flag[0]) {
+      // Some row's columns do not increase: look for a repeated (row,
+      // column) pair with a bitmap of the dense block.
+      for (int i = tid; i < kWinRows * words; i += kThreads) seen[i] = 0;
+      __syncthreads();
+      if (ri < nr) {
+        for (int64_t q = rs + j8; q < re; q += 8) {
+          const int64_t c = static_cast<int64_t>(indices[q]);
+          const int64_t w = c - lo;
+          if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(n_cols) ||
+              static_cast<uint64_t>(w) >= static_cast<uint64_t>(nw))
+            continue;
+          const uint32_t bit = 1u << (w & 31);
+          if (atomicOr(&seen[ri * words + static_cast<int>(w >> 5)], bit) & bit) flag[0] = 1;
+        }
+      }
+    }
+    __syncthreads();
+    if (flag[0]) {
       // Stored order from global memory, 8 columns per thread.
       for (int q = tid; q < nr * CH; q += kThreads) {
         const int i = q >> LG;

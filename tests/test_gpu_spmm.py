@@ -254,6 +254,41 @@ def test_window_mfma_tiles_that_keep_stored_order(vtype):
     plan.close()
 
 
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_window_mfma_repeated_columns_at_every_lane_boundary(index_dtype):
+    """Eight lanes take a row's entries, four per lane and step (entry e on
+    lane e % 8, step e // 32): a repeated column is caught whether the pair
+    sits on neighbouring lanes (0, 1), across the group's wrap (7, 8) or
+    across two steps (31, 32); its tile keeps the stored-order sum, equal to
+    the oracle bit for bit."""
+    vtype, n, k = "float16", 4000, 64
+    m, data = _banded(n, 24, seed=31, vtype=vtype, index_dtype=index_dtype)
+    rng = np.random.default_rng(32)
+    X = _values(rng, (n, k), vtype)
+    ip = m.indptr.astype(np.int64)
+    idx = m.indices.copy()
+    rows = {}
+    lengths = np.diff(ip)
+    for r0, (a, b) in zip((330, 1650, 2990), ((0, 1), (7, 8), (31, 32))):
+        r = r0 + int(np.argmax(lengths[r0:] > b))  # the first row from r0 long enough
+        assert lengths[r] > b, (r, lengths[r])
+        idx[ip[r] + b] = idx[ip[r] + a]
+        rows[r] = (a, b)
+    d, i, p = to_torch(data, vtype, DEV), to_torch(idx, None, DEV), to_torch(m.indptr, None, DEV)
+    plan = _capi.Plan(p, n, m.nnz, data=d, indices=i, n_cols=n)
+    assert plan.info().window_rows > 0
+    got = to_numpy(_capi.spmm(d, i, p, to_torch(X, vtype, DEV), n, n, plan=plan))
+    torch.cuda.synchronize()
+    want = orc.csr_matmul(data, idx.astype(np.int64), ip, X, n, vtype=vtype, n_threads=8)
+    for r in rows:
+        t = r // 32
+        np.testing.assert_array_equal(got[32 * t:32 * t + 32], want[32 * t:32 * t + 32],
+                                      err_msg=f"stored-order tile {t}, pair {rows[r]}")
+    scale = orc.row_scale(data, idx.astype(np.int64), ip, X, n, vtype=vtype)
+    assert_rows_close(got, want, scale, vtype, "window mfma repeated columns")
+    plan.close()
+
+
 @pytest.mark.parametrize("vtype", ["float16", "bfloat16"])
 def test_window_mfma_nonfinite_x_and_unsorted_rows(vtype):
     """An infinite or NaN X value inside a tile's window would reach every
