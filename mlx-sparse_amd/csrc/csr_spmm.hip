@@ -518,6 +518,8 @@ struct Mfma16<BF16> {
 // long, so 8 consecutive rows start in 8 different groups of 4 banks (of
 // 32) and stay 16-byte aligned for the operand reads.
 constexpr int kMfmaPad = 8;
+// Entries of one tile read through 32-bit descriptor offsets.
+constexpr int64_t kMfmaTileEntries = int64_t{1} << 26;
 
 // DPP moves within rows of 16 lanes (pure VALU): lane i takes lane i - 1
 // (row_shr:1), or lane (i - 9) mod 16 (row_ror:9: lanes 0 and 8 take lanes 7
@@ -587,7 +589,17 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
         Kp, std::max<int64_t>(0, static_cast<int64_t>(win[2 * t + 1]) - lo + 1)));
     const int64_t r0 = t * kWinRows;
     const int nr = static_cast<int>(std::min<int64_t>(kWinRows, n_rows - r0));
-    if (tid <= nr) rptr[tid] = clamp64(static_cast<int64_t>(indptr[r0 + tid]), 0, nnz);
+    // Loads through descriptors: whatever lies past a descriptor reads as
+    // zero, so no load needs a branch and every load of this part is issued
+    // before the first wait.  The tile's row pointers:
+    const auto r_ptr = make_rsrc(indptr + r0, sizeof(I) * static_cast<uint64_t>(nr + 1));
+    const I rp = buffer_index<I>(r_ptr, static_cast<uint32_t>(tid * sizeof(I)));
+    // the window's X rows inside x (nv of them; rows past them read zero,
+    // so the padded part of K adds nothing), two row pairs per thread and
+    // step:
+    const int64_t nv = std::max<int64_t>(0, std::min<int64_t>(nw, n_cols - lo));
+    const auto r_x = make_rsrc(X + (nv > 0 ? lo : 0) * ldx, 2 * static_cast<uint64_t>(nv * ldx));
+    const uint32_t row_bytes = static_cast<uint32_t>(2 * ldx);
     for (int i = tid; i < kWinRows * stride / 8; i += kThreads)
       reinterpret_cast<uint4 *>(ad)[i] = uint4{0, 0, 0, 0};
     if (tid == 0) {
@@ -595,30 +607,34 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
       flag[1] = 0;  // some row's columns do not increase
     }
     // X window, transposed two rows at a time (one 4-byte LDS write per
-    // column, packed by a byte permute); rows past the window or past x read
-    // as zero, so the padded part of K adds nothing.  A non-finite X value
-    // in the window would reach every row of the tile through a zero of the
-    // dense block (0 x inf), so such a tile keeps the stored-order sum: the
-    // largest magnitude bits seen are kept per half.
+    // column, packed by a byte permute).  A non-finite X value in the window
+    // would reach every row of the tile through a zero of the dense block
+    // (0 x inf), so such a tile keeps the stored-order sum: the largest
+    // magnitude bits seen are kept per half.
     u16x2 big = {0, 0};
-    for (int wr = 2 * pair0; wr < Kp; wr += 2 * kPairsPerStep) {
-      uint4 v0{0, 0, 0, 0}, v1{0, 0, 0, 0};
-      if (wr < nw && lo + wr < n_cols) v0 = *reinterpret_cast<const uint4 *>(X + (lo + wr) * ldx + c8);
-      if (wr + 1 < nw && lo + wr + 1 < n_cols)
-        v1 = *reinterpret_cast<const uint4 *>(X + (lo + wr + 1) * ldx + c8);
-      const uint32_t a4[4] = {v0.x, v0.y, v0.z, v0.w}, b4[4] = {v1.x, v1.y, v1.z, v1.w};
+    auto stage = [&](int wr, const u32x4 &v0, const u32x4 &v1) {
       uint16_t *dst = xt + c8 * xstride + wr;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, a4[j] & 0x7FFF7FFFu));
-        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, b4[j] & 0x7FFF7FFFu));
+        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, v0.w[j] & 0x7FFF7FFFu));
+        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, v1.w[j] & 0x7FFF7FFFu));
         // column c8 + 2j: (row wr, row wr + 1) = low halves; c8 + 2j + 1: high halves
         *reinterpret_cast<uint32_t *>(dst + (2 * j) * xstride) =
-            __builtin_amdgcn_perm(b4[j], a4[j], 0x05040100u);
+            __builtin_amdgcn_perm(v1.w[j], v0.w[j], 0x05040100u);
         *reinterpret_cast<uint32_t *>(dst + (2 * j + 1) * xstride) =
-            __builtin_amdgcn_perm(b4[j], a4[j], 0x07060302u);
+            __builtin_amdgcn_perm(v1.w[j], v0.w[j], 0x07060302u);
       }
+    };
+    for (int wr = 2 * pair0; wr < Kp; wr += 4 * kPairsPerStep) {
+      const int wr2 = wr + 2 * kPairsPerStep;
+      const uint32_t o = static_cast<uint32_t>(wr) * row_bytes + 2 * c8;
+      const uint32_t o2 = static_cast<uint32_t>(wr2) * row_bytes + 2 * c8;
+      const u32x4 v0 = BufLoad<16>::load(r_x, o), v1 = BufLoad<16>::load(r_x, o + row_bytes);
+      const u32x4 v2 = BufLoad<16>::load(r_x, o2), v3 = BufLoad<16>::load(r_x, o2 + row_bytes);
+      stage(wr, v0, v1);
+      if (wr2 < Kp) stage(wr2, v2, v3);
     }
+    if (tid <= nr) rptr[tid] = clamp64(static_cast<int64_t>(rp), 0, nnz);
     const bool nonfinite = (big.x > big.y ? big.x : big.y) >= Mfma16<V>::kInfBits;
     __syncthreads();
     if (nonfinite) flag[0] = 1;  // after the barrier that follows the flags' reset
@@ -634,7 +650,15 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
       rs = rptr[ri];
       re = std::max<int64_t>(rptr[ri + 1], rs);
     }
-    if (ri < nr) {
+    // The tile's entries [q0, q1) through descriptors (offsets relative to
+    // q0, so at most kMfmaTileEntries of them; a tile with more holds
+    // repeated pairs and keeps the stored-order sum).
+    const int64_t q0 = rptr[0], q1 = std::max<int64_t>(rptr[nr], q0);
+    if (q1 - q0 > kMfmaTileEntries) {
+      if (tid == 0) flag[0] = 1;
+    } else if (ri < nr) {
+      const auto r_ind = make_rsrc(indices + q0, sizeof(I) * static_cast<uint64_t>(q1 - q0));
+      const auto r_dat = make_rsrc(data + q0, 2 * static_cast<uint64_t>(q1 - q0));
       constexpr int kU = 4;
       I cu[kU];
       uint16_t du[kU];
@@ -644,8 +668,13 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
           const int64_t q = qb + 8 * u;
-          cu[u] = q < re ? indices[q] : I{-1};
-          du[u] = q < re ? data[q] : uint16_t{0};
+          // rows out of [q0, q1) (decreasing row pointers) read zero and
+          // are caught below
+          const uint32_t e = static_cast<uint32_t>(q - q0);
+          const I c = buffer_index<I>(r_ind, e * static_cast<uint32_t>(sizeof(I)));
+          const uint16_t v = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r_dat, 2 * e, 0, 0));
+          cu[u] = q < re ? c : I{-1};
+          du[u] = v;
         }
       };
       auto place = [&](int64_t qb) {
@@ -810,7 +839,8 @@ msx_status spmm_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *d
         plan->n_win == (n_rows + kWinRows - 1) / kWinRows && lg > 0) {
       const int64_t Kp = (plan->win_rows_max + 31) / 32 * 32;
       const int64_t lds = mfma_window_lds(Kp, k);
-      if (lds <= kWinLdsBytes) {
+      // the kernel reads a window of Kp rows of X through one descriptor
+      if (lds <= kWinLdsBytes && static_cast<uint64_t>(Kp + 1) * 2 * ldx <= kGatherMaxBytes) {
         const uint32_t grid = static_cast<uint32_t>(std::min<int64_t>(plan->n_win, kMaxGrid));
         auto go = [&](auto kern) {
           hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), static_cast<size_t>(lds), stream,
