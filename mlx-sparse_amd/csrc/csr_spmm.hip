@@ -170,8 +170,12 @@ __device__ inline void row_segment(const typename V::Storage *__restrict__ data,
 
 // LRT: the group width LR as a compile-time constant (a runtime width in
 // every shuffle and index measured 6 % slower at k = 256); 0 takes LR_rt.
+// Float32 rows of 16-byte chunks are held to 72 registers, 7 waves per SIMD
+// (k = 256 on the 3D Poisson matrix: 1,641 -> 1,607 us; at 64 registers the
+// spills cost 30 %).
 template <class V, class I, int CW, bool SHUF, int LRT = 0, bool NTY = true>
 __global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(std::is_same_v<V, F32> && CW == 4 ? 7 : 1, 8)))
     spmm_rows(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
               const I *__restrict__ indptr, const typename V::Storage *__restrict__ X,
               int64_t ldx, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t n_rows,
