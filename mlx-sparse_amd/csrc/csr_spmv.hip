@@ -174,12 +174,18 @@ __device__ __forceinline__ void block_products_n(int nch,
 // XCD g % 8) sum long-row pieces, the rest walk the short blocks; the two
 // halves gather from different places (one slice of x per XCD, all of x),
 // so they overlap instead of running back to back.
-// 16-bit values with int32 indices at W = 512 are held to 72 registers, 7
-// waves per SIMD instead of 6 (banded f16 / bf16: 71 -> 67 us; float32 runs
-// slower so, 75 -> 78 us, and keeps its 78 registers).
+// 16-bit values with int32 indices at W = 512, and complex64 with int32
+// indices at W = 256 outside the fused launch, are held to 72 registers, 7
+// waves per SIMD instead of 6 (banded f16 / bf16: 71 -> 67 us, complex64
+// 128 -> 123 us; float32 runs slower so, 75 -> 78 us, and keeps its 78
+// registers; the other variants would spill).
 template <class V, class I, int W, int AUX, bool FUSE>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(W == 512 && sizeof(I) == 4 && sizeof(typename V::Storage) == 2 ? 7 : 1, 8)))
+__attribute__((amdgpu_waves_per_eu((W == 512 && sizeof(I) == 4 && sizeof(typename V::Storage) == 2) ||
+                                    (W == 256 && !FUSE && sizeof(I) == 4 && sizeof(typename V::Storage) == 8)
+                                ? 7
+                                : 1,
+                                8)))
     spmv_blocks(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
                 const I *__restrict__ indptr, const typename V::Storage *__restrict__ x,
                 typename V::Storage *__restrict__ y, const int32_t *__restrict__ bounds,
