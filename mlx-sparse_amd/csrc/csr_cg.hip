@@ -459,13 +459,19 @@ msx_status spmv(const Solve &s, const float *x, float *y) {
                      s.stream);
 }
 
-// Host loop: enqueue iterations in batches (1, 2, 4, ... up to 32 between
-// reads of the state), stop when the device says so or maxiter is reached.
+// Host loop: enqueue iterations in batches between reads of the state
+// (BatchSchedule), stop when the device says so or maxiter is reached.
+// The residual of the schedule: sqrt(r.r) (CG) or of the true r.r (PCG).
 template <class Step>
-msx_status drive(const Solve &s, int64_t maxiter, CgState *st_dev, CgState *st_host,
+msx_status drive(const Solve &s, int64_t maxiter, CgState *st_dev, CgState *st_host, bool pcg,
                  Step step) {
+  auto residual = [&]() {
+    const double rr = pcg ? st_host->true_rr : st_host->rr;
+    return std::sqrt(std::max(rr, 0.0));
+  };
   int64_t done = 0;
-  int64_t batch = 1;
+  BatchSchedule schedule;
+  int64_t batch = schedule.next(0, residual(), st_host->tol);  // the start's state
   while (done < maxiter) {
     const int64_t todo = std::min(batch, maxiter - done);
     for (int64_t k = 0; k < todo; ++k) {
@@ -476,7 +482,8 @@ msx_status drive(const Solve &s, int64_t maxiter, CgState *st_dev, CgState *st_h
     MSX_HIP_TRY(hipMemcpyAsync(st_host, st_dev, sizeof(CgState), hipMemcpyDeviceToHost, s.stream));
     MSX_HIP_TRY(hipStreamSynchronize(s.stream));
     if (!st_host->running) return MSX_OK;
-    batch = std::min<int64_t>(batch * 2, 32);
+    // still running: every enqueued iteration has completed
+    batch = schedule.next(done, residual(), st_host->tol);
   }
   return MSX_OK;
 }
@@ -563,7 +570,7 @@ msx_status solve(const Solve &s, const float *b, const float *x0, const float *i
       MSX_HIP_TRY(hipGetLastError());
       return MSX_OK;
     };
-    e = drive(s, maxiter, st, &host, step);
+    e = drive(s, maxiter, st, &host, pcg, step);
     if (e != MSX_OK) return e;
     if (pcg)
       hipLaunchKernelGGL(pcg_finish, dim3(1), dim3(kWave), 0, s.stream, st);

@@ -771,7 +771,8 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, 
   int64_t next = 1;    // next iteration to launch
   int close_prev = 0;  // whether bi_p(next) closes iteration next - 1
   const double *dots = start_part;
-  int64_t batch = 1;
+  BatchSchedule schedule;  // its residual: the last iteration closed on the device
+  int64_t batch = schedule.next(0, host.residual, host.tol);  // the start's state
   for (;;) {
     if (host.running) {
       const int64_t last = std::min(maxiter, next + batch - 1);
@@ -796,7 +797,7 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, 
       MSX_HIP_TRY(hipGetLastError());
       if ((e = read_state(s, st, &host)) != MSX_OK) return e;
       next = last + 1;
-      batch = std::min<int64_t>(batch * 2, 32);
+      batch = schedule.next(last, host.residual, host.tol);
       continue;
     }
     if (host.pause == kNoPause) break;
@@ -856,7 +857,9 @@ msx_status minres(const System &s, const float *b, const float *x0, float *x, fl
                      maxiter, st);
   MSX_HIP_TRY(hipGetLastError());
   if ((e = read_state(s, st, &host)) != MSX_OK) return e;
-  int64_t next = 1, batch = 1;
+  int64_t next = 1;
+  BatchSchedule schedule;  // its residual: the last iteration tested on the device
+  int64_t batch = schedule.next(0, host.residual, host.tol);  // the start's state
   while (host.running && next <= maxiter) {
     const int64_t last = std::min(maxiter, next + batch - 1);
     for (int64_t k = next; k <= last; ++k) {
@@ -885,7 +888,7 @@ msx_status minres(const System &s, const float *b, const float *x0, float *x, fl
     MSX_HIP_TRY(hipGetLastError());
     if ((e = read_state(s, st, &host)) != MSX_OK) return e;
     next = last + 1;
-    batch = std::min<int64_t>(batch * 2, 32);
+    batch = schedule.next(last, host.residual, host.tol);
   }
   *result = {host.status, host.completed, host.residual, 0};
   return MSX_OK;

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+
 #include "msx_device.h"
 
 namespace msx {
@@ -100,6 +102,37 @@ __device__ inline void read_totals(const double *part, int nparts, double (&t)[k
       }                                                                                      \
     }                                                                                        \
   }
+
+// Host side: iterations to enqueue before the next read of the solver
+// state.  An iteration enqueued past the solve's stop still runs its SpMVs
+// in full (only the vector passes return early), while a read costs a round
+// trip to the host; so the batch doubles (1, 2, 4, ... kMaxBatch) until two
+// reads give a rate of residual decrease, and from then on covers the
+// iterations that rate needs to reach the tolerance (at most kMaxBatch).
+// The device alone decides where the solve stops, so results do not depend
+// on the batches.
+class BatchSchedule {
+ public:
+  static constexpr int64_t kMaxBatch = 32;
+  // `completed` iterations done, their residual norm, the solve's tolerance.
+  int64_t next(int64_t completed, double residual, double tol) {
+    int64_t b = doubling_;
+    if (k_ >= 0 && completed > k_ && residual > tol && tol > 0.0 && residual < res_) {
+      const double rate = std::log(residual / res_) / static_cast<double>(completed - k_);
+      const double need = std::ceil(std::log(tol / residual) / rate);
+      b = need >= static_cast<double>(kMaxBatch) ? kMaxBatch : (need < 1.0 ? 1 : static_cast<int64_t>(need));
+    }
+    doubling_ = doubling_ * 2 < kMaxBatch ? doubling_ * 2 : kMaxBatch;
+    k_ = completed;
+    res_ = residual;
+    return b;
+  }
+
+ private:
+  int64_t doubling_ = 1;
+  int64_t k_ = -1;
+  double res_ = 0.0;
+};
 
 // Workgroups of a solver pass over n elements (kUnroll per thread and round).
 inline uint32_t blocks_for(int64_t n) {
