@@ -482,17 +482,18 @@ __global__ void __launch_bounds__(kThreads)
 // 16).  One 256-thread workgroup per 32-row tile: the tile's values are
 // scattered into a dense 32 x Kp block of its window in LDS (Kp: the
 // plan's widest window rounded up to 32 columns), the window's X rows are
-// staged transposed (each column's Kp values contiguous, so every MFMA
-// operand of a lane is one 16-byte read), and v_mfma_f32_16x16x32 forms
+// staged transposed (each column's Kp values contiguous, so a lane's MFMA
+// operand is four 4-byte reads), and v_mfma_f32_16x16x32 forms
 // the 32 x k tile of Y with float32 accumulation (lane layout, checked on
 // gfx950: A lane l holds row l % 16, k = 8 (l / 16) + 0..7; B lane l holds
 // column l % 16, the same k; D lane l holds column l % 16, rows
 // 4 (l / 16) + 0..3).  A product of two 16-bit values is exact in float32;
 // the sums run in the matrix core's order, within the float16 / bfloat16
 // tolerance of the reference's stored-order sum.  A tile with a repeated
-// (row, column) pair, a column outside its window or row pointers outside
-// the tile's range takes the stored-order path from global memory instead
-// (its result then equals the reference's).
+// (row, column) pair, a column outside its window, row pointers outside
+// the tile's range or a non-finite X value in its window takes the
+// stored-order path from global memory instead (its result then equals the
+// reference's).
 typedef float MfmaAcc __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
