@@ -281,12 +281,19 @@ extern "C" msx_status msx_csr_batched_spmv(msx_vtype vt, msx_itype it, int64_t n
   const bool thin = kpad <= kNarrow;
   st = thin ? narrow(vt, true, X, batch, kpad, n_cols, ldx, Xt, stream)
             : transpose(vt, X, batch, kpad, n_cols, ldx, Xt, kpad, stream);
+  // Up to 8 16-byte vectors per row of Xt the sums go straight to Y;
+  // otherwise through an n_rows x kpad SpMM result and its transpose.
+  bool direct = false;
   if (st == MSX_OK)
+    st = launch_spmv_batch_rows(vt, it, n_rows, n_cols, nnz, data, indices, indptr, Xt, kpad, Y,
+                                ldy, batch, stream, &direct);
+  if (st == MSX_OK && !direct) {
     st = launch_spmm_batched(vt, it, n_rows, n_cols, nnz, data, indices, indptr, 1, kpad, Xt, 0,
                              kpad, Yt, 0, kpad, false, stream);  // Yt is read back next
-  if (st == MSX_OK)
-    st = thin ? narrow(vt, false, Yt, batch, kpad, n_rows, ldy, Y, stream)
-              : transpose(vt, Yt, n_rows, n_rows, batch, kpad, Y, ldy, stream);
+    if (st == MSX_OK)
+      st = thin ? narrow(vt, false, Yt, batch, kpad, n_rows, ldy, Y, stream)
+                : transpose(vt, Yt, n_rows, n_rows, batch, kpad, Y, ldy, stream);
+  }
   const hipError_t e = hipFreeAsync(scratch, stream);
   if (st == MSX_OK && e != hipSuccess) return hip_fail(e, "csr_batched_matvec scratch release");
   return st;

@@ -216,6 +216,42 @@ __attribute__((amdgpu_waves_per_eu(std::is_same_v<V, F32> && CW == 4 ? 7 : 1, 8)
   }
 }
 
+// Batched SpMV from the transposed vectors: Xt is n_cols x kpad (row c
+// holds x_b[c] of every vector b, padded to whole 16-byte vectors), and
+// each row's sums go straight to the vectors of Y (Y[b * ldy + row], b <
+// batch) - the same sums as spmm_rows over Xt, without an n_rows x kpad
+// intermediate and its transpose.  A wave's stores for one vector are
+// consecutive rows.
+template <class V, class I, int CW, int LR>
+__global__ void __launch_bounds__(kThreads)
+    spmv_batch_rows(const typename V::Storage *__restrict__ data, const I *__restrict__ indices,
+                    const I *__restrict__ indptr, const typename V::Storage *__restrict__ Xt,
+                    int64_t kpad, typename V::Storage *__restrict__ Y, int64_t ldy, int64_t batch,
+                    int64_t n_rows, int64_t nnz, int64_t n_cols) {
+  using S = typename V::Storage;
+  using A = typename V::Acc;
+  constexpr int kRowsPerGroup = kThreads / LR;
+  const int g = threadIdx.x / LR;
+  const int l = threadIdx.x % LR;
+  const int64_t n_tiles = (n_rows + kRowsPerGroup - 1) / kRowsPerGroup;
+  for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_tiles; t += gridDim.x) {
+    const int64_t row = t * kRowsPerGroup + g;
+    if (row >= n_rows) continue;
+    const int64_t s = clamp64(static_cast<int64_t>(indptr[row]), 0, nnz);
+    const int64_t e = clamp64(static_cast<int64_t>(indptr[row + 1]), s, nnz);
+    A acc[CW];
+    const S *Xc = Xt + static_cast<int64_t>(l) * CW;
+    row_segment<V, I, CW, (LR >= kChunk)>(
+        data, indices, [&](int c) { return load_vec<S, CW>(Xc + static_cast<int64_t>(c) * kpad); },
+        n_cols, s, e, l, LR, acc);
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const int64_t b = static_cast<int64_t>(l) * CW + c;
+      if (b < batch) Y[b * ldy + row] = V::narrow(acc[c]);
+    }
+  }
+}
+
 // Line-tiled SpMM for X rows of G whole 128-byte cache lines.  XCD x
 // (workgroup g runs on XCD g % 8) owns column tile x % G (one line) and a
 // contiguous G/8 share of the rows.  Each XCD then keeps only its own line of
@@ -1016,6 +1052,62 @@ msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64
                                bool y_nt, hipStream_t stream) {
   return spmm_dispatch(vt, it, n_rows, n_cols, nnz, data, indices, indptr, batch, k, X, x_batch,
                        ldx, Y, y_batch, ldy, nullptr, y_nt, stream);
+}
+
+template <class V, class I>
+bool batch_rows_typed(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                      const void *indices, const void *indptr, const void *Xt, int64_t kpad,
+                      void *Y, int64_t ldy, int64_t batch, hipStream_t stream) {
+  using S = typename V::Storage;
+  constexpr int CW = static_cast<int>(16 / sizeof(S));
+  if (kpad % CW != 0 || (reinterpret_cast<uintptr_t>(Xt) & 15u) != 0) return false;
+  const int64_t LR = kpad / CW;
+  if (LR != 1 && LR != 2 && LR != 4 && LR != 8) return false;
+  const int64_t rows_per_group = kThreads / LR;
+  const int64_t tiles = (n_rows + rows_per_group - 1) / rows_per_group;
+  const uint32_t grid = static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(tiles, kMaxGrid)));
+  const auto *d = static_cast<const S *>(data);
+  const auto *ix = static_cast<const I *>(indices);
+  const auto *ip = static_cast<const I *>(indptr);
+  const auto *x = static_cast<const S *>(Xt);
+  auto *y = static_cast<S *>(Y);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, d, ix, ip, x, kpad, y, ldy,
+                       batch, n_rows, nnz, n_cols);
+  };
+  switch (LR) {
+  case 1: go(spmv_batch_rows<V, I, CW, 1>); break;
+  case 2: go(spmv_batch_rows<V, I, CW, 2>); break;
+  case 4: go(spmv_batch_rows<V, I, CW, 4>); break;
+  default: go(spmv_batch_rows<V, I, CW, 8>); break;
+  }
+  return true;
+}
+
+template <class V>
+bool batch_rows_vt(msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                   const void *indices, const void *indptr, const void *Xt, int64_t kpad, void *Y,
+                   int64_t ldy, int64_t batch, hipStream_t stream) {
+  return it == MSX_I32 ? batch_rows_typed<V, int32_t>(n_rows, n_cols, nnz, data, indices, indptr,
+                                                       Xt, kpad, Y, ldy, batch, stream)
+                       : batch_rows_typed<V, int64_t>(n_rows, n_cols, nnz, data, indices, indptr,
+                                                       Xt, kpad, Y, ldy, batch, stream);
+}
+
+msx_status launch_spmv_batch_rows(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                                  int64_t nnz, const void *data, const void *indices,
+                                  const void *indptr, const void *Xt, int64_t kpad, void *Y,
+                                  int64_t ldy, int64_t batch, hipStream_t stream, bool *done) {
+  bool ok = false;
+  switch (vt) {
+  case MSX_F32: ok = batch_rows_vt<F32>(it, n_rows, n_cols, nnz, data, indices, indptr, Xt, kpad, Y, ldy, batch, stream); break;
+  case MSX_F16: ok = batch_rows_vt<F16>(it, n_rows, n_cols, nnz, data, indices, indptr, Xt, kpad, Y, ldy, batch, stream); break;
+  case MSX_BF16: ok = batch_rows_vt<BF16>(it, n_rows, n_cols, nnz, data, indices, indptr, Xt, kpad, Y, ldy, batch, stream); break;
+  case MSX_C64: ok = batch_rows_vt<C64>(it, n_rows, n_cols, nnz, data, indices, indptr, Xt, kpad, Y, ldy, batch, stream); break;
+  }
+  *done = ok;
+  if (ok) MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
 }
 
 msx_status build_windows(msx_csr_plan *p, const void *indices, const void *indptr,

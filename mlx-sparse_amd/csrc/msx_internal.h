@@ -202,6 +202,14 @@ msx_status launch_spmm_batched(msx_vtype vt, msx_itype it, int64_t n_rows, int64
                                const void *indptr, int64_t batch, int64_t k, const void *X,
                                int64_t x_batch, int64_t ldx, void *Y, int64_t y_batch, int64_t ldy,
                                bool y_nt, hipStream_t stream);
+
+// Batched SpMV from transposed vectors (Xt: n_cols x kpad, 16-byte aligned
+// rows) into batch-major Y (Y[b * ldy + i], b < batch); *done is false when
+// kpad is not a width the kernel takes (nothing is launched then).
+msx_status launch_spmv_batch_rows(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
+                                  int64_t nnz, const void *data, const void *indices,
+                                  const void *indptr, const void *Xt, int64_t kpad, void *Y,
+                                  int64_t ldy, int64_t batch, hipStream_t stream, bool *done);
 msx_status launch_spmm(msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols, int64_t nnz,
                        const void *data, const void *indices, const void *indptr, int64_t k,
                        const void *X, int64_t ldx, void *Y, int64_t ldy, const msx_csr_plan *plan,
