@@ -247,7 +247,12 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
       const int64_t b = static_cast<int64_t>(l) * CW + c;
-      if (b < batch) Y[b * ldy + row] = V::narrow(acc[c]);
+      if (b >= batch) continue;
+      // float32: non-temporal (each wave writes whole lines, read by no one here)
+      if constexpr (std::is_same_v<V, F32>)
+        __builtin_nontemporal_store(V::narrow(acc[c]), Y + b * ldy + row);
+      else
+        Y[b * ldy + row] = V::narrow(acc[c]);
     }
   }
 }
