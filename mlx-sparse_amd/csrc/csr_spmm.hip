@@ -523,8 +523,10 @@ __global__ void __launch_bounds__(kThreads)
 // 16).  One 256-thread workgroup per 32-row tile: the tile's values are
 // scattered into a dense 32 x Kp block of its window in LDS (Kp: the
 // plan's widest window rounded up to 32 columns), the window's X rows are
-// staged transposed (each column's Kp values contiguous, so a lane's MFMA
-// operand is four 4-byte reads), and v_mfma_f32_16x16x32 forms
+// staged row-major by buffer-to-LDS loads (no registers), each lane's MFMA
+// operand of X comes from two transposing LDS reads (ds_read_b64_tr_b16:
+// within 16 lanes, lane j's 4 values are element j % 4 of the addresses of
+// lanes 4 t + j / 4, t = 0..3 - checked on gfx950), and v_mfma_f32_16x16x32 forms
 // the 32 x k tile of Y with float32 accumulation (lane layout, checked on
 // gfx950: A lane l holds row l % 16, k = 8 (l / 16) + 0..7; B lane l holds
 // column l % 16, the same k; D lane l holds column l % 16, rows
@@ -582,17 +584,27 @@ __device__ inline int32_t dpp_move(int32_t v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 constexpr int kDppShr1 = 0x111, kDppRor9 = 0x129;
-// Halves of padding per row of the transposed X window: an odd number of
-// 4-byte words per row, so the staging writes of 8 columns 8 apart land in
-// different banks.  Its operand reads are 4-byte reads.
-constexpr int kMfmaPadX = 2;
-
-// Halves of the transposed-X area, which afterwards holds the tile's output
-// (kWinRows rows of k + kMfmaPad halves).
+// The X window in LDS: Kp rows of k halves, row-major, each row's 16-byte
+// chunks permuted by a swizzle of the row (below).  The area afterwards holds
+// the tile's output (kWinRows rows of k + kMfmaPad halves).
 __host__ __device__ inline int64_t mfma_xt_halves(int64_t Kp, int64_t k) {
-  const int64_t a = k * (Kp + kMfmaPadX), b = kWinRows * (k + kMfmaPad);
+  const int64_t a = k * Kp, b = kWinRows * (k + kMfmaPad);
   return a > b ? a : b;
 }
+
+// Chunk c of window row r sits at chunk slot c ^ 2 x(r) of its row.  A
+// transposing operand read takes 32 bytes (two chunks, an even pair) from
+// each of 4 consecutive rows; x(r) in 0..3 moves those pairs into 4
+// different 32-byte bank groups (of 128 bytes).  With P = CH / 2 pairs per
+// row, rows already start in different groups for P < 4.
+template <int CH>
+__device__ inline int mfma_swizzle(int r) {
+  constexpr int P = CH / 2;
+  constexpr int S = P >= 4 ? 0 : (P == 2 ? 1 : 2);
+  return 2 * ((r & 3) >> S);
+}
+
+typedef short MfmaHalf4 __attribute__((ext_vector_type(4)));
 
 // LDS bytes of spmm_window_mfma for a padded window Kp and k columns.
 __host__ __device__ inline int64_t mfma_window_lds(int64_t Kp, int64_t k) {
@@ -615,9 +627,8 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
   constexpr int K = 8 * CH;    // columns
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int stride = Kp + kMfmaPad;    // dense block rows
-  const int xstride = Kp + kMfmaPadX;  // transposed X rows
   uint16_t *ad = reinterpret_cast<uint16_t *>(lds_raw);              // kWinRows x stride
-  uint16_t *xt = ad + kWinRows * stride;                              // K x xstride
+  uint16_t *xt = ad + kWinRows * stride;                              // Kp x K, swizzled
   int64_t *rptr = reinterpret_cast<int64_t *>(xt + mfma_xt_halves(Kp, K));  // kWinRows + 1
   uint32_t *seen = reinterpret_cast<uint32_t *>(rptr + kWinRows + 2);  // kWinRows x Kp / 32
   int *flag = reinterpret_cast<int *>(seen + kWinRows * (Kp / 32));
@@ -625,10 +636,11 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
   const int lane = tid % kWave;
   const int wave = tid / kWave;
   const int words = Kp / 32;
-  // staging: thread tid owns column chunk c8 and X-row pair tid >> LG (+ steps)
-  const int c8 = (tid & (CH - 1)) * 8;
-  const int pair0 = tid >> LG;
-  constexpr int kPairsPerStep = kThreads >> LG;
+  // staging: one buffer-to-LDS load per lane and step writes 16 bytes at
+  // 16 * lane of its wave's destination, so a wave step covers 64 / CH rows
+  // (lane: row lane / CH, chunk slot lane % CH)
+  constexpr int kRowsPerLoad = kWave / CH;
+  const int ld_row = lane / CH, ld_slot = lane % CH;
   for (int64_t t = xcd_remap(blockIdx.x, gridDim.x); t < n_win; t += gridDim.x) {
     const int64_t lo = win[2 * t];
     const int nw = static_cast<int>(std::min<int64_t>(
@@ -652,38 +664,32 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
       flag[0] = 0;  // the tile keeps the stored-order sum
       flag[1] = 0;  // some row's columns do not increase
     }
-    // X window, transposed two rows at a time (one 4-byte LDS write per
-    // column, packed by a byte permute).  A non-finite X value in the window
-    // would reach every row of the tile through a zero of the dense block
-    // (0 x inf), so such a tile keeps the stored-order sum: the largest
-    // magnitude bits seen are kept per half.
-    u16x2 big = {0, 0};
-    auto stage = [&](int wr, const u32x4 &v0, const u32x4 &v1) {
-      uint16_t *dst = xt + c8 * xstride + wr;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, v0.w[j] & 0x7FFF7FFFu));
-        big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, v1.w[j] & 0x7FFF7FFFu));
-        // column c8 + 2j: (row wr, row wr + 1) = low halves; c8 + 2j + 1: high halves
-        *reinterpret_cast<uint32_t *>(dst + (2 * j) * xstride) =
-            __builtin_amdgcn_perm(v1.w[j], v0.w[j], 0x05040100u);
-        *reinterpret_cast<uint32_t *>(dst + (2 * j + 1) * xstride) =
-            __builtin_amdgcn_perm(v1.w[j], v0.w[j], 0x07060302u);
-      }
-    };
-    for (int wr = 2 * pair0; wr < Kp; wr += 4 * kPairsPerStep) {
-      const int wr2 = wr + 2 * kPairsPerStep;
-      const uint32_t o = static_cast<uint32_t>(wr) * row_bytes + 2 * c8;
-      const uint32_t o2 = static_cast<uint32_t>(wr2) * row_bytes + 2 * c8;
-      const u32x4 v0 = BufLoad<16>::load(r_x, o), v1 = BufLoad<16>::load(r_x, o + row_bytes);
-      const u32x4 v2 = BufLoad<16>::load(r_x, o2), v3 = BufLoad<16>::load(r_x, o2 + row_bytes);
-      stage(wr, v0, v1);
-      if (wr2 < Kp) stage(wr2, v2, v3);
+    // X window rows into LDS by buffer-to-LDS loads (no registers; rows past
+    // the window's nv rows read zero, so the padded part of K adds nothing).
+    for (int r0 = wave * kRowsPerLoad; r0 < Kp; r0 += (kThreads / kWave) * kRowsPerLoad) {
+      const int r = r0 + ld_row;
+      const uint32_t voff = static_cast<uint32_t>(r) * row_bytes +
+                            16u * static_cast<uint32_t>(ld_slot ^ mfma_swizzle<CH>(r));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r_x, (__attribute__((address_space(3))) void *)(xt + r0 * K), 16, voff, 0, 0, 0);
     }
     if (tid <= nr) rptr[tid] = clamp64(static_cast<int64_t>(rp), 0, nnz);
-    const bool nonfinite = (big.x > big.y ? big.x : big.y) >= Mfma16<V>::kInfBits;
+    __builtin_amdgcn_s_waitcnt(0);  // the buffer-to-LDS loads have landed
     __syncthreads();
-    if (nonfinite) flag[0] = 1;  // after the barrier that follows the flags' reset
+    {
+      // A non-finite X value in the window would reach every row of the tile
+      // through a zero of the dense block (0 x inf), so such a tile keeps the
+      // stored-order sum: the largest magnitude bits of the window.
+      u16x2 big = {0, 0};
+      for (int i = tid; i < Kp * CH; i += kThreads) {
+        const uint4 v = reinterpret_cast<const uint4 *>(xt)[i];
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, w4[j] & 0x7FFF7FFFu));
+      }
+      if ((big.x > big.y ? big.x : big.y) >= Mfma16<V>::kInfBits) flag[0] = 1;
+    }
     // Values into the dense block, in stored order: 8 threads per row (lanes
     // 8 g .. 8 g + 7 of a wave), each taking kU entries (8 apart) per step,
     // all loaded before the first is placed (one memory round trip per
@@ -813,6 +819,18 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
     constexpr int kWaves = kThreads / kWave;
     constexpr int kPerWave = (kBlocks + kWaves - 1) / kWaves;
     const int lr = lane % 16, lk = 8 * (lane / 16);
+    // B operand of lane (k-group gq = lane / 16, column n = lane % 16): two
+    // transposing reads of 4 rows each; the lane's address is row
+    // kk + 8 gq + 4 h + n / 4, columns 16 cb + 4 (n % 4) .. + 3, and the read
+    // hands it rows kk + 8 gq + 4 h + 0..3 of column 16 cb + n.
+    const int b_row = 8 * (lane / 16) + (lr >> 2);
+    const int b_col = 4 * (lr & 3);
+    auto b_read = [&](int row, int col) {
+      const int c = col >> 3;
+      const int off = row * (2 * K) + 16 * (c ^ mfma_swizzle<CH>(row)) + 2 * (col & 7);
+      return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) MfmaHalf4 *)(reinterpret_cast<unsigned char *>(xt) + off));
+    };
     MfmaAcc accs[kPerWave];
 #pragma unroll
     for (int b = 0; b < kPerWave; ++b) {
@@ -821,9 +839,11 @@ __attribute__((amdgpu_waves_per_eu(LG <= 3 ? 7 : 1, 8)))
       if (blk < kBlocks) {
         const int rb = blk & 1, cb = blk >> 1;
         const uint16_t *arow = ad + (rb * 16 + lr) * stride + lk;
-        const uint32_t *bcol = reinterpret_cast<const uint32_t *>(xt + (cb * 16 + lr) * xstride + lk);
         for (int kk = 0; kk < Kp; kk += 32) {
-          const uint4 bv{bcol[kk / 2], bcol[kk / 2 + 1], bcol[kk / 2 + 2], bcol[kk / 2 + 3]};
+          const MfmaHalf4 lo4 = b_read(kk + b_row, 16 * cb + b_col);
+          const MfmaHalf4 hi4 = b_read(kk + b_row + 4, 16 * cb + b_col);
+          const uint2 l2 = __builtin_bit_cast(uint2, lo4), h2 = __builtin_bit_cast(uint2, hi4);
+          const uint4 bv{l2.x, l2.y, h2.x, h2.y};
           accs[b] = Mfma16<V>::mma(*reinterpret_cast<const uint4 *>(arow + kk), bv, accs[b]);
         }
       }
