@@ -458,6 +458,8 @@ __global__ void __launch_bounds__(kThreads)
   unsigned long long *gap = reinterpret_cast<unsigned long long *>(xw + TW);     // NB
   uint32_t *before = reinterpret_cast<uint32_t *>(gap + NB);                     // NB
   uint32_t *wsum = before + NB;                                                  // one per wave
+  int32_t *nextg = reinterpret_cast<int32_t *>(wsum + kWavesPerGroup);           // NB
+  int32_t *wmin = nextg + NB;                                                    // one per wave
   const int64_t T = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
@@ -546,6 +548,27 @@ __global__ void __launch_bounds__(kThreads)
     uint32_t off = 0;
     for (int w = 0; w < wave; ++w) off += wsum[w];
     if (threadIdx.x < NB) before[threadIdx.x] = off + incl - c;
+    // The first gap after each bitmap word (where the last row that starts
+    // in the word has its gap when it runs past the word): an exclusive
+    // suffix minimum of the words' first gaps.
+    int32_t first = INT32_MAX;
+    if (threadIdx.x < NB) {
+      const unsigned long long b = gap[threadIdx.x];
+      if (b != 0) first = static_cast<int32_t>(threadIdx.x) * 64 + static_cast<int32_t>(__builtin_ctzll(b));
+    }
+    int32_t suf = first;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int32_t t = __shfl_down(suf, d, kWave);
+      if (lane + d < kWave) suf = t < suf ? t : suf;
+    }
+    if (lane == 0) wmin[wave] = suf;
+    __syncthreads();
+    int32_t later = INT32_MAX;
+    for (int v = wave + 1; v < NB / kWave; ++v) later = wmin[v] < later ? wmin[v] : later;
+    int32_t next_in_wave = __shfl_down(suf, 1, kWave);
+    if (lane == kWave - 1) next_in_wave = INT32_MAX;
+    if (threadIdx.x < NB) nextg[threadIdx.x] = next_in_wave < later ? next_in_wave : later;
     __syncthreads();
   }
 
@@ -563,20 +586,9 @@ __global__ void __launch_bounds__(kThreads)
     const unsigned long long rest = bits >> lane;  // bit 0: w itself
     const uint32_t pos = static_cast<uint32_t>(w) - (before[k] + below);
     if ((rest & 1ull) || pos >= npos) continue;  // a gap word, or past the tile's values
-    int g;
-    if (rest != 0) {
-      g = w + static_cast<int>(__builtin_ctzll(rest));
-    } else {  // the row's gap lies in a later bitmap word
-      g = -1;
-      for (int kk = k + 1; kk < NB; ++kk) {
-        const unsigned long long b = gap[kk];
-        if (b != 0) {
-          g = kk * 64 + static_cast<int>(__builtin_ctzll(b));
-          break;
-        }
-      }
-      if (g < 0) continue;
-    }
+    // the row's gap: in this bitmap word, or the first gap of a later word
+    const int g = rest != 0 ? w + static_cast<int>(__builtin_ctzll(rest)) : nextg[k];
+    if (g >= TW) continue;  // none (INT32_MAX)
     nt_store(ob + pos, V::narrow(amul(xw[g], xw[w])));
   }
 }
@@ -599,8 +611,8 @@ constexpr size_t kMaxLdsBytes = 163840;
 template <class A>
 size_t vjp_lds(const msx_csr_plan *p) {
   const size_t words = static_cast<size_t>(p->tile_words);
-  return sizeof(A) * words + (words / 64) * (sizeof(unsigned long long) + sizeof(uint32_t)) +
-         sizeof(uint32_t) * kWavesPerGroup;
+  return sizeof(A) * words + (words / 64) * (sizeof(unsigned long long) + 2 * sizeof(uint32_t)) +
+         2 * sizeof(uint32_t) * kWavesPerGroup;
 }
 
 // Both passes take more than 64 KB of dynamic LDS.  The limit is raised
