@@ -437,8 +437,11 @@ __global__ void __launch_bounds__(kFixupThreads)
 // value word w's row i is the number of gaps before it (a prefix count per
 // bitmap word plus a popcount), its cotangent sits in the next gap, and
 // its gradient goes to position b0 + w - i, so the stores stay coalesced.
-// LDS: the words, TW / 8 bytes of bitmap and a count per bitmap word (67 KB
-// for 4-byte accumulators), so two workgroups share a compute unit.  Only
+// A row whose gap lies past its bitmap word takes the first gap of a later
+// word, precomputed per word (a suffix minimum) so that no lane searches.
+// LDS: the words, TW / 8 bytes of bitmap, a count and a next gap per bitmap
+// word (68 KB for 4-byte accumulators), so two workgroups share a compute
+// unit.  Only
 // for copies that dropped no value (every value word is then written).
 template <class V, class RP, bool LONG>
 __global__ void __launch_bounds__(kThreads)
