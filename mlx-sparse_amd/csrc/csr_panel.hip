@@ -441,8 +441,8 @@ __global__ void __launch_bounds__(kFixupThreads)
 // word, precomputed per word (a suffix minimum) so that no lane searches.
 // LDS: the words, TW / 8 bytes of bitmap, a count and a next gap per bitmap
 // word (68 KB for 4-byte accumulators), so two workgroups share a compute
-// unit.  Only
-// for copies that dropped no value (every value word is then written).
+// unit.  Only for copies that dropped no value (every value word is then
+// written).
 template <class V, class RP, bool LONG>
 __global__ void __launch_bounds__(kThreads)
     panel_vjp_scatter(const typename V::Acc *__restrict__ xg, const uint16_t *__restrict__ dest,
