@@ -226,6 +226,43 @@ def test_data_vjp_through_panel_plan(vtype, index_dtype, bad_cols):
         plan.close()
 
 
+@pytest.mark.parametrize("vtype", ["float32", "complex64"])
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_data_vjp_through_panel_plan_rows_past_bitmap_words(vtype, index_dtype):
+    """Rows of 65..256 values and no long row (W = 256): a row's gap word
+    lies one to four 64-word bitmap words after its first value, with words
+    holding no gap in between, so each value finds its row's gap through
+    the next-gap table of its bitmap word.  Empty rows, rows of one value
+    and a last row that ends the matrix are mixed in.  Bit-exact against
+    the oracle."""
+    rng = np.random.default_rng(31)
+    n_rows, n_cols = 4000, 150_000
+    lengths = rng.integers(65, 256, n_rows)
+    lengths[rng.random(n_rows) < 0.05] = 0
+    lengths[rng.random(n_rows) < 0.05] = 1
+    lengths[-1] = 255
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    nnz = int(indptr[-1])
+    indices = rng.integers(0, n_cols, nnz).astype(index_dtype)
+    indptr = indptr.astype(index_dtype)
+    data = _values(rng, nnz, vtype)
+    x = _values(rng, n_cols, vtype)
+    cot = _values(rng, n_rows, vtype)
+    want = orc.csr_data_vjp(indices, indptr, x, cot, n_rows, n_cols, nnz, vtype=vtype)
+    d, i, p = _dev(data, vtype), _dev(indices), _dev(indptr)
+    plan = _capi.Plan(p, n_rows, nnz, 256, data=d, indices=i, n_cols=n_cols,
+                      slice_mode=_capi.SLICE_PANELS)
+    info = plan.info()
+    assert info.n_panels > 0 and info.n_long_rows == 0
+    print(f"data_vjp panels wide rows {vtype} {np.dtype(index_dtype).name}", flush=True)
+    for _ in range(2):
+        got = _capi.spmv_data_vjp(i, p, _dev(x, vtype), _dev(cot, vtype), n_rows, n_cols,
+                                  plan=plan)
+        np.testing.assert_array_equal(_bytes(to_numpy(got)), _bytes(want))
+    plan.close()
+
+
 @pytest.mark.parametrize("vtype", VTYPES)
 def test_deterministic_route_equals_one_worker_reference(vtype):
     # transpose, then the zero-start stored-order SpMM with k = 1: every
