@@ -435,8 +435,9 @@ void transpose_product(int64_t n_rows, int64_t n_cols, int64_t k, const void *da
 // CSR of A^T by a counting sort: column counts, prefix, then the rows in
 // order, so every column lists its entries by increasing row.
 template <class V, class I>
-void transpose_csr(int64_t n_rows, int64_t n_cols, const void *data, const void *indices,
-                   const void *indptr, void *t_data, void *t_indices, void *t_indptr) {
+void transpose_csr(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                   const void *indices, const void *indptr, void *t_data, void *t_indices,
+                   void *t_indptr) {
   const auto *d = static_cast<const typename V::S *>(data);
   const auto *ix = static_cast<const I *>(indices);
   const auto *ip = static_cast<const I *>(indptr);
@@ -459,6 +460,13 @@ void transpose_csr(int64_t n_rows, int64_t n_cols, const void *data, const void 
       td[slot] = d[p];
       ti[slot] = static_cast<I>(row);
     }
+  // dropped values (columns out of range): zero bits and row 0 past
+  // t_indptr[n_cols] (nnz is the length of the output buffers), the same
+  // tail as the GPU transpose writes
+  for (int64_t slot = next[n_cols]; slot < nnz; ++slot) {
+    memset(&td[slot], 0, sizeof(td[slot]));
+    ti[slot] = I(0);
+  }
 }
 
 // Value gradients: g[p] = sum_q cot[row, q] * X[col, q] from zero, or with
@@ -698,9 +706,11 @@ struct TransposeProductCpu {
 
 template <class V, class I>
 struct TransposeCsrCpu {
-  static void run(int64_t n_rows, int64_t n_cols, const void *data, const void *indices,
-                  const void *indptr, void *t_data, void *t_indices, void *t_indptr) {
-    cpu::transpose_csr<V, I>(n_rows, n_cols, data, indices, indptr, t_data, t_indices, t_indptr);
+  static void run(int64_t n_rows, int64_t n_cols, int64_t nnz, const void *data,
+                  const void *indices, const void *indptr, void *t_data, void *t_indices,
+                  void *t_indptr) {
+    cpu::transpose_csr<V, I>(n_rows, n_cols, nnz, data, indices, indptr, t_data, t_indices,
+                             t_indptr);
   }
 };
 
@@ -726,8 +736,8 @@ extern "C" msx_status msx_csr_transpose_cpu(msx_vtype vt, msx_itype it, int64_t 
   if (t_indptr == nullptr || (nnz > 0 && (t_data == nullptr || t_indices == nullptr)))
     return fail(MSX_EINVAL, "csr_transpose output buffers must be non-NULL.");
   return guarded("csr_transpose", [&] {
-    dispatch_cpu<TransposeCsrCpu>(vt, it, n_rows, n_cols, data, indices, indptr, t_data, t_indices,
-                                  t_indptr);
+    dispatch_cpu<TransposeCsrCpu>(vt, it, n_rows, n_cols, nnz, data, indices, indptr, t_data,
+                                  t_indices, t_indptr);
   });
 }
 

@@ -91,7 +91,8 @@ __device__ inline void atomic_acc(c64 *p, c64 v) {
 }
 
 // out[i] = src[pos[i]] (conjugated on request) for pos[i] in [0, n_src);
-// entries with another position are left alone.
+// entries with another position (the dropped values past t_indptr[n_cols])
+// get zero bits, as a fresh transpose writes them.
 template <class S>
 __global__ void __launch_bounds__(kThreads)
     gather_positions(const S *__restrict__ src, int64_t n_src, const int32_t *__restrict__ pos,
@@ -99,7 +100,10 @@ __global__ void __launch_bounds__(kThreads)
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
        i += static_cast<int64_t>(gridDim.x) * kThreads) {
     const int64_t p = pos[i];
-    if (p < 0 || p >= n_src) continue;
+    if (p < 0 || p >= n_src) {
+      out[i] = S(0);
+      continue;
+    }
     S v = src[p];
     if constexpr (sizeof(S) == 8) {
       if (conjugate) {
@@ -195,7 +199,11 @@ __global__ void __launch_bounds__(kThreads)
                      int64_t n_cols, S *__restrict__ t_data, I *__restrict__ t_indices) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < nnz;
        i += static_cast<int64_t>(gridDim.x) * kThreads) {
-    if (static_cast<int64_t>(key[i]) >= n_cols) continue;  // dropped: past t_indptr[n_cols]
+    if (static_cast<int64_t>(key[i]) >= n_cols) {  // dropped: past t_indptr[n_cols]
+      t_data[i] = S{};
+      t_indices[i] = I(0);
+      continue;
+    }
     const int64_t p = clamp64(pos[i], 0, nnz - 1);
     t_data[i] = data[p];
     t_indices[i] = row[p];
@@ -240,8 +248,9 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Sorted pairs -> t_data, t_indices, and t_indptr[c] = first sorted index
-// with key >= c, written by the index where the key crosses c.  With kPos
-// the entries past t_indptr[n_cols] (dropped values) get position -1.
+// with key >= c, written by the index where the key crosses c.  The entries
+// past t_indptr[n_cols] (dropped values) get zero bits and row 0 (position
+// -1 with kPos).
 template <class S, class I, bool kPos = false>
 __global__ void __launch_bounds__(kThreads)
     packed_unpack(const uint32_t *__restrict__ key, const uint64_t *__restrict__ val, int64_t nnz,
@@ -259,8 +268,9 @@ __global__ void __launch_bounds__(kThreads)
       __builtin_memcpy(&d, &bits, sizeof(S));
       t_data[i] = d;
       t_indices[i] = static_cast<I>(v >> 32);
-    } else if constexpr (kPos) {
-      if (i < nnz) t_data[i] = S(-1);
+    } else if (i < nnz) {  // dropped values: zero bits (position -1 with kPos), row 0
+      t_data[i] = kPos ? S(-1) : S(0);
+      t_indices[i] = I(0);
     }
   }
 }

@@ -37,7 +37,9 @@ The column-panel layout of a bound plan (csr_panel_build.hip; exported by
   padded to a multiple of 4 entries, so ``seg_begin[k]`` is the sum over
   keys k' < k of ceil(count(k') / 4) * 4 (k = 0 .. n_panels * n_tiles).
 
-Without long rows the virtual rows are the rows.
+Without long rows the virtual rows are the rows.  ``virtual_slots`` gives
+each virtual row's output slot (its row, or -1 - row for a chunk of a long
+row) and each row's first virtual row.
 
 Pinned by ``panel_layout_loop`` (plain per-row loops) and by the tile and
 segment invariants in the same test file.
@@ -119,6 +121,42 @@ def virtual_rows(indptr, nnz: int, W: int = 256):
     vs_full = np.concatenate([vs, [np.clip(p[n], 0, nnz)]]) if n > 0 else np.zeros(1, np.int64)
     ve = np.maximum(vs_full[1:], vs)
     return vs.astype(np.int64), ve.astype(np.int64), row
+
+
+def virtual_slots(indptr, nnz: int, W: int = 256):
+    """(vslot, vbase) of the virtual rows (csr_panel_build.hip vrow_fill):
+    vslot[v] = r for the one virtual row of a short row r, -1 - r for each
+    chunk of a long row r; vbase[r] = the first virtual row of row r
+    (vbase[n] = the number of virtual rows).  Pass 2 of the SpMV stores a
+    virtual row's sum at y[vslot[v]] when vslot[v] >= 0, else at
+    partial[v]; the long-row fixup adds partial[vbase[r] .. vbase[r+1]) into
+    y[r]."""
+    p = np.asarray(indptr, dtype=np.int64)
+    n = len(p) - 1
+    _, _, row = virtual_rows(p, nnz, W)
+    long_ = (p[1:] - p[:-1]) > W
+    vslot = np.where(long_[row], -1 - row, row).astype(np.int64)
+    count = np.bincount(row, minlength=n) if n > 0 else np.zeros(0, np.int64)
+    vbase = np.concatenate([[0], np.cumsum(count)]).astype(np.int64)
+    return vslot, vbase
+
+
+def virtual_slots_loop(indptr, nnz: int, W: int = 256):
+    """Same as ``virtual_slots`` with a plain per-row loop."""
+    p = [int(v) for v in indptr]
+    n = len(p) - 1
+    C = min(W, LONG_CHUNK)
+    vslot, vbase = [], [0]
+    for r in range(n):
+        s = min(max(p[r], 0), nnz)
+        e = max(min(max(p[r + 1], 0), nnz), s)
+        if p[r + 1] - p[r] > W:
+            for _ in range(max(1, (e - s + C - 1) // C)):
+                vslot.append(-1 - r)
+        else:
+            vslot.append(r)
+        vbase.append(len(vslot))
+    return np.array(vslot, np.int64), np.array(vbase, np.int64)
 
 
 def panel_layout(indptr, indices, n_cols: int, acc_bytes: int = 4, W: int = 256):

@@ -49,6 +49,27 @@ def widen(arr: np.ndarray, vtype: str) -> np.ndarray:
     return arr.astype(np.float64)
 
 
+def close_or_same_nonfinite(g: np.ndarray, w: np.ndarray, err: np.ndarray,
+                            bound: np.ndarray) -> np.ndarray:
+    """Entries that pass: ``err <= bound`` (False for a NaN error or bound),
+    or both sides the same non-finite value (NaN and NaN, or infinities of one
+    sign; for complex values, per component)."""
+    ok = err <= bound
+    if np.iscomplexobj(g) or np.iscomplexobj(w):
+        g = np.asarray(g, dtype=np.complex128)
+        w = np.asarray(w, dtype=np.complex128)
+        same = (_same_nonfinite(g.real, w.real) & (_same_nonfinite(g.imag, w.imag)
+                                                   | (g.imag == w.imag))) \
+            | (_same_nonfinite(g.imag, w.imag) & (g.real == w.real))
+    else:
+        same = _same_nonfinite(g, w)
+    return ok | same
+
+
+def _same_nonfinite(g: np.ndarray, w: np.ndarray) -> np.ndarray:
+    return (np.isnan(g) & np.isnan(w)) | (np.isinf(g) & (g == w))
+
+
 def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtype: str,
                       what: str = "", exact: np.ndarray | None = None,
                       lengths: np.ndarray | None = None, min_len_exempt: int = 0) -> dict:
@@ -63,9 +84,10 @@ def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtyp
     """
     g = widen(got, vtype)
     w = widen(want, vtype)
-    err = np.abs(g - w)
+    with np.errstate(invalid="ignore"):
+        err = np.abs(g - w)
     bound = TOL[vtype] * scale + 1e-30
-    bad = err > bound
+    bad = ~close_or_same_nonfinite(g, w, err, bound)
     report = {"rows_outside_tol_vs_oracle": int(bad.sum()), "exempt_rows": 0}
     if bad.any() and exact is not None:
         closer = np.abs(g - exact) <= np.abs(w - exact)
@@ -86,6 +108,6 @@ def assert_rows_close(got: np.ndarray, want: np.ndarray, scale: np.ndarray, vtyp
             f"(first {idx.tolist()}: got {g[tuple(idx[0])]}, want {w[tuple(idx[0])]}, "
             f"scale {scale[tuple(idx[0])]})")
     with np.errstate(divide="ignore", invalid="ignore"):
-        rel = np.where(scale > 0, err / np.maximum(scale, 1e-300), 0.0)
+        rel = np.where((scale > 0) & np.isfinite(err), err / np.maximum(scale, 1e-300), 0.0)
     report["max_rel_err"] = float(rel.max()) if rel.size else 0.0
     return report

@@ -60,6 +60,27 @@ def test_transpose_cpu_equals_oracle(oracle, vtype, index_dtype):
 
 
 @pytest.mark.parametrize("vtype", VTYPES)
+def test_transpose_cpu_dropped_columns_tail(oracle, vtype):
+    """Columns out of range are dropped from the transpose (the oracle's
+    transpose holds t_indptr[n_cols] entries); the output buffers' tail past
+    t_indptr[n_cols] holds zero bits and row 0 on the native CPU path, not
+    whatever the buffers held."""
+    rng = np.random.default_rng(3)
+    data, ind, ptr = _case(rng, 400, 200, np.int32, vtype)
+    ind = ind.copy()
+    ind[[2, 50, 51]] = [200, 10_000, -4]
+    nnz = int(ptr[-1])
+    td, ti, tp = _capi.transpose(_t(data, vtype), _t(ind), _t(ptr), 400, 200)
+    wd, wi, wp = oracle.csr_transpose(data, ind, ptr, 400, 200, vtype=vtype)
+    kept = nnz - 3
+    assert int(wp[-1]) == kept and len(wd) == kept
+    np.testing.assert_array_equal(to_numpy(tp), wp)
+    np.testing.assert_array_equal(to_numpy(ti)[:kept], wi)
+    np.testing.assert_array_equal(_bits(to_numpy(td)[:kept]), _bits(wd))
+    assert not _bits(to_numpy(td)[kept:]).any() and not to_numpy(ti)[kept:].any()
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
 @pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
 @pytest.mark.parametrize("threads", [1, 3, 8])
 def test_spmv_transpose_cpu_equals_oracle(oracle, vtype, index_dtype, threads):

@@ -140,14 +140,49 @@ def test_transpose_positions_and_values(vtype):
     assert kept == nnz - 1
     assert torch.equal(tp, tp2) and torch.equal(ti[:kept], ti2[:kept])
     assert torch.all(pos[kept:] == -1)
-    out = torch.zeros_like(d)
+    # the dropped values' tail is defined (zero bits, row 0) on every route,
+    # so a regathered transpose equals a fresh one element for element
+    assert torch.all(ti2[kept:] == 0) and torch.all(ti[kept:] == 0)
+    out = torch.full_like(d, 7.0)
     _capi.transpose_values(d, pos, out)
-    np.testing.assert_array_equal(to_numpy(out[:kept]), to_numpy(td[:kept]))
+    np.testing.assert_array_equal(to_numpy(out), to_numpy(td))
     ot, oi, op = orc.csr_transpose(data, indices, indptr, n_rows, n_cols, vtype=vtype)
     np.testing.assert_array_equal(to_numpy(out[:kept]), ot)
+    np.testing.assert_array_equal(to_numpy(ti2[:kept]), oi)
+    assert not to_numpy(out)[kept:].any()
     if vtype == "complex64":
         _capi.transpose_values(d, pos, out, conjugate=True)
         np.testing.assert_array_equal(to_numpy(out[:kept]), np.conj(ot))
+        assert not to_numpy(out)[kept:].any()
+
+
+def test_refreshed_transpose_equals_a_fresh_one(gpu):
+    """A matrix with an out-of-range column: after an in-place update of
+    A.data, the cached A.T (values regathered through stored positions)
+    equals a freshly built transpose of the new values in every element,
+    the dropped values' tail included."""
+    ms = gpu
+    rng = np.random.default_rng(17)
+    n_rows, n_cols = 2000, 1500
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, 20)
+    indices[11] = n_cols + 5
+    indices[300] = n_cols
+    nnz = int(indptr[-1])
+    data = _values(rng, nnz, "float32")
+    A = ms.csr_array((torch.from_numpy(data), torch.from_numpy(indices), torch.from_numpy(indptr)),
+                     shape=(n_rows, n_cols), validate=False)
+    T0 = A.T
+    assert int(T0.indptr[-1]) == nnz - 2
+    _sgd(A, 0.25)
+    T1 = A.T
+    assert T1 is not T0
+    fresh = ms.csr_array((A.data.detach().clone(), A.indices, A.indptr), shape=(n_rows, n_cols),
+                         validate=False).T
+    assert torch.equal(T1.data, fresh.data) and torch.equal(T1.indices, fresh.indices)
+    assert torch.equal(T1.indptr, fresh.indptr)
+    ot, oi, op = orc.csr_transpose(A.data.detach().cpu().numpy(), indices, indptr, n_rows, n_cols)
+    np.testing.assert_array_equal(T1.data[:nnz - 2].cpu().numpy(), ot)
+    assert not T1.data[nnz - 2:].cpu().numpy().any()
 
 
 # -- the drop-in API: in-place updates of A.data ------------------------------------------

@@ -131,3 +131,42 @@ def test_panel_layout_invariants(kind, acc_bytes):
     np.testing.assert_array_equal(np.diff(seg), -(-counts // 4) * 4)
     assert np.all(np.diff(seg) - counts < 4)
     assert counts.sum() == int(((idx >= 0) & (idx < n_cols)).sum())
+
+
+@pytest.mark.parametrize("kind", ["uniform", "mixed", "empty", "zipf"])
+@pytest.mark.parametrize("W", [256, 512])
+def test_virtual_slots_stay_in_bounds(kind, W):
+    """Pass 2 of the panel SpMV (``panel_rows<..., true>``) runs over virtual
+    rows, which outnumber the rows when rows are long; it may store only
+    through ``vslot`` (y) or at the virtual row itself (partial).  Pinned
+    against the per-row loop, then every store index is checked: a short
+    virtual row's slot is a row in [0, n) and each such row is written once,
+    a chunk's slot names a long row, its partial index lies in [0, n_v), and
+    the fixup's ranges vbase[r] .. vbase[r+1] cover exactly the chunks of
+    long row r.  Indexing y by the virtual row instead would write past y
+    whenever n_v > n."""
+    rng = np.random.default_rng(7 + W)
+    p = _indptr(rng, 4000, kind)
+    nnz = int(p[-1])
+    vslot, vbase = plan_oracle.virtual_slots(p, nnz, W=W)
+    ls, lb = plan_oracle.virtual_slots_loop(p, nnz, W=W)
+    np.testing.assert_array_equal(vslot, ls)
+    np.testing.assert_array_equal(vbase, lb)
+    n = len(p) - 1
+    nv = len(vslot)
+    assert vbase[-1] == nv
+    tb, te, _ = plan_oracle.panel_layout(p, np.zeros(nnz, np.int64), 1, W=W)
+    assert tb[0] == 0 and te[-1] == nv and np.all(tb < te) and np.all(tb[1:] == te[:-1])
+    long_ = (p[1:] - p[:-1]) > W
+    short_v = vslot >= 0
+    # y stores: rows in [0, n), every short row exactly once, no long row
+    assert np.all(vslot[short_v] < n)
+    np.testing.assert_array_equal(np.bincount(vslot[short_v], minlength=n), (~long_).astype(np.int64))
+    # partial stores: chunks of long rows, indexed by the virtual row < n_v
+    chunk_rows = -1 - vslot[~short_v]
+    assert np.all((chunk_rows >= 0) & (chunk_rows < n)) and np.all(long_[chunk_rows])
+    for r in np.flatnonzero(long_):
+        assert np.all(vslot[vbase[r]:vbase[r + 1]] == -1 - r)
+        assert vbase[r + 1] > vbase[r]
+    if kind in ("mixed", "zipf"):
+        assert nv > n  # y[v] for every virtual row v would run past y
