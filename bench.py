@@ -28,7 +28,7 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``cg``: conjugate gradients (device-resident loop) on the Poisson matrix,
   time per iteration against its bytes, and the single-threaded reference
   loop on the host;
-- ``krylov``: BiCGSTAB and MINRES (device-resident loops) at n = 128^3, the
+- ``krylov``: BiCGSTAB, MINRES and GMRES(20) (device-resident loops) at n = 128^3, the
   same figures;
 - ``mtx`` (with ``--mtx PATH``): SpMV on a Matrix Market matrix read by the
   native reader (``mmread``);
@@ -477,7 +477,59 @@ def krylov_leg(dev) -> dict:
         log(f"{name}: {out[name]}")
         del A
         torch.cuda.empty_cache()
+    out["gmres"] = gmres_row(dev, m, conv, b, b_np, spmv_bytes)
     return out
+
+
+def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
+    """Restarted GMRES(20) on the convection-diffusion variant at n = 128^3,
+    rtol 1e-5.  Bytes per Arnoldi step j (0-based): the SpMV's compulsory
+    bytes, 8 n for the first Gram-Schmidt dot, 16 n for each of the 2 (j+1)
+    later passes (w, two basis vectors read, w written) and 8 n for the
+    normalisation; per cycle also the residual (12 n) and the update
+    ((used + 2) 4 n).  The CPU figure is the oracle's single-threaded
+    restatement of the reference loop, timed over one cycle of 20 steps."""
+    import mlx_sparse as ms
+    from mlx_sparse import linalg
+    from oracle import oracle as orc
+
+    n = m.shape[0]
+    restart = 20
+    A = ms.csr_array((conv, m.indices, m.indptr), shape=m.shape, canonical=True)
+    linalg.gmres(A, b, rtol=1e-5, restart=restart, maxiter=500)  # plan, allocator
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        x, info = linalg.gmres(A, b, rtol=1e-5, restart=restart, maxiter=500, return_info=True)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    solve_s = statistics.median(times)
+    its = max(info.iterations, 1)
+    cycles = -(-its // restart)
+    step_bytes = 0
+    for j in range(restart):
+        step_bytes += spmv_bytes + 8 * n + 2 * (j + 1) * 16 * n + 8 * n
+    cycle_bytes = step_bytes + 12 * n + (restart + 2) * 4 * n + spmv_bytes
+    total_bytes = cycles * cycle_bytes
+    t0 = time.perf_counter()
+    _, cinfo, _, cits = orc.csr_gmres(conv, m.indices, m.indptr, b_np, rtol=1e-5,
+                                      restart=restart, maxiter=restart)
+    cpu_it = (time.perf_counter() - t0) / max(cits, 1)
+    row = {"matrix": "convection-diffusion variant of poisson3d", "restart": restart,
+           "info": info.status, "iterations": info.iterations, "residual": info.residual_norm,
+           "solve_ms": round(solve_s * 1e3, 2),
+           "us_per_iteration": round(solve_s / its * 1e6, 1),
+           "bytes_per_cycle": cycle_bytes,
+           "gbs": round(total_bytes / solve_s / 1e9, 1),
+           "frac": round(total_bytes / solve_s / 1e9 / HBM_PEAK_GBS, 4),
+           "cpu_us_per_iteration": round(cpu_it * 1e6, 1),
+           "cpu_iterations": cits,
+           "speedup_per_iteration": round(cpu_it / (solve_s / its), 1)}
+    log(f"gmres: {row}")
+    del A
+    torch.cuda.empty_cache()
+    return row
 
 
 def configs_leg(ext, dev, scratch) -> list:

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 5
+#define MSX_ABI_VERSION 6
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -569,6 +569,35 @@ msx_status msx_csr_minres(msx_itype it, int64_t n, int64_t nnz,
                           msx_solver_result *result, void *stream);
 
 /*
+ * Restarted GMRES for a square float32 CSR matrix (n x n, not necessarily
+ * symmetric): x from x0 (device pointers; x0 and x may not overlap).
+ * Each cycle of at most `restart` Arnoldi steps (and at most the budget
+ * left, and n) starts from the true residual; every step is device-wide:
+ * one SpMV of the path with `plan` (nullable) and one fused pass per
+ * modified Gram-Schmidt column (two sweeps, as the reference's CPU
+ * Arnoldi).  The host reads the Hessenberg matrix once per cycle, solves
+ * the small least-squares problem in double by Givens rotations, and the
+ * device adds V y to x.  `maxiter` counts Arnoldi steps over all cycles;
+ * info > 0 is maxiter (1 when maxiter is 0) when the budget ran out; -1 a
+ * failed least-squares solve; -3 non-finite values (residual = infinity
+ * when the inputs are not finite).  `stream` is synchronised; scratch
+ * (restart + 6 vectors of n floats) comes from its stream-ordered
+ * allocator.
+ *
+ * Replaces the GPU path of csr_gmres (reference:
+ * src/linalg/gmres/gmres.cpp:58-220, whose Arnoldi step is
+ * CSRArnoldi::eval_gpu, src/linalg/arnoldi/arnoldi.cpp:184-225, a
+ * single-threadgroup kernel in arnoldi.metal) with the arithmetic of the
+ * reference's CPU Arnoldi (arnoldi.cpp:79-159) and restart loop.
+ */
+msx_status msx_csr_gmres(msx_itype it, int64_t n, int64_t nnz,
+                         const float *data, const void *indices,
+                         const void *indptr, const float *b, const float *x0,
+                         float *x, float rtol, float atol, int64_t restart,
+                         int64_t maxiter, const msx_csr_plan *plan,
+                         msx_solver_result *result, void *stream);
+
+/*
  * Host (CPU) solvers, host pointers: the reference's sequential loops
  * (csr_cg_cpu_impl, cg.cpp:75-246; csr_pcg_jacobi_cpu_impl,
  * pcg.cpp:71-236), one thread.
@@ -598,6 +627,14 @@ msx_status msx_csr_minres_cpu(msx_itype it, int64_t n, int64_t nnz,
                               const float *x0, float *x, float rtol,
                               float atol, int64_t maxiter, float shift,
                               msx_solver_result *result);
+/* csr_gmres_impl (gmres.cpp:58-220) over csr_arnoldi_cpu_impl
+ * (arnoldi.cpp:79-159), one thread. */
+msx_status msx_csr_gmres_cpu(msx_itype it, int64_t n, int64_t nnz,
+                             const float *data, const void *indices,
+                             const void *indptr, const float *b,
+                             const float *x0, float *x, float rtol,
+                             float atol, int64_t restart, int64_t maxiter,
+                             msx_solver_result *result);
 
 /*
  * Matrix Market files (the text format of the SuiteSparse collection).

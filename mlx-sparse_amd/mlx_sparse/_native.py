@@ -103,6 +103,14 @@ def csr_minres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, ato
                                   maxiter, shift, plan=plan)
 
 
+def csr_gmres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
+              restart: int, maxiter: int, plan=None):
+    """(x, info, residual, iterations) of restarted GMRES (reference:
+    mlx_sparse/_native.py:1505-1530 csr_gmres)."""
+    return extension().csr_gmres(data, indices, indptr, b, x0, shape[0], shape[1], rtol, atol,
+                                 restart, maxiter, plan=plan)
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

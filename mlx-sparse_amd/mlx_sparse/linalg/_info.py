@@ -59,16 +59,25 @@ def status_reason(status: int) -> tuple[str, str | None, str]:
 
 
 def finish(x, status: int, residual: float, iterations: int, *, solver: str, return_info: bool,
-           callback=None, rtol=None, atol=None, maxiter=None, preconditioner=None):
+           callback=None, callback_type: str | None = None, rtol=None, atol=None, maxiter=None,
+           restart=None, preconditioner=None):
     """``(x, int)`` by default, ``(x, SolverInfo)`` with ``return_info``; a
-    callback is called once with ``x`` after the solve."""
+    callback is called once after the solve, with ``x`` or, for
+    ``callback_type`` "pr_norm" / "legacy", the final residual norm
+    (reference: mlx_sparse/linalg/utils/diagnostics/callbacks.py:11-58)."""
     if return_info or callback is not None:
         reason, breakdown, message = status_reason(int(status))
         info = SolverInfo(solver=solver, status=int(status), residual_norm=float(residual),
                           iterations=int(iterations), convergence_reason=reason,
                           breakdown_reason=breakdown, message=message, rtol=rtol, atol=atol,
-                          maxiter=maxiter, preconditioner=preconditioner)
+                          maxiter=maxiter, restart=restart, preconditioner=preconditioner)
         if callback is not None:
-            callback(x)
+            if not callable(callback):
+                raise TypeError(f"{solver} callback must be callable.")
+            if callback_type in ("pr_norm", "legacy"):
+                callback(info.preconditioned_residual_norm
+                         if info.preconditioned_residual_norm is not None else info.residual_norm)
+            else:
+                callback(x)
         return x, info if return_info else info.status
     return x, int(status)

@@ -1,12 +1,15 @@
 """Krylov solvers on the path's SpMV (reference: mlx_sparse/linalg/_iterative.py:
-69-323 ``cg``, :328-640 ``bicgstab``, :993-1145 ``minres``; native loops
-src/linalg/cg/cg.cpp, src/preconditioners/pcg/pcg.cpp,
-src/linalg/bicgstab/bicgstab.cpp, src/linalg/minres/minres.cpp).
+69-323 ``cg``, :328-640 ``bicgstab``, :640-990 ``gmres``, :993-1145
+``minres``; native loops src/linalg/cg/cg.cpp, src/preconditioners/pcg/pcg.cpp,
+src/linalg/bicgstab/bicgstab.cpp, src/linalg/gmres/gmres.cpp,
+src/linalg/minres/minres.cpp).
 
 On the GPU each loop runs on the device (``msx_csr_cg``, ``msx_csr_bicgstab``,
 ``msx_csr_minres``): the path's SpMV with the matrix's cached plan, fused
-vector passes, scalars on the device.  With ``use_cpu()`` the reference's
-sequential loops run natively.
+vector passes, scalars on the device.  GMRES (``msx_csr_gmres``) runs each
+Arnoldi step on the device and solves the small least-squares problem of a
+restart cycle on the host, as the reference does.  With ``use_cpu()`` the
+reference's sequential loops run natively.
 """
 
 from __future__ import annotations
@@ -206,4 +209,40 @@ def minres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, shift: float
         maxiter=maxiter_value, shift=shift_value, plan=csr.plan(device))
     return finish(x, info, residual, iterations, solver="minres", return_info=bool(return_info),
                   callback=callback, rtol=float(rtol), atol=float(atol), maxiter=maxiter_value,
+                  preconditioner=kind)
+
+
+def gmres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, restart: int | None = None,
+          maxiter: int | None = None, M=None, callback=None, callback_type: str = "x",
+          return_info: bool = False):
+    """Solve a square (not necessarily symmetric) sparse system ``A @ x = b``
+    with restarted GMRES (reference: mlx_sparse/linalg/_iterative.py:640-990).
+
+    Each cycle builds an Arnoldi basis of ``restart`` vectors (default
+    ``min(20, n)``; one SpMV per step) from the true residual and minimises
+    the residual over it.  ``maxiter`` counts SpMVs over all cycles (default
+    ``10 * n``).  Stops when ``||b - A x|| <= max(atol, rtol * ||b||)``,
+    tested between cycles.  ``M``: ``None`` or ``preconditioners.identity``.
+    ``callback`` is called once after the solve, with ``x``
+    (``callback_type="x"``) or the final residual norm ("pr_norm",
+    "legacy").
+
+    Returns ``(x, info)``: ``info`` 0 converged, > 0 the budget ran out, -1
+    a failed least-squares solve, -3 non-finite values.  With
+    ``return_info=True`` a :class:`SolverInfo` replaces the integer.
+    """
+    if callback_type not in {"x", "pr_norm", "legacy"}:
+        raise ValueError("callback_type must be 'x', 'pr_norm', or 'legacy'.")
+    csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "gmres")
+    restart_value = min(20, csr.shape[0]) if restart is None else int(restart)
+    if restart_value <= 0:
+        raise ValueError("restart must be positive.")
+    kind = _plain_preconditioner(M, csr, "gmres")
+    data, indices, indptr = csr.buffers(device)
+    x, info, residual, iterations = _native.csr_gmres(
+        data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
+        restart=restart_value, maxiter=maxiter_value, plan=csr.plan(device))
+    return finish(x, info, residual, iterations, solver="gmres", return_info=bool(return_info),
+                  callback=callback, callback_type=callback_type, rtol=float(rtol),
+                  atol=float(atol), maxiter=maxiter_value, restart=restart_value,
                   preconditioner=kind)

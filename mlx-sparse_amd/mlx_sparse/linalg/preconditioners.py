@@ -139,5 +139,9 @@ def aspreconditioner(M, A=None):
         return M
     if isinstance(M, torch.Tensor) and M.ndim == 1:
         return diagonal(M, inverse=True)
+    if isinstance(M, CSRArray):
+        # reference: mlx_sparse/linalg/preconditioners.py:1585-1590
+        raise TypeError("sparse matrices are not inverse-apply preconditioners; use "
+                        "preconditioners.jacobi(A) or preconditioners.diagonal(...).")
     raise TypeError(
         "cg currently supports only identity, diagonal and Jacobi native-backed preconditioners.")

@@ -6,7 +6,8 @@
 // `csr_matmul`, :998-1008 `csr_batched_matmul`, :661-665 `csr_transpose`,
 // :942-947 `csr_matvec_transpose`, :1035-1040 `csr_matmul_transpose`; the
 // value gradients, internal to the reference's VJPs, are bound as
-// `csr_matvec_data_vjp` / `csr_matmul_data_vjp`): same names and argument
+// `csr_matvec_data_vjp` / `csr_matmul_data_vjp`; the solvers, :1470-1482
+// `csr_gmres` among them): same names and argument
 // order (data, indices, indptr, x | rhs, n_rows, n_cols).  Arrays are torch
 // tensors; the module reads their pointer, dtype, shape, strides and device
 // through the tensor's Python attributes, so no torch headers are compiled
@@ -469,24 +470,26 @@ py::tuple solve_cg(py::handle data_o, py::handle indices_o, py::handle indptr_o,
 py::tuple solve_krylov(msx::Krylov kind, py::handle data_o, py::handle indices_o,
                        py::handle indptr_o, py::handle b_o, py::handle x0_o, int64_t n_rows,
                        int64_t n_cols, float rtol, float atol, int64_t maxiter, float shift,
-                       py::object plan) {
+                       py::object plan, int64_t restart = 0) {
   py::object data = contiguous(data_o), indices = contiguous(indices_o),
              indptr = contiguous(indptr_o), b = contiguous(b_o), x0 = contiguous(x0_o);
   const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vb = view_of(b),
                   vx0 = view_of(x0);
   if (vb.ndim != 1)
-    msx::require_rank(vb, 1, kind == msx::Krylov::BiCGSTAB ? "csr_bicgstab b" : "csr_minres b");
+    msx::require_rank(vb, 1, kind == msx::Krylov::BiCGSTAB ? "csr_bicgstab b"
+                             : kind == msx::Krylov::MINRES ? "csr_minres b"
+                                                           : "csr_gmres b");
   py::object x = empty_like_out(vb, b, py::make_tuple(vb.shape[0]));
   const ArrayView vx = view_of(x);
   const msx::ExecContext ctx = context_for(vd, 0);
   msx_solver_result res{};
   if (vd.device >= 0) {
     res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
-                          shift, plan_ptr(plan), ctx);
+                          shift, plan_ptr(plan), ctx, restart);
   } else {
     py::gil_scoped_release nogil;
     res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
-                          shift, nullptr, ctx);
+                          shift, nullptr, ctx, restart);
   }
   return py::make_tuple(x, res.info, res.residual, res.iterations);
 }
@@ -725,6 +728,18 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("maxiter"),
       py::arg("shift") = 0.0f, py::arg("plan") = py::none(),
       "MINRES on (A - shift I) x = b: (x, info, residual, iterations).");
+  m.def(
+      "csr_gmres",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         int64_t n_rows, int64_t n_cols, float rtol, float atol, int64_t restart, int64_t maxiter,
+         py::object plan) {
+        return solve_krylov(msx::Krylov::GMRES, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, 0.0f, plan, restart);
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("restart"),
+      py::arg("maxiter"), py::arg("plan") = py::none(),
+      "Restarted GMRES: (x, info, residual, iterations).");
   m.def("mm_info", &mm_info, py::arg("path"), "Header of a Matrix Market file.");
   m.def("mm_read_csr", &mm_read_csr, py::arg("path"), py::arg("dtype"), py::arg("index_dtype"),
         py::arg("n_threads") = 0,

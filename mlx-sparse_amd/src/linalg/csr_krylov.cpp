@@ -12,12 +12,17 @@ msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView
                              const ArrayView &indptr, const ArrayView &b, const ArrayView &x0,
                              const ArrayView &x, int64_t n_rows, int64_t n_cols, float rtol,
                              float atol, int64_t maxiter, float shift, const msx_csr_plan *plan,
-                             const ExecContext &ctx) {
+                             const ExecContext &ctx, int64_t restart) {
   // reference: src/linalg/bicgstab/bicgstab.cpp:440-480 (require_* calls
-  // of csr_bicgstab), src/linalg/minres/minres.cpp (csr_minres)
-  const std::string op = kind == Krylov::BiCGSTAB ? "csr_bicgstab" : "csr_minres";
+  // of csr_bicgstab), src/linalg/minres/minres.cpp (csr_minres),
+  // src/linalg/gmres/gmres.cpp:223-263 (csr_gmres)
+  const std::string op = kind == Krylov::BiCGSTAB ? "csr_bicgstab"
+                         : kind == Krylov::MINRES ? "csr_minres"
+                                                  : "csr_gmres";
   if (n_rows <= 0 || n_cols <= 0 || n_rows != n_cols || n_rows >= 2147483647)
     throw std::invalid_argument(op + " requires a non-empty square matrix.");
+  if (kind == Krylov::GMRES && (restart <= 0 || maxiter < 0))
+    throw std::invalid_argument("csr_gmres requires restart > 0 and maxiter >= 0.");
   if (maxiter < 0) throw std::invalid_argument(op + " maxiter must be non-negative.");
   if (maxiter > 2147483647) throw std::invalid_argument(op + " maxiter must fit in int32.");
   require_rank(data, 1, (op + " data").c_str());
@@ -56,6 +61,15 @@ msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView
     else
       check_status(msx_csr_bicgstab_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, xx,
                                         rtol, atol, maxiter, &res),
+                   op.c_str());
+  } else if (kind == Krylov::GMRES) {
+    if (data.device >= 0)
+      check_status(msx_csr_gmres(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, xx, rtol,
+                                 atol, restart, maxiter, plan, &res, ctx.stream),
+                   op.c_str());
+    else
+      check_status(msx_csr_gmres_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, xx,
+                                     rtol, atol, restart, maxiter, &res),
                    op.c_str());
   } else {
     if (data.device >= 0)

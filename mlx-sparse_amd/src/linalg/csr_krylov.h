@@ -6,17 +6,18 @@
 
 namespace msx {
 
-enum class Krylov { BiCGSTAB, MINRES };
+enum class Krylov { BiCGSTAB, MINRES, GMRES };
 
 // x (caller-allocated, n) from x0 for A x = b (MINRES: (A - shift I) x = b),
 // A square float32 CSR (n x n).  Validates like the reference ops
 // (reference: src/linalg/bicgstab/bicgstab.cpp:440-480 csr_bicgstab,
-// src/linalg/minres/minres.cpp csr_minres), then runs the device solver on
-// ctx.stream (with `plan`, nullable) or the host loop.
+// src/linalg/minres/minres.cpp csr_minres, src/linalg/gmres/gmres.cpp:223-263
+// csr_gmres), then runs the device solver on ctx.stream (with `plan`,
+// nullable) or the host loop.  `restart`: GMRES's cycle length (> 0).
 msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView &indices,
                              const ArrayView &indptr, const ArrayView &b, const ArrayView &x0,
                              const ArrayView &x, int64_t n_rows, int64_t n_cols, float rtol,
                              float atol, int64_t maxiter, float shift, const msx_csr_plan *plan,
-                             const ExecContext &ctx);
+                             const ExecContext &ctx, int64_t restart = 0);
 
 }  // namespace msx

@@ -32,7 +32,11 @@
  *     csr_pcg_jacobi_cpu_impl), float32 values only;
  *   - BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
  *     and MINRES with its shift (src/linalg/minres/minres.cpp:68-312,
- *     csr_minres_cpu_impl), float32.
+ *     csr_minres_cpu_impl), float32;
+ *   - restarted GMRES (src/linalg/gmres/gmres.cpp:58-220, csr_gmres_impl)
+ *     with its Arnoldi factorisation (src/linalg/arnoldi/arnoldi.cpp:79-159,
+ *     csr_arnoldi_cpu_impl) and the Givens least-squares solve
+ *     (src/linalg/common/common.h:143-234), float32.
  *
  * Built with -ffp-contract=off so every product and every sum is rounded on
  * its own, as the reference's separate multiply_accumulate / `+=` are.
@@ -1323,5 +1327,277 @@ done:
   *residual = true_residual;
   *iterations = completed;
   free(r1); free(r2); free(y); free(v); free(w); free(w2); free(av);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Restarted GMRES (src/linalg/gmres/gmres.cpp:58-220, csr_gmres_impl) over
+ * the CPU Arnoldi factorisation (src/linalg/arnoldi/arnoldi.cpp:79-159,
+ * csr_arnoldi_cpu_impl) and the small upper-Hessenberg least-squares solve
+ * by Givens QR (src/linalg/common/common.h:143-234,
+ * least_squares_upper_hessenberg_givens_qr), float32 values; the solver SpMV
+ * is csr_spmv_float (common.h:35-45), summed from zero. */
+
+/* norm_float (common.h:56-73): float(sqrt(max(float(sum of double
+ * squares), 0))). */
+static float norm_f(const float *v, int64_t n) {
+  const float dd = dot_f(v, v, n);
+  return sqrtf(max0f(dd));
+}
+
+/* k Arnoldi steps from v0: h is (k+1) x k row-major, basis n x (k+1)
+ * row-major (basis[row * (k+1) + col]); *used = steps taken.  Two passes of
+ * modified Gram-Schmidt per step, each coefficient a double sum of float
+ * products, subtracted in float; the step ends early when the new norm is
+ * at most FLT_EPSILON. */
+int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices,
+                       const void *indptr, const float *v0, int64_t k, float *h, float *basis,
+                       int32_t *used_out) {
+  const int64_t cols = k + 1;
+  float *w = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+  float *q = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+  if (!w || !q) {
+    free(w);
+    free(q);
+    return -1;
+  }
+  memset(h, 0, (size_t)cols * (size_t)k * sizeof(float));
+  memset(basis, 0, (size_t)n * (size_t)cols * sizeof(float));
+  double v_norm2 = 0.0;
+  for (int64_t i = 0; i < n; ++i) v_norm2 += (double)v0[i] * (double)v0[i];
+  const float v_norm = (float)sqrt(v_norm2 < 0.0 ? 0.0 : v_norm2);
+  const float eps = FLT_EPSILON;
+  for (int64_t i = 0; i < n; ++i)
+    basis[i * cols] = v_norm <= eps ? (i == 0 ? 1.0f : 0.0f) : v0[i] / v_norm;
+  int32_t used = 0;
+  for (int64_t j = 0; j < k; ++j) {
+    for (int64_t i = 0; i < n; ++i) q[i] = basis[i * cols + j];
+    cg_spmv(it, n, data, indices, indptr, q, w);
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int64_t col = 0; col <= j; ++col) {
+        double coeff = 0.0;
+        for (int64_t row = 0; row < n; ++row) {
+          const float prod = basis[row * cols + col] * w[row];
+          coeff += (double)prod;
+        }
+        const float c = (float)coeff;
+        h[col * k + j] = h[col * k + j] + c;
+        for (int64_t row = 0; row < n; ++row) {
+          const float t = c * basis[row * cols + col];
+          w[row] = w[row] - t;
+        }
+      }
+    }
+    const float h_next = norm_f(w, n);
+    h[(j + 1) * k + j] = h_next;
+    used = (int32_t)(j + 1);
+    if (h_next <= eps) break;
+    for (int64_t row = 0; row < n; ++row) basis[row * cols + j + 1] = w[row] / h_next;
+  }
+  *used_out = used;
+  free(w);
+  free(q);
+  return 0;
+}
+
+/* min ||a y - b|| for an upper-Hessenberg a of rows = cols + 1 (row-major,
+ * double) by Givens rotations; returns 0, or 1 where the reference throws
+ * (non-finite input, rank-deficient matrix, degenerate rotation or R
+ * factor, non-finite solution). */
+static int lsq_hessenberg(const double *a, const double *b, int64_t rows, int64_t cols, double *y) {
+  if (rows != cols + 1 || rows <= 1 || cols <= 0) return 1;
+  double *r = (double *)malloc((size_t)(rows * cols) * sizeof(double));
+  double *rhs = (double *)malloc((size_t)rows * sizeof(double));
+  int err = 0;
+  if (!r || !rhs) {
+    free(r);
+    free(rhs);
+    return 1;
+  }
+  memcpy(r, a, (size_t)(rows * cols) * sizeof(double));
+  memcpy(rhs, b, (size_t)rows * sizeof(double));
+  double scale = 0.0;
+  for (int64_t i = 0; i < rows * cols; ++i) {
+    if (!isfinite(r[i])) err = 1;
+    const double m = fabs(r[i]);
+    if (m > scale) scale = m;
+  }
+  for (int64_t i = 0; i < rows; ++i)
+    if (!isfinite(rhs[i])) err = 1;
+  const double big = (double)(rows > cols ? rows : cols);
+  const double rank_tol = DBL_EPSILON * big * (scale > 1.0 ? scale : 1.0);
+  if (!err && scale <= rank_tol) err = 1;
+  for (int64_t col = 0; !err && col < cols; ++col) {
+    const int64_t row = col + 1;
+    const double pivot = r[col * cols + col];
+    const double entry = r[row * cols + col];
+    if (entry == 0.0) continue;
+    const double radius = hypot(pivot, entry);
+    if (!isfinite(radius) || radius <= rank_tol) {
+      err = 1;
+      break;
+    }
+    const double c = pivot / radius;
+    const double s = entry / radius;
+    for (int64_t j = col; j < cols; ++j) {
+      const double top = r[col * cols + j];
+      const double bottom = r[row * cols + j];
+      r[col * cols + j] = c * top + s * bottom;
+      r[row * cols + j] = -s * top + c * bottom;
+    }
+    const double rt = rhs[col], rb = rhs[row];
+    rhs[col] = c * rt + s * rb;
+    rhs[row] = -s * rt + c * rb;
+  }
+  for (int64_t row = cols - 1; !err && row >= 0; --row) {
+    double sum = rhs[row];
+    for (int64_t col = row + 1; col < cols; ++col) sum -= r[row * cols + col] * y[col];
+    const double diag = r[row * cols + row];
+    if (!isfinite(diag) || fabs(diag) <= rank_tol) {
+      err = 1;
+      break;
+    }
+    y[row] = sum / diag;
+    if (!isfinite(y[row])) err = 1;
+  }
+  free(r);
+  free(rhs);
+  return err;
+}
+
+/* b - A x into r; returns norm_float(r), *finite = every r entry and the
+ * norm finite. */
+static float gm_residual(int it, int64_t n, const float *data, const void *indices,
+                         const void *indptr, const float *b, const float *x, float *ax, float *r,
+                         int *finite) {
+  cg_spmv(it, n, data, indices, indptr, x, ax);
+  int ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    r[i] = b[i] - ax[i];
+    ok = ok && fin(r[i]);
+  }
+  const float nr = norm_f(r, n);
+  *finite = ok && fin(nr);
+  return nr;
+}
+
+/* Restarted GMRES: info 0 converged, maxiter (1 when maxiter is 0) when the
+ * budget ran out, -1 a failed least-squares solve, -3 non-finite; residual
+ * the last true residual norm (infinity when the inputs are not finite);
+ * iterations the Arnoldi steps taken. */
+int oracle_csr_gmres(int it, int64_t n, const float *data, const void *indices, const void *indptr,
+                     const float *b, const float *x0, float *x, float rtol, float atol,
+                     int64_t restart, int64_t maxiter, int32_t *info, float *residual,
+                     int32_t *iterations) {
+  const size_t nb = (size_t)(n > 0 ? n : 1) * sizeof(float);
+  const int64_t kmax = restart < maxiter ? restart : maxiter;
+  const int64_t kcap = (kmax < n ? kmax : n) > 0 ? (kmax < n ? kmax : n) : 1;
+  float *r = (float *)malloc(nb), *ax = (float *)malloc(nb), *v0 = (float *)malloc(nb);
+  float *h = (float *)malloc((size_t)((kcap + 1) * kcap) * sizeof(float));
+  float *basis = (float *)malloc((size_t)n * (size_t)(kcap + 1) * sizeof(float));
+  double *hd = (double *)malloc((size_t)((kcap + 1) * kcap) * sizeof(double));
+  double *e1 = (double *)malloc((size_t)(kcap + 1) * sizeof(double));
+  double *y = (double *)malloc((size_t)kcap * sizeof(double));
+  if (!r || !ax || !v0 || !h || !basis || !hd || !e1 || !y) {
+    free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
+    return -1;
+  }
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  const float b_norm = norm_f(b, n);
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  int64_t iters = 0;
+  int32_t status = maxiter > 0 ? (int32_t)maxiter : 1;
+  float res = INFINITY;
+  int inputs_ok = fin(b_norm) && fin(tol);
+  for (int64_t i = 0; i < n; ++i) inputs_ok = inputs_ok && fin(x[i]) && fin(b[i]);
+  if (!inputs_ok) {
+    status = -3;
+    goto done;
+  }
+  while (iters < maxiter) {
+    int finite = 1;
+    const float beta = gm_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
+    res = beta;
+    if (!finite) {
+      status = -3;
+      break;
+    }
+    if (beta <= tol) {
+      status = 0;
+      break;
+    }
+    int64_t steps = restart;
+    if (maxiter - iters < steps) steps = maxiter - iters;
+    if (n < steps) steps = n;
+    for (int64_t i = 0; i < n; ++i) v0[i] = r[i] / beta;
+    int32_t used = 0;
+    if (oracle_csr_arnoldi(it, n, data, indices, indptr, v0, steps, h, basis, &used) != 0) {
+      free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
+      return -1;
+    }
+    if (used == 0) {
+      status = -1;
+      break;
+    }
+    int bad = 0;
+    for (int64_t row = 0; row < used + 1; ++row)
+      for (int64_t col = 0; col < used; ++col) {
+        hd[row * used + col] = (double)h[row * steps + col];
+        if (!isfinite(hd[row * used + col])) bad = 1;
+      }
+    if (bad) {
+      status = -3;
+      break;
+    }
+    e1[0] = (double)beta;
+    for (int64_t i = 1; i < used + 1; ++i) e1[i] = 0.0;
+    if (lsq_hessenberg(hd, e1, used + 1, used, y) != 0) {
+      status = -1;
+      break;
+    }
+    for (int64_t c = 0; c < used; ++c)
+      if (!isfinite(y[c])) bad = 1;
+    if (bad) {
+      status = -3;
+      break;
+    }
+    for (int64_t row = 0; row < n; ++row) {
+      double update = 0.0;
+      for (int64_t col = 0; col < used; ++col)
+        update += (double)basis[row * (steps + 1) + col] * y[col];
+      if (!isfinite(update)) {
+        bad = 1;
+        break;
+      }
+      x[row] = x[row] + (float)update;
+      if (!fin(x[row])) {
+        bad = 1;
+        break;
+      }
+    }
+    if (bad) {
+      status = -3;
+      break;
+    }
+    iters += used;
+    if (iters >= maxiter) {
+      res = gm_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
+      if (!finite) status = -3;
+      else if (res <= tol) status = 0;
+      break;
+    }
+  }
+  if (maxiter == 0 && status > 0) {
+    int finite = 1;
+    res = gm_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
+    if (!finite) status = -3;
+    else if (res <= tol) status = 0;
+  }
+done:
+  *info = status;
+  *residual = res;
+  *iterations = (int32_t)iters;
+  free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
   return 0;
 }

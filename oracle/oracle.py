@@ -108,6 +108,11 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_minres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                            vp, vp, vp]
         _lib.oracle_csr_minres.restype = ci
+        _lib.oracle_csr_arnoldi.argtypes = [ci, i64, vp, vp, vp, vp, i64, vp, vp, vp]
+        _lib.oracle_csr_arnoldi.restype = ci
+        _lib.oracle_csr_gmres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
+                                          vp, vp, vp]
+        _lib.oracle_csr_gmres.restype = ci
     return _lib
 
 
@@ -304,6 +309,42 @@ def csr_minres(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: f
                                  ctypes.addressof(its))
     if rc != 0:
         raise MemoryError("oracle_csr_minres failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_arnoldi(data, indices, indptr, v0, k: int):
+    """k Arnoldi steps of a square float32 CSR matrix from v0 (reference
+    src/linalg/arnoldi/arnoldi.cpp:79-159).  Returns (h of shape (k+1, k),
+    basis of shape (n, k+1), used)."""
+    data, indices, indptr, v0, _, n = _solver_inputs(data, indices, indptr, v0, None)
+    h = np.empty((k + 1, k), np.float32)
+    basis = np.empty((n, k + 1), np.float32)
+    used = ctypes.c_int32()
+    rc = lib().oracle_csr_arnoldi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                  _ptr(indptr), _ptr(v0), k, _ptr(h), _ptr(basis),
+                                  ctypes.addressof(used))
+    if rc != 0:
+        raise MemoryError("oracle_csr_arnoldi failed")
+    return h, basis, used.value
+
+
+def csr_gmres(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: float = 0.0,
+              restart: int | None = None, maxiter: int | None = None):
+    """Restarted GMRES on a square float32 CSR matrix (reference
+    src/linalg/gmres/gmres.cpp:58-220).  ``restart`` defaults to min(20, n),
+    ``maxiter`` (Arnoldi steps over all cycles) to 10 n.  Returns (x, info,
+    residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    restart = min(20, n) if restart is None else int(restart)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_gmres(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                _ptr(indptr), _ptr(b), _ptr(x0), _ptr(x), rtol, atol, restart,
+                                maxiter, ctypes.addressof(info), ctypes.addressof(res),
+                                ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_gmres failed")
     return x, info.value, res.value, its.value
 
 

@@ -105,6 +105,10 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_bicgstab_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp]
         L.msx_csr_minres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                          vp]
+        L.msx_csr_gmres.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64, vp,
+                                    vp, vp]
+        L.msx_csr_gmres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
+                                        vp]
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
@@ -122,7 +126,8 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_spmm_data_vjp", "msx_csr_spmv_data_vjp_cpu",
                      "msx_csr_spmm_data_vjp_cpu", "msx_csr_cg", "msx_csr_pcg_jacobi",
                      "msx_csr_cg_cpu", "msx_csr_pcg_jacobi_cpu", "msx_csr_bicgstab",
-                     "msx_csr_minres", "msx_csr_bicgstab_cpu", "msx_csr_minres_cpu"):
+                     "msx_csr_minres", "msx_csr_bicgstab_cpu", "msx_csr_minres_cpu",
+                     "msx_csr_gmres", "msx_csr_gmres_cpu"):
             getattr(L, name).restype = ci
         _lib = L
     return _lib
@@ -406,4 +411,24 @@ def krylov(kind, data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxi
         st = getattr(L, f"msx_csr_{kind}")(*head, *extra, plan.ptr if plan else None,
                                             ctypes.byref(res), _stream())
     _check(st, f"msx_csr_{kind}")
+    return x, res.info, res.residual, res.iterations
+
+
+def gmres(data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, restart=None, maxiter=None,
+          plan=None):
+    """(x, info, residual, iterations) through msx_csr_gmres[_cpu]."""
+    n = b.numel()
+    x0 = torch.zeros_like(b) if x0 is None else x0
+    x = torch.empty_like(b)
+    restart = min(20, n) if restart is None else restart
+    maxiter = 10 * n if maxiter is None else maxiter
+    res = SolverResult()
+    head = (IT[indices.dtype], n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b), _p(x0),
+            _p(x), rtol, atol, restart, maxiter)
+    L = lib()
+    if b.device.type == "cpu":
+        st = L.msx_csr_gmres_cpu(*head, ctypes.byref(res))
+    else:
+        st = L.msx_csr_gmres(*head, plan.ptr if plan else None, ctypes.byref(res), _stream())
+    _check(st, "msx_csr_gmres")
     return x, res.info, res.residual, res.iterations

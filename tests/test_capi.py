@@ -22,7 +22,7 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _capi.lib().msx_abi_version() == 5
+    assert _capi.lib().msx_abi_version() == 6
 
 
 def _f32(a):
