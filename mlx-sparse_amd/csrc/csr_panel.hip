@@ -126,6 +126,19 @@ __device__ inline void stage_panel(typename V::Acc *xs, const typename V::Storag
   for (int i = done + static_cast<int>(threadIdx.x); i < w; i += kThreads) xs[i] = V::widen(src[i]);
 }
 
+// Issue the loads of `bytes` bytes at `src` straight into LDS at `lds`
+// (buffer-to-LDS loads: lane l's 16 bytes land at 16 l of its wave's 1 KB;
+// bytes past `bytes` read zero).  The caller waits for them.
+__device__ inline void issue_panel_direct(unsigned char *lds, const void *src, uint32_t bytes) {
+  const auto r = make_rsrc(src, bytes);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t lane = threadIdx.x % kWave;
+  for (uint32_t u = wave; u * 1024u < bytes; u += kWavesPerGroup)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void *)(lds + u * 1024u), 16, u * 1024u + 16u * lane,
+        0, 0, 0);
+}
+
 // A store that is not read back soon (the value gradient).
 template <class T>
 __device__ inline void nt_store(T *p, T v) {
@@ -189,15 +202,45 @@ __global__ void __launch_bounds__(kThreads)
     return o;
   };
   const int64_t t0 = threadIdx.x;
+  // x needs no widening (float32, complex64): the panel goes straight into
+  // LDS by buffer-to-LDS loads, issued before the prefetch of the chunk
+  // (lane l's 16 bytes land at 16 l of its wave's 1 KB; bytes past the
+  // panel read zero), so no registers hold it and no LDS stores copy it.
+  constexpr bool kDirect = sizeof(S) == sizeof(A);
+  if constexpr (kDirect) issue_panel_direct(lds_raw, x + c0, static_cast<uint32_t>(w) * sizeof(S));
   Four<S> pd[kPrefetch] = {};
   uint2 pk[kPrefetch] = {};
+  if constexpr (kDirect) {
+    // Unconditional loads through descriptors over the chunk's quads (quads
+    // past it read zero and are never stored): a load under a branch would
+    // be waited on inside it, and with it the panel loads issued before.
+    const auto r_d = make_rsrc(d4, static_cast<uint64_t>(nq) * sizeof(Four<S>));
+    const auto r_k = make_rsrc(k4, static_cast<uint64_t>(nq) * sizeof(uint2));
 #pragma unroll
-  for (int u = 0; u < kPrefetch; ++u)
-    if (t0 + u * kThreads < nq) {
-      if constexpr (!XONLY) pd[u] = nt_load(d4 + t0 + u * kThreads);
-      pk[u] = nt_load(k4 + t0 + u * kThreads);
+    for (int u = 0; u < kPrefetch; ++u) {
+      const auto qi = static_cast<uint32_t>(t0 + u * kThreads);
+      if constexpr (!XONLY)
+        pd[u] = __builtin_bit_cast(
+            Four<S>, (BufLoad<sizeof(Four<S>), kCacheStream>::load(r_d, qi * sizeof(Four<S>))));
+      pk[u] = __builtin_bit_cast(uint2, (BufLoad<8, kCacheStream>::load(r_k, qi * 8u)));
     }
-  stage_panel<V>(xs, x, c0, w);
+    // The panel's loads were issued first and loads complete in order: wait
+    // until no more than the prefetch's loads are outstanding.
+    constexpr int kLoadsPerQuad = XONLY ? 1 : (sizeof(Four<S>) == 32 ? 3 : 2);
+    constexpr int kAfter = kPrefetch * kLoadsPerQuad;
+    static_assert(kAfter < 64, "vmcnt field");
+    // s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at
+    // their maxima (not waited on)
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | ((kAfter >> 4) << 14) | (7 << 4) | (15 << 8));
+  } else {
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u)
+      if (t0 + u * kThreads < nq) {
+        if constexpr (!XONLY) pd[u] = nt_load(d4 + t0 + u * kThreads);
+        pk[u] = nt_load(k4 + t0 + u * kThreads);
+      }
+    stage_panel<V>(xs, x, c0, w);
+  }
   __syncthreads();
   for (int64_t i = b + threadIdx.x; i < a; i += kThreads)
     prod[i] = term(XONLY ? S{} : data[i], col[i]);
