@@ -65,6 +65,9 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# The allocation-free transposed product's file-scope device array
+# (csr_transpose.hip), resident on every GPU the library runs on.
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 def log(msg: str) -> None:
@@ -84,12 +87,22 @@ def _events_time(fn, iters: int) -> float:
     return start.elapsed_time(stop) / iters
 
 
-def _graph_time(fn, calls: int = 20, replays: int = 10) -> tuple[float, torch.Tensor]:
-    """Mean milliseconds per call of ``fn`` with the host out of the loop:
+class GraphTime(float):
+    """Median milliseconds per call over the replays (the float value), with
+    the mean over all of them as ``.mean``."""
+
+    mean: float
+    replays: int
+
+
+def _graph_time(fn, calls: int = 20, replays: int = 50) -> tuple[GraphTime, torch.Tensor]:
+    """Milliseconds per call of ``fn`` with the host out of the loop:
     ``calls`` launches are captured in one HIP graph, replayed ``replays``
-    times between HIP events.  Every replay's last output is compared with
-    the eager result (the kernels are deterministic), so a replay that went
-    wrong cannot go unnoticed.  Returns (ms per call, eager output)."""
+    times, each replay between its own HIP events.  The result is the median
+    over the replays of (replay time / calls), with the mean beside it.
+    Every replay's last output is compared with the eager result (the
+    kernels are deterministic), so a replay that went wrong cannot go
+    unnoticed.  Returns (ms per call, eager output)."""
     eager = fn()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -103,16 +116,19 @@ def _graph_time(fn, calls: int = 20, replays: int = 10) -> tuple[float, torch.Te
     torch.cuda.synchronize()
     if not torch.equal(outs[-1], eager):
         raise RuntimeError("graph replay result differs from the eager call")
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(replays)]
+    for a, b in events:
+        a.record()
         graph.replay()
-    stop.record()
-    stop.synchronize()
+        b.record()
+    events[-1][1].synchronize()
     if not torch.equal(outs[-1], eager):
         raise RuntimeError("graph replay result differs from the eager call")
-    ms = start.elapsed_time(stop) / (replays * calls)
+    per = [a.elapsed_time(b) / calls for a, b in events]
+    ms = GraphTime(statistics.median(per))
+    ms.mean = statistics.fmean(per)
+    ms.replays = replays
     del graph, outs
     return ms, eager
 
@@ -262,7 +278,52 @@ def adjoint_leg(ext, A, m, x, spmv_bytes: int) -> dict:
         train_step()
     t = _events_time(train_step, 20)
     out["autograd_step_us"] = round(t * 1e3, 1)
+    out.update(inplace_training(A, x, g))
     log(f"adjoint: {out}")
+    return out
+
+
+def inplace_training(A, x, g) -> dict:
+    """One SGD step on the headline matrix's values, in place: the forward
+    ``A @ x`` (the bound panel plan refreshed from the new values first),
+    the backward (``x.grad = A^T g`` over the cached transpose, its values
+    regathered after the update; ``A.data.grad`` by the value gradient
+    through the panel plan) and ``A.data -= lr * A.data.grad``.  Timed with
+    HIP events over 20 steps after 3 warm-up steps (the first backward
+    scatters, the second builds the transpose, later ones regather); the
+    plan refresh and the transposed-values regather are also timed alone."""
+    import mlx_sparse as ms
+    from mlx_sparse import _native
+
+    vals = A.data.detach().clone().requires_grad_()
+    A2 = ms.csr_array((vals, A.indices, A.indptr), shape=A.shape)
+    x2 = x.clone().requires_grad_()
+
+    def sgd_step():
+        x2.grad = None
+        (A2 @ x2).backward(g)
+        with torch.no_grad():
+            vals.sub_(1e-3 * vals.grad)
+        vals.grad = None
+
+    for _ in range(3):
+        sgd_step()
+    out = {"inplace_train_step_us": round(_events_time(sgd_step, 20) * 1e3, 1)}
+    plan = A2.plan(x.device)
+    d = vals.detach()
+    refresh = lambda: plan.refresh(d)
+    refresh()
+    out["plan_refresh_us"] = round(_events_time(refresh, 20) * 1e3, 1)
+    _, i, p = A2.buffers(x.device)
+    pos = _native.csr_transpose_positions(i, p, A2.shape)[0]
+    t_vals = torch.empty_like(d)
+    regather = lambda: _native.csr_transpose_values(d, pos, False, t_vals)
+    regather()
+    out["transpose_regather_us"] = round(_events_time(regather, 20) * 1e3, 1)
+    out["inplace_train_step"] = ("SGD step on A.data in place: plan refresh + forward SpMV + "
+                                 "A^T g over the regathered cached transpose + value "
+                                 "gradient through the panel plan + the update")
+    del A2, vals, x2, pos, t_vals
     return out
 
 
@@ -397,7 +458,8 @@ def _operands(case: str, m, dev):
 
 def _case_call(ext, case: str, m, data, X, dev):
     """(call, info, compulsory bytes, flops, keep-alive) of a case through its
-    cached bound plan (AUTO's choice)."""
+    cached bound plan (AUTO's choice); the keep-alive tuple ends with the
+    plan's build time in ms (its first-call cost)."""
     import mlx_sparse as ms
     from mlx_sparse import synthetic
 
@@ -406,7 +468,11 @@ def _case_call(ext, case: str, m, data, X, dev):
     A = ms.csr_array((data, torch.from_numpy(m.indices), torch.from_numpy(m.indptr)),
                      shape=m.shape)
     d, i, p = A.buffers(dev)
-    plan = A.plan(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = A.plan(dev)  # the first call's cost: the bound plan is built here
+    torch.cuda.synchronize()
+    build_ms = round((time.perf_counter() - t0) * 1e3, 2)
     if k is None:
         fn = lambda: ext.csr_matvec(d, i, p, X, n_rows, n_cols, plan=plan)
     else:
@@ -414,7 +480,7 @@ def _case_call(ext, case: str, m, data, X, dev):
     vb, ib = data.element_size(), m.indices.dtype.itemsize
     nbytes = synthetic.compulsory_bytes(m.nnz, n_rows, n_cols, vb, ib, k=k or 1)
     nflops = synthetic.flops(m.nnz, k or 1, dt == torch.complex64)
-    return fn, plan.info(), nbytes, nflops, (A, d, i, p, plan)
+    return fn, plan.info(), nbytes, nflops, (A, d, i, p, plan, build_ms)
 
 
 def _kind(info) -> str:
@@ -553,6 +619,7 @@ def configs_leg(ext, dev, scratch) -> list:
         row = {"case": label, "id": case, "nnz": m.nnz,
                "op": "spmv" if k is None else f"spmm k={k}",
                "plan": _kind(info), "plan_bytes": info["plan_bytes"],
+               "plan_build_ms": keep[-1], "kernel_us_mean": round(t.mean * 1e3, 2),
                "block_nnz": info["block_nnz"], "window_rows": info["window_rows"],
                "long_rows": info["n_long_rows"], "compulsory_bytes": nbytes, "flops": nflops,
                "kernel_us": round(t * 1e3, 2), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
@@ -565,6 +632,56 @@ def configs_leg(ext, dev, scratch) -> list:
         del fn, keep, data, X
         torch.cuda.empty_cache()
     return rows
+
+
+def solver_system(name: str):
+    """(csr arrays, b, keyword arguments) of a solver leg's system at n =
+    128^3: CG on the Poisson matrix with b = 1 and rtol 1e-6; MINRES on
+    the Poisson matrix with shift -1; BiCGSTAB and GMRES(20) on the
+    convection-diffusion variant (x-direction off-diagonals -1.3 and -0.7,
+    diagonal 8) with b ~ U[-1, 1]; rtol 1e-5."""
+    from mlx_sparse import synthetic
+
+    m = synthetic.poisson_3d(128)
+    n = m.shape[0]
+    if name == "cg":
+        return m, m.data, np.ones(n, np.float32), {"rtol": 1e-6}
+    b = synthetic.uniform(n, -1.0, 1.0, seed=7)
+    if name == "minres":
+        return m, m.data, b, {"rtol": 1e-5, "maxiter": 500, "shift": -1.0}
+    rows = np.repeat(np.arange(n), np.diff(m.indptr))
+    cols = m.indices.astype(np.int64)
+    conv = m.data.copy()
+    conv[cols == rows + 1] = -0.7
+    conv[cols == rows - 1] = -1.3
+    conv[cols == rows] = 8.0
+    kw = {"rtol": 1e-5, "maxiter": 500}
+    if name == "gmres":
+        kw["restart"] = 20
+    return m, conv, b, kw
+
+
+def profile_solver(dev, name: str) -> dict:
+    """One solver alone, for rocprofv3 --kernel-trace --stats: its system
+    (``solver_system``), a warm-up solve (plan, allocator), then one timed
+    solve."""
+    import mlx_sparse as ms
+    from mlx_sparse import linalg
+
+    m, data, b_np, kw = solver_system(name)
+    A = ms.csr_array((data, m.indices, m.indptr), shape=m.shape, canonical=True)
+    b = torch.from_numpy(b_np).to(dev)
+    solver = getattr(linalg, name)
+    solver(A, b, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    x, info = solver(A, b, return_info=True, **kw)
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t0
+    return {"profile_solver": name, "n": m.shape[0], "info": info.status,
+            "iterations": info.iterations, "residual": info.residual_norm,
+            "solve_ms": round(t * 1e3, 2),
+            "us_per_iteration": round(t / max(info.iterations, 1) * 1e6, 1)}
 
 
 def profile_case(ext, dev, case: str, calls: int) -> dict:
@@ -608,6 +725,9 @@ def main() -> int:
     ap.add_argument("--profile-case", default=None, choices=sorted(CASES),
                     help="run only this configuration (calls back to back, for rocprofv3)")
     ap.add_argument("--calls", type=int, default=10, help="calls of --profile-case")
+    ap.add_argument("--profile-solver", default=None,
+                    choices=["cg", "minres", "bicgstab", "gmres"],
+                    help="run only this solver at n = 128^3 (two solves, for rocprofv3)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -627,6 +747,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.profile_case:
         print(json.dumps(profile_case(ext, dev, args.profile_case, args.calls)), flush=True)
+        return 0
+    if args.profile_solver:
+        print(json.dumps(profile_solver(dev, args.profile_solver)), flush=True)
         return 0
     if args.calibrate:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -677,9 +800,10 @@ def main() -> int:
     def launch():
         return ext.csr_matvec(data, indices, indptr, x, m.shape[0], m.shape[1], plan=plan)
 
-    kern_ms, y_graph = _graph_time(launch)
+    kern_t, y_graph = _graph_time(launch)
     if not torch.equal(y_graph, y):
         raise RuntimeError("kernel-timing output differs from the API step output")
+    kern_ms = kern_t.mean  # the average launch duration (the rocprofv3 average's twin)
     events_ms = _events_time(launch, args.steps)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     log(f"kernel (graph replay): {kern_ms * 1e3:.1f} us  {achieved:.0f} GB/s  "
@@ -728,8 +852,19 @@ def main() -> int:
                                 "slices": "spmv_sliced<F32> + slice_merge<F32>"}.get(
                                     plan_kind, f"spmv_blocks<F32,int,{info['block_nnz']}>"),
                      "kernel_us": round(kern_ms * 1e3, 2),
+                     "kernel_us_median": round(float(kern_t) * 1e3, 2),
+                     "frac_median": round(nbytes / (float(kern_t) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "cold_kernel_us": round(cold_ms * 1e3, 2),
+                     "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
                      "plan_bytes": info["plan_bytes"],
-                     "timing": "HIP-graph replay of 20 calls x 10, HIP events"},
+                     "footprint_bytes": {"matrix": m.nnz * 8 + (m.shape[0] + 1) * 4,
+                                         "plan": info["plan_bytes"],
+                                         "noalloc_scratch": NOALLOC_SCRATCH_BYTES},
+                     "timing": ("HIP-graph replays of 20 calls, 50 replays each between "
+                                "HIP events: kernel_us / achieved / frac use the mean per "
+                                "call (the average launch duration), kernel_us_median the "
+                                "median over replays; cold: median of 30 calls after a "
+                                "1 GiB write")},
         "cold": {"kernel_us": round(cold_ms * 1e3, 2), "gbs": round(cold_gbs, 1),
                  "frac": round(cold_gbs / HBM_PEAK_GBS, 4)},
     }
@@ -813,9 +948,12 @@ def main() -> int:
                 "id": "cfg2", "plan": plan_kind, "plan_bytes": info["plan_bytes"],
                 "block_nnz": info["block_nnz"], "window_rows": info["window_rows"],
                 "long_rows": info["n_long_rows"], "compulsory_bytes": nbytes, "flops": nflops,
-                "kernel_us": round(kern_ms * 1e3, 2), "gbs": round(achieved, 1),
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "gflops": round(nflops / (kern_ms * 1e-3) / 1e9, 1),
+                "plan_build_ms": round(plan_ms, 2),
+                "kernel_us": round(float(kern_t) * 1e3, 2),
+                "kernel_us_mean": round(kern_ms * 1e3, 2),
+                "gbs": round(nbytes / (float(kern_t) * 1e-3) / 1e9, 1),
+                "frac": round(nbytes / (float(kern_t) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "gflops": round(nflops / (float(kern_t) * 1e-3) / 1e9, 1),
                 "cold_us": round(cold_ms * 1e3, 2),
                 "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4)}
         result["configs"] = [head] + configs_leg(ext, dev, scratch)
