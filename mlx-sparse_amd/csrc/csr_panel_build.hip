@@ -255,22 +255,55 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Refresh of the copy's values after the matrix's values changed (same
-// indices and indptr): one workgroup per tile.  The tile's virtual rows fill
-// a map from LDS word to (virtual row - first of the tile); an entry with
-// word d then came from position b0 + d - map[d], the inverse of dest =
-// (p - b0) + (v - v0).  Every panel's segment of the tile is regathered;
-// padding entries (word 0xFFFF, outside every tile) keep their zero.
+// indices and indptr): one workgroup per tile.  The tile's values are one
+// contiguous range [b0, b1) of the matrix (at most TW of them), so they are
+// first copied into LDS with coalesced dword loads through a descriptor (no
+// branch per load); the tile's virtual rows fill a map from LDS word to
+// (virtual row - first of the tile); an entry with word d then came from
+// position b0 + d - map[d], the inverse of dest = (p - b0) + (v - v0), and
+// is read from LDS.  Every panel's segment of the tile is rewritten;
+// padding entries (word 0xFFFF, outside every tile) keep their zero.  LDS: TW 16-bit map entries + the values
+// (refresh_lds_bytes).
+constexpr int kRefreshUnroll = 4;
+constexpr int kRefreshThreads = 1024;  // one workgroup per CU (its LDS), 16 waves
+constexpr int kRefreshPanels = 8;      // panel segments per wave whose loads are in flight
+
+__host__ __device__ inline int64_t refresh_map_bytes(int64_t TW) { return (TW * 2 + 15) / 16 * 16; }
+__host__ __device__ inline int64_t refresh_lds_bytes(int64_t TW, int64_t value_bytes) {
+  return refresh_map_bytes(TW) + TW * value_bytes + 16;
+}
+
 template <class S, class RP>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kRefreshThreads)
     panel_refresh(const S *__restrict__ data, const RP *__restrict__ rowptr, int64_t nnz,
                   const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
                   const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles, int64_t TW,
                   const uint16_t *__restrict__ dest, S *__restrict__ out) {
-  __shared__ uint16_t row_of[kTileBytes / 4];  // TW <= 16384 words
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  uint16_t *row_of = reinterpret_cast<uint16_t *>(lds_raw);
+  unsigned char *vals = lds_raw + refresh_map_bytes(TW);
   const int64_t t = blockIdx.x;
   const int64_t v0 = tile_begin[t], v1 = tile_end[t];
   const int64_t b0 = vpos(rowptr, v0, nnz);
-  for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads) {
+  const int64_t b1 = clamp64(vpos(rowptr, v1, nnz), b0, b0 + TW);
+  // values [b0, b1) as the dwords that hold them: byte `off0` of the first
+  // dword is position b0 (16-bit values may start mid-dword)
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(data + b0);
+  const uint32_t off0 = static_cast<uint32_t>(a0 & 3u);
+  const uint32_t n_dw =
+      static_cast<uint32_t>((off0 + static_cast<uint64_t>(b1 - b0) * sizeof(S) + 3) / 4);
+  const auto r = make_rsrc(reinterpret_cast<const void *>(a0 - off0), uint64_t{4} * n_dw);
+  auto *vw = reinterpret_cast<uint32_t *>(vals);
+  for (uint32_t i = threadIdx.x; i < n_dw; i += kRefreshUnroll * kRefreshThreads) {
+    uint32_t w[kRefreshUnroll];
+#pragma unroll
+    for (int u = 0; u < kRefreshUnroll; ++u)
+      w[u] = __builtin_amdgcn_raw_buffer_load_b32(r, 4u * (i + u * kRefreshThreads), 0, 0);
+#pragma unroll
+    for (int u = 0; u < kRefreshUnroll; ++u)
+      if (i + u * kRefreshThreads < n_dw) vw[i + u * kRefreshThreads] = w[u];
+  }
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += kRefreshThreads) {
     const int64_t s = vpos(rowptr, v, nnz);
     const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, nnz);
     for (int64_t p = s; p < e; ++p) {
@@ -280,12 +313,39 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  for (int64_t q = wave; q < n_panels; q += kThreads / kWave) {
-    const int64_t a = seg[q * n_tiles + t], b = seg[q * n_tiles + t + 1];
-    for (int64_t e = a + lane; e < b; e += kWave) {
-      const int64_t d = dest[e];
-      if (d >= TW) continue;
-      out[e] = data[clamp64(b0 + d - row_of[d], 0, nnz - 1)];
+  const int64_t nb = b1 - b0;
+  auto value_at = [&](int64_t d) -> S {
+    S v{};
+    const int64_t i = d - row_of[d];  // position - b0
+    if (i >= 0 && i < nb) __builtin_memcpy(&v, vals + off0 + i * sizeof(S), sizeof(S));
+    return v;
+  };
+  // Wave w takes panels w, w + 16, ... in batches of kRefreshPanels: the
+  // word loads of all of a batch's segments are issued before the first
+  // is used (one round trip per 64 entries of the longest segment, not one
+  // per segment).  Segments start on a multiple of 4 entries, so dest + a
+  // is 8-byte aligned.
+  constexpr int kWaves = kRefreshThreads / kWave;
+  for (int64_t qb = 0; qb < n_panels; qb += kWaves * kRefreshPanels) {
+    int64_t a[kRefreshPanels];
+    uint32_t len[kRefreshPanels], most = 0;
+    __amdgpu_buffer_rsrc_t rd[kRefreshPanels];
+#pragma unroll
+    for (int k = 0; k < kRefreshPanels; ++k) {
+      const int64_t q = qb + wave + static_cast<int64_t>(kWaves) * k;
+      a[k] = q < n_panels ? static_cast<int64_t>(seg[q * n_tiles + t]) : 0;
+      len[k] = q < n_panels ? static_cast<uint32_t>(seg[q * n_tiles + t + 1] - a[k]) : 0u;
+      most = len[k] > most ? len[k] : most;
+      rd[k] = make_rsrc(dest + a[k], uint64_t{2} * len[k]);
+    }
+    for (uint32_t e = lane; e < most; e += kWave) {
+      uint32_t d[kRefreshPanels];
+#pragma unroll
+      for (int k = 0; k < kRefreshPanels; ++k)
+        d[k] = __builtin_amdgcn_raw_buffer_load_b16(rd[k], 2u * e, 0, 0);
+#pragma unroll
+      for (int k = 0; k < kRefreshPanels; ++k)
+        if (e < len[k] && d[k] < TW) out[a[k] + e] = value_at(d[k]);
     }
   }
 }
@@ -590,17 +650,25 @@ template <class V, class I>
 msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) {
   using S = typename V::Storage;
   if (p->n_tiles == 0 || p->pn_values == 0) return MSX_OK;
-  if (p->pn_vstart != nullptr)
+  const size_t lds = static_cast<size_t>(refresh_lds_bytes(p->tile_words, sizeof(S)));
+  if (p->pn_vstart != nullptr) {
+    MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_refresh<S, uint32_t>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)));
     hipLaunchKernelGGL((panel_refresh<S, uint32_t>), dim3(static_cast<uint32_t>(p->n_tiles)),
-                       dim3(kThreads), 0, stream, static_cast<const S *>(data), p->pn_vstart, p->nnz,
-                       p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels, p->n_tiles,
-                       p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
-  else
+                       dim3(kRefreshThreads), lds, stream, static_cast<const S *>(data), p->pn_vstart,
+                       p->nnz, p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels,
+                       p->n_tiles, p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
+  } else {
+    MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_refresh<S, I>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)));
     hipLaunchKernelGGL((panel_refresh<S, I>), dim3(static_cast<uint32_t>(p->n_tiles)),
-                       dim3(kThreads), 0, stream, static_cast<const S *>(data),
+                       dim3(kRefreshThreads), lds, stream, static_cast<const S *>(data),
                        static_cast<const I *>(p->indptr), p->nnz, p->pn_tile_begin, p->pn_tile_end,
                        p->pn_seg, p->n_panels, p->n_tiles, p->tile_words, p->pn_dest,
                        static_cast<S *>(p->pn_data));
+  }
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
 }
