@@ -110,9 +110,14 @@ __global__ void __launch_bounds__(kSolverThreads)
     cg_alpha(const float *__restrict__ p, const float *__restrict__ ap, int64_t n, int32_t it,
              const double *dir_part, double *part, int nparts, CgState *st) {
   if (!st->running) return;
+  double pin[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  if (it > 1) load_partials(dir_part, nparts, pin);
+  const float *const vec[2] = {p, ap};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   if (it > 1) {
     double t[kSlots];
-    read_totals(dir_part, nparts, t);
+    reduce_partials(pin, nparts, t);
     if (t[3] != 0.0) {
       if (blockIdx.x == 0 && threadIdx.x == 0) stop(st, -3, it - 1);
       return;
@@ -120,13 +125,13 @@ __global__ void __launch_bounds__(kSolverThreads)
     if (blockIdx.x == 0 && threadIdx.x == 0) st->rr = st->rr_next;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double pd = p[i], ad = ap[i];
+  for_rounds<2>(vec, n, first, [&](int64_t, const float(&e)[2]) {
+    const double pd = e[0], ad = e[1];
     v[0] += pd * ad;
     v[1] += pd * pd;
     v[2] += ad * ad;
-    if (!(fin(p[i]) && fin(ap[i]))) v[3] += 1.0;
-  })
+    if (!(fin(e[0]) && fin(e[1]))) v[3] += 1.0;
+  });
   write_partials(v, part);
 }
 
@@ -137,8 +142,13 @@ __global__ void __launch_bounds__(kSolverThreads)
               const float *__restrict__ ap, int64_t n, int32_t it, const double *alpha_part,
               double *part, int nparts, CgState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(alpha_part, nparts, pin);
+  const float *const vec[4] = {x, r, p, ap};
+  Round<4> first;
+  load_round<4>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(alpha_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const double denom = t[0];
   const double eps = static_cast<double>(FLT_EPSILON);
@@ -158,37 +168,20 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  // All loads of a thread's kUnroll elements first (an index past n reads
-  // element `base` instead), then the arithmetic and the stores: written as
-  // one loop body, the compiler waited for each element's loads in turn.
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
-       base += kUnroll * stride) {
-    float xo[kUnroll], ro[kUnroll], pv[kUnroll], av[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = base + u * stride < n ? base + u * stride : base;
-      xo[u] = x[j];
-      ro[u] = r[j];
-      pv[u] = p[j];
-      av[u] = ap[j];
+  // All loads of a round first, then the arithmetic and the stores: written
+  // as one loop body, the compiler waited for each element's loads in turn.
+  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
+    const double xc = static_cast<double>(e[0]) + alpha * static_cast<double>(e[2]);
+    const double rc = static_cast<double>(e[1]) - alpha * static_cast<double>(e[3]);
+    const float xf = static_cast<float>(xc), rf = static_cast<float>(rc);
+    if (!fin(xc) || !fin(rc) || !fin(xf) || !fin(rf)) {
+      v[3] += 1.0;
+    } else {
+      x[i] = xf;
+      r[i] = rf;
+      v[0] += static_cast<double>(rf) * static_cast<double>(rf);
     }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + u * stride;
-      if (i >= n) break;
-      const double xc = static_cast<double>(xo[u]) + alpha * static_cast<double>(pv[u]);
-      const double rc = static_cast<double>(ro[u]) - alpha * static_cast<double>(av[u]);
-      const float xf = static_cast<float>(xc), rf = static_cast<float>(rc);
-      if (!fin(xc) || !fin(rc) || !fin(xf) || !fin(rf)) {
-        v[3] += 1.0;
-      } else {
-        x[i] = xf;
-        r[i] = rf;
-        v[0] += static_cast<double>(rf) * static_cast<double>(rf);
-      }
-    }
-  }
+  });
   write_partials(v, part);
 }
 
@@ -198,8 +191,13 @@ __global__ void __launch_bounds__(kSolverThreads)
     cg_direction(const float *__restrict__ r, float *__restrict__ p, int64_t n, int32_t it,
                  const double *upd_part, double *part, int nparts, CgState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(upd_part, nparts, pin);
+  const float *const vec[2] = {r, p};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(upd_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const double rr_new = t[0];
   const float r_norm = static_cast<float>(sqrt(max0(rr_new)));
@@ -220,27 +218,12 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  // loads first, then arithmetic and stores, as in cg_update
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
-       base += kUnroll * stride) {
-    float rv[kUnroll], pv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = base + u * stride < n ? base + u * stride : base;
-      rv[u] = r[j];
-      pv[u] = p[j];
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + u * stride;
-      if (i >= n) break;
-      const double pc = static_cast<double>(rv[u]) + beta * static_cast<double>(pv[u]);
-      const float pf = static_cast<float>(pc);
-      if (!fin(pc) || !fin(pf)) v[3] += 1.0;
-      else p[i] = pf;
-    }
-  }
+  for_rounds<2>(vec, n, first, [&](int64_t i, const float(&e)[2]) {
+    const double pc = static_cast<double>(e[0]) + beta * static_cast<double>(e[1]);
+    const float pf = static_cast<float>(pc);
+    if (!fin(pc) || !fin(pf)) v[3] += 1.0;
+    else p[i] = pf;
+  });
   write_partials(v, part);
   if (lead) {
     st->completed = it;
@@ -339,8 +322,13 @@ __global__ void __launch_bounds__(kSolverThreads)
                const float *__restrict__ inv_diag, int64_t n, int32_t it,
                const double *alpha_part, double *part, int nparts, CgState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(alpha_part, nparts, pin);
+  const float *const vec[5] = {x, p, r, ap, inv_diag};
+  Round<5> first;
+  load_round<5>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(alpha_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const float eps = FLT_EPSILON;
   const float denom = to_f(t[0]), p2 = to_f(t[1]), ap2 = to_f(t[2]);
@@ -356,35 +344,17 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  // loads first, then arithmetic and stores, as in cg_update
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
-       base += kUnroll * stride) {
-    float xo[kUnroll], po[kUnroll], ro[kUnroll], ao[kUnroll], dv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = base + u * stride < n ? base + u * stride : base;
-      xo[u] = x[j];
-      po[u] = p[j];
-      ro[u] = r[j];
-      ao[u] = ap[j];
-      dv[u] = inv_diag[j];
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + u * stride;
-      if (i >= n) break;
-      const float xi = xo[u] + alpha * po[u];
-      const float ri = ro[u] - alpha * ao[u];
-      const float zi = dv[u] * ri;
-      x[i] = xi;
-      r[i] = ri;
-      z[i] = zi;
-      v[0] += static_cast<double>(ri) * static_cast<double>(ri);
-      v[1] += static_cast<double>(ri) * static_cast<double>(zi);
-      if (!(fin(xi) && fin(ri) && fin(zi))) v[3] += 1.0;
-    }
-  }
+  for_rounds<5>(vec, n, first, [&](int64_t i, const float(&e)[5]) {
+    const float xi = e[0] + alpha * e[1];
+    const float ri = e[2] - alpha * e[3];
+    const float zi = e[4] * ri;
+    x[i] = xi;
+    r[i] = ri;
+    z[i] = zi;
+    v[0] += static_cast<double>(ri) * static_cast<double>(ri);
+    v[1] += static_cast<double>(ri) * static_cast<double>(zi);
+    if (!(fin(xi) && fin(ri) && fin(zi))) v[3] += 1.0;
+  });
   write_partials(v, part);
 }
 
@@ -393,8 +363,13 @@ __global__ void __launch_bounds__(kSolverThreads)
     pcg_direction(const float *__restrict__ z, float *__restrict__ p, int64_t n, int32_t it,
                   const double *upd_part, int nparts, CgState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(upd_part, nparts, pin);
+  const float *const vec[2] = {z, p};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(upd_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   const float true_rr = to_f(t[0]);
   const float r_norm = sqrtf(max0(true_rr));
@@ -413,23 +388,7 @@ __global__ void __launch_bounds__(kSolverThreads)
     if (lead) stop(st, verdict, it);
     return;
   }
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x; base < n;
-       base += kUnroll * stride) {  // loads first, as in cg_update
-    float zv[kUnroll], pv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = base + u * stride < n ? base + u * stride : base;
-      zv[u] = z[j];
-      pv[u] = p[j];
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + u * stride;
-      if (i >= n) break;
-      p[i] = zv[u] + beta * pv[u];
-    }
-  }
+  for_rounds<2>(vec, n, first, [&](int64_t i, const float(&e)[2]) { p[i] = e[0] + beta * e[1]; });
   if (lead) st->rr_next = rho_new;
 }
 

@@ -123,47 +123,69 @@ __global__ void __launch_bounds__(kSolverThreads)
 // with s > 0, column (s - 1) % ncol's coefficient (the previous pass's
 // total, rounded to float) goes into h and its projection leaves w; then
 // the dot product of the next column (s < 2 ncol) or w.w (s = 2 ncol).
+// The previous pass's partials, then a thread's first kUnroll elements of w
+// and of both basis vectors, are loaded before the partials are reduced, so
+// that the reduction (its wave sums and barriers) overlaps the element
+// loads.
 __global__ void __launch_bounds__(kSolverThreads)
     gm_mgs(const float *__restrict__ V, int64_t ld, float *__restrict__ w, int64_t n, int32_t j,
            int32_t s, const double *part_in, int nparts, double *part_out, float *__restrict__ h,
            int64_t k, const GmState *st) {
   if (st->stop_at < j) return;  // an earlier step ended this cycle
   const int32_t ncol = j + 1;
+  const bool sub = s > 0, norm = s == 2 * ncol;
+  const float *q_prev = V + static_cast<int64_t>(sub ? (s - 1) % ncol : 0) * ld;
+  const float *q = V + static_cast<int64_t>(norm ? 0 : s % ncol) * ld;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  const int64_t base0 = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x;
+  double pv_in[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  if (sub) load_partials(part_in, nparts, pv_in);
+  float w0[kUnroll], p0[kUnroll], q0[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base0 + u * stride < n ? base0 + u * stride : (base0 < n ? base0 : 0);
+    w0[u] = w[i];
+    p0[u] = q_prev[i];
+    q0[u] = q[i];
+  }
   float coeff = 0.0f;
-  const float *q_prev = V;
-  if (s > 0) {
+  if (sub) {
     double t[kSlots];
-    read_totals(part_in, nparts, t);
+    reduce_partials(pv_in, nparts, t);
     coeff = static_cast<float>(t[0]);
-    const int32_t c_prev = (s - 1) % ncol;
-    q_prev = V + static_cast<int64_t>(c_prev) * ld;
-    if (lead()) h[static_cast<int64_t>(c_prev) * k + j] += coeff;
+    if (lead()) h[static_cast<int64_t>((s - 1) % ncol) * k + j] += coeff;
   }
-  double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  if (s < 2 * ncol) {
-    const float *q = V + static_cast<int64_t>(s % ncol) * ld;
-    if (s > 0) {
-      MSX_SOLVER_LOOP({
-        const float t = coeff * q_prev[i];
-        const float wi = w[i] - t;
-        w[i] = wi;
-        const float prod = q[i] * wi;
-        v[0] += static_cast<double>(prod);
-      })
-    } else {
-      MSX_SOLVER_LOOP({
-        const float prod = q[i] * w[i];
-        v[0] += static_cast<double>(prod);
-      })
+  double acc = 0.0;
+  auto one = [&](int64_t i, float wv, float pv, float qv) {
+    if (sub) {
+      const float t = coeff * pv;
+      wv = wv - t;
+      w[i] = wv;
     }
-  } else {
-    MSX_SOLVER_LOOP({
-      const float t = coeff * q_prev[i];
-      const float wi = w[i] - t;
-      w[i] = wi;
-      v[0] += static_cast<double>(wi) * static_cast<double>(wi);
-    })
+    if (norm) {
+      acc += static_cast<double>(wv) * static_cast<double>(wv);
+    } else {
+      const float prod = qv * wv;
+      acc += static_cast<double>(prod);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (base0 + u * stride < n) one(base0 + u * stride, w0[u], p0[u], q0[u]);
+  for (int64_t base = base0 + kUnroll * stride; base < n; base += kUnroll * stride) {
+    float wv[kUnroll], pv[kUnroll], qv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * stride < n ? base + u * stride : base;
+      wv[u] = w[i];
+      pv[u] = q_prev[i];
+      qv[u] = q[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (base + u * stride < n) one(base + u * stride, wv[u], pv[u], qv[u]);
   }
+  double v[kSlots] = {acc, 0.0, 0.0, 0.0};
   write_partials(v, part_out);
 }
 

@@ -173,8 +173,13 @@ __global__ void __launch_bounds__(kSolverThreads)
          int64_t n, int32_t k, int close_prev, const double *dots, double *part, int nparts,
          BiState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(dots, nparts, pin);
+  const float *const vec[3] = {r, p, v};
+  Round<3> first;
+  load_round<3>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(dots, nparts, t);
+  reduce_partials(pin, nparts, t);
   if (close_prev && !bi_close(t, k - 1, st)) return;
   if (close_prev && lead()) st->residual = static_cast<float>(sqrt(max0(t[0])));
   const double rho = t[2], rr = t[3], hh = st->hh;
@@ -196,15 +201,15 @@ __global__ void __launch_bounds__(kSolverThreads)
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
   if (k == 1) {
-    MSX_SOLVER_LOOP({ p[i] = r[i]; })
+    for_rounds<3>(vec, n, first, [&](int64_t i, const float(&e)[3]) { p[i] = e[0]; });
   } else {
-    MSX_SOLVER_LOOP({
-      const double pi = static_cast<double>(r[i]) +
-                        beta * (static_cast<double>(p[i]) - omega * static_cast<double>(v[i]));
+    for_rounds<3>(vec, n, first, [&](int64_t i, const float(&e)[3]) {
+      const double pi = static_cast<double>(e[0]) +
+                        beta * (static_cast<double>(e[1]) - omega * static_cast<double>(e[2]));
       const float pf = static_cast<float>(pi);
       p[i] = pf;
       if (!fin(pi) || !fin(pf)) acc[1] += 1.0;
-    })
+    });
   }
   write_partials(acc, part);
   if (lead()) st->rho[k & 1] = rho;
@@ -215,18 +220,23 @@ __global__ void __launch_bounds__(kSolverThreads)
     bi_v(const float *__restrict__ r_hat, const float *__restrict__ v, int64_t n, int32_t k,
          const double *p_part, double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(p_part, nparts, pin);
+  const float *const vec[2] = {r_hat, v};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(p_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   if (t[1] != 0.0) {
     if (lead()) bi_stop(st, -3, k - 1);
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double vi = v[i];
-    acc[0] += static_cast<double>(r_hat[i]) * vi;
+  for_rounds<2>(vec, n, first, [&](int64_t, const float(&e)[2]) {
+    const double vi = e[1];
+    acc[0] += static_cast<double>(e[0]) * vi;
     acc[1] += vi * vi;
-  })
+  });
   write_partials(acc, part);
 }
 
@@ -237,8 +247,13 @@ __global__ void __launch_bounds__(kSolverThreads)
          float *__restrict__ x, float *__restrict__ s, int64_t n, int32_t k, const double *v_part,
          double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(v_part, nparts, pin);
+  const float *const vec[4] = {r, v, x, p};
+  Round<4> first;
+  load_round<4>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(v_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const double hv = t[0], vv = t[1];
   int32_t verdict = 1;
   double alpha = 0.0;
@@ -253,15 +268,15 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double si = static_cast<double>(r[i]) - alpha * static_cast<double>(v[i]);
-    const double xi = static_cast<double>(x[i]) + alpha * static_cast<double>(p[i]);
+  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
+    const double si = static_cast<double>(e[0]) - alpha * static_cast<double>(e[1]);
+    const double xi = static_cast<double>(e[2]) + alpha * static_cast<double>(e[3]);
     const float sf = static_cast<float>(si), xf = static_cast<float>(xi);
     s[i] = sf;
     x[i] = xf;
     acc[0] += si * si;
     if (!(fin(si) && fin(xi) && fin(sf) && fin(xf))) acc[1] += 1.0;
-  })
+  });
   write_partials(acc, part);
   if (lead()) {
     st->alpha = alpha;
@@ -275,9 +290,14 @@ __global__ void __launch_bounds__(kSolverThreads)
     bi_t(const float *__restrict__ s, const float *__restrict__ t_vec, int64_t n, int32_t k,
          int check, const double *s_part, double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  double pin[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  if (check) load_partials(s_part, nparts, pin);
+  const float *const vec[2] = {s, t_vec};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   if (check) {
     double t[kSlots];
-    read_totals(s_part, nparts, t);
+    reduce_partials(pin, nparts, t);
     const float s_norm = static_cast<float>(sqrt(max0(t[0])));
     if (t[1] != 0.0 || !fin(t[0]) || !fin(s_norm)) {
       if (lead()) bi_stop(st, -3, k);
@@ -293,11 +313,11 @@ __global__ void __launch_bounds__(kSolverThreads)
     }
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double ti = t_vec[i];
-    acc[0] += ti * static_cast<double>(s[i]);
+  for_rounds<2>(vec, n, first, [&](int64_t, const float(&e)[2]) {
+    const double ti = e[1];
+    acc[0] += ti * static_cast<double>(e[0]);
     acc[1] += ti * ti;
-  })
+  });
   write_partials(acc, part);
 }
 
@@ -309,8 +329,13 @@ __global__ void __launch_bounds__(kSolverThreads)
          float *__restrict__ r, const float *__restrict__ r_hat, int64_t n, int32_t k,
          const double *t_part, double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(t_part, nparts, pin);
+  const float *const vec[4] = {x, s, t_vec, r_hat};
+  Round<4> first;
+  load_round<4>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(t_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const double ts = t[0], tt = t[1];
   int32_t verdict = 1;
   double omega = 0.0;
@@ -325,17 +350,17 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double xi = static_cast<double>(x[i]) + omega * static_cast<double>(s[i]);
-    const double ri = static_cast<double>(s[i]) - omega * static_cast<double>(t_vec[i]);
+  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
+    const double xi = static_cast<double>(e[0]) + omega * static_cast<double>(e[1]);
+    const double ri = static_cast<double>(e[1]) - omega * static_cast<double>(e[2]);
     const float xf = static_cast<float>(xi), rf = static_cast<float>(ri);
     x[i] = xf;
     r[i] = rf;
     acc[0] += ri * ri;
     if (!(fin(xi) && fin(ri) && fin(xf) && fin(rf))) acc[1] += 1.0;
-    acc[2] += static_cast<double>(r_hat[i]) * static_cast<double>(rf);
+    acc[2] += static_cast<double>(e[3]) * static_cast<double>(rf);
     acc[3] += static_cast<double>(rf) * static_cast<double>(rf);
-  })
+  });
   write_partials(acc, part);
   if (lead()) st->omega = omega;
 }
@@ -498,9 +523,14 @@ __global__ void __launch_bounds__(kSolverThreads)
     mr_v(const float *__restrict__ r2, float *__restrict__ v, int64_t n, int32_t k,
          const double *res_part, int nparts, MrState *st) {
   if (!st->running) return;
+  double pin[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  if (k > 1) load_partials(res_part, nparts, pin);
+  const float *const vec[1] = {r2};
+  Round<1> first;
+  load_round<1>(vec, first_base(), n, first);
   if (k > 1) {
     double t[kSlots];
-    read_totals(res_part, nparts, t);
+    reduce_partials(pin, nparts, t);
     if (!mr_close(t, k - 1, st)) return;
   }
   const double beta = st->g[(k - 1) & 1].beta;
@@ -509,7 +539,9 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   const double inv_beta = 1.0 / beta;
-  MSX_SOLVER_LOOP({ v[i] = static_cast<float>(inv_beta * static_cast<double>(r2[i])); })
+  for_rounds<1>(vec, n, first, [&](int64_t i, const float(&e)[1]) {
+    v[i] = static_cast<float>(inv_beta * static_cast<double>(e[0]));
+  });
 }
 
 // av -= shift v, av -= (beta / oldb) r1 from the second iteration on
@@ -550,8 +582,13 @@ __global__ void __launch_bounds__(kSolverThreads)
     mr_b(float *__restrict__ av, const float *__restrict__ r2, int64_t n, int32_t k,
          const double *a_part, double *part, int nparts, MrState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(a_part, nparts, pin);
+  const float *const vec[2] = {av, r2};
+  Round<2> first;
+  load_round<2>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(a_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   const double alfa = static_cast<double>(static_cast<float>(t[0]));
   if (!fin(alfa)) {
     if (lead()) mr_stop(st, -3, k - 1);
@@ -559,11 +596,11 @@ __global__ void __launch_bounds__(kSolverThreads)
   }
   const float diag_scale = static_cast<float>(alfa / st->g[(k - 1) & 1].beta);
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const float a = av[i] - diag_scale * r2[i];
+  for_rounds<2>(vec, n, first, [&](int64_t i, const float(&e)[2]) {
+    const float a = e[0] - diag_scale * e[1];
     av[i] = a;
     acc[0] += static_cast<double>(a) * static_cast<double>(a);
-  })
+  });
   write_partials(acc, part);
 }
 
@@ -575,9 +612,15 @@ __global__ void __launch_bounds__(kSolverThreads)
          float *__restrict__ x, int64_t n, int32_t k, const double *a_part,
          const double *b_part, double *part, int nparts, MrState *st) {
   if (!st->running) return;
+  double pa[kSlots], pb[kSlots];
+  load_partials(a_part, nparts, pa);
+  load_partials(b_part, nparts, pb);
+  const float *const vec[4] = {v, w, w2, x};
+  Round<4> first;
+  load_round<4>(vec, first_base(), n, first);
   double ta[kSlots], tb[kSlots];
-  read_totals(a_part, nparts, ta);
-  read_totals(b_part, nparts, tb);
+  reduce_partials(pa, nparts, ta);
+  reduce_partials(pb, nparts, tb);
   const Givens g = st->g[(k - 1) & 1];
   const double alfa = static_cast<double>(static_cast<float>(ta[0]));
   const double beta_sq = static_cast<double>(static_cast<float>(tb[0]));
@@ -608,15 +651,15 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const double older = w2[i], old = w[i];
+  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
+    const double older = e[2], old = e[1];
     const float wn =
-        static_cast<float>((static_cast<double>(v[i]) - oldeps * older - delta * old) / gamma);
-    const float xn = x[i] + static_cast<float>(phi * static_cast<double>(wn));
+        static_cast<float>((static_cast<double>(e[0]) - oldeps * older - delta * old) / gamma);
+    const float xn = e[3] + static_cast<float>(phi * static_cast<double>(wn));
     w2[i] = wn;
     x[i] = xn;
     if (!(fin(wn) && fin(xn))) acc[0] += 1.0;
-  })
+  });
   write_partials(acc, part);
   if (lead()) {
     st->g[k & 1] = h;
@@ -631,19 +674,24 @@ __global__ void __launch_bounds__(kSolverThreads)
          float shift, int64_t n, int32_t k, const double *x_part, double *part, int nparts,
          MrState *st) {
   if (!st->running) return;
+  double pin[kSlots];
+  load_partials(x_part, nparts, pin);
+  const float *const vec[3] = {b, x, ax};
+  Round<3> first;
+  load_round<3>(vec, first_base(), n, first);
   double t[kSlots];
-  read_totals(x_part, nparts, t);
+  reduce_partials(pin, nparts, t);
   if (t[0] != 0.0) {
     if (lead()) mr_stop(st, -3, k);
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  MSX_SOLVER_LOOP({
-    const float ai = ax[i] - shift * x[i];
-    const float ri = b[i] - ai;
+  for_rounds<3>(vec, n, first, [&](int64_t, const float(&e)[3]) {
+    const float ai = e[2] - shift * e[1];
+    const float ri = e[0] - ai;
     acc[0] += static_cast<double>(ri) * static_cast<double>(ri);
     if (!(fin(ai) && fin(ri))) acc[1] += 1.0;
-  })
+  });
   write_partials(acc, part);
 }
 

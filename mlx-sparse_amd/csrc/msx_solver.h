@@ -55,16 +55,21 @@ __device__ inline void write_partials(double (&v)[kSlots], double *part) {
 }
 
 // Totals of the previous pass's `nparts` partials, the same bits in every
-// workgroup (fixed order, written by an earlier kernel).
-__device__ inline void read_totals(const double *part, int nparts, double (&t)[kSlots]) {
-  __shared__ double sh[kSlots][kSolverThreads / kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  // all kSlots loads first (clamped index, no branch), then the sums
-  const bool mine = static_cast<int>(threadIdx.x) < nparts;
-  const int idx = mine ? static_cast<int>(threadIdx.x) : 0;
-  double v[kSlots];
+// workgroup (fixed order, written by an earlier kernel).  In two steps, so
+// that a kernel can issue its own element loads between them: loads are
+// waited on in issue order, so partials loaded after the elements would wait
+// for the elements too.
+__device__ inline void load_partials(const double *part, int nparts, double (&v)[kSlots]) {
+  // all kSlots loads at once (clamped index, no branch)
+  const int idx = static_cast<int>(threadIdx.x) < nparts ? static_cast<int>(threadIdx.x) : 0;
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) v[k] = part[k * kSolverMaxBlocks + idx];
+}
+
+__device__ inline void reduce_partials(const double (&v)[kSlots], int nparts, double (&t)[kSlots]) {
+  __shared__ double sh[kSlots][kSolverThreads / kWave];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const bool mine = static_cast<int>(threadIdx.x) < nparts;
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) {
     const double w = wave_sum(mine ? v[k] : 0.0);
@@ -77,6 +82,12 @@ __device__ inline void read_totals(const double *part, int nparts, double (&t)[k
     t[k] = s;
   }
   __syncthreads();
+}
+
+__device__ inline void read_totals(const double *part, int nparts, double (&t)[kSlots]) {
+  double v[kSlots];
+  load_partials(part, nparts, v);
+  reduce_partials(v, nparts, t);
 }
 
 // Grid-stride over [0, n) with kUnroll coalesced elements per round.
@@ -102,6 +113,53 @@ __device__ inline void read_totals(const double *part, int nparts, double (&t)[k
       }                                                                                      \
     }                                                                                        \
   }
+
+// A pass whose arithmetic needs the previous pass's totals issues, in this
+// order, that pass's partial loads (load_partials), the loads of its own
+// first round of elements (load_round: kUnroll grid-stride elements of each
+// of NV vectors; an index past n reads the thread's first element, or
+// element 0), then reduces the partials (reduce_partials) and runs
+// for_rounds: op(i, e) for every element i of the thread in grid-stride
+// order, e holding its NV values - the first round from those registers,
+// each later round loaded whole before its first use.  The reduction's
+// wave sums and barriers then overlap the element loads.
+template <int NV>
+struct Round {
+  float e[kUnroll][NV];
+};
+
+template <int NV>
+__device__ inline void load_round(const float *const (&vec)[NV], int64_t base, int64_t n,
+                                  Round<NV> &r) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t j = base + u * stride < n ? base + u * stride : (base < n ? base : 0);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) r.e[u][k] = vec[k][j];
+  }
+}
+
+__device__ inline int64_t first_base() {
+  return static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x;
+}
+
+template <int NV, class Op>
+__device__ inline void for_rounds(const float *const (&vec)[NV], int64_t n, const Round<NV> &first,
+                                  Op op) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
+  const int64_t base0 = first_base();
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (base0 + u * stride < n) op(base0 + u * stride, first.e[u]);
+  for (int64_t base = base0 + kUnroll * stride; base < n; base += kUnroll * stride) {
+    Round<NV> r;
+    load_round<NV>(vec, base, n, r);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (base + u * stride < n) op(base + u * stride, r.e[u]);
+  }
+}
 
 // Host side: iterations to enqueue before the next read of the solver
 // state.  An iteration enqueued past the solve's stop still runs its SpMVs
