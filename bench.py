@@ -317,13 +317,24 @@ def inplace_training(A, x, g) -> dict:
     _, i, p = A2.buffers(x.device)
     pos = _native.csr_transpose_positions(i, p, A2.shape)[0]
     t_vals = torch.empty_like(d)
-    regather = lambda: _native.csr_transpose_values(d, pos, False, t_vals)
+    gather = lambda: _native.csr_transpose_values(d, pos, False, t_vals)
+    gather()
+    out["transpose_gather_us"] = round(_events_time(gather, 20) * 1e3, 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    layout = _native.csr_transpose_layout(pos, d)
+    torch.cuda.synchronize()
+    out["transpose_layout_build_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+    scratch = torch.empty_like(d)
+    regather = lambda: _native.csr_transpose_values_layout(d, layout, False, scratch, t_vals)
     regather()
     out["transpose_regather_us"] = round(_events_time(regather, 20) * 1e3, 1)
     out["inplace_train_step"] = ("SGD step on A.data in place: plan refresh + forward SpMV + "
-                                 "A^T g over the regathered cached transpose + value "
-                                 "gradient through the panel plan + the update")
-    del A2, vals, x2, pos, t_vals
+                                 "A^T g over the cached transpose (values regathered in two "
+                                 "streaming passes) + value gradient through the panel plan + "
+                                 "the update; transpose_gather_us: the one-pass random gather "
+                                 "it replaces")
+    del A2, vals, x2, pos, t_vals, layout, scratch
     return out
 
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSX_ABI_VERSION 6
+#define MSX_ABI_VERSION 7
 
 typedef enum msx_vtype {
   MSX_F32 = 0,  /* float32 */
@@ -360,12 +360,44 @@ msx_status msx_csr_transpose_positions(msx_itype it, int64_t n_rows,
 /*
  * t_data[i] = data[t_pos[i]] for i < nnz whose t_pos[i] lies in [0, nnz)
  * (complex conjugated when `conjugate` is nonzero and vt is complex64, which
- * gives the values of A^H); other entries are left alone.  Device pointers,
- * asynchronous on `stream`.
+ * gives the values of A^H); other entries get zero bits, as
+ * msx_csr_transpose writes them.  Device pointers, asynchronous on
+ * `stream`.  One random gather per value.
  */
 msx_status msx_csr_transpose_values(msx_vtype vt, int64_t nnz,
                                     const void *data, const int32_t *t_pos,
                                     int conjugate, void *t_data, void *stream);
+
+/*
+ * The same regather as msx_csr_transpose_values in two streaming passes,
+ * for a transpose whose values are refreshed many times (a training loop):
+ *
+ * msx_csr_transpose_layout computes, once, from t_pos (as
+ * msx_csr_transpose_positions writes it) the layout of the two passes for
+ * values of type vt: slot1 (nnz uint16), src1 (nnz uint32), slot2 (nnz
+ * uint16).  Scratch from `stream`'s stream-ordered allocator (24 bytes per
+ * value).
+ *
+ * msx_csr_transpose_values_layout then writes t_data exactly as
+ * msx_csr_transpose_values would (conjugation, zero bits for dropped
+ * entries), with `scratch` nnz values of type vt (overwritten) and a layout
+ * built for the same vt and nnz.  Device pointers, asynchronous on
+ * `stream`; calls that share `scratch` must not overlap.
+ *
+ * No reference counterpart (the reference's arrays are immutable,
+ * reference: mlx_sparse/_csr.py:33).
+ */
+msx_status msx_csr_transpose_layout(msx_vtype vt, int64_t nnz,
+                                    const int32_t *t_pos, uint16_t *slot1,
+                                    uint32_t *src1, uint16_t *slot2,
+                                    void *stream);
+msx_status msx_csr_transpose_values_layout(msx_vtype vt, int64_t nnz,
+                                           const void *data,
+                                           const uint16_t *slot1,
+                                           const uint32_t *src1,
+                                           const uint16_t *slot2, int conjugate,
+                                           void *scratch, void *t_data,
+                                           void *stream);
 
 /*
  * y = A^T x (x: n_rows, y: n_cols) and Y = A^T X (X: n_rows x k, row stride

@@ -682,6 +682,268 @@ struct SpmmDataVjpOp {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Regather of a cached transpose's values in two streaming passes.
+//
+// t_data[i] = data[t_pos[i]] is a random gather (one 4-byte read per value
+// from a 268 MB array on the headline matrix: 1.28 ms).  With the
+// permutation fixed, it splits into two passes that each stream:
+//
+//   pass 1 (one workgroup per source tile of D1 values): the tile's values
+//           are placed in LDS at slot1[p], their order sorted by destination
+//           bucket, and written back in place to the scratch array S1
+//           (coalesced in and out);
+//   pass 2 (one workgroup per destination bucket of D2 entries): the
+//           bucket's entries are read from S1 at src1[s] - per tile, one
+//           contiguous run of D1 * D2 / nnz values - placed in LDS at
+//           slot2[s] (their offset in the bucket) and written out in order.
+//
+// The layout (slot1, src1, slot2) comes from two stable radix sorts of the
+// positions, once.  Sizes by value width: D1 * width = 128 KB of LDS at
+// most (64 KB for 16-bit values), D2 * width = 64 KB; D1 <= 32768, so a
+// slot fits 16 bits and 0xFFFF marks a source no entry takes.
+template <int VB>
+struct PermSizes {
+  static constexpr int D1 = VB == 8 ? 16384 : 32768;
+  static constexpr int D2 = VB == 8 ? 8192 : (VB == 4 ? 16384 : 32768);
+};
+constexpr int kPermThreads = 1024;
+constexpr int kPermUnroll = 4;
+constexpr uint16_t kNoSlot = 0xFFFF;
+constexpr uint32_t kNoSource = 0xFFFFFFFFu;
+
+template <class S>
+__device__ inline S conj_bits(S v, bool conjugate) {
+  if constexpr (sizeof(S) == 8) {
+    if (conjugate) v ^= uint64_t{1} << 63;  // sign of the imaginary part (the high float)
+  }
+  return v;
+}
+
+template <class S>
+__global__ void __launch_bounds__(kPermThreads)
+    perm_tiles(const S *__restrict__ data, const uint16_t *__restrict__ slot1, int64_t nnz,
+               bool conjugate, S *__restrict__ s1) {
+  constexpr int D1 = PermSizes<sizeof(S)>::D1;
+  extern __shared__ unsigned char perm_lds[];
+  S *lds = reinterpret_cast<S *>(perm_lds);
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * D1;
+  const int len = static_cast<int>(std::min<int64_t>(D1, nnz - p0));
+  for (int j0 = threadIdx.x; j0 < len; j0 += kPermUnroll * kPermThreads) {
+    S v[kPermUnroll];
+    uint16_t sl[kPermUnroll];
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {  // clamped index: every load issued before any use
+      const int j = j0 + u * kPermThreads < len ? j0 + u * kPermThreads : j0;
+      v[u] = __builtin_nontemporal_load(data + p0 + j);
+      sl[u] = __builtin_nontemporal_load(slot1 + p0 + j);
+    }
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u)
+      if (j0 + u * kPermThreads < len && sl[u] < D1) lds[sl[u]] = conj_bits(v[u], conjugate);
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < len; j += kPermThreads) s1[p0 + j] = lds[j];
+}
+
+template <class S>
+__global__ void __launch_bounds__(kPermThreads)
+    perm_buckets(const S *__restrict__ s1, const uint32_t *__restrict__ src1,
+                 const uint16_t *__restrict__ slot2, int64_t nnz, S *__restrict__ out) {
+  constexpr int D2 = PermSizes<sizeof(S)>::D2;
+  extern __shared__ unsigned char perm_lds[];
+  S *lds = reinterpret_cast<S *>(perm_lds);
+  // each XCD takes a contiguous range of buckets: neighbouring buckets read
+  // neighbouring runs of every tile, which then share L2 lines
+  const int64_t b0 = static_cast<int64_t>(xcd_remap(blockIdx.x, gridDim.x)) * D2;
+  const int len = static_cast<int>(std::min<int64_t>(D2, nnz - b0));
+  for (int s0 = threadIdx.x; s0 < len; s0 += kPermUnroll * kPermThreads) {
+    uint32_t a[kPermUnroll];
+    uint16_t sl[kPermUnroll];
+    S v[kPermUnroll];
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const int s = s0 + u * kPermThreads < len ? s0 + u * kPermThreads : s0;
+      a[u] = __builtin_nontemporal_load(src1 + b0 + s);
+      sl[u] = __builtin_nontemporal_load(slot2 + b0 + s);
+    }
+    // an address past the array (kNoSource: a dropped entry) reads element 0
+    // and is replaced by zero, so every load is issued before any is used
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) v[u] = s1[static_cast<int64_t>(a[u]) < nnz ? a[u] : 0u];
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u)
+      if (static_cast<int64_t>(a[u]) >= nnz) v[u] = S(0);
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u)
+      if (s0 + u * kPermThreads < len && sl[u] < D2) lds[sl[u]] = v[u];
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < len; j += kPermThreads) out[b0 + j] = lds[j];
+}
+
+// Layout build.  key[i] = (bucket of i, source of i) - the source nnz for
+// a dropped entry, so it sorts last in its bucket; val[i] = i.
+__global__ void __launch_bounds__(kThreads)
+    layout_keys(const int32_t *__restrict__ t_pos, int64_t nnz, int D2, int pbits,
+                uint64_t *__restrict__ key, uint32_t *__restrict__ val) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < nnz;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t p = t_pos[i];
+    const uint64_t pv = (p >= 0 && p < nnz) ? static_cast<uint64_t>(p) : static_cast<uint64_t>(nnz);
+    key[i] = (static_cast<uint64_t>(i / D2) << pbits) | pv;
+    val[i] = static_cast<uint32_t>(i);
+  }
+}
+
+// Sorted by (bucket, source): position s of the S order.  slot2[s] = the
+// entry's offset in its bucket; then key (tile of the source; ntile for a
+// dropped entry) and value (s << 32 | source) for the stable sort by tile.
+__global__ void __launch_bounds__(kThreads)
+    layout_buckets(const uint64_t *__restrict__ key_s, const uint32_t *__restrict__ val_s,
+                   int64_t nnz, int D1, int D2, uint64_t pmask, uint32_t ntile,
+                   uint16_t *__restrict__ slot2, uint32_t *__restrict__ tkey,
+                   uint64_t *__restrict__ tval) {
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; s < nnz;
+       s += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t b0 = s / D2 * D2;
+    slot2[s] = static_cast<uint16_t>(static_cast<int64_t>(val_s[s]) - b0);
+    const uint64_t pv = key_s[s] & pmask;
+    tkey[s] = pv < static_cast<uint64_t>(nnz) ? static_cast<uint32_t>(pv / D1) : ntile;
+    tval[s] = (static_cast<uint64_t>(s) << 32) | pv;
+  }
+}
+
+// tstart[t] = first index of the tile-sorted keys with key >= t, t <= ntile.
+__global__ void __launch_bounds__(kThreads)
+    layout_tile_starts(const uint32_t *__restrict__ tkey_s, int64_t nnz, uint32_t ntile,
+                       int64_t *__restrict__ tstart) {
+  for (int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; g <= nnz;
+       g += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t prev = g == 0 ? -1 : static_cast<int64_t>(tkey_s[g - 1]);
+    const int64_t cur = g == nnz ? ntile : std::min<int64_t>(tkey_s[g], ntile);
+    for (int64_t t = prev + 1; t <= cur; ++t) tstart[t] = g;
+  }
+}
+
+// In tile order: the k-th entry of tile t (in S order) takes slot k of the
+// tile: src1[s] = t * D1 + k, slot1[source] = k.  Dropped entries get
+// kNoSource.
+__global__ void __launch_bounds__(kThreads)
+    layout_tiles(const uint32_t *__restrict__ tkey_s, const uint64_t *__restrict__ tval_s,
+                 const int64_t *__restrict__ tstart, int64_t nnz, int D1, uint32_t ntile,
+                 uint32_t *__restrict__ src1, uint16_t *__restrict__ slot1) {
+  for (int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; g < nnz;
+       g += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint32_t t = tkey_s[g];
+    const uint64_t v = tval_s[g];
+    const int64_t s = static_cast<int64_t>(v >> 32);
+    const int64_t p = static_cast<int64_t>(v & 0xFFFFFFFFu);
+    if (s >= nnz) continue;
+    if (t >= ntile || p >= nnz) {
+      src1[s] = kNoSource;
+      continue;
+    }
+    const int64_t k = g - tstart[t];
+    src1[s] = static_cast<uint32_t>(static_cast<int64_t>(t) * D1 + k);
+    slot1[p] = k < D1 ? static_cast<uint16_t>(k) : kNoSlot;
+  }
+}
+
+template <int VB>
+msx_status transpose_layout_sized(int64_t nnz, const int32_t *t_pos, uint16_t *slot1,
+                                  uint32_t *src1, uint16_t *slot2, hipStream_t stream) {
+  constexpr int D1 = PermSizes<VB>::D1, D2 = PermSizes<VB>::D2;
+  const int pbits = bits_for(static_cast<uint64_t>(nnz));
+  const int64_t nb = (nnz + D2 - 1) / D2;
+  const uint32_t ntile = static_cast<uint32_t>((nnz + D1 - 1) / D1);
+  const int key_bits = pbits + bits_for(static_cast<uint64_t>(nb));
+  const int tile_bits = bits_for(ntile);
+  const size_t n = static_cast<size_t>(nnz);
+  auto round = [](size_t b) { return (b + 255) / 256 * 256; };
+  size_t t1 = 0, t2 = 0;
+  MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t1, static_cast<uint64_t *>(nullptr),
+                                                 static_cast<uint64_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<int>(nnz), 0, key_bits, stream));
+  MSX_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t2, static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint32_t *>(nullptr),
+                                                 static_cast<uint64_t *>(nullptr),
+                                                 static_cast<uint64_t *>(nullptr),
+                                                 static_cast<int>(nnz), 0, tile_bits, stream));
+  // A, B: 8 bytes per entry; C, D: 4 bytes; then tile starts and sort temp.
+  const size_t bA = round(n * 8), bC = round(n * 4), bT = round((size_t{ntile} + 1) * 8);
+  char *work = nullptr;
+  MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&work), 2 * bA + 2 * bC + bT + std::max(t1, t2),
+                             stream));
+  char *A = work, *B = work + bA, *C = work + 2 * bA, *D = work + 2 * bA + bC;
+  auto *tstart = reinterpret_cast<int64_t *>(work + 2 * bA + 2 * bC);
+  void *tmp = work + 2 * bA + 2 * bC + bT;
+  size_t tb1 = t1, tb2 = t2;
+  hipError_t e = hipSuccess;
+  hipLaunchKernelGGL(layout_keys, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, t_pos, nnz, D2,
+                     pbits, reinterpret_cast<uint64_t *>(A), reinterpret_cast<uint32_t *>(C));
+  e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipcub::DeviceRadixSort::SortPairs(tmp, tb1, reinterpret_cast<uint64_t *>(A),
+                                           reinterpret_cast<uint64_t *>(B),
+                                           reinterpret_cast<uint32_t *>(C),
+                                           reinterpret_cast<uint32_t *>(D), static_cast<int>(nnz), 0,
+                                           key_bits, stream);
+  if (e == hipSuccess) {
+    // sorted (B, D) -> slot2, tile keys in C, tile values in A
+    hipLaunchKernelGGL(layout_buckets, dim3(grid_for(nnz)), dim3(kThreads), 0, stream,
+                       reinterpret_cast<const uint64_t *>(B), reinterpret_cast<const uint32_t *>(D),
+                       nnz, D1, D2, (uint64_t{1} << pbits) - 1, ntile, slot2,
+                       reinterpret_cast<uint32_t *>(C), reinterpret_cast<uint64_t *>(A));
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess)
+    e = hipcub::DeviceRadixSort::SortPairs(tmp, tb2, reinterpret_cast<uint32_t *>(C),
+                                           reinterpret_cast<uint32_t *>(D),
+                                           reinterpret_cast<uint64_t *>(A),
+                                           reinterpret_cast<uint64_t *>(B), static_cast<int>(nnz), 0,
+                                           tile_bits, stream);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(fill<uint16_t>, dim3(grid_for(nnz)), dim3(kThreads), 0, stream, slot1, nnz,
+                       kNoSlot);
+    hipLaunchKernelGGL(layout_tile_starts, dim3(grid_for(nnz + 1)), dim3(kThreads), 0, stream,
+                       reinterpret_cast<const uint32_t *>(D), nnz, ntile, tstart);
+    hipLaunchKernelGGL(layout_tiles, dim3(grid_for(nnz)), dim3(kThreads), 0, stream,
+                       reinterpret_cast<const uint32_t *>(D), reinterpret_cast<const uint64_t *>(B),
+                       tstart, nnz, D1, ntile, src1, slot1);
+    e = hipGetLastError();
+  }
+  msx_status st = MSX_OK;
+  if (e != hipSuccess) st = hip_fail(e, "csr_transpose_layout");
+  const hipError_t ef = hipFreeAsync(work, stream);
+  if (st == MSX_OK && ef != hipSuccess) st = hip_fail(ef, "csr_transpose_layout scratch release");
+  return st;
+}
+
+template <class S>
+msx_status transpose_permute(int64_t nnz, const void *data, const uint16_t *slot1,
+                             const uint32_t *src1, const uint16_t *slot2, bool conjugate,
+                             void *scratch, void *t_data, hipStream_t stream) {
+  constexpr int D1 = PermSizes<sizeof(S)>::D1, D2 = PermSizes<sizeof(S)>::D2;
+  // LDS beyond the default dynamic limit, set for the current device
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&perm_tiles<S>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, D1 * sizeof(S)));
+  MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&perm_buckets<S>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, D2 * sizeof(S)));
+  const int64_t ntile = (nnz + D1 - 1) / D1, nb = (nnz + D2 - 1) / D2;
+  hipLaunchKernelGGL(perm_tiles<S>, dim3(static_cast<uint32_t>(ntile)), dim3(kPermThreads),
+                     D1 * sizeof(S), stream, static_cast<const S *>(data), slot1, nnz, conjugate,
+                     static_cast<S *>(scratch));
+  MSX_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(perm_buckets<S>, dim3(static_cast<uint32_t>(nb)), dim3(kPermThreads),
+                     D2 * sizeof(S), stream, static_cast<const S *>(scratch), src1, slot2, nnz,
+                     static_cast<S *>(t_data));
+  MSX_HIP_TRY(hipGetLastError());
+  return MSX_OK;
+}
+
 msx_status check_csr(const char *op, msx_vtype vt, msx_itype it, int64_t n_rows, int64_t n_cols,
                      int64_t nnz, const void *indices, const void *indptr) {
   if (!valid_itype(it)) return fail(MSX_ETYPE, std::string(op) + " requires int32 or int64 indices.");
@@ -778,6 +1040,49 @@ extern "C" msx_status msx_csr_transpose_values(msx_vtype vt, int64_t nnz, const 
   }
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
+}
+
+extern "C" msx_status msx_csr_transpose_layout(msx_vtype vt, int64_t nnz, const int32_t *t_pos,
+                                               uint16_t *slot1, uint32_t *src1, uint16_t *slot2,
+                                               void *stream) {
+  clear_error();
+  if (!valid_vtype(vt)) return fail(MSX_ETYPE, "csr_transpose_layout unsupported value dtype.");
+  if (nnz < 0 || nnz >= kIntMax)
+    return fail(MSX_EINVAL, "csr_transpose_layout supports 0 to 2^31 - 2 stored values.");
+  if (nnz > 0 && (t_pos == nullptr || slot1 == nullptr || src1 == nullptr || slot2 == nullptr))
+    return fail(MSX_EINVAL, "csr_transpose_layout buffers must be non-NULL.");
+  if (nnz == 0) return MSX_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  switch (value_bytes(vt)) {
+  case 2: return transpose_layout_sized<2>(nnz, t_pos, slot1, src1, slot2, s);
+  case 4: return transpose_layout_sized<4>(nnz, t_pos, slot1, src1, slot2, s);
+  default: return transpose_layout_sized<8>(nnz, t_pos, slot1, src1, slot2, s);
+  }
+}
+
+extern "C" msx_status msx_csr_transpose_values_layout(msx_vtype vt, int64_t nnz, const void *data,
+                                                      const uint16_t *slot1, const uint32_t *src1,
+                                                      const uint16_t *slot2, int conjugate,
+                                                      void *scratch, void *t_data, void *stream) {
+  clear_error();
+  if (!valid_vtype(vt))
+    return fail(MSX_ETYPE, "csr_transpose_values_layout unsupported value dtype.");
+  if (nnz < 0 || nnz >= kIntMax)
+    return fail(MSX_EINVAL, "csr_transpose_values_layout supports 0 to 2^31 - 2 stored values.");
+  if (nnz > 0 && (data == nullptr || slot1 == nullptr || src1 == nullptr || slot2 == nullptr ||
+                  scratch == nullptr || t_data == nullptr))
+    return fail(MSX_EINVAL, "csr_transpose_values_layout buffers must be non-NULL.");
+  if (nnz == 0) return MSX_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  const bool conj = conjugate != 0 && vt == MSX_C64;
+  switch (value_bytes(vt)) {
+  case 2:
+    return transpose_permute<uint16_t>(nnz, data, slot1, src1, slot2, false, scratch, t_data, s);
+  case 4:
+    return transpose_permute<uint32_t>(nnz, data, slot1, src1, slot2, false, scratch, t_data, s);
+  default:
+    return transpose_permute<uint64_t>(nnz, data, slot1, src1, slot2, conj, scratch, t_data, s);
+  }
 }
 
 extern "C" msx_status msx_csr_spmv_transpose(msx_vtype vt, msx_itype it, int64_t n_rows,

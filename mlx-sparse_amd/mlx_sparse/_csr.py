@@ -188,8 +188,9 @@ class CSRArray:
         """CSR of the transpose (of the conjugate transpose with
         ``conjugate``), computed on ``device``.  Cached while this array is
         unchanged; after new values, the cached transpose's values are
-        regathered on the GPU through the stored position of each of its
-        entries (computed on the first such update), as a new array."""
+        regathered on the GPU in two streaming passes through a layout
+        computed, on the first such update, from the stored position of each
+        of its entries (8 bytes per value), as a new array."""
         from mlx_sparse import _native
 
         device = torch.device(device)
@@ -198,16 +199,19 @@ class CSRArray:
         now = self._stamps()
         hit = self._cache.get(key)
         if hit is not None:
-            built, T, pos = hit
+            built, T, layout = hit
             if built == now:
                 return T
             if built[1:] == now[1:] and data.device.type == "cuda":
-                if pos is None:
+                if layout is None:
                     pos = _native.csr_transpose_positions(indices, indptr, self.shape)[0]
+                    layout = _native.csr_transpose_layout(pos, T.data)
+                    del pos
                 t_data = torch.empty_like(T.data)
-                _native.csr_transpose_values(data.detach(), pos, conjugate, t_data)
+                scratch = torch.empty_like(T.data)
+                _native.csr_transpose_values_layout(data.detach(), layout, conjugate, scratch, t_data)
                 T = T._with_values(t_data)
-                self._cache[key] = (now, T, pos)
+                self._cache[key] = (now, T, layout)
                 return T
         src = data.detach()
         if conjugate:

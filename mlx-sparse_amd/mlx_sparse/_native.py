@@ -50,6 +50,19 @@ def csr_transpose_values(data, positions, conjugate: bool, out) -> None:
     extension().csr_transpose_values(data, positions, conjugate, out)
 
 
+def csr_transpose_layout(positions, like):
+    """(slot1, src1, slot2): the layout of the two-pass regather of a
+    transpose's values (dtype of ``like``), from its positions."""
+    return tuple(extension().csr_transpose_layout(positions, like))
+
+
+def csr_transpose_values_layout(data, layout, conjugate: bool, scratch, out) -> None:
+    """``out`` = the regathered values through ``layout`` (``scratch``: as
+    many values as ``data``, overwritten)."""
+    slot1, src1, slot2 = layout
+    extension().csr_transpose_values_layout(data, slot1, src1, slot2, conjugate, scratch, out)
+
+
 def csr_matvec_transpose(data, indices, indptr, x, shape: Shape2D) -> torch.Tensor:
     """A^T x, without conjugation (reference: mlx_sparse/_native.py:260-270)."""
     return extension().csr_matvec_transpose(data, indices, indptr, x, shape[0], shape[1])

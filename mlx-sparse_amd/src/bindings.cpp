@@ -362,6 +362,71 @@ void csr_transpose_values(py::handle data_o, py::handle pos_o, bool conjugate, p
   msx::check_status(st, "csr_transpose_values");
 }
 
+// (slot1 int16, src1 int32, slot2 int16): the layout of the two-pass
+// regather of values of `like`'s dtype, from the transpose positions.
+py::tuple csr_transpose_layout(py::handle pos_o, py::handle like_o) {
+  py::object pos = contiguous(pos_o);
+  const ArrayView vpos = view_of(pos), vl = view_of(like_o);
+  msx::require_rank(vpos, 1, "csr_transpose_layout positions");
+  if (vpos.dtype != DType::Int32) throw std::invalid_argument("csr_transpose_layout positions must be int32.");
+  if (vpos.device < 0) throw std::invalid_argument("csr_transpose_layout needs GPU tensors.");
+  const int64_t n = vpos.shape[0];
+  py::dict k16, k32;
+  k16["dtype"] = torch().attr("int16");
+  k16["device"] = pos.attr("device");
+  k32["dtype"] = torch().attr("int32");
+  k32["device"] = pos.attr("device");
+  py::object slot1 = torch().attr("empty")(py::make_tuple(n), **k16);
+  py::object src1 = torch().attr("empty")(py::make_tuple(n), **k32);
+  py::object slot2 = torch().attr("empty")(py::make_tuple(n), **k16);
+  const ArrayView v1 = view_of(slot1), vs = view_of(src1), v2 = view_of(slot2);
+  void *stream = stream_for(vpos.device);
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_transpose_layout(msx::to_vtype(vl.dtype), n, static_cast<const int32_t *>(vpos.ptr),
+                                  static_cast<uint16_t *>(v1.ptr), static_cast<uint32_t *>(vs.ptr),
+                                  static_cast<uint16_t *>(v2.ptr), stream);
+  }
+  msx::check_status(st, "csr_transpose_layout");
+  return py::make_tuple(slot1, src1, slot2);
+}
+
+// out = data regathered through a layout of csr_transpose_layout; scratch:
+// as many values as data (overwritten).
+void csr_transpose_values_layout(py::handle data_o, py::handle slot1_o, py::handle src1_o,
+                                 py::handle slot2_o, bool conjugate, py::handle scratch_o,
+                                 py::handle out_o) {
+  py::object data = contiguous(data_o), slot1 = contiguous(slot1_o), src1 = contiguous(src1_o),
+             slot2 = contiguous(slot2_o);
+  const ArrayView vd = view_of(data), v1 = view_of(slot1), vs = view_of(src1), v2 = view_of(slot2),
+                  vsc = view_of(scratch_o), vo = view_of(out_o);
+  const char *op = "csr_transpose_values_layout";
+  msx::require_rank(vd, 1, "csr_transpose_values_layout data");
+  msx::require_same_value_dtype(vd, vo, "csr_transpose_values_layout data",
+                                "csr_transpose_values_layout out");
+  msx::require_same_value_dtype(vd, vsc, "csr_transpose_values_layout data",
+                                "csr_transpose_values_layout scratch");
+  if (v1.dtype_name != "int16" || v2.dtype_name != "int16" || vs.dtype != DType::Int32)
+    throw std::invalid_argument("csr_transpose_values_layout layout must be (int16, int32, int16).");
+  for (const ArrayView *v : {&v1, &vs, &v2, &vsc, &vo})
+    msx::require_size(*v, vd.shape[0], "csr_transpose_values_layout operand");
+  msx::require_contiguous(vsc, "csr_transpose_values_layout scratch");
+  msx::require_contiguous(vo, "csr_transpose_values_layout out");
+  msx::require_same_device({&vd, &v1, &vs, &v2, &vsc, &vo}, op);
+  if (vd.device < 0) throw std::invalid_argument("csr_transpose_values_layout needs GPU tensors.");
+  void *stream = stream_for(vd.device);
+  msx_status st;
+  {
+    py::gil_scoped_release nogil;
+    st = msx_csr_transpose_values_layout(
+        msx::to_vtype(vd.dtype), vd.shape[0], vd.ptr, static_cast<const uint16_t *>(v1.ptr),
+        static_cast<const uint32_t *>(vs.ptr), static_cast<const uint16_t *>(v2.ptr),
+        conjugate ? 1 : 0, vsc.ptr, vo.ptr, stream);
+  }
+  msx::check_status(st, op);
+}
+
 py::object csr_matvec_transpose(py::handle data_o, py::handle indices_o, py::handle indptr_o,
                                 py::handle x_o, int64_t n_rows, int64_t n_cols, int n_threads) {
   py::object data = contiguous(data_o), indices = contiguous(indices_o),
@@ -669,6 +734,12 @@ PYBIND11_MODULE(_ext, m) {
   m.def("csr_transpose_values", &csr_transpose_values, py::arg("data"), py::arg("positions"),
         py::arg("conjugate"), py::arg("out"),
         "out[i] = data[positions[i]] (conjugated on request), in place.");
+  m.def("csr_transpose_layout", &csr_transpose_layout, py::arg("positions"), py::arg("like"),
+        "(slot1, src1, slot2): layout of the two-pass regather of values of like's dtype.");
+  m.def("csr_transpose_values_layout", &csr_transpose_values_layout, py::arg("data"),
+        py::arg("slot1"), py::arg("src1"), py::arg("slot2"), py::arg("conjugate"),
+        py::arg("scratch"), py::arg("out"),
+        "out = data regathered through a csr_transpose_layout layout, in place.");
   m.def("csr_matvec_transpose", &csr_matvec_transpose, py::arg("data"), py::arg("indices"),
         py::arg("indptr"), py::arg("x"), py::arg("n_rows"), py::arg("n_cols"),
         py::arg("n_threads") = 0, "A^T x for CSR buffers of shape (n_rows, n_cols).");

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_plan_refresh.argtypes = [vp, vp, vp]
         L.msx_csr_transpose_positions.argtypes = [ci, i64, i64, i64, vp, vp, vp, vp, vp, vp]
         L.msx_csr_transpose_values.argtypes = [ci, i64, vp, vp, ci, vp, vp]
+        L.msx_csr_transpose_layout.argtypes = [ci, i64, vp, vp, vp, vp, vp]
+        L.msx_csr_transpose_values_layout.argtypes = [ci, i64, vp, vp, vp, vp, ci, vp, vp, vp]
         L.msx_csr_plan_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
         L.msx_csr_plan_export.argtypes = [vp, vp, vp, vp]
         L.msx_csr_plan_export_panels.argtypes = [vp, vp, vp, vp]
@@ -114,6 +116,7 @@ def lib() -> ctypes.CDLL:
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
                      "msx_csr_plan_destroy", "msx_csr_plan_refresh",
                      "msx_csr_transpose_positions", "msx_csr_transpose_values",
+                     "msx_csr_transpose_layout", "msx_csr_transpose_values_layout",
                      "msx_csr_plan_info", "msx_csr_plan_export", "msx_csr_plan_export_panels",
                      "msx_csr_spmv", "msx_csr_spmm", "msx_csr_batched_spmv",
                      "msx_csr_batched_spmm", "msx_csr_batched_spmv_cpu",
@@ -298,6 +301,27 @@ def transpose_values(data, pos, out, conjugate=False):
     _check(lib().msx_csr_transpose_values(VT[data.dtype], data.numel(), _p(data), _p(pos),
                                           1 if conjugate else 0, _p(out), _stream()),
            "msx_csr_transpose_values")
+    return out
+
+
+def transpose_layout(pos, vtype):
+    """(slot1, src1, slot2) of the two-pass regather of values of dtype `vtype`."""
+    nnz = pos.numel()
+    slot1 = torch.empty(nnz, dtype=torch.int16, device=pos.device)
+    src1 = torch.empty(nnz, dtype=torch.int32, device=pos.device)
+    slot2 = torch.empty(nnz, dtype=torch.int16, device=pos.device)
+    _check(lib().msx_csr_transpose_layout(VT[vtype], nnz, _p(pos), _p(slot1), _p(src1), _p(slot2),
+                                          _stream()), "msx_csr_transpose_layout")
+    return slot1, src1, slot2
+
+
+def transpose_values_layout(data, layout, out, conjugate=False, scratch=None):
+    slot1, src1, slot2 = layout
+    scratch = torch.empty_like(data) if scratch is None else scratch
+    _check(lib().msx_csr_transpose_values_layout(VT[data.dtype], data.numel(), _p(data), _p(slot1),
+                                                 _p(src1), _p(slot2), 1 if conjugate else 0,
+                                                 _p(scratch), _p(out), _stream()),
+           "msx_csr_transpose_values_layout")
     return out
 
 

@@ -22,7 +22,7 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _capi.lib().msx_abi_version() == 6
+    assert _capi.lib().msx_abi_version() == 7
 
 
 def _f32(a):
@@ -91,3 +91,22 @@ def test_cpu_ranges_entry_point():
     ranges = out[: 2 * n.value].reshape(-1, 2)
     assert ranges[0, 0] == 0 and ranges[-1, 1] == 6
     assert np.all(ranges[1:, 0] == ranges[:-1, 1])
+
+
+def test_transpose_layout_argument_errors():
+    """The two-pass regather's entry points check their arguments before any
+    HIP call: value type, nnz range, NULL buffers; nnz = 0 is a no-op."""
+    L = _capi.lib()
+    d = ctypes.c_void_p(16)
+    assert L.msx_csr_transpose_layout(9, 10, d, d, d, d, None) == _capi.ETYPE
+    assert L.msx_csr_transpose_layout(0, -1, d, d, d, d, None) == _capi.EINVAL
+    assert L.msx_csr_transpose_layout(0, 1 << 31, d, d, d, d, None) == _capi.EINVAL
+    assert L.msx_csr_transpose_layout(0, 10, None, d, d, d, None) == _capi.EINVAL
+    assert L.msx_csr_transpose_layout(0, 10, d, d, None, d, None) == _capi.EINVAL
+    assert L.msx_csr_transpose_layout(0, 0, None, None, None, None, None) == _capi.OK
+    f = L.msx_csr_transpose_values_layout
+    assert f(9, 10, d, d, d, d, 0, d, d, None) == _capi.ETYPE
+    assert f(0, -1, d, d, d, d, 0, d, d, None) == _capi.EINVAL
+    assert f(0, 10, d, d, d, d, 0, None, d, None) == _capi.EINVAL
+    assert f(3, 10, d, d, d, d, 1, d, None, None) == _capi.EINVAL
+    assert f(0, 0, None, None, None, None, 0, None, None, None) == _capi.OK

@@ -156,6 +156,90 @@ def test_transpose_positions_and_values(vtype):
         assert not to_numpy(out)[kept:].any()
 
 
+# tile and bucket sizes of the two-pass regather, by value width
+LAYOUT_SIZES = {2: (32768, 32768), 4: (32768, 16384), 8: (16384, 8192)}
+
+
+def _check_layout(layout, pos, width):
+    """The layout composes to the permutation: S position s (bucket s // D2)
+    reads the slot src1[s] of tile src1[s] // D1, which holds the source p
+    with slot1[p] == src1[s] % D1, and lands at bucket offset slot2[s] -
+    so the destination (s // D2) * D2 + slot2[s] must list p in pos.  Also:
+    every bucket's slot2 is a permutation of its offsets, a tile's slots
+    are 0..count-1, and dropped entries (pos -1) read nothing."""
+    D1, D2 = LAYOUT_SIZES[width]
+    slot1 = to_numpy(layout[0]).view(np.uint16).astype(np.int64)
+    src1 = to_numpy(layout[1]).view(np.uint32).astype(np.int64)
+    slot2 = to_numpy(layout[2]).view(np.uint16).astype(np.int64)
+    p = to_numpy(pos).astype(np.int64)
+    n = p.size
+    for b0 in range(0, n, D2):
+        seg = slot2[b0:b0 + D2]
+        assert np.array_equal(np.sort(seg), np.arange(seg.size)), b0
+    used = slot1 != 0xFFFF
+    assert np.array_equal(np.sort(np.flatnonzero(used)), np.sort(p[p >= 0]))
+    addr = (np.flatnonzero(used) // D1) * D1 + slot1[used]
+    for t0 in range(0, n, D1):
+        k = slot1[t0:t0 + D1][used[t0:t0 + D1]]
+        assert np.array_equal(np.sort(k), np.arange(k.size)), t0
+    source_at = np.full(n, -1, np.int64)
+    source_at[addr] = np.flatnonzero(used)
+    valid = src1 != 0xFFFFFFFF
+    assert int((~valid).sum()) == int((p < 0).sum())
+    s = np.flatnonzero(valid)
+    dest = (s // D2) * D2 + slot2[s]
+    np.testing.assert_array_equal(p[dest], source_at[src1[s]])
+    assert np.all(p[(np.flatnonzero(~valid) // D2) * D2 + slot2[~valid]] < 0)
+
+
+def _bits(t, vtype):
+    a = to_numpy(t)
+    return a.view(np.float32).view(np.uint32) if vtype == "complex64" else a.view(
+        np.uint16 if a.dtype.itemsize == 2 else np.uint32)
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("n_rows,n_cols,max_len",
+                         [(300, 200, 9), (9000, 7000, 30), (40000, 31000, 12),
+                          (200000, 150000, 21)])
+def test_transpose_layout_regather(vtype, n_rows, n_cols, max_len):
+    """msx_csr_transpose_values_layout (two streaming passes through the
+    layout of msx_csr_transpose_layout) writes exactly what the one-pass
+    gather msx_csr_transpose_values writes - the oracle's transpose for the
+    kept entries, zero bits for the dropped ones, conjugated on request -
+    below one tile and across many tiles and buckets with ragged ends, on
+    two calls in a row that share the scratch (new values the second time)."""
+    rng = np.random.default_rng(n_rows + max_len)
+    indices, indptr, _ = _random_csr(rng, n_rows, n_cols, max_len)
+    indices[3] = n_cols + 1  # dropped from the transpose
+    indices[-1] = -4
+    nnz = int(indptr[-1])
+    i, p = to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    pos, ti, tp = _capi.transpose_positions(i, p, n_rows, n_cols)
+    kept = int(tp[-1].item())
+    assert kept == nnz - 2
+    width = {"float32": 4, "float16": 2, "bfloat16": 2, "complex64": 8}[vtype]
+    layout = _capi.transpose_layout(pos, TORCH[vtype])
+    if nnz <= 300000:
+        _check_layout(layout, pos, width)
+    scratch = torch.empty(nnz, dtype=TORCH[vtype], device=DEV)
+    for trial in range(2):
+        data = _values(rng, nnz, vtype)
+        d = to_torch(data, vtype, DEV)
+        want = torch.full_like(d, 7.0)
+        _capi.transpose_values(d, pos, want)
+        got = torch.full_like(d, 3.0)
+        _capi.transpose_values_layout(d, layout, got, scratch=scratch)
+        np.testing.assert_array_equal(_bits(got, vtype), _bits(want, vtype), err_msg=f"trial {trial}")
+        ot, _, _ = orc.csr_transpose(data, indices, indptr, n_rows, n_cols, vtype=vtype)
+        np.testing.assert_array_equal(to_numpy(got[:kept]), ot)
+        assert not to_numpy(got)[kept:].any()
+        if vtype == "complex64":
+            _capi.transpose_values_layout(d, layout, got, conjugate=True, scratch=scratch)
+            np.testing.assert_array_equal(to_numpy(got[:kept]), np.conj(ot))
+            assert not to_numpy(got)[kept:].any()
+
+
 def test_refreshed_transpose_equals_a_fresh_one(gpu):
     """A matrix with an out-of-range column: after an in-place update of
     A.data, the cached A.T (values regathered through stored positions)
