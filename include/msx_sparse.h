@@ -581,6 +581,30 @@ msx_status msx_csr_bicgstab(msx_itype it, int64_t n, int64_t nnz,
                             void *stream);
 
 /*
+ * BiCGSTAB with the Jacobi preconditioner M = diag(inv_diag) (inv_diag: n
+ * device floats): msx_csr_bicgstab's device loop with x advanced along
+ * p_hat = M p and s_hat = M s, which the SpMVs take.  The reference's
+ * preconditioned loop differs from the plain one in its edge cases, kept
+ * here: ||b|| is rounded to float before its square root; non-finite b or
+ * x0, or a non-finite true residual, ends the solve with -3 and the
+ * reported residual left as it was (infinity before the first iteration);
+ * the reported residual follows ||s|| after the s update.
+ *
+ * Replaces CSRBiCGSTABJacobi::eval_gpu (reference:
+ * src/preconditioners/bicgstab/bicgstab.cpp:548-598, a single-threadgroup
+ * kernel of bicgstab.metal) with the arithmetic of
+ * left_preconditioned_bicgstab_host (bicgstab.cpp:140-421) and the Jacobi
+ * apply of csr_bicgstab_jacobi_cpu_impl (bicgstab.cpp:425-521).
+ */
+msx_status msx_csr_bicgstab_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                   const float *data, const void *indices,
+                                   const void *indptr, const float *b,
+                                   const float *x0, const float *inv_diag,
+                                   float *x, float rtol, float atol,
+                                   int64_t maxiter, const msx_csr_plan *plan,
+                                   msx_solver_result *result, void *stream);
+
+/*
  * MINRES for (A - shift I) x = b with A square symmetric (possibly
  * indefinite) float32 CSR: x from x0 (device pointers).  Per iteration two
  * SpMVs (A v for the Lanczos step, A x for the true residual the reference
@@ -645,14 +669,21 @@ msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
                                   const float *x0, const float *inv_diag,
                                   float *x, float rtol, float atol,
                                   int64_t maxiter, msx_solver_result *result);
-/* csr_bicgstab_cpu_impl (bicgstab.cpp:80-362) and csr_minres_cpu_impl
- * (minres.cpp:93-312), one thread. */
+/* csr_bicgstab_cpu_impl (bicgstab.cpp:80-362), csr_bicgstab_jacobi_cpu_impl
+ * (src/preconditioners/bicgstab/bicgstab.cpp:140-521) and
+ * csr_minres_cpu_impl (minres.cpp:93-312), one thread. */
 msx_status msx_csr_bicgstab_cpu(msx_itype it, int64_t n, int64_t nnz,
                                 const float *data, const void *indices,
                                 const void *indptr, const float *b,
                                 const float *x0, float *x, float rtol,
                                 float atol, int64_t maxiter,
                                 msx_solver_result *result);
+msx_status msx_csr_bicgstab_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                       const float *data, const void *indices,
+                                       const void *indptr, const float *b,
+                                       const float *x0, const float *inv_diag,
+                                       float *x, float rtol, float atol,
+                                       int64_t maxiter, msx_solver_result *result);
 msx_status msx_csr_minres_cpu(msx_itype it, int64_t n, int64_t nnz,
                               const float *data, const void *indices,
                               const void *indptr, const float *b,

@@ -106,14 +106,18 @@ __global__ void __launch_bounds__(kSolverThreads)
   write_partials(v, part);
 }
 
-// bicgstab.cpp:123-167.
+// bicgstab.cpp:123-167.  J (the Jacobi loop, preconditioners/bicgstab/
+// bicgstab.cpp:150-200): ||b|| rounded to float before its square root, and
+// a failed start reports an infinite residual.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_decide_start(const double *part, int nparts, float rtol, float atol, int64_t maxiter,
                     BiState *st) {
   double t[kSlots];
   read_totals(part, nparts, t);
   if (threadIdx.x != 0) return;
-  const float b_norm = static_cast<float>(sqrt(max0(t[0])));
+  const float b_norm = J ? sqrtf(max0(static_cast<float>(t[0])))
+                         : static_cast<float>(sqrt(max0(t[0])));
   const float scaled = rtol * b_norm;
   st->tol = atol > scaled ? atol : scaled;
   st->residual = static_cast<float>(sqrt(max0(t[2])));
@@ -124,6 +128,7 @@ __global__ void __launch_bounds__(kSolverThreads)
   st->pause_it = 0;
   st->completed = 0;
   if (t[1] != 0.0 || !fin(b_norm) || !fin(st->tol) || !fin(t[2]) || !fin(st->residual)) {
+    if (J) st->residual = INFINITY;
     bi_stop(st, -3, 0);
   } else if (st->residual <= st->tol) {
     bi_stop(st, 0, 0);
@@ -167,17 +172,22 @@ __device__ inline bool bi_close(const double (&t)[kSlots], int32_t k, BiState *s
 
 // Iteration k's first pass (bicgstab.cpp:180-230).  `dots`: slots 2 and 3
 // are r_hat.r and r.r; with `close_prev`, slots 0 and 1 close iteration
-// k - 1 first.
+// k - 1 first.  J: also p_hat = inv_diag p (its non-finite entries counted
+// with p's).
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_p(const float *__restrict__ r, float *__restrict__ p, const float *__restrict__ v,
-         int64_t n, int32_t k, int close_prev, const double *dots, double *part, int nparts,
-         BiState *st) {
+         const float *__restrict__ inv_diag, float *__restrict__ p_hat, int64_t n, int32_t k,
+         int close_prev, const double *dots, double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  constexpr int NV = J ? 4 : 3;
   double pin[kSlots];
   load_partials(dots, nparts, pin);
-  const float *const vec[3] = {r, p, v};
-  Round<3> first;
-  load_round<3>(vec, first_base(), n, first);
+  const float *vec[NV];
+  vec[0] = r, vec[1] = p, vec[2] = v;
+  if constexpr (J) vec[3] = inv_diag;
+  Round<NV> first;
+  load_round<NV>(vec, first_base(), n, first);
   double t[kSlots];
   reduce_partials(pin, nparts, t);
   if (close_prev && !bi_close(t, k - 1, st)) return;
@@ -200,15 +210,27 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  // J: p_hat = inv_diag p in float (the Jacobi apply, bicgstab.cpp:500-507)
+  auto hat = [&](int64_t i, float pf, const float(&e)[NV]) {
+    if constexpr (J) {
+      const float ph = e[NV - 1] * pf;
+      p_hat[i] = ph;
+      if (!fin(ph)) acc[1] += 1.0;
+    }
+  };
   if (k == 1) {
-    for_rounds<3>(vec, n, first, [&](int64_t i, const float(&e)[3]) { p[i] = e[0]; });
+    for_rounds<NV>(vec, n, first, [&](int64_t i, const float(&e)[NV]) {
+      p[i] = e[0];
+      hat(i, e[0], e);
+    });
   } else {
-    for_rounds<3>(vec, n, first, [&](int64_t i, const float(&e)[3]) {
+    for_rounds<NV>(vec, n, first, [&](int64_t i, const float(&e)[NV]) {
       const double pi = static_cast<double>(e[0]) +
                         beta * (static_cast<double>(e[1]) - omega * static_cast<double>(e[2]));
       const float pf = static_cast<float>(pi);
       p[i] = pf;
       if (!fin(pi) || !fin(pf)) acc[1] += 1.0;
+      hat(i, pf, e);
     });
   }
   write_partials(acc, part);
@@ -241,17 +263,23 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // alpha (bicgstab.cpp:232-255); s = r - alpha v, x += alpha p; s.s of the
-// unrounded s, non-finite count.
+// unrounded s, non-finite count.  J: `p` is p_hat, and s_hat = inv_diag s
+// is written too (slot 2: its non-finite count).
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_s(const float *__restrict__ r, const float *__restrict__ v, const float *__restrict__ p,
-         float *__restrict__ x, float *__restrict__ s, int64_t n, int32_t k, const double *v_part,
-         double *part, int nparts, BiState *st) {
+         const float *__restrict__ inv_diag, float *__restrict__ x, float *__restrict__ s,
+         float *__restrict__ s_hat, int64_t n, int32_t k, const double *v_part, double *part,
+         int nparts, BiState *st) {
   if (!st->running) return;
+  constexpr int NV = J ? 5 : 4;
   double pin[kSlots];
   load_partials(v_part, nparts, pin);
-  const float *const vec[4] = {r, v, x, p};
-  Round<4> first;
-  load_round<4>(vec, first_base(), n, first);
+  const float *vec[NV];
+  vec[0] = r, vec[1] = v, vec[2] = x, vec[3] = p;
+  if constexpr (J) vec[4] = inv_diag;
+  Round<NV> first;
+  load_round<NV>(vec, first_base(), n, first);
   double t[kSlots];
   reduce_partials(pin, nparts, t);
   const double hv = t[0], vv = t[1];
@@ -268,7 +296,7 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
+  for_rounds<NV>(vec, n, first, [&](int64_t i, const float(&e)[NV]) {
     const double si = static_cast<double>(e[0]) - alpha * static_cast<double>(e[1]);
     const double xi = static_cast<double>(e[2]) + alpha * static_cast<double>(e[3]);
     const float sf = static_cast<float>(si), xf = static_cast<float>(xi);
@@ -276,6 +304,11 @@ __global__ void __launch_bounds__(kSolverThreads)
     x[i] = xf;
     acc[0] += si * si;
     if (!(fin(si) && fin(xi) && fin(sf) && fin(xf))) acc[1] += 1.0;
+    if constexpr (J) {
+      const float sh = e[NV - 1] * sf;
+      s_hat[i] = sh;
+      if (!fin(sh)) acc[2] += 1.0;
+    }
   });
   write_partials(acc, part);
   if (lead()) {
@@ -285,20 +318,24 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // The s-check (bicgstab.cpp:270-287; skipped when the host has already
-// run it), then t.s and t.t.
+// run it), then t.s and t.t.  J: the reported residual becomes ||s||
+// (preconditioners/bicgstab/bicgstab.cpp:314), and a non-finite s_hat ends
+// the solve after the check.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_t(const float *__restrict__ s, const float *__restrict__ t_vec, int64_t n, int32_t k,
          int check, const double *s_part, double *part, int nparts, BiState *st) {
   if (!st->running) return;
   double pin[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  if (check) load_partials(s_part, nparts, pin);
+  if (check || J) load_partials(s_part, nparts, pin);
   const float *const vec[2] = {s, t_vec};
   Round<2> first;
   load_round<2>(vec, first_base(), n, first);
+  double t[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  if (check || J) reduce_partials(pin, nparts, t);
   if (check) {
-    double t[kSlots];
-    reduce_partials(pin, nparts, t);
     const float s_norm = static_cast<float>(sqrt(max0(t[0])));
+    if (J && lead()) st->residual = s_norm;
     if (t[1] != 0.0 || !fin(t[0]) || !fin(s_norm)) {
       if (lead()) bi_stop(st, -3, k);
       return;
@@ -312,6 +349,10 @@ __global__ void __launch_bounds__(kSolverThreads)
       return;
     }
   }
+  if (J && t[2] != 0.0) {
+    if (lead()) bi_stop(st, -3, k);
+    return;
+  }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
   for_rounds<2>(vec, n, first, [&](int64_t, const float(&e)[2]) {
     const double ti = e[1];
@@ -323,17 +364,23 @@ __global__ void __launch_bounds__(kSolverThreads)
 
 // omega (bicgstab.cpp:290-305); x += omega s, r = s - omega t.  Slots: r.r
 // of the unrounded r, non-finite count, r_hat.r and r.r of the stored r
-// (the next iteration's rho and r.r).
+// (the next iteration's rho and r.r).  J: x += omega s_hat.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
-    bi_r(const float *__restrict__ s, const float *__restrict__ t_vec, float *__restrict__ x,
-         float *__restrict__ r, const float *__restrict__ r_hat, int64_t n, int32_t k,
-         const double *t_part, double *part, int nparts, BiState *st) {
+    bi_r(const float *__restrict__ s, const float *__restrict__ t_vec,
+         const float *__restrict__ s_hat, float *__restrict__ x, float *__restrict__ r,
+         const float *__restrict__ r_hat, int64_t n, int32_t k, const double *t_part,
+         double *part, int nparts, BiState *st) {
   if (!st->running) return;
+  constexpr int NV = J ? 5 : 4;
   double pin[kSlots];
   load_partials(t_part, nparts, pin);
-  const float *const vec[4] = {x, s, t_vec, r_hat};
-  Round<4> first;
-  load_round<4>(vec, first_base(), n, first);
+  const float *vec[NV];
+  vec[0] = x, vec[1] = s, vec[2] = t_vec, vec[3] = r_hat;
+  if constexpr (J) vec[4] = s_hat;
+  constexpr int kStep = J ? 4 : 1;  // x advances along s_hat (J) or s
+  Round<NV> first;
+  load_round<NV>(vec, first_base(), n, first);
   double t[kSlots];
   reduce_partials(pin, nparts, t);
   const double ts = t[0], tt = t[1];
@@ -350,8 +397,8 @@ __global__ void __launch_bounds__(kSolverThreads)
     return;
   }
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  for_rounds<4>(vec, n, first, [&](int64_t i, const float(&e)[4]) {
-    const double xi = static_cast<double>(e[0]) + omega * static_cast<double>(e[1]);
+  for_rounds<NV>(vec, n, first, [&](int64_t i, const float(&e)[NV]) {
+    const double xi = static_cast<double>(e[0]) + omega * static_cast<double>(e[kStep]);
     const double ri = static_cast<double>(e[1]) - omega * static_cast<double>(e[2]);
     const float xf = static_cast<float>(xi), rf = static_cast<float>(ri);
     x[i] = xf;
@@ -379,7 +426,9 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // dst = b - A x (A x in ax).  Slots: dst.dst, non-finite count, r_hat.dst,
-// dst.dst - the layout bi_p reads when the loop resumes with dst as r.
+// dst.dst - the layout bi_p reads when the loop resumes with dst as r.  J
+// counts the entries of A x and dst only (bicgstab.cpp:166-192 there).
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_resid(const float *__restrict__ b, const float *__restrict__ ax, const float *__restrict__ x,
              const float *__restrict__ r_hat, float *__restrict__ dst, int64_t n, double *part) {
@@ -389,7 +438,7 @@ __global__ void __launch_bounds__(kSolverThreads)
     const float ri = b[i] - a;
     dst[i] = ri;
     acc[0] += static_cast<double>(ri) * static_cast<double>(ri);
-    if (!(fin(ri) && fin(a) && fin(x[i]))) acc[1] += 1.0;
+    if (!(fin(ri) && fin(a) && (J || fin(x[i])))) acc[1] += 1.0;
     acc[2] += static_cast<double>(r_hat[i]) * static_cast<double>(ri);
   })
   acc[3] = acc[0];
@@ -399,6 +448,9 @@ __global__ void __launch_bounds__(kSolverThreads)
 // The host-driven true-residual checks (bicgstab.cpp:274-287, 319-332,
 // 340-350): kind kSCheck / kRCheck resume the loop (running = 1) when the
 // true residual is above the tolerance; kind 3 is the check after the loop.
+// J: a failed evaluation (the reference's exception) leaves the reported
+// residual as it was.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     bi_check(const double *part, int nparts, int32_t kind, BiState *st) {
   double t[kSlots];
@@ -409,13 +461,13 @@ __global__ void __launch_bounds__(kSolverThreads)
   const int32_t k = st->pause_it;
   st->pause = kNoPause;
   if (kind == 3) {
-    st->residual = norm;
+    if (!J || finite) st->residual = norm;
     if (!finite) st->status = -3;
     else if (norm <= st->tol) st->status = 0;
     return;
   }
   if (!finite) {
-    st->residual = norm;
+    if (!J) st->residual = norm;
     bi_stop(st, -3, k);
   } else if (norm <= st->tol) {
     st->residual = norm;
@@ -769,15 +821,20 @@ msx_status read_state(const System &s, const State *dev, State *host) {
   return MSX_OK;
 }
 
-msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, float rtol,
-                    float atol, int64_t maxiter, msx_solver_result *result) {
+// J: the Jacobi loop, inv_diag non-null (p_hat and s_hat in two more
+// vectors; the SpMVs take them).
+template <bool J>
+msx_status bicgstab(const System &s, const float *b, const float *x0, const float *inv_diag,
+                    float *x, float rtol, float atol, int64_t maxiter,
+                    msx_solver_result *result) {
   const int64_t n = s.n;
   Scratch sc;
   sc.stream = s.stream;
-  msx_status e = sc.alloc(n, 7, 7);
+  msx_status e = sc.alloc(n, J ? 9 : 7, 7);
   if (e != MSX_OK) return e;
   float *r = sc.vector(0), *r_hat = sc.vector(1), *p = sc.vector(2), *v = sc.vector(3),
         *sv = sc.vector(4), *tv = sc.vector(5), *ax = sc.vector(6);
+  float *p_hat = J ? sc.vector(7) : p, *s_hat = J ? sc.vector(8) : sv;
   auto *st = static_cast<BiState *>(sc.state());
   double *start_part = sc.part(0), *p_part = sc.part(1), *v_part = sc.part(2),
          *s_part = sc.part(3), *t_part = sc.part(4), *r_part = sc.part(5),
@@ -790,8 +847,8 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, 
   MSX_HIP_TRY(hipGetLastError());
   if ((e = spmv(s, x, ax)) != MSX_OK) return e;
   hipLaunchKernelGGL(bi_start, s.grid, s.block, 0, s.stream, b, x, ax, r, r_hat, n, start_part);
-  hipLaunchKernelGGL(bi_decide_start, dim3(1), s.block, 0, s.stream, start_part, np, rtol, atol,
-                     maxiter, st);
+  hipLaunchKernelGGL(bi_decide_start<J>, dim3(1), s.block, 0, s.stream, start_part, np, rtol,
+                     atol, maxiter, st);
   MSX_HIP_TRY(hipGetLastError());
   if ((e = read_state(s, st, &host)) != MSX_OK) return e;
 
@@ -799,19 +856,20 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, 
   auto true_check = [&](float *dst, int32_t kind) -> msx_status {
     msx_status es = spmv(s, x, ax);
     if (es != MSX_OK) return es;
-    hipLaunchKernelGGL(bi_resid, s.grid, s.block, 0, s.stream, b, ax, x, r_hat, dst, n, chk_part);
-    hipLaunchKernelGGL(bi_check, dim3(1), s.block, 0, s.stream, chk_part, np, kind, st);
+    hipLaunchKernelGGL(bi_resid<J>, s.grid, s.block, 0, s.stream, b, ax, x, r_hat, dst, n,
+                       chk_part);
+    hipLaunchKernelGGL(bi_check<J>, dim3(1), s.block, 0, s.stream, chk_part, np, kind, st);
     MSX_HIP_TRY(hipGetLastError());
     return read_state(s, st, &host);
   };
   // the rest of iteration k after its s-check
   auto second_half = [&](int32_t k, int check) -> msx_status {
-    msx_status es = spmv(s, sv, tv);
+    msx_status es = spmv(s, s_hat, tv);
     if (es != MSX_OK) return es;
-    hipLaunchKernelGGL(bi_t, s.grid, s.block, 0, s.stream, sv, tv, n, k, check, s_part, t_part,
+    hipLaunchKernelGGL(bi_t<J>, s.grid, s.block, 0, s.stream, sv, tv, n, k, check, s_part, t_part,
                        np, st);
-    hipLaunchKernelGGL(bi_r, s.grid, s.block, 0, s.stream, sv, tv, x, r, r_hat, n, k, t_part,
-                       r_part, np, st);
+    hipLaunchKernelGGL(bi_r<J>, s.grid, s.block, 0, s.stream, sv, tv, s_hat, x, r, r_hat, n, k,
+                       t_part, r_part, np, st);
     MSX_HIP_TRY(hipGetLastError());
     return MSX_OK;
   };
@@ -826,14 +884,14 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, float *x, 
       const int64_t last = std::min(maxiter, next + batch - 1);
       for (int64_t k = next; k <= last; ++k) {
         const auto kk = static_cast<int32_t>(k);
-        hipLaunchKernelGGL(bi_p, s.grid, s.block, 0, s.stream, r, p, v, n, kk, close_prev, dots,
-                           p_part, np, st);
+        hipLaunchKernelGGL(bi_p<J>, s.grid, s.block, 0, s.stream, r, p, v, inv_diag, p_hat, n, kk,
+                           close_prev, dots, p_part, np, st);
         MSX_HIP_TRY(hipGetLastError());
-        if ((e = spmv(s, p, v)) != MSX_OK) return e;
+        if ((e = spmv(s, p_hat, v)) != MSX_OK) return e;
         hipLaunchKernelGGL(bi_v, s.grid, s.block, 0, s.stream, r_hat, v, n, kk, p_part, v_part,
                            np, st);
-        hipLaunchKernelGGL(bi_s, s.grid, s.block, 0, s.stream, r, v, p, x, sv, n, kk, v_part,
-                           s_part, np, st);
+        hipLaunchKernelGGL(bi_s<J>, s.grid, s.block, 0, s.stream, r, v, p_hat, inv_diag, x, sv,
+                           s_hat, n, kk, v_part, s_part, np, st);
         MSX_HIP_TRY(hipGetLastError());
         if ((e = second_half(kk, 1)) != MSX_OK) return e;
         close_prev = 1;
@@ -976,7 +1034,28 @@ extern "C" msx_status msx_csr_bicgstab(msx_itype it, int64_t n, int64_t nnz, con
   const uint32_t blocks = blocks_for(n);
   const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
                  dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
-  return bicgstab(s, b, x0, x, rtol, atol, maxiter, result);
+  return bicgstab<false>(s, b, x0, nullptr, x, rtol, atol, maxiter, result);
+}
+
+extern "C" msx_status msx_csr_bicgstab_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                              const float *data, const void *indices,
+                                              const void *indptr, const float *b,
+                                              const float *x0, const float *inv_diag, float *x,
+                                              float rtol, float atol, int64_t maxiter,
+                                              const msx_csr_plan *plan, msx_solver_result *result,
+                                              void *stream) {
+  clear_error();
+  msx_status st =
+      check("csr_bicgstab_jacobi", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
+  if (st != MSX_OK) return st;
+  if (inv_diag == nullptr)
+    return fail(MSX_EINVAL, "csr_bicgstab_jacobi buffers must be non-NULL.");
+  st = check_plan("csr_bicgstab_jacobi", plan, MSX_F32, it, n, n, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  const uint32_t blocks = blocks_for(n);
+  const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
+                 dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
+  return bicgstab<true>(s, b, x0, inv_diag, x, rtol, atol, maxiter, result);
 }
 
 extern "C" msx_status msx_csr_minres(msx_itype it, int64_t n, int64_t nnz, const float *data,

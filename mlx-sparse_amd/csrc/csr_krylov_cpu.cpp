@@ -3,6 +3,9 @@
 //
 //   msx_csr_bicgstab_cpu  csr_bicgstab_cpu_impl (reference:
 //                         src/linalg/bicgstab/bicgstab.cpp:80-362)
+//   msx_csr_bicgstab_jacobi_cpu  left_preconditioned_bicgstab_host with the
+//                         Jacobi apply (reference:
+//                         src/preconditioners/bicgstab/bicgstab.cpp:140-521)
 //   msx_csr_minres_cpu    csr_minres_cpu_impl (reference:
 //                         src/linalg/minres/minres.cpp:68-312)
 //
@@ -371,6 +374,240 @@ void minres(const Csr<I> &A, const float *b, const float *x0, float *x, float rt
   *res = {status, done, residual, 0};
 }
 
+// BiCGSTAB with the Jacobi preconditioner M = diag(inv_diag): the
+// reference's left_preconditioned_bicgstab_host with the Jacobi apply
+// (src/preconditioners/bicgstab/bicgstab.cpp:140-521).  Against bicgstab
+// above: ||b|| rounded to float before its square root (norm_float,
+// src/linalg/common/common.h:56-73); x advances along p_hat = M p and
+// s_hat = M s, which the SpMVs take; a failed true-residual evaluation ends
+// the solve with -3 and leaves the reported residual as it was (+inf before
+// the first iteration); the reported residual follows ||s|| after the s
+// update.
+template <class I>
+struct JacobiBicgstab {
+  const Csr<I> &A;
+  const float *b;
+  const float *inv_diag;
+  float *x;
+  int64_t n;
+  Vec ax;
+
+  // true_residual_into (bicgstab.cpp:166-192); false where the reference throws
+  bool true_residual(float *dst, float *norm) {
+    A.apply(x, ax.data());
+    for (int64_t i = 0; i < n; ++i)
+      if (!fin(ax[i])) return false;
+    double rr = 0.0;
+    bool ok = true;
+    for (int64_t i = 0; i < n; ++i) {
+      const float ri = b[i] - ax[i];
+      dst[i] = ri;
+      rr += static_cast<double>(ri) * static_cast<double>(ri);
+      ok = ok && fin(ri);
+    }
+    const float nv = static_cast<float>(std::sqrt(std::max(rr, 0.0)));
+    if (!ok || !fin(rr) || !fin(nv)) return false;
+    *norm = nv;
+    return true;
+  }
+  bool apply(const Vec &src, Vec &out) const {
+    bool ok = true;
+    for (int64_t i = 0; i < n; ++i) {
+      out[i] = inv_diag[i] * src[i];
+      ok = ok && fin(out[i]);
+    }
+    return ok;
+  }
+};
+
+template <class I>
+void bicgstab_jacobi(const Csr<I> &A, const float *b, const float *x0, const float *inv_diag,
+                     float *x, float rtol, float atol, int64_t maxiter, msx_solver_result *res) {
+  const int64_t n = A.n;
+  Vec r(n, 0.0f), r_hat(n, 0.0f), p(n, 0.0f), p_hat(n, 0.0f), v(n, 0.0f), s(n, 0.0f),
+      s_hat(n, 0.0f), t(n, 0.0f);
+  JacobiBicgstab<I> J{A, b, inv_diag, x, n, Vec(n, 0.0f)};
+  std::copy(x0, x0 + n, x);
+  int32_t status = maxiter > 0 ? static_cast<int32_t>(maxiter) : 1, done = 0;
+  float residual = INFINITY;
+  double bb = 0.0;
+  bool inputs_finite = true;
+  for (int64_t i = 0; i < n; ++i) {
+    bb += static_cast<double>(b[i]) * static_cast<double>(b[i]);
+    inputs_finite = inputs_finite && fin(b[i]) && fin(x[i]);
+  }
+  const float bbf = static_cast<float>(bb);
+  const float b_norm = std::sqrt(bbf < 0.0f ? 0.0f : bbf);
+  const float tol = std::max(atol, rtol * b_norm);
+  auto all_finite = [n](const Vec &a) {
+    for (int64_t i = 0; i < n; ++i)
+      if (!fin(a[i])) return false;
+    return true;
+  };
+  if (!inputs_finite || !fin(b_norm) || !fin(tol) || !J.true_residual(r.data(), &residual)) {
+    *res = {-3, 0, residual, 0};
+    return;
+  }
+  r_hat = r;
+  if (residual <= tol) {
+    *res = {0, 0, residual, 0};
+    return;
+  }
+  double rho_prev = 1.0, alpha = 1.0, omega = 1.0;
+  const double eps = static_cast<double>(FLT_EPSILON);
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    const auto prev = static_cast<int32_t>(k - 1);
+    const double rho = dot(r_hat, r), hh = dot(r_hat, r_hat), rr = dot(r, r);
+    if (!fin(rho) || !fin(hh) || !fin(rr)) {
+      status = -3, done = prev;
+      break;
+    }
+    if (near_zero(rho, hh, rr)) {
+      status = -1, done = prev;
+      break;
+    }
+    if (k == 1) {
+      p = r;
+    } else {
+      if (std::fabs(omega) <= eps) {
+        status = -1, done = prev;
+        break;
+      }
+      const double beta = (rho / rho_prev) * (alpha / omega);
+      if (!fin(beta)) {
+        status = -3, done = prev;
+        break;
+      }
+      bool ok = true;
+      for (int64_t i = 0; i < n; ++i) {
+        const double pi = static_cast<double>(r[i]) +
+                          beta * (static_cast<double>(p[i]) - omega * static_cast<double>(v[i]));
+        p[i] = static_cast<float>(pi);
+        ok = ok && fin(pi) && fin(p[i]);
+      }
+      if (!ok) {
+        status = -3, done = prev;
+        break;
+      }
+    }
+    if (!J.apply(p, p_hat)) {
+      status = -3, done = prev;
+      break;
+    }
+    A.apply(p_hat.data(), v.data());
+    if (!all_finite(v)) {
+      status = -3, done = prev;
+      break;
+    }
+    const double hv = dot(r_hat, v), vv = dot(v, v);
+    if (!fin(hv) || !fin(vv)) {
+      status = -3, done = prev;
+      break;
+    }
+    if (near_zero(hv, hh, vv)) {
+      status = -1, done = prev;
+      break;
+    }
+    alpha = rho / hv;
+    if (!fin(alpha)) {
+      status = -3, done = prev;
+      break;
+    }
+    double ss = 0.0;
+    bool ok = true;
+    for (int64_t i = 0; i < n; ++i) {
+      const double si = static_cast<double>(r[i]) - alpha * static_cast<double>(v[i]);
+      const double xi = static_cast<double>(x[i]) + alpha * static_cast<double>(p_hat[i]);
+      s[i] = static_cast<float>(si);
+      x[i] = static_cast<float>(xi);
+      ss += si * si;
+      ok = ok && fin(si) && fin(xi) && fin(s[i]) && fin(x[i]);
+    }
+    done = static_cast<int32_t>(k);
+    residual = static_cast<float>(std::sqrt(std::max(ss, 0.0)));
+    if (!ok || !fin(ss) || !fin(residual)) {
+      status = -3;
+      break;
+    }
+    if (residual <= tol) {
+      float tn = 0.0f;
+      if (!J.true_residual(t.data(), &tn)) {
+        status = -3;
+        break;
+      }
+      if (tn <= tol) {
+        status = 0, residual = tn;
+        break;
+      }
+    }
+    if (!J.apply(s, s_hat)) {
+      status = -3;
+      break;
+    }
+    A.apply(s_hat.data(), t.data());
+    if (!all_finite(t)) {
+      status = -3;
+      break;
+    }
+    const double ts = dot(t, s), tt = dot(t, t);
+    if (!fin(ts) || !fin(tt)) {
+      status = -3;
+      break;
+    }
+    if (near_zero(tt, tt, 1.0)) {
+      status = -1;
+      break;
+    }
+    omega = ts / tt;
+    if (!fin(omega)) {
+      status = -3;
+      break;
+    }
+    double rn = 0.0;
+    ok = true;
+    for (int64_t i = 0; i < n; ++i) {
+      const double xi = static_cast<double>(x[i]) + omega * static_cast<double>(s_hat[i]);
+      const double ri = static_cast<double>(s[i]) - omega * static_cast<double>(t[i]);
+      x[i] = static_cast<float>(xi);
+      r[i] = static_cast<float>(ri);
+      rn += ri * ri;
+      ok = ok && fin(xi) && fin(ri) && fin(x[i]) && fin(r[i]);
+    }
+    residual = static_cast<float>(std::sqrt(std::max(rn, 0.0)));
+    if (!ok || !fin(rn) || !fin(residual)) {
+      status = -3;
+      break;
+    }
+    if (residual <= tol) {
+      float tn = 0.0f;
+      if (!J.true_residual(r.data(), &tn)) {
+        status = -3;
+        break;
+      }
+      residual = tn;
+      if (tn <= tol) {
+        status = 0;
+        break;
+      }
+    }
+    if (std::fabs(omega) <= eps) {
+      status = -1;
+      break;
+    }
+    rho_prev = rho;
+  }
+  if (status > 0 || status == -1) {
+    float tn = 0.0f;
+    if (!J.true_residual(r.data(), &tn)) {
+      status = -3;
+    } else {
+      residual = tn;
+      if (tn <= tol) status = 0;
+    }
+  }
+  *res = {status, done, residual, 0};
+}
+
 msx_status check(const char *op, msx_itype it, int64_t n, int64_t nnz, const void *data,
                  const void *indices, const void *indptr, const void *b, const void *x0, void *x,
                  int64_t maxiter, msx_solver_result *result) {
@@ -406,6 +643,33 @@ extern "C" msx_status msx_csr_bicgstab_cpu(msx_itype it, int64_t n, int64_t nnz,
                b, x0, x, rtol, atol, maxiter, result);
   } catch (const std::bad_alloc &) {
     return msx::fail(MSX_ENOMEM, "csr_bicgstab: out of host memory.");
+  }
+  return MSX_OK;
+}
+
+extern "C" msx_status msx_csr_bicgstab_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                                  const float *data, const void *indices,
+                                                  const void *indptr, const float *b,
+                                                  const float *x0, const float *inv_diag, float *x,
+                                                  float rtol, float atol, int64_t maxiter,
+                                                  msx_solver_result *result) {
+  msx::clear_error();
+  msx_status st =
+      check("csr_bicgstab_jacobi", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
+  if (st != MSX_OK) return st;
+  if (inv_diag == nullptr)
+    return msx::fail(MSX_EINVAL, "csr_bicgstab_jacobi buffers must be non-NULL.");
+  try {
+    if (it == MSX_I32)
+      bicgstab_jacobi(Csr<int32_t>{n, data, static_cast<const int32_t *>(indices),
+                                   static_cast<const int32_t *>(indptr)},
+                      b, x0, inv_diag, x, rtol, atol, maxiter, result);
+    else
+      bicgstab_jacobi(Csr<int64_t>{n, data, static_cast<const int64_t *>(indices),
+                                   static_cast<const int64_t *>(indptr)},
+                      b, x0, inv_diag, x, rtol, atol, maxiter, result);
+  } catch (const std::bad_alloc &) {
+    return msx::fail(MSX_ENOMEM, "csr_bicgstab_jacobi: out of host memory.");
   }
   return MSX_OK;
 }

@@ -108,6 +108,14 @@ def csr_bicgstab(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, a
                                     maxiter, plan=plan)
 
 
+def csr_bicgstab_jacobi(data, indices, indptr, b, x0, inv_diag, shape: Shape2D, *, rtol: float,
+                        atol: float, maxiter: int, plan=None):
+    """(x, info, residual, iterations) of Jacobi-preconditioned BiCGSTAB
+    (reference: mlx_sparse/_native.py csr_bicgstab_jacobi)."""
+    return extension().csr_bicgstab_jacobi(data, indices, indptr, b, x0, inv_diag, shape[0],
+                                           shape[1], rtol, atol, maxiter, plan=plan)
+
+
 def csr_minres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
                maxiter: int, shift: float = 0.0, plan=None):
     """(x, info, residual, iterations) of (A - shift I) x = b (reference:

@@ -148,16 +148,28 @@ def _system(A, b, x0, maxiter, solver: str):
     return csr, rhs, guess, maxiter_value, device
 
 
-def _plain_preconditioner(M, csr, solver: str):
-    """The preconditioner kind when ``M`` is None or the identity; other
-    kinds raise (this build runs BiCGSTAB and MINRES unpreconditioned)."""
+# Solvers with a Jacobi-preconditioned loop (the reference's native
+# diagonal paths: mlx_sparse/linalg/_iterative.py:437-461 csr_bicgstab_jacobi).
+_JACOBI_SOLVERS = {"bicgstab"}
+
+
+def _preconditioner(M, csr, solver: str, device):
+    """(kind, pc, inverse diagonal or None) of ``M``: None or the identity
+    run the plain loop; a diagonal/Jacobi preconditioner runs the solver's
+    Jacobi loop; other kinds raise."""
     if M is None:
-        return None
+        return None, None, None
     pc = _pc.aspreconditioner(M, csr)
     if isinstance(pc, _pc.IdentityPreconditioner):
-        return pc.kind
-    raise TypeError(f"{solver} in this build supports only the identity preconditioner "
-                    f"(M=None or preconditioners.identity); got {pc.kind}.")
+        return pc.kind, pc, None
+    if isinstance(pc, _pc.DiagonalPreconditioner) and solver in _JACOBI_SOLVERS:
+        if pc.inverse_diagonal.shape[0] != csr.shape[0]:
+            raise ValueError("preconditioner size does not match the matrix.")
+        inv = pc.inverse_diagonal.to(device=device, dtype=torch.float32).contiguous()
+        return pc.kind, pc, inv
+    supported = "identity and diagonal/Jacobi" if solver in _JACOBI_SOLVERS else "identity"
+    raise TypeError(f"{solver} in this build supports only the {supported} preconditioners; "
+                    f"got {pc.kind}.")
 
 
 def bicgstab(A, b, x0=None, *, rtol: float | None = None, atol: float = 0.0,
@@ -171,6 +183,10 @@ def bicgstab(A, b, x0=None, *, rtol: float | None = None, atol: float = 0.0,
     ``1e-5``; ``tol`` is SciPy's alias for it (both may be given only when
     equal).  ``maxiter`` defaults to ``10 * n``.
 
+    ``M``: ``None``, ``preconditioners.identity`` or a diagonal/Jacobi
+    preconditioner (the reference's Jacobi loop: x advances along
+    ``M @ p`` and ``M @ s``).
+
     Returns ``(x, info)``: ``info`` 0 converged, > 0 the iteration budget
     ran out, -1 breakdown (near-zero ``rho``, ``alpha`` denominator or
     ``omega``), -3 non-finite values.  With ``return_info=True`` a
@@ -178,11 +194,16 @@ def bicgstab(A, b, x0=None, *, rtol: float | None = None, atol: float = 0.0,
     """
     rtol_value, atol_value = _normalize_tolerances(rtol, tol, atol)
     csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "bicgstab")
-    kind = _plain_preconditioner(M, csr, "bicgstab")
+    kind, _, inv_diag = _preconditioner(M, csr, "bicgstab", device)
     data, indices, indptr = csr.buffers(device)
-    x, info, residual, iterations = _native.csr_bicgstab(
-        data, indices, indptr, rhs, guess, csr.shape, rtol=rtol_value, atol=atol_value,
-        maxiter=maxiter_value, plan=csr.plan(device))
+    if inv_diag is None:
+        x, info, residual, iterations = _native.csr_bicgstab(
+            data, indices, indptr, rhs, guess, csr.shape, rtol=rtol_value, atol=atol_value,
+            maxiter=maxiter_value, plan=csr.plan(device))
+    else:
+        x, info, residual, iterations = _native.csr_bicgstab_jacobi(
+            data, indices, indptr, rhs, guess, inv_diag, csr.shape, rtol=rtol_value,
+            atol=atol_value, maxiter=maxiter_value, plan=csr.plan(device))
     return finish(x, info, residual, iterations, solver="bicgstab", return_info=bool(return_info),
                   callback=callback, rtol=rtol_value, atol=atol_value, maxiter=maxiter_value,
                   preconditioner=kind)
@@ -202,7 +223,7 @@ def minres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, shift: float
     """
     csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "minres")
     shift_value = _finite_scalar("shift", shift)
-    kind = _plain_preconditioner(M, csr, "minres")
+    kind, _, _ = _preconditioner(M, csr, "minres", device)
     data, indices, indptr = csr.buffers(device)
     x, info, residual, iterations = _native.csr_minres(
         data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
@@ -237,7 +258,7 @@ def gmres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, restart: int 
     restart_value = min(20, csr.shape[0]) if restart is None else int(restart)
     if restart_value <= 0:
         raise ValueError("restart must be positive.")
-    kind = _plain_preconditioner(M, csr, "gmres")
+    kind, _, _ = _preconditioner(M, csr, "gmres", device)
     data, indices, indptr = csr.buffers(device)
     x, info, residual, iterations = _native.csr_gmres(
         data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),

@@ -535,11 +535,19 @@ py::tuple solve_cg(py::handle data_o, py::handle indices_o, py::handle indptr_o,
 py::tuple solve_krylov(msx::Krylov kind, py::handle data_o, py::handle indices_o,
                        py::handle indptr_o, py::handle b_o, py::handle x0_o, int64_t n_rows,
                        int64_t n_cols, float rtol, float atol, int64_t maxiter, float shift,
-                       py::object plan, int64_t restart = 0) {
+                       py::object plan, int64_t restart = 0,
+                       py::object inv_diag_o = py::none()) {
   py::object data = contiguous(data_o), indices = contiguous(indices_o),
              indptr = contiguous(indptr_o), b = contiguous(b_o), x0 = contiguous(x0_o);
   const ArrayView vd = view_of(data), vi = view_of(indices), vp = view_of(indptr), vb = view_of(b),
                   vx0 = view_of(x0);
+  py::object inv;
+  ArrayView vinv;
+  if (!inv_diag_o.is_none()) {
+    inv = contiguous(inv_diag_o);
+    vinv = view_of(inv);
+  }
+  const ArrayView *pinv = inv_diag_o.is_none() ? nullptr : &vinv;
   if (vb.ndim != 1)
     msx::require_rank(vb, 1, kind == msx::Krylov::BiCGSTAB ? "csr_bicgstab b"
                              : kind == msx::Krylov::MINRES ? "csr_minres b"
@@ -550,11 +558,11 @@ py::tuple solve_krylov(msx::Krylov kind, py::handle data_o, py::handle indices_o
   msx_solver_result res{};
   if (vd.device >= 0) {
     res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
-                          shift, plan_ptr(plan), ctx, restart);
+                          shift, plan_ptr(plan), ctx, restart, pinv);
   } else {
     py::gil_scoped_release nogil;
     res = msx::csr_krylov(kind, vd, vi, vp, vb, vx0, vx, n_rows, n_cols, rtol, atol, maxiter,
-                          shift, nullptr, ctx, restart);
+                          shift, nullptr, ctx, restart, pinv);
   }
   return py::make_tuple(x, res.info, res.residual, res.iterations);
 }
@@ -787,6 +795,19 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
       py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("maxiter"),
       py::arg("plan") = py::none(), "BiCGSTAB: (x, info, residual, iterations).");
+  m.def(
+      "csr_bicgstab_jacobi",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         py::handle inv_diag, int64_t n_rows, int64_t n_cols, float rtol, float atol,
+         int64_t maxiter, py::object plan) {
+        return solve_krylov(msx::Krylov::BiCGSTAB, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, 0.0f, plan, 0,
+                            py::reinterpret_borrow<py::object>(inv_diag));
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
+      py::arg("atol"), py::arg("maxiter"), py::arg("plan") = py::none(),
+      "Jacobi-preconditioned BiCGSTAB: (x, info, residual, iterations).");
   m.def(
       "csr_minres",
       [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,

@@ -14,10 +14,13 @@ enum class Krylov { BiCGSTAB, MINRES, GMRES };
 // src/linalg/minres/minres.cpp csr_minres, src/linalg/gmres/gmres.cpp:223-263
 // csr_gmres), then runs the device solver on ctx.stream (with `plan`,
 // nullable) or the host loop.  `restart`: GMRES's cycle length (> 0).
+// `inv_diag` non-null: the Jacobi-preconditioned loop (reference:
+// src/preconditioners/bicgstab/bicgstab.cpp:607-635 csr_bicgstab_jacobi).
 msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView &indices,
                              const ArrayView &indptr, const ArrayView &b, const ArrayView &x0,
                              const ArrayView &x, int64_t n_rows, int64_t n_cols, float rtol,
                              float atol, int64_t maxiter, float shift, const msx_csr_plan *plan,
-                             const ExecContext &ctx, int64_t restart = 0);
+                             const ExecContext &ctx, int64_t restart = 0,
+                             const ArrayView *inv_diag = nullptr);
 
 }  // namespace msx

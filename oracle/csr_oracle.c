@@ -33,6 +33,8 @@
  *   - BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
  *     and MINRES with its shift (src/linalg/minres/minres.cpp:68-312,
  *     csr_minres_cpu_impl), float32;
+ *   - BiCGSTAB with a Jacobi preconditioner
+ *     (src/preconditioners/bicgstab/bicgstab.cpp:140-521), float32;
  *   - restarted GMRES (src/linalg/gmres/gmres.cpp:58-220, csr_gmres_impl)
  *     with its Arnoldi factorisation (src/linalg/arnoldi/arnoldi.cpp:79-159,
  *     csr_arnoldi_cpu_impl) and the Givens least-squares solve
@@ -1168,6 +1170,264 @@ done:
   *residual = residual_norm;
   *iterations = completed;
   free(r); free(r_hat); free(p); free(v); free(s); free(t); free(ax);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* BiCGSTAB with a Jacobi preconditioner: the reference's
+ * left_preconditioned_bicgstab_host (src/preconditioners/bicgstab/
+ * bicgstab.cpp:140-421) with apply(v)[i] = inv_diag[i] * v[i] in float
+ * (csr_bicgstab_jacobi_cpu_impl, bicgstab.cpp:425-521).  Against
+ * oracle_csr_bicgstab: ||b|| is rounded to float before its square root
+ * (norm_float, src/linalg/common/common.h:56-73); x advances along
+ * p_hat = M p and s_hat = M s, which the SpMVs take; a failed true-residual
+ * evaluation (a non-finite A x entry, residual entry, sum or norm: the
+ * reference's exception) ends the solve with status -3 and leaves the
+ * reported residual as it was (+inf before the first iteration); the
+ * reported residual follows ||s|| after the s update. */
+
+/* true_residual_into (bicgstab.cpp:166-192): 0 where the reference throws. */
+static int bj_true_residual(int it, int64_t n, const float *data, const void *indices,
+                            const void *indptr, const float *b, const float *x, float *ax,
+                            float *dst, float *norm_out) {
+  cg_spmv(it, n, data, indices, indptr, x, ax);
+  for (int64_t i = 0; i < n; ++i)
+    if (!fin(ax[i])) return 0;
+  double rr = 0.0;
+  int ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    const float ri = b[i] - ax[i];
+    dst[i] = ri;
+    rr += (double)ri * (double)ri;
+    ok = ok && fin(ri);
+  }
+  const float norm = (float)sqrt(max0(rr));
+  if (!ok || !isfinite(rr) || !fin(norm)) return 0;
+  *norm_out = norm;
+  return 1;
+}
+
+/* out = inv_diag * src in float; returns 1 when every entry is finite. */
+static int bj_apply(int64_t n, const float *inv_diag, const float *src, float *out) {
+  int ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    out[i] = inv_diag[i] * src[i];
+    ok = ok && fin(out[i]);
+  }
+  return ok;
+}
+
+static int all_finite(int64_t n, const float *v) {
+  for (int64_t i = 0; i < n; ++i)
+    if (!fin(v[i])) return 0;
+  return 1;
+}
+
+int oracle_csr_bicgstab_jacobi(int it, int64_t n, const float *data, const void *indices,
+                               const void *indptr, const float *b, const float *x0,
+                               const float *inv_diag, float *x, float rtol, float atol,
+                               int64_t maxiter, int32_t *info, float *residual,
+                               int32_t *iterations) {
+  const size_t bytes = (size_t)(n > 0 ? n : 1) * sizeof(float);
+  float *buf = (float *)calloc(9, bytes);
+  if (!buf) return -1;
+  const size_t m = bytes / sizeof(float);
+  float *r = buf, *r_hat = buf + m, *p = buf + 2 * m, *p_hat = buf + 3 * m, *v = buf + 4 * m;
+  float *s = buf + 5 * m, *s_hat = buf + 6 * m, *t = buf + 7 * m, *ax = buf + 8 * m;
+  int32_t status = maxiter > 0 ? (int32_t)maxiter : 1, completed = 0;
+  float residual_norm = INFINITY;
+  memcpy(x, x0, (size_t)n * sizeof(float));
+  double bb = 0.0;
+  int setup_finite = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    bb += (double)b[i] * (double)b[i];
+    setup_finite = setup_finite && fin(b[i]) && fin(x[i]);
+  }
+  const float b_norm = sqrtf(max0f((float)bb));
+  const float scaled = rtol * b_norm;
+  const float tol = atol > scaled ? atol : scaled;
+  if (!setup_finite || !fin(b_norm) || !fin(tol)) {
+    status = -3;
+    goto done;
+  }
+  if (!bj_true_residual(it, n, data, indices, indptr, b, x, ax, r, &residual_norm)) {
+    status = -3;
+    goto done;
+  }
+  memcpy(r_hat, r, (size_t)n * sizeof(float));
+  if (residual_norm <= tol) {
+    status = 0;
+    goto done;
+  }
+  double rho_prev = 1.0, alpha = 1.0, omega = 1.0;
+  for (int64_t k = 1; k <= maxiter; ++k) {
+    const double rho = dot_d(r_hat, r, n);
+    const double r_hat_norm2 = dot_d(r_hat, r_hat, n);
+    const double r_norm2 = dot_d(r, r, n);
+    if (!isfinite(rho) || !isfinite(r_hat_norm2) || !isfinite(r_norm2)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (near_zero_dot(rho, r_hat_norm2, r_norm2)) {
+      status = -1;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (k == 1) {
+      memcpy(p, r, (size_t)n * sizeof(float));
+    } else {
+      if (fabs(omega) <= (double)FLT_EPSILON) {
+        status = -1;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+      const double beta = (rho / rho_prev) * (alpha / omega);
+      if (!isfinite(beta)) {
+        status = -3;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+      int ok = 1;
+      for (int64_t i = 0; i < n; ++i) {
+        const double pi = (double)r[i] + beta * ((double)p[i] - omega * (double)v[i]);
+        p[i] = (float)pi;
+        ok = ok && isfinite(pi) && fin(p[i]);
+      }
+      if (!ok) {
+        status = -3;
+        completed = (int32_t)(k - 1);
+        break;
+      }
+    }
+    if (!bj_apply(n, inv_diag, p, p_hat)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    cg_spmv(it, n, data, indices, indptr, p_hat, v);
+    if (!all_finite(n, v)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    const double alpha_den = dot_d(r_hat, v, n);
+    const double v_norm2 = dot_d(v, v, n);
+    if (!isfinite(alpha_den) || !isfinite(v_norm2)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    if (near_zero_dot(alpha_den, r_hat_norm2, v_norm2)) {
+      status = -1;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    alpha = rho / alpha_den;
+    if (!isfinite(alpha)) {
+      status = -3;
+      completed = (int32_t)(k - 1);
+      break;
+    }
+    double s_norm2 = 0.0;
+    int ok = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      const double si = (double)r[i] - alpha * (double)v[i];
+      const double xi = (double)x[i] + alpha * (double)p_hat[i];
+      s[i] = (float)si;
+      x[i] = (float)xi;
+      s_norm2 += si * si;
+      ok = ok && isfinite(si) && isfinite(xi) && fin(s[i]) && fin(x[i]);
+    }
+    completed = (int32_t)k;
+    residual_norm = (float)sqrt(max0(s_norm2));
+    if (!ok || !isfinite(s_norm2) || !fin(residual_norm)) {
+      status = -3;
+      break;
+    }
+    if (residual_norm <= tol) {
+      float true_norm = 0.0f;
+      if (!bj_true_residual(it, n, data, indices, indptr, b, x, ax, t, &true_norm)) {
+        status = -3;
+        break;
+      }
+      if (true_norm <= tol) {
+        status = 0;
+        residual_norm = true_norm;
+        break;
+      }
+    }
+    if (!bj_apply(n, inv_diag, s, s_hat)) {
+      status = -3;
+      break;
+    }
+    cg_spmv(it, n, data, indices, indptr, s_hat, t);
+    if (!all_finite(n, t)) {
+      status = -3;
+      break;
+    }
+    const double omega_num = dot_d(t, s, n);
+    const double omega_den = dot_d(t, t, n);
+    if (!isfinite(omega_num) || !isfinite(omega_den)) {
+      status = -3;
+      break;
+    }
+    if (near_zero_dot(omega_den, omega_den, 1.0)) {
+      status = -1;
+      break;
+    }
+    omega = omega_num / omega_den;
+    if (!isfinite(omega)) {
+      status = -3;
+      break;
+    }
+    double r_norm2_new = 0.0;
+    ok = 1;
+    for (int64_t i = 0; i < n; ++i) {
+      const double xi = (double)x[i] + omega * (double)s_hat[i];
+      const double ri = (double)s[i] - omega * (double)t[i];
+      x[i] = (float)xi;
+      r[i] = (float)ri;
+      r_norm2_new += ri * ri;
+      ok = ok && isfinite(xi) && isfinite(ri) && fin(x[i]) && fin(r[i]);
+    }
+    residual_norm = (float)sqrt(max0(r_norm2_new));
+    if (!ok || !isfinite(r_norm2_new) || !fin(residual_norm)) {
+      status = -3;
+      break;
+    }
+    if (residual_norm <= tol) {
+      float true_norm = 0.0f;
+      if (!bj_true_residual(it, n, data, indices, indptr, b, x, ax, r, &true_norm)) {
+        status = -3;
+        break;
+      }
+      residual_norm = true_norm;
+      if (true_norm <= tol) {
+        status = 0;
+        break;
+      }
+    }
+    if (fabs(omega) <= (double)FLT_EPSILON) {
+      status = -1;
+      break;
+    }
+    rho_prev = rho;
+  }
+  if (status > 0 || status == -1) {
+    float true_norm = 0.0f;
+    if (!bj_true_residual(it, n, data, indices, indptr, b, x, ax, r, &true_norm)) {
+      status = -3;
+    } else {
+      residual_norm = true_norm;
+      if (true_norm <= tol) status = 0;
+    }
+  }
+done:
+  *info = status;
+  *residual = residual_norm;
+  *iterations = completed;
+  free(buf);
   return 0;
 }
 

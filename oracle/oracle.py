@@ -105,6 +105,9 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_bicgstab.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp,
                                              vp, vp]
         _lib.oracle_csr_bicgstab.restype = ci
+        _lib.oracle_csr_bicgstab_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                                    i64, vp, vp, vp]
+        _lib.oracle_csr_bicgstab_jacobi.restype = ci
         _lib.oracle_csr_minres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                            vp, vp, vp]
         _lib.oracle_csr_minres.restype = ci
@@ -291,6 +294,27 @@ def csr_bicgstab(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol:
                                    ctypes.addressof(its))
     if rc != 0:
         raise MemoryError("oracle_csr_bicgstab failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_bicgstab_jacobi(data, indices, indptr, b, inv_diag, x0=None, *, rtol: float = 1e-5,
+                        atol: float = 0.0, maxiter: int | None = None):
+    """BiCGSTAB with the Jacobi preconditioner M = diag(inv_diag) (reference
+    src/preconditioners/bicgstab/bicgstab.cpp:140-521,
+    left_preconditioned_bicgstab_host with csr_bicgstab_jacobi_cpu_impl's
+    apply).  Returns (x, info, residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    inv_diag = np.ascontiguousarray(inv_diag, np.float32)
+    assert inv_diag.shape == (n,)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_bicgstab_jacobi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                          _ptr(indptr), _ptr(b), _ptr(x0), _ptr(inv_diag),
+                                          _ptr(x), rtol, atol, maxiter, ctypes.addressof(info),
+                                          ctypes.addressof(res), ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_bicgstab_jacobi failed")
     return x, info.value, res.value, its.value
 
 

@@ -105,6 +105,10 @@ def lib() -> ctypes.CDLL:
         L.msx_csr_minres.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32, vp,
                                      vp, vp]
         L.msx_csr_bicgstab_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, vp]
+        L.msx_csr_bicgstab_jacobi.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                              i64, vp, vp, vp]
+        L.msx_csr_bicgstab_jacobi_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32,
+                                                  f32, i64, vp]
         L.msx_csr_minres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                          vp]
         L.msx_csr_gmres.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64, vp,
@@ -130,6 +134,7 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_spmm_data_vjp_cpu", "msx_csr_cg", "msx_csr_pcg_jacobi",
                      "msx_csr_cg_cpu", "msx_csr_pcg_jacobi_cpu", "msx_csr_bicgstab",
                      "msx_csr_minres", "msx_csr_bicgstab_cpu", "msx_csr_minres_cpu",
+                     "msx_csr_bicgstab_jacobi", "msx_csr_bicgstab_jacobi_cpu",
                      "msx_csr_gmres", "msx_csr_gmres_cpu"):
             getattr(L, name).restype = ci
         _lib = L
@@ -416,9 +421,10 @@ def cg(data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxiter=None, 
 
 
 def krylov(kind, data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxiter=None,
-           shift=0.0, plan=None):
+           shift=0.0, plan=None, inv_diag=None):
     """(x, info, residual, iterations) through msx_csr_bicgstab[_cpu]
-    (kind "bicgstab") or msx_csr_minres[_cpu] (kind "minres")."""
+    (kind "bicgstab") or msx_csr_minres[_cpu] (kind "minres"); with
+    `inv_diag`, their Jacobi-preconditioned entry points (*_jacobi)."""
     n = b.numel()
     x0 = torch.zeros_like(b) if x0 is None else x0
     x = torch.empty_like(b)
@@ -426,9 +432,12 @@ def krylov(kind, data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxi
     res = SolverResult()
     it = IT[indices.dtype]
     L = lib()
-    head = (it, n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b), _p(x0), _p(x), rtol,
-            atol, maxiter)
-    extra = (shift,) if kind == "minres" else ()
+    pre = () if inv_diag is None else (_p(inv_diag),)
+    if inv_diag is not None:
+        kind = f"{kind}_jacobi"
+    head = (it, n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b), _p(x0), *pre, _p(x),
+            rtol, atol, maxiter)
+    extra = (shift,) if kind.startswith("minres") else ()
     if b.device.type == "cpu":
         st = getattr(L, f"msx_csr_{kind}_cpu")(*head, *extra, ctypes.byref(res))
     else:

@@ -136,16 +136,16 @@ def test_cpu_krylov_errors():
             _capi.krylov(kind, d, i, p, torch.ones(1), maxiter=-1)
 
 
-@pytest.mark.parametrize("solver", ["bicgstab", "minres", "gmres"])
+@pytest.mark.parametrize("solver", ["minres", "gmres"])
 def test_preconditioned_variants_are_an_explicit_deviation(cpu, solver):
-    """The reference dispatches a diagonal / Jacobi M of bicgstab, minres and
-    gmres to separate native loops (csr_bicgstab_jacobi, csr_minres_jacobi,
-    csr_gmres_jacobi: reference mlx_sparse/linalg/_iterative.py:436-461,
-    :765-797, :1083-1125).  This build has no such loops: every inverse
-    diagonal form of M raises TypeError naming the supported choices, a
-    sparse matrix as M raises the reference's TypeError, and M = None or
-    the identity runs the plain loop (minres: whatever check_preconditioner
-    says, since no preconditioner is checked)."""
+    """The reference dispatches a diagonal / Jacobi M of minres and gmres to
+    separate native loops (csr_minres_jacobi, csr_gmres_jacobi: reference
+    mlx_sparse/linalg/_iterative.py:765-797, :1083-1125).  Where this build
+    has no such loop, every inverse diagonal form of M raises TypeError
+    naming the supported choices, a sparse matrix as M raises the
+    reference's TypeError, and M = None or the identity runs the plain loop
+    (minres: whatever check_preconditioner says, since no preconditioner is
+    checked)."""
     ms = cpu
     from mlx_sparse import linalg
     from mlx_sparse.linalg import preconditioners
@@ -157,7 +157,7 @@ def test_preconditioned_variants_are_an_explicit_deviation(cpu, solver):
     fn = getattr(linalg, solver)
     for M in (preconditioners.jacobi(A), preconditioners.diagonal(np.diag(dense)),
               torch.from_numpy((1.0 / np.diag(dense)).astype(np.float32))):
-        with pytest.raises(TypeError, match="identity preconditioner"):
+        with pytest.raises(TypeError, match="supports only the identity preconditioners"):
             fn(A, b, M=M)
     with pytest.raises(TypeError, match="sparse matrices"):
         fn(A, b, M=A)
@@ -167,3 +167,81 @@ def test_preconditioned_variants_are_an_explicit_deviation(cpu, solver):
         assert info.status == 0
         np.testing.assert_allclose(x.numpy(), np.linalg.solve(dense, b), rtol=1e-4, atol=1e-5)
         assert ms.default_torch_device().type == "cpu"
+
+
+# -- BiCGSTAB with a Jacobi preconditioner ---------------------------------------------
+
+def _row_scaled(g=16, seed=9):
+    import scipy.sparse as sp
+
+    A0 = convection_2d(g)
+    rng = np.random.default_rng(seed)
+    scale = np.float32(10.0) ** rng.uniform(-2, 2, A0.shape[0]).astype(np.float32)
+    A = (sp.diags(scale) @ A0).tocsr().astype(np.float32)
+    A.sort_indices()
+    b = (scale * rng.uniform(-1, 1, A.shape[0])).astype(np.float32)
+    return A, b
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_bicgstab_jacobi_cpu_equals_oracle(oracle, index_dtype):
+    """msx_csr_bicgstab_jacobi_cpu runs the oracle's loop bit for bit: x,
+    status, residual and iterations, on converging solves, short budgets,
+    the row-scaled system the preconditioner rescues, and the status cases
+    where the Jacobi loop differs from the plain one (non-finite b: residual
+    +inf; a non-finite inverse diagonal entry)."""
+    import scipy.sparse as sp
+
+    cases = []
+    A = convection_2d(20)
+    b = np.random.default_rng(4).uniform(-1, 1, A.shape[0]).astype(np.float32)
+    inv = (1.0 / A.diagonal()).astype(np.float32)
+    for kw in ({"rtol": 1e-4}, {"rtol": 1e-6}, {"maxiter": 3, "rtol": 1e-9}, {"maxiter": 0}):
+        cases.append((A, b, inv, None, kw))
+    cases.append((A, b, inv, np.full(A.shape[0], 0.25, np.float32), {"rtol": 1e-4}))
+    As, bs = _row_scaled()
+    cases.append((As, bs, (1.0 / As.diagonal()).astype(np.float32), None, {"rtol": 1e-5}))
+    N = sp.csr_matrix(NONSYM)
+    invn = (1.0 / np.diag(NONSYM)).astype(np.float32)
+    bn = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    cases.append((N, bn, invn, None, {"rtol": 1e-4, "atol": 1e-7, "maxiter": 80}))
+    bad_b = bn.copy()
+    bad_b[1] = np.nan
+    cases.append((N, bad_b, invn, None, {}))
+    bad_inv = invn.copy()
+    bad_inv[2] = np.inf
+    cases.append((N, bn, bad_inv, None, {}))
+    cases.append((N, np.zeros(4, np.float32), invn, None, {}))
+    for M, rhs, iv, x0, kw in cases:
+        args = (M.data.astype(np.float32), M.indices.astype(index_dtype),
+                M.indptr.astype(index_dtype))
+        got = _capi.krylov("bicgstab", *(torch.from_numpy(np.ascontiguousarray(a)) for a in args),
+                           torch.from_numpy(rhs), None if x0 is None else torch.from_numpy(x0),
+                           inv_diag=torch.from_numpy(iv), **kw)
+        want = oracle.csr_bicgstab_jacobi(*args, rhs, iv, x0, **kw)
+        _same(got, want)
+
+
+def test_bicgstab_jacobi_api_on_cpu(cpu, oracle):
+    """linalg.bicgstab(A, b, M=jacobi(A)) on the CPU device runs the Jacobi
+    loop (the reference's test system and bounds,
+    tests/test_linalg_bicgstab.py:175-201), equal to the oracle bit for
+    bit; diagonal(...) and a plain inverse-diagonal tensor are the same
+    preconditioner."""
+    ms = cpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    d, i, p = _csr(NONSYM)
+    A = ms.csr_array((d, i, p), shape=NONSYM.shape, canonical=True)
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    want = oracle.csr_bicgstab_jacobi(d, i, p, b, (1.0 / np.diag(NONSYM)).astype(np.float32),
+                                      rtol=1e-4, atol=1e-7, maxiter=80)
+    for M in (preconditioners.jacobi(A), preconditioners.diagonal(np.diag(NONSYM))):
+        x, info = linalg.bicgstab(A, b, M=M, rtol=1e-4, atol=1e-7, maxiter=80, return_info=True)
+        assert info.status == 0 and info.preconditioner in {"jacobi", "diagonal"}
+        assert info.iterations == want[3]
+        assert x.numpy().tobytes() == want[0].tobytes()
+        np.testing.assert_allclose(x.numpy(), np.linalg.solve(NONSYM, b), rtol=8e-5, atol=8e-5)
+    with pytest.raises(TypeError, match="sparse matrices"):
+        linalg.bicgstab(A, b, M=A)

@@ -228,3 +228,123 @@ def test_full_size_minres_and_bicgstab(gpu):
         assert info.residual_norm <= 1e-5 * np.linalg.norm(b_np) * (1 + 1e-5)
         ref = np.linalg.norm(wx.astype(np.float64))
         assert np.linalg.norm(x.cpu().numpy().astype(np.float64) - wx) <= 1e-4 * ref
+
+
+# -- BiCGSTAB with a Jacobi preconditioner (msx_csr_bicgstab_jacobi) ------------------
+
+def _scaled_convection(g, seed=9):
+    """convection_2d(g) with rows scaled by 10^U[-2, 2]: the plain loop
+    struggles, the Jacobi loop does not."""
+    A0 = convection_2d(g)
+    rng = np.random.default_rng(seed)
+    scale = np.float32(10.0) ** rng.uniform(-2, 2, A0.shape[0]).astype(np.float32)
+    A = (sp.diags(scale) @ A0).tocsr().astype(np.float32)
+    A.sort_indices()
+    b = (scale * rng.uniform(-1, 1, A.shape[0])).astype(np.float32)
+    return A, b, (1.0 / A.diagonal()).astype(np.float32)
+
+
+def _gpu_jacobi(A, b, inv, index_dtype=np.int32, slice_mode=None, plan=True, x0=None, **kw):
+    d, i, p = (torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in _args(A, index_dtype))
+    pl = _capi.Plan(p, A.shape[0], d.numel(), data=d, indices=i, n_cols=A.shape[1],
+                    slice_mode=slice_mode) if plan else None
+    out = _capi.krylov("bicgstab", d, i, p, torch.from_numpy(b).to(DEV),
+                       None if x0 is None else torch.from_numpy(x0).to(DEV), plan=pl,
+                       inv_diag=torch.from_numpy(inv).to(DEV), **kw)
+    torch.cuda.synchronize()
+    return (out[0].cpu().numpy(),) + tuple(out[1:])
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_bicgstab_jacobi_matches_oracle(index_dtype):
+    """Status equal to the oracle's, iterations within two, x solving the
+    system, the reported residual the true one - on the row-scaled system
+    and on the plain convection system."""
+    # float32 BiCGSTAB stops with -1 once r turns orthogonal to r_hat (the
+    # reference's relative rho test), on either side depending on rounding:
+    # tolerances where the oracle converges with margin (it still converges
+    # at a third of them)
+    for g, scaled, rtol in ((48, True, 1e-4), (32, False, 1e-5)):
+        if scaled:
+            A, b, inv = _scaled_convection(g, seed=3)
+        else:
+            A = convection_2d(g)
+            b = np.random.default_rng(4).uniform(-1, 1, A.shape[0]).astype(np.float32)
+            inv = (1.0 / A.diagonal()).astype(np.float32)
+        print(f"bicgstab jacobi g={g} scaled={scaled} {np.dtype(index_dtype).name}", flush=True)
+        x, info, res, its = _gpu_jacobi(A, b, inv, index_dtype, rtol=rtol, maxiter=600)
+        wx, winfo, wres, wits = orc.csr_bicgstab_jacobi(*_args(A, index_dtype), b, inv,
+                                                        rtol=rtol, maxiter=600)
+        assert info == winfo == 0 and abs(its - wits) <= 2, (its, wits)
+        dense = A.toarray().astype(np.float64)
+        want = np.linalg.solve(dense, b.astype(np.float64))
+        cond = np.linalg.cond(np.diag(inv.astype(np.float64)) @ dense)
+        assert np.linalg.norm(x - want) <= 4 * rtol * cond * np.linalg.norm(want)
+        true_res = np.linalg.norm(b.astype(np.float64) - dense @ x.astype(np.float64))
+        assert res <= rtol * np.linalg.norm(b) * (1 + 1e-5)
+        assert abs(true_res - res) <= 1e-5 * np.linalg.norm(b) + 1e-3 * res
+
+
+@pytest.mark.parametrize("mode", ["blocks", "panels", "none"])
+def test_bicgstab_jacobi_routes_and_reproducible(mode):
+    A, b, inv = _scaled_convection(96, seed=2)
+    kw = {"plan": mode != "none",
+          "slice_mode": {"blocks": _capi.SLICE_OFF, "panels": _capi.SLICE_PANELS,
+                         "none": None}[mode]}
+    print(f"bicgstab jacobi route={mode} n={A.shape[0]}", flush=True)
+    r1 = _gpu_jacobi(A, b, inv, rtol=1e-4, maxiter=2000, **kw)
+    r2 = _gpu_jacobi(A, b, inv, rtol=1e-4, maxiter=2000, **kw)
+    assert r1[1:] == r2[1:] and r1[0].tobytes() == r2[0].tobytes()
+    wx, winfo, wres, wits = orc.csr_bicgstab_jacobi(*_args(A), b, inv, rtol=1e-4, maxiter=2000)
+    # BiCGSTAB's residual is not monotone: on this row-scaled system another
+    # rounding of the double dot products moves the tolerance crossing by a
+    # few percent of the iterations
+    assert r1[1] == winfo == 0 and abs(r1[3] - wits) <= max(2, wits // 20), (r1[3], wits)
+    assert np.linalg.norm(r1[0].astype(np.float64) - wx) <= 1e-2 * np.linalg.norm(wx)
+
+
+def test_bicgstab_jacobi_status_cases_match_oracle():
+    """The edge cases where the Jacobi loop differs from the plain one: a
+    non-finite b (status -3, residual +inf), a non-finite inverse diagonal
+    entry (-3 in the first iteration), plus a zero right-hand side, an exact
+    x0, maxiter 0 and 1."""
+    A = sp.csr_matrix(NONSYM)
+    inv = (1.0 / np.diag(NONSYM)).astype(np.float32)
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    bad_b = b.copy()
+    bad_b[2] = np.nan
+    bad_inv = inv.copy()
+    bad_inv[1] = np.inf
+    exact = np.linalg.solve(NONSYM, b).astype(np.float32)
+    bx = (NONSYM.astype(np.float64) @ exact).astype(np.float32)
+    cases = [(np.zeros(4, np.float32), inv, None, {}), (b, inv, None, {"maxiter": 0}),
+             (b, inv, None, {"maxiter": 1, "rtol": 1e-9}), (bad_b, inv, None, {}),
+             (b, bad_inv, None, {}), (bx, inv, exact, {"rtol": 1e-3}),
+             (b, inv, None, {"rtol": 1e-4, "atol": 1e-7, "maxiter": 80})]
+    for rhs, iv, x0, kw in cases:
+        x, info, res, its = _gpu_jacobi(A, rhs, iv, x0=x0, **kw)
+        wx, winfo, wres, wits = orc.csr_bicgstab_jacobi(*_args(A), rhs, iv, x0, **kw)
+        print(f"jacobi status case {kw}: gpu {info, its, res} oracle {winfo, wits, wres}",
+              flush=True)
+        assert (info, its) == (winfo, wits)
+        assert np.isinf(res) == np.isinf(wres) and np.isnan(res) == np.isnan(wres)
+        if np.isfinite(wres):
+            assert abs(res - wres) <= 1e-6 * max(1.0, abs(wres))
+
+
+def test_bicgstab_jacobi_api_on_gpu(gpu):
+    """linalg.bicgstab with M = preconditioners.jacobi(A) on the device: the
+    reference's GPU test (test_linalg_bicgstab.py:313-333) and its bounds."""
+    ms = gpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    A = sp.csr_matrix(NONSYM)
+    csr = ms.csr_array((A.data, A.indices.astype(np.int32), A.indptr.astype(np.int32)),
+                       shape=NONSYM.shape, canonical=True)
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    x, info = linalg.bicgstab(csr, b, M=preconditioners.jacobi(csr), rtol=1e-4, atol=1e-7,
+                              maxiter=80, return_info=True)
+    assert info.status == 0 and info.preconditioner == "jacobi" and x.device.type == "cuda"
+    xn = x.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(NONSYM @ xn - b) / max(np.linalg.norm(b), 1.0) < 2e-5

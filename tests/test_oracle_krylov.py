@@ -264,3 +264,124 @@ def test_minres_status_rules():
     bad[1] = np.inf
     assert orc.csr_minres(d, i, p, bad)[1] == -3
     assert orc.csr_minres(d, i, p, np.ones(4, np.float32), shift=float("nan"))[1] == -3
+
+
+# -- BiCGSTAB with a Jacobi preconditioner ---------------------------------------------
+#
+# oracle_csr_bicgstab_jacobi (reference src/preconditioners/bicgstab/
+# bicgstab.cpp:140-521) is pinned by: M = I reproducing the unpreconditioned
+# loop bit for bit; the closed form of a diagonal system (M = A^-1: one
+# iteration); the reference's own test system with its bounds
+# (tests/test_linalg_bicgstab.py:175-201, 313-333); SciPy's bicgstab with the
+# same M (the same right-preconditioned recurrences) on a badly row-scaled
+# system, where the preconditioner decides convergence; and the status rules
+# in which the reference's preconditioned loop differs from the plain one.
+
+def _inv_diag(A):
+    d = np.asarray(A.diagonal() if sp.issparse(A) else np.diag(A), np.float32)
+    return (np.float32(1.0) / d).astype(np.float32)
+
+
+@pytest.mark.parametrize("system", ["nonsym", "convection", "conv2d"])
+def test_bicgstab_jacobi_identity_matches_plain(system):
+    if system == "nonsym":
+        A, b, kw = NONSYM, np.array([1.0, 2.0, 3.0, 4.0], np.float32), dict(rtol=1e-6, atol=1e-7)
+        args = _csr(A)
+    elif system == "convection":
+        A, b, kw = convection_diffusion(), np.linspace(0.25, 1.5, 6, dtype=np.float32), {}
+        args = _csr(A)
+    else:
+        A = convection_2d(16)
+        b = np.random.default_rng(2).uniform(-1, 1, A.shape[0]).astype(np.float32)
+        kw = dict(rtol=1e-4)
+        args = (A.data, A.indices, A.indptr)
+    ones = np.ones(len(b), np.float32)
+    xj, ij, rj, kj = orc.csr_bicgstab_jacobi(*args, b, ones, **kw)
+    xp, ip, rp, kp = orc.csr_bicgstab(*args, b, **kw)
+    assert (ij, kj) == (ip, kp) and ij == 0
+    np.testing.assert_array_equal(xj, xp)
+    assert rj == rp
+
+
+def test_bicgstab_jacobi_diagonal_system_one_step():
+    d = np.array([2.0, 0.5, 4.0, 8.0, 1.25], np.float32)
+    b = np.array([1.0, -2.0, 3.0, 0.5, 7.0], np.float32)
+    A = np.diag(d)
+    x, info, res, its = orc.csr_bicgstab_jacobi(*_csr(A), b, _inv_diag(A), rtol=1e-6)
+    assert (info, its) == (0, 1)
+    np.testing.assert_allclose(x, b / d, rtol=2e-7)
+    assert res <= 1e-6 * np.linalg.norm(b)
+    # the plain loop needs one step per distinct eigenvalue (up to 5)
+    _, info_p, _, its_p = orc.csr_bicgstab(*_csr(A), b, rtol=1e-6)
+    assert info_p == 0 and its_p > 1
+
+
+def test_bicgstab_jacobi_reference_system():
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    x, info, res, its = orc.csr_bicgstab_jacobi(*_csr(NONSYM), b, _inv_diag(NONSYM), rtol=1e-4,
+                                                atol=1e-7, maxiter=80)
+    assert info == 0 and its > 0
+    assert _rel_residual(NONSYM, x, b) < 2e-5
+    np.testing.assert_allclose(x, np.linalg.solve(NONSYM, b), rtol=8e-5, atol=8e-5)
+
+
+def test_bicgstab_jacobi_row_scaled_against_scipy():
+    A0 = convection_2d(20)
+    n = A0.shape[0]
+    rng = np.random.default_rng(9)
+    scale = np.float32(10.0) ** rng.uniform(-2, 2, n).astype(np.float32)
+    A = (sp.diags(scale) @ A0).tocsr().astype(np.float32)
+    A.sort_indices()
+    b = (scale * rng.uniform(-1, 1, n)).astype(np.float32)
+    inv = _inv_diag(A)
+    x, info, res, its = orc.csr_bicgstab_jacobi(A.data, A.indices, A.indptr, b, inv, rtol=1e-5,
+                                                maxiter=400)
+    assert info == 0
+    dense = A.toarray().astype(np.float64)
+    want = np.linalg.solve(dense, b.astype(np.float64))
+    cond = np.linalg.cond(np.diag(inv.astype(np.float64)) @ dense)
+    assert np.linalg.norm(x - want) <= 4e-5 * cond * np.linalg.norm(want)
+    assert abs(res - np.linalg.norm(b - dense @ x)) <= 1e-4 * res + 1e-6 * np.linalg.norm(b)
+    count = [0]
+    M = spla.LinearOperator((n, n), matvec=lambda v: inv.astype(np.float64) * v)
+    sx, sinfo = spla.bicgstab(A.astype(np.float64), b.astype(np.float64), rtol=1e-5, M=M,
+                              maxiter=400, callback=lambda _: count.__setitem__(0, count[0] + 1))
+    assert sinfo == 0
+    assert abs(its - count[0]) <= max(2, count[0] // 10), (its, count[0])
+    # without the preconditioner the same budget is far from enough
+    _, info_p, _, its_p = orc.csr_bicgstab(A.data, A.indices, A.indptr, b, rtol=1e-5,
+                                           maxiter=400)
+    assert info_p != 0 or its_p > 2 * its
+
+
+def test_bicgstab_jacobi_status_rules():
+    b = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    args = _csr(NONSYM)
+    inv = _inv_diag(NONSYM)
+    # zero right-hand side and exact x0: status 0 before the first iteration
+    x, info, res, its = orc.csr_bicgstab_jacobi(*args, np.zeros(4, np.float32), inv)
+    assert (info, its, res) == (0, 0, 0.0) and not x.any()
+    exact = np.linalg.solve(NONSYM.astype(np.float64), b).astype(np.float32)
+    bb = (NONSYM.astype(np.float64) @ exact).astype(np.float32)
+    _, info, _, its = orc.csr_bicgstab_jacobi(*args, bb, inv, x0=exact, rtol=1e-3)
+    assert (info, its) == (0, 0)
+    # maxiter 0: the budget status (1) and the true residual of x0
+    _, info, res, its = orc.csr_bicgstab_jacobi(*args, b, inv, maxiter=0)
+    assert (info, its) == (1, 0) and res == np.float32(np.linalg.norm(b))
+    # non-finite right-hand side: -3 before any residual (reported +inf),
+    # where the plain loop reports the residual it computed
+    bad = b.copy()
+    bad[2] = np.nan
+    _, info, res, its = orc.csr_bicgstab_jacobi(*args, bad, inv)
+    assert (info, its) == (-3, 0) and res == np.inf
+    _, info_p, res_p, _ = orc.csr_bicgstab(*args, bad)
+    assert info_p == -3 and not np.isinf(res_p)
+    # a non-finite preconditioner entry: p_hat is non-finite in iteration 1
+    inv_bad = inv.copy()
+    inv_bad[1] = np.inf
+    _, info, res, its = orc.csr_bicgstab_jacobi(*args, b, inv_bad)
+    assert (info, its) == (-3, 0) and res == np.float32(np.linalg.norm(b))
+    # a budget that ends before convergence: status = maxiter, true residual
+    x, info, res, its = orc.csr_bicgstab_jacobi(*args, b, inv, rtol=1e-7, atol=0.0, maxiter=1)
+    assert (info, its) == (1, 1)
+    assert res == pytest.approx(np.linalg.norm(b - NONSYM.astype(np.float64) @ x), rel=1e-5)
