@@ -625,6 +625,28 @@ msx_status msx_csr_minres(msx_itype it, int64_t n, int64_t nnz,
                           msx_solver_result *result, void *stream);
 
 /*
+ * MINRES with the Jacobi preconditioner M = diag(inv_diag) (inv_diag: n
+ * device floats, each > 0): msx_csr_minres's device loop with the Lanczos
+ * vectors normalised in the M inner product (y = M r2, beta^2 = r2.y).  As
+ * the reference's Jacobi loop: an inverse diagonal entry that is not > 0
+ * stops the start with -2 (after the non-finite test, before the
+ * convergence test), and a non-finite or non-positive r2.y gives -2.
+ *
+ * Replaces CSRMINRESJacobi::eval_gpu (reference:
+ * src/preconditioners/minres/minres.cpp:359-410, a single-threadgroup
+ * kernel of minres.metal) with the arithmetic of csr_minres_jacobi_cpu_impl
+ * (minres.cpp:93-330).
+ */
+msx_status msx_csr_minres_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                 const float *data, const void *indices,
+                                 const void *indptr, const float *b,
+                                 const float *x0, const float *inv_diag,
+                                 float *x, float rtol, float atol,
+                                 int64_t maxiter, float shift,
+                                 const msx_csr_plan *plan,
+                                 msx_solver_result *result, void *stream);
+
+/*
  * Restarted GMRES for a square float32 CSR matrix (n x n, not necessarily
  * symmetric): x from x0 (device pointers; x0 and x may not overlap).
  * Each cycle of at most `restart` Arnoldi steps (and at most the budget
@@ -670,8 +692,9 @@ msx_status msx_csr_pcg_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
                                   float *x, float rtol, float atol,
                                   int64_t maxiter, msx_solver_result *result);
 /* csr_bicgstab_cpu_impl (bicgstab.cpp:80-362), csr_bicgstab_jacobi_cpu_impl
- * (src/preconditioners/bicgstab/bicgstab.cpp:140-521) and
- * csr_minres_cpu_impl (minres.cpp:93-312), one thread. */
+ * (src/preconditioners/bicgstab/bicgstab.cpp:140-521), csr_minres_cpu_impl
+ * (minres.cpp:93-312) and csr_minres_jacobi_cpu_impl
+ * (src/preconditioners/minres/minres.cpp:93-330), one thread. */
 msx_status msx_csr_bicgstab_cpu(msx_itype it, int64_t n, int64_t nnz,
                                 const float *data, const void *indices,
                                 const void *indptr, const float *b,
@@ -690,6 +713,13 @@ msx_status msx_csr_minres_cpu(msx_itype it, int64_t n, int64_t nnz,
                               const float *x0, float *x, float rtol,
                               float atol, int64_t maxiter, float shift,
                               msx_solver_result *result);
+msx_status msx_csr_minres_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                     const float *data, const void *indices,
+                                     const void *indptr, const float *b,
+                                     const float *x0, const float *inv_diag,
+                                     float *x, float rtol, float atol,
+                                     int64_t maxiter, float shift,
+                                     msx_solver_result *result);
 /* csr_gmres_impl (gmres.cpp:58-220) over csr_arnoldi_cpu_impl
  * (arnoldi.cpp:79-159), one thread. */
 msx_status msx_csr_gmres_cpu(msx_itype it, int64_t n, int64_t nnz,

@@ -502,10 +502,13 @@ __device__ inline void mr_stop(MrState *st, int32_t status, int32_t completed) {
 }
 
 // r2 = b - (A x - shift x) (minres.cpp:68-91, 186-191).  Slots: b.b, r2.r2,
-// non-finite count.
+// non-finite count; J (the Jacobi loop, preconditioners/minres/
+// minres.cpp:93-330): also y = inv_diag r2 and slot 3 r2.y.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     mr_start(const float *__restrict__ b, const float *__restrict__ x, const float *__restrict__ ax,
-             float shift, float *__restrict__ r2, int64_t n, double *part) {
+             float shift, const float *__restrict__ inv_diag, float *__restrict__ r2,
+             float *__restrict__ y, int64_t n, double *part) {
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
   MSX_SOLVER_LOOP({
     const float ai = ax[i] - shift * x[i];
@@ -514,16 +517,36 @@ __global__ void __launch_bounds__(kSolverThreads)
     v[0] += static_cast<double>(b[i]) * static_cast<double>(b[i]);
     v[1] += static_cast<double>(ri) * static_cast<double>(ri);
     if (!(fin(ai) && fin(ri))) v[2] += 1.0;
+    if constexpr (J) {
+      const float yi = inv_diag[i] * ri;
+      y[i] = yi;
+      v[3] += static_cast<double>(ri) * static_cast<double>(yi);
+    }
   })
   write_partials(v, part);
 }
 
-// minres.cpp:160-210.
+// The Jacobi loop's preconditioner test (minres.cpp:160-166 there): slot 0
+// counts the inverse diagonal entries that are not > 0.
 __global__ void __launch_bounds__(kSolverThreads)
-    mr_decide_start(const double *part, int nparts, float rtol, float atol, int64_t maxiter,
-                    MrState *st) {
-  double t[kSlots];
+    mr_diag_check(const float *__restrict__ inv_diag, int64_t n, double *part) {
+  double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  MSX_SOLVER_LOOP({
+    if (!(inv_diag[i] > 0.0f)) v[0] += 1.0;
+  })
+  write_partials(v, part);
+}
+
+// minres.cpp:160-210.  J: a preconditioner entry not > 0 stops the start
+// with -2 (after the non-finite test, before the convergence test); beta
+// from r2.y, and its failure is -2.
+template <bool J>
+__global__ void __launch_bounds__(kSolverThreads)
+    mr_decide_start(const double *part, const double *diag_part, int nparts, float rtol,
+                    float atol, int64_t maxiter, MrState *st) {
+  double t[kSlots], dg[kSlots] = {0.0, 0.0, 0.0, 0.0};
   read_totals(part, nparts, t);
+  if (J) read_totals(diag_part, nparts, dg);
   if (threadIdx.x != 0) return;
   const float b_norm = static_cast<float>(sqrt(max0(t[0])));
   const float scaled = rtol * b_norm;
@@ -535,6 +558,10 @@ __global__ void __launch_bounds__(kSolverThreads)
     mr_stop(st, -3, 0);
     return;
   }
+  if (J && dg[0] != 0.0) {
+    mr_stop(st, -2, 0);
+    return;
+  }
   if (st->residual <= st->tol) {
     mr_stop(st, 0, 0);
     return;
@@ -543,9 +570,9 @@ __global__ void __launch_bounds__(kSolverThreads)
     mr_stop(st, budget, 0);
     return;
   }
-  const double beta_sq = static_cast<double>(static_cast<float>(t[1]));
+  const double beta_sq = static_cast<double>(static_cast<float>(J ? t[3] : t[1]));
   if (!fin(beta_sq) || beta_sq <= 0.0) {
-    mr_stop(st, -1, 0);
+    mr_stop(st, J ? -2 : -1, 0);
     return;
   }
   const double beta = sqrt(beta_sq);
@@ -570,7 +597,9 @@ __device__ inline bool mr_close(const double (&t)[kSlots], int32_t k, MrState *s
   return true;
 }
 
-// Closes iteration k - 1, then v = r2 / beta (minres.cpp:212-222).
+// Closes iteration k - 1, then v = r2 / beta (minres.cpp:212-222); J: `r2`
+// is y = M r2, and a failed beta test is -2.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     mr_v(const float *__restrict__ r2, float *__restrict__ v, int64_t n, int32_t k,
          const double *res_part, int nparts, MrState *st) {
@@ -587,7 +616,7 @@ __global__ void __launch_bounds__(kSolverThreads)
   }
   const double beta = st->g[(k - 1) & 1].beta;
   if (!fin(beta) || beta <= kEps) {
-    if (lead()) mr_stop(st, -1, k - 1);
+    if (lead()) mr_stop(st, J ? -2 : -1, k - 1);
     return;
   }
   const double inv_beta = 1.0 / beta;
@@ -630,15 +659,21 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // alfa; av -= (alfa / beta) r2 (minres.cpp:238-246); the new r2's norm.
+// J: also y = inv_diag av, and the sum is av.y.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
-    mr_b(float *__restrict__ av, const float *__restrict__ r2, int64_t n, int32_t k,
-         const double *a_part, double *part, int nparts, MrState *st) {
+    mr_b(float *__restrict__ av, const float *__restrict__ r2, const float *__restrict__ inv_diag,
+         float *__restrict__ y, int64_t n, int32_t k, const double *a_part, double *part,
+         int nparts, MrState *st) {
   if (!st->running) return;
+  constexpr int NV = J ? 3 : 2;
   double pin[kSlots];
   load_partials(a_part, nparts, pin);
-  const float *const vec[2] = {av, r2};
-  Round<2> first;
-  load_round<2>(vec, first_base(), n, first);
+  const float *vec[NV];
+  vec[0] = av, vec[1] = r2;
+  if constexpr (J) vec[2] = inv_diag;
+  Round<NV> first;
+  load_round<NV>(vec, first_base(), n, first);
   double t[kSlots];
   reduce_partials(pin, nparts, t);
   const double alfa = static_cast<double>(static_cast<float>(t[0]));
@@ -648,17 +683,24 @@ __global__ void __launch_bounds__(kSolverThreads)
   }
   const float diag_scale = static_cast<float>(alfa / st->g[(k - 1) & 1].beta);
   double acc[kSlots] = {0.0, 0.0, 0.0, 0.0};
-  for_rounds<2>(vec, n, first, [&](int64_t i, const float(&e)[2]) {
+  for_rounds<NV>(vec, n, first, [&](int64_t i, const float(&e)[NV]) {
     const float a = e[0] - diag_scale * e[1];
     av[i] = a;
-    acc[0] += static_cast<double>(a) * static_cast<double>(a);
+    if constexpr (J) {
+      const float yi = e[2] * a;
+      y[i] = yi;
+      acc[0] += static_cast<double>(a) * static_cast<double>(yi);
+    } else {
+      acc[0] += static_cast<double>(a) * static_cast<double>(a);
+    }
   });
   write_partials(acc, part);
 }
 
 // The next Givens rotation (minres.cpp:248-275), then w and x
 // (minres.cpp:277-290).  The new w is written over w2 (the host swaps the
-// two).  Slots: non-finite count.
+// two).  Slots: non-finite count.  J: a failed beta test is -2.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     mr_x(const float *__restrict__ v, const float *__restrict__ w, float *__restrict__ w2,
          float *__restrict__ x, int64_t n, int32_t k, const double *a_part,
@@ -677,7 +719,7 @@ __global__ void __launch_bounds__(kSolverThreads)
   const double alfa = static_cast<double>(static_cast<float>(ta[0]));
   const double beta_sq = static_cast<double>(static_cast<float>(tb[0]));
   if (!fin(beta_sq) || beta_sq < 0.0) {
-    if (lead()) mr_stop(st, -1, k - 1);
+    if (lead()) mr_stop(st, J ? -2 : -1, k - 1);
     return;
   }
   Givens h;
@@ -939,18 +981,23 @@ msx_status bicgstab(const System &s, const float *b, const float *x0, const floa
   return MSX_OK;
 }
 
-msx_status minres(const System &s, const float *b, const float *x0, float *x, float rtol,
-                  float atol, int64_t maxiter, float shift, msx_solver_result *result) {
+// J: the Jacobi loop, inv_diag non-null (y = M r2 in one more vector).
+template <bool J>
+msx_status minres(const System &s, const float *b, const float *x0, const float *inv_diag,
+                  float *x, float rtol, float atol, int64_t maxiter, float shift,
+                  msx_solver_result *result) {
   const int64_t n = s.n;
   Scratch sc;
   sc.stream = s.stream;
-  msx_status e = sc.alloc(n, 7, 5);
+  msx_status e = sc.alloc(n, J ? 8 : 7, J ? 6 : 5);
   if (e != MSX_OK) return e;
   float *r1 = sc.vector(0), *r2 = sc.vector(1), *av = sc.vector(2), *v = sc.vector(3),
         *w = sc.vector(4), *w2 = sc.vector(5), *q = sc.vector(6);
+  float *y = J ? sc.vector(7) : nullptr;
   auto *st = static_cast<MrState *>(sc.state());
   double *start_part = sc.part(0), *a_part = sc.part(1), *b_part = sc.part(2),
          *x_part = sc.part(3), *res_part = sc.part(4);
+  double *diag_part = J ? sc.part(5) : start_part;
   const int np = s.nparts;
   MrState host{};
 
@@ -958,9 +1005,11 @@ msx_status minres(const System &s, const float *b, const float *x0, float *x, fl
   for (float *z : {r1, w, w2}) hipLaunchKernelGGL(zero_vec, s.grid, s.block, 0, s.stream, z, n);
   MSX_HIP_TRY(hipGetLastError());
   if ((e = spmv(s, x, av)) != MSX_OK) return e;
-  hipLaunchKernelGGL(mr_start, s.grid, s.block, 0, s.stream, b, x, av, shift, r2, n, start_part);
-  hipLaunchKernelGGL(mr_decide_start, dim3(1), s.block, 0, s.stream, start_part, np, rtol, atol,
-                     maxiter, st);
+  hipLaunchKernelGGL(mr_start<J>, s.grid, s.block, 0, s.stream, b, x, av, shift, inv_diag, r2, y,
+                     n, start_part);
+  if (J) hipLaunchKernelGGL(mr_diag_check, s.grid, s.block, 0, s.stream, inv_diag, n, diag_part);
+  hipLaunchKernelGGL(mr_decide_start<J>, dim3(1), s.block, 0, s.stream, start_part, diag_part, np,
+                     rtol, atol, maxiter, st);
   MSX_HIP_TRY(hipGetLastError());
   if ((e = read_state(s, st, &host)) != MSX_OK) return e;
   int64_t next = 1;
@@ -970,13 +1019,14 @@ msx_status minres(const System &s, const float *b, const float *x0, float *x, fl
     const int64_t last = std::min(maxiter, next + batch - 1);
     for (int64_t k = next; k <= last; ++k) {
       const auto kk = static_cast<int32_t>(k);
-      hipLaunchKernelGGL(mr_v, s.grid, s.block, 0, s.stream, r2, v, n, kk, res_part, np, st);
+      hipLaunchKernelGGL(mr_v<J>, s.grid, s.block, 0, s.stream, J ? y : r2, v, n, kk, res_part,
+                         np, st);
       MSX_HIP_TRY(hipGetLastError());
       if ((e = spmv(s, v, av)) != MSX_OK) return e;
       hipLaunchKernelGGL(mr_a, s.grid, s.block, 0, s.stream, v, av, r1, shift, n, kk, a_part, st);
-      hipLaunchKernelGGL(mr_b, s.grid, s.block, 0, s.stream, av, r2, n, kk, a_part, b_part, np,
-                         st);
-      hipLaunchKernelGGL(mr_x, s.grid, s.block, 0, s.stream, v, w, w2, x, n, kk, a_part, b_part,
+      hipLaunchKernelGGL(mr_b<J>, s.grid, s.block, 0, s.stream, av, r2, inv_diag, y, n, kk, a_part,
+                         b_part, np, st);
+      hipLaunchKernelGGL(mr_x<J>, s.grid, s.block, 0, s.stream, v, w, w2, x, n, kk, a_part, b_part,
                          x_part, np, st);
       MSX_HIP_TRY(hipGetLastError());
       // the Lanczos vectors move on (r1 <- r2 <- av) and w2 <- w <- new w
@@ -1071,5 +1121,25 @@ extern "C" msx_status msx_csr_minres(msx_itype it, int64_t n, int64_t nnz, const
   const uint32_t blocks = blocks_for(n);
   const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
                  dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
-  return minres(s, b, x0, x, rtol, atol, maxiter, shift, result);
+  return minres<false>(s, b, x0, nullptr, x, rtol, atol, maxiter, shift, result);
+}
+
+extern "C" msx_status msx_csr_minres_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                            const float *data, const void *indices,
+                                            const void *indptr, const float *b, const float *x0,
+                                            const float *inv_diag, float *x, float rtol,
+                                            float atol, int64_t maxiter, float shift,
+                                            const msx_csr_plan *plan, msx_solver_result *result,
+                                            void *stream) {
+  clear_error();
+  msx_status st =
+      check("csr_minres_jacobi", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
+  if (st != MSX_OK) return st;
+  if (inv_diag == nullptr) return fail(MSX_EINVAL, "csr_minres_jacobi buffers must be non-NULL.");
+  st = check_plan("csr_minres_jacobi", plan, MSX_F32, it, n, n, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  const uint32_t blocks = blocks_for(n);
+  const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
+                 dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
+  return minres<true>(s, b, x0, inv_diag, x, rtol, atol, maxiter, shift, result);
 }

@@ -6,6 +6,8 @@
 //   msx_csr_bicgstab_jacobi_cpu  left_preconditioned_bicgstab_host with the
 //                         Jacobi apply (reference:
 //                         src/preconditioners/bicgstab/bicgstab.cpp:140-521)
+//   msx_csr_minres_jacobi_cpu  csr_minres_jacobi_cpu_impl (reference:
+//                         src/preconditioners/minres/minres.cpp:93-330)
 //   msx_csr_minres_cpu    csr_minres_cpu_impl (reference:
 //                         src/linalg/minres/minres.cpp:68-312)
 //
@@ -243,10 +245,20 @@ void bicgstab(const Csr<I> &A, const float *b, const float *x0, float *x, float 
 }
 
 template <class I>
-void minres(const Csr<I> &A, const float *b, const float *x0, float *x, float rtol, float atol,
-            int64_t maxiter, float shift, msx_solver_result *res) {
+void minres(const Csr<I> &A, const float *b, const float *x0, const float *inv_diag, float *x,
+            float rtol, float atol, int64_t maxiter, float shift, msx_solver_result *res) {
   const int64_t n = A.n;
   Vec r1(n, 0.0f), r2(n, 0.0f), v(n, 0.0f), w(n, 0.0f), w2(n, 0.0f), av(n, 0.0f);
+  // Jacobi (inv_diag non-null, src/preconditioners/minres/minres.cpp:93-330):
+  // y = M r2 in float, a non-positive inverse diagonal entry or preconditioned
+  // product gives -2
+  Vec y(inv_diag ? n : 0, 0.0f);
+  const int32_t beta_fail = inv_diag ? -2 : -1;
+  auto precondition = [&]() -> const Vec & {
+    if (!inv_diag) return r2;
+    for (int64_t i = 0; i < n; ++i) y[i] = inv_diag[i] * r2[i];
+    return y;
+  };
   std::copy(x0, x0 + n, x);
   double bb = 0.0;
   for (int64_t i = 0; i < n; ++i) bb += static_cast<double>(b[i]) * static_cast<double>(b[i]);
@@ -276,15 +288,24 @@ void minres(const Csr<I> &A, const float *b, const float *x0, float *x, float rt
     *res = {-3, 0, residual, 0};
     return;
   }
+  if (inv_diag) {
+    for (int64_t i = 0; i < n; ++i) {
+      if (!(inv_diag[i] > 0.0f)) {
+        *res = {-2, 0, residual, 0};
+        return;
+      }
+    }
+  }
   if (residual <= tol || maxiter == 0) {
     *res = {residual <= tol ? 0 : status, 0, residual, 0};
     return;
   }
-  // r2 = y = b - (A - shift I) x (y is a copy of r2 throughout)
+  // r2 = b - (A - shift I) x, y = M r2 (plain: y is r2 throughout)
   for (int64_t i = 0; i < n; ++i) r2[i] = b[i] - (av[i] - shift * x[i]);
-  double beta_sq = static_cast<double>(static_cast<float>(dot(r2, r2)));
+  const Vec *yv = &precondition();
+  double beta_sq = static_cast<double>(static_cast<float>(dot(r2, *yv)));
   if (!fin(beta_sq) || beta_sq <= 0.0) {
-    *res = {-1, 0, residual, 0};
+    *res = {beta_fail, 0, residual, 0};
     return;
   }
   const double eps = FLT_EPSILON;
@@ -292,11 +313,12 @@ void minres(const Csr<I> &A, const float *b, const float *x0, float *x, float rt
   double cs = -1.0, sn = 0.0;
   for (int64_t k = 1; k <= maxiter; ++k) {
     if (!fin(beta) || beta <= eps) {
-      status = -1;
+      status = beta_fail;
       break;
     }
     const double inv_beta = 1.0 / beta;
-    for (int64_t i = 0; i < n; ++i) v[i] = static_cast<float>(inv_beta * static_cast<double>(r2[i]));
+    const Vec &yy = inv_diag ? y : r2;
+    for (int64_t i = 0; i < n; ++i) v[i] = static_cast<float>(inv_beta * static_cast<double>(yy[i]));
     A.apply(v.data(), av.data());
     for (int64_t i = 0; i < n; ++i) av[i] -= shift * v[i];
     if (k >= 2) {
@@ -317,10 +339,11 @@ void minres(const Csr<I> &A, const float *b, const float *x0, float *x, float rt
     // the Lanczos vectors move on: r1 <- r2 <- A v (the old r1 is scratch)
     std::swap(r1, r2);
     std::swap(r2, av);
+    yv = &precondition();
     oldb = beta;
-    beta_sq = static_cast<double>(static_cast<float>(dot(r2, r2)));
+    beta_sq = static_cast<double>(static_cast<float>(dot(r2, *yv)));
     if (!fin(beta_sq) || beta_sq < 0.0) {
-      status = -1;
+      status = beta_fail;
       break;
     }
     beta = std::sqrt(std::max(beta_sq, 0.0));
@@ -687,13 +710,40 @@ extern "C" msx_status msx_csr_minres_cpu(msx_itype it, int64_t n, int64_t nnz, c
     if (it == MSX_I32)
       minres(Csr<int32_t>{n, data, static_cast<const int32_t *>(indices),
                           static_cast<const int32_t *>(indptr)},
-             b, x0, x, rtol, atol, maxiter, shift, result);
+             b, x0, nullptr, x, rtol, atol, maxiter, shift, result);
     else
       minres(Csr<int64_t>{n, data, static_cast<const int64_t *>(indices),
                           static_cast<const int64_t *>(indptr)},
-             b, x0, x, rtol, atol, maxiter, shift, result);
+             b, x0, nullptr, x, rtol, atol, maxiter, shift, result);
   } catch (const std::bad_alloc &) {
     return msx::fail(MSX_ENOMEM, "csr_minres: out of host memory.");
+  }
+  return MSX_OK;
+}
+
+extern "C" msx_status msx_csr_minres_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                                const float *data, const void *indices,
+                                                const void *indptr, const float *b,
+                                                const float *x0, const float *inv_diag, float *x,
+                                                float rtol, float atol, int64_t maxiter,
+                                                float shift, msx_solver_result *result) {
+  msx::clear_error();
+  msx_status st =
+      check("csr_minres_jacobi", it, n, nnz, data, indices, indptr, b, x0, x, maxiter, result);
+  if (st != MSX_OK) return st;
+  if (inv_diag == nullptr)
+    return msx::fail(MSX_EINVAL, "csr_minres_jacobi buffers must be non-NULL.");
+  try {
+    if (it == MSX_I32)
+      minres(Csr<int32_t>{n, data, static_cast<const int32_t *>(indices),
+                          static_cast<const int32_t *>(indptr)},
+             b, x0, inv_diag, x, rtol, atol, maxiter, shift, result);
+    else
+      minres(Csr<int64_t>{n, data, static_cast<const int64_t *>(indices),
+                          static_cast<const int64_t *>(indptr)},
+             b, x0, inv_diag, x, rtol, atol, maxiter, shift, result);
+  } catch (const std::bad_alloc &) {
+    return msx::fail(MSX_ENOMEM, "csr_minres_jacobi: out of host memory.");
   }
   return MSX_OK;
 }

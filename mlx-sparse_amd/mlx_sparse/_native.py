@@ -124,6 +124,14 @@ def csr_minres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, ato
                                   maxiter, shift, plan=plan)
 
 
+def csr_minres_jacobi(data, indices, indptr, b, x0, inv_diag, shape: Shape2D, *, rtol: float,
+                      atol: float, maxiter: int, shift: float = 0.0, plan=None):
+    """(x, info, residual, iterations) of Jacobi-preconditioned MINRES on
+    (A - shift I) x = b (reference: mlx_sparse/_native.py csr_minres_jacobi)."""
+    return extension().csr_minres_jacobi(data, indices, indptr, b, x0, inv_diag, shape[0],
+                                         shape[1], rtol, atol, maxiter, shift, plan=plan)
+
+
 def csr_gmres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol: float,
               restart: int, maxiter: int, plan=None):
     """(x, info, residual, iterations) of restarted GMRES (reference:

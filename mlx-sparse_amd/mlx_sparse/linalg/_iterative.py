@@ -149,8 +149,9 @@ def _system(A, b, x0, maxiter, solver: str):
 
 
 # Solvers with a Jacobi-preconditioned loop (the reference's native
-# diagonal paths: mlx_sparse/linalg/_iterative.py:437-461 csr_bicgstab_jacobi).
-_JACOBI_SOLVERS = {"bicgstab"}
+# diagonal paths: mlx_sparse/linalg/_iterative.py:437-461 csr_bicgstab_jacobi,
+# :1086-1110 csr_minres_jacobi).
+_JACOBI_SOLVERS = {"bicgstab", "minres"}
 
 
 def _preconditioner(M, csr, solver: str, device):
@@ -159,7 +160,14 @@ def _preconditioner(M, csr, solver: str, device):
     Jacobi loop; other kinds raise."""
     if M is None:
         return None, None, None
-    pc = _pc.aspreconditioner(M, csr)
+    minres_text = ("minres currently supports only identity, diagonal, and Jacobi "
+                   "symmetric positive-definite native-backed preconditioners.")
+    try:
+        pc = _pc.aspreconditioner(M, csr)
+    except TypeError:
+        if solver == "minres" and not isinstance(M, CSRArray):
+            raise TypeError(minres_text) from None  # the reference's text (:1118-1122)
+        raise
     if isinstance(pc, _pc.IdentityPreconditioner):
         return pc.kind, pc, None
     if isinstance(pc, _pc.DiagonalPreconditioner) and solver in _JACOBI_SOLVERS:
@@ -167,6 +175,8 @@ def _preconditioner(M, csr, solver: str, device):
             raise ValueError("preconditioner size does not match the matrix.")
         inv = pc.inverse_diagonal.to(device=device, dtype=torch.float32).contiguous()
         return pc.kind, pc, inv
+    if solver == "minres":
+        raise TypeError(minres_text)
     supported = "identity and diagonal/Jacobi" if solver in _JACOBI_SOLVERS else "identity"
     raise TypeError(f"{solver} in this build supports only the {supported} preconditioners; "
                     f"got {pc.kind}.")
@@ -219,15 +229,30 @@ def minres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, shift: float
     Two SpMVs per iteration (the Lanczos step and the true residual the
     reference tests every iteration).  Stops when
     ``||b - (A - shift I) x|| <= max(rtol * ||b||, atol)``.  ``maxiter``
-    defaults to ``10 * n``.  Returns ``(x, info)`` as :func:`bicgstab` does.
+    defaults to ``10 * n``.  ``M``: ``None``, ``preconditioners.identity``
+    or a diagonal/Jacobi preconditioner, which must be symmetric positive
+    definite (checked unless ``check_preconditioner=False``; the loop then
+    ends with -2 on a non-positive entry).  Returns ``(x, info)`` as
+    :func:`bicgstab` does, plus -2: a non-positive preconditioned product.
     """
     csr, rhs, guess, maxiter_value, device = _system(A, b, x0, maxiter, "minres")
     shift_value = _finite_scalar("shift", shift)
-    kind, _, _ = _preconditioner(M, csr, "minres", device)
+    kind, pc, inv_diag = _preconditioner(M, csr, "minres", device)
     data, indices, indptr = csr.buffers(device)
-    x, info, residual, iterations = _native.csr_minres(
-        data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
-        maxiter=maxiter_value, shift=shift_value, plan=csr.plan(device))
+    if inv_diag is None:
+        x, info, residual, iterations = _native.csr_minres(
+            data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
+            maxiter=maxiter_value, shift=shift_value, plan=csr.plan(device))
+    else:
+        # reference: mlx_sparse/linalg/_iterative.py:1087-1096
+        if check_preconditioner and (not pc.is_symmetric
+                                     or not bool(torch.isfinite(inv_diag).all())
+                                     or not bool((inv_diag > 0.0).all())):
+            raise ValueError("minres requires a symmetric positive-definite preconditioner; "
+                             "diagonal inverse entries must be finite and strictly positive.")
+        x, info, residual, iterations = _native.csr_minres_jacobi(
+            data, indices, indptr, rhs, guess, inv_diag, csr.shape, rtol=float(rtol),
+            atol=float(atol), maxiter=maxiter_value, shift=shift_value, plan=csr.plan(device))
     return finish(x, info, residual, iterations, solver="minres", return_info=bool(return_info),
                   callback=callback, rtol=float(rtol), atol=float(atol), maxiter=maxiter_value,
                   preconditioner=kind)

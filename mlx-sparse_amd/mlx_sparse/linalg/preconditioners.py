@@ -19,6 +19,7 @@ from mlx_sparse._validation import ensure_array
 class IdentityPreconditioner:
     shape: tuple[int, int]
     kind: str = "identity"
+    is_symmetric: bool = True
 
     def __call__(self, x):
         return x
@@ -29,6 +30,7 @@ class DiagonalPreconditioner:
     inverse_diagonal: torch.Tensor
     shape: tuple[int, int]
     kind: str = "diagonal"
+    is_symmetric: bool = True
 
     def __call__(self, x):
         return self.inverse_diagonal * x if x.ndim == 1 else self.inverse_diagonal[:, None] * x

@@ -821,6 +821,19 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("shift") = 0.0f, py::arg("plan") = py::none(),
       "MINRES on (A - shift I) x = b: (x, info, residual, iterations).");
   m.def(
+      "csr_minres_jacobi",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         py::handle inv_diag, int64_t n_rows, int64_t n_cols, float rtol, float atol,
+         int64_t maxiter, float shift, py::object plan) {
+        return solve_krylov(msx::Krylov::MINRES, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, shift, plan, 0,
+                            py::reinterpret_borrow<py::object>(inv_diag));
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
+      py::arg("atol"), py::arg("maxiter"), py::arg("shift") = 0.0f, py::arg("plan") = py::none(),
+      "Jacobi-preconditioned MINRES on (A - shift I) x = b: (x, info, residual, iterations).");
+  m.def(
       "csr_gmres",
       [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
          int64_t n_rows, int64_t n_cols, float rtol, float atol, int64_t restart, int64_t maxiter,

@@ -83,6 +83,15 @@ msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView
       check_status(msx_csr_bicgstab_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, xx,
                                         rtol, atol, maxiter, &res),
                    op.c_str());
+  } else if (kind == Krylov::MINRES && inv) {
+    if (data.device >= 0)
+      check_status(msx_csr_minres_jacobi(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, inv,
+                                         xx, rtol, atol, maxiter, shift, plan, &res, ctx.stream),
+                   op.c_str());
+    else
+      check_status(msx_csr_minres_jacobi_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0,
+                                             inv, xx, rtol, atol, maxiter, shift, &res),
+                   op.c_str());
   } else if (inv) {
     throw std::invalid_argument(op + " is not available.");
   } else if (kind == Krylov::GMRES) {

@@ -33,8 +33,9 @@
  *   - BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
  *     and MINRES with its shift (src/linalg/minres/minres.cpp:68-312,
  *     csr_minres_cpu_impl), float32;
- *   - BiCGSTAB with a Jacobi preconditioner
- *     (src/preconditioners/bicgstab/bicgstab.cpp:140-521), float32;
+ *   - BiCGSTAB and MINRES with a Jacobi preconditioner
+ *     (src/preconditioners/bicgstab/bicgstab.cpp:140-521,
+ *     src/preconditioners/minres/minres.cpp:93-330), float32;
  *   - restarted GMRES (src/linalg/gmres/gmres.cpp:58-220, csr_gmres_impl)
  *     with its Arnoldi factorisation (src/linalg/arnoldi/arnoldi.cpp:79-159,
  *     csr_arnoldi_cpu_impl) and the Givens least-squares solve
@@ -1451,10 +1452,17 @@ static float mr_true_residual(int it, int64_t n, const float *data, const void *
   return norm;
 }
 
-int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
-                      const void *indptr, const float *b, const float *x0, float *x, float rtol,
-                      float atol, int64_t maxiter, float shift, int32_t *info, float *residual,
-                      int32_t *iterations) {
+/* MINRES, plain (inv_diag NULL) or with the Jacobi preconditioner
+ * M = diag(inv_diag) (src/preconditioners/minres/minres.cpp:93-330,
+ * csr_minres_jacobi_cpu_impl): there y = M r2 in float instead of y = r2;
+ * an inverse diagonal entry that is not > 0 stops the start with -2 (after
+ * the non-finite test, before the convergence test); and the non-positive
+ * or non-finite beta tests give -2 instead of -1. */
+static int minres_loop(int it, int64_t n, const float *data, const void *indices,
+                       const void *indptr, const float *b, const float *x0, const float *inv_diag,
+                       float *x, float rtol, float atol, int64_t maxiter, float shift,
+                       int32_t *info, float *residual, int32_t *iterations) {
+  const int32_t beta_fail = inv_diag ? -2 : -1;
   const size_t bytes = (size_t)(n > 0 ? n : 1) * sizeof(float);
   float *r1 = (float *)calloc(1, bytes), *r2 = (float *)calloc(1, bytes);
   float *y = (float *)calloc(1, bytes), *v = (float *)calloc(1, bytes);
@@ -1479,6 +1487,14 @@ int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
     status = -3;
     goto done;
   }
+  if (inv_diag) {
+    for (int64_t i = 0; i < n; ++i) {
+      if (!(inv_diag[i] > 0.0f)) {
+        status = -2;
+        goto done;
+      }
+    }
+  }
   if (true_residual <= tol) {
     status = 0;
     goto done;
@@ -1488,11 +1504,11 @@ int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
     const float ai = av[i] - shift * x[i];
     const float ri = b[i] - ai;
     r2[i] = ri;
-    y[i] = ri;
+    y[i] = inv_diag ? inv_diag[i] * ri : ri;
   }
   double beta_inner = (double)(float)dot_d(r2, y, n);
   if (!isfinite(beta_inner) || beta_inner <= 0.0) {
-    status = -1;
+    status = beta_fail;
     goto done;
   }
   const double eps = (double)FLT_EPSILON;
@@ -1500,7 +1516,7 @@ int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
   double cs = -1.0, sn = 0.0;
   for (int64_t k = 1; k <= maxiter; ++k) {
     if (!isfinite(beta) || beta <= eps) {
-      status = -1;
+      status = beta_fail;
       break;
     }
     const double inv_beta = 1.0 / beta;
@@ -1522,16 +1538,16 @@ int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
     }
     const float diag_scale = (float)(alfa / beta);
     for (int64_t i = 0; i < n; ++i) av[i] = av[i] - diag_scale * r2[i];
-    /* r1 <- r2, r2 <- av, y = r2 (the old r1 becomes scratch) */
+    /* r1 <- r2, r2 <- av, y = M r2 (the old r1 becomes scratch) */
     float *old_r1 = r1;
     r1 = r2;
     r2 = av;
     av = old_r1;
-    memcpy(y, r2, (size_t)n * sizeof(float));
+    for (int64_t i = 0; i < n; ++i) y[i] = inv_diag ? inv_diag[i] * r2[i] : r2[i];
     oldb = beta;
     beta_inner = (double)(float)dot_d(r2, y, n);
     if (!isfinite(beta_inner) || beta_inner < 0.0) {
-      status = -1;
+      status = beta_fail;
       break;
     }
     beta = sqrt(max0(beta_inner));
@@ -1588,6 +1604,23 @@ done:
   *iterations = completed;
   free(r1); free(r2); free(y); free(v); free(w); free(w2); free(av);
   return 0;
+}
+
+int oracle_csr_minres(int it, int64_t n, const float *data, const void *indices,
+                      const void *indptr, const float *b, const float *x0, float *x, float rtol,
+                      float atol, int64_t maxiter, float shift, int32_t *info, float *residual,
+                      int32_t *iterations) {
+  return minres_loop(it, n, data, indices, indptr, b, x0, NULL, x, rtol, atol, maxiter, shift,
+                     info, residual, iterations);
+}
+
+int oracle_csr_minres_jacobi(int it, int64_t n, const float *data, const void *indices,
+                             const void *indptr, const float *b, const float *x0,
+                             const float *inv_diag, float *x, float rtol, float atol,
+                             int64_t maxiter, float shift, int32_t *info, float *residual,
+                             int32_t *iterations) {
+  return minres_loop(it, n, data, indices, indptr, b, x0, inv_diag, x, rtol, atol, maxiter, shift,
+                     info, residual, iterations);
 }
 
 /* ---------------------------------------------------------------------- */

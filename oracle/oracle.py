@@ -111,6 +111,9 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_minres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                            vp, vp, vp]
         _lib.oracle_csr_minres.restype = ci
+        _lib.oracle_csr_minres_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                                  i64, f32, vp, vp, vp]
+        _lib.oracle_csr_minres_jacobi.restype = ci
         _lib.oracle_csr_arnoldi.argtypes = [ci, i64, vp, vp, vp, vp, i64, vp, vp, vp]
         _lib.oracle_csr_arnoldi.restype = ci
         _lib.oracle_csr_gmres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
@@ -333,6 +336,26 @@ def csr_minres(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: f
                                  ctypes.addressof(its))
     if rc != 0:
         raise MemoryError("oracle_csr_minres failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_minres_jacobi(data, indices, indptr, b, inv_diag, x0=None, *, rtol: float = 1e-5,
+                      atol: float = 0.0, maxiter: int | None = None, shift: float = 0.0):
+    """MINRES with the Jacobi preconditioner M = diag(inv_diag) on
+    (A - shift I) x = b (reference src/preconditioners/minres/minres.cpp:93-330,
+    csr_minres_jacobi_cpu_impl).  Returns (x, info, residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    inv_diag = np.ascontiguousarray(inv_diag, np.float32)
+    assert inv_diag.shape == (n,)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_minres_jacobi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                        _ptr(indptr), _ptr(b), _ptr(x0), _ptr(inv_diag), _ptr(x),
+                                        rtol, atol, maxiter, shift, ctypes.addressof(info),
+                                        ctypes.addressof(res), ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_minres_jacobi failed")
     return x, info.value, res.value, its.value
 
 

@@ -111,6 +111,10 @@ def lib() -> ctypes.CDLL:
                                                   f32, i64, vp]
         L.msx_csr_minres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, f32,
                                          vp]
+        L.msx_csr_minres_jacobi.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                            i64, f32, vp, vp, vp]
+        L.msx_csr_minres_jacobi_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                                i64, f32, vp]
         L.msx_csr_gmres.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64, vp,
                                     vp, vp]
         L.msx_csr_gmres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
@@ -135,6 +139,7 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_cg_cpu", "msx_csr_pcg_jacobi_cpu", "msx_csr_bicgstab",
                      "msx_csr_minres", "msx_csr_bicgstab_cpu", "msx_csr_minres_cpu",
                      "msx_csr_bicgstab_jacobi", "msx_csr_bicgstab_jacobi_cpu",
+                     "msx_csr_minres_jacobi", "msx_csr_minres_jacobi_cpu",
                      "msx_csr_gmres", "msx_csr_gmres_cpu"):
             getattr(L, name).restype = ci
         _lib = L

@@ -121,8 +121,9 @@ def test_api_on_cpu_reference_systems(cpu):
         linalg.minres(csr(dense), np.ones(3, np.float32), shift=float("inf"))
     from mlx_sparse.linalg import preconditioners
 
-    with pytest.raises(TypeError, match="identity preconditioner"):
-        linalg.minres(csr(dense), np.ones(3, np.float32), M=preconditioners.jacobi(csr(dense)))
+    x, info = linalg.minres(csr(dense), np.ones(3, np.float32),
+                            M=preconditioners.jacobi(csr(dense)), rtol=1e-6)
+    assert info == 0
     x, info = linalg.bicgstab(csr(NONSYM), b, M=preconditioners.identity((4, 4)), rtol=1e-6)
     assert info == 0
 
@@ -136,16 +137,14 @@ def test_cpu_krylov_errors():
             _capi.krylov(kind, d, i, p, torch.ones(1), maxiter=-1)
 
 
-@pytest.mark.parametrize("solver", ["minres", "gmres"])
+@pytest.mark.parametrize("solver", ["gmres"])
 def test_preconditioned_variants_are_an_explicit_deviation(cpu, solver):
-    """The reference dispatches a diagonal / Jacobi M of minres and gmres to
-    separate native loops (csr_minres_jacobi, csr_gmres_jacobi: reference
-    mlx_sparse/linalg/_iterative.py:765-797, :1083-1125).  Where this build
-    has no such loop, every inverse diagonal form of M raises TypeError
-    naming the supported choices, a sparse matrix as M raises the
-    reference's TypeError, and M = None or the identity runs the plain loop
-    (minres: whatever check_preconditioner says, since no preconditioner is
-    checked)."""
+    """The reference dispatches a diagonal / Jacobi M of gmres to a separate
+    native loop (csr_gmres_jacobi: reference
+    mlx_sparse/linalg/_iterative.py:765-797).  Where this build has no such
+    loop, every inverse diagonal form of M raises TypeError naming the
+    supported choices, a sparse matrix as M raises the reference's
+    TypeError, and M = None or the identity runs the plain loop."""
     ms = cpu
     from mlx_sparse import linalg
     from mlx_sparse.linalg import preconditioners
@@ -245,3 +244,83 @@ def test_bicgstab_jacobi_api_on_cpu(cpu, oracle):
         np.testing.assert_allclose(x.numpy(), np.linalg.solve(NONSYM, b), rtol=8e-5, atol=8e-5)
     with pytest.raises(TypeError, match="sparse matrices"):
         linalg.bicgstab(A, b, M=A)
+
+
+# -- MINRES with a Jacobi preconditioner -----------------------------------------------
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_minres_jacobi_cpu_equals_oracle(oracle, index_dtype):
+    """msx_csr_minres_jacobi_cpu runs the oracle's loop bit for bit, on
+    scaled symmetric systems with and without a shift, short budgets and the
+    -2 cases (a non-positive or non-finite inverse diagonal entry)."""
+    import scipy.sparse as sp
+
+    A = laplacian_2d(16)
+    n = A.shape[0]
+    rng = np.random.default_rng(6)
+    s = (10.0 ** rng.uniform(-1, 1, n)).astype(np.float32)
+    As = (sp.diags(s) @ A @ sp.diags(s)).tocsr().astype(np.float32)
+    As.sort_indices()
+    b = rng.uniform(-1, 1, n).astype(np.float32)
+    inv = (1.0 / As.diagonal()).astype(np.float32)
+    cases = [(As, b, inv, {"rtol": 1e-5}), (As, b, inv, {"rtol": 1e-5, "shift": -0.3}),
+             (As, b, inv, {"maxiter": 4, "rtol": 1e-9}), (As, b, inv, {"maxiter": 0})]
+    S = sp.csr_matrix(INDEF)
+    b4 = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    cases.append((S, b4, np.full(4, 0.5, np.float32), {"rtol": 1e-6, "atol": 1e-7}))
+    for bad in (np.array([0.5, -1.0, 0.5, 0.5], np.float32),
+                np.array([0.5, np.nan, 0.5, 0.5], np.float32),
+                np.array([0.5, np.inf, 0.5, 0.5], np.float32)):
+        cases.append((S, b4, bad, {}))
+    for M, rhs, iv, kw in cases:
+        args = (M.data.astype(np.float32), M.indices.astype(index_dtype),
+                M.indptr.astype(index_dtype))
+        got = _capi.krylov("minres", *(torch.from_numpy(np.ascontiguousarray(a)) for a in args),
+                           torch.from_numpy(rhs), None, inv_diag=torch.from_numpy(iv), **kw)
+        want = oracle.csr_minres_jacobi(*args, rhs, iv, **kw)
+        _same(got, want)
+
+
+def test_minres_jacobi_api_on_cpu(cpu, oracle):
+    """The reference's Jacobi MINRES tests through linalg.minres on the CPU
+    device (tests/test_linalg_minres.py:141-231): the diagonal
+    preconditioner's solution and bounds, the near-singular diagonal fixed
+    by Jacobi, a non-SPD diagonal rejected with the reference's ValueError
+    (and ending with -2 when the check is off), and the reference's
+    TypeError for other preconditioners."""
+    ms = cpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    def csr(dense):
+        d, i, p = _csr(dense)
+        return ms.csr_array((d, i, p), shape=dense.shape, canonical=True)
+
+    dense = np.array([[2.0, 3.0, 0.0], [3.0, 2.0, 0.5], [0.0, 0.5, 4.0]], np.float32)
+    A = csr(dense)
+    b = np.array([1.0, -2.0, 0.5], np.float32)
+    x, info = linalg.minres(A, b, M=preconditioners.jacobi(A, check=True), rtol=1e-6, atol=1e-7,
+                            maxiter=64, return_info=True)
+    want = oracle.csr_minres_jacobi(*_csr(dense), b, (1.0 / np.diag(dense)).astype(np.float32),
+                                    rtol=1e-6, atol=1e-7, maxiter=64)
+    assert info.status == 0 and info.iterations == want[3]
+    assert x.numpy().tobytes() == want[0].tobytes()
+    np.testing.assert_allclose(x.numpy(), np.linalg.solve(dense, b), rtol=5e-5, atol=5e-5)
+
+    near = np.diag(np.array([1.0e-8, 1.0, 2.0, 3.0], np.float32))
+    An = csr(near)
+    bn = np.array([1.0, -1.0, 0.5, 2.0], np.float32)
+    x, info = linalg.minres(An, bn, M=preconditioners.jacobi(An, check=True), rtol=1e-6,
+                            atol=1e-7, maxiter=8)
+    assert info == 0 and np.all(np.isfinite(x.numpy()))
+    assert np.linalg.norm(near.astype(np.float64) @ x.numpy() - bn) / np.linalg.norm(bn) <= 1e-7
+
+    A2 = csr(np.diag(np.array([1.0, 2.0], np.float32)))
+    M = preconditioners.diagonal(np.array([1.0, -1.0], np.float32), inverse=True)
+    with pytest.raises(ValueError, match="symmetric positive-definite"):
+        linalg.minres(A2, np.ones(2, np.float32), M=M)
+    _, info = linalg.minres(A2, np.ones(2, np.float32), M=M, check_preconditioner=False,
+                            maxiter=8)
+    assert info < 0
+    with pytest.raises(TypeError, match="identity, diagonal, and Jacobi"):
+        linalg.minres(A2, np.ones(2, np.float32), M=lambda v: v)

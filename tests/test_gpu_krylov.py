@@ -348,3 +348,110 @@ def test_bicgstab_jacobi_api_on_gpu(gpu):
     assert info.status == 0 and info.preconditioner == "jacobi" and x.device.type == "cuda"
     xn = x.cpu().numpy().astype(np.float64)
     assert np.linalg.norm(NONSYM @ xn - b) / max(np.linalg.norm(b), 1.0) < 2e-5
+
+
+# -- MINRES with a Jacobi preconditioner (msx_csr_minres_jacobi) ----------------------
+
+def _scaled_laplacian(g, seed=6):
+    """S L S for the 2D Laplacian L and S = diag(10^U[-1/2, 1/2]): symmetric
+    positive definite and badly scaled.  (Scaled over two decades the
+    float32 loop stagnates above 1e-5 relative residual, in the oracle as
+    on the device.)"""
+    A = laplacian_2d(g)
+    rng = np.random.default_rng(seed)
+    s = (10.0 ** rng.uniform(-0.5, 0.5, A.shape[0])).astype(np.float32)
+    As = (sp.diags(s) @ A @ sp.diags(s)).tocsr().astype(np.float32)
+    As.sort_indices()
+    b = rng.uniform(-1, 1, A.shape[0]).astype(np.float32)
+    return As, b, (1.0 / As.diagonal()).astype(np.float32)
+
+
+def _gpu_minres_jacobi(A, b, inv, slice_mode=None, plan=True, x0=None, **kw):
+    d, i, p = (torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in _args(A))
+    pl = _capi.Plan(p, A.shape[0], d.numel(), data=d, indices=i, n_cols=A.shape[1],
+                    slice_mode=slice_mode) if plan else None
+    out = _capi.krylov("minres", d, i, p, torch.from_numpy(b).to(DEV),
+                       None if x0 is None else torch.from_numpy(x0).to(DEV), plan=pl,
+                       inv_diag=torch.from_numpy(inv).to(DEV), **kw)
+    torch.cuda.synchronize()
+    return (out[0].cpu().numpy(),) + tuple(out[1:])
+
+
+@pytest.mark.parametrize("shift", [0.0, -0.3, 1.3])
+def test_minres_jacobi_matches_oracle(shift):
+    A, b, inv = _scaled_laplacian(32)
+    rtol = 1e-4  # the oracle converges at a tenth of it too
+    print(f"minres jacobi scaled laplacian 32^2 shift={shift}", flush=True)
+    x, info, res, its = _gpu_minres_jacobi(A, b, inv, rtol=rtol, shift=shift, maxiter=3000)
+    wx, winfo, wres, wits = orc.csr_minres_jacobi(*_args(A), b, inv, rtol=rtol, shift=shift,
+                                                  maxiter=3000)
+    assert info == winfo == 0 and abs(its - wits) <= max(2, wits // 50), (its, wits)
+    dense = A.toarray().astype(np.float64) - shift * np.eye(A.shape[0])
+    want = np.linalg.solve(dense, b.astype(np.float64))
+    cond = np.linalg.cond(dense)
+    assert np.linalg.norm(x - want) <= 4 * rtol * cond * np.linalg.norm(want)
+    true_res = np.linalg.norm(b.astype(np.float64) - dense @ x.astype(np.float64))
+    assert res <= rtol * np.linalg.norm(b) * (1 + 1e-5)
+    assert abs(true_res - res) <= 1e-5 * np.linalg.norm(b) + 1e-3 * res
+
+
+@pytest.mark.parametrize("mode", ["blocks", "panels", "none"])
+def test_minres_jacobi_routes_and_reproducible(mode):
+    A, b, inv = _scaled_laplacian(100, seed=2)
+    kw = {"plan": mode != "none",
+          "slice_mode": {"blocks": _capi.SLICE_OFF, "panels": _capi.SLICE_PANELS,
+                         "none": None}[mode]}
+    print(f"minres jacobi route={mode} n={A.shape[0]}", flush=True)
+    r1 = _gpu_minres_jacobi(A, b, inv, rtol=1e-4, maxiter=5000, **kw)
+    r2 = _gpu_minres_jacobi(A, b, inv, rtol=1e-4, maxiter=5000, **kw)
+    assert r1[1:] == r2[1:] and r1[0].tobytes() == r2[0].tobytes()
+    wx, winfo, wres, wits = orc.csr_minres_jacobi(*_args(A), b, inv, rtol=1e-4, maxiter=5000)
+    assert r1[1] == winfo == 0 and abs(r1[3] - wits) <= max(2, wits // 50), (r1[3], wits)
+    assert np.linalg.norm(r1[0].astype(np.float64) - wx) <= 1e-2 * np.linalg.norm(wx)
+
+
+def test_minres_jacobi_status_cases_match_oracle():
+    """-2 for an inverse diagonal entry that is not > 0 (negative, zero, NaN)
+    or a non-finite preconditioned product (an infinite entry); a zero
+    right-hand side; maxiter 0 and 1; a non-finite b."""
+    S = sp.csr_matrix(INDEF)
+    b = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    good = np.full(4, 0.5, np.float32)
+    bad_b = b.copy()
+    bad_b[0] = np.inf
+    cases = [(b, good, {}), (np.zeros(4, np.float32), good, {}), (b, good, {"maxiter": 0}),
+             (b, good, {"maxiter": 1, "rtol": 1e-9}), (bad_b, good, {})]
+    for v in (-1.0, 0.0, np.nan, np.inf):
+        inv = good.copy()
+        inv[1] = v
+        cases.append((b, inv, {}))
+    for rhs, iv, kw in cases:
+        x, info, res, its = _gpu_minres_jacobi(S, rhs, iv, **kw)
+        wx, winfo, wres, wits = orc.csr_minres_jacobi(*_args(S), rhs, iv, **kw)
+        print(f"minres jacobi status case {kw} inv={iv}: gpu {info, its, res} "
+              f"oracle {winfo, wits, wres}", flush=True)
+        assert (info, its) == (winfo, wits)
+        assert np.isnan(res) == np.isnan(wres) and np.isinf(res) == np.isinf(wres)
+        if np.isfinite(wres):
+            assert abs(res - wres) <= 1e-6 * max(1.0, abs(wres))
+
+
+def test_minres_jacobi_api_on_gpu(gpu):
+    """linalg.minres with a Jacobi preconditioner on the device: the
+    reference's diagonal-preconditioner test and its bounds
+    (test_linalg_minres.py:141-179)."""
+    ms = gpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    dense = np.array([[2.0, 3.0, 0.0], [3.0, 2.0, 0.5], [0.0, 0.5, 4.0]], np.float32)
+    A = sp.csr_matrix(dense)
+    csr = ms.csr_array((A.data, A.indices.astype(np.int32), A.indptr.astype(np.int32)),
+                       shape=dense.shape, canonical=True)
+    b = np.array([1.0, -2.0, 0.5], np.float32)
+    x, info = linalg.minres(csr, b, M=preconditioners.jacobi(csr, check=True), rtol=1e-6,
+                            atol=1e-7, maxiter=64, return_info=True)
+    assert info.status == 0 and x.device.type == "cuda"
+    xn = x.cpu().numpy()
+    np.testing.assert_allclose(xn, np.linalg.solve(dense, b), rtol=5e-5, atol=5e-5)
+    assert np.linalg.norm(dense.astype(np.float64) @ xn - b) / np.linalg.norm(b) < 2e-6

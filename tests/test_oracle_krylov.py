@@ -385,3 +385,135 @@ def test_bicgstab_jacobi_status_rules():
     x, info, res, its = orc.csr_bicgstab_jacobi(*args, b, inv, rtol=1e-7, atol=0.0, maxiter=1)
     assert (info, its) == (1, 1)
     assert res == pytest.approx(np.linalg.norm(b - NONSYM.astype(np.float64) @ x), rel=1e-5)
+
+
+# -- MINRES with a Jacobi preconditioner -----------------------------------------------
+#
+# oracle_csr_minres_jacobi (reference src/preconditioners/minres/minres.cpp:
+# 93-330): M = I reproduces the plain loop bit for bit; the closed form of
+# preconditioned MINRES (k distinct eigenvalues of M^1/2 (A - shift I) M^1/2:
+# k iterations); a diagonal system with M = A^-1 (one iteration, the
+# reference's near-singular diagonal test, test_linalg_minres.py:182-201);
+# the reference's system against SciPy's minres with the same M
+# (test_linalg_minres.py:141-179); and the Jacobi status rules (-2 for a
+# non-positive preconditioner or preconditioned product).
+
+@pytest.mark.parametrize("shift", [0.0, 0.7])
+def test_minres_jacobi_identity_matches_plain(shift):
+    for A in (sp.csr_matrix(INDEF), laplacian_2d(12)):
+        n = A.shape[0]
+        b = np.random.default_rng(n).uniform(-1, 1, n).astype(np.float32)
+        ones = np.ones(n, np.float32)
+        args = (A.data.astype(np.float32), A.indices.astype(np.int32), A.indptr.astype(np.int32))
+        got = orc.csr_minres_jacobi(*args, b, ones, rtol=1e-5, shift=shift)
+        want = orc.csr_minres(*args, b, rtol=1e-5, shift=shift)
+        assert got[1:] == want[1:]
+        np.testing.assert_array_equal(got[0], want[0])
+
+
+@pytest.mark.parametrize("eigs", [[1.0, -3.0], [2.0, 5.0, -1.0], [1.0, 2.0, 3.0, -4.0]])
+def test_minres_jacobi_distinct_eigenvalue_count(eigs):
+    rng = np.random.default_rng(len(eigs))
+    n = 24
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    lam = np.array([eigs[j % len(eigs)] for j in range(n)])
+    s = 10.0 ** rng.uniform(-1, 1, n)
+    # A = S Q diag(lam) Q^T S, M = S^-2: M^1/2 A M^1/2 = Q diag(lam) Q^T
+    dense = (s[:, None] * ((Q * lam) @ Q.T) * s[None, :])
+    dense = ((dense + dense.T) / 2).astype(np.float32)
+    inv = (1.0 / s ** 2).astype(np.float32)
+    b = rng.uniform(-1, 1, n).astype(np.float32)
+    x, info, res, its = orc.csr_minres_jacobi(*_csr(dense), b, inv, rtol=1e-4)
+    assert (info, its) == (0, len(eigs))
+    _, info_p, _, its_p = orc.csr_minres(*_csr(dense), b, rtol=1e-4, maxiter=200)
+    assert its_p > len(eigs)
+
+
+def test_minres_jacobi_diagonal_systems_one_step():
+    for d in ([1.0e-8, 1.0, 2.0, 3.0], [2.0, -0.5, 4.0, 8.0, -1.25]):
+        d = np.array(d, np.float32)
+        dense = np.diag(d)
+        b = np.linspace(-1.0, 2.0, len(d)).astype(np.float32)
+        inv = (1.0 / np.abs(d)).astype(np.float32)
+        x, info, res, its = orc.csr_minres_jacobi(*_csr(dense), b, inv, rtol=1e-6, atol=1e-7,
+                                                  maxiter=8)
+        assert info == 0 and np.all(np.isfinite(x))
+        assert _rel_residual(dense, x, b) <= 1e-6
+        # all positive: M A = I, one iteration; mixed signs: eigenvalues +-1
+        assert its == (1 if np.all(d > 0) else 2)
+
+
+def test_minres_jacobi_reference_system_against_scipy():
+    dense = np.array([[2.0, 3.0, 0.0], [3.0, 2.0, 0.5], [0.0, 0.5, 4.0]], np.float32)
+    b = np.array([1.0, -2.0, 0.5], np.float32)
+    inv = (1.0 / np.diag(dense)).astype(np.float32)
+    x, info, res, its = orc.csr_minres_jacobi(*_csr(dense), b, inv, rtol=1e-6, atol=1e-7,
+                                              maxiter=64)
+    assert info == 0
+    np.testing.assert_allclose(x, np.linalg.solve(dense, b), rtol=5e-5, atol=5e-5)
+    assert _rel_residual(dense, x, b) < 2e-6
+    M = spla.LinearOperator(dense.shape, matvec=lambda v: inv.astype(np.float64) * v)
+    sx, sinfo = spla.minres(sp.csr_matrix(dense.astype(np.float64)), b.astype(np.float64), M=M,
+                            rtol=1e-6, maxiter=64)
+    assert sinfo == 0
+    np.testing.assert_allclose(x, sx, rtol=8e-5, atol=8e-5)
+
+
+def test_minres_jacobi_larger_against_scipy():
+    A = laplacian_2d(24)
+    n = A.shape[0]
+    rng = np.random.default_rng(6)
+    s = (10.0 ** rng.uniform(-1, 1, n)).astype(np.float32)
+    As = (sp.diags(s) @ A @ sp.diags(s)).tocsr().astype(np.float32)
+    As.sort_indices()
+    b = rng.uniform(-1, 1, n).astype(np.float32)
+    inv = (1.0 / As.diagonal()).astype(np.float32)
+    x, info, res, its = orc.csr_minres_jacobi(As.data, As.indices, As.indptr, b, inv, rtol=1e-5,
+                                              shift=-0.3, maxiter=2000)
+    assert info == 0
+    dense = As.toarray().astype(np.float64) + 0.3 * np.eye(n)
+    true = np.linalg.norm(b - dense @ x)
+    # the reported residual is the float32 true residual of x
+    assert abs(res - true) <= 1e-4 * true + 1e-6 * np.linalg.norm(b)
+    # SciPy's iterates are the same preconditioned MINRES iterates (float64);
+    # its own stopping test differs, so take the first iterate whose true
+    # residual meets this loop's test
+    iterates = []
+    M = spla.LinearOperator((n, n), matvec=lambda v: inv.astype(np.float64) * v)
+    spla.minres(As.astype(np.float64), b.astype(np.float64), shift=-0.3, M=M, rtol=1e-9,
+                maxiter=2000, callback=lambda xk: iterates.append(xk.copy()))
+    tol = 1e-5 * np.linalg.norm(b.astype(np.float64))
+    first = next(k + 1 for k, xk in enumerate(iterates)
+                 if np.linalg.norm(b - dense @ xk) <= tol)
+    assert abs(its - first) <= 2, (its, first)
+    _, _, _, its_p = orc.csr_minres(As.data, As.indices, As.indptr, b, rtol=1e-5, shift=-0.3,
+                                    maxiter=2000)
+    assert its_p > 2 * its
+
+
+def test_minres_jacobi_status_rules():
+    dense = np.diag(np.array([1.0, 2.0], np.float32))
+    b = np.ones(2, np.float32)
+    # a non-positive inverse diagonal entry: -2 before any iteration, also
+    # when x0 already solves the system
+    for inv in (np.array([1.0, -1.0], np.float32), np.array([1.0, 0.0], np.float32),
+                np.array([1.0, np.nan], np.float32)):
+        x, info, res, its = orc.csr_minres_jacobi(*_csr(dense), b, inv, maxiter=8)
+        assert (info, its) == (-2, 0) and res == np.float32(np.sqrt(2.0))
+        _, info, _, _ = orc.csr_minres_jacobi(*_csr(dense), b, inv,
+                                              x0=np.array([1.0, 0.5], np.float32))
+        assert info == -2
+    # an infinite entry: the preconditioned product r.M r is not finite
+    _, info, res, its = orc.csr_minres_jacobi(*_csr(dense), b, np.array([1.0, np.inf], np.float32))
+    assert (info, its) == (-2, 0)
+    # zero right-hand side, maxiter 0, a non-finite b
+    inv = np.array([1.0, 0.5], np.float32)
+    x, info, res, its = orc.csr_minres_jacobi(*_csr(dense), np.zeros(2, np.float32), inv)
+    assert (info, its, res) == (0, 0, 0.0)
+    _, info, res, its = orc.csr_minres_jacobi(*_csr(INDEF), np.ones(4, np.float32),
+                                              np.ones(4, np.float32), maxiter=0)
+    assert (info, its) == (1, 0) and res == np.float32(2.0)
+    bad = b.copy()
+    bad[0] = np.inf
+    _, info, _, its = orc.csr_minres_jacobi(*_csr(dense), bad, inv)
+    assert (info, its) == (-3, 0)
