@@ -676,6 +676,33 @@ msx_status msx_csr_gmres(msx_itype it, int64_t n, int64_t nnz,
                          msx_solver_result *result, void *stream);
 
 /*
+ * Restarted GMRES with the Jacobi preconditioner M = diag(inv_diag)
+ * (inv_diag: n device floats): msx_csr_gmres's device cycles over the
+ * Arnoldi basis of M A (each step's w = M (A v_j), folded into the first
+ * Gram-Schmidt pass), each cycle started from z0 = M r with the
+ * least-squares right-hand side ||z0||.  As the reference's Jacobi loop:
+ * ||r|| decides convergence; ||z0|| <= FLT_EPSILON (or not finite) gives
+ * -1; a non-finite inverse diagonal entry is a non-finite input (-3,
+ * residual infinity); a non-finite new Arnoldi norm ends the cycle with no
+ * steps (-1); the least-squares solution is not tested on its own (a
+ * non-finite update row ends the solve with -3, the rows before it
+ * updated).
+ *
+ * Replaces the GPU path of csr_gmres_jacobi (reference:
+ * src/preconditioners/gmres/gmres.cpp:572-748, whose Arnoldi step is
+ * CSRArnoldiJacobi::eval_gpu, gmres.cpp:474-517, gmres.metal) with the
+ * arithmetic of csr_arnoldi_jacobi_cpu_impl (gmres.cpp:342-447).
+ */
+msx_status msx_csr_gmres_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                const float *data, const void *indices,
+                                const void *indptr, const float *b,
+                                const float *x0, const float *inv_diag,
+                                float *x, float rtol, float atol,
+                                int64_t restart, int64_t maxiter,
+                                const msx_csr_plan *plan,
+                                msx_solver_result *result, void *stream);
+
+/*
  * Host (CPU) solvers, host pointers: the reference's sequential loops
  * (csr_cg_cpu_impl, cg.cpp:75-246; csr_pcg_jacobi_cpu_impl,
  * pcg.cpp:71-236), one thread.
@@ -728,6 +755,13 @@ msx_status msx_csr_gmres_cpu(msx_itype it, int64_t n, int64_t nnz,
                              const float *x0, float *x, float rtol,
                              float atol, int64_t restart, int64_t maxiter,
                              msx_solver_result *result);
+msx_status msx_csr_gmres_jacobi_cpu(msx_itype it, int64_t n, int64_t nnz,
+                                    const float *data, const void *indices,
+                                    const void *indptr, const float *b,
+                                    const float *x0, const float *inv_diag,
+                                    float *x, float rtol, float atol,
+                                    int64_t restart, int64_t maxiter,
+                                    msx_solver_result *result);
 
 /*
  * Matrix Market files (the text format of the SuiteSparse collection).

@@ -61,19 +61,41 @@ struct GmState {
 __device__ inline bool lead() { return blockIdx.x == 0 && threadIdx.x == 0; }
 
 // r = b - A x.  Slots: r.r, non-finite r count, b.b, non-finite b or x count.
+// J (the Jacobi loop, preconditioners/gmres/gmres.cpp:572-748): also
+// z = inv_diag r; slot 2 holds z.z instead (a double sum of float squares:
+// non-finite exactly when some z is) and slot 3 also counts inv_diag.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     gm_resid(const float *__restrict__ b, const float *__restrict__ x,
-             const float *__restrict__ ax, float *__restrict__ r, int64_t n, double *part) {
+             const float *__restrict__ ax, const float *__restrict__ inv_diag,
+             float *__restrict__ r, float *__restrict__ z, int64_t n, double *part) {
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
   MSX_SOLVER_LOOP({
     const float bi = b[i], xi = x[i];
     const float ri = bi - ax[i];
     r[i] = ri;
     v[0] += static_cast<double>(ri) * static_cast<double>(ri);
-    if (!fin(ri)) v[1] += 1.0;
-    v[2] += static_cast<double>(bi) * static_cast<double>(bi);
-    if (!(fin(bi) && fin(xi))) v[3] += 1.0;
+    if constexpr (J) {
+      const float di = inv_diag[i];
+      const float zi = di * ri;
+      z[i] = zi;
+      if (!fin(ri)) v[1] += 1.0;
+      v[2] += static_cast<double>(zi) * static_cast<double>(zi);
+      if (!(fin(bi) && fin(xi) && fin(di))) v[3] += 1.0;
+    } else {
+      if (!fin(ri)) v[1] += 1.0;
+      v[2] += static_cast<double>(bi) * static_cast<double>(bi);
+      if (!(fin(bi) && fin(xi))) v[3] += 1.0;
+    }
   })
+  write_partials(v, part);
+}
+
+// Slot 0: v.v (the Jacobi loop's ||b||).
+__global__ void __launch_bounds__(kSolverThreads)
+    gm_sumsq(const float *__restrict__ vec, int64_t n, double *part) {
+  double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
+  MSX_SOLVER_LOOP({ v[0] += static_cast<double>(vec[i]) * static_cast<double>(vec[i]); })
   write_partials(v, part);
 }
 
@@ -86,18 +108,23 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // (r / beta).(r / beta): the norm the reference's Arnoldi takes of its start
-// vector (arnoldi.cpp:104-109).
+// vector (arnoldi.cpp:104-109); slot 1 counts its non-finite entries.
 __global__ void __launch_bounds__(kSolverThreads)
     gm_v0norm(const float *__restrict__ r, float beta, int64_t n, double *part) {
   double v[kSlots] = {0.0, 0.0, 0.0, 0.0};
   MSX_SOLVER_LOOP({
     const float vi = r[i] / beta;
     v[0] += static_cast<double>(vi) * static_cast<double>(vi);
+    if (!fin(vi)) v[1] += 1.0;
   })
   write_partials(v, part);
 }
 
-// V0 and a fresh cycle: h (hn floats) cleared, state reset.
+// V0 and a fresh cycle: h (hn floats) cleared, state reset.  J: a start
+// vector with a non-finite entry or norm takes no step (the Jacobi
+// Arnoldi's input test, gmres.cpp:382-391 there): every step returns at
+// once and the cycle reports zero steps.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     gm_start(const float *__restrict__ r, float beta, const double *part, int nparts,
              float *__restrict__ v0, int64_t n, float *__restrict__ h, int64_t hn, GmState *st) {
@@ -105,6 +132,7 @@ __global__ void __launch_bounds__(kSolverThreads)
   read_totals(part, nparts, t);
   const float v_norm = static_cast<float>(sqrt(max0(t[0])));
   const bool unit = v_norm <= kEpsF;
+  const bool no_steps = J && (t[1] != 0.0 || !fin(v_norm));
   MSX_SOLVER_LOOP({
     const float vi = r[i] / beta;
     v0[i] = unit ? (i == 0 ? 1.0f : 0.0f) : vi / v_norm;
@@ -113,7 +141,7 @@ __global__ void __launch_bounds__(kSolverThreads)
        i += static_cast<int64_t>(gridDim.x) * kSolverThreads)
     h[i] = 0.0f;
   if (lead()) {
-    st->stop_at = INT_MAX;
+    st->stop_at = no_steps ? -1 : INT_MAX;
     st->used = 0;
     st->bad = ~0ull;
   }
@@ -126,15 +154,19 @@ __global__ void __launch_bounds__(kSolverThreads)
 // The previous pass's partials, then a thread's first kUnroll elements of w
 // and of both basis vectors, are loaded before the partials are reduced, so
 // that the reduction (its wave sums and barriers) overlaps the element
-// loads.
+// loads.  J: pass 0 first scales w = A v_j by inv_diag in float (the Jacobi
+// Arnoldi's w = M A q, gmres.cpp:413-415 there) and writes it back.
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
-    gm_mgs(const float *__restrict__ V, int64_t ld, float *__restrict__ w, int64_t n, int32_t j,
-           int32_t s, const double *part_in, int nparts, double *part_out, float *__restrict__ h,
-           int64_t k, const GmState *st) {
+    gm_mgs(const float *__restrict__ V, int64_t ld, float *__restrict__ w,
+           const float *__restrict__ inv_diag, int64_t n, int32_t j, int32_t s,
+           const double *part_in, int nparts, double *part_out, float *__restrict__ h, int64_t k,
+           const GmState *st) {
   if (st->stop_at < j) return;  // an earlier step ended this cycle
   const int32_t ncol = j + 1;
   const bool sub = s > 0, norm = s == 2 * ncol;
-  const float *q_prev = V + static_cast<int64_t>(sub ? (s - 1) % ncol : 0) * ld;
+  // pass 0 has no projection to subtract: with J its second stream is inv_diag
+  const float *q_prev = (J && !sub) ? inv_diag : V + static_cast<int64_t>(sub ? (s - 1) % ncol : 0) * ld;
   const float *q = V + static_cast<int64_t>(norm ? 0 : s % ncol) * ld;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
   const int64_t base0 = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x;
@@ -160,6 +192,9 @@ __global__ void __launch_bounds__(kSolverThreads)
     if (sub) {
       const float t = coeff * pv;
       wv = wv - t;
+      w[i] = wv;
+    } else if (J) {
+      wv = wv * pv;
       w[i] = wv;
     }
     if (norm) {
@@ -190,7 +225,9 @@ __global__ void __launch_bounds__(kSolverThreads)
 }
 
 // h[j+1][j] = ||w|| (norm_float); the next basis vector w / ||w||, or the
-// end of the cycle's steps when ||w|| <= eps.
+// end of the cycle's steps when ||w|| <= eps.  J: a non-finite ||w|| ends
+// the cycle with no steps (gmres.cpp:437-440 there).
+template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
     gm_norm(const float *__restrict__ w, float *__restrict__ next, int64_t n, int32_t j,
             const double *part, int nparts, float *__restrict__ h, int64_t k, GmState *st) {
@@ -199,12 +236,13 @@ __global__ void __launch_bounds__(kSolverThreads)
   read_totals(part, nparts, t);
   const float ww = static_cast<float>(t[0]);
   const float h_next = sqrtf(max0(ww));
+  const bool lost = J && !fin(h_next);
   if (lead()) {
     h[static_cast<int64_t>(j + 1) * k + j] = h_next;
-    st->used = j + 1;
-    if (h_next <= kEpsF) st->stop_at = j;
+    st->used = lost ? 0 : j + 1;
+    if (lost || h_next <= kEpsF) st->stop_at = j;
   }
-  if (h_next <= kEpsF) return;
+  if (lost || h_next <= kEpsF) return;
   MSX_SOLVER_LOOP({ next[i] = w[i] / h_next; })
 }
 
@@ -276,8 +314,11 @@ float norm_of(double total) {
   return std::sqrt(f < 0.0f ? 0.0f : f);
 }
 
-msx_status gmres(const System &s, const float *b, const float *x0, float *x, float rtol,
-                 float atol, int64_t restart, int64_t maxiter, msx_solver_result *result) {
+// J: the Jacobi loop, inv_diag non-null (z = M r in one more vector).
+template <bool J>
+msx_status gmres(const System &s, const float *b, const float *x0, const float *inv_diag,
+                 float *x, float rtol, float atol, int64_t restart, int64_t maxiter,
+                 msx_solver_result *result) {
   const int64_t n = s.n;
   const int64_t kcap = std::max<int64_t>(1, std::min({restart, maxiter, n}));
   const size_t vec = (static_cast<size_t>(n) * sizeof(float) + 255) / 256 * 256;
@@ -285,7 +326,7 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
   const size_t hbytes = (static_cast<size_t>((kcap + 1) * kcap) * sizeof(float) + 255) / 256 * 256;
   const size_t ybytes = (static_cast<size_t>(kcap) * sizeof(double) + 255) / 256 * 256;
   const size_t part_bytes = sizeof(double) * kSlots * kSolverMaxBlocks;
-  const size_t nvec = static_cast<size_t>(kcap + 1) + 5;
+  const size_t nvec = static_cast<size_t>(kcap + 1) + (J ? 6 : 5);
   Scratch sc;
   sc.stream = s.stream;
   MSX_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&sc.base),
@@ -298,7 +339,8 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
   float *r = reinterpret_cast<float *>(p + 2 * vec);
   float *xa = reinterpret_cast<float *>(p + 3 * vec);
   float *xb = reinterpret_cast<float *>(p + 4 * vec);
-  p += 5 * vec;
+  float *z = J ? reinterpret_cast<float *>(p + 5 * vec) : r;
+  p += (J ? 6 : 5) * vec;
   float *h = reinterpret_cast<float *>(p);
   p += hbytes;
   double *y_dev = reinterpret_cast<double *>(p);
@@ -322,7 +364,8 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
   auto residual = [&](const float *xv) -> msx_status {
     msx_status es = spmv(xv, ax);
     if (es != MSX_OK) return es;
-    hipLaunchKernelGGL(gm_resid, s.grid, s.block, 0, s.stream, b, xv, ax, r, n, part[2]);
+    hipLaunchKernelGGL(gm_resid<J>, s.grid, s.block, 0, s.stream, b, xv, ax, inv_diag, r, z, n,
+                       part[2]);
     hipLaunchKernelGGL(gm_totals, dim3(1), s.block, 0, s.stream, part[2], np, tot);
     MSX_HIP_TRY(hipGetLastError());
     MSX_HIP_TRY(hipMemcpyAsync(host.tot, tot, sizeof(host.tot), hipMemcpyDeviceToHost, s.stream));
@@ -333,8 +376,15 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
 
   hipLaunchKernelGGL(gm_copy, s.grid, s.block, 0, s.stream, x0, xa, n);
   MSX_HIP_TRY(hipGetLastError());
+  double bb = 0.0;  // J: ||b||^2 from its own pass (gm_resid's slot 2 holds z.z)
+  if (J) {
+    hipLaunchKernelGGL(gm_sumsq, s.grid, s.block, 0, s.stream, b, n, part[1]);
+    hipLaunchKernelGGL(gm_totals, dim3(1), s.block, 0, s.stream, part[1], np, tot);
+    MSX_HIP_TRY(hipGetLastError());
+    MSX_HIP_TRY(hipMemcpyAsync(&bb, tot, sizeof(double), hipMemcpyDeviceToHost, s.stream));
+  }
   if ((e = residual(xa)) != MSX_OK) return e;
-  const float b_norm = norm_of(host.tot[2]);
+  const float b_norm = norm_of(J ? bb : host.tot[2]);
   const float scaled = rtol * b_norm;
   const float tol = atol > scaled ? atol : scaled;
   int64_t iters = 0;
@@ -355,19 +405,26 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
   std::vector<double> y;
   // host.tot holds the residual of the current x (xa) at the top of the loop
   while (iters < maxiter) {
-    const float beta = norm_of(host.tot[0]);
+    float beta = norm_of(host.tot[0]);
     res = beta;
-    if (host.tot[1] != 0.0 || !std::isfinite(beta)) {
+    if (host.tot[1] != 0.0 || !std::isfinite(res) || (J && !std::isfinite(host.tot[2]))) {
       status = -3;
       break;
     }
-    if (beta <= tol) {
+    if (res <= tol) {
       status = 0;
       break;
     }
+    if (J) {  // the cycle starts from z = M r (gmres.cpp:632-637 there)
+      beta = norm_of(host.tot[2]);
+      if (!std::isfinite(beta) || beta <= kEpsF) {
+        status = -1;
+        break;
+      }
+    }
     const int64_t steps = std::min({restart, maxiter - iters, n});
-    hipLaunchKernelGGL(gm_v0norm, s.grid, s.block, 0, s.stream, r, beta, n, part[2]);
-    hipLaunchKernelGGL(gm_start, s.grid, s.block, 0, s.stream, r, beta, part[2], np, V, n, h,
+    hipLaunchKernelGGL(gm_v0norm, s.grid, s.block, 0, s.stream, z, beta, n, part[2]);
+    hipLaunchKernelGGL(gm_start<J>, s.grid, s.block, 0, s.stream, z, beta, part[2], np, V, n, h,
                        (steps + 1) * steps, st);
     MSX_HIP_TRY(hipGetLastError());
     for (int64_t j = 0; j < steps; ++j) {
@@ -375,11 +432,11 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
       const auto jj = static_cast<int32_t>(j);
       int cur = 0;
       for (int32_t pass = 0; pass <= 2 * jj + 2; ++pass) {
-        hipLaunchKernelGGL(gm_mgs, s.grid, s.block, 0, s.stream, V, ld, w, n, jj, pass,
-                           part[cur ^ 1], np, part[cur], h, steps, st);
+        hipLaunchKernelGGL(gm_mgs<J>, s.grid, s.block, 0, s.stream, V, ld, w, inv_diag, n, jj,
+                           pass, part[cur ^ 1], np, part[cur], h, steps, st);
         cur ^= 1;
       }
-      hipLaunchKernelGGL(gm_norm, s.grid, s.block, 0, s.stream, w, V + (j + 1) * ld, n, jj,
+      hipLaunchKernelGGL(gm_norm<J>, s.grid, s.block, 0, s.stream, w, V + (j + 1) * ld, n, jj,
                          part[cur ^ 1], np, h, steps, st);
       MSX_HIP_TRY(hipGetLastError());
     }
@@ -409,7 +466,8 @@ msx_status gmres(const System &s, const float *b, const float *x0, float *x, flo
       status = -1;
       break;
     }
-    for (double v : y) bad = bad || !std::isfinite(v);
+    if (!J)  // the Jacobi loop tests only each row's update (gmres.cpp:693-707 there)
+      for (double v : y) bad = bad || !std::isfinite(v);
     if (bad) {
       status = -3;
       break;
@@ -473,5 +531,33 @@ extern "C" msx_status msx_csr_gmres(msx_itype it, int64_t n, int64_t nnz, const 
   const uint32_t blocks = blocks_for(n);
   const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
                  dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
-  return gmres(s, b, x0, x, rtol, atol, restart, maxiter, result);
+  return gmres<false>(s, b, x0, nullptr, x, rtol, atol, restart, maxiter, result);
+}
+
+extern "C" msx_status msx_csr_gmres_jacobi(msx_itype it, int64_t n, int64_t nnz,
+                                           const float *data, const void *indices,
+                                           const void *indptr, const float *b, const float *x0,
+                                           const float *inv_diag, float *x, float rtol,
+                                           float atol, int64_t restart, int64_t maxiter,
+                                           const msx_csr_plan *plan, msx_solver_result *result,
+                                           void *stream) {
+  clear_error();
+  if (!valid_itype(it)) return fail(MSX_ETYPE, "csr_gmres_jacobi requires int32 or int64 indices.");
+  if (n <= 0 || n >= 2147483647)
+    return fail(MSX_EINVAL, "csr_gmres_jacobi requires a non-empty square matrix.");
+  if (restart <= 0 || maxiter < 0)
+    return fail(MSX_EINVAL, "csr_gmres_jacobi requires restart > 0 and maxiter >= 0.");
+  if (maxiter > 2147483647) return fail(MSX_EINVAL, "csr_gmres_jacobi maxiter must fit in int32.");
+  if (nnz < 0 || nnz >= 2147483647)
+    return fail(MSX_EINVAL, "csr_gmres_jacobi supports at most 2^31 - 2 stored values.");
+  if (indptr == nullptr || b == nullptr || x0 == nullptr || x == nullptr || result == nullptr ||
+      inv_diag == nullptr || (nnz > 0 && (data == nullptr || indices == nullptr)))
+    return fail(MSX_EINVAL, "csr_gmres_jacobi buffers must be non-NULL.");
+  const msx_status st =
+      check_plan("csr_gmres_jacobi", plan, MSX_F32, it, n, n, nnz, data, indices, indptr);
+  if (st != MSX_OK) return st;
+  const uint32_t blocks = blocks_for(n);
+  const System s{n, nnz, it, data, indices, indptr, plan, static_cast<hipStream_t>(stream),
+                 dim3(blocks), dim3(kSolverThreads), static_cast<int>(blocks)};
+  return gmres<true>(s, b, x0, inv_diag, x, rtol, atol, restart, maxiter, result);
 }

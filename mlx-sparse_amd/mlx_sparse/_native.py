@@ -140,6 +140,14 @@ def csr_gmres(data, indices, indptr, b, x0, shape: Shape2D, *, rtol: float, atol
                                  restart, maxiter, plan=plan)
 
 
+def csr_gmres_jacobi(data, indices, indptr, b, x0, inv_diag, shape: Shape2D, *, rtol: float,
+                     atol: float, restart: int, maxiter: int, plan=None):
+    """(x, info, residual, iterations) of Jacobi-preconditioned restarted
+    GMRES (reference: mlx_sparse/_native.py csr_gmres_jacobi)."""
+    return extension().csr_gmres_jacobi(data, indices, indptr, b, x0, inv_diag, shape[0],
+                                        shape[1], rtol, atol, restart, maxiter, plan=plan)
+
+
 def csr_plan(indptr, n_rows: int, nnz: int, block_nnz: int = 0, *, data=None, indices=None,
              n_cols: int = -1, slice_mode: int = 0):
     """Row-block plan; with ``data``/``indices`` a plan bound to the matrix,

@@ -150,8 +150,8 @@ def _system(A, b, x0, maxiter, solver: str):
 
 # Solvers with a Jacobi-preconditioned loop (the reference's native
 # diagonal paths: mlx_sparse/linalg/_iterative.py:437-461 csr_bicgstab_jacobi,
-# :1086-1110 csr_minres_jacobi).
-_JACOBI_SOLVERS = {"bicgstab", "minres"}
+# :770-797 csr_gmres_jacobi, :1086-1110 csr_minres_jacobi).
+_JACOBI_SOLVERS = {"bicgstab", "gmres", "minres"}
 
 
 def _preconditioner(M, csr, solver: str, device):
@@ -268,7 +268,9 @@ def gmres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, restart: int 
     ``min(20, n)``; one SpMV per step) from the true residual and minimises
     the residual over it.  ``maxiter`` counts SpMVs over all cycles (default
     ``10 * n``).  Stops when ``||b - A x|| <= max(atol, rtol * ||b||)``,
-    tested between cycles.  ``M``: ``None`` or ``preconditioners.identity``.
+    tested between cycles.  ``M``: ``None``, ``preconditioners.identity`` or
+    a diagonal/Jacobi preconditioner (left preconditioning: the Arnoldi
+    basis of ``M @ A``, each cycle from ``M @ r``).
     ``callback`` is called once after the solve, with ``x``
     (``callback_type="x"``) or the final residual norm ("pr_norm",
     "legacy").
@@ -283,11 +285,17 @@ def gmres(A, b, *, x0=None, rtol: float = 1e-5, atol: float = 0.0, restart: int 
     restart_value = min(20, csr.shape[0]) if restart is None else int(restart)
     if restart_value <= 0:
         raise ValueError("restart must be positive.")
-    kind, _, _ = _preconditioner(M, csr, "gmres", device)
+    kind, _, inv_diag = _preconditioner(M, csr, "gmres", device)
     data, indices, indptr = csr.buffers(device)
-    x, info, residual, iterations = _native.csr_gmres(
-        data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
-        restart=restart_value, maxiter=maxiter_value, plan=csr.plan(device))
+    if inv_diag is None:
+        x, info, residual, iterations = _native.csr_gmres(
+            data, indices, indptr, rhs, guess, csr.shape, rtol=float(rtol), atol=float(atol),
+            restart=restart_value, maxiter=maxiter_value, plan=csr.plan(device))
+    else:
+        x, info, residual, iterations = _native.csr_gmres_jacobi(
+            data, indices, indptr, rhs, guess, inv_diag, csr.shape, rtol=float(rtol),
+            atol=float(atol), restart=restart_value, maxiter=maxiter_value,
+            plan=csr.plan(device))
     return finish(x, info, residual, iterations, solver="gmres", return_info=bool(return_info),
                   callback=callback, callback_type=callback_type, rtol=float(rtol),
                   atol=float(atol), maxiter=maxiter_value, restart=restart_value,

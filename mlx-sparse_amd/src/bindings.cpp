@@ -845,6 +845,19 @@ PYBIND11_MODULE(_ext, m) {
       py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"), py::arg("atol"), py::arg("restart"),
       py::arg("maxiter"), py::arg("plan") = py::none(),
       "Restarted GMRES: (x, info, residual, iterations).");
+  m.def(
+      "csr_gmres_jacobi",
+      [](py::handle data, py::handle indices, py::handle indptr, py::handle b, py::handle x0,
+         py::handle inv_diag, int64_t n_rows, int64_t n_cols, float rtol, float atol,
+         int64_t restart, int64_t maxiter, py::object plan) {
+        return solve_krylov(msx::Krylov::GMRES, data, indices, indptr, b, x0, n_rows, n_cols,
+                            rtol, atol, maxiter, 0.0f, plan, restart,
+                            py::reinterpret_borrow<py::object>(inv_diag));
+      },
+      py::arg("data"), py::arg("indices"), py::arg("indptr"), py::arg("b"), py::arg("x0"),
+      py::arg("inv_diag"), py::arg("n_rows"), py::arg("n_cols"), py::arg("rtol"),
+      py::arg("atol"), py::arg("restart"), py::arg("maxiter"), py::arg("plan") = py::none(),
+      "Jacobi-preconditioned restarted GMRES: (x, info, residual, iterations).");
   m.def("mm_info", &mm_info, py::arg("path"), "Header of a Matrix Market file.");
   m.def("mm_read_csr", &mm_read_csr, py::arg("path"), py::arg("dtype"), py::arg("index_dtype"),
         py::arg("n_threads") = 0,

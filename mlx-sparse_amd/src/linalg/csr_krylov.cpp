@@ -43,7 +43,8 @@ msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView
   if (indices.size() != data.size())
     throw std::invalid_argument(op + " data and indices must have equal length.");
   if (inv_diag) {
-    // reference: src/preconditioners/bicgstab/bicgstab.cpp:615-617
+    // reference: src/preconditioners/bicgstab/bicgstab.cpp:615-617,
+    // minres/minres.cpp:418-440, gmres/gmres.cpp:750-790
     require_rank(*inv_diag, 1, (op + " inv_diag").c_str());
     if (inv_diag->dtype != DType::Float32)
       throw std::invalid_argument(op + " inv_diag currently requires dtype float32.");
@@ -92,8 +93,15 @@ msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView
       check_status(msx_csr_minres_jacobi_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0,
                                              inv, xx, rtol, atol, maxiter, shift, &res),
                    op.c_str());
-  } else if (inv) {
-    throw std::invalid_argument(op + " is not available.");
+  } else if (kind == Krylov::GMRES && inv) {
+    if (data.device >= 0)
+      check_status(msx_csr_gmres_jacobi(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, inv,
+                                        xx, rtol, atol, restart, maxiter, plan, &res, ctx.stream),
+                   op.c_str());
+    else
+      check_status(msx_csr_gmres_jacobi_cpu(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0,
+                                            inv, xx, rtol, atol, restart, maxiter, &res),
+                   op.c_str());
   } else if (kind == Krylov::GMRES) {
     if (data.device >= 0)
       check_status(msx_csr_gmres(it, n_rows, nnz, d, indices.ptr, indptr.ptr, bb, xx0, xx, rtol,

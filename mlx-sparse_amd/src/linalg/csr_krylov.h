@@ -15,7 +15,9 @@ enum class Krylov { BiCGSTAB, MINRES, GMRES };
 // csr_gmres), then runs the device solver on ctx.stream (with `plan`,
 // nullable) or the host loop.  `restart`: GMRES's cycle length (> 0).
 // `inv_diag` non-null: the Jacobi-preconditioned loop (reference:
-// src/preconditioners/bicgstab/bicgstab.cpp:607-635 csr_bicgstab_jacobi).
+// src/preconditioners/bicgstab/bicgstab.cpp:607-635 csr_bicgstab_jacobi,
+// minres/minres.cpp:418-440 csr_minres_jacobi, gmres/gmres.cpp:750-790
+// csr_gmres_jacobi).
 msx_solver_result csr_krylov(Krylov kind, const ArrayView &data, const ArrayView &indices,
                              const ArrayView &indptr, const ArrayView &b, const ArrayView &x0,
                              const ArrayView &x, int64_t n_rows, int64_t n_cols, float rtol,

@@ -33,9 +33,10 @@
  *   - BiCGSTAB (src/linalg/bicgstab/bicgstab.cpp:80-362, csr_bicgstab_cpu_impl)
  *     and MINRES with its shift (src/linalg/minres/minres.cpp:68-312,
  *     csr_minres_cpu_impl), float32;
- *   - BiCGSTAB and MINRES with a Jacobi preconditioner
+ *   - BiCGSTAB, MINRES and restarted GMRES with a Jacobi preconditioner
  *     (src/preconditioners/bicgstab/bicgstab.cpp:140-521,
- *     src/preconditioners/minres/minres.cpp:93-330), float32;
+ *     src/preconditioners/minres/minres.cpp:93-330,
+ *     src/preconditioners/gmres/gmres.cpp:342-748), float32;
  *   - restarted GMRES (src/linalg/gmres/gmres.cpp:58-220, csr_gmres_impl)
  *     with its Arnoldi factorisation (src/linalg/arnoldi/arnoldi.cpp:79-159,
  *     csr_arnoldi_cpu_impl) and the Givens least-squares solve
@@ -1643,9 +1644,13 @@ static float norm_f(const float *v, int64_t n) {
  * modified Gram-Schmidt per step, each coefficient a double sum of float
  * products, subtracted in float; the step ends early when the new norm is
  * at most FLT_EPSILON. */
-int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices,
-                       const void *indptr, const float *v0, int64_t k, float *h, float *basis,
-                       int32_t *used_out) {
+/* With inv_diag (the Jacobi Arnoldi, src/preconditioners/gmres/gmres.cpp:
+ * 342-447): the basis of M A, M = diag(inv_diag) - w = M (A q) in float -
+ * no step when v0 or inv_diag holds a non-finite entry, and a non-finite
+ * new norm ends the factorisation with zero steps. */
+static int arnoldi_impl(int it, int64_t n, const float *data, const void *indices,
+                        const void *indptr, const float *inv_diag, const float *v0, int64_t k,
+                        float *h, float *basis, int32_t *used_out) {
   const int64_t cols = k + 1;
   float *w = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
   float *q = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
@@ -1657,15 +1662,27 @@ int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices
   memset(h, 0, (size_t)cols * (size_t)k * sizeof(float));
   memset(basis, 0, (size_t)n * (size_t)cols * sizeof(float));
   double v_norm2 = 0.0;
-  for (int64_t i = 0; i < n; ++i) v_norm2 += (double)v0[i] * (double)v0[i];
+  int inputs_ok = 1;
+  for (int64_t i = 0; i < n; ++i) {
+    v_norm2 += (double)v0[i] * (double)v0[i];
+    if (inv_diag) inputs_ok = inputs_ok && fin(v0[i]) && fin(inv_diag[i]);
+  }
   const float v_norm = (float)sqrt(v_norm2 < 0.0 ? 0.0 : v_norm2);
   const float eps = FLT_EPSILON;
+  if (inv_diag && (!inputs_ok || !fin(v_norm))) {
+    *used_out = 0;
+    free(w);
+    free(q);
+    return 0;
+  }
   for (int64_t i = 0; i < n; ++i)
     basis[i * cols] = v_norm <= eps ? (i == 0 ? 1.0f : 0.0f) : v0[i] / v_norm;
   int32_t used = 0;
   for (int64_t j = 0; j < k; ++j) {
     for (int64_t i = 0; i < n; ++i) q[i] = basis[i * cols + j];
     cg_spmv(it, n, data, indices, indptr, q, w);
+    if (inv_diag)
+      for (int64_t row = 0; row < n; ++row) w[row] = w[row] * inv_diag[row];
     for (int pass = 0; pass < 2; ++pass) {
       for (int64_t col = 0; col <= j; ++col) {
         double coeff = 0.0;
@@ -1684,6 +1701,10 @@ int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices
     const float h_next = norm_f(w, n);
     h[(j + 1) * k + j] = h_next;
     used = (int32_t)(j + 1);
+    if (inv_diag && !fin(h_next)) {
+      used = 0;
+      break;
+    }
     if (h_next <= eps) break;
     for (int64_t row = 0; row < n; ++row) basis[row * cols + j + 1] = w[row] / h_next;
   }
@@ -1691,6 +1712,18 @@ int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices
   free(w);
   free(q);
   return 0;
+}
+
+int oracle_csr_arnoldi(int it, int64_t n, const float *data, const void *indices,
+                       const void *indptr, const float *v0, int64_t k, float *h, float *basis,
+                       int32_t *used_out) {
+  return arnoldi_impl(it, n, data, indices, indptr, NULL, v0, k, h, basis, used_out);
+}
+
+int oracle_csr_arnoldi_jacobi(int it, int64_t n, const float *data, const void *indices,
+                              const void *indptr, const float *inv_diag, const float *v0,
+                              int64_t k, float *h, float *basis, int32_t *used_out) {
+  return arnoldi_impl(it, n, data, indices, indptr, inv_diag, v0, k, h, basis, used_out);
 }
 
 /* min ||a y - b|| for an upper-Hessenberg a of rows = cols + 1 (row-major,
@@ -1778,21 +1811,29 @@ static float gm_residual(int it, int64_t n, const float *data, const void *indic
  * budget ran out, -1 a failed least-squares solve, -3 non-finite; residual
  * the last true residual norm (infinity when the inputs are not finite);
  * iterations the Arnoldi steps taken. */
-int oracle_csr_gmres(int it, int64_t n, const float *data, const void *indices, const void *indptr,
-                     const float *b, const float *x0, float *x, float rtol, float atol,
-                     int64_t restart, int64_t maxiter, int32_t *info, float *residual,
-                     int32_t *iterations) {
+/* With inv_diag: GMRES with the Jacobi preconditioner
+ * (src/preconditioners/gmres/gmres.cpp:572-748, csr_gmres_jacobi_impl):
+ * each cycle starts from z0 = M r (its norm ||M r|| is the least-squares
+ * right-hand side, at most FLT_EPSILON: -1) over the Jacobi Arnoldi basis;
+ * the true residual ||r|| decides convergence; a non-finite inverse
+ * diagonal entry is a non-finite input; the least-squares solution is not
+ * tested on its own (a non-finite update row is). */
+static int gmres_impl(int it, int64_t n, const float *data, const void *indices,
+                      const void *indptr, const float *b, const float *x0, const float *inv_diag,
+                      float *x, float rtol, float atol, int64_t restart, int64_t maxiter,
+                      int32_t *info, float *residual, int32_t *iterations) {
   const size_t nb = (size_t)(n > 0 ? n : 1) * sizeof(float);
   const int64_t kmax = restart < maxiter ? restart : maxiter;
   const int64_t kcap = (kmax < n ? kmax : n) > 0 ? (kmax < n ? kmax : n) : 1;
   float *r = (float *)malloc(nb), *ax = (float *)malloc(nb), *v0 = (float *)malloc(nb);
+  float *z0 = (float *)malloc(nb);
   float *h = (float *)malloc((size_t)((kcap + 1) * kcap) * sizeof(float));
   float *basis = (float *)malloc((size_t)n * (size_t)(kcap + 1) * sizeof(float));
   double *hd = (double *)malloc((size_t)((kcap + 1) * kcap) * sizeof(double));
   double *e1 = (double *)malloc((size_t)(kcap + 1) * sizeof(double));
   double *y = (double *)malloc((size_t)kcap * sizeof(double));
-  if (!r || !ax || !v0 || !h || !basis || !hd || !e1 || !y) {
-    free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
+  if (!r || !ax || !v0 || !z0 || !h || !basis || !hd || !e1 || !y) {
+    free(r); free(ax); free(v0); free(z0); free(h); free(basis); free(hd); free(e1); free(y);
     return -1;
   }
   memcpy(x, x0, (size_t)n * sizeof(float));
@@ -1803,30 +1844,44 @@ int oracle_csr_gmres(int it, int64_t n, const float *data, const void *indices, 
   int32_t status = maxiter > 0 ? (int32_t)maxiter : 1;
   float res = INFINITY;
   int inputs_ok = fin(b_norm) && fin(tol);
-  for (int64_t i = 0; i < n; ++i) inputs_ok = inputs_ok && fin(x[i]) && fin(b[i]);
+  for (int64_t i = 0; i < n; ++i)
+    inputs_ok = inputs_ok && fin(x[i]) && fin(b[i]) && (!inv_diag || fin(inv_diag[i]));
   if (!inputs_ok) {
     status = -3;
     goto done;
   }
   while (iters < maxiter) {
     int finite = 1;
-    const float beta = gm_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
+    float beta = gm_residual(it, n, data, indices, indptr, b, x, ax, r, &finite);
     res = beta;
+    if (inv_diag) {
+      for (int64_t i = 0; i < n; ++i) {
+        z0[i] = inv_diag[i] * r[i];
+        finite = finite && fin(z0[i]);
+      }
+    }
     if (!finite) {
       status = -3;
       break;
     }
-    if (beta <= tol) {
+    if (res <= tol) {
       status = 0;
       break;
+    }
+    if (inv_diag) {
+      beta = norm_f(z0, n);
+      if (!fin(beta) || beta <= FLT_EPSILON) {
+        status = -1;
+        break;
+      }
     }
     int64_t steps = restart;
     if (maxiter - iters < steps) steps = maxiter - iters;
     if (n < steps) steps = n;
-    for (int64_t i = 0; i < n; ++i) v0[i] = r[i] / beta;
+    for (int64_t i = 0; i < n; ++i) v0[i] = (inv_diag ? z0[i] : r[i]) / beta;
     int32_t used = 0;
-    if (oracle_csr_arnoldi(it, n, data, indices, indptr, v0, steps, h, basis, &used) != 0) {
-      free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
+    if (arnoldi_impl(it, n, data, indices, indptr, inv_diag, v0, steps, h, basis, &used) != 0) {
+      free(r); free(ax); free(v0); free(z0); free(h); free(basis); free(hd); free(e1); free(y);
       return -1;
     }
     if (used == 0) {
@@ -1849,7 +1904,7 @@ int oracle_csr_gmres(int it, int64_t n, const float *data, const void *indices, 
       status = -1;
       break;
     }
-    for (int64_t c = 0; c < used; ++c)
+    for (int64_t c = 0; c < used && !inv_diag; ++c)
       if (!isfinite(y[c])) bad = 1;
     if (bad) {
       status = -3;
@@ -1891,6 +1946,23 @@ done:
   *info = status;
   *residual = res;
   *iterations = (int32_t)iters;
-  free(r); free(ax); free(v0); free(h); free(basis); free(hd); free(e1); free(y);
+  free(r); free(ax); free(v0); free(z0); free(h); free(basis); free(hd); free(e1); free(y);
   return 0;
+}
+
+int oracle_csr_gmres(int it, int64_t n, const float *data, const void *indices, const void *indptr,
+                     const float *b, const float *x0, float *x, float rtol, float atol,
+                     int64_t restart, int64_t maxiter, int32_t *info, float *residual,
+                     int32_t *iterations) {
+  return gmres_impl(it, n, data, indices, indptr, b, x0, NULL, x, rtol, atol, restart, maxiter,
+                    info, residual, iterations);
+}
+
+int oracle_csr_gmres_jacobi(int it, int64_t n, const float *data, const void *indices,
+                            const void *indptr, const float *b, const float *x0,
+                            const float *inv_diag, float *x, float rtol, float atol,
+                            int64_t restart, int64_t maxiter, int32_t *info, float *residual,
+                            int32_t *iterations) {
+  return gmres_impl(it, n, data, indices, indptr, b, x0, inv_diag, x, rtol, atol, restart,
+                    maxiter, info, residual, iterations);
 }

@@ -119,6 +119,11 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_csr_gmres.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
                                           vp, vp, vp]
         _lib.oracle_csr_gmres.restype = ci
+        _lib.oracle_csr_arnoldi_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, i64, vp, vp, vp]
+        _lib.oracle_csr_arnoldi_jacobi.restype = ci
+        _lib.oracle_csr_gmres_jacobi.argtypes = [ci, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                                 i64, i64, vp, vp, vp]
+        _lib.oracle_csr_gmres_jacobi.restype = ci
     return _lib
 
 
@@ -392,6 +397,46 @@ def csr_gmres(data, indices, indptr, b, x0=None, *, rtol: float = 1e-5, atol: fl
                                 ctypes.addressof(its))
     if rc != 0:
         raise MemoryError("oracle_csr_gmres failed")
+    return x, info.value, res.value, its.value
+
+
+def csr_arnoldi_jacobi(data, indices, indptr, inv_diag, v0, k: int):
+    """k Jacobi Arnoldi steps (the basis of M A, M = diag(inv_diag);
+    reference src/preconditioners/gmres/gmres.cpp:342-447).  Returns (h,
+    basis, used) as csr_arnoldi."""
+    data, indices, indptr, v0, _, n = _solver_inputs(data, indices, indptr, v0, None)
+    inv_diag = np.ascontiguousarray(inv_diag, np.float32)
+    assert inv_diag.shape == (n,)
+    h = np.empty((k + 1, k), np.float32)
+    basis = np.empty((n, k + 1), np.float32)
+    used = ctypes.c_int32()
+    rc = lib().oracle_csr_arnoldi_jacobi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                         _ptr(indptr), _ptr(inv_diag), _ptr(v0), k, _ptr(h),
+                                         _ptr(basis), ctypes.addressof(used))
+    if rc != 0:
+        raise MemoryError("oracle_csr_arnoldi_jacobi failed")
+    return h, basis, used.value
+
+
+def csr_gmres_jacobi(data, indices, indptr, b, inv_diag, x0=None, *, rtol: float = 1e-5,
+                     atol: float = 0.0, restart: int | None = None,
+                     maxiter: int | None = None):
+    """Restarted GMRES with the Jacobi preconditioner M = diag(inv_diag)
+    (reference src/preconditioners/gmres/gmres.cpp:572-748).  Returns (x,
+    info, residual, iterations)."""
+    data, indices, indptr, b, x0, n = _solver_inputs(data, indices, indptr, b, x0)
+    inv_diag = np.ascontiguousarray(inv_diag, np.float32)
+    assert inv_diag.shape == (n,)
+    restart = min(20, n) if restart is None else int(restart)
+    maxiter = 10 * n if maxiter is None else int(maxiter)
+    x = np.empty(n, np.float32)
+    info, res, its = ctypes.c_int32(), ctypes.c_float(), ctypes.c_int32()
+    rc = lib().oracle_csr_gmres_jacobi(ITYPES[indices.dtype], n, _ptr(data), _ptr(indices),
+                                       _ptr(indptr), _ptr(b), _ptr(x0), _ptr(inv_diag), _ptr(x),
+                                       rtol, atol, restart, maxiter, ctypes.addressof(info),
+                                       ctypes.addressof(res), ctypes.addressof(its))
+    if rc != 0:
+        raise MemoryError("oracle_csr_gmres_jacobi failed")
     return x, info.value, res.value, its.value
 
 

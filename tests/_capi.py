@@ -119,6 +119,10 @@ def lib() -> ctypes.CDLL:
                                     vp, vp]
         L.msx_csr_gmres_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, f32, f32, i64, i64,
                                         vp]
+        L.msx_csr_gmres_jacobi.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32, i64,
+                                           i64, vp, vp, vp]
+        L.msx_csr_gmres_jacobi_cpu.argtypes = [ci, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, f32,
+                                               i64, i64, vp]
         L.msx_cpu_worker_count.restype = ci
         L.msx_cpu_ranges.argtypes = [vp, i64, ci, vp, ctypes.POINTER(i64)]
         for name in ("msx_device_count", "msx_csr_plan_create", "msx_csr_plan_create_bound",
@@ -140,7 +144,8 @@ def lib() -> ctypes.CDLL:
                      "msx_csr_minres", "msx_csr_bicgstab_cpu", "msx_csr_minres_cpu",
                      "msx_csr_bicgstab_jacobi", "msx_csr_bicgstab_jacobi_cpu",
                      "msx_csr_minres_jacobi", "msx_csr_minres_jacobi_cpu",
-                     "msx_csr_gmres", "msx_csr_gmres_cpu"):
+                     "msx_csr_gmres", "msx_csr_gmres_cpu", "msx_csr_gmres_jacobi",
+                     "msx_csr_gmres_jacobi_cpu"):
             getattr(L, name).restype = ci
         _lib = L
     return _lib
@@ -453,20 +458,23 @@ def krylov(kind, data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, maxi
 
 
 def gmres(data, indices, indptr, b, x0=None, *, rtol=1e-5, atol=0.0, restart=None, maxiter=None,
-          plan=None):
-    """(x, info, residual, iterations) through msx_csr_gmres[_cpu]."""
+          plan=None, inv_diag=None):
+    """(x, info, residual, iterations) through msx_csr_gmres[_cpu]; with
+    `inv_diag`, msx_csr_gmres_jacobi[_cpu]."""
     n = b.numel()
     x0 = torch.zeros_like(b) if x0 is None else x0
     x = torch.empty_like(b)
     restart = min(20, n) if restart is None else restart
     maxiter = 10 * n if maxiter is None else maxiter
     res = SolverResult()
+    pre = () if inv_diag is None else (_p(inv_diag),)
+    name = "msx_csr_gmres" if inv_diag is None else "msx_csr_gmres_jacobi"
     head = (IT[indices.dtype], n, data.numel(), _p(data), _p(indices), _p(indptr), _p(b), _p(x0),
-            _p(x), rtol, atol, restart, maxiter)
+            *pre, _p(x), rtol, atol, restart, maxiter)
     L = lib()
     if b.device.type == "cpu":
-        st = L.msx_csr_gmres_cpu(*head, ctypes.byref(res))
+        st = getattr(L, f"{name}_cpu")(*head, ctypes.byref(res))
     else:
-        st = L.msx_csr_gmres(*head, plan.ptr if plan else None, ctypes.byref(res), _stream())
-    _check(st, "msx_csr_gmres")
+        st = getattr(L, name)(*head, plan.ptr if plan else None, ctypes.byref(res), _stream())
+    _check(st, name)
     return x, res.info, res.residual, res.iterations

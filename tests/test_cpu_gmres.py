@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import _capi
-from test_oracle_gmres import _csr, _random_nonsym
+from test_oracle_gmres import _csr, _random_nonsym, _scaled_nonsym
 
 
 def _native(A, b, index_dtype=np.int32, x0=None, **kw):
@@ -146,9 +146,135 @@ def test_linalg_gmres_argument_errors(cpu):
         ms.linalg.gmres(A, b, restart=0)
     with pytest.raises(TypeError, match="sparse matrices"):
         ms.linalg.gmres(A, b, M=A)
-    with pytest.raises(TypeError, match="identity"):
-        ms.linalg.gmres(A, b, M=ms.linalg.preconditioners.jacobi(A))
+    with pytest.raises(ValueError, match="preconditioner size"):
+        ms.linalg.gmres(A, b, M=ms.linalg.preconditioners.diagonal(np.ones(3, np.float32)))
     x, info = ms.linalg.gmres(A, b, M=ms.linalg.preconditioners.identity(A), maxiter=8)
     assert info == 0
     with pytest.raises(ValueError, match="length"):
         ms.linalg.gmres(A, torch.ones(3))
+
+
+# -- GMRES with a Jacobi preconditioner -------------------------------------------------------
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("restart", [1, 5, 20])
+def test_gmres_jacobi_cpu_equals_oracle(oracle, index_dtype, restart):
+    """msx_csr_gmres_jacobi_cpu runs the oracle's loop bit for bit: x,
+    status, residual and iterations, on row-scaled systems (converging, a
+    short budget, maxiter 0, a starting guess) and the Jacobi status rules
+    (a non-finite inverse diagonal entry: -3 with an infinite residual;
+    ||M r|| <= FLT_EPSILON: -1; a zero right-hand side: 0)."""
+    A, inv = _scaled_nonsym(300, seed=restart)
+    rng = np.random.default_rng(restart)
+    b = rng.uniform(-1, 1, 300).astype(np.float32)
+    x0 = (0.1 * rng.standard_normal(300)).astype(np.float32)
+    cases = [(A, b, inv, None, {"rtol": 1e-5, "maxiter": 3000}),
+             (A, b, inv, x0, {"rtol": 1e-4, "maxiter": 3000}),
+             (A, b, inv, None, {"rtol": 1e-9, "maxiter": 7}),
+             (A, b, inv, None, {"maxiter": 0})]
+    bad = inv.copy()
+    bad[7] = np.inf
+    cases.append((A, b, bad, None, {}))
+    cases.append((A, b, np.zeros(300, np.float32), None, {}))
+    cases.append((A, np.zeros(300, np.float32), inv, None, {}))
+    nan_b = b.copy()
+    nan_b[3] = np.nan
+    cases.append((A, nan_b, inv, None, {}))
+    for M, rhs, iv, guess, kw in cases:
+        kw = {"restart": restart, **kw}
+        args = (M.data.astype(np.float32), M.indices.astype(index_dtype),
+                M.indptr.astype(index_dtype))
+        got = _capi.gmres(*(torch.from_numpy(np.ascontiguousarray(a)) for a in args),
+                          torch.from_numpy(rhs), None if guess is None else torch.from_numpy(guess),
+                          inv_diag=torch.from_numpy(iv), **kw)
+        want = oracle.csr_gmres_jacobi(*args, rhs, iv, guess, **kw)
+        _same(got, want)
+
+
+def test_gmres_jacobi_cpu_rejects_bad_arguments():
+    d = torch.tensor([1.0])
+    i = torch.tensor([0], dtype=torch.int32)
+    p = torch.tensor([0, 1], dtype=torch.int32)
+    b = torch.ones(1)
+    with pytest.raises(RuntimeError, match="csr_gmres_jacobi requires restart > 0"):
+        _capi.gmres(d, i, p, b, restart=0, inv_diag=torch.ones(1))
+    L = _capi.lib()
+    res = _capi.SolverResult()
+    st = L.msx_csr_gmres_jacobi_cpu(_capi.IT[torch.int32], 1, 1, _capi._p(d), _capi._p(i),
+                                    _capi._p(p), _capi._p(b), _capi._p(b), None, _capi._p(b),
+                                    1e-5, 0.0, 1, 1, _capi.ctypes.byref(res))
+    assert st != 0 and "non-NULL" in _capi.last_error()
+
+
+def test_native_gmres_jacobi_reference_tests(cpu):
+    """The reference's native Jacobi GMRES tests through _native on the CPU
+    device (tests/test_linalg_preconditioners.py:1600-1667): the true
+    residual and a bounded iteration count, and a non-finite inverse
+    diagonal entry ending with -3, no iterations, an infinite residual and
+    x = x0."""
+    ms = cpu
+    from mlx_sparse import _native
+    from mlx_sparse.linalg import preconditioners
+
+    dense = np.array([[5.0, -1.0, 0.25, 0.0], [1.25, 4.0, -0.5, 0.25], [0.0, 0.75, 3.5, -1.0],
+                      [0.5, 0.0, 1.0, 4.5]], np.float32)
+    d, i, p = (torch.from_numpy(a) for a in _csr(dense))
+    A = ms.csr_array((d, i, p), shape=dense.shape, canonical=True)
+    b = np.array([2.0, -1.0, 0.25, 3.0], np.float32)
+    M = preconditioners.jacobi(A)
+    x, info, residual, iterations = _native.csr_gmres_jacobi(
+        d, i, p, torch.from_numpy(b), torch.zeros(4), M.inverse_diagonal, A.shape, rtol=1e-6,
+        atol=1e-7, restart=4, maxiter=32)
+    true = np.linalg.norm(dense @ x.numpy() - b)
+    assert int(info) == 0 and int(iterations) <= 8
+    assert float(residual) == pytest.approx(true, abs=1e-5)
+    assert true <= 2e-6 * max(np.linalg.norm(b), 1.0)
+
+    A2 = _spd_2x2(ms)
+    d2, i2, p2 = A2.buffers(torch.device("cpu"))
+    x, info, residual, iterations = _native.csr_gmres_jacobi(
+        d2, i2, p2, torch.tensor([1.0, 2.0]), torch.zeros(2), torch.tensor([np.inf, 1.0]),
+        (2, 2), rtol=1e-6, atol=1e-8, restart=2, maxiter=8)
+    assert int(info) == -3 and int(iterations) == 0 and np.isinf(float(residual))
+    assert not x.numpy().any()
+
+
+def test_linalg_gmres_jacobi_on_cpu(cpu, oracle):
+    """linalg.gmres(A, b, M=jacobi(A)) on the CPU device: the reference's
+    left-preconditioned test against SciPy
+    (tests/test_linalg_preconditioners.py:1547-1597), equal to the oracle's
+    Jacobi loop bit for bit; diagonal(...) and an inverse-diagonal tensor
+    are the same preconditioner, and the identity runs the plain loop."""
+    import scipy.sparse as sp
+    import scipy.sparse.linalg as spla
+
+    ms = cpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    dense = np.array([[7.0, -2.0, 0.5, 0.0], [1.0, 5.5, -1.0, 0.25], [0.0, -0.5, 4.5, 1.0],
+                      [0.25, 0.0, -0.75, 3.75]], np.float32)
+    d, i, p = _csr(dense)
+    A = ms.csr_array((torch.from_numpy(d), torch.from_numpy(i), torch.from_numpy(p)),
+                     shape=dense.shape, canonical=True)
+    b = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    inv = (1.0 / np.diag(dense)).astype(np.float32)
+    want = oracle.csr_gmres_jacobi(d, i, p, b, inv, rtol=1e-6, atol=1e-7, restart=4, maxiter=32)
+    Ms = spla.LinearOperator(dense.shape, matvec=lambda v: (1.0 / np.diag(dense)) * v,
+                             dtype=np.float32)
+    x_scipy, info_scipy = spla.gmres(sp.csr_matrix(dense), b, M=Ms, rtol=1e-6, atol=1e-7,
+                                     restart=4, maxiter=32)
+    assert info_scipy == 0
+    for M in (preconditioners.jacobi(A), preconditioners.diagonal(np.diag(dense)),
+              torch.from_numpy(inv)):
+        x, info = linalg.gmres(A, b, M=M, rtol=1e-6, atol=1e-7, restart=4, maxiter=32,
+                               return_info=True)
+        assert info.status == 0 and info.iterations == want[3]
+        assert x.numpy().tobytes() == want[0].tobytes()
+        np.testing.assert_allclose(x.numpy(), x_scipy, rtol=2e-4, atol=2e-4)
+        rel = np.linalg.norm(dense.astype(np.float64) @ x.numpy() - b) / np.linalg.norm(b)
+        assert rel <= 2e-6
+    x_id, info_id = linalg.gmres(A, b, M=preconditioners.identity(A), rtol=1e-6, maxiter=32)
+    x_base, info_base = linalg.gmres(A, b, rtol=1e-6, maxiter=32)
+    assert info_id == info_base == 0
+    assert x_id.numpy().tobytes() == x_base.numpy().tobytes()

@@ -137,37 +137,6 @@ def test_cpu_krylov_errors():
             _capi.krylov(kind, d, i, p, torch.ones(1), maxiter=-1)
 
 
-@pytest.mark.parametrize("solver", ["gmres"])
-def test_preconditioned_variants_are_an_explicit_deviation(cpu, solver):
-    """The reference dispatches a diagonal / Jacobi M of gmres to a separate
-    native loop (csr_gmres_jacobi: reference
-    mlx_sparse/linalg/_iterative.py:765-797).  Where this build has no such
-    loop, every inverse diagonal form of M raises TypeError naming the
-    supported choices, a sparse matrix as M raises the reference's
-    TypeError, and M = None or the identity runs the plain loop."""
-    ms = cpu
-    from mlx_sparse import linalg
-    from mlx_sparse.linalg import preconditioners
-
-    dense = np.array([[4.0, 1.0, 0.0], [1.0, 2.5, 0.5], [0.0, 0.5, 3.0]], np.float32)
-    d, i, p = _csr(dense)
-    A = ms.csr_array((d, i, p), shape=dense.shape, canonical=True)
-    b = np.ones(3, np.float32)
-    fn = getattr(linalg, solver)
-    for M in (preconditioners.jacobi(A), preconditioners.diagonal(np.diag(dense)),
-              torch.from_numpy((1.0 / np.diag(dense)).astype(np.float32))):
-        with pytest.raises(TypeError, match="supports only the identity preconditioners"):
-            fn(A, b, M=M)
-    with pytest.raises(TypeError, match="sparse matrices"):
-        fn(A, b, M=A)
-    kw = {"check_preconditioner": False} if solver == "minres" else {}
-    for M in (None, preconditioners.identity(A)):
-        x, info = fn(A, b, M=M, rtol=1e-6, return_info=True, **kw)
-        assert info.status == 0
-        np.testing.assert_allclose(x.numpy(), np.linalg.solve(dense, b), rtol=1e-4, atol=1e-5)
-        assert ms.default_torch_device().type == "cpu"
-
-
 # -- BiCGSTAB with a Jacobi preconditioner ---------------------------------------------
 
 def _row_scaled(g=16, seed=9):

@@ -239,3 +239,138 @@ def test_full_size_gmres_three_cycles(gpu):
     assert abs(info.residual_norm - wres) <= 1e-4 * wres
     ref = np.linalg.norm(wx.astype(np.float64))
     assert np.linalg.norm(x.cpu().numpy().astype(np.float64) - wx) <= 1e-4 * ref
+
+
+# -- GMRES with a Jacobi preconditioner (msx_csr_gmres_jacobi) ----------------------------
+
+def _row_scaled(A0, seed, decades=1.0):
+    """A0 with rows scaled by 10^U[-decades, decades] and its inverse
+    diagonal: the Jacobi loop undoes the scaling, the plain loop needs many
+    more Arnoldi steps."""
+    rng = np.random.default_rng(seed)
+    s = (10.0 ** rng.uniform(-decades, decades, A0.shape[0])).astype(np.float32)
+    A = (sp.diags(s) @ A0).tocsr().astype(np.float32)
+    A.sort_indices()
+    b = (s * rng.uniform(-1, 1, A.shape[0])).astype(np.float32)
+    return A, b, (1.0 / A.diagonal()).astype(np.float32)
+
+
+def _gpu_jacobi(A, b, inv, index_dtype=np.int32, slice_mode=None, plan=True, x0=None, **kw):
+    d, i, p = (torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in _args(A, index_dtype))
+    pl = _capi.Plan(p, A.shape[0], d.numel(), data=d, indices=i, n_cols=A.shape[1],
+                    slice_mode=slice_mode) if plan else None
+    out = _capi.gmres(d, i, p, torch.from_numpy(b).to(DEV),
+                      None if x0 is None else torch.from_numpy(x0).to(DEV), plan=pl,
+                      inv_diag=torch.from_numpy(inv).to(DEV), **kw)
+    torch.cuda.synchronize()
+    return (out[0].cpu().numpy(),) + tuple(out[1:])
+
+
+def _jacobi_checks(A, b, inv, x, res, rtol, wx):
+    dense = A.toarray().astype(np.float64)
+    exact = np.linalg.solve(dense, b.astype(np.float64))
+    cond = np.linalg.cond(np.diag(inv.astype(np.float64)) @ dense)
+    assert np.linalg.norm(x - exact) <= 4 * cond * rtol * np.linalg.norm(exact)
+    true_res = np.linalg.norm(b.astype(np.float64) - dense @ x.astype(np.float64))
+    assert res <= rtol * np.linalg.norm(b) * (1 + 1e-5), res
+    assert abs(true_res - res) <= 1e-5 * np.linalg.norm(b) + 1e-3 * res
+    assert np.linalg.norm(x - wx) <= 1e-4 * np.linalg.norm(wx) + 4 * cond * rtol * \
+        np.linalg.norm(exact)
+
+
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("restart", [1, 5, 20])
+def test_gmres_jacobi_matches_oracle(index_dtype, restart):
+    """Status equal to the oracle's, iterations within one cycle, x solving
+    the system as well as the oracle's, on row-scaled random systems (and
+    one with a starting guess)."""
+    A, b, inv = _row_scaled(_random_nonsym(1200, seed=restart, density=0.005, shift=0.5),
+                            seed=restart + 1)
+    x0 = np.random.default_rng(restart).uniform(-0.1, 0.1, 1200).astype(np.float32)
+    for guess in (None, x0):
+        print(f"gmres jacobi random n=1200 restart={restart} x0={guess is not None} "
+              f"{np.dtype(index_dtype).name}", flush=True)
+        x, info, res, its = _gpu_jacobi(A, b, inv, index_dtype, x0=guess, rtol=1e-5,
+                                        restart=restart, maxiter=20000)
+        wx, winfo, wres, wits = orc.csr_gmres_jacobi(*_args(A, index_dtype), b, inv, guess,
+                                                     rtol=1e-5, restart=restart, maxiter=20000)
+        assert info == winfo == 0 and abs(its - wits) <= restart, (its, wits)
+        _jacobi_checks(A, b, inv, x, res, 1e-5, wx)
+
+
+@pytest.mark.parametrize("mode", ["blocks", "panels", "none"])
+def test_gmres_jacobi_routes_and_reproducible(mode):
+    A, b, inv = _row_scaled(convection_3d(40), seed=3)
+    kw = {"plan": mode != "none",
+          "slice_mode": {"blocks": _capi.SLICE_OFF, "panels": _capi.SLICE_PANELS,
+                         "none": None}[mode]}
+    print(f"gmres jacobi route={mode} n={A.shape[0]}", flush=True)
+    r1 = _gpu_jacobi(A, b, inv, rtol=1e-5, restart=10, **kw)
+    r2 = _gpu_jacobi(A, b, inv, rtol=1e-5, restart=10, **kw)
+    assert r1[1:] == r2[1:] and r1[0].tobytes() == r2[0].tobytes()
+    wx, winfo, wres, wits = orc.csr_gmres_jacobi(*_args(A), b, inv, rtol=1e-5, restart=10)
+    assert r1[1] == winfo == 0 and abs(r1[3] - wits) <= 10 + wits // 20, (r1[3], wits)
+    true_res = np.linalg.norm(b - A.astype(np.float64) @ r1[0].astype(np.float64))
+    assert r1[2] <= 1e-5 * np.linalg.norm(b) * (1 + 1e-5)
+    assert abs(true_res - r1[2]) <= 1e-5 * np.linalg.norm(b) + 1e-3 * r1[2]
+    assert np.linalg.norm(r1[0].astype(np.float64) - wx) <= 1e-2 * np.linalg.norm(wx)
+
+
+def test_gmres_jacobi_status_cases_match_oracle():
+    """The Jacobi status rules against the oracle: a non-finite inverse
+    diagonal entry or b (-3, residual +inf, no iterations), ||M r|| at most
+    FLT_EPSILON (-1), a zero right-hand side, an exact x0, maxiter 0 and a
+    short budget."""
+    dense = np.diag([2.0, 3.0, 4.0, 5.0, 6.0, 7.0]).astype(np.float32)
+    dense[0, 5] = 0.5
+    dense[3, 1] = -0.25
+    A = sp.csr_matrix(dense)
+    A.sort_indices()
+    inv = (1.0 / np.diag(dense)).astype(np.float32)
+    b = np.linspace(-1.0, 1.5, 6, dtype=np.float32)
+    bad_b = b.copy()
+    bad_b[2] = np.nan
+    bad_inv = inv.copy()
+    bad_inv[1] = np.inf
+    exact = np.linalg.solve(dense.astype(np.float64), b).astype(np.float32)
+    bx = (dense.astype(np.float64) @ exact).astype(np.float32)
+    cases = [(np.zeros(6, np.float32), inv, None, {}), (b, inv, None, {"maxiter": 0}),
+             (b, inv, None, {"maxiter": 3, "restart": 2, "rtol": 1e-9}),
+             (bad_b, inv, None, {}), (b, bad_inv, None, {}),
+             (b, np.zeros(6, np.float32), None, {}), (b, np.full(6, 1e-30, np.float32), None, {}),
+             (bx, inv, exact, {"atol": 1e-5}),
+             (b, inv, None, {"rtol": 1e-6, "atol": 1e-7, "restart": 4, "maxiter": 32})]
+    for rhs, iv, x0, kw in cases:
+        print(f"gmres jacobi status case {kw} inv0={iv[0]} inv1={iv[1]}", flush=True)
+        x, info, res, its = _gpu_jacobi(A, rhs, iv, x0=x0, **kw)
+        wx, winfo, wres, wits = orc.csr_gmres_jacobi(*_args(A), rhs, iv, x0, **kw)
+        assert (info, its) == (winfo, wits), (kw, info, its, winfo, wits)
+        assert np.isinf(res) == np.isinf(wres) and np.isnan(res) == np.isnan(wres)
+        if np.isfinite(wres):
+            assert res == pytest.approx(wres, rel=1e-5, abs=1e-7)
+        finite = np.isfinite(wx)
+        np.testing.assert_array_equal(np.isfinite(x), finite)
+        np.testing.assert_allclose(x[finite], wx[finite], rtol=1e-4, atol=1e-5)
+
+
+def test_gmres_jacobi_api_on_gpu(gpu):
+    """linalg.gmres with M = preconditioners.jacobi(A) on the device: the
+    reference's left-preconditioned system and bounds
+    (tests/test_linalg_preconditioners.py:1547-1597, 1600-1639)."""
+    ms = gpu
+    from mlx_sparse import linalg
+    from mlx_sparse.linalg import preconditioners
+
+    dense = np.array([[7.0, -2.0, 0.5, 0.0], [1.0, 5.5, -1.0, 0.25], [0.0, -0.5, 4.5, 1.0],
+                      [0.25, 0.0, -0.75, 3.75]], np.float32)
+    d, ix, ip = _csr(dense)
+    csr = ms.csr_array((torch.from_numpy(d), torch.from_numpy(ix), torch.from_numpy(ip)),
+                       shape=dense.shape, canonical=True)
+    b = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    x, info = linalg.gmres(csr, b, M=preconditioners.jacobi(csr), rtol=1e-6, atol=1e-7,
+                           restart=4, maxiter=32, return_info=True)
+    assert info.status == 0 and info.preconditioner == "jacobi" and x.device.type == "cuda"
+    xn = x.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(dense @ xn - b) / np.linalg.norm(b) <= 2e-6
+    np.testing.assert_allclose(xn, np.linalg.solve(dense.astype(np.float64), b), rtol=2e-4,
+                               atol=2e-4)

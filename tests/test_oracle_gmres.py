@@ -316,3 +316,129 @@ def test_restart_larger_than_n_clamps_to_n():
                                       maxiter=100)
     assert info == 0 and its <= 12 + 12  # one full cycle of n steps, then at most one more
     assert _rel_residual(A.toarray(), x, b) <= 1e-5 * 1.01
+
+
+# -- GMRES with a Jacobi preconditioner ------------------------------------------------
+#
+# oracle_csr_arnoldi_jacobi / oracle_csr_gmres_jacobi (reference
+# src/preconditioners/gmres/gmres.cpp:342-748) are pinned by: M = I
+# reproducing the plain loops bit for bit; the Arnoldi relation of M A; the
+# Krylov closed form for M A with k distinct eigenvalues; the reference's own
+# tests (tests/test_linalg_preconditioners.py:1600-1667); the Jacobi status
+# rules (||M r|| <= FLT_EPSILON: -1; a non-finite inverse diagonal: -3 with an
+# infinite residual).
+
+def _scaled_nonsym(n, seed, decades=1.0):
+    """_random_nonsym with rows scaled by 10^U[-decades, decades]; over two
+    decades the float32 true residual stagnates near 2e-5 relative."""
+    A0 = _random_nonsym(n, seed)
+    rng = np.random.default_rng(seed + 1)
+    d = (10.0 ** rng.uniform(-decades, decades, n)).astype(np.float32)
+    A = (sp.diags(d) @ A0).tocsr().astype(np.float32)
+    A.sort_indices()
+    return A, (1.0 / A.diagonal()).astype(np.float32)
+
+
+@pytest.mark.parametrize("restart", [3, 10])
+def test_gmres_jacobi_identity_matches_plain(restart):
+    A = _random_nonsym(80, seed=restart)
+    b = np.random.default_rng(restart).uniform(-1, 1, 80).astype(np.float32)
+    ones = np.ones(80, np.float32)
+    got = orc.csr_gmres_jacobi(A.data, A.indices, A.indptr, b, ones, rtol=1e-5, restart=restart)
+    want = orc.csr_gmres(A.data, A.indices, A.indptr, b, rtol=1e-5, restart=restart)
+    assert got[1:] == want[1:]
+    np.testing.assert_array_equal(got[0], want[0])
+    v0 = np.random.default_rng(1).standard_normal(80).astype(np.float32)
+    hj, Vj, uj = orc.csr_arnoldi_jacobi(A.data, A.indices, A.indptr, ones, v0, 7)
+    hp, Vp, up = orc.csr_arnoldi(A.data, A.indices, A.indptr, v0, 7)
+    assert uj == up == 7
+    np.testing.assert_array_equal(hj, hp)
+    np.testing.assert_array_equal(Vj, Vp)
+
+
+def test_arnoldi_jacobi_relation():
+    A, inv = _scaled_nonsym(60, seed=3, decades=2.0)
+    v0 = np.random.default_rng(2).standard_normal(60).astype(np.float32)
+    k = 8
+    h, V, used = orc.csr_arnoldi_jacobi(A.data, A.indices, A.indptr, inv, v0, k)
+    assert used == k
+    MA = np.diag(inv.astype(np.float64)) @ A.toarray().astype(np.float64)
+    H, V = h.astype(np.float64), V.astype(np.float64)
+    np.testing.assert_allclose(MA @ V[:, :k], V @ H, atol=3e-5 * np.abs(MA).max())
+    np.testing.assert_allclose(V.T @ V, np.eye(k + 1), atol=1e-5)
+    # the plain factorisation is of A, not M A
+    hp, _, _ = orc.csr_arnoldi(A.data, A.indices, A.indptr, v0, k)
+    assert np.abs(hp - h).max() > 1e-2
+
+
+@pytest.mark.parametrize("k", [2, 3, 5])
+def test_gmres_jacobi_k_distinct_eigenvalues(k):
+    rng = np.random.default_rng(k)
+    n = 30
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    lam = np.array([[1.0, 3.0, -2.0, 5.0, 0.5][j % k] for j in range(n)])
+    B = (Q * lam) @ Q.T
+    d = 10.0 ** rng.uniform(-1, 1, n)
+    dense = (B / d[:, None]).astype(np.float32)  # M A = B for M = diag(d)
+    inv = d.astype(np.float32)
+    b = rng.uniform(-1, 1, n).astype(np.float32)
+    x, info, res, its = orc.csr_gmres_jacobi(*_csr(dense), b, inv, rtol=1e-4, restart=k,
+                                             maxiter=k)
+    assert (info, its) == (0, k)
+    _, info1, _, _ = orc.csr_gmres_jacobi(*_csr(dense), b, inv, rtol=1e-4, restart=k - 1,
+                                          maxiter=k - 1)
+    assert info1 == k - 1
+
+
+def test_gmres_jacobi_reference_tests():
+    A = np.array([[5.0, -1.0, 0.25, 0.0], [1.25, 4.0, -0.5, 0.25], [0.0, 0.75, 3.5, -1.0],
+                  [0.5, 0.0, 1.0, 4.5]], np.float32)
+    b = np.array([2.0, -1.0, 0.25, 3.0], np.float32)
+    inv = (1.0 / np.diag(A)).astype(np.float32)
+    x, info, res, its = orc.csr_gmres_jacobi(*_csr(A), b, inv, rtol=1e-6, atol=1e-7, restart=4,
+                                             maxiter=32)
+    true = np.linalg.norm(A.astype(np.float64) @ x - b)
+    assert info == 0 and its <= 8
+    assert res == pytest.approx(true, abs=1e-5)
+    assert true <= 2e-6 * max(np.linalg.norm(b), 1.0)
+    spd = np.array([[4.0, 1.0], [1.0, 3.0]], np.float32)
+    x, info, res, its = orc.csr_gmres_jacobi(*_csr(spd), np.array([1.0, 2.0], np.float32),
+                                             np.array([np.inf, 1.0], np.float32), rtol=1e-6,
+                                             atol=1e-8, restart=2, maxiter=8)
+    assert (info, its) == (-3, 0) and np.isinf(res) and not x.any()
+
+
+def test_gmres_jacobi_row_scaled_against_dense():
+    A, inv = _scaled_nonsym(200, seed=11)
+    b = np.random.default_rng(5).uniform(-1, 1, 200).astype(np.float32)
+    x, info, res, its = orc.csr_gmres_jacobi(A.data, A.indices, A.indptr, b, inv, rtol=1e-5,
+                                             restart=20, maxiter=400)
+    assert info == 0
+    dense = A.toarray().astype(np.float64)
+    want = np.linalg.solve(dense, b.astype(np.float64))
+    cond = np.linalg.cond(np.diag(inv.astype(np.float64)) @ dense)
+    assert np.linalg.norm(x - want) <= 1e-5 * cond * np.linalg.norm(want)
+    true = np.linalg.norm(b - dense @ x)
+    assert abs(res - true) <= 1e-4 * true + 1e-6 * np.linalg.norm(b)
+    # the plain loop on the badly scaled rows needs more Arnoldi steps
+    _, info_p, _, its_p = orc.csr_gmres(A.data, A.indices, A.indptr, b, rtol=1e-5, restart=20,
+                                        maxiter=400)
+    assert info_p != 0 or its_p > its
+
+
+def test_gmres_jacobi_status_rules():
+    A = np.array([[4.0, 1.0], [1.0, 3.0]], np.float32)
+    b = np.array([1.0, 2.0], np.float32)
+    # ||M r|| <= FLT_EPSILON while ||r|| > tol: -1 before any step
+    for inv in (np.zeros(2, np.float32), np.full(2, 1e-30, np.float32)):
+        x, info, res, its = orc.csr_gmres_jacobi(*_csr(A), b, inv, rtol=1e-6)
+        assert (info, its) == (-1, 0) and res == np.float32(np.linalg.norm(b))
+    inv = np.array([0.25, 1.0 / 3.0], np.float32)
+    x, info, res, its = orc.csr_gmres_jacobi(*_csr(A), np.zeros(2, np.float32), inv)
+    assert (info, its, res) == (0, 0, 0.0)
+    x, info, res, its = orc.csr_gmres_jacobi(*_csr(A), b, inv, maxiter=0)
+    assert (info, its) == (1, 0) and res == np.float32(np.linalg.norm(b))
+    bad = b.copy()
+    bad[1] = np.nan
+    _, info, res, its = orc.csr_gmres_jacobi(*_csr(A), bad, inv)
+    assert (info, its) == (-3, 0) and np.isinf(res)
