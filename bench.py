@@ -617,7 +617,8 @@ def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
 def configs_leg(ext, dev, scratch) -> list:
     """SpMV / SpMM on each benchmark configuration but the headline, through
     the cached bound plan (AUTO's choice), timed like the headline (graph
-    replay) and cold (1 GiB written between calls), against the compulsory
+    replay) and cold (1 GiB written between calls; cold_clean: written, then
+    read, so no dirty lines of the flush remain), against the compulsory
     bytes nnz*(value+index) + indptr + x once + y once (X, Y at width k)."""
     rows = []
     m_kind, m = None, None
@@ -632,6 +633,7 @@ def configs_leg(ext, dev, scratch) -> list:
         fn, info, nbytes, nflops, keep = _case_call(ext, case, m, data, X, dev)
         t, _ = _graph_time(fn, calls=10 if k else 20)
         cold = _cold_time(fn, 10, scratch)
+        clean = _cold_time(fn, 10, scratch, clean=True)
         row = {"case": label, "id": case, "nnz": m.nnz,
                "op": "spmv" if k is None else f"spmm k={k}",
                "plan": _kind(info), "plan_bytes": info["plan_bytes"],
@@ -642,7 +644,9 @@ def configs_leg(ext, dev, scratch) -> list:
                "frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "gflops": round(nflops / (t * 1e-3) / 1e9, 1),
                "cold_us": round(cold * 1e3, 2),
-               "cold_frac": round(nbytes / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+               "cold_frac": round(nbytes / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "cold_clean_us": round(clean * 1e3, 2),
+               "cold_clean_frac": round(nbytes / (clean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"config: {row}")
         rows.append(row)
         del fn, keep, data, X
@@ -977,7 +981,9 @@ def main() -> int:
                 "frac": round(nbytes / (float(kern_t) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "gflops": round(nflops / (float(kern_t) * 1e-3) / 1e9, 1),
                 "cold_us": round(cold_ms * 1e3, 2),
-                "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4)}
+                "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
+                "cold_clean_us": round(clean_ms * 1e3, 2),
+                "cold_clean_frac": round(clean_gbs / HBM_PEAK_GBS, 4)}
         result["configs"] = [head] + configs_leg(ext, dev, scratch)
         torch.cuda.empty_cache()
 
