@@ -566,10 +566,11 @@ def krylov_leg(dev) -> dict:
 def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
     """Restarted GMRES(20) on the convection-diffusion variant at n = 128^3,
     rtol 1e-5.  Bytes per Arnoldi step j (0-based): the SpMV's compulsory
-    bytes, 8 n for the first Gram-Schmidt dot, 16 n for each of the 2 (j+1)
-    later passes (w, two basis vectors read, w written) and 8 n for the
-    normalisation; per cycle also the residual (12 n) and the update
-    ((used + 2) 4 n).  The CPU figure is the oracle's single-threaded
+    bytes, then the paired Gram-Schmidt passes - 12 n for the first (w and
+    two basis vectors read), 24 n for each of the j later pairs (w and four
+    basis vectors read, w written), 16 n for the last pass (w and two basis
+    vectors read, w written, w.w) - and 8 n for the normalisation; per cycle
+    also the residual (12 n) and the update ((used + 2) 4 n).  The CPU figure is the oracle's single-threaded
     restatement of the reference loop, timed over one cycle of 20 steps."""
     import mlx_sparse as ms
     from mlx_sparse import linalg
@@ -591,7 +592,7 @@ def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
     cycles = -(-its // restart)
     step_bytes = 0
     for j in range(restart):
-        step_bytes += spmv_bytes + 8 * n + 2 * (j + 1) * 16 * n + 8 * n
+        step_bytes += spmv_bytes + 12 * n + j * 24 * n + 16 * n + 8 * n
     cycle_bytes = step_bytes + 12 * n + (restart + 2) * 4 * n + spmv_bytes
     total_bytes = cycles * cycle_bytes
     t0 = time.perf_counter()

@@ -5,13 +5,14 @@
 // kernel of one 256-thread threadgroup (reference:
 // src/linalg/gmres/gmres.cpp:58-220, src/linalg/arnoldi/arnoldi.cpp:184-225,
 // arnoldi.metal).  Here every Arnoldi step is device-wide: the path's SpMV
-// with the matrix's plan, then one fused pass per modified Gram-Schmidt
-// column (two passes over the basis, as the reference's CPU Arnoldi,
-// arnoldi.cpp:118-146).  Pass s subtracts the previous column's projection
-// from w and forms the next column's dot product, so each coefficient costs
-// one pass over w: the coefficients stay sequential, as MGS needs, and every
-// workgroup adds the previous pass's double partials in the same order
-// (msx_solver.h), so all of them subtract the same float coefficient.
+// with the matrix's plan, then modified Gram-Schmidt with two sweeps over
+// the basis, as the reference's CPU Arnoldi (arnoldi.cpp:118-146), two
+// projections per pass over w: a pass subtracts the previous pair's
+// projections from w and forms the dot products of the next pair's columns
+// with w and with each other, from which the second coefficient of the pair
+// is the sequential one in exact arithmetic (gm_pair).  Every workgroup
+// adds the previous pass's double partials in the same order (msx_solver.h),
+// so all of them subtract the same float coefficients.
 //
 // Per cycle (the host loop of gmres.cpp:86-207):
 //   gm_resid   r = b - A x; r.r, its non-finite count, b.b, non-finite b, x
@@ -19,7 +20,7 @@
 //   gm_v0norm  (r / beta).(r / beta)
 //   gm_start   V0 = (r / beta) / ||r / beta|| (e0 when that norm <= eps);
 //              clears h and the cycle state
-//   step j:    w = A V_j; gm_mgs s = 0 .. 2 (j + 1); gm_norm
+//   step j:    w = A V_j; gm_pair m = 0 .. j + 1; gm_norm
 //              (h[j+1][j] = ||w||; V_{j+1} = w / ||w|| unless ||w|| <= eps,
 //              which ends the cycle's steps: later passes return at once)
 //   (host)     reads h and the steps taken, solves the (used + 1) x used
@@ -147,80 +148,104 @@ __global__ void __launch_bounds__(kSolverThreads)
   }
 }
 
-// Gram-Schmidt pass s of Arnoldi step j (ncol = j + 1 columns, two sweeps):
-// with s > 0, column (s - 1) % ncol's coefficient (the previous pass's
-// total, rounded to float) goes into h and its projection leaves w; then
-// the dot product of the next column (s < 2 ncol) or w.w (s = 2 ncol).
-// The previous pass's partials, then a thread's first kUnroll elements of w
-// and of both basis vectors, are loaded before the partials are reduced, so
-// that the reduction (its wave sums and barriers) overlaps the element
-// loads.  J: pass 0 first scales w = A v_j by inv_diag in float (the Jacobi
-// Arnoldi's w = M A q, gmres.cpp:413-415 there) and writes it back.
+// Gram-Schmidt pass m of Arnoldi step j (ncol = j + 1 columns).  The two
+// sweeps project w onto the columns in the order 0..j, 0..j; pass m takes
+// the pair of projections 2m and 2m + 1 of that list (columns a = 2m % ncol
+// and b = (2m + 1) % ncol) and the last pass (m = ncol) takes w.w.
+//   - m > 0: the previous pair's coefficients come from the previous
+//     pass's totals: c_a = d_a rounded to float, c_b = (d_b - c_a g)
+//     rounded to float, where d_a = w.q_a, d_b = w.q_b and g = q_a.q_b
+//     were summed before either projection left w - the value of
+//     (w - c_a q_a).q_b in exact arithmetic, so one pass does the work of
+//     two sequential ones; both go into h and leave w in the sequential
+//     order (w = w - c_a q_a, then w = w - c_b q_b, float operations);
+//   - then d_a, d_b and g of this pair (double sums of float products).
+// The previous pass's partials, then a thread's first kUnroll elements of
+// every stream, are loaded before the partials are reduced, so that the
+// reduction (its wave sums and barriers) overlaps the element loads.  J:
+// pass 0 first scales w = A v_j by inv_diag in float (the Jacobi Arnoldi's
+// w = M A q, gmres.cpp:413-415 there) and writes it back.
 template <bool J>
 __global__ void __launch_bounds__(kSolverThreads)
-    gm_mgs(const float *__restrict__ V, int64_t ld, float *__restrict__ w,
-           const float *__restrict__ inv_diag, int64_t n, int32_t j, int32_t s,
-           const double *part_in, int nparts, double *part_out, float *__restrict__ h, int64_t k,
-           const GmState *st) {
+    gm_pair(const float *__restrict__ V, int64_t ld, float *__restrict__ w,
+            const float *__restrict__ inv_diag, int64_t n, int32_t j, int32_t m,
+            const double *part_in, int nparts, double *part_out, float *__restrict__ h, int64_t k,
+            const GmState *st) {
   if (st->stop_at < j) return;  // an earlier step ended this cycle
   const int32_t ncol = j + 1;
-  const bool sub = s > 0, norm = s == 2 * ncol;
-  // pass 0 has no projection to subtract: with J its second stream is inv_diag
-  const float *q_prev = (J && !sub) ? inv_diag : V + static_cast<int64_t>(sub ? (s - 1) % ncol : 0) * ld;
-  const float *q = V + static_cast<int64_t>(norm ? 0 : s % ncol) * ld;
+  const bool sub = m > 0, norm = m == ncol;
+  const int64_t pa = sub ? (2 * m - 2) % ncol : 0, pb = sub ? (2 * m - 1) % ncol : 0;
+  const int64_t qa = norm ? 0 : (2 * m) % ncol, qb = norm ? 0 : (2 * m + 1) % ncol;
+  // pass 0 subtracts nothing: with J its first projection stream is inv_diag
+  const float *ua = (J && !sub) ? inv_diag : V + pa * ld;
+  const float *ub = V + pb * ld;
+  const float *va = V + qa * ld;
+  const float *vb = V + qb * ld;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kSolverThreads;
   const int64_t base0 = static_cast<int64_t>(blockIdx.x) * kSolverThreads + threadIdx.x;
   double pv_in[kSlots] = {0.0, 0.0, 0.0, 0.0};
   if (sub) load_partials(part_in, nparts, pv_in);
-  float w0[kUnroll], p0[kUnroll], q0[kUnroll];
+  float w0[kUnroll], a0[kUnroll], b0[kUnroll], x0[kUnroll], y0[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t i = base0 + u * stride < n ? base0 + u * stride : (base0 < n ? base0 : 0);
     w0[u] = w[i];
-    p0[u] = q_prev[i];
-    q0[u] = q[i];
+    a0[u] = (sub || J) ? ua[i] : 0.0f;
+    b0[u] = sub ? ub[i] : 0.0f;
+    x0[u] = norm ? 0.0f : va[i];
+    y0[u] = norm ? 0.0f : vb[i];
   }
-  float coeff = 0.0f;
+  float ca = 0.0f, cb = 0.0f;
   if (sub) {
     double t[kSlots];
     reduce_partials(pv_in, nparts, t);
-    coeff = static_cast<float>(t[0]);
-    if (lead()) h[static_cast<int64_t>((s - 1) % ncol) * k + j] += coeff;
+    ca = static_cast<float>(t[0]);
+    cb = static_cast<float>(t[1] - static_cast<double>(ca) * t[2]);
+    if (lead()) {
+      h[pa * k + j] += ca;
+      h[pb * k + j] += cb;
+    }
   }
-  double acc = 0.0;
-  auto one = [&](int64_t i, float wv, float pv, float qv) {
+  double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
+  auto one = [&](int64_t i, float wv, float av, float bv, float xv, float yv) {
     if (sub) {
-      const float t = coeff * pv;
-      wv = wv - t;
+      const float ta = ca * av;
+      wv = wv - ta;
+      const float tb = cb * bv;
+      wv = wv - tb;
       w[i] = wv;
     } else if (J) {
-      wv = wv * pv;
+      wv = wv * av;
       w[i] = wv;
     }
     if (norm) {
-      acc += static_cast<double>(wv) * static_cast<double>(wv);
+      acc0 += static_cast<double>(wv) * static_cast<double>(wv);
     } else {
-      const float prod = qv * wv;
-      acc += static_cast<double>(prod);
+      const float pa_ = xv * wv, pb_ = yv * wv, g = xv * yv;
+      acc0 += static_cast<double>(pa_);
+      acc1 += static_cast<double>(pb_);
+      acc2 += static_cast<double>(g);
     }
   };
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u)
-    if (base0 + u * stride < n) one(base0 + u * stride, w0[u], p0[u], q0[u]);
+    if (base0 + u * stride < n) one(base0 + u * stride, w0[u], a0[u], b0[u], x0[u], y0[u]);
   for (int64_t base = base0 + kUnroll * stride; base < n; base += kUnroll * stride) {
-    float wv[kUnroll], pv[kUnroll], qv[kUnroll];
+    float wv[kUnroll], av[kUnroll], bv[kUnroll], xv[kUnroll], yv[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = base + u * stride < n ? base + u * stride : base;
       wv[u] = w[i];
-      pv[u] = q_prev[i];
-      qv[u] = q[i];
+      av[u] = (sub || J) ? ua[i] : 0.0f;
+      bv[u] = sub ? ub[i] : 0.0f;
+      xv[u] = norm ? 0.0f : va[i];
+      yv[u] = norm ? 0.0f : vb[i];
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
-      if (base + u * stride < n) one(base + u * stride, wv[u], pv[u], qv[u]);
+      if (base + u * stride < n) one(base + u * stride, wv[u], av[u], bv[u], xv[u], yv[u]);
   }
-  double v[kSlots] = {acc, 0.0, 0.0, 0.0};
+  double v[kSlots] = {acc0, acc1, acc2, 0.0};
   write_partials(v, part_out);
 }
 
@@ -431,8 +456,8 @@ msx_status gmres(const System &s, const float *b, const float *x0, const float *
       if ((e = spmv(V + j * ld, w)) != MSX_OK) return e;
       const auto jj = static_cast<int32_t>(j);
       int cur = 0;
-      for (int32_t pass = 0; pass <= 2 * jj + 2; ++pass) {
-        hipLaunchKernelGGL(gm_mgs<J>, s.grid, s.block, 0, s.stream, V, ld, w, inv_diag, n, jj,
+      for (int32_t pass = 0; pass <= jj + 1; ++pass) {
+        hipLaunchKernelGGL(gm_pair<J>, s.grid, s.block, 0, s.stream, V, ld, w, inv_diag, n, jj,
                            pass, part[cur ^ 1], np, part[cur], h, steps, st);
         cur ^= 1;
       }

@@ -3,10 +3,13 @@ and through ``linalg.gmres``.
 
 The device Arnoldi follows the reference's CPU arithmetic (float SpMV from
 zero, two sweeps of modified Gram-Schmidt with double sums of float
-products, float subtractions, norm_float) but adds each dot product per
-workgroup, so the rounding of the double sums differs from the sequential
-loop; the small least-squares problem and the restart logic run on the
-host exactly as in the oracle.  The bar:
+products, float subtractions, norm_float) with two differences: each dot
+product is added per workgroup, and the projections are taken in pairs per
+pass over w, the second coefficient of a pair as d_b - c_a (q_a.q_b) from
+sums taken before the first projection (equal to the sequential one in
+exact arithmetic), so the rounding differs from the sequential loop; the
+small least-squares problem and the restart logic run on the host exactly
+as in the oracle.  The bar:
 
 - status equal to the oracle's; iterations equal on cases whose stopping
   cycle is not at the tolerance's edge, else within one cycle;
@@ -16,7 +19,8 @@ host exactly as in the oracle.  The bar:
   oracle's x;
 - the status cases (zero right-hand side, exact x0, maxiter 0 and short
   budgets, non-finite input or value, an Arnoldi breakdown) give the
-  oracle's status, iterations and residual;
+  oracle's status, iterations and residual; the Hilbert 5x5 case, which the
+  budget ends at float32 rounding, meets the reference's own residual bound;
 - a solve is reproducible (two runs give the same bits), on every SpMV route
   (row blocks, LDS panels, no plan);
 - the reference's own GPU-reachable test systems
@@ -138,8 +142,25 @@ def test_gmres_status_cases_equal_oracle(case):
     assert (info, its) == (winfo, wits), (case, info, its, winfo, wits)
     if np.isnan(wres):
         assert np.isnan(res)
-    elif case == "hilbert":  # the budget ends it, not a tolerance: residuals agree loosely
-        assert abs(res - wres) <= 1e-2 * wres + 1e-6
+    elif case == "hilbert":
+        # cond ~ 5e5, ||x|| ~ 8e3 and the budget ends the solve: the
+        # residual is where float rounding leaves it (the device's paired
+        # Gram-Schmidt rounds differently from the sequential loop), so the
+        # check is the reference's own bound on the returned x
+        # (tests/test_linalg_pathological.py:615-643), the reported residual
+        # within the float32 rounding of b - A x of the true one, and the
+        # error bound of the true residual
+        A64 = dense.astype(np.float64)
+        x64 = x.astype(np.float64)
+        true_res = np.linalg.norm(A64 @ x64 - b)
+        assert true_res / max(np.linalg.norm(b), 1.0) < 2e-4
+        assert res / max(np.linalg.norm(b), 1.0) < 2e-4
+        rounding = 8 * np.finfo(np.float32).eps * np.linalg.norm(np.abs(A64) @ np.abs(x64) + np.abs(b))
+        assert abs(true_res - res) <= rounding
+        exact = np.linalg.solve(A64, b.astype(np.float64))
+        cond = np.linalg.cond(A64)
+        assert np.linalg.norm(x - exact) <= cond * true_res / np.linalg.norm(b) * np.linalg.norm(exact)
+        return
     else:
         assert res == pytest.approx(wres, rel=1e-5, abs=1e-7)
     finite = np.isfinite(wx)
@@ -214,7 +235,8 @@ def test_full_size_gmres_three_cycles(gpu):
     """n = 128^3 (the SpMM benchmark's matrix, with the x-direction
     convection of the full-size BiCGSTAB test): three cycles of 20 Arnoldi
     steps on the device with the matrix's cached plan, against the oracle's
-    loop: same status and iterations, residual and x within 1e-4."""
+    loop: same status and iterations, residual within 1e-3 and x within
+    1e-4."""
     ms = gpu
     from mlx_sparse import linalg, synthetic
 
@@ -236,7 +258,10 @@ def test_full_size_gmres_three_cycles(gpu):
     print(f"gmres 128^3: gpu status {info.status} iterations {info.iterations} residual "
           f"{info.residual_norm:.6g}; oracle {winfo} {wits} {wres:.6g}", flush=True)
     assert (info.status, info.iterations) == (winfo, wits)
-    assert abs(info.residual_norm - wres) <= 1e-4 * wres
+    # the residual ends near 1e-7 of ||b||, where the float32 b - A x of
+    # either loop rounds: within 1e-3 of each other (the paired Gram-Schmidt
+    # passes round differently from the sequential ones)
+    assert abs(info.residual_norm - wres) <= 1e-3 * wres
     ref = np.linalg.norm(wx.astype(np.float64))
     assert np.linalg.norm(x.cpu().numpy().astype(np.float64) - wx) <= 1e-4 * ref
 
