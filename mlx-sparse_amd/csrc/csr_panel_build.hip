@@ -255,37 +255,55 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Refresh of the copy's values after the matrix's values changed (same
-// indices and indptr): one workgroup per tile.  The tile's values are one
-// contiguous range [b0, b1) of the matrix (at most TW of them), so they are
-// first copied into LDS with coalesced dword loads through a descriptor (no
-// branch per load); the tile's virtual rows fill a map from LDS word to
-// (virtual row - first of the tile); an entry with word d then came from
-// position b0 + d - map[d], the inverse of dest = (p - b0) + (v - v0), and
-// is read from LDS.  Every panel's segment of the tile is rewritten;
-// padding entries (word 0xFFFF, outside every tile) keep their zero.  LDS: TW 16-bit map entries + the values
+// indices and indptr): one workgroup per tile, two per CU.  The tile's
+// values are one contiguous range [b0, b1) of the matrix (at most TW of
+// them), so they are first copied into LDS with coalesced dword loads
+// through a descriptor (no branch per load).  Each virtual row v of the
+// tile leaves a spare word after its values, dest = (p - b0) + (v - v0), so
+// a bitmap of those gap words (one bit per LDS word, set by the rows) and
+// the gaps before each 64-bit word of it (a prefix scan) turn an entry's
+// word d back into its position: p - b0 = d - (gaps below d).  Every
+// panel's segment of the tile is rewritten in quads (segments are padded to
+// multiples of 4 entries): 4 words in one 8-byte load, 4 values in one
+// store; padding entries (word 0xFFFF, outside every tile) get zero, as the
+// build gave them.  LDS: the values, the bitmap and its prefix
 // (refresh_lds_bytes).
 constexpr int kRefreshUnroll = 4;
-constexpr int kRefreshThreads = 1024;  // one workgroup per CU (its LDS), 16 waves
-constexpr int kRefreshPanels = 8;      // panel segments per wave whose loads are in flight
+constexpr int kRefreshThreads = 1024;  // 16 waves; two workgroups per CU
+constexpr int kRefreshWaves = kRefreshThreads / kWave;
+constexpr int kRefreshPanels = 4;      // panel segments per wave whose loads are in flight
 
-__host__ __device__ inline int64_t refresh_map_bytes(int64_t TW) { return (TW * 2 + 15) / 16 * 16; }
+__host__ __device__ inline int64_t refresh_vals_bytes(int64_t TW, int64_t value_bytes) {
+  return (TW * value_bytes + 16 + 15) / 16 * 16;  // + the start's offset inside a dword
+}
 __host__ __device__ inline int64_t refresh_lds_bytes(int64_t TW, int64_t value_bytes) {
-  return refresh_map_bytes(TW) + TW * value_bytes + 16;
+  const int64_t nb = TW / 64;
+  return refresh_vals_bytes(TW, value_bytes) + nb * 8 + nb * 4 + kRefreshWaves * 4;
 }
 
+template <class S>
+struct alignas(4 * sizeof(S)) RefreshQuad {
+  S v[4];
+};
+
+// held to 64 registers: two workgroups (eight waves per SIMD) per CU
 template <class S, class RP>
-__global__ void __launch_bounds__(kRefreshThreads)
+__global__ void __launch_bounds__(kRefreshThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
     panel_refresh(const S *__restrict__ data, const RP *__restrict__ rowptr, int64_t nnz,
                   const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
                   const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles, int64_t TW,
                   const uint16_t *__restrict__ dest, S *__restrict__ out) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  uint16_t *row_of = reinterpret_cast<uint16_t *>(lds_raw);
-  unsigned char *vals = lds_raw + refresh_map_bytes(TW);
+  unsigned char *vals = lds_raw;
+  const int nbw = static_cast<int>(TW / 64);  // bitmap words (TW is a multiple of 64, <= 65536)
+  auto *gap = reinterpret_cast<unsigned long long *>(lds_raw + refresh_vals_bytes(TW, sizeof(S)));
+  auto *before = reinterpret_cast<uint32_t *>(gap + nbw);
+  uint32_t *wsum = before + nbw;
   const int64_t t = blockIdx.x;
   const int64_t v0 = tile_begin[t], v1 = tile_end[t];
   const int64_t b0 = vpos(rowptr, v0, nnz);
   const int64_t b1 = clamp64(vpos(rowptr, v1, nnz), b0, b0 + TW);
+  for (int i = threadIdx.x; i < nbw; i += kRefreshThreads) gap[i] = 0;
   // values [b0, b1) as the dwords that hold them: byte `off0` of the first
   // dword is position b0 (16-bit values may start mid-dword)
   const uintptr_t a0 = reinterpret_cast<uintptr_t>(data + b0);
@@ -294,58 +312,91 @@ __global__ void __launch_bounds__(kRefreshThreads)
       static_cast<uint32_t>((off0 + static_cast<uint64_t>(b1 - b0) * sizeof(S) + 3) / 4);
   const auto r = make_rsrc(reinterpret_cast<const void *>(a0 - off0), uint64_t{4} * n_dw);
   auto *vw = reinterpret_cast<uint32_t *>(vals);
-  for (uint32_t i = threadIdx.x; i < n_dw; i += kRefreshUnroll * kRefreshThreads) {
-    uint32_t w[kRefreshUnroll];
+  // The whole dwords of the tile's values in 16-byte loads, all issued
+  // before the first is used (kRefreshUnroll per thread cover TW values of
+  // up to 8 bytes); the last n_dw % 4 dwords in dword loads.
+  const uint32_t n_q = n_dw / 4;
+  u32x4 w[kRefreshUnroll];
 #pragma unroll
-    for (int u = 0; u < kRefreshUnroll; ++u)
-      w[u] = __builtin_amdgcn_raw_buffer_load_b32(r, 4u * (i + u * kRefreshThreads), 0, 0);
-#pragma unroll
-    for (int u = 0; u < kRefreshUnroll; ++u)
-      if (i + u * kRefreshThreads < n_dw) vw[i + u * kRefreshThreads] = w[u];
+  for (int u = 0; u < kRefreshUnroll; ++u) {
+    const uint32_t qi = threadIdx.x + u * kRefreshThreads;
+    w[u] = qi < n_q ? BufLoad<16, kCacheStream>::load(r, 16u * qi) : u32x4{{0u, 0u, 0u, 0u}};
   }
+  const uint32_t tail_i = 4 * n_q + threadIdx.x;
+  const uint32_t tail = tail_i < n_dw ? __builtin_amdgcn_raw_buffer_load_b32(r, 4u * tail_i, 0, 0) : 0u;
+  __syncthreads();  // the bitmap is clear
   for (int64_t v = v0 + threadIdx.x; v < v1; v += kRefreshThreads) {
     const int64_t s = vpos(rowptr, v, nnz);
     const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, nnz);
-    for (int64_t p = s; p < e; ++p) {
-      const int64_t w = (p - b0) + (v - v0);
-      if (w >= 0 && w < TW) row_of[w] = static_cast<uint16_t>(v - v0);
-    }
+    const int64_t g = (e - b0) + (v - v0);  // the row's spare word
+    if (g >= 0 && g < TW) atomicOr(&gap[g >> 6], 1ull << (g & 63));
   }
+#pragma unroll
+  for (int u = 0; u < kRefreshUnroll; ++u) {
+    const uint32_t qi = threadIdx.x + u * kRefreshThreads;
+    if (qi < n_q) reinterpret_cast<u32x4 *>(vw)[qi] = w[u];
+  }
+  if (tail_i < n_dw) vw[tail_i] = tail;
   __syncthreads();
+  {  // gaps before each bitmap word: a wave scan, then the wave totals in order
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int k = static_cast<int>(threadIdx.x);
+    const uint32_t c = k < nbw ? static_cast<uint32_t>(__popcll(gap[k])) : 0u;
+    uint32_t incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t u = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += u;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    uint32_t off = 0;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    if (k < nbw) before[k] = off + incl - c;
+    __syncthreads();
+  }
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t nb = b1 - b0;
-  auto value_at = [&](int64_t d) -> S {
+  auto value_at = [&](uint32_t d) -> S {
     S v{};
-    const int64_t i = d - row_of[d];  // position - b0
-    if (i >= 0 && i < nb) __builtin_memcpy(&v, vals + off0 + i * sizeof(S), sizeof(S));
+    if (d < static_cast<uint32_t>(TW)) {
+      const unsigned long long bits = gap[d >> 6];
+      const unsigned long long lower = bits & ((1ull << (d & 63)) - 1ull);
+      const int64_t i = static_cast<int64_t>(d) - before[d >> 6] - __popcll(lower);
+      if (i >= 0 && i < nb) __builtin_memcpy(&v, vals + off0 + i * sizeof(S), sizeof(S));
+    }
     return v;
   };
   // Wave w takes panels w, w + 16, ... in batches of kRefreshPanels: the
-  // word loads of all of a batch's segments are issued before the first
-  // is used (one round trip per 64 entries of the longest segment, not one
-  // per segment).  Segments start on a multiple of 4 entries, so dest + a
-  // is 8-byte aligned.
-  constexpr int kWaves = kRefreshThreads / kWave;
-  for (int64_t qb = 0; qb < n_panels; qb += kWaves * kRefreshPanels) {
+  // word loads of all of a batch's segments are issued before the first is
+  // used.  Segments start on a multiple of 4 entries, so dest + a is 8-byte
+  // and out + a 4 * sizeof(S)-byte aligned.
+  auto *oq = reinterpret_cast<RefreshQuad<S> *>(out);
+  for (int64_t qb = 0; qb < n_panels; qb += kRefreshWaves * kRefreshPanels) {
     int64_t a[kRefreshPanels];
-    uint32_t len[kRefreshPanels], most = 0;
+    uint32_t len4[kRefreshPanels], most = 0;
     __amdgpu_buffer_rsrc_t rd[kRefreshPanels];
 #pragma unroll
     for (int k = 0; k < kRefreshPanels; ++k) {
-      const int64_t q = qb + wave + static_cast<int64_t>(kWaves) * k;
+      const int64_t q = qb + wave + static_cast<int64_t>(kRefreshWaves) * k;
       a[k] = q < n_panels ? static_cast<int64_t>(seg[q * n_tiles + t]) : 0;
-      len[k] = q < n_panels ? static_cast<uint32_t>(seg[q * n_tiles + t + 1] - a[k]) : 0u;
-      most = len[k] > most ? len[k] : most;
-      rd[k] = make_rsrc(dest + a[k], uint64_t{2} * len[k]);
+      len4[k] = q < n_panels ? static_cast<uint32_t>(seg[q * n_tiles + t + 1] - a[k]) / 4u : 0u;
+      most = len4[k] > most ? len4[k] : most;
+      rd[k] = make_rsrc(dest + a[k], uint64_t{8} * len4[k]);
     }
     for (uint32_t e = lane; e < most; e += kWave) {
-      uint32_t d[kRefreshPanels];
+      uint64_t d[kRefreshPanels];
 #pragma unroll
-      for (int k = 0; k < kRefreshPanels; ++k)
-        d[k] = __builtin_amdgcn_raw_buffer_load_b16(rd[k], 2u * e, 0, 0);
+      for (int k = 0; k < kRefreshPanels; ++k) d[k] = BufLoad<8, kCacheStream>::load(rd[k], 8u * e);
 #pragma unroll
-      for (int k = 0; k < kRefreshPanels; ++k)
-        if (e < len[k] && d[k] < TW) out[a[k] + e] = value_at(d[k]);
+      for (int k = 0; k < kRefreshPanels; ++k) {
+        if (e < len4[k]) {
+          RefreshQuad<S> qv;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) qv.v[u] = value_at(static_cast<uint32_t>((d[k] >> (16 * u)) & 0xFFFFu));
+          oq[a[k] / 4 + e] = qv;
+        }
+      }
     }
   }
 }
