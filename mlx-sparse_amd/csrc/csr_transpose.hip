@@ -782,6 +782,135 @@ __global__ void __launch_bounds__(kPermThreads)
   for (int j = threadIdx.x; j < len; j += kPermThreads) out[b0 + j] = lds[j];
 }
 
+// The same two passes with every stream read and written in quads of 4
+// elements (16-byte loads of 4-byte values), each thread's whole share of
+// its tile or bucket loaded before any is used - all of a thread's index
+// quads, then all of its gathers - so that a workgroup waits on memory
+// once per stage, not once per 4 elements.  Used when every buffer is
+// aligned to its quad; the elements past the last whole quad of a tile or
+// bucket go one per thread.
+template <class S>
+__global__ void __launch_bounds__(kPermThreads)
+    perm_tiles_q(const S *__restrict__ data, const uint16_t *__restrict__ slot1, int64_t nnz,
+                 bool conjugate, S *__restrict__ s1) {
+  using V4 = S __attribute__((ext_vector_type(4)));
+  using H4 = uint16_t __attribute__((ext_vector_type(4)));
+  constexpr int D1 = PermSizes<sizeof(S)>::D1;
+  constexpr int NQ = D1 / 4 / kPermThreads;  // quads per thread
+  extern __shared__ unsigned char perm_lds[];
+  S *lds = reinterpret_cast<S *>(perm_lds);
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * D1;
+  const int len = static_cast<int>(std::min<int64_t>(D1, nnz - p0));
+  const int nq = len / 4;
+  const auto *dq = reinterpret_cast<const V4 *>(data + p0);
+  const auto *sq = reinterpret_cast<const H4 *>(slot1 + p0);
+  V4 v[NQ];
+  H4 sl[NQ];
+  if (nq > 0) {  // clamped indices: every load issued before any use
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = static_cast<int>(threadIdx.x) + u * kPermThreads;
+      const int qc = qi < nq ? qi : 0;
+      v[u] = __builtin_nontemporal_load(dq + qc);
+      sl[u] = __builtin_nontemporal_load(sq + qc);
+    }
+  }
+  const int te = 4 * nq + static_cast<int>(threadIdx.x);  // the tail, one element per thread
+  S tv{};
+  uint16_t ts = kNoSlot;
+  if (te < len) {
+    tv = data[p0 + te];
+    ts = slot1[p0 + te];
+  }
+  if (nq > 0) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = static_cast<int>(threadIdx.x) + u * kPermThreads;
+      if (qi < nq) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (sl[u][e] < D1) lds[sl[u][e]] = conj_bits(static_cast<S>(v[u][e]), conjugate);
+      }
+    }
+  }
+  if (te < len && ts < D1) lds[ts] = conj_bits(tv, conjugate);
+  __syncthreads();
+  const auto *lq = reinterpret_cast<const V4 *>(lds);
+  auto *oq = reinterpret_cast<V4 *>(s1 + p0);
+  for (int qi = threadIdx.x; qi < nq; qi += kPermThreads) oq[qi] = lq[qi];
+  if (te < len) s1[p0 + te] = lds[te];
+}
+
+template <class S>
+__global__ void __launch_bounds__(kPermThreads)
+    perm_buckets_q(const S *__restrict__ s1, const uint32_t *__restrict__ src1,
+                   const uint16_t *__restrict__ slot2, int64_t nnz, S *__restrict__ out) {
+  using V4 = S __attribute__((ext_vector_type(4)));
+  using H4 = uint16_t __attribute__((ext_vector_type(4)));
+  using W4 = uint32_t __attribute__((ext_vector_type(4)));
+  constexpr int D2 = PermSizes<sizeof(S)>::D2;
+  constexpr int NQ = D2 / 4 / kPermThreads;
+  extern __shared__ unsigned char perm_lds[];
+  S *lds = reinterpret_cast<S *>(perm_lds);
+  // each XCD takes a contiguous range of buckets (as in perm_buckets)
+  const int64_t b0 = static_cast<int64_t>(xcd_remap(blockIdx.x, gridDim.x)) * D2;
+  const int len = static_cast<int>(std::min<int64_t>(D2, nnz - b0));
+  const int nq = len / 4;
+  const auto *aq = reinterpret_cast<const W4 *>(src1 + b0);
+  const auto *sq = reinterpret_cast<const H4 *>(slot2 + b0);
+  W4 a[NQ];
+  H4 sl[NQ];
+  if (nq > 0) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = static_cast<int>(threadIdx.x) + u * kPermThreads;
+      const int qc = qi < nq ? qi : 0;
+      a[u] = __builtin_nontemporal_load(aq + qc);
+      sl[u] = __builtin_nontemporal_load(sq + qc);
+    }
+  }
+  const int te = 4 * nq + static_cast<int>(threadIdx.x);
+  uint32_t ta = kNoSource;
+  uint16_t ts = kNoSlot;
+  if (te < len) {
+    ta = src1[b0 + te];
+    ts = slot2[b0 + te];
+  }
+  // the gathers: an address past the array (kNoSource: a dropped entry)
+  // reads element 0 and is replaced by zero
+  S v[NQ][4];
+  if (nq > 0) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t ai = a[u][e];
+        v[u][e] = s1[static_cast<int64_t>(ai) < nnz ? ai : 0u];
+      }
+  }
+  S tv = s1[static_cast<int64_t>(ta) < nnz ? ta : 0u];
+  if (static_cast<int64_t>(ta) >= nnz) tv = S(0);
+  if (nq > 0) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = static_cast<int>(threadIdx.x) + u * kPermThreads;
+      if (qi < nq) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const S x = static_cast<int64_t>(a[u][e]) < nnz ? v[u][e] : S(0);
+          if (sl[u][e] < D2) lds[sl[u][e]] = x;
+        }
+      }
+    }
+  }
+  if (te < len && ts < D2) lds[ts] = tv;
+  __syncthreads();
+  const auto *lq = reinterpret_cast<const V4 *>(lds);
+  auto *oq = reinterpret_cast<V4 *>(out + b0);
+  for (int qi = threadIdx.x; qi < nq; qi += kPermThreads) oq[qi] = lq[qi];
+  if (te < len) out[b0 + te] = lds[te];
+}
+
 // Layout build.  key[i] = (bucket of i, source of i) - the source nnz for
 // a dropped entry, so it sorts last in its bucket; val[i] = i.
 __global__ void __launch_bounds__(kThreads)
@@ -933,6 +1062,24 @@ msx_status transpose_permute(int64_t nnz, const void *data, const uint16_t *slot
   MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&perm_buckets<S>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, D2 * sizeof(S)));
   const int64_t ntile = (nnz + D1 - 1) / D1, nb = (nnz + D2 - 1) / D2;
+  const size_t qb = 4 * sizeof(S);  // the quad kernels need every buffer aligned to its quad
+  const auto al = [](const void *p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+  if (al(data, qb) && al(scratch, qb) && al(t_data, qb) && al(slot1, 8) && al(slot2, 8) &&
+      al(src1, 16)) {
+    MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&perm_tiles_q<S>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, D1 * sizeof(S)));
+    MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&perm_buckets_q<S>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, D2 * sizeof(S)));
+    hipLaunchKernelGGL(perm_tiles_q<S>, dim3(static_cast<uint32_t>(ntile)), dim3(kPermThreads),
+                       D1 * sizeof(S), stream, static_cast<const S *>(data), slot1, nnz, conjugate,
+                       static_cast<S *>(scratch));
+    MSX_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(perm_buckets_q<S>, dim3(static_cast<uint32_t>(nb)), dim3(kPermThreads),
+                       D2 * sizeof(S), stream, static_cast<const S *>(scratch), src1, slot2, nnz,
+                       static_cast<S *>(t_data));
+    MSX_HIP_TRY(hipGetLastError());
+    return MSX_OK;
+  }
   hipLaunchKernelGGL(perm_tiles<S>, dim3(static_cast<uint32_t>(ntile)), dim3(kPermThreads),
                      D1 * sizeof(S), stream, static_cast<const S *>(data), slot1, nnz, conjugate,
                      static_cast<S *>(scratch));

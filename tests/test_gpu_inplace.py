@@ -208,7 +208,9 @@ def test_transpose_layout_regather(vtype, n_rows, n_cols, max_len):
     gather msx_csr_transpose_values writes - the oracle's transpose for the
     kept entries, zero bits for the dropped ones, conjugated on request -
     below one tile and across many tiles and buckets with ragged ends, on
-    two calls in a row that share the scratch (new values the second time)."""
+    calls in a row that share the scratch (new values each time); the third
+    call's values and output are views one element off their allocation, so
+    the element-wise passes run instead of the quad ones."""
     rng = np.random.default_rng(n_rows + max_len)
     indices, indptr, _ = _random_csr(rng, n_rows, n_cols, max_len)
     indices[3] = n_cols + 1  # dropped from the transpose
@@ -223,12 +225,16 @@ def test_transpose_layout_regather(vtype, n_rows, n_cols, max_len):
     if nnz <= 300000:
         _check_layout(layout, pos, width)
     scratch = torch.empty(nnz, dtype=TORCH[vtype], device=DEV)
-    for trial in range(2):
+    for trial in range(3):
         data = _values(rng, nnz, vtype)
         d = to_torch(data, vtype, DEV)
         want = torch.full_like(d, 7.0)
         _capi.transpose_values(d, pos, want)
         got = torch.full_like(d, 3.0)
+        if trial == 2:  # misaligned views
+            d = torch.cat([d[:1], d])[1:]
+            got = torch.full((nnz + 1,), 3.0, dtype=d.dtype, device=DEV)[1:]
+            assert d.data_ptr() % 16 != 0 and got.data_ptr() % 16 != 0
         _capi.transpose_values_layout(d, layout, got, scratch=scratch)
         np.testing.assert_array_equal(_bits(got, vtype), _bits(want, vtype), err_msg=f"trial {trial}")
         ot, _, _ = orc.csr_transpose(data, indices, indptr, n_rows, n_cols, vtype=vtype)
