@@ -455,3 +455,62 @@ def test_minres_jacobi_api_on_gpu(gpu):
     xn = x.cpu().numpy()
     np.testing.assert_allclose(xn, np.linalg.solve(dense, b), rtol=5e-5, atol=5e-5)
     assert np.linalg.norm(dense.astype(np.float64) @ xn - b) / np.linalg.norm(b) < 2e-6
+
+
+def test_full_size_jacobi_solvers(gpu):
+    """The four Jacobi-preconditioned loops at n = 128^3 on the device with
+    the matrix's cached plan, against the oracle, on rows scaled by
+    10^U[-1, 1] (which the inverse diagonal undoes): BiCGSTAB and GMRES(20)
+    on the convection-diffusion variant scaled by rows, CG and MINRES on the
+    Poisson matrix (plus the identity for MINRES) scaled on both sides, so
+    it stays symmetric.  Status equal, iterations within two (GMRES: one
+    cycle), the reported residual under the tolerance, the true residual
+    of x as small as that of the oracle's x, x within 1e-3 of the
+    oracle's."""
+    ms = gpu
+    from mlx_sparse import linalg, synthetic
+    from mlx_sparse.linalg import preconditioners
+
+    m = synthetic.poisson_3d(128)
+    n = m.shape[0]
+    rows = np.repeat(np.arange(n), np.diff(m.indptr))
+    cols = m.indices.astype(np.int64)
+    conv = m.data.copy()
+    conv[cols == rows + 1] = -0.7
+    conv[cols == rows - 1] = -1.3
+    conv[cols == rows] = 8.0
+    s = (10.0 ** np.random.default_rng(11).uniform(-1, 1, n)).astype(np.float32)
+    conv_s = (conv * s[rows]).astype(np.float32)
+    pois_s = (m.data * s[rows] * s[cols]).astype(np.float32)
+    shifted = m.data.copy()
+    shifted[cols == rows] += 1.0
+    shifted_s = (shifted * s[rows] * s[cols]).astype(np.float32)
+    b_np = synthetic.uniform(n, -1.0, 1.0, seed=7)
+    b = torch.from_numpy(b_np).to(DEV)
+    cases = (("bicgstab", conv_s, orc.csr_bicgstab_jacobi, {"maxiter": 500}, 2),
+             ("gmres", conv_s, orc.csr_gmres_jacobi, {"restart": 20, "maxiter": 400}, 20),
+             ("cg", pois_s, orc.csr_pcg_jacobi, {"maxiter": 2000}, 2),
+             ("minres", shifted_s, orc.csr_minres_jacobi, {"maxiter": 500}, 2))
+    for name, data, oracle_fn, kw, slack in cases:
+        A = ms.csr_array((data, m.indices, m.indptr), shape=m.shape, canonical=True)
+        inv = (1.0 / data[cols == rows]).astype(np.float32)
+        x, info = getattr(linalg, name)(A, b, M=preconditioners.jacobi(A), rtol=1e-5,
+                                        return_info=True, **kw)
+        wx, winfo, wres, wits = oracle_fn(data, m.indices, m.indptr, b_np, inv, rtol=1e-5, **kw)
+        print(f"{name} jacobi: gpu status {info.status} iterations {info.iterations} residual "
+              f"{info.residual_norm:.5g}; oracle {winfo} {wits} {wres:.5g}", flush=True)
+        assert info.status == winfo == 0 and abs(info.iterations - wits) <= slack
+        assert info.preconditioner == "jacobi"
+        assert info.residual_norm <= 1e-5 * np.linalg.norm(b_np) * (1 + 1e-5)
+        xn = x.cpu().numpy().astype(np.float64)
+        A64 = sp.csr_matrix((data.astype(np.float64), m.indices, m.indptr), shape=m.shape)
+        # The recurrence residual drifts from the true one in float32 (CG over
+        # hundreds of steps on a badly scaled system most): the oracle's x
+        # carries the same drift, so the true residuals are compared.
+        true_res = np.linalg.norm(b_np - A64 @ xn)
+        true_orc = np.linalg.norm(b_np - A64 @ wx.astype(np.float64))
+        print(f"  true residual {true_res:.5g}; oracle's x {true_orc:.5g}", flush=True)
+        assert true_res <= 1.5 * true_orc + 1e-5 * np.linalg.norm(b_np)
+        ref = np.linalg.norm(wx.astype(np.float64))
+        print(f"  |x - x_oracle| / |x_oracle| = {np.linalg.norm(xn - wx) / ref:.3g}", flush=True)
+        assert np.linalg.norm(xn - wx) <= 1e-3 * ref
