@@ -514,23 +514,30 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t b0 = clamp64(static_cast<int64_t>(rowptr[v0]), 0, nnz);
   const int64_t b1 = clamp64(static_cast<int64_t>(rowptr[v1]), b0, std::min<int64_t>(nnz, b0 + TW));
   if (threadIdx.x < NB) gap[threadIdx.x] = 0;
-  __syncthreads();
-
-  // Rows: the cotangent into the gap word, the gap's bit into the bitmap.
-  for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads) {
-    const int64_t s = clamp64(static_cast<int64_t>(rowptr[v]), b0, b1);
-    const int64_t e = clamp64(static_cast<int64_t>(rowptr[v + 1]), s, b1);
-    int64_t r = v;
-    if constexpr (LONG) {
-      const int32_t slot = vslot[v];
-      r = slot >= 0 ? slot : -1 - static_cast<int64_t>(slot);
-    }
-    const int64_t g = (e - b0) + (v - v0);
-    if (g < TW) {
-      xw[g] = V::widen(cot[r]);
-      atomicOr(&gap[g >> 6], 1ull << (g & 63));
+  // The bounds (and, for rows that are their own virtual row, the
+  // cotangents) of the thread's first kRowsAhead rows are loaded before the
+  // tile's x values, so that their latency overlaps those loads; they go to
+  // LDS after the runs.
+  int64_t s_ahead[kRowsAhead], e_ahead[kRowsAhead];
+  A c_ahead[kRowsAhead];
+  int32_t slot_ahead[kRowsAhead];
+#pragma unroll
+  for (int k = 0; k < kRowsAhead; ++k) {
+    const int64_t v = v0 + threadIdx.x + static_cast<int64_t>(k) * kThreads;
+    s_ahead[k] = 0;
+    e_ahead[k] = 0;
+    c_ahead[k] = vzero<A>();
+    slot_ahead[k] = 0;
+    if (v < v1) {
+      s_ahead[k] = static_cast<int64_t>(rowptr[v]);
+      e_ahead[k] = static_cast<int64_t>(rowptr[v + 1]);
+      if constexpr (LONG)
+        slot_ahead[k] = vslot[v];
+      else
+        c_ahead[k] = V::widen(cot[v]);
     }
   }
+  __syncthreads();  // the bitmap is clear
 
   const auto *xq = reinterpret_cast<const ProdQuad<A> *>(xg);
   for (int qb = 0; qb < P; qb += kWavesPerGroup * kRunsPerWave) {
@@ -577,6 +584,45 @@ __global__ void __launch_bounds__(kThreads)
       }
     }
   }
+
+  // Rows: the cotangent into the gap word, the gap's bit into the bitmap.
+  int k_row = 0;
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += kThreads, ++k_row) {
+    int64_t s, e;
+    A c;
+    if (k_row < kRowsAhead) {
+      // a select over the prefetched rows (no dynamic register indexing)
+      s = s_ahead[0];
+      e = e_ahead[0];
+      c = c_ahead[0];
+      int32_t slot = slot_ahead[0];
+#pragma unroll
+      for (int k = 1; k < kRowsAhead; ++k)
+        if (k_row == k) {
+          s = s_ahead[k];
+          e = e_ahead[k];
+          c = c_ahead[k];
+          slot = slot_ahead[k];
+        }
+      if constexpr (LONG) c = V::widen(cot[slot >= 0 ? slot : -1 - static_cast<int64_t>(slot)]);
+    } else {
+      s = static_cast<int64_t>(rowptr[v]);
+      e = static_cast<int64_t>(rowptr[v + 1]);
+      int64_t r = v;
+      if constexpr (LONG) {
+        const int32_t slot = vslot[v];
+        r = slot >= 0 ? slot : -1 - static_cast<int64_t>(slot);
+      }
+      c = V::widen(cot[r]);
+    }
+    s = clamp64(s, b0, b1);
+    e = clamp64(e, s, b1);
+    const int64_t g = (e - b0) + (v - v0);
+    if (g < TW) {
+      xw[g] = c;
+      atomicOr(&gap[g >> 6], 1ull << (g & 63));
+    }
+  }
   __syncthreads();
 
   // Gaps before each bitmap word: a scan of the NB counts (a wave scan,
@@ -618,25 +664,53 @@ __global__ void __launch_bounds__(kThreads)
     __syncthreads();
   }
 
-  // The walk: lane l of every wave step holds word w (w % 64 == l), so the
-  // gaps below it in its bitmap word are an mbcnt of that word.
+  // The walk: thread t holds the WPT consecutive words from t * WPT, all in
+  // one bitmap word.  The cotangent of a value word is the word of the next
+  // gap: inside the chunk, found going backwards over its words; after the
+  // chunk's last gap, the first gap above the chunk (in this bitmap word, or
+  // a later one's first gap).  A value word's position is its word minus the
+  // gaps below it, so the chunk's products land at consecutive positions;
+  // they are written over the words (after every chunk has been read) and
+  // then stored from LDS in position order, coalesced.
+  constexpr int WPT = TW / kThreads;  // 16 words (4-byte accumulators), 8 (complex64)
+  static_assert(WPT * kThreads == TW && 64 % WPT == 0, "a chunk lies in one bitmap word");
   const uint32_t npos = static_cast<uint32_t>(b1 - b0);
-  typename V::Storage *ob = out + b0;
+  const int w0 = static_cast<int>(threadIdx.x) * WPT;
+  const int k = w0 >> 6, sh = w0 & 63;
+  const unsigned long long bits = gap[k];
+  const uint32_t cbits = static_cast<uint32_t>((bits >> sh) & ((1ull << WPT) - 1ull));
+  // gaps below the chunk
+  const uint32_t gb = before[k] + static_cast<uint32_t>(__popcll(bits & ((1ull << sh) - 1ull)));
+  const unsigned long long above = sh + WPT < 64 ? bits >> (sh + WPT) : 0ull;
+  const int later = nextg[k];
+  const int tail_g = above != 0 ? w0 + WPT + static_cast<int>(__builtin_ctzll(above)) : later;
+  using Chunk = Four<A>;  // four words per LDS read
+  Chunk cv[WPT / 4];
 #pragma unroll
-  for (int j = 0; j < TW / kThreads; ++j) {
-    const int w = j * kThreads + static_cast<int>(threadIdx.x);
-    const int k = w >> 6;
-    const unsigned long long bits = gap[k];
-    const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
-    const uint32_t below = __builtin_amdgcn_mbcnt_hi(bhi, __builtin_amdgcn_mbcnt_lo(blo, 0u));
-    const unsigned long long rest = bits >> lane;  // bit 0: w itself
-    const uint32_t pos = static_cast<uint32_t>(w) - (before[k] + below);
-    if ((rest & 1ull) || pos >= npos) continue;  // a gap word, or past the tile's values
-    // the row's gap: in this bitmap word, or the first gap of a later word
-    const int g = rest != 0 ? w + static_cast<int>(__builtin_ctzll(rest)) : nextg[k];
-    if (g >= TW) continue;  // none (INT32_MAX)
-    nt_store(ob + pos, V::narrow(amul(xw[g], xw[w])));
+  for (int u = 0; u < WPT / 4; ++u) cv[u] = reinterpret_cast<const Chunk *>(xw + w0)[u];
+  // (no gap above the chunk: its words after its last gap lie past the
+  // tile's last row, at positions >= npos, which are not written)
+  A c = xw[tail_g < TW ? tail_g : 0];
+  __syncthreads();  // every chunk and tail read before the products overwrite the words
+  A prod[WPT];
+#pragma unroll
+  for (int i = WPT - 1; i >= 0; --i) {
+    const A v = cv[i / 4].v[i % 4];
+    prod[i] = amul(c, v);
+    if ((cbits >> i) & 1u) c = v;
   }
+  uint32_t pos = static_cast<uint32_t>(w0) - gb;
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    if (!((cbits >> i) & 1u)) {
+      if (pos < npos) xw[pos] = prod[i];
+      ++pos;
+    }
+  }
+  __syncthreads();
+  typename V::Storage *ob = out + b0;
+#pragma unroll 4
+  for (uint32_t q = threadIdx.x; q < npos; q += kThreads) nt_store(ob + q, V::narrow(xw[q]));
 }
 
 template <class A>
