@@ -261,13 +261,14 @@ __global__ void __launch_bounds__(kThreads)
 // through a descriptor (no branch per load).  Each virtual row v of the
 // tile leaves a spare word after its values, dest = (p - b0) + (v - v0), so
 // a bitmap of those gap words (one bit per LDS word, set by the rows) and
-// the gaps before each 64-bit word of it (a prefix scan) turn an entry's
-// word d back into its position: p - b0 = d - (gaps below d).  Every
-// panel's segment of the tile is rewritten in quads (segments are padded to
-// multiples of 4 entries): 4 words in one 8-byte load, 4 values in one
-// store; padding entries (word 0xFFFF, outside every tile) get zero, as the
-// build gave them.  LDS: the values, the bitmap and its prefix
-// (refresh_lds_bytes).
+// the gaps before each 64-bit word of it (a prefix scan) give each word's
+// position: p - b0 = d - (gaps below d).  The values are then spread in
+// place from their positions to their words, so that a panel entry reads
+// its value at its word d.  Every panel's segment of the tile is rewritten
+// in quads (segments are padded to multiples of 4 entries): 4 words in one
+// 8-byte load, 4 values in one store; padding entries (word 0xFFFF, outside
+// every tile) get zero, as the build gave them.  LDS: the values, the
+// bitmap and its prefix (refresh_lds_bytes).
 constexpr int kRefreshUnroll = 4;
 constexpr int kRefreshThreads = 1024;  // 16 waves; two workgroups per CU
 constexpr int kRefreshWaves = kRefreshThreads / kWave;
@@ -291,8 +292,11 @@ template <class S, class RP>
 __global__ void __launch_bounds__(kRefreshThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
     panel_refresh(const S *__restrict__ data, const RP *__restrict__ rowptr, int64_t nnz,
                   const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_end,
-                  const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles, int64_t TW,
+                  const uint32_t *__restrict__ seg, int64_t n_panels, int64_t n_tiles,
                   const uint16_t *__restrict__ dest, S *__restrict__ out) {
+  // the tile's LDS words: 64 KB of accumulators (8-byte values: complex64)
+  constexpr int kRefreshWords = static_cast<int>(kTileBytes / (sizeof(S) == 8 ? 8 : 4));
+  constexpr int64_t TW = kRefreshWords;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char *vals = lds_raw;
   const int nbw = static_cast<int>(TW / 64);  // bitmap words (TW is a multiple of 64, <= 65536)
@@ -357,16 +361,36 @@ __global__ void __launch_bounds__(kRefreshThreads) __attribute__((amdgpu_waves_p
   }
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t nb = b1 - b0;
-  auto value_at = [&](uint32_t d) -> S {
-    S v{};
-    if (d < static_cast<uint32_t>(TW)) {
-      const unsigned long long bits = gap[d >> 6];
-      const unsigned long long lower = bits & ((1ull << (d & 63)) - 1ull);
-      const int64_t i = static_cast<int64_t>(d) - before[d >> 6] - __popcll(lower);
-      if (i >= 0 && i < nb) __builtin_memcpy(&v, vals + off0 + i * sizeof(S), sizeof(S));
+  {
+    // The values are spread to their words: thread t takes the WPT
+    // consecutive words from t * WPT (all in one bitmap word); value word i
+    // of them holds the value at position (t * WPT + i) - (gaps below it),
+    // so the chunk's values are one run of consecutive positions.  Every run
+    // is read before any word is written (the words overlay the positions);
+    // gap words get zero.
+    constexpr int WPT = kRefreshWords / kRefreshThreads;  // 16, or 8 for 8-byte values
+    const int w0 = static_cast<int>(threadIdx.x) * WPT;
+    const int k = w0 >> 6, sh = w0 & 63;
+    const unsigned long long bits = gap[k];
+    const uint32_t cbits = static_cast<uint32_t>((bits >> sh) & ((1ull << WPT) - 1ull));
+    int64_t pp = static_cast<int64_t>(w0) - before[k] - __popcll(bits & ((1ull << sh) - 1ull));
+    RefreshQuad<S> wq[WPT / 4];
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      S v{};
+      if (!((cbits >> i) & 1u)) {
+        if (pp >= 0 && pp < nb) __builtin_memcpy(&v, vals + off0 + pp * sizeof(S), sizeof(S));
+        ++pp;
+      }
+      wq[i / 4].v[i % 4] = v;
     }
-    return v;
-  };
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < WPT / 4; ++u) reinterpret_cast<RefreshQuad<S> *>(vals)[threadIdx.x * (WPT / 4) + u] = wq[u];
+    __syncthreads();
+  }
+  const S *words = reinterpret_cast<const S *>(vals);
+  auto value_at = [&](uint32_t d) -> S { return d < static_cast<uint32_t>(kRefreshWords) ? words[d] : S{}; };
   // Wave w takes panels w, w + 16, ... in batches of kRefreshPanels: the
   // word loads of all of a batch's segments are issued before the first is
   // used.  Segments start on a multiple of 4 entries, so dest + a is 8-byte
@@ -701,6 +725,8 @@ template <class V, class I>
 msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) {
   using S = typename V::Storage;
   if (p->n_tiles == 0 || p->pn_values == 0) return MSX_OK;
+  if (p->tile_words != kTileBytes / static_cast<int64_t>(sizeof(typename V::Acc)))
+    return fail(MSX_EINVAL, "msx_csr_plan_refresh: unexpected tile size in the panel layout.");
   const size_t lds = static_cast<size_t>(refresh_lds_bytes(p->tile_words, sizeof(S)));
   if (p->pn_vstart != nullptr) {
     MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_refresh<S, uint32_t>),
@@ -709,7 +735,7 @@ msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) 
     hipLaunchKernelGGL((panel_refresh<S, uint32_t>), dim3(static_cast<uint32_t>(p->n_tiles)),
                        dim3(kRefreshThreads), lds, stream, static_cast<const S *>(data), p->pn_vstart,
                        p->nnz, p->pn_tile_begin, p->pn_tile_end, p->pn_seg, p->n_panels,
-                       p->n_tiles, p->tile_words, p->pn_dest, static_cast<S *>(p->pn_data));
+                       p->n_tiles, p->pn_dest, static_cast<S *>(p->pn_data));
   } else {
     MSX_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&panel_refresh<S, I>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -717,7 +743,7 @@ msx_status refresh_typed(msx_csr_plan *p, const void *data, hipStream_t stream) 
     hipLaunchKernelGGL((panel_refresh<S, I>), dim3(static_cast<uint32_t>(p->n_tiles)),
                        dim3(kRefreshThreads), lds, stream, static_cast<const S *>(data),
                        static_cast<const I *>(p->indptr), p->nnz, p->pn_tile_begin, p->pn_tile_end,
-                       p->pn_seg, p->n_panels, p->n_tiles, p->tile_words, p->pn_dest,
+                       p->pn_seg, p->n_panels, p->n_tiles, p->pn_dest,
                        static_cast<S *>(p->pn_data));
   }
   MSX_HIP_TRY(hipGetLastError());

@@ -95,6 +95,44 @@ def test_plan_refresh_rewrites_the_copy(vtype, mode):
     plan.close()
 
 
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_plan_refresh_with_long_rows(vtype, index_dtype):
+    """A panel plan with virtual rows (W = 64: long rows cut into chunks,
+    rows of 0..200 values, a few of thousands) refreshed twice: short rows
+    equal the oracle bit for bit, every row within the tolerance; values
+    that changed place would move the sums far past it."""
+    rng = np.random.default_rng(23)
+    n_rows, n_cols = 12_000, 250_000
+    lengths = rng.integers(0, 200, n_rows)
+    lengths[rng.random(n_rows) < 0.1] = 0
+    lengths[[3, 7000, n_rows - 1]] = [4000, 9000, 1500]
+    indptr = np.zeros(n_rows + 1, np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    nnz = int(indptr[-1])
+    indices = rng.integers(0, n_cols, nnz).astype(index_dtype)
+    indptr = indptr.astype(index_dtype)
+    data0, data1 = _values(rng, nnz, vtype), _values(rng, nnz, vtype)
+    x = _values(rng, n_cols, vtype)
+    d = to_torch(data0, vtype, DEV)
+    i, p = to_torch(indices, None, DEV), to_torch(indptr, None, DEV)
+    xt = to_torch(x, vtype, DEV)
+    plan = _capi.Plan(p, n_rows, nnz, 64, data=d, indices=i, n_cols=n_cols,
+                      slice_mode=_capi.SLICE_PANELS)
+    info = plan.info()
+    assert info.n_panels > 0 and info.n_long_rows > 0
+    for step, new in enumerate((data1, data0)):
+        d.copy_(to_torch(new, vtype, DEV))
+        plan.refresh(d)
+        print(f"refresh long rows {vtype} {np.dtype(index_dtype).name} step {step}", flush=True)
+        y = to_numpy(_capi.spmv(d, i, p, xt, n_rows, n_cols, plan=plan))
+        want = orc.csr_matvec(new, indices, indptr, x, n_rows, vtype=vtype, n_threads=8)
+        scale = orc.row_scale(new, indices, indptr, x, n_rows, vtype=vtype)
+        assert_rows_close(y, want, scale, vtype, f"refresh long rows {step} {vtype}")
+        _short_rows_equal(y, want, lengths, info.block_nnz, vtype, f"long rows {step}")
+    plan.close()
+
+
 def test_plan_is_bound_to_its_indptr_buffer():
     """Same n_rows and nnz, other rows: both plan kinds reject the matrix."""
     rng = np.random.default_rng(3)
