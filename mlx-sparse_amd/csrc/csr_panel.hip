@@ -439,7 +439,7 @@ constexpr int kFixupThreads = 256;
 template <class V>
 __global__ void __launch_bounds__(kFixupThreads)
     panel_long_fixup(const typename V::Acc *__restrict__ partial, const uint32_t *__restrict__ vbase,
-                     const int32_t *__restrict__ long_rows, int64_t n_long, int64_t n_rows,
+                     const int32_t *__restrict__ long_rows, int64_t n_rows,
                      typename V::Storage *__restrict__ y) {
   using A = typename V::Acc;
   __shared__ A wave_sum[kFixupThreads / kWave];
@@ -799,7 +799,7 @@ msx_status launch_typed(const msx_csr_plan *p, const void *indptr, const void *x
   MSX_HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL((panel_long_fixup<V>), dim3(static_cast<uint32_t>(p->n_long)),
                      dim3(kFixupThreads), 0, stream, static_cast<const A *>(p->pn_partial), p->pn_vbase,
-                     p->long_rows, p->n_long, p->n_rows, static_cast<S *>(y));
+                     p->long_rows, p->n_rows, static_cast<S *>(y));
   MSX_HIP_TRY(hipGetLastError());
   return MSX_OK;
 }
