@@ -207,3 +207,29 @@ def test_cfg5_banded_spmm_k64(gpu, banded, vtype):
     info = _spmm_check(gpu, banded, storage(banded.data, vtype), X, vtype,
                        f"cfg5 banded {vtype} spmm k=64", exact=False)
     assert 0 < info["window_rows"] <= 32 + 2 * 32
+
+
+def test_cfg2_value_gradient_full_size(gpu):
+    """The value gradient of y = A x through the headline's panel plan
+    (pass A: x per copy entry; pass B: the tile's x placed by LDS word, the
+    cotangent from each row's gap word, the gradient stored in position
+    order), reached through autograd: equal to the oracle bit for bit on
+    two backward passes in a row."""
+    from mlx_sparse import synthetic
+
+    ms = gpu
+    m = synthetic.random_fixed_row(1 << 22, 16, seed=0)
+    n_rows, n_cols = m.shape
+    x = synthetic.uniform(n_cols, -1.0, 1.0, seed=1)
+    g = synthetic.uniform(n_rows, -1.0, 1.0, seed=3)
+    data = torch.from_numpy(m.data).to(DEV).requires_grad_()
+    A = ms.csr_array((data, torch.from_numpy(m.indices), torch.from_numpy(m.indptr)),
+                     shape=m.shape)
+    assert _kind(A.plan().info()) == "panels"
+    want = orc.csr_data_vjp(m.indices, m.indptr, x, g, n_rows, n_cols, m.nnz, vtype="float32")
+    xt, gt = torch.from_numpy(x).to(DEV), torch.from_numpy(g).to(DEV)
+    for k in range(2):
+        data.grad = None
+        (A @ xt).backward(gt)
+        print(f"cfg2 value gradient, backward {k}", flush=True)
+        np.testing.assert_array_equal(to_numpy(data.grad), want, err_msg=f"backward {k}")
