@@ -64,12 +64,15 @@ def _bytes(a):
 
 
 def _abs_scale(data, indices, indptr, X, n_rows, n_cols, vtype):
-    """sum_i |a_ij| |x_i| per output (float64)."""
+    """sum_i |a_ij| |x_i| per output (float64); columns out of range add
+    nothing."""
     a = np.abs(widen(data, vtype))
     x = np.abs(widen(X, vtype))
     rows = np.repeat(np.arange(n_rows), np.diff(indptr.astype(np.int64)))
+    cols = indices.astype(np.int64)
+    ok = (cols >= 0) & (cols < n_cols)
     out = np.zeros((n_cols,) + x.shape[1:])
-    np.add.at(out, indices.astype(np.int64), a.reshape((-1,) + (1,) * (x.ndim - 1)) * x[rows])
+    np.add.at(out, cols[ok], (a.reshape((-1,) + (1,) * (x.ndim - 1)) * x[rows])[ok])
     return out
 
 
@@ -131,6 +134,36 @@ def test_spmv_transpose(vtype, index_dtype):
     data = _values(rng, nnz, vtype)
     x = _values(rng, n_rows, vtype)
     print(f"spmv_transpose tol {vtype} {np.dtype(index_dtype).name}", flush=True)
+    got = to_numpy(_capi.spmv_transpose(_dev(data, vtype), _dev(indices), _dev(indptr),
+                                        _dev(x, vtype), n_rows, n_cols))
+    want = orc.csr_transpose_product(data, indices, indptr, x, n_rows, n_cols, vtype=vtype)
+    scale = _abs_scale(data, indices, indptr, x, n_rows, n_cols, vtype)
+    err = np.abs(widen(got, vtype) - widen(want, vtype))
+    assert np.all(err <= TOL[vtype] * scale + 1e-30), float(np.max(err - TOL[vtype] * scale))
+
+
+@pytest.mark.parametrize("vtype", VTYPES)
+@pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
+def test_spmv_transpose_wide_output(vtype, index_dtype):
+    """1.5 M columns (accumulators of 6 or 12 MB, more than one XCD's L2)
+    and columns out of range, which the scatter drops: integer values give
+    an exact result in any order of the atomics, random ones stay within
+    the tolerance."""
+    rng = np.random.default_rng(33)
+    n_rows, n_cols = 200_000, 1_500_000
+    indices, indptr, nnz = _matrix(rng, n_rows, n_cols, index_dtype)
+    indices[rng.random(nnz) < 0.001] = -1
+    indices[rng.random(nnz) < 0.001] = n_cols + 3
+    data = _values(rng, nnz, vtype, integer=True)
+    x = _values(rng, n_rows, vtype, integer=True)
+    print(f"spmv_transpose wide exact {vtype} {np.dtype(index_dtype).name}", flush=True)
+    got = _capi.spmv_transpose(_dev(data, vtype), _dev(indices), _dev(indptr), _dev(x, vtype),
+                               n_rows, n_cols)
+    want = orc.csr_transpose_product(data, indices, indptr, x, n_rows, n_cols, vtype=vtype)
+    np.testing.assert_array_equal(_bytes(to_numpy(got)), _bytes(want))
+    data = _values(rng, nnz, vtype)
+    x = _values(rng, n_rows, vtype)
+    print(f"spmv_transpose wide tol {vtype} {np.dtype(index_dtype).name}", flush=True)
     got = to_numpy(_capi.spmv_transpose(_dev(data, vtype), _dev(indices), _dev(indptr),
                                         _dev(x, vtype), n_rows, n_cols))
     want = orc.csr_transpose_product(data, indices, indptr, x, n_rows, n_cols, vtype=vtype)
