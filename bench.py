@@ -26,8 +26,8 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``batched_spmv``: 8 vectors at once on the same Poisson matrix (native
   batched entry point), against 8 single SpMVs;
 - ``cg``: conjugate gradients (device-resident loop) on the Poisson matrix,
-  time per iteration against its bytes, and the single-threaded reference
-  loop on the host;
+  time per iteration against its bytes (the single-threaded reference loop
+  on the host is timed in the CPU leg);
 - ``krylov``: BiCGSTAB, MINRES and GMRES(20) (device-resident loops) at n = 128^3, the
   same figures;
 - ``mtx`` (with ``--mtx PATH``): SpMV on a Matrix Market matrix read by the
@@ -44,7 +44,11 @@ traffic, nnz*(4+4) + (n+1)*4 + 4n (x) + 4n (y) bytes per step.  Extra fields:
 - ``cpu_baseline``: the product's CPU path (``ms.use_cpu()``, the C++
   restatement of the reference CPU kernel in csrc/csr_cpu.cpp, ``-O3``
   without ``-march=native``) on the headline matrix, at the reference-resolved
-  worker count and at one thread, on this host's cores, with the CPU model.
+  worker count and at one thread, on this host's cores, with the CPU model;
+  and (``solvers``) the oracle's single-threaded restatements of the
+  reference solver loops on the solver legs' systems, whose per-iteration
+  times and speedups are added to the ``cg`` and ``krylov`` rows.  With
+  ``--no-cpu`` no CPU figure is taken.
 """
 
 from __future__ import annotations
@@ -378,11 +382,10 @@ def cg_leg(dev) -> dict:
     Poisson matrix 128^3, b = 1, x0 = 0, rtol = 1e-6.  Bytes per iteration:
     the SpMV's compulsory bytes plus 11 float vectors of n (p.ap reads p, ap;
     the update reads x, p, r, ap and writes x, r; the direction reads r, p and
-    writes p).  The CPU figure is the oracle's single-threaded restatement of
-    the reference CPU loop (cg.cpp:75-246) on the same system, 20 iterations."""
+    writes p).  Its CPU figure comes from the CPU baseline leg
+    (``cpu_solver_baselines``)."""
     import mlx_sparse as ms
     from mlx_sparse import linalg, synthetic
-    from oracle import oracle as orc
 
     p = synthetic.poisson_3d(128)
     n = p.shape[0]
@@ -401,10 +404,6 @@ def cg_leg(dev) -> dict:
     its = info.iterations
     per_it = solve_s / max(its, 1)
     it_bytes = synthetic.compulsory_bytes(p.nnz, n, n, 4, 4) + 11 * 4 * n
-    t0 = time.perf_counter()
-    _, cinfo, _, cits = orc.csr_cg(p.data, p.indices, p.indptr, np.ones(n, np.float32),
-                                   rtol=1e-6, maxiter=20)
-    cpu_per_it = (time.perf_counter() - t0) / max(cits, 1)
     out = {
         "workload": "poisson3d 128^3 n=2097152 nnz=14581760 f32/i32, b=1, x0=0, rtol=1e-6",
         "info": info.status, "iterations": its, "residual": info.residual_norm,
@@ -412,9 +411,6 @@ def cg_leg(dev) -> dict:
         "bytes_per_iteration": it_bytes,
         "gbs": round(it_bytes / per_it / 1e9, 1),
         "frac": round(it_bytes / per_it / 1e9 / HBM_PEAK_GBS, 4),
-        "cpu_us_per_iteration": round(cpu_per_it * 1e6, 1),
-        "cpu_sample": "oracle CG (one thread, the reference loop), 20 iterations",
-        "speedup_per_iteration": round(cpu_per_it / per_it, 1),
     }
     log(f"cg: {out}")
     return out
@@ -509,11 +505,10 @@ def krylov_leg(dev) -> dict:
     convection-diffusion variant of it (x-direction off-diagonals -1.3 and
     -0.7, diagonal 8); b ~ U[-1, 1], rtol 1e-5.  Bytes per iteration: two
     SpMVs' compulsory bytes plus the vector passes (BiCGSTAB 20, MINRES 18
-    float vectors of n).  The CPU figure is the oracle's single-threaded
-    restatement of the reference loop on the same system."""
+    float vectors of n).  Their CPU figures come from the CPU baseline leg
+    (``cpu_solver_baselines``)."""
     import mlx_sparse as ms
     from mlx_sparse import linalg, synthetic
-    from oracle import oracle as orc
 
     m = synthetic.poisson_3d(128)
     n = m.shape[0]
@@ -527,8 +522,8 @@ def krylov_leg(dev) -> dict:
     b = torch.from_numpy(b_np).to(dev)
     spmv_bytes = synthetic.compulsory_bytes(m.nnz, n, n, 4, 4)
     out = {"workload": "n=2097152 (128^3) f32/i32, b~U[-1,1], rtol=1e-5"}
-    for name, data, kw, nvec, f in (("minres", m.data, {"shift": -1.0}, 18, orc.csr_minres),
-                                    ("bicgstab", conv, {}, 20, orc.csr_bicgstab)):
+    for name, data, kw, nvec in (("minres", m.data, {"shift": -1.0}, 18),
+                                 ("bicgstab", conv, {}, 20)):
         A = ms.csr_array((data, m.indices, m.indptr), shape=m.shape, canonical=True)
         solver = getattr(linalg, name)
         solver(A, b, rtol=1e-5, maxiter=500, **kw)  # plan, allocator
@@ -542,9 +537,6 @@ def krylov_leg(dev) -> dict:
         solve_s = statistics.median(times)
         its = max(info.iterations, 1)
         it_bytes = 2 * spmv_bytes + nvec * 4 * n
-        t0 = time.perf_counter()
-        _, cinfo, _, cits = f(data, m.indices, m.indptr, b_np, rtol=1e-5, maxiter=500, **kw)
-        cpu_it = (time.perf_counter() - t0) / max(cits, 1)
         out[name] = {"matrix": "poisson3d + shift -1" if name == "minres" else
                      "convection-diffusion variant of poisson3d",
                      "info": info.status, "iterations": info.iterations,
@@ -552,10 +544,7 @@ def krylov_leg(dev) -> dict:
                      "us_per_iteration": round(solve_s / its * 1e6, 1),
                      "bytes_per_iteration": it_bytes,
                      "gbs": round(it_bytes / (solve_s / its) / 1e9, 1),
-                     "frac": round(it_bytes / (solve_s / its) / 1e9 / HBM_PEAK_GBS, 4),
-                     "cpu_us_per_iteration": round(cpu_it * 1e6, 1),
-                     "cpu_iterations": cits,
-                     "speedup_per_iteration": round(cpu_it / (solve_s / its), 1)}
+                     "frac": round(it_bytes / (solve_s / its) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"{name}: {out[name]}")
         del A
         torch.cuda.empty_cache()
@@ -570,11 +559,10 @@ def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
     two basis vectors read), 24 n for each of the j later pairs (w and four
     basis vectors read, w written), 16 n for the last pass (w and two basis
     vectors read, w written, w.w) - and 8 n for the normalisation; per cycle
-    also the residual (12 n) and the update ((used + 2) 4 n).  The CPU figure is the oracle's single-threaded
-    restatement of the reference loop, timed over one cycle of 20 steps."""
+    also the residual (12 n) and the update ((used + 2) 4 n).  Its CPU
+    figure comes from the CPU baseline leg (``cpu_solver_baselines``)."""
     import mlx_sparse as ms
     from mlx_sparse import linalg
-    from oracle import oracle as orc
 
     n = m.shape[0]
     restart = 20
@@ -595,20 +583,13 @@ def gmres_row(dev, m, conv, b, b_np, spmv_bytes) -> dict:
         step_bytes += spmv_bytes + 12 * n + j * 24 * n + 16 * n + 8 * n
     cycle_bytes = step_bytes + 12 * n + (restart + 2) * 4 * n + spmv_bytes
     total_bytes = cycles * cycle_bytes
-    t0 = time.perf_counter()
-    _, cinfo, _, cits = orc.csr_gmres(conv, m.indices, m.indptr, b_np, rtol=1e-5,
-                                      restart=restart, maxiter=restart)
-    cpu_it = (time.perf_counter() - t0) / max(cits, 1)
     row = {"matrix": "convection-diffusion variant of poisson3d", "restart": restart,
            "info": info.status, "iterations": info.iterations, "residual": info.residual_norm,
            "solve_ms": round(solve_s * 1e3, 2),
            "us_per_iteration": round(solve_s / its * 1e6, 1),
            "bytes_per_cycle": cycle_bytes,
            "gbs": round(total_bytes / solve_s / 1e9, 1),
-           "frac": round(total_bytes / solve_s / 1e9 / HBM_PEAK_GBS, 4),
-           "cpu_us_per_iteration": round(cpu_it * 1e6, 1),
-           "cpu_iterations": cits,
-           "speedup_per_iteration": round(cpu_it / (solve_s / its), 1)}
+           "frac": round(total_bytes / solve_s / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"gmres: {row}")
     del A
     torch.cuda.empty_cache()
@@ -680,6 +661,38 @@ def solver_system(name: str):
     if name == "gmres":
         kw["restart"] = 20
     return m, conv, b, kw
+
+
+def cpu_solver_baselines(result: dict) -> dict:
+    """Part of the CPU baseline leg: the oracle's single-threaded
+    restatements of the reference solver loops timed on the solver legs'
+    systems (``solver_system``) - CG over 20 iterations, MINRES and BiCGSTAB
+    over their whole solves, GMRES over one cycle of 20 steps - and the
+    per-iteration speedup of the device loops in ``result``, whose rows gain
+    ``cpu_us_per_iteration`` and ``speedup_per_iteration`` in place."""
+    from oracle import oracle as orc
+
+    runs = {"cg": (orc.csr_cg, {"maxiter": 20}),
+            "minres": (orc.csr_minres, {}),
+            "bicgstab": (orc.csr_bicgstab, {}),
+            "gmres": (orc.csr_gmres, {"maxiter": 20})}
+    krylov = result.get("krylov") or {}
+    rows = {"cg": result.get("cg"), "minres": krylov.get("minres"),
+            "bicgstab": krylov.get("bicgstab"), "gmres": krylov.get("gmres")}
+    out = {}
+    for name, (f, over) in runs.items():
+        if rows[name] is None:
+            continue
+        m, data, b_np, kw = solver_system(name)
+        t0 = time.perf_counter()
+        _, _, _, its = f(data, m.indices, m.indptr, b_np, **{**kw, **over})
+        cpu_us = (time.perf_counter() - t0) / max(its, 1) * 1e6
+        out[name] = {"us_per_iteration": round(cpu_us, 1), "iterations": its}
+        rows[name]["cpu_us_per_iteration"] = round(cpu_us, 1)
+        rows[name]["cpu_iterations"] = its
+        rows[name]["speedup_per_iteration"] = round(cpu_us / rows[name]["us_per_iteration"], 1)
+        log(f"cpu {name}: {out[name]}")
+    return out
 
 
 def profile_solver(dev, name: str) -> dict:
@@ -1012,6 +1025,7 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(m, x_np)
+        result["cpu_baseline"]["solvers"] = cpu_solver_baselines(result)
         log(f"cpu: {result['cpu_baseline']}")
     else:
         result["cpu_baseline"] = None
